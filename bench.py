@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Benchmark of the KV compression hot path on one MI355X.
+
+A step is one round trip of the hot path over one request: compress (K-statistics
+pass + fused gather/FWHT/quantize/bitpack pass) and decompress (fused
+unpack/dequantize/inverse-FWHT/scatter pass) of the BASELINE config-2 request:
+Llama-3-8B-shaped, 32 layers x 8 KV heads x D=128 x 8192 tokens of bf16 KV in
+16-token paged blocks scattered over a 65536-block pool per layer (128 GiB of
+pools), K/V ~ N(0,1) with 4 outlier K channels per head, head split with the
+Llama-3.1-8B mask at hybrid 0.3, 16/16 levels, bitpack 4 bits, 4 streams of 8 layers.
+
+value = raw bf16 KV bytes of the request / (compress + decompress time), GB/s.
+Inputs are resident in HBM before the timed region; plans (device descriptors) are
+built before it too.  Per-direction throughput and the fraction of HBM peak are
+printed alongside.  Prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+METRIC = "compress/decompress GB/s of raw bf16 KV on 1 MI355X; % of HBM peak"
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(wl, budget_s: float):
+    """Time the CPU oracle (numpy restatement of the reference pipeline) on whole
+    layers of the same request until `budget_s` is spent; returns GB/s of raw KV per
+    second for a round trip (compress + decompress), single thread."""
+    import numpy as np
+    import torch
+
+    from oracle import kvpipe as kp
+
+    req = wl.requests[0]
+    ids = req.block_ids.long()
+    B = ids.numel()
+    done_bytes, t_total, layers = 0, 0.0, 0
+    for l in range(len(req.pools)):
+        blocks = req.pools[l][:, ids].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+        p = req.profiles[l]
+        prof = kp.LayerProfile(kp.PartProfile(p.k_order, p.k_levels, p.k_groups()),
+                               kp.PartProfile(p.v_order, p.v_levels, p.v_group))
+        t0 = time.perf_counter()
+        chunks = kp.compress_request([blocks], list(range(B)), [prof], wl.seed, wl.bits)
+        dst = np.zeros_like(blocks)
+        kp.decompress_request(chunks, [dst], list(range(B)), [prof], wl.seed, wl.bits)
+        t_total += time.perf_counter() - t0
+        done_bytes += blocks.nbytes
+        layers += 1
+        if t_total >= budget_s:
+            break
+    return {
+        "value": round(done_bytes / t_total / 1e9, 4),
+        "unit": "GB/s (round trip, raw bf16 KV)",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{layers} of {len(req.pools)} layers of the config-2 request ({done_bytes / 2**20:.0f} MiB raw), "
+                  f"numpy oracle compress+decompress on {cpu_model()} (os.cpu_count()={os.cpu_count()}), "
+                  f"{t_total:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layers", type=int, default=32, help="(debug) layers of the config-2 request")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from kvserve_amd.engine import FusedKVCodec
+    from kvserve_amd.workloads import make_config2
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    print("bench: building config-2 workload", file=sys.stderr, flush=True)
+    wl = make_config2(device=dev, num_layers=args.layers)
+    req = wl.requests[0]
+    L, B = len(req.pools), req.block_ids.numel()
+    S, H, D, bits = wl.block_size, wl.num_heads, wl.head_dim, wl.bits
+    codec = FusedKVCodec(H, D, S, bits, wl.seed)
+    cplan = codec.plan_compress(req.pools, req.block_ids, req.profiles, req.layer_ids)
+    packet = cplan.packet
+    dplan = codec.plan_decompress(packet, req.pools, req.block_ids)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    launches = [(cplan, n) for n in cplan.launches()] + [(dplan, n) for n in dplan.launches()]
+    print(f"bench: warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        for plan, name in launches:
+            plan.launch(name)
+    torch.cuda.synchronize()
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)] for _ in range(args.steps)]
+    print(f"bench: timing {args.steps} steps", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        ev[k][0].record(stream)
+        for i, (plan, name) in enumerate(launches):
+            plan.launch(name)
+            ev[k][i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    cplan.check_errors()
+    dplan.check_errors()
+
+    per = {name: 0.0 for _, name in launches}
+    for k in range(args.steps):
+        for i, (_, name) in enumerate(launches):
+            per[name] += ev[k][i].elapsed_time(ev[k][i + 1]) / args.steps
+    t_c = per["kvmi_kstats_paged"] + per["kvmi_encode_paged"]
+    t_d = per["kvmi_decode_paged"]
+
+    R = L * 2 * B * S * H * D * 2
+    P = packet.compressed_bytes()
+    M = (packet.kmeta.numel() + packet.vmeta.numel()) * 2
+    idx = L * B * 4
+    alg = R + P + M + idx  # one direction: read KV + write stream/meta (or the reverse)
+    comp_gbps, dec_gbps = R / t_c / 1e6, R / t_d / 1e6
+    comp_frac, dec_frac = alg / t_c / 1e6 / HBM_PEAK_GBPS, alg / t_d / 1e6 / HBM_PEAK_GBPS
+    dom = "kvmi_encode_paged" if per["kvmi_encode_paged"] >= per["kvmi_decode_paged"] else "kvmi_decode_paged"
+    dom_kernel = {"kvmi_encode_paged": "encode_kernel<128,4>", "kvmi_decode_paged": "decode_kernel<128,4>"}[dom]
+    achieved = alg / per[dom] / 1e6
+    ms_step = wall / args.steps * 1e3
+
+    out = {
+        "metric": METRIC,
+        "value": round(R / ((t_c + t_d) / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
+        "config": {
+            "workload": "config2: Llama-3-8B-shaped request, 32 layers x 8 KV heads x D=128 x 8192 tokens, "
+                        "16-token blocks at seeded random ids of a 65536-block pool per layer, "
+                        "Hadamard seed 0xC0FEBABE, head split (Llama-3.1-8B mask, hybrid 0.3), "
+                        "16/16 levels, bitpack 4 bits, 4 streams of 8 layers; step = compress + decompress",
+            "layers": L, "tokens": B * S, "raw_bytes": R, "packed_bytes": P, "meta_bytes": M,
+        },
+        "compress_gbps": round(comp_gbps, 2),
+        "decompress_gbps": round(dec_gbps, 2),
+        "compress_hbm_frac": round(comp_frac, 4),
+        "decompress_hbm_frac": round(dec_frac, 4),
+        "kernel_ms": {k: round(v, 4) for k, v in per.items()},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom_kernel,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": alg,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,196 @@
+/*
+ * kvserve_amd.h -- C ABI of the MI355X (gfx950) KV-cache compression engine.
+ *
+ * The library replaces KVServe's compression hot path:
+ *   compress:   paged-KV block gather -> random-sign Hadamard (FWHT) -> min-max
+ *               quantizer (K per channel, V per token) -> bitpack (16-byte header)
+ *   decompress: unpack -> dequantize -> inverse FWHT -> sign -> paged scatter
+ *
+ * Conventions of every entry point:
+ *   - all data pointers are device addresses owned by the caller, who keeps them
+ *     alive until the stream has finished the work;
+ *   - work is enqueued on `stream`; no entry point allocates, frees or
+ *     synchronizes, and none uses the null stream unless `stream` is null;
+ *   - the return value is 0 or a negative errno-style code for errors the host can
+ *     see (bad sizes, bad bit width, launch failure).  Data errors found by the
+ *     kernels (a symbol that does not fit the bit width, a stream header that does
+ *     not match) are OR-ed into the caller's device word `err`
+ *     (KVMI_ERR_* bits below); the caller reads it after the stream completes.
+ *
+ * Reference interfaces replaced (paths relative to the KVServe source tree):
+ *   kvmi_bitpack_encode / kvmi_bitpack_decode
+ *       kvserve_v1/compression/codec/bitpack_codec.py:100-135 (BitPackCodec.encode /
+ *       .decode and the Triton _pack / _unpack kernels at :24-69)
+ *   kvmi_gather_blocks
+ *       kvserve_v1/utils/kv_utils.py:59-80 (extract_kv_from_layer_by_blocks)
+ *   kvmi_scatter_blocks
+ *       kvserve_v1/utils/kv_utils.py:83-119 (inject_kv_into_layer_by_blocks)
+ *   kvmi_hadamard
+ *       kvserve_v1/compression/transformer/hadamard_func.py:161-231
+ *       (HadamardTransform.transform / .inverse)
+ *   kvmi_encode_paged (with kvmi_kstats_paged before it)
+ *       kvserve_v1/compression/compression_manager.py:200-537 (compress_all_layers and
+ *       its chunked variant: transform -> KVServeQuantizer.quantize
+ *       (quantizer/kvserve_quantizer.py:171-233) -> codec-buffer permute (:155-164)
+ *       -> KVServeCodec.encode (codec/kvserve_codec.py:289-313)), fused with the
+ *       gather of kv_utils.py:59-80
+ *   kvmi_decode_paged
+ *       kvserve_v1/compression/compression_manager.py:539-757 (decompress_all_layers
+ *       and its chunked variant), fused with the scatter of kv_utils.py:83-119
+ */
+#ifndef KVSERVE_AMD_H
+#define KVSERVE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef struct ihipStream_t* kvmi_stream_t;
+
+#define KVMI_ABI_VERSION 1
+
+/* Bits OR-ed into the caller's device error word. */
+#define KVMI_ERR_SYMBOL_RANGE 1 /* a symbol >= 2^bits reached the packer */
+#define KVMI_ERR_BAD_HEADER 2   /* stream header does not match the decode contract */
+
+/* Host-visible return codes. */
+#define KVMI_OK 0
+#define KVMI_EINVAL (-22)
+#define KVMI_ELAUNCH (-5)
+
+/* Stream format constants (bitpack_codec.py:20-21). */
+#define KVMI_HEADER_BYTES 16
+#define KVMI_MAGIC 0x0150424Bu
+
+/* Flags of kvmi_geometry.flags */
+#define KVMI_F_NO_TRANSFORM 1u /* skip signs + FWHT (pipeline without "transformer") */
+#define KVMI_F_NATIVE_LAYOUT 2u /* symbol order [l,2,B,S,H',D] instead of [l,2,H',B,S,D] */
+#define KVMI_F_NO_HEADER 4u     /* raw symbol buffer: no 16-byte header (bits must be 8) */
+
+/* Launch-wide geometry shared by every job of one call. */
+typedef struct kvmi_geometry {
+  int32_t block_size; /* S: tokens per paged block (vLLM block_size) */
+  int32_t num_heads;  /* H: KV heads of this worker's shard */
+  int32_t head_dim;   /* D: 64, 128 or 256 */
+  int32_t bits;       /* bitpack width in [1, 8] */
+  uint32_t flags;     /* KVMI_F_* */
+  int32_t max_groups; /* G: V statistic groups per layer (<= H) */
+  int32_t reserved[2];
+} kvmi_geometry;
+
+/*
+ * One (request, layer) unit of work.  An array of these lives in device memory.
+ *
+ * profile: uint8 [2 parts][3][H]
+ *   [p][0][j] source head that is stored at output position j (low heads first,
+ *             ascending, then high heads: kvserve_quantizer.py:216-220)
+ *   [p][1][j] quantization levels (max_value) of output position j, in [2, 255]
+ *   [p][2][j] statistic group of output position j; groups are contiguous runs of
+ *             positions. Only the V part uses groups (per-token stats are shared by
+ *             the heads of a group, quantizer_func.py:44-53 with axis "token").
+ * kmeta: bf16 [2][H][D]: [0] = per-channel min, [1] = scale, by output position.
+ * vmeta: bf16 [2][G][num_blocks*S]: [0] = per-token min, [1] = scale, by group.
+ * kstats: uint32 [2][H][D] order-preserving keys of the running K min / max,
+ *         initialised to {0xFFFFFFFF, 0}; kvmi_kstats_paged leaves it initialised.
+ * counter: uint32 [1] work counter, initialised to 0; left at 0.
+ */
+typedef struct kvmi_layer_job {
+  void* pool;                /* bf16 [2, P, S, H, D] paged KV of this layer (NHD) */
+  const int32_t* block_ids;  /* [num_blocks] pool block of each logical block */
+  uint8_t* stream;           /* packed chunk stream this layer belongs to */
+  uint16_t* kmeta;
+  uint16_t* vmeta;
+  const uint32_t* signs;     /* [H][D/32] Rademacher sign bits per source head (1 = -1) */
+  const uint8_t* profile;
+  uint32_t* kstats;
+  uint32_t* counter;
+  int64_t pool_part_stride;  /* elements between the K and V halves of `pool` */
+  int64_t symbol_offset;     /* index of this layer's first symbol in the chunk */
+  int64_t chunk_symbols;     /* symbol count N of the chunk (header bytes 8..15) */
+  int32_t num_blocks;        /* B */
+  int32_t write_header;      /* 1 for exactly one job of each chunk */
+} kvmi_layer_job;
+
+/* ABI version of the loaded library (KVMI_ABI_VERSION). */
+int kvmi_abi_version(void);
+
+/*
+ * Bitpack codec.  Replaces BitPackCodec.encode (bitpack_codec.py:100-110):
+ * out[0..15] = header {4B 42 50 01, bits, 0,0,0, n as u64 LE}; out[16 + ...] =
+ * symbols packed LSB-first, symbol i at stream bit i*bits.  `out` holds
+ * 16 + ceil(n*bits/8) bytes.  Symbols >= 2^bits set KVMI_ERR_SYMBOL_RANGE.
+ */
+int kvmi_bitpack_encode(const uint8_t* sym, int64_t n, int32_t bits, uint8_t* out,
+                        int32_t* err, kvmi_stream_t stream);
+
+/*
+ * Replaces BitPackCodec.decode (bitpack_codec.py:112-135).  `in_bytes` must equal
+ * 16 + ceil(n*bits/8) (else KVMI_EINVAL, the reference's length ValueError).  A
+ * header that does not name (bits, n) sets KVMI_ERR_BAD_HEADER and leaves `sym`
+ * unwritten.
+ */
+int kvmi_bitpack_decode(const uint8_t* in, int64_t in_bytes, int64_t n, int32_t bits,
+                        uint8_t* sym, int32_t* err, kvmi_stream_t stream);
+
+/*
+ * Paged gather of whole blocks (kv_utils.py:59-80, FlashAttention NHD layout):
+ * out[p, i] = pool[p, block_ids[i]] for p in {K, V}; `block_elems` = S*H*D.
+ * out is contiguous [2, num_blocks, S, H, D]; element size 2 bytes.
+ */
+int kvmi_gather_blocks(const void* pool, int64_t pool_part_stride, const int32_t* block_ids,
+                       int32_t num_blocks, int64_t block_elems, void* out,
+                       kvmi_stream_t stream);
+
+/*
+ * Paged scatter (kv_utils.py:83-119): pool[p, block_ids[i]] = src[p, i] for
+ * i < num_blocks (the caller passes min(len(block_ids), payload blocks)).
+ */
+int kvmi_scatter_blocks(void* pool, int64_t pool_part_stride, const int32_t* block_ids,
+                        int32_t num_blocks, int64_t block_elems, const void* src,
+                        kvmi_stream_t stream);
+
+/*
+ * Random-sign Hadamard transform of contiguous bf16 rows [rows, D], row r
+ * belonging to head r % num_heads (hadamard_func.py:161-231).
+ *   forward: out = bf16( FWHT_fp32(x * s) * (1/sqrt(D)) )
+ *   inverse: out = bf16( FWHT_fp32(x) * (1/sqrt(D)) ) * s
+ * signs: [num_heads][D/32] bits (1 = -1).  in and out may alias.
+ */
+int kvmi_hadamard(const void* in, void* out, int64_t rows, int32_t num_heads,
+                  int32_t head_dim, const uint32_t* signs, int32_t inverse,
+                  kvmi_stream_t stream);
+
+/*
+ * Pass 1 of compress: per-channel K statistics over all tokens of each job
+ * (quantizer_func.py:41-53, axis "channel" reduces blocks and tokens).  Fills
+ * each job's kmeta (min and scale of every K channel) and leaves kstats/counter
+ * re-initialised.  `max_blocks` = max num_blocks over jobs (grid sizing).
+ */
+int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                      int32_t max_blocks, int32_t* err, kvmi_stream_t stream);
+
+/*
+ * Pass 2 of compress: gather, transform, quantize K with the kmeta of pass 1 and V
+ * with per-token group statistics, and bitpack every job into its chunk stream
+ * (plus the 16-byte header of jobs with write_header = 1) and vmeta.
+ */
+int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                      int32_t max_blocks, int32_t* err, kvmi_stream_t stream);
+
+/*
+ * Decompress: check each chunk header, unpack, dequantize
+ * (quantizer_func.py:77-113: bf16(bf16(q*scale)+min)), inverse transform and
+ * scatter every job's blocks into its pool.  Blocks of a chunk whose header does
+ * not match are left unwritten and KVMI_ERR_BAD_HEADER is set.
+ */
+int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                      int32_t max_blocks, int32_t* err, kvmi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVSERVE_AMD_H */

@@ -1,0 +1,111 @@
+"""ctypes binding of the gfx950 C-ABI library (include/kvserve_amd.h).
+
+The library must exist (``python -m kvserve_amd.build``); there is no CPU fallback:
+every entry point of the package raises if it is missing.  ctypes releases the GIL
+for the duration of each call, like the reference's pybind11 bindings
+(runtime/csrc/kvs_bind.cpp:10-23).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libkvserve_amd.so"
+ABI_VERSION = 1
+
+# Device error bits (KVMI_ERR_*) and host return codes (KVMI_*).
+ERR_SYMBOL_RANGE = 1
+ERR_BAD_HEADER = 2
+OK, EINVAL, ELAUNCH = 0, -22, -5
+
+F_NO_TRANSFORM = 1
+F_NATIVE_LAYOUT = 2
+F_NO_HEADER = 4
+
+# Every symbol include/kvserve_amd.h declares.
+EXPORTS = (
+    "kvmi_abi_version",
+    "kvmi_bitpack_encode",
+    "kvmi_bitpack_decode",
+    "kvmi_gather_blocks",
+    "kvmi_scatter_blocks",
+    "kvmi_hadamard",
+    "kvmi_kstats_paged",
+    "kvmi_encode_paged",
+    "kvmi_decode_paged",
+)
+
+
+class Geometry(ctypes.Structure):
+    _fields_ = [
+        ("block_size", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("max_groups", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 2),
+    ]
+
+
+# kvmi_layer_job: 9 pointers, 3 int64, 2 int32 -> 104 bytes, 8-byte aligned.  It is
+# written as 13 int64 words; the last word carries num_blocks (low half) and
+# write_header (high half).
+JOB_FIELDS = (
+    "pool", "block_ids", "stream", "kmeta", "vmeta", "signs", "profile", "kstats", "counter",
+    "pool_part_stride", "symbol_offset", "chunk_symbols", "num_blocks_and_header",
+)
+JOB_INT64S = 13
+JOB_BYTES = JOB_INT64S * 8
+
+_lock = threading.Lock()
+_lib = None
+
+_vp, _i64, _i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+_SIGNATURES = {
+    "kvmi_abi_version": ([], ctypes.c_int),
+    "kvmi_bitpack_encode": ([_vp, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
+    "kvmi_bitpack_decode": ([_vp, _i64, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
+    "kvmi_gather_blocks": ([_vp, _i64, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
+    "kvmi_scatter_blocks": ([_vp, _i64, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
+    "kvmi_hadamard": ([_vp, _vp, _i64, _i32, _i32, _vp, _i32, _vp], ctypes.c_int),
+    "kvmi_kstats_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
+    "kvmi_encode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
+    "kvmi_decode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
+}
+
+
+class KvmiError(RuntimeError):
+    """A host-visible failure of a C-ABI call."""
+
+
+def load(path: Path = LIB_PATH):
+    """Load (once) and return the ctypes library; raises if it was not built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not path.exists():
+            raise KvmiError(
+                f"{path} is missing: build the HIP library with `python -m kvserve_amd.build` "
+                "(no CPU fallback exists)")
+        lib = ctypes.CDLL(str(path))
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        ver = lib.kvmi_abi_version()
+        if ver != ABI_VERSION:
+            raise KvmiError(f"{path} has ABI version {ver}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == OK:
+        return
+    if rc == EINVAL:
+        raise ValueError(f"{what}: invalid arguments (KVMI_EINVAL)")
+    raise KvmiError(f"{what}: failed with code {rc}")

@@ -1,0 +1,545 @@
+// Fused paged compress / decompress kernels for gfx950.
+//
+// Work unit: a workgroup of 512 threads (8 wave64s) owns a run of paged blocks of
+// one (request, layer) job.  The run's rows (one row = one token x one KV head =
+// D contiguous bf16) are processed 128 at a time; row r of a pass is held by the
+// quad of lanes 4r..4r+3, lane q of the quad owning elements [q*D/4, (q+1)*D/4).
+// Rows of a pass are contiguous in the pool (a block is [S, H, D] row-major), so
+// every wave reads 16 consecutive rows.  Because 128 % H == 0, a lane always sees
+// the same KV head, which keeps sign bits and per-channel K statistics in place.
+//
+// Compress is two launches:
+//   kstats: gather + transform of K, per-channel running min/max per lane,
+//           workgroup reduction through LDS atomics, device reduction through
+//           global atomics; the last workgroup of a job (work counter) turns the
+//           keys into the job's K metadata and re-initialises the scratch.
+//   encode: gather + transform of K and V, K quantized with the per-channel
+//           metadata, V with per-(token, group) statistics reduced through LDS;
+//           symbols bitpacked straight into the chunk stream.
+// Decompress is one launch: header check, unpack, dequantize, inverse transform,
+// sign and scatter into the pool.
+#include "kvmi_device.hpp"
+#include "../../include/kvserve_amd.h"
+
+static_assert(sizeof(kvmi_layer_job) == 104, "kvmi_layer_job layout is part of the ABI");
+static_assert(sizeof(kvmi_geometry) == 32, "kvmi_geometry layout is part of the ABI");
+
+namespace kvmi {
+namespace {
+
+constexpr int kWG = 512;
+constexpr int kRows = kWG / 4;  // rows per pass
+constexpr int kMaxH = 16;       // heads per worker shard supported by the LDS tables
+constexpr int kMaxHD = kMaxH * 128;
+
+struct Geo {
+  int S, H, D, bits;
+  uint32_t flags;
+  int G;
+  int bpw;      // paged blocks per workgroup
+  float scale;  // fp32 value of 1/sqrt(D)
+};
+
+struct Profile {  // decoded kvmi_layer_job::profile for one part
+  const uint8_t* order;
+  const uint8_t* levels;
+  const uint8_t* group;
+};
+__device__ __forceinline__ Profile part_profile(const uint8_t* p, int part, int H) {
+  const uint8_t* b = p + part * 3 * H;
+  return Profile{b, b + H, b + 2 * H};
+}
+
+// Sign bits of lane q's E elements for head h.
+template <int D>
+__device__ __forceinline__ uint32_t lane_signs(const uint32_t* signs, int h, int q) {
+  constexpr int E = D / 4;
+  const uint32_t* sg = signs + h * (D / 32);
+  if constexpr (E == 32) {
+    return sg[q];
+  } else {  // E == 16
+    return (sg[q >> 1] >> ((q & 1) * 16)) & 0xffffu;
+  }
+}
+
+// Load one row segment, apply signs + FWHT + scale (unless NO_TRANSFORM) and return
+// the fp32 values.  ROUND: round the result to bf16 values.
+template <int D, bool ROUND>
+__device__ __forceinline__ void load_transform(const uint16_t* __restrict__ src, uint32_t sb, bool transform,
+                                               float scale, int q, float (&y)[D / 4]) {
+  constexpr int E = D / 4;
+  uint32_t w[E / 2];
+  load_bf16_seg<E>(src, w);
+  if (transform) {
+    apply_sign_bf16<E>(w, sb);
+    unpack_bf16<E>(w, y);
+    fwht_row<E>(y, q);
+#pragma unroll
+    for (int i = 0; i < E; ++i) y[i] = ROUND ? round_bf16(y[i] * scale) : y[i] * scale;
+  } else {
+    unpack_bf16<E>(w, y);
+  }
+}
+
+struct RowPos {
+  int64_t pool_row;  // row index in the pool part: physical block * S*H + within
+  int tok;           // token index within the job (logical block * S + token in block)
+  bool active;
+};
+__device__ __forceinline__ RowPos row_pos(const kvmi_layer_job& job, int blk0, int64_t rows, int64_t r, int S,
+                                          int H) {
+  RowPos p;
+  p.active = r < rows;
+  if (!p.active) {
+    p.pool_row = 0;
+    p.tok = 0;
+    return p;
+  }
+  const int rpb = S * H;
+  const int b = blk0 + (int)(r / rpb);
+  const int within = (int)(r % rpb);
+  p.pool_row = (int64_t)job.block_ids[b] * rpb + within;
+  p.tok = b * S + within / H;
+  return p;
+}
+
+// Byte address of the packed segment of (part, output position j, token tok) for
+// lane q, in the permuted [l,2,H',B,S,D] or native [l,2,B,S,H',D] symbol order.
+template <int D, int BITS>
+__device__ __forceinline__ uint8_t* seg_addr(const kvmi_layer_job& job, const Geo& g, int part, int j, int tok,
+                                             int q) {
+  const int64_t ntok = (int64_t)job.num_blocks * g.S;
+  int64_t ts, hs, ps;
+  if (g.flags & KVMI_F_NATIVE_LAYOUT) {
+    ts = (int64_t)g.H * D;
+    hs = D;
+    ps = ntok * g.H * D;
+  } else {
+    ts = D;
+    hs = ntok * D;
+    ps = (int64_t)g.H * hs;
+  }
+  const int64_t sym = job.symbol_offset + part * ps + j * hs + tok * ts + q * (D / 4);
+  const int64_t base = (g.flags & KVMI_F_NO_HEADER) ? 0 : KVMI_HEADER_BYTES;
+  return job.stream + base + (sym * BITS) / 8;
+}
+
+// ============================================================== K statistics
+template <int D>
+__global__ __launch_bounds__(kWG) void kstats_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                     int32_t* __restrict__ err) {
+  constexpr int E = D / 4;
+  const kvmi_layer_job job = jobs[blockIdx.y];
+  const int B = job.num_blocks;
+  const int nwg = (B + g.bpw - 1) / g.bpw;
+  if ((int)blockIdx.x >= nwg) return;
+  const int H = g.H, S = g.S, HD = H * D;
+  const int blk0 = blockIdx.x * g.bpw;
+  const int blk1 = min(B, blk0 + g.bpw);
+  const int64_t rows = (int64_t)(blk1 - blk0) * S * H;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3;
+  const int h = Q % H;
+  const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
+  const uint32_t sb = transform ? lane_signs<D>(job.signs, h, q) : 0u;
+
+  __shared__ uint32_t lkey[2 * kMaxHD];
+  __shared__ int last;
+  for (int i = tid; i < HD; i += kWG) {
+    lkey[i] = 0xffffffffu;
+    lkey[HD + i] = 0u;
+  }
+
+  float mn[E], mx[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    mn[i] = __builtin_inff();
+    mx[i] = -__builtin_inff();
+  }
+  const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
+  for (int64_t r0 = 0; r0 < rows; r0 += kRows) {
+    const RowPos rp = row_pos(job, blk0, rows, r0 + Q, S, H);
+    if (rp.active) {
+      float y[E];
+      load_transform<D, false>(pool + rp.pool_row * D + q * E, sb, transform, g.scale, q, y);
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        mn[i] = fminf(mn[i], y[i]);
+        mx[i] = fmaxf(mx[i], y[i]);
+      }
+    }
+  }
+  __syncthreads();
+  if (Q < (int)((rows < kRows) ? rows : kRows)) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      const int c = h * D + q * E + i;
+      atomicMin(&lkey[c], f2key(mn[i]));
+      atomicMax(&lkey[HD + c], f2key(mx[i]));
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < HD; i += kWG) {
+    atomicMin(&job.kstats[i], lkey[i]);
+    atomicMax(&job.kstats[HD + i], lkey[HD + i]);
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) last = (atomicAdd(job.counter, 1u) == (unsigned)(nwg - 1)) ? 1 : 0;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const Profile pk = part_profile(job.profile, 0, H);
+  for (int i = tid; i < HD; i += kWG) {
+    const float kmn = round_bf16(key2f(__hip_atomic_exchange(&job.kstats[i], 0xffffffffu, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT)));
+    const float kmx =
+        round_bf16(key2f(__hip_atomic_exchange(&job.kstats[HD + i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+    const int hs = i / D, e = i % D;
+    int j = 0;
+    for (int k = 0; k < H; ++k)
+      if (pk.order[k] == hs) j = k;
+    const float sc = quant_scale(kmn, kmx, pk.levels[j]);
+    job.kmeta[j * D + e] = (uint16_t)f32_to_bf16_bits(kmn);
+    job.kmeta[HD + j * D + e] = (uint16_t)f32_to_bf16_bits(sc);
+  }
+  if (tid == 0) __hip_atomic_exchange(job.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ============================================================== encode
+template <int D, int BITS>
+__global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                     int32_t* __restrict__ err) {
+  constexpr int E = D / 4;
+  const kvmi_layer_job job = jobs[blockIdx.y];
+  const int B = job.num_blocks;
+  const int nwg = (B + g.bpw - 1) / g.bpw;
+  if ((int)blockIdx.x >= nwg) return;
+  const int H = g.H, S = g.S, HD = H * D, G = g.G;
+  const int blk0 = blockIdx.x * g.bpw;
+  const int blk1 = min(B, blk0 + g.bpw);
+  const int64_t rows = (int64_t)(blk1 - blk0) * S * H;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3;
+  const int h = Q % H;
+  const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
+  const uint32_t sb = transform ? lane_signs<D>(job.signs, h, q) : 0u;
+  const Profile pk = part_profile(job.profile, 0, H);
+  const Profile pv = part_profile(job.profile, 1, H);
+
+  __shared__ float2 kq[kMaxHD];     // (min, 1/scale) by source head and channel
+  __shared__ int posk[kMaxH], posv[kMaxH];
+  __shared__ float2 rowmm[kRows];   // V row (min, max)
+  __shared__ float2 tokq[kRows];    // V (min, 1/scale) by (token of pass, group)
+  __shared__ int ngv;
+
+  if (tid < H) {
+    for (int k = 0; k < H; ++k) {
+      if (pk.order[k] == tid) posk[tid] = k;
+      if (pv.order[k] == tid) posv[tid] = k;
+    }
+  }
+  if (tid == 0) {
+    int m = 0;
+    for (int k = 0; k < H; ++k) m = max(m, (int)pv.group[k]);
+    ngv = m + 1;
+    if (job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER)) {
+      uint32_t* o = reinterpret_cast<uint32_t*>(job.stream);
+      o[0] = KVMI_MAGIC;
+      o[1] = (uint32_t)BITS;
+      o[2] = (uint32_t)((uint64_t)job.chunk_symbols & 0xffffffffu);
+      o[3] = (uint32_t)((uint64_t)job.chunk_symbols >> 32);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < HD; i += kWG) {
+    const int hs = i / D, e = i % D, j = posk[hs];
+    const float m = bf16_to_f32(job.kmeta[j * D + e]);
+    const float sc = bf16_to_f32(job.kmeta[HD + j * D + e]);
+    kq[i] = make_float2(m, 1.0f / sc);
+  }
+  __syncthreads();
+
+  const int jk = posk[h], jv = posv[h];
+  const float lk = (float)pk.levels[jk];
+  const float lvv = (float)pv.levels[jv];
+  const int gv = pv.group[jv];
+  const int ngroups = ngv;
+  const int tpp = kRows / H;  // tokens per pass
+  const uint16_t* poolK = reinterpret_cast<const uint16_t*>(job.pool);
+  const uint16_t* poolV = poolK + job.pool_part_stride;
+  const int64_t ntok = (int64_t)B * S;
+  uint32_t over = 0;
+
+  for (int64_t r0 = 0; r0 < rows; r0 += kRows) {
+    const RowPos rp = row_pos(job, blk0, rows, r0 + Q, S, H);
+    // ---------------- K: per-channel statistics from the kstats pass
+    if (rp.active) {
+      float y[E];
+      load_transform<D, true>(poolK + rp.pool_row * D + q * E, sb, transform, g.scale, q, y);
+      uint32_t s[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float2 c = kq[h * D + q * E + i];
+        s[i] = (uint32_t)quant_value(y[i], c.x, c.y, lk);
+        over |= s[i];
+      }
+      Packed<E, BITS> pkd;
+      pack_syms<E, BITS>(s, pkd);
+      store_packed<E, BITS>(seg_addr<D, BITS>(job, g, 0, jk, rp.tok, q), pkd);
+    }
+    // ---------------- V: per-token statistics over the heads of a group
+    float y[E];
+    if (rp.active) {
+      load_transform<D, true>(poolV + rp.pool_row * D + q * E, sb, transform, g.scale, q, y);
+      float lmn = y[0], lmx = y[0];
+#pragma unroll
+      for (int i = 1; i < E; ++i) {
+        lmn = fminf(lmn, y[i]);
+        lmx = fmaxf(lmx, y[i]);
+      }
+      lmn = quad_min(lmn);
+      lmx = quad_max(lmx);
+      if (q == 0) rowmm[Q] = make_float2(lmn, lmx);
+    }
+    __syncthreads();
+    if (tid < tpp * G) {
+      const int tp = tid / G, gg = tid % G;
+      const int64_t rr = r0 + (int64_t)tp * H;
+      if (gg < ngroups && rr < rows) {
+        float mn = __builtin_inff(), mx = -__builtin_inff();
+        int lv = 2;
+        for (int k = 0; k < H; ++k) {
+          if (pv.group[k] == gg) {
+            const float2 m = rowmm[tp * H + pv.order[k]];
+            mn = fminf(mn, m.x);
+            mx = fmaxf(mx, m.y);
+            lv = pv.levels[k];
+          }
+        }
+        const float sc = quant_scale(mn, mx, lv);
+        tokq[tid] = make_float2(mn, 1.0f / sc);
+        const RowPos tpz = row_pos(job, blk0, rows, rr, S, H);
+        job.vmeta[(int64_t)gg * ntok + tpz.tok] = (uint16_t)f32_to_bf16_bits(mn);
+        job.vmeta[(int64_t)(G + gg) * ntok + tpz.tok] = (uint16_t)f32_to_bf16_bits(sc);
+      }
+    }
+    __syncthreads();
+    if (rp.active) {
+      const float2 c = tokq[(Q / H) * G + gv];
+      uint32_t s[E];
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        s[i] = (uint32_t)quant_value(y[i], c.x, c.y, lvv);
+        over |= s[i];
+      }
+      Packed<E, BITS> pkd;
+      pack_syms<E, BITS>(s, pkd);
+      store_packed<E, BITS>(seg_addr<D, BITS>(job, g, 1, jv, rp.tok, q), pkd);
+    }
+    __syncthreads();
+  }
+  if (over >> BITS) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
+}
+
+// ============================================================== decode
+template <int D, int BITS>
+__global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                     int32_t* __restrict__ err) {
+  constexpr int E = D / 4;
+  const kvmi_layer_job job = jobs[blockIdx.y];
+  const int B = job.num_blocks;
+  const int nwg = (B + g.bpw - 1) / g.bpw;
+  if ((int)blockIdx.x >= nwg) return;
+  const int H = g.H, S = g.S, HD = H * D, G = g.G;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3;
+
+  __shared__ float2 kd[kMaxHD];  // (min, scale) by source head and channel
+  __shared__ int posk[kMaxH], posv[kMaxH];
+  __shared__ int ok;
+  const Profile pk = part_profile(job.profile, 0, H);
+  const Profile pv = part_profile(job.profile, 1, H);
+  if (tid == 0) {
+    int good = 1;
+    if (!(g.flags & KVMI_F_NO_HEADER)) {
+      const uint8_t* in = job.stream;
+      uint32_t hw[4];
+      for (int i = 0; i < 4; ++i)
+        hw[i] = (uint32_t)in[4 * i] | ((uint32_t)in[4 * i + 1] << 8) | ((uint32_t)in[4 * i + 2] << 16) |
+                ((uint32_t)in[4 * i + 3] << 24);
+      const uint64_t n = (uint64_t)job.chunk_symbols;
+      good = hw[0] == KVMI_MAGIC && hw[1] == (uint32_t)BITS && hw[2] == (uint32_t)(n & 0xffffffffu) &&
+             hw[3] == (uint32_t)(n >> 32);
+      if (!good && blockIdx.x == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
+    }
+    ok = good;
+  }
+  if (tid < H) {
+    for (int k = 0; k < H; ++k) {
+      if (pk.order[k] == tid) posk[tid] = k;
+      if (pv.order[k] == tid) posv[tid] = k;
+    }
+  }
+  __syncthreads();
+  if (!ok) return;
+  for (int i = tid; i < HD; i += kWG) {
+    const int hs = i / D, e = i % D, j = posk[hs];
+    kd[i] = make_float2(bf16_to_f32(job.kmeta[j * D + e]), bf16_to_f32(job.kmeta[HD + j * D + e]));
+  }
+  __syncthreads();
+
+  const int blk0 = blockIdx.x * g.bpw;
+  const int blk1 = min(B, blk0 + g.bpw);
+  const int64_t rows = (int64_t)(blk1 - blk0) * S * H;
+  const int h = Q % H;
+  const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
+  const uint32_t sb = transform ? lane_signs<D>(job.signs, h, q) : 0u;
+  const int jk = posk[h], jv = posv[h];
+  const int gv = pv.group[jv];
+  uint16_t* poolK = reinterpret_cast<uint16_t*>(job.pool);
+  uint16_t* poolV = poolK + job.pool_part_stride;
+  const int64_t ntok = (int64_t)B * S;
+
+  for (int64_t r0 = 0; r0 < rows; r0 += kRows) {
+    const RowPos rp = row_pos(job, blk0, rows, r0 + Q, S, H);
+    if (!rp.active) continue;  // quads are whole: DPP partners share activity
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      const int j = part ? jv : jk;
+      Packed<E, BITS> pkd;
+      load_packed<E, BITS>(seg_addr<D, BITS>(job, g, part, j, rp.tok, q), pkd);
+      uint32_t s[E];
+      unpack_syms<E, BITS>(pkd, s);
+      float x[E];
+      if (part == 0) {
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+          const float2 c = kd[h * D + q * E + i];
+          x[i] = dequant_value((float)s[i], c.x, c.y);
+        }
+      } else {
+        const float mn = bf16_to_f32(job.vmeta[(int64_t)gv * ntok + rp.tok]);
+        const float sc = bf16_to_f32(job.vmeta[(int64_t)(G + gv) * ntok + rp.tok]);
+#pragma unroll
+        for (int i = 0; i < E; ++i) x[i] = dequant_value((float)s[i], mn, sc);
+      }
+      uint32_t w[E / 2];
+      if (transform) {
+        fwht_row<E>(x, q);
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) w[i] = pack_bf16x2(x[2 * i] * g.scale, x[2 * i + 1] * g.scale);
+        apply_sign_bf16<E>(w, sb);
+      } else {
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
+      }
+      store_bf16_seg<E>((part ? poolV : poolK) + rp.pool_row * D + q * E, w);
+    }
+  }
+}
+
+// ============================================================== host side
+int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_blocks, Geo* out) {
+  if (!geom || num_jobs < 0 || max_blocks < 0) return KVMI_EINVAL;
+  const int S = geom->block_size, H = geom->num_heads, D = geom->head_dim, bits = geom->bits;
+  if (S < 1 || H < 1 || H > kMaxH || (kRows % H) != 0) return KVMI_EINVAL;
+  if (D != 64 && D != 128) return KVMI_EINVAL;
+  if (bits < 1 || bits > 8) return KVMI_EINVAL;
+  if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
+  if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
+  if (geom->flags & ~(KVMI_F_NO_TRANSFORM | KVMI_F_NATIVE_LAYOUT | KVMI_F_NO_HEADER)) return KVMI_EINVAL;
+  out->S = S;
+  out->H = H;
+  out->D = D;
+  out->bits = bits;
+  out->flags = geom->flags;
+  out->G = geom->max_groups;
+  out->scale = (float)(1.0 / __builtin_sqrt((double)D));
+  const int rpb = S * H;
+  out->bpw = rpb >= kRows ? 1 : (kRows + rpb - 1) / rpb;
+  return KVMI_OK;
+}
+
+template <int D, int BITS>
+void launch_encode_db(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
+  hipLaunchKernelGGL((encode_kernel<D, BITS>), grid, dim3(kWG), 0, st, g, jobs, err);
+}
+template <int D, int BITS>
+void launch_decode_db(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
+  hipLaunchKernelGGL((decode_kernel<D, BITS>), grid, dim3(kWG), 0, st, g, jobs, err);
+}
+
+template <template <int, int> class F, int D>
+struct BitsDispatch;
+
+#define KVMI_DISPATCH_BITS(FN, D, g, grid, jobs, err, st) \
+  switch ((g).bits) {                                     \
+    case 1: FN<D, 1>(g, grid, jobs, err, st); break;      \
+    case 2: FN<D, 2>(g, grid, jobs, err, st); break;      \
+    case 3: FN<D, 3>(g, grid, jobs, err, st); break;      \
+    case 4: FN<D, 4>(g, grid, jobs, err, st); break;      \
+    case 5: FN<D, 5>(g, grid, jobs, err, st); break;      \
+    case 6: FN<D, 6>(g, grid, jobs, err, st); break;      \
+    case 7: FN<D, 7>(g, grid, jobs, err, st); break;      \
+    default: FN<D, 8>(g, grid, jobs, err, st); break;     \
+  }
+
+}  // namespace
+}  // namespace kvmi
+
+extern "C" int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                                 int32_t max_blocks, int32_t* err, kvmi_stream_t stream) {
+  using namespace kvmi;
+  Geo g;
+  int rc = check_geo(geom, num_jobs, max_blocks, &g);
+  if (rc) return rc;
+  if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
+  if (!jobs || !err) return KVMI_EINVAL;
+  // Statistics need only K: give each workgroup enough blocks that a job has at
+  // most ~16 workgroups, which keeps the global atomics per channel small.
+  const int rpb = g.S * g.H;
+  const int min_bpw = rpb >= kRows ? 1 : (kRows + rpb - 1) / rpb;
+  int bpw = (max_blocks + 15) / 16;
+  g.bpw = bpw < min_bpw ? min_bpw : bpw;
+  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (g.D == 64)
+    hipLaunchKernelGGL((kstats_kernel<64>), grid, dim3(kWG), 0, st, g, jobs, err);
+  else
+    hipLaunchKernelGGL((kstats_kernel<128>), grid, dim3(kWG), 0, st, g, jobs, err);
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+extern "C" int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                                 int32_t max_blocks, int32_t* err, kvmi_stream_t stream) {
+  using namespace kvmi;
+  Geo g;
+  int rc = check_geo(geom, num_jobs, max_blocks, &g);
+  if (rc) return rc;
+  if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
+  if (!jobs || !err) return KVMI_EINVAL;
+  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (g.D == 64) {
+    KVMI_DISPATCH_BITS(launch_encode_db, 64, g, grid, jobs, err, st)
+  } else {
+    KVMI_DISPATCH_BITS(launch_encode_db, 128, g, grid, jobs, err, st)
+  }
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+extern "C" int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                                 int32_t max_blocks, int32_t* err, kvmi_stream_t stream) {
+  using namespace kvmi;
+  Geo g;
+  int rc = check_geo(geom, num_jobs, max_blocks, &g);
+  if (rc) return rc;
+  if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
+  if (!jobs || !err) return KVMI_EINVAL;
+  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (g.D == 64) {
+    KVMI_DISPATCH_BITS(launch_decode_db, 64, g, grid, jobs, err, st)
+  } else {
+    KVMI_DISPATCH_BITS(launch_decode_db, 128, g, grid, jobs, err, st)
+  }
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}

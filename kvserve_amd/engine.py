@@ -1,0 +1,352 @@
+"""Fused paged KV compression engine (host side of kvmi_kstats/encode/decode_paged).
+
+One call compresses every layer of a request straight from vLLM's paged KV caches:
+gather + random-sign FWHT + min-max quantization + bitpack, written into one packed
+stream per layer chunk (the reference's 8-layer chunks above 500 MiB,
+compression_manager.py:229-235, :365-537), plus bf16 metadata.  Decompression is
+the exact inverse and scatters into the caches through the block table.
+
+All work is enqueued on the current torch stream; nothing synchronizes unless the
+caller asks for the device error word (``check_errors``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import threading
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from .profiles import LayerProfile, rademacher_sign_bits
+
+CHUNK_THRESHOLD_BYTES = 500 * 1024 * 1024  # compression_manager.py:230-231
+CHUNK_LAYERS = 8                             # compression_manager.py:235
+DEFAULT_SEED = 0x3333                        # kvserve_transformer.py:253
+
+
+def chunk_ranges(num_layers: int, raw_bytes: int, chunk_layers: int = CHUNK_LAYERS) -> List[Tuple[int, int]]:
+    if raw_bytes > CHUNK_THRESHOLD_BYTES:
+        return [(s, min(s + chunk_layers, num_layers)) for s in range(0, num_layers, chunk_layers)]
+    return [(0, num_layers)]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> int:
+    return 0 if t is None else int(t.data_ptr())
+
+
+def _stream_handle() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class _SignCache:
+    """Per-(seed, layer, H, D) device sign tables, like the reference's signs_cache
+    (hadamard_func.py:130-159)."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._cache: Dict[tuple, torch.Tensor] = {}
+
+    def table(self, seed: int, layer_ids: Sequence[int], H: int, D: int, device) -> torch.Tensor:
+        key = (seed, tuple(layer_ids), H, D, str(device))
+        with self._lock:
+            t = self._cache.get(key)
+        if t is None:
+            host = np.stack([rademacher_sign_bits(seed, l, H, D) for l in layer_ids])
+            t = torch.from_numpy(host.view(np.int32)).to(device)
+            with self._lock:
+                self._cache[key] = t
+        return t
+
+
+SIGNS = _SignCache()
+
+
+@dataclass
+class Packet:
+    """Device-resident result of compressing one request."""
+
+    streams: List[torch.Tensor]          # uint8 per chunk: header + payload
+    chunks: List[Tuple[int, int]]        # layer ranges [start, stop)
+    kmeta: torch.Tensor                  # bf16 [L, 2, H, D]   (min, scale) by output position
+    vmeta: torch.Tensor                  # bf16 [L, 2, G, B*S] (min, scale) by group
+    profiles: List[LayerProfile]
+    num_blocks: int
+    block_size: int
+    num_heads: int
+    head_dim: int
+    bits: int
+    seed: int
+    transform: bool
+    layout: str
+    layer_ids: List[int]
+
+    @property
+    def num_layers(self) -> int:
+        return len(self.profiles)
+
+    def layer_shape(self) -> Tuple[int, int, int, int, int]:
+        return (2, self.num_blocks, self.block_size, self.num_heads, self.head_dim)
+
+    def compressed_bytes(self) -> int:
+        return sum(int(s.numel()) for s in self.streams)
+
+
+class FusedKVCodec:
+    """Fused compress / decompress of paged KV for one worker's geometry.
+
+    Parameters mirror the reference's configuration keys:
+      bits       codec_config.bitpack_bits (bitpack_codec.py:87-91)
+      seed       transformer_config.seed (kvserve_transformer.py:253)
+      transform  "transformer" in the pipeline
+      layout     KVSERVE_CODEC_LAYOUT permuted|native (compression_manager.py:136-140)
+    """
+
+    def __init__(self, num_heads: int, head_dim: int, block_size: int, bits: int = 4,
+                 seed: int = DEFAULT_SEED, transform: bool = True, layout: str = "permuted",
+                 header: bool = True):
+        if type(bits) is not int or not 1 <= bits <= 8:
+            raise ValueError("bitpack_bits must be an integer in [1, 8]")
+        if head_dim not in (64, 128):
+            raise ValueError("head_dim must be 64 or 128")
+        if layout not in ("permuted", "native"):
+            raise ValueError("layout must be 'permuted' or 'native'")
+        if not header and bits != 8:
+            raise ValueError("a stream without header carries raw 8-bit symbols")
+        self.H, self.D, self.S, self.bits = num_heads, head_dim, block_size, bits
+        self.seed, self.transform, self.layout, self.header = int(seed), transform, layout, header
+        self._lib = _lib.load()
+
+    # ---------------------------------------------------------------- helpers
+    def _flags(self) -> int:
+        f = 0
+        if not self.transform:
+            f |= _lib.F_NO_TRANSFORM
+        if self.layout == "native":
+            f |= _lib.F_NATIVE_LAYOUT
+        if not self.header:
+            f |= _lib.F_NO_HEADER
+        return f
+
+    def _geometry(self, groups: int) -> _lib.Geometry:
+        g = _lib.Geometry()
+        g.block_size, g.num_heads, g.head_dim, g.bits = self.S, self.H, self.D, self.bits
+        g.flags, g.max_groups = self._flags(), groups
+        return g
+
+    def _kstats_scratch(self, L: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
+        """uint32 keys [L, 2, H, D] = {0xFFFFFFFF, 0} and counters [L] = 0.  The
+        kernels leave them initialised, so a plan reuses its own set on every run."""
+        keys = torch.empty((L, 2, self.H, self.D), dtype=torch.int32, device=device)
+        keys[:, 0].fill_(-1)
+        keys[:, 1].zero_()
+        cnt = torch.zeros(L, dtype=torch.int32, device=device)
+        return keys, cnt
+
+    def _check_pools(self, pools: Sequence[torch.Tensor]) -> torch.device:
+        if not pools:
+            raise ValueError("at least one layer is required")
+        dev = pools[0].device
+        for p in pools:
+            if p.dtype != torch.bfloat16:
+                raise TypeError("KV caches must be bfloat16")
+            if p.dim() != 5 or p.shape[0] != 2 or tuple(p.shape[2:]) != (self.S, self.H, self.D):
+                raise ValueError(f"KV cache must be [2, num_blocks, {self.S}, {self.H}, {self.D}], got {tuple(p.shape)}")
+            if not p.is_contiguous():
+                raise ValueError("KV caches must be contiguous")
+            if p.device != dev or p.device.type != "cuda":
+                raise ValueError("KV caches must live on one GPU")
+        return dev
+
+    def _block_table(self, block_ids, device, pool_blocks: int) -> torch.Tensor:
+        """int32 device block table; every id is checked against the cache size on
+        the host before a kernel dereferences it (a plan is built once, so the
+        synchronization of a device-tensor check is off the hot path)."""
+        if isinstance(block_ids, torch.Tensor):
+            if block_ids.dim() != 1:
+                raise ValueError("block_ids must be 1-D")
+            ids = block_ids.to(device=device, dtype=torch.int32).contiguous()
+            if ids.numel():
+                lo, hi = int(ids.min().item()), int(ids.max().item())
+                if lo < 0 or hi >= pool_blocks:
+                    raise IndexError("block id outside the KV cache")
+            return ids
+        ids_list = [int(b) for b in block_ids]
+        if ids_list and (min(ids_list) < 0 or max(ids_list) >= pool_blocks):
+            raise IndexError("block id outside the KV cache")
+        return torch.tensor(ids_list, dtype=torch.int32, device=device)
+
+    def _jobs(self, pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, cnt, B) -> torch.Tensor:
+        L = len(pools)
+        H, D, S = self.H, self.D, self.S
+        per_layer = 2 * H * B * S * D
+        rows = np.zeros((L, _lib.JOB_INT64S), dtype=np.int64)
+        ci = 0
+        for l in range(L):
+            while not (chunks[ci][0] <= l < chunks[ci][1]):
+                ci += 1
+            start, stop = chunks[ci]
+            rows[l, 0] = _ptr(pools[l])
+            rows[l, 1] = _ptr(ids)
+            rows[l, 2] = _ptr(streams[ci])
+            rows[l, 3] = _ptr(kmeta[l])
+            rows[l, 4] = _ptr(vmeta[l])
+            rows[l, 5] = _ptr(signs[l]) if signs is not None else 0
+            rows[l, 6] = _ptr(prof_dev[l])
+            rows[l, 7] = _ptr(keys[l])
+            rows[l, 8] = _ptr(cnt[l:l + 1])
+            rows[l, 9] = pools[l].shape[1] * S * H * D
+            rows[l, 10] = (l - start) * per_layer
+            rows[l, 11] = (stop - start) * per_layer
+            rows[l, 12] = B | ((1 if l == start else 0) << 32)
+        return torch.from_numpy(rows).to(pools[0].device, non_blocking=False)
+
+    # ---------------------------------------------------------------- plans
+    def plan_compress(self, pools: Sequence[torch.Tensor], block_ids, profiles: Sequence[LayerProfile],
+                      layer_ids: Optional[Sequence[int]] = None, chunk_layers: Optional[int] = None) -> "Plan":
+        """Allocate the outputs and device descriptors for compressing blocks
+        `block_ids` of every layer cache in `pools` (one tensor [2, P, S, H, D] per
+        layer, vLLM FlashAttention NHD layout).  `run` then enqueues the kernels.
+
+        layer_ids: the reference's layer index of each pool (sign seeds); by default
+        0..L-1, the position in the connector's sorted layer list.
+        chunk_layers: layers per stream; default = the reference's rule (one stream,
+        or 8-layer chunks above 500 MiB); 0 = one stream."""
+        dev = self._check_pools(pools)
+        L = len(pools)
+        if len(profiles) != L:
+            raise ValueError("one profile per layer is required")
+        for p in profiles:
+            p.validate(self.H)
+        layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
+        ids = self._block_table(block_ids, dev, pools[0].shape[1])
+        B = int(ids.numel())
+        H, D, S = self.H, self.D, self.S
+        raw = L * 2 * B * S * H * D * 2
+        if chunk_layers == 0:
+            chunks = [(0, L)]
+        else:
+            chunks = chunk_ranges(L, raw, chunk_layers or CHUNK_LAYERS)
+        G = max(p.num_v_groups() for p in profiles)
+        hdr = 16 if self.header else 0
+        streams = []
+        for s, e in chunks:
+            n = (e - s) * 2 * H * B * S * D
+            streams.append(torch.empty(hdr + (n * self.bits + 7) // 8, dtype=torch.uint8, device=dev))
+        kmeta = torch.empty((L, 2, H, D), dtype=torch.bfloat16, device=dev)
+        vmeta = torch.empty((L, 2, G, B * S), dtype=torch.bfloat16, device=dev)
+        packet = Packet(streams, chunks, kmeta, vmeta, list(profiles), B, S, H, D, self.bits, self.seed,
+                        self.transform, self.layout, layer_ids)
+        if B == 0 and self.header:
+            for st in streams:
+                st.copy_(torch.from_numpy(_header_bytes(self.bits, 0)).to(dev))
+        return Plan(self, "compress", list(pools), ids, packet)
+
+    def plan_decompress(self, packet: Packet, pools: Sequence[torch.Tensor], block_ids) -> "Plan":
+        """Descriptors for writing `packet` into `pools` at `block_ids` (only the
+        first packet.num_blocks ids are used, kv_utils.py:100-106)."""
+        dev = self._check_pools(pools)
+        if len(pools) != packet.num_layers:
+            raise ValueError("one KV cache per compressed layer is required")
+        if (packet.bits, packet.num_heads, packet.head_dim, packet.block_size) != (self.bits, self.H, self.D, self.S):
+            raise ValueError("packet geometry does not match this codec")
+        if (packet.seed, packet.transform, packet.layout) != (self.seed, self.transform, self.layout):
+            raise ValueError("packet transform / layout does not match this codec")
+        ids = self._block_table(block_ids, dev, pools[0].shape[1])
+        if ids.numel() < packet.num_blocks:
+            raise ValueError("fewer block ids than compressed blocks")
+        ids = ids[: packet.num_blocks].contiguous()
+        hdr = 16 if self.header else 0
+        for (s, e), st in zip(packet.chunks, packet.streams):
+            n = (e - s) * 2 * self.H * packet.num_blocks * self.S * self.D
+            if st.dtype != torch.uint8 or st.dim() != 1:
+                raise TypeError("packed streams are 1-D uint8 tensors")
+            if st.numel() != hdr + (n * self.bits + 7) // 8:
+                raise ValueError("BitPackCodec payload length does not match shape and bit width")
+            if st.device != dev:
+                raise ValueError("BitPackCodec decodes on the payload's CUDA device")
+        return Plan(self, "decompress", list(pools), ids, packet)
+
+    # ---------------------------------------------------------------- one-shot API
+    def compress(self, pools: Sequence[torch.Tensor], block_ids, profiles: Sequence[LayerProfile],
+                 layer_ids: Optional[Sequence[int]] = None, chunk_layers: Optional[int] = None) -> Packet:
+        plan = self.plan_compress(pools, block_ids, profiles, layer_ids, chunk_layers)
+        plan.run()
+        return plan.packet
+
+    def decompress(self, packet: Packet, pools: Sequence[torch.Tensor], block_ids) -> None:
+        self.plan_decompress(packet, pools, block_ids).run()
+
+
+class Plan:
+    """Device descriptors of one compress or decompress of one request.  `run()`
+    enqueues the kernels on the current stream (two launches to compress, one to
+    decompress) and can be repeated; the outputs are overwritten in place."""
+
+    def __init__(self, codec: FusedKVCodec, kind: str, pools, ids: torch.Tensor, packet: Packet):
+        self.codec, self.kind, self.pools, self.ids, self.packet = codec, kind, pools, ids, packet
+        dev = pools[0].device
+        self.device = dev
+        L, B = len(pools), packet.num_blocks
+        self.num_jobs, self.max_blocks = L, B
+        self.signs = None
+        if codec.transform:
+            self.signs = SIGNS.table(codec.seed, packet.layer_ids, codec.H, codec.D, dev)
+        self.prof = torch.from_numpy(np.stack([p.to_array() for p in packet.profiles])).to(dev)
+        self.keys, self.cnt = codec._kstats_scratch(L, dev)
+        self.jobs = codec._jobs(pools, ids, packet.streams, packet.chunks, packet.kmeta, packet.vmeta,
+                                self.signs, self.prof, self.keys, self.cnt, B)
+        self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.geo = codec._geometry(packet.vmeta.shape[2])
+        packet.__dict__["_err"] = self.err
+
+    def launches(self) -> List[str]:
+        """Names of the C entry points one run() enqueues, in order."""
+        if self.max_blocks == 0:
+            return []
+        return ["kvmi_kstats_paged", "kvmi_encode_paged"] if self.kind == "compress" else ["kvmi_decode_paged"]
+
+    def launch(self, name: str) -> None:
+        """Enqueue one of launches() on the current stream."""
+        fn = getattr(self.codec._lib, name)
+        with torch.cuda.device(self.device):
+            _lib.check(fn(ctypes.byref(self.geo), _ptr(self.jobs), self.num_jobs, self.max_blocks, _ptr(self.err),
+                          _stream_handle()), name)
+
+    def run(self) -> None:
+        for name in self.launches():
+            self.launch(name)
+
+    def error_code(self) -> int:
+        """Synchronizes the stream and returns the sticky device error word."""
+        return int(self.err.item())
+
+    def check_errors(self) -> None:
+        raise_device_error(self.error_code())
+
+
+def raise_device_error(code: int) -> None:
+    """Raise the reference's device-assert messages (bitpack_codec.py:32, :38, :60)."""
+    if code & _lib.ERR_SYMBOL_RANGE:
+        raise RuntimeError("symbol exceeds bitpack_bits")
+    if code & _lib.ERR_BAD_HEADER:
+        raise RuntimeError("invalid bitpack header or decode configuration")
+
+
+def check_packet(packet: Packet) -> None:
+    """Synchronize on the packet's last run and raise on a device data error."""
+    err = packet.__dict__.get("_err")
+    if err is not None:
+        raise_device_error(int(err.item()))
+
+
+def _header_bytes(bits: int, n: int) -> np.ndarray:
+    h = np.zeros(16, np.uint8)
+    h[0:4] = np.frombuffer(np.uint32(0x0150424B).tobytes(), np.uint8)
+    h[4] = bits
+    h[8:16] = np.frombuffer(np.uint64(n).tobytes(), np.uint8)
+    return h

@@ -1,0 +1,156 @@
+"""Torch-level wrappers of the unit C-ABI entry points (bitpack, gather / scatter,
+Hadamard).  Each enqueues on the current stream of the tensors' device.
+
+Device data errors (a symbol wider than the bit width, a header that does not match)
+are reported through a device error word.  By default the wrappers synchronize and
+raise, which is the loud failure of the reference's device asserts
+(bitpack_codec.py:32, :38, :60); set ``KVSERVE_AMD_CHECK_ERRORS=0`` (or pass
+``check=False``) to keep calls asynchronous, and no check is made while a stream is
+being captured into a graph.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from .engine import SIGNS, raise_device_error
+
+HEADER_BYTES = 16
+
+
+def _check_default() -> bool:
+    return os.environ.get("KVSERVE_AMD_CHECK_ERRORS", "1") != "0"
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _maybe_check(err: torch.Tensor, check: Optional[bool]) -> None:
+    if check is None:
+        check = _check_default()
+    if check and not torch.cuda.is_current_stream_capturing():
+        raise_device_error(int(err.item()))
+
+
+def _bits(bits) -> int:
+    if type(bits) is not int or not 1 <= bits <= 8:
+        raise ValueError("bitpack_bits must be an integer in [1, 8]")
+    return bits
+
+
+def bitpack_encode(sym: torch.Tensor, bits: int, check: Optional[bool] = None) -> torch.Tensor:
+    """BitPackCodec.encode (bitpack_codec.py:100-110): 1-D uint8 stream of
+    16 + ceil(n*bits/8) bytes for the contiguous flattening of `sym`."""
+    bits = _bits(bits)
+    if not isinstance(sym, torch.Tensor) or sym.dtype != torch.uint8:
+        raise TypeError("BitPackCodec requires a torch.uint8 tensor")
+    if not sym.is_cuda:
+        raise ValueError("BitPackCodec requires a CUDA tensor")
+    src = sym.contiguous()
+    n = src.numel()
+    out = torch.empty(HEADER_BYTES + (n * bits + 7) // 8, dtype=torch.uint8, device=src.device)
+    err = torch.zeros(1, dtype=torch.int32, device=src.device)
+    with torch.cuda.device(src.device):
+        _lib.check(_lib.load().kvmi_bitpack_encode(src.data_ptr() if n else None, n, bits, out.data_ptr(),
+                                                   err.data_ptr(), _stream()), "kvmi_bitpack_encode")
+    _maybe_check(err, check)
+    return out
+
+
+def bitpack_decode(stream: torch.Tensor, shape: Sequence[int], bits: int, check: Optional[bool] = None) -> torch.Tensor:
+    """BitPackCodec.decode (bitpack_codec.py:112-135): uint8 tensor of `shape`."""
+    bits = _bits(bits)
+    if not isinstance(stream, torch.Tensor) or stream.dtype != torch.uint8:
+        raise TypeError("BitPackCodec requires a torch.uint8 tensor")
+    if not stream.is_cuda:
+        raise ValueError("BitPackCodec requires a CUDA tensor")
+    if any(type(d) is not int or d < 0 for d in shape):
+        raise ValueError("original_shape must contain nonnegative integers")
+    n = math.prod(shape)
+    if stream.numel() != HEADER_BYTES + (n * bits + 7) // 8:
+        raise ValueError("BitPackCodec payload length does not match shape and bit width")
+    src = stream.contiguous()
+    out = torch.empty(list(shape), dtype=torch.uint8, device=src.device)
+    err = torch.zeros(1, dtype=torch.int32, device=src.device)
+    with torch.cuda.device(src.device):
+        _lib.check(_lib.load().kvmi_bitpack_decode(src.data_ptr(), src.numel(), n, bits,
+                                                   out.data_ptr() if n else None, err.data_ptr(), _stream()),
+                   "kvmi_bitpack_decode")
+    _maybe_check(err, check)
+    return out
+
+
+def _pool_check(pool: torch.Tensor) -> None:
+    if pool.dim() < 3 or pool.shape[0] != 2:
+        raise RuntimeError(f"Unsupported KV layout shape: {tuple(pool.shape)}")
+    if pool.element_size() != 2 or not pool.is_contiguous() or not pool.is_cuda:
+        raise ValueError("paged gather/scatter needs a contiguous 16-bit CUDA KV cache")
+
+
+def _ids(block_ids, pool: torch.Tensor) -> torch.Tensor:
+    if isinstance(block_ids, torch.Tensor):
+        ids = block_ids.to(device=pool.device, dtype=torch.int32).contiguous()
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= pool.shape[1]):
+            raise IndexError("block id outside the KV cache")
+        return ids
+    ids_list = [int(b) for b in block_ids]
+    if ids_list and (min(ids_list) < 0 or max(ids_list) >= pool.shape[1]):
+        raise IndexError("block id outside the KV cache")
+    return torch.tensor(ids_list, dtype=torch.int32, device=pool.device)
+
+
+def gather_blocks(pool: torch.Tensor, block_ids) -> torch.Tensor:
+    """extract_kv_from_layer_by_blocks (kv_utils.py:59-80), FlashAttention layout
+    [2, num_blocks, ...]: returns pool[:, block_ids] as a new contiguous tensor."""
+    _pool_check(pool)
+    ids = _ids(block_ids, pool)
+    out = torch.empty((2, ids.numel()) + tuple(pool.shape[2:]), dtype=pool.dtype, device=pool.device)
+    blk = math.prod(pool.shape[2:])
+    with torch.cuda.device(pool.device):
+        _lib.check(_lib.load().kvmi_gather_blocks(pool.data_ptr(), pool.shape[1] * blk, ids.data_ptr(), ids.numel(),
+                                                  blk, out.data_ptr(), _stream()), "kvmi_gather_blocks")
+    return out
+
+
+def scatter_blocks(pool: torch.Tensor, payload: torch.Tensor, block_ids) -> None:
+    """inject_kv_into_layer_by_blocks (kv_utils.py:83-119): pool[:, ids[:nb]] = payload."""
+    _pool_check(pool)
+    n_ids = block_ids.numel() if isinstance(block_ids, torch.Tensor) else len(block_ids)
+    if n_ids == 0:
+        return
+    ids = _ids(block_ids, pool)
+    src = payload.to(device=pool.device, dtype=pool.dtype).contiguous()
+    nb = src.shape[1]
+    ids = ids[:nb].contiguous()
+    if ids.numel() < nb or tuple(src.shape[2:]) != tuple(pool.shape[2:]):
+        raise ValueError("payload does not match the KV cache blocks")
+    blk = math.prod(pool.shape[2:])
+    with torch.cuda.device(pool.device):
+        _lib.check(_lib.load().kvmi_scatter_blocks(pool.data_ptr(), pool.shape[1] * blk, ids.data_ptr(), nb, blk,
+                                                   src.data_ptr(), _stream()), "kvmi_scatter_blocks")
+
+
+def hadamard(x: torch.Tensor, layer_id: int, seed: int, inverse: bool = False,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """HadamardTransform.transform / .inverse (hadamard_func.py:161-231) of a bf16
+    tensor [..., H, D] with the signs of (seed, layer_id)."""
+    if x.dtype != torch.bfloat16 or not x.is_cuda:
+        raise TypeError("the Hadamard transform takes a bf16 CUDA tensor")
+    H, D = x.shape[-2], x.shape[-1]
+    src = x.contiguous()
+    dst = torch.empty_like(src) if out is None else out
+    if dst.shape != src.shape or not dst.is_contiguous() or dst.dtype != torch.bfloat16:
+        raise ValueError("out must be a contiguous bf16 tensor of the input's shape")
+    signs = SIGNS.table(int(seed), [int(layer_id)], H, D, src.device)
+    rows = src.numel() // D
+    with torch.cuda.device(src.device):
+        _lib.check(_lib.load().kvmi_hadamard(src.data_ptr(), dst.data_ptr(), rows, H, D, signs.data_ptr(),
+                                             1 if inverse else 0, _stream()), "kvmi_hadamard")
+    return dst

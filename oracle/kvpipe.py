@@ -1,0 +1,372 @@
+"""numpy restatement of KVServe's modular compression pipeline (test oracle).
+
+TEST INFRASTRUCTURE ONLY -- see oracle/__init__.py.  bf16 tensors are carried as
+uint16 bit patterns; every elementwise bf16 op of the reference is computed in
+float32 (IEEE round-to-nearest-even, as torch does on CPU and GPU) and rounded to
+bf16 before the next op.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+HEADER_BYTES = 16
+MAGIC = 0x0150424B
+CHUNK_THRESHOLD_BYTES = 500 * 1024 * 1024  # compression_manager.py:230-231
+CHUNK_LAYERS = 8  # compression_manager.py:235
+
+
+# ------------------------------------------------------------------ bf16
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round-to-nearest-even (finite inputs)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = ((u >> 16) & 1) + np.uint32(0x7FFF)
+    return ((u + r) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def rbf(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to bf16 values (kept as float32)."""
+    return bf16_to_f32(f32_to_bf16(x))
+
+
+# ------------------------------------------------------------------ signs
+def rademacher_signs(base_seed: int, layer_id: int, num_heads: int, head_dim: int) -> np.ndarray:
+    """[H, D] float32 of +-1.  hadamard_func.py:33-48 and :137-152: one CPU generator
+    re-seeded with base_seed ^ (layer << 16) ^ head, then randint(0, 2, (D,), int8)*2-1."""
+    import torch
+
+    gen = torch.Generator(device="cpu")
+    rows = []
+    for h in range(num_heads):
+        gen.manual_seed(base_seed ^ (layer_id << 16) ^ h)
+        s = torch.randint(0, 2, (head_dim,), generator=gen, dtype=torch.int8)
+        rows.append(s.numpy().astype(np.float32) * 2 - 1)
+    return np.stack(rows)
+
+
+def sign_bits(signs: np.ndarray) -> np.ndarray:
+    """[H, D] +-1 -> [H, D/32] uint32, bit (d % 32) of word d // 32 set when sign is -1."""
+    neg = (signs < 0).astype(np.uint64)
+    H, D = signs.shape
+    w = neg.reshape(H, D // 32, 32) << np.arange(32, dtype=np.uint64)
+    return w.sum(axis=2).astype(np.uint32)
+
+
+# ------------------------------------------------------------------ FWHT
+def fwht_f32(x: np.ndarray) -> np.ndarray:
+    """Unnormalised Walsh-Hadamard transform over the last axis in float32, natural
+    (Sylvester) order, radix-2 stages from the lowest index bit up."""
+    y = np.array(x, dtype=np.float32, copy=True)
+    D = y.shape[-1]
+    assert D & (D - 1) == 0, "power-of-two head_dim"
+    lead = y.shape[:-1]
+    h = 1
+    while h < D:
+        v = y.reshape(*lead, D // (2 * h), 2, h)
+        a = v[..., 0, :].copy()
+        b = v[..., 1, :]
+        v[..., 0, :] = a + b
+        v[..., 1, :] = a - b
+        h *= 2
+    return y
+
+
+def _scale(D: int) -> np.float32:
+    return np.float32(1.0 / math.sqrt(D))  # hadamard_func.py:98 scale=1/sqrt(size)
+
+
+def hadamard_forward(x_bits: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """bf16 [..., H, D] -> bf16.  hadamard_func.py:161-197: x*s (exact in bf16), FWHT
+    with scale 1/sqrt(D) in fp32, one bf16 rounding."""
+    x = bf16_to_f32(x_bits) * signs
+    D = x.shape[-1]
+    return f32_to_bf16(fwht_f32(x) * _scale(D))
+
+
+def hadamard_inverse(y_bits: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """hadamard_func.py:199-231: FWHT (rounded to bf16) first, then * signs."""
+    y = bf16_to_f32(y_bits)
+    D = y.shape[-1]
+    z = rbf(fwht_f32(y) * _scale(D))
+    return f32_to_bf16(z * signs)
+
+
+# ------------------------------------------------------------------ quantizer
+_FLOOR = float(bf16_to_f32(f32_to_bf16(np.array([1e-5], np.float32)))[0])
+
+
+def section_scale(mn: np.ndarray, mx: np.ndarray, max_value: int) -> np.ndarray:
+    """quantizer_func.py:56: bf16 (max-min).clamp_(min=1e-5).div_(max_value-1)."""
+    d = rbf(mx - mn)
+    d = np.where(d < np.float32(1e-5), np.float32(_FLOOR), d).astype(np.float32)
+    return rbf(d / np.float32(max_value - 1))
+
+
+def quantize(max_value: int, x: np.ndarray, axis: str) -> Tuple[np.ndarray, Optional[np.ndarray], Optional[np.ndarray]]:
+    """quantizer_func.py:9-75 on a bf16-valued float32 tensor [B, S, Hg, D].
+    Returns (uint8 symbols, min, scale) with min/scale keepdim-shaped bf16 values,
+    or (empty, None, None) for an empty section."""
+    if x.size == 0:
+        return x.astype(np.uint8), None, None
+    dims = {"channel": (0, 1), "token": (2, 3), "tensor": (0, 1, 2, 3)}[axis]
+    mx = x.max(axis=dims, keepdims=True)
+    mn = x.min(axis=dims, keepdims=True)
+    sc = section_scale(mn, mx, max_value)
+    t = rbf(x - mn)
+    q = rbf(t / sc)
+    sym = np.clip(np.rint(q), 0, max_value).astype(np.uint8)
+    return sym, mn, sc
+
+
+def dequantize(sym: np.ndarray, mn: Optional[np.ndarray], sc: Optional[np.ndarray]) -> np.ndarray:
+    """quantizer_func.py:77-113: bf16(bf16(q * scale) + min)."""
+    q = sym.astype(np.float32)
+    if mn is None:
+        return q
+    return rbf(rbf(q * sc) + mn)
+
+
+# ------------------------------------------------------------------ masks / profiles
+def head_mask_from_scores(scores: np.ndarray, hybrid_ratio: float) -> np.ndarray:
+    """kvserve_quantizer.py:58-63: the round(numel*ratio) lowest scores are low precision."""
+    n_low = int(round(scores.size * hybrid_ratio))
+    flat = np.argsort(scores.reshape(-1), kind="stable")[:n_low]
+    mask = np.zeros(scores.size, dtype=bool)
+    mask[flat] = True
+    return mask.reshape(scores.shape)
+
+
+def layer_mask(num_layers: int) -> np.ndarray:
+    """kvserve_quantizer.py:65-68: the last round(0.33*L) layers are low precision."""
+    m = np.zeros(num_layers, dtype=bool)
+    n = int(round(num_layers * 0.33))
+    if n:
+        m[-n:] = True
+    return m
+
+
+@dataclass
+class PartProfile:
+    """Output head order, levels and V statistic groups of one part of one layer."""
+
+    order: List[int]   # source head at output position j
+    levels: List[int]  # max_value at output position j
+    group: List[int]   # statistic group of output position j (contiguous runs)
+
+
+@dataclass
+class LayerProfile:
+    k: PartProfile
+    v: PartProfile
+
+
+def head_split_profile(low_mask_row: Sequence[bool], hk: int, hv: int, lk: int, lv: int) -> LayerProfile:
+    """split_func.py:40-72 + kvserve_quantizer.py:210-220: [low asc, high asc]."""
+    low = [h for h, m in enumerate(low_mask_row) if m]
+    high = [h for h, m in enumerate(low_mask_row) if not m]
+    order = low + high
+    grp = [0] * len(low) + [1 if low else 0] * len(high)
+    return LayerProfile(
+        PartProfile(order, [lk] * len(low) + [hk] * len(high), grp),
+        PartProfile(order, [lv] * len(low) + [hv] * len(high), grp),
+    )
+
+
+def layer_split_profile(is_low: bool, H: int, hk: int, hv: int, lk: int, lv: int) -> LayerProfile:
+    """split_func.py:9-38: the whole layer is one section."""
+    order = list(range(H))
+    return LayerProfile(
+        PartProfile(order, [lk if is_low else hk] * H, [0] * H),
+        PartProfile(order, [lv if is_low else hv] * H, [0] * H),
+    )
+
+
+# ------------------------------------------------------------------ one layer
+@dataclass
+class LayerMeta:
+    """Quantization metadata of one layer as bf16 values (float32 arrays).
+    kmin/kscale: [H', D] by output position.  vmin/vscale: [G, B*S] by group."""
+
+    kmin: np.ndarray
+    kscale: np.ndarray
+    vmin: np.ndarray
+    vscale: np.ndarray
+
+
+def quantize_layer(y: np.ndarray, prof: LayerProfile) -> Tuple[np.ndarray, LayerMeta]:
+    """KVServeQuantizer.quantize (kvserve_quantizer.py:171-233) generalised to any
+    number of contiguous statistic groups: K per channel (stats per output position),
+    V per token over the heads of a group.  y: bf16-valued float32 [2, B, S, H, D].
+    Returns uint8 [2, B, S, H', D] with heads in output order, and metadata."""
+    _, B, S, H, D = y.shape
+    out = np.empty(y.shape, dtype=np.uint8)
+    kmin = np.empty((H, D), np.float32)
+    ksc = np.empty((H, D), np.float32)
+    kx = y[0][:, :, prof.k.order, :]
+    # K: channel stats are per head, levels per output position
+    for j in range(H):
+        sym, mn, sc = quantize(prof.k.levels[j], kx[:, :, j : j + 1, :], "channel")
+        out[0, :, :, j : j + 1, :] = sym
+        kmin[j], ksc[j] = mn[0, 0, 0], sc[0, 0, 0]
+    vx = y[1][:, :, prof.v.order, :]
+    groups = sorted(set(prof.v.group))
+    vmin = np.empty((len(groups), B * S), np.float32)
+    vsc = np.empty((len(groups), B * S), np.float32)
+    for g in groups:
+        js = [j for j in range(H) if prof.v.group[j] == g]
+        lo, hi = js[0], js[-1] + 1
+        assert js == list(range(lo, hi)), "groups are contiguous runs of output positions"
+        sym, mn, sc = quantize(prof.v.levels[lo], vx[:, :, lo:hi, :], "token")
+        out[1, :, :, lo:hi, :] = sym
+        vmin[g], vsc[g] = mn.reshape(-1), sc.reshape(-1)
+    return out, LayerMeta(kmin, ksc, vmin, vsc)
+
+
+def dequantize_layer(sym: np.ndarray, meta: LayerMeta, prof: LayerProfile) -> np.ndarray:
+    """KVServeQuantizer.dequantize (kvserve_quantizer.py:235-294): returns bf16-valued
+    float32 [2, B, S, H, D] in source head order."""
+    _, B, S, H, D = sym.shape
+    out = np.empty(sym.shape, np.float32)
+    kx = dequantize(sym[0], meta.kmin[None, None], meta.kscale[None, None])
+    out[0][:, :, prof.k.order, :] = kx
+    vd = np.empty((B, S, H, D), np.float32)
+    for g in range(meta.vmin.shape[0]):
+        js = [j for j in range(H) if prof.v.group[j] == g]
+        mn = meta.vmin[g].reshape(B, S, 1, 1)
+        sc = meta.vscale[g].reshape(B, S, 1, 1)
+        vd[:, :, js, :] = dequantize(sym[1][:, :, js, :], mn, sc)
+    out[1][:, :, prof.v.order, :] = vd
+    return out
+
+
+# ------------------------------------------------------------------ bitpack
+def bitpack_encode(sym: np.ndarray, bits: int) -> np.ndarray:
+    """bitpack_codec.py:24-47,100-110: header + LSB-first packing of the flattened symbols."""
+    s = np.ascontiguousarray(sym, dtype=np.uint8).reshape(-1)
+    if np.any(s >> bits):
+        raise ValueError("symbol exceeds bitpack_bits")
+    n = s.size
+    hdr = np.zeros(HEADER_BYTES, np.uint8)
+    hdr[0:4] = np.frombuffer(np.uint32(MAGIC).tobytes(), np.uint8)
+    hdr[4] = bits
+    hdr[8:16] = np.frombuffer(np.uint64(n).tobytes(), np.uint8)
+    if n == 0:
+        return hdr
+    bitsarr = np.unpackbits(s[:, None], axis=1, count=bits, bitorder="little").reshape(-1)
+    payload = np.packbits(bitsarr, bitorder="little")
+    assert payload.size == (n * bits + 7) // 8
+    return np.concatenate([hdr, payload])
+
+
+def bitpack_decode(stream: np.ndarray, n: int, bits: int) -> np.ndarray:
+    """bitpack_codec.py:50-69,112-135 (header and length checked)."""
+    stream = np.asarray(stream, np.uint8)
+    if stream.size != HEADER_BYTES + (n * bits + 7) // 8:
+        raise ValueError("BitPackCodec payload length does not match shape and bit width")
+    expect = bitpack_encode(np.zeros(0, np.uint8), bits)
+    expect[8:16] = np.frombuffer(np.uint64(n).tobytes(), np.uint8)
+    if not np.array_equal(stream[:HEADER_BYTES], expect):
+        raise ValueError("invalid bitpack header or decode configuration")
+    if n == 0:
+        return np.zeros(0, np.uint8)
+    b = np.unpackbits(stream[HEADER_BYTES:], bitorder="little")[: n * bits].reshape(n, bits)
+    return (b.astype(np.uint8) << np.arange(bits, dtype=np.uint8)).sum(axis=1).astype(np.uint8)
+
+
+# ------------------------------------------------------------------ paged I/O
+def gather_blocks(pool: np.ndarray, block_ids: Sequence[int]) -> np.ndarray:
+    """kv_utils.py:59-80 (FlashAttention NHD layout): kv[:, idx].clone()."""
+    return pool[:, np.asarray(block_ids, dtype=np.int64)].copy()
+
+
+def scatter_blocks(pool: np.ndarray, payload: np.ndarray, block_ids: Sequence[int]) -> None:
+    """kv_utils.py:83-119: kv[:, idx[:num_blocks]] = payload."""
+    idx = np.asarray(block_ids, dtype=np.int64)[: payload.shape[1]]
+    pool[:, idx] = payload
+
+
+# ------------------------------------------------------------------ request level
+def chunk_ranges(num_layers: int, raw_bytes: int) -> List[Tuple[int, int]]:
+    """compression_manager.py:229-235, :383-390: one chunk, or 8-layer chunks above 500 MiB."""
+    if raw_bytes > CHUNK_THRESHOLD_BYTES:
+        return [(s, min(s + CHUNK_LAYERS, num_layers)) for s in range(0, num_layers, CHUNK_LAYERS)]
+    return [(0, num_layers)]
+
+
+@dataclass
+class Chunk:
+    start: int
+    stop: int
+    symbols: np.ndarray       # uint8 codec buffer [l, 2, H', B, S, D] (permuted) or [l,2,B,S,H',D]
+    stream: np.ndarray        # packed bytes with header
+    metas: List[LayerMeta]
+
+
+def compress_request(
+    pools: Sequence[np.ndarray],
+    block_ids: Sequence[int],
+    profiles: Sequence[LayerProfile],
+    base_seed: int,
+    bits: int,
+    transform: bool = True,
+    layout: str = "permuted",
+) -> List[Chunk]:
+    """Gather every layer (kv_utils.py:59-80), then compress_all_layers
+    (compression_manager.py:200-537): per layer transform (KVServeTransformer,
+    kvserve_transformer.py:268-274) and quantize, codec-buffer layout (:155-164),
+    and one bitpack stream per chunk."""
+    L = len(pools)
+    _, _, S, H, D = pools[0].shape
+    B = len(block_ids)
+    raw = L * 2 * B * S * H * D * 2
+    chunks = []
+    for s, e in chunk_ranges(L, raw):
+        syms, metas = [], []
+        for l in range(s, e):
+            x = gather_blocks(pools[l], block_ids)
+            if transform:
+                sg = rademacher_signs(base_seed, l, H, D)
+                y = np.stack([bf16_to_f32(hadamard_forward(x[p], sg)) for p in (0, 1)])
+            else:
+                y = bf16_to_f32(x)
+            sym, meta = quantize_layer(y, profiles[l])
+            syms.append(sym.transpose(0, 3, 1, 2, 4) if layout == "permuted" else sym)
+            metas.append(meta)
+        buf = np.ascontiguousarray(np.stack(syms))
+        chunks.append(Chunk(s, e, buf, bitpack_encode(buf, bits), metas))
+    return chunks
+
+
+def decompress_request(
+    chunks: Sequence[Chunk],
+    pools: Sequence[np.ndarray],
+    block_ids: Sequence[int],
+    profiles: Sequence[LayerProfile],
+    base_seed: int,
+    bits: int,
+    transform: bool = True,
+    layout: str = "permuted",
+) -> None:
+    """decompress_all_layers (compression_manager.py:539-757) then
+    inject_kv_into_layer_by_blocks (kv_utils.py:83-119), into `pools` in place."""
+    for ch in chunks:
+        shape = ch.symbols.shape
+        buf = bitpack_decode(ch.stream, int(np.prod(shape)), bits).reshape(shape)
+        for i, l in enumerate(range(ch.start, ch.stop)):
+            sym = buf[i].transpose(0, 2, 3, 1, 4) if layout == "permuted" else buf[i]
+            x = dequantize_layer(sym, ch.metas[i], profiles[l])
+            H, D = x.shape[-2], x.shape[-1]
+            if transform:
+                sg = rademacher_signs(base_seed, l, H, D)
+                xb = np.stack([hadamard_inverse(f32_to_bf16(x[p]), sg) for p in (0, 1)])
+            else:
+                xb = f32_to_bf16(x)
+            scatter_blocks(pools[l], xb, block_ids)
