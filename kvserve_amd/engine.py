@@ -227,10 +227,12 @@ class FusedKVCodec:
         B = int(ids.numel())
         H, D, S = self.H, self.D, self.S
         raw = L * 2 * B * S * H * D * 2
-        if chunk_layers == 0:
+        if chunk_layers is None:
+            chunks = chunk_ranges(L, raw)
+        elif chunk_layers == 0:
             chunks = [(0, L)]
         else:
-            chunks = chunk_ranges(L, raw, chunk_layers or CHUNK_LAYERS)
+            chunks = [(s, min(s + chunk_layers, L)) for s in range(0, L, chunk_layers)]
         G = max(p.num_v_groups() for p in profiles)
         hdr = 16 if self.header else 0
         streams = []

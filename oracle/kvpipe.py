@@ -318,22 +318,26 @@ def compress_request(
     bits: int,
     transform: bool = True,
     layout: str = "permuted",
+    layer_ids: Optional[Sequence[int]] = None,
+    chunks: Optional[Sequence[Tuple[int, int]]] = None,
 ) -> List[Chunk]:
     """Gather every layer (kv_utils.py:59-80), then compress_all_layers
     (compression_manager.py:200-537): per layer transform (KVServeTransformer,
     kvserve_transformer.py:268-274) and quantize, codec-buffer layout (:155-164),
-    and one bitpack stream per chunk."""
+    and one bitpack stream per chunk.  layer_ids: sign seed layer of each pool
+    (default 0..L-1); chunks: explicit layer ranges (default: the reference's rule)."""
     L = len(pools)
     _, _, S, H, D = pools[0].shape
     B = len(block_ids)
     raw = L * 2 * B * S * H * D * 2
-    chunks = []
-    for s, e in chunk_ranges(L, raw):
+    lids = list(range(L)) if layer_ids is None else list(layer_ids)
+    out = []
+    for s, e in (chunk_ranges(L, raw) if chunks is None else chunks):
         syms, metas = [], []
         for l in range(s, e):
             x = gather_blocks(pools[l], block_ids)
             if transform:
-                sg = rademacher_signs(base_seed, l, H, D)
+                sg = rademacher_signs(base_seed, lids[l], H, D)
                 y = np.stack([bf16_to_f32(hadamard_forward(x[p], sg)) for p in (0, 1)])
             else:
                 y = bf16_to_f32(x)
@@ -341,8 +345,8 @@ def compress_request(
             syms.append(sym.transpose(0, 3, 1, 2, 4) if layout == "permuted" else sym)
             metas.append(meta)
         buf = np.ascontiguousarray(np.stack(syms))
-        chunks.append(Chunk(s, e, buf, bitpack_encode(buf, bits), metas))
-    return chunks
+        out.append(Chunk(s, e, buf, bitpack_encode(buf, bits), metas))
+    return out
 
 
 def decompress_request(
@@ -354,9 +358,11 @@ def decompress_request(
     bits: int,
     transform: bool = True,
     layout: str = "permuted",
+    layer_ids: Optional[Sequence[int]] = None,
 ) -> None:
     """decompress_all_layers (compression_manager.py:539-757) then
     inject_kv_into_layer_by_blocks (kv_utils.py:83-119), into `pools` in place."""
+    lids = list(range(len(pools))) if layer_ids is None else list(layer_ids)
     for ch in chunks:
         shape = ch.symbols.shape
         buf = bitpack_decode(ch.stream, int(np.prod(shape)), bits).reshape(shape)
@@ -365,7 +371,7 @@ def decompress_request(
             x = dequantize_layer(sym, ch.metas[i], profiles[l])
             H, D = x.shape[-2], x.shape[-1]
             if transform:
-                sg = rademacher_signs(base_seed, l, H, D)
+                sg = rademacher_signs(base_seed, lids[l], H, D)
                 xb = np.stack([hadamard_inverse(f32_to_bf16(x[p]), sg) for p in (0, 1)])
             else:
                 xb = f32_to_bf16(x)

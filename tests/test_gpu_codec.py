@@ -53,7 +53,7 @@ def test_bitpack_large_and_unaligned(cuda):
     from kvserve_amd import ops
 
     g = torch.Generator().manual_seed(7)
-    x = torch.randint(16, (1 << 22) + 5, generator=g, dtype=torch.uint8)
+    x = torch.randint(16, ((1 << 22) + 5,), generator=g, dtype=torch.uint8)
     xd = x.to(cuda)
     for view in (xd, xd[1:], xd[3:-1]):
         p = ops.bitpack_encode(view, 4)
@@ -203,19 +203,15 @@ def test_fused_multi_chunk_and_many_layers(cuda):
     packet = codec.compress([p.to(cuda) for p in pools], ids.to(torch.int32), prof, chunk_layers=2)
     check_packet(packet)
     assert packet.chunks == [(0, 2), (2, 4), (4, 5)]
-    chunks_ref = []
-    for s, e in packet.chunks:
-        chunks_ref += kp.compress_request([_bits(p) for p in pools[s:e]], ids.tolist(),
-                                          [_oracle_profile(p) for p in prof[s:e]], 1234, 4)
-    # layer ids of later chunks continue the global numbering
-    for (s, e), st, ch in zip(packet.chunks, packet.streams, chunks_ref):
-        if s == 0:
-            sym = cbitpack.decode(st.cpu().numpy(), ch.symbols.size, 4)
-            dmax, frac = sym_diff(sym, ch.symbols.reshape(-1))
-            assert dmax <= 1 and frac <= SYM_MISMATCH_FRAC
-        else:
-            hdr = st.cpu().numpy()[:16]
-            assert np.array_equal(hdr, ch.stream[:16])
+    # layer ids of later chunks continue the global numbering (sign seeds)
+    chunks_ref = kp.compress_request([_bits(p) for p in pools], ids.tolist(), [_oracle_profile(p) for p in prof],
+                                     1234, 4, chunks=packet.chunks)
+    for st, ch in zip(packet.streams, chunks_ref):
+        got = st.cpu().numpy()
+        assert np.array_equal(got[:16], ch.stream[:16])
+        sym = cbitpack.decode(got, ch.symbols.size, 4)
+        dmax, frac = sym_diff(sym, ch.symbols.reshape(-1))
+        assert dmax <= 1 and frac <= SYM_MISMATCH_FRAC
     dst = [torch.zeros_like(p).to(cuda) for p in pools]
     codec.decompress(packet, dst, ids.to(torch.int32))
     torch.cuda.synchronize()
