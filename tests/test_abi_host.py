@@ -1,0 +1,130 @@
+"""C-ABI and host-logic checks that need no GPU (no kernel is launched)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kvserve_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*int\s+(kvmi_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from kvserve_amd import _lib
+
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert syms, "no declarations parsed"
+    assert set(syms) == set(_lib.EXPORTS)
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert lib.kvmi_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layouts_match_header():
+    from kvserve_amd import _lib
+
+    assert ctypes.sizeof(_lib.Geometry) == 32
+    assert _lib.JOB_BYTES == 104
+
+
+def test_host_contract_errors_return_einval():
+    """Argument checks happen on the host before any HIP call."""
+    from kvserve_amd import _lib
+
+    lib = _lib.load()
+    E = _lib.EINVAL
+    assert lib.kvmi_bitpack_encode(None, 4, 0, None, None, None) == E
+    assert lib.kvmi_bitpack_encode(None, 4, 9, None, None, None) == E
+    assert lib.kvmi_bitpack_decode(None, 16, 1, 4, None, None, None) == E
+    buf = ctypes.create_string_buffer(32)
+    err = ctypes.create_string_buffer(4)
+    # wrong stream length for (n=5, bits=4): 16 + 3 bytes expected
+    assert lib.kvmi_bitpack_decode(ctypes.addressof(buf), 18, 5, 4, ctypes.addressof(buf), ctypes.addressof(err),
+                                   None) == E
+    assert lib.kvmi_hadamard(None, None, 4, 8, 96, None, 0, None) == E
+    g = _lib.Geometry()
+    g.block_size, g.num_heads, g.head_dim, g.bits, g.max_groups = 16, 8, 128, 4, 2
+    for field, bad in (("head_dim", 96), ("bits", 0), ("num_heads", 3), ("max_groups", 9), ("num_heads", 32)):
+        gg = _lib.Geometry.from_buffer_copy(g)
+        setattr(gg, field, bad)
+        for fn in (lib.kvmi_kstats_paged, lib.kvmi_encode_paged, lib.kvmi_decode_paged):
+            assert fn(ctypes.byref(gg), None, 1, 1, None, None) == E, (field, bad)
+    gg = _lib.Geometry.from_buffer_copy(g)
+    gg.flags = _lib.F_NO_HEADER  # raw symbols need 8 bits
+    assert lib.kvmi_encode_paged(ctypes.byref(gg), None, 1, 1, None, None) == E
+    # zero jobs / zero blocks: nothing to do
+    assert lib.kvmi_encode_paged(ctypes.byref(g), None, 0, 5, None, None) == 0
+
+
+def test_profiles_validate_and_serialize():
+    from kvserve_amd.profiles import LayerProfile, per_head_profile, section_profile, whole_layer_profile
+
+    p = section_profile([True, False, False, False, False, False, True, False], 16, 16, 12, 12)
+    assert p.k_order == [0, 6, 1, 2, 3, 4, 5, 7]
+    assert p.v_group == [0, 0, 1, 1, 1, 1, 1, 1]
+    p.validate(8)
+    a = p.to_array()
+    assert a.shape == (2, 3, 8) and a.dtype == np.uint8
+    assert list(a[1, 1]) == [12, 12, 16, 16, 16, 16, 16, 16]
+    q = per_head_profile([6, 12, 6, 6], [12, 6, 6, 12])
+    assert q.v_order == [1, 2, 0, 3] and q.v_group == [0, 0, 1, 1] and q.v_levels == [6, 6, 12, 12]
+    assert q.k_levels == [12, 6, 6, 6]
+    q.validate(4)
+    whole_layer_profile(8, 6, 6).validate(8)
+    with pytest.raises(ValueError):
+        LayerProfile([0, 0], [4, 4], [0, 1], [4, 4], [0, 0]).validate(2)
+    with pytest.raises(ValueError):
+        LayerProfile([0, 1], [4, 4], [0, 1], [4, 8], [0, 0]).validate(2)
+    with pytest.raises(ValueError):
+        LayerProfile([0, 1], [4, 1], [0, 1], [4, 4], [0, 0]).validate(2)
+
+
+def test_profiles_from_reference_config_match_oracle():
+    from oracle import kvpipe as kp
+    from kvserve_amd.profiles import profiles_from_quantizer_config, scores_from_csv
+
+    qc = dict(model_name="Llama-3.1-8B-Instruct", hybrid_ratio=0.3, high_key_max_value=16,
+              high_value_max_value=16, low_key_max_value=12, low_value_max_value=8)
+    prof = profiles_from_quantizer_config(qc, 32, 8)
+    m = kp.head_mask_from_scores(scores_from_csv("Llama-3.1-8B-Instruct"), 0.3)
+    for l in range(32):
+        o = kp.head_split_profile(m[l], 16, 16, 12, 8)
+        assert prof[l].k_order == o.k.order and prof[l].k_levels == o.k.levels
+        assert prof[l].v_levels == o.v.levels and prof[l].v_group == o.v.group
+    lay = profiles_from_quantizer_config({**qc, "split_type": "layer"}, 32, 8)
+    assert [p.k_levels[0] for p in lay].count(12) == 11
+    # TP: 2 ranks of 4 heads each see their own mask columns
+    r1 = profiles_from_quantizer_config({**qc, "tp_rank": 1, "tensor_parallel_size": 2}, 32, 4)
+    assert sorted(r1[0].k_order) == [0, 1, 2, 3]
+    with pytest.raises(NotImplementedError):
+        profiles_from_quantizer_config({**qc, "axis_key": "token"}, 1, 8)
+    with pytest.raises(IndexError):
+        profiles_from_quantizer_config(qc, 33, 8)
+
+
+def test_chunk_rule():
+    from kvserve_amd.engine import chunk_ranges
+
+    assert chunk_ranges(32, 500 * 2 ** 20) == [(0, 32)]
+    assert chunk_ranges(32, 500 * 2 ** 20 + 1) == [(0, 8), (8, 16), (16, 24), (24, 32)]
+    assert chunk_ranges(9, 2 ** 30) == [(0, 8), (8, 9)]
+
+
+def test_codec_constructor_contracts():
+    from kvserve_amd.engine import FusedKVCodec
+
+    for bits in (0, 9, True, 3.5, None):
+        with pytest.raises(ValueError, match="bitpack_bits"):
+            FusedKVCodec(8, 128, 16, bits)
+    with pytest.raises(ValueError):
+        FusedKVCodec(8, 96, 16, 4)
+    with pytest.raises(ValueError):
+        FusedKVCodec(8, 128, 16, 4, header=False)
