@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 import threading
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -223,7 +224,7 @@ class FusedKVCodec:
         for p in profiles:
             p.validate(self.H)
         layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
-        ids = self._block_table(block_ids, dev, pools[0].shape[1])
+        ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
         B = int(ids.numel())
         H, D, S = self.H, self.D, self.S
         raw = L * 2 * B * S * H * D * 2
@@ -258,7 +259,7 @@ class FusedKVCodec:
             raise ValueError("packet geometry does not match this codec")
         if (packet.seed, packet.transform, packet.layout) != (self.seed, self.transform, self.layout):
             raise ValueError("packet transform / layout does not match this codec")
-        ids = self._block_table(block_ids, dev, pools[0].shape[1])
+        ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
         if ids.numel() < packet.num_blocks:
             raise ValueError("fewer block ids than compressed blocks")
         ids = ids[: packet.num_blocks].contiguous()
@@ -339,11 +340,16 @@ def raise_device_error(code: int) -> None:
         raise RuntimeError("invalid bitpack header or decode configuration")
 
 
-def check_packet(packet: Packet) -> None:
-    """Synchronize on the packet's last run and raise on a device data error."""
+def check_packet(packet: Packet, force: bool = False) -> None:
+    """Synchronize on the packet's last run and raise on a device data error.
+    Skipped while the stream is being captured into a graph, and (unless `force`)
+    when KVSERVE_AMD_CHECK_ERRORS=0 keeps calls asynchronous."""
     err = packet.__dict__.get("_err")
-    if err is not None:
-        raise_device_error(int(err.item()))
+    if err is None or torch.cuda.is_current_stream_capturing():
+        return
+    if not force and os.environ.get("KVSERVE_AMD_CHECK_ERRORS", "1") == "0":
+        return
+    raise_device_error(int(err.item()))
 
 
 def _header_bytes(bits: int, n: int) -> np.ndarray:

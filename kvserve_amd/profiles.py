@@ -122,6 +122,7 @@ class LayerProfile:
     v_levels: List[int]
     v_group: List[int]
     k_group: Optional[List[int]] = None  # K sections (metadata only: K stats are per channel)
+    n_low: Optional[int] = None  # leading output positions forming the reference's "low" section
 
     def num_v_groups(self) -> int:
         return max(self.v_group) + 1
@@ -159,13 +160,14 @@ def section_profile(low_mask_row: Sequence[bool], hk: int, hv: int, lk: int, lv:
     high = [h for h, m in enumerate(low_mask_row) if not m]
     order = low + high
     grp = [0] * len(low) + [1 if low else 0] * len(high)
-    return LayerProfile(order, [lk] * len(low) + [hk] * len(high), order, [lv] * len(low) + [hv] * len(high), grp)
+    return LayerProfile(order, [lk] * len(low) + [hk] * len(high), order, [lv] * len(low) + [hv] * len(high), grp,
+                        n_low=len(low))
 
 
-def whole_layer_profile(H: int, k_levels: int, v_levels: int) -> LayerProfile:
-    """Layer split (split_func.py:9-38): the layer is one section."""
+def whole_layer_profile(H: int, k_levels: int, v_levels: int, is_low: bool = False) -> LayerProfile:
+    """Layer split (split_func.py:9-38): the layer is one section (low or high)."""
     order = list(range(H))
-    return LayerProfile(order, [k_levels] * H, order, [v_levels] * H, [0] * H)
+    return LayerProfile(order, [k_levels] * H, order, [v_levels] * H, [0] * H, n_low=H if is_low else 0)
 
 
 def per_head_profile(k_levels: Sequence[int], v_levels: Sequence[int]) -> LayerProfile:
@@ -202,5 +204,6 @@ def profiles_from_quantizer_config(qc: Dict, num_layers: int, num_heads: int, tp
         lm = layer_low_mask(scores.shape[0])
         if num_layers > lm.shape[0]:
             raise IndexError(f"layer mask of {model} covers {lm.shape[0]} layers, got {num_layers}")
-        return [whole_layer_profile(num_heads, lk if lm[l] else hk, lv if lm[l] else hv) for l in range(num_layers)]
+        return [whole_layer_profile(num_heads, lk if lm[l] else hk, lv if lm[l] else hv, bool(lm[l]))
+                for l in range(num_layers)]
     raise ValueError(f"split_type must be 'head' or 'layer', got {split}")

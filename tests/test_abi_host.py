@@ -128,3 +128,43 @@ def test_codec_constructor_contracts():
         FusedKVCodec(8, 96, 16, 4)
     with pytest.raises(ValueError):
         FusedKVCodec(8, 128, 16, 4, header=False)
+
+
+def test_adapter_registry_contracts():
+    from kvserve_amd.compression import (CompressionManager, FusedCompressionManager, KVCompressionAdapter,
+                                         get_default_compression_config)
+
+    base = {"pipeline": ["transformer", "quantizer", "codec"],
+            "transformer_config": {"transform_type": "hadamard", "seed": 7},
+            "quantizer_config": {"model_name": "Llama-3.1-8B-Instruct"},
+            "codec_config": {"codec_type": "bitpack", "bitpack_bits": 4}}
+    ad = KVCompressionAdapter(base, num_kv_heads=8, head_size=128)
+    assert isinstance(ad._manager, FusedCompressionManager)
+    assert ad._config.quantizer_config["tp_rank"] == 0
+    hip = KVCompressionAdapter({**base, "quantizer_config": {"impl": "hip_fused"}}, 8, 128)
+    assert isinstance(hip._manager, FusedCompressionManager)
+    codec_only = KVCompressionAdapter({"pipeline": ["codec"], "codec_config": {"codec_type": "bitpack"}}, 8, 128)
+    assert type(codec_only._manager) is CompressionManager
+    for bad, exc in (({**base, "quantizer_config": {"impl": "tilelang_fused"}}, ValueError),
+                     ({**base, "impl": "centered_codebook"}, ValueError),
+                     ({**base, "pipeline": ["transformer", "zip"]}, ValueError),
+                     ({**base, "codec_config": {"codec_type": "nvcomp"}}, ValueError),
+                     ({**base, "transformer_config": {"transform_type": "dct"}}, ValueError),
+                     ({"mode": "controller", "library_path": "x"}, NotImplementedError)):
+        with pytest.raises(exc):
+            KVCompressionAdapter(bad, num_kv_heads=8, head_size=128)
+    d = KVCompressionAdapter("default", num_kv_heads=4, head_size=128, model_name="Qwen2.5-7B-Instruct")
+    assert d._config.quantizer_config["model_name"] == "Qwen2.5-7B-Instruct"
+    assert get_default_compression_config()["codec_config"]["codec_type"] == "bitpack"
+
+
+def test_quantizer_validation_matches_reference_asserts():
+    from kvserve_amd.compression import KVServeQuantizer
+
+    for kw in ({"hybrid_ratio": 1.5}, {"low_key_max_value": 0}, {"high_value_max_value": 255},
+               {"low_key_max_value": 16, "high_key_max_value": 12}, {"axis_key": "row"}, {"split_type": "x"}):
+        with pytest.raises(AssertionError):
+            KVServeQuantizer(**kw)
+    q = KVServeQuantizer(split_type="layer", low_key_max_value=6, high_key_max_value=12)
+    assert q.layer_profile(31, 8).k_levels == [6] * 8 and q.layer_profile(0, 8).k_levels == [12] * 8
+    assert q.layer_profile(31, 8).n_low == 8 and q.layer_profile(0, 8).n_low == 0
