@@ -69,6 +69,8 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_F_NO_TRANSFORM 1u /* skip signs + FWHT (pipeline without "transformer") */
 #define KVMI_F_NATIVE_LAYOUT 2u /* symbol order [l,2,B,S,H',D] instead of [l,2,H',B,S,D] */
 #define KVMI_F_NO_HEADER 4u     /* raw symbol buffer: no 16-byte header (bits must be 8) */
+#define KVMI_F_VALU_FWHT 8u     /* force the register (VALU) FWHT kernels instead of MFMA */
+#define KVMI_F_CLAMP_LEVELS 16u /* some level count exceeds 128: clamp symbols to the level */
 
 /* Launch-wide geometry shared by every job of one call. */
 typedef struct kvmi_geometry {

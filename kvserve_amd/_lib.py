@@ -23,6 +23,8 @@ OK, EINVAL, ELAUNCH = 0, -22, -5
 F_NO_TRANSFORM = 1
 F_NATIVE_LAYOUT = 2
 F_NO_HEADER = 4
+F_VALU_FWHT = 8
+F_CLAMP_LEVELS = 16
 
 # Every symbol include/kvserve_amd.h declares.
 EXPORTS = (

@@ -18,8 +18,7 @@
 //           symbols bitpacked straight into the chunk stream.
 // Decompress is one launch: header check, unpack, dequantize, inverse transform,
 // sign and scatter into the pool.
-#include "kvmi_device.hpp"
-#include "../../include/kvserve_amd.h"
+#include "kvmi_common.hpp"
 
 static_assert(sizeof(kvmi_layer_job) == 104, "kvmi_layer_job layout is part of the ABI");
 static_assert(sizeof(kvmi_geometry) == 32, "kvmi_geometry layout is part of the ABI");
@@ -29,26 +28,6 @@ namespace {
 
 constexpr int kWG = 512;
 constexpr int kRows = kWG / 4;  // rows per pass
-constexpr int kMaxH = 16;       // heads per worker shard supported by the LDS tables
-constexpr int kMaxHD = kMaxH * 128;
-
-struct Geo {
-  int S, H, D, bits;
-  uint32_t flags;
-  int G;
-  int bpw;      // paged blocks per workgroup
-  float scale;  // fp32 value of 1/sqrt(D)
-};
-
-struct Profile {  // decoded kvmi_layer_job::profile for one part
-  const uint8_t* order;
-  const uint8_t* levels;
-  const uint8_t* group;
-};
-__device__ __forceinline__ Profile part_profile(const uint8_t* p, int part, int H) {
-  const uint8_t* b = p + part * 3 * H;
-  return Profile{b, b + H, b + 2 * H};
-}
 
 // Sign bits of lane q's E elements for head h.
 template <int D>
@@ -79,49 +58,6 @@ __device__ __forceinline__ void load_transform(const uint16_t* __restrict__ src,
   } else {
     unpack_bf16<E>(w, y);
   }
-}
-
-struct RowPos {
-  int64_t pool_row;  // row index in the pool part: physical block * S*H + within
-  int tok;           // token index within the job (logical block * S + token in block)
-  bool active;
-};
-__device__ __forceinline__ RowPos row_pos(const kvmi_layer_job& job, int blk0, int64_t rows, int64_t r, int S,
-                                          int H) {
-  RowPos p;
-  p.active = r < rows;
-  if (!p.active) {
-    p.pool_row = 0;
-    p.tok = 0;
-    return p;
-  }
-  const int rpb = S * H;
-  const int b = blk0 + (int)(r / rpb);
-  const int within = (int)(r % rpb);
-  p.pool_row = (int64_t)job.block_ids[b] * rpb + within;
-  p.tok = b * S + within / H;
-  return p;
-}
-
-// Byte address of the packed segment of (part, output position j, token tok) for
-// lane q, in the permuted [l,2,H',B,S,D] or native [l,2,B,S,H',D] symbol order.
-template <int D, int BITS>
-__device__ __forceinline__ uint8_t* seg_addr(const kvmi_layer_job& job, const Geo& g, int part, int j, int tok,
-                                             int q) {
-  const int64_t ntok = (int64_t)job.num_blocks * g.S;
-  int64_t ts, hs, ps;
-  if (g.flags & KVMI_F_NATIVE_LAYOUT) {
-    ts = (int64_t)g.H * D;
-    hs = D;
-    ps = ntok * g.H * D;
-  } else {
-    ts = D;
-    hs = ntok * D;
-    ps = (int64_t)g.H * hs;
-  }
-  const int64_t sym = job.symbol_offset + part * ps + j * hs + tok * ts + q * (D / 4);
-  const int64_t base = (g.flags & KVMI_F_NO_HEADER) ? 0 : KVMI_HEADER_BYTES;
-  return job.stream + base + (sym * BITS) / 8;
 }
 
 // ============================================================== K statistics
@@ -241,13 +177,8 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
     int m = 0;
     for (int k = 0; k < H; ++k) m = max(m, (int)pv.group[k]);
     ngv = m + 1;
-    if (job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER)) {
-      uint32_t* o = reinterpret_cast<uint32_t*>(job.stream);
-      o[0] = KVMI_MAGIC;
-      o[1] = (uint32_t)BITS;
-      o[2] = (uint32_t)((uint64_t)job.chunk_symbols & 0xffffffffu);
-      o[3] = (uint32_t)((uint64_t)job.chunk_symbols >> 32);
-    }
+    if (job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER))
+      write_stream_header(job.stream, BITS, job.chunk_symbols);
   }
   __syncthreads();
   for (int i = tid; i < HD; i += kWG) {
@@ -284,7 +215,7 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
       }
       Packed<E, BITS> pkd;
       pack_syms<E, BITS>(s, pkd);
-      store_packed<E, BITS>(seg_addr<D, BITS>(job, g, 0, jk, rp.tok, q), pkd);
+      store_packed<E, BITS>(seg_addr<BITS>(job, g, 0, jk, rp.tok, q * (D / 4)), pkd);
     }
     // ---------------- V: per-token statistics over the heads of a group
     float y[E];
@@ -333,7 +264,7 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
       }
       Packed<E, BITS> pkd;
       pack_syms<E, BITS>(s, pkd);
-      store_packed<E, BITS>(seg_addr<D, BITS>(job, g, 1, jv, rp.tok, q), pkd);
+      store_packed<E, BITS>(seg_addr<BITS>(job, g, 1, jv, rp.tok, q * (D / 4)), pkd);
     }
     __syncthreads();
   }
@@ -360,14 +291,7 @@ __global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job
   if (tid == 0) {
     int good = 1;
     if (!(g.flags & KVMI_F_NO_HEADER)) {
-      const uint8_t* in = job.stream;
-      uint32_t hw[4];
-      for (int i = 0; i < 4; ++i)
-        hw[i] = (uint32_t)in[4 * i] | ((uint32_t)in[4 * i + 1] << 8) | ((uint32_t)in[4 * i + 2] << 16) |
-                ((uint32_t)in[4 * i + 3] << 24);
-      const uint64_t n = (uint64_t)job.chunk_symbols;
-      good = hw[0] == KVMI_MAGIC && hw[1] == (uint32_t)BITS && hw[2] == (uint32_t)(n & 0xffffffffu) &&
-             hw[3] == (uint32_t)(n >> 32);
+      good = header_matches(job.stream, BITS, job.chunk_symbols);
       if (!good && blockIdx.x == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
     }
     ok = good;
@@ -405,7 +329,7 @@ __global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job
     for (int part = 0; part < 2; ++part) {
       const int j = part ? jv : jk;
       Packed<E, BITS> pkd;
-      load_packed<E, BITS>(seg_addr<D, BITS>(job, g, part, j, rp.tok, q), pkd);
+      load_packed<E, BITS>(seg_addr<BITS>(job, g, part, j, rp.tok, q * (D / 4)), pkd);
       uint32_t s[E];
       unpack_syms<E, BITS>(pkd, s);
       float x[E];
@@ -437,27 +361,6 @@ __global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job
 }
 
 // ============================================================== host side
-int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_blocks, Geo* out) {
-  if (!geom || num_jobs < 0 || max_blocks < 0) return KVMI_EINVAL;
-  const int S = geom->block_size, H = geom->num_heads, D = geom->head_dim, bits = geom->bits;
-  if (S < 1 || H < 1 || H > kMaxH || (kRows % H) != 0) return KVMI_EINVAL;
-  if (D != 64 && D != 128) return KVMI_EINVAL;
-  if (bits < 1 || bits > 8) return KVMI_EINVAL;
-  if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
-  if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
-  if (geom->flags & ~(KVMI_F_NO_TRANSFORM | KVMI_F_NATIVE_LAYOUT | KVMI_F_NO_HEADER)) return KVMI_EINVAL;
-  out->S = S;
-  out->H = H;
-  out->D = D;
-  out->bits = bits;
-  out->flags = geom->flags;
-  out->G = geom->max_groups;
-  out->scale = (float)(1.0 / __builtin_sqrt((double)D));
-  const int rpb = S * H;
-  out->bpw = rpb >= kRows ? 1 : (kRows + rpb - 1) / rpb;
-  return KVMI_OK;
-}
-
 template <int D, int BITS>
 void launch_encode_db(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
   hipLaunchKernelGGL((encode_kernel<D, BITS>), grid, dim3(kWG), 0, st, g, jobs, err);
@@ -466,9 +369,6 @@ template <int D, int BITS>
 void launch_decode_db(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
   hipLaunchKernelGGL((decode_kernel<D, BITS>), grid, dim3(kWG), 0, st, g, jobs, err);
 }
-
-template <template <int, int> class F, int D>
-struct BitsDispatch;
 
 #define KVMI_DISPATCH_BITS(FN, D, g, grid, jobs, err, st) \
   switch ((g).bits) {                                     \
@@ -482,6 +382,12 @@ struct BitsDispatch;
     default: FN<D, 8>(g, grid, jobs, err, st); break;     \
   }
 
+// Register-FWHT kernels work on 128-row passes: enough blocks per workgroup to fill one.
+void set_valu_bpw(Geo* g) {
+  const int rpb = g->S * g->H;
+  g->bpw = rpb >= kRows ? 1 : (kRows + rpb - 1) / rpb;
+}
+
 }  // namespace
 }  // namespace kvmi
 
@@ -493,14 +399,14 @@ extern "C" int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (rc) return rc;
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (mfma_eligible(g)) return mfma_kstats(g, jobs, num_jobs, max_blocks, err, st);
   // Statistics need only K: give each workgroup enough blocks that a job has at
   // most ~16 workgroups, which keeps the global atomics per channel small.
-  const int rpb = g.S * g.H;
-  const int min_bpw = rpb >= kRows ? 1 : (kRows + rpb - 1) / rpb;
-  int bpw = (max_blocks + 15) / 16;
-  g.bpw = bpw < min_bpw ? min_bpw : bpw;
+  set_valu_bpw(&g);
+  const int bpw = (max_blocks + 15) / 16;
+  if (bpw > g.bpw) g.bpw = bpw;
   dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (g.D == 64)
     hipLaunchKernelGGL((kstats_kernel<64>), grid, dim3(kWG), 0, st, g, jobs, err);
   else
@@ -516,8 +422,10 @@ extern "C" int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (rc) return rc;
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
-  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (mfma_eligible(g)) return mfma_encode(g, jobs, num_jobs, max_blocks, err, st);
+  set_valu_bpw(&g);
+  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   if (g.D == 64) {
     KVMI_DISPATCH_BITS(launch_encode_db, 64, g, grid, jobs, err, st)
   } else {
@@ -534,8 +442,10 @@ extern "C" int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (rc) return rc;
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
-  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (mfma_eligible(g)) return mfma_decode(g, jobs, num_jobs, max_blocks, err, st);
+  set_valu_bpw(&g);
+  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   if (g.D == 64) {
     KVMI_DISPATCH_BITS(launch_decode_db, 64, g, grid, jobs, err, st)
   } else {

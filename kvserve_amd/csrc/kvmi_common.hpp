@@ -1,0 +1,132 @@
+// Definitions shared by the paged codec kernels (register-FWHT and MFMA variants).
+#pragma once
+
+#include "kvmi_device.hpp"
+#include "../../include/kvserve_amd.h"
+
+namespace kvmi {
+
+constexpr int kMaxH = 16;  // heads per worker shard supported by the LDS tables
+constexpr int kMaxHD = kMaxH * 128;
+
+// Launch geometry (kernel argument).
+struct Geo {
+  int S, H, D, bits;
+  uint32_t flags;
+  int G;
+  int bpw;      // paged blocks per workgroup
+  float scale;  // fp32 value of 1/sqrt(D)
+};
+
+struct Profile {  // decoded kvmi_layer_job::profile for one part
+  const uint8_t* order;
+  const uint8_t* levels;
+  const uint8_t* group;
+};
+__device__ __forceinline__ Profile part_profile(const uint8_t* p, int part, int H) {
+  const uint8_t* b = p + part * 3 * H;
+  return Profile{b, b + H, b + 2 * H};
+}
+
+// Where row r (0-based, token-major) of a workgroup's block run lives.
+struct RowPos {
+  int64_t pool_row;  // row index in the pool part: physical block * S*H + within
+  int tok;           // token index within the job (logical block * S + token in block)
+  bool active;
+};
+__device__ __forceinline__ RowPos row_pos(const kvmi_layer_job& job, int blk0, int64_t rows, int64_t r, int S,
+                                          int H) {
+  RowPos p;
+  p.active = r < rows;
+  if (!p.active) {
+    p.pool_row = 0;
+    p.tok = 0;
+    return p;
+  }
+  const int rpb = S * H;
+  const int b = blk0 + (int)(r / rpb);
+  const int within = (int)(r % rpb);
+  p.pool_row = (int64_t)job.block_ids[b] * rpb + within;
+  p.tok = b * S + within / H;
+  return p;
+}
+
+// Byte address of the packed symbols of (part, output head position j, token tok)
+// starting at element e0 of the row, in the permuted [l,2,H',B,S,D] or native
+// [l,2,B,S,H',D] symbol order.  Callers keep e0*BITS a multiple of 8.
+template <int BITS>
+__device__ __forceinline__ uint8_t* seg_addr(const kvmi_layer_job& job, const Geo& g, int part, int j, int tok,
+                                             int e0) {
+  const int64_t D = g.D;
+  const int64_t ntok = (int64_t)job.num_blocks * g.S;
+  int64_t ts, hs, ps;
+  if (g.flags & KVMI_F_NATIVE_LAYOUT) {
+    ts = (int64_t)g.H * D;
+    hs = D;
+    ps = ntok * g.H * D;
+  } else {
+    ts = D;
+    hs = ntok * D;
+    ps = (int64_t)g.H * hs;
+  }
+  const int64_t sym = job.symbol_offset + part * ps + j * hs + tok * ts + e0;
+  const int64_t base = (g.flags & KVMI_F_NO_HEADER) ? 0 : KVMI_HEADER_BYTES;
+  return job.stream + base + (sym * BITS) / 8;
+}
+
+__device__ __forceinline__ bool header_matches(const uint8_t* in, int bits, int64_t chunk_symbols) {
+  uint32_t hw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    hw[i] = (uint32_t)in[4 * i] | ((uint32_t)in[4 * i + 1] << 8) | ((uint32_t)in[4 * i + 2] << 16) |
+            ((uint32_t)in[4 * i + 3] << 24);
+  const uint64_t n = (uint64_t)chunk_symbols;
+  return hw[0] == KVMI_MAGIC && hw[1] == (uint32_t)bits && hw[2] == (uint32_t)(n & 0xffffffffu) &&
+         hw[3] == (uint32_t)(n >> 32);
+}
+
+__device__ __forceinline__ void write_stream_header(uint8_t* out, int bits, int64_t chunk_symbols) {
+  uint32_t* o = reinterpret_cast<uint32_t*>(out);
+  o[0] = KVMI_MAGIC;
+  o[1] = (uint32_t)bits;
+  o[2] = (uint32_t)((uint64_t)chunk_symbols & 0xffffffffu);
+  o[3] = (uint32_t)((uint64_t)chunk_symbols >> 32);
+}
+
+// Host-side validation of a launch geometry; fills the kernel argument.
+inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_blocks, Geo* out) {
+  if (!geom || num_jobs < 0 || max_blocks < 0) return KVMI_EINVAL;
+  const int S = geom->block_size, H = geom->num_heads, D = geom->head_dim, bits = geom->bits;
+  if (S < 1 || H < 1 || H > kMaxH || (128 % H) != 0) return KVMI_EINVAL;
+  if (D != 64 && D != 128) return KVMI_EINVAL;
+  if (bits < 1 || bits > 8) return KVMI_EINVAL;
+  if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
+  if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
+  if (geom->flags & ~(KVMI_F_NO_TRANSFORM | KVMI_F_NATIVE_LAYOUT | KVMI_F_NO_HEADER | KVMI_F_VALU_FWHT |
+                      KVMI_F_CLAMP_LEVELS))
+    return KVMI_EINVAL;
+  out->S = S;
+  out->H = H;
+  out->D = D;
+  out->bits = bits;
+  out->flags = geom->flags;
+  out->G = geom->max_groups;
+  out->scale = (float)(1.0 / __builtin_sqrt((double)D));
+  out->bpw = 1;
+  return KVMI_OK;
+}
+
+// MFMA variants (kvmi_mfma.hip).  They serve the transform profile for geometries
+// with H dividing 8 and S*H a multiple of 32, unless the caller forces the register
+// FWHT (KVMI_F_VALU_FWHT); everything else runs the register-FWHT kernels.
+inline bool mfma_eligible(const Geo& g) {
+  return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_NO_TRANSFORM)) && (8 % g.H) == 0 && ((g.S * g.H) % 32) == 0;
+}
+int mfma_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
+                hipStream_t st);
+int mfma_encode(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
+                hipStream_t st);
+int mfma_decode(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
+                hipStream_t st);
+
+}  // namespace kvmi

@@ -109,7 +109,7 @@ class FusedKVCodec:
 
     def __init__(self, num_heads: int, head_dim: int, block_size: int, bits: int = 4,
                  seed: int = DEFAULT_SEED, transform: bool = True, layout: str = "permuted",
-                 header: bool = True):
+                 header: bool = True, fwht: Optional[str] = None):
         if type(bits) is not int or not 1 <= bits <= 8:
             raise ValueError("bitpack_bits must be an integer in [1, 8]")
         if head_dim not in (64, 128):
@@ -120,10 +120,14 @@ class FusedKVCodec:
             raise ValueError("a stream without header carries raw 8-bit symbols")
         self.H, self.D, self.S, self.bits = num_heads, head_dim, block_size, bits
         self.seed, self.transform, self.layout, self.header = int(seed), transform, layout, header
+        # Hadamard on MFMA (default) or the register FWHT kernels (KVSERVE_AMD_FWHT=valu)
+        self.fwht = (fwht or os.environ.get("KVSERVE_AMD_FWHT", "mfma")).strip().lower()
+        if self.fwht not in ("mfma", "valu"):
+            raise ValueError("fwht must be 'mfma' or 'valu'")
         self._lib = _lib.load()
 
     # ---------------------------------------------------------------- helpers
-    def _flags(self) -> int:
+    def _flags(self, max_level: int) -> int:
         f = 0
         if not self.transform:
             f |= _lib.F_NO_TRANSFORM
@@ -131,12 +135,16 @@ class FusedKVCodec:
             f |= _lib.F_NATIVE_LAYOUT
         if not self.header:
             f |= _lib.F_NO_HEADER
+        if self.fwht == "valu":
+            f |= _lib.F_VALU_FWHT
+        if max_level > 128:
+            f |= _lib.F_CLAMP_LEVELS
         return f
 
-    def _geometry(self, groups: int) -> _lib.Geometry:
+    def _geometry(self, groups: int, max_level: int) -> _lib.Geometry:
         g = _lib.Geometry()
         g.block_size, g.num_heads, g.head_dim, g.bits = self.S, self.H, self.D, self.bits
-        g.flags, g.max_groups = self._flags(), groups
+        g.flags, g.max_groups = self._flags(max_level), groups
         return g
 
     def _kstats_scratch(self, L: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -304,7 +312,8 @@ class Plan:
         self.jobs = codec._jobs(pools, ids, packet.streams, packet.chunks, packet.kmeta, packet.vmeta,
                                 self.signs, self.prof, self.keys, self.cnt, B)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.geo = codec._geometry(packet.vmeta.shape[2])
+        max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
+        self.geo = codec._geometry(packet.vmeta.shape[2], max_level)
         packet.__dict__["_err"] = self.err
 
     def launches(self) -> List[str]:
