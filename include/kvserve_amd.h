@@ -97,12 +97,12 @@ typedef struct kvmi_geometry {
  * vmeta: bf16 [2][G][num_blocks*S]: [0] = per-token min, [1] = scale, by group.
  * kstats: uint32 [2][H][D] order-preserving keys of the running K min / max,
  *         initialised to {0xFFFFFFFF, 0}; kvmi_kstats_paged leaves it initialised.
- * counter: uint32 [1] work counter, initialised to 0; left at 0.
+ * counter: unused (may be null; kept for the layout of this struct).
  */
 typedef struct kvmi_layer_job {
   void* pool;                /* bf16 [2, P, S, H, D] paged KV of this layer (NHD) */
   const int32_t* block_ids;  /* [num_blocks] pool block of each logical block */
-  uint8_t* stream;           /* packed chunk stream this layer belongs to */
+  uint8_t* stream;           /* packed chunk stream this layer belongs to (16-byte aligned) */
   uint16_t* kmeta;
   uint16_t* vmeta;
   const uint32_t* signs;     /* [H][D/32] Rademacher sign bits per source head (1 = -1) */
@@ -168,8 +168,9 @@ int kvmi_hadamard(const void* in, void* out, int64_t rows, int32_t num_heads,
 /*
  * Pass 1 of compress: per-channel K statistics over all tokens of each job
  * (quantizer_func.py:41-53, axis "channel" reduces blocks and tokens).  Fills
- * each job's kmeta (min and scale of every K channel) and leaves kstats/counter
- * re-initialised.  `max_blocks` = max num_blocks over jobs (grid sizing).
+ * each job's kmeta (min and scale of every K channel) and leaves kstats
+ * re-initialised (two kernel launches).  `max_blocks` = max num_blocks over jobs
+ * (grid sizing).  Jobs with num_blocks == 0 keep their kmeta.
  */
 int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
                       int32_t max_blocks, int32_t* err, kvmi_stream_t stream);

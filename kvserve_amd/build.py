@@ -30,6 +30,9 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     # packed-fp32 VALU ops stay disabled on this pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the accumulators feed VALU code directly, without
+    # v_accvgpr_read copies out of AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-command-line-argument",
 ]
 

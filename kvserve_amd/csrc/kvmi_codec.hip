@@ -8,11 +8,13 @@
 // every wave reads 16 consecutive rows.  Because 128 % H == 0, a lane always sees
 // the same KV head, which keeps sign bits and per-channel K statistics in place.
 //
-// Compress is two launches:
+// Compress is three launches:
 //   kstats: gather + transform of K, per-channel running min/max per lane,
 //           workgroup reduction through LDS atomics, device reduction through
-//           global atomics; the last workgroup of a job (work counter) turns the
-//           keys into the job's K metadata and re-initialises the scratch.
+//           global atomics;
+//   kstats finalize: one workgroup per job turns the keys into the job's K
+//           metadata and re-initialises them (a launch of its own, so no
+//           device-wide fence is needed between the workgroups of the first);
 //   encode: gather + transform of K and V, K quantized with the per-channel
 //           metadata, V with per-(token, group) statistics reduced through LDS;
 //           symbols bitpacked straight into the chunk stream.
@@ -35,9 +37,9 @@ __device__ __forceinline__ uint32_t lane_signs(const uint32_t* signs, int h, int
   constexpr int E = D / 4;
   const uint32_t* sg = signs + h * (D / 32);
   if constexpr (E == 32) {
-    return sg[q];
+    return gld(sg + q);
   } else {  // E == 16
-    return (sg[q >> 1] >> ((q & 1) * 16)) & 0xffffu;
+    return (gld(sg + (q >> 1)) >> ((q & 1) * 16)) & 0xffffu;
   }
 }
 
@@ -79,7 +81,6 @@ __global__ __launch_bounds__(kWG) void kstats_kernel(Geo g, const kvmi_layer_job
   const uint32_t sb = transform ? lane_signs<D>(job.signs, h, q) : 0u;
 
   __shared__ uint32_t lkey[2 * kMaxHD];
-  __shared__ int last;
   for (int i = tid; i < HD; i += kWG) {
     lkey[i] = 0xffffffffu;
     lkey[HD + i] = 0u;
@@ -118,27 +119,34 @@ __global__ __launch_bounds__(kWG) void kstats_kernel(Geo g, const kvmi_layer_job
     atomicMin(&job.kstats[i], lkey[i]);
     atomicMax(&job.kstats[HD + i], lkey[HD + i]);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last = (atomicAdd(job.counter, 1u) == (unsigned)(nwg - 1)) ? 1 : 0;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const Profile pk = part_profile(job.profile, 0, H);
-  for (int i = tid; i < HD; i += kWG) {
-    const float kmn = round_bf16(key2f(__hip_atomic_exchange(&job.kstats[i], 0xffffffffu, __ATOMIC_RELAXED,
-                                                             __HIP_MEMORY_SCOPE_AGENT)));
-    const float kmx =
-        round_bf16(key2f(__hip_atomic_exchange(&job.kstats[HD + i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
-    const int hs = i / D, e = i % D;
-    int j = 0;
-    for (int k = 0; k < H; ++k)
-      if (pk.order[k] == hs) j = k;
-    const float sc = quant_scale(kmn, kmx, pk.levels[j]);
-    job.kmeta[j * D + e] = (uint16_t)f32_to_bf16_bits(kmn);
-    job.kmeta[HD + j * D + e] = (uint16_t)f32_to_bf16_bits(sc);
+}
+
+// Pass 1b: per job, turn the accumulated keys into kmeta (bf16 min and scale of
+// every K channel, by output position) and re-initialise the keys.  A kernel of its
+// own: the launch boundary makes every workgroup's atomics of pass 1a visible, with
+// no device-wide fence inside the accumulating kernels.
+__global__ __launch_bounds__(kWG) void kstats_finalize_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs) {
+  const kvmi_layer_job job = jobs[blockIdx.x];
+  if (job.num_blocks <= 0) return;  // nothing accumulated: kmeta is left as it is
+  const int H = g.H, D = g.D, HD = H * D;
+  __shared__ int pos[kMaxH];
+  __shared__ uint8_t lev[kMaxH];
+  if (threadIdx.x < (unsigned)H) {
+    const int k = threadIdx.x;
+    pos[gld(job.profile + k)] = k;  // order[k] = source head at output position k
+    lev[k] = gld(job.profile + H + k);
   }
-  if (tid == 0) __hip_atomic_exchange(job.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  for (int i = threadIdx.x; i < HD; i += kWG) {
+    const int hs = i / D, e = i % D, j = pos[hs];
+    const float kmn = round_bf16(key2f(gld(job.kstats + i)));
+    const float kmx = round_bf16(key2f(gld(job.kstats + HD + i)));
+    const float sc = quant_scale(kmn, kmx, lev[j]);
+    gst(job.kmeta + j * D + e, (uint16_t)f32_to_bf16_bits(kmn));
+    gst(job.kmeta + HD + j * D + e, (uint16_t)f32_to_bf16_bits(sc));
+    gst(job.kstats + i, 0xffffffffu);
+    gst(job.kstats + HD + i, 0u);
+  }
 }
 
 // ============================================================== encode
@@ -183,8 +191,8 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
   __syncthreads();
   for (int i = tid; i < HD; i += kWG) {
     const int hs = i / D, e = i % D, j = posk[hs];
-    const float m = bf16_to_f32(job.kmeta[j * D + e]);
-    const float sc = bf16_to_f32(job.kmeta[HD + j * D + e]);
+    const float m = bf16_to_f32(gld(job.kmeta + j * D + e));
+    const float sc = bf16_to_f32(gld(job.kmeta + HD + j * D + e));
     kq[i] = make_float2(m, 1.0f / sc);
   }
   __syncthreads();
@@ -249,8 +257,8 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
         const float sc = quant_scale(mn, mx, lv);
         tokq[tid] = make_float2(mn, 1.0f / sc);
         const RowPos tpz = row_pos(job, blk0, rows, rr, S, H);
-        job.vmeta[(int64_t)gg * ntok + tpz.tok] = (uint16_t)f32_to_bf16_bits(mn);
-        job.vmeta[(int64_t)(G + gg) * ntok + tpz.tok] = (uint16_t)f32_to_bf16_bits(sc);
+        gst(job.vmeta + (int64_t)gg * ntok + tpz.tok, (uint16_t)f32_to_bf16_bits(mn));
+        gst(job.vmeta + (int64_t)(G + gg) * ntok + tpz.tok, (uint16_t)f32_to_bf16_bits(sc));
       }
     }
     __syncthreads();
@@ -306,7 +314,7 @@ __global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job
   if (!ok) return;
   for (int i = tid; i < HD; i += kWG) {
     const int hs = i / D, e = i % D, j = posk[hs];
-    kd[i] = make_float2(bf16_to_f32(job.kmeta[j * D + e]), bf16_to_f32(job.kmeta[HD + j * D + e]));
+    kd[i] = make_float2(bf16_to_f32(gld(job.kmeta + j * D + e)), bf16_to_f32(gld(job.kmeta + HD + j * D + e)));
   }
   __syncthreads();
 
@@ -340,8 +348,8 @@ __global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job
           x[i] = dequant_value((float)s[i], c.x, c.y);
         }
       } else {
-        const float mn = bf16_to_f32(job.vmeta[(int64_t)gv * ntok + rp.tok]);
-        const float sc = bf16_to_f32(job.vmeta[(int64_t)(G + gv) * ntok + rp.tok]);
+        const float mn = bf16_to_f32(gld(job.vmeta + (int64_t)gv * ntok + rp.tok));
+        const float sc = bf16_to_f32(gld(job.vmeta + (int64_t)(G + gv) * ntok + rp.tok));
 #pragma unroll
         for (int i = 0; i < E; ++i) x[i] = dequant_value((float)s[i], mn, sc);
       }
@@ -400,17 +408,23 @@ extern "C" int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (mfma_eligible(g)) return mfma_kstats(g, jobs, num_jobs, max_blocks, err, st);
-  // Statistics need only K: give each workgroup enough blocks that a job has at
-  // most ~16 workgroups, which keeps the global atomics per channel small.
-  set_valu_bpw(&g);
-  const int bpw = (max_blocks + 15) / 16;
-  if (bpw > g.bpw) g.bpw = bpw;
-  dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
-  if (g.D == 64)
-    hipLaunchKernelGGL((kstats_kernel<64>), grid, dim3(kWG), 0, st, g, jobs, err);
-  else
-    hipLaunchKernelGGL((kstats_kernel<128>), grid, dim3(kWG), 0, st, g, jobs, err);
+  if (mfma_eligible(g)) {
+    rc = mfma_kstats(g, jobs, num_jobs, max_blocks, err, st);
+    if (rc) return rc;
+  } else {
+    // Statistics need only K: give each workgroup enough blocks that a job has at
+    // most ~16 workgroups, which keeps the global atomics per channel small.
+    set_valu_bpw(&g);
+    const int bpw = (max_blocks + 15) / 16;
+    if (bpw > g.bpw) g.bpw = bpw;
+    dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
+    if (g.D == 64)
+      hipLaunchKernelGGL((kstats_kernel<64>), grid, dim3(kWG), 0, st, g, jobs, err);
+    else
+      hipLaunchKernelGGL((kstats_kernel<128>), grid, dim3(kWG), 0, st, g, jobs, err);
+    if (hipGetLastError() != hipSuccess) return KVMI_ELAUNCH;
+  }
+  hipLaunchKernelGGL(kstats_finalize_kernel, dim3((unsigned)num_jobs), dim3(kWG), 0, st, g, jobs);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 

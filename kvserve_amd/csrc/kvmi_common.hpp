@@ -19,12 +19,12 @@ struct Geo {
 };
 
 struct Profile {  // decoded kvmi_layer_job::profile for one part
-  const uint8_t* order;
-  const uint8_t* levels;
-  const uint8_t* group;
+  const KVMI_GLOBAL uint8_t* order;
+  const KVMI_GLOBAL uint8_t* levels;
+  const KVMI_GLOBAL uint8_t* group;
 };
 __device__ __forceinline__ Profile part_profile(const uint8_t* p, int part, int H) {
-  const uint8_t* b = p + part * 3 * H;
+  const KVMI_GLOBAL uint8_t* b = (const KVMI_GLOBAL uint8_t*)p + part * 3 * H;
   return Profile{b, b + H, b + 2 * H};
 }
 
@@ -46,7 +46,7 @@ __device__ __forceinline__ RowPos row_pos(const kvmi_layer_job& job, int blk0, i
   const int rpb = S * H;
   const int b = blk0 + (int)(r / rpb);
   const int within = (int)(r % rpb);
-  p.pool_row = (int64_t)job.block_ids[b] * rpb + within;
+  p.pool_row = (int64_t)gld(job.block_ids + b) * rpb + within;
   p.tok = b * S + within / H;
   return p;
 }
@@ -74,23 +74,20 @@ __device__ __forceinline__ uint8_t* seg_addr(const kvmi_layer_job& job, const Ge
   return job.stream + base + (sym * BITS) / 8;
 }
 
+// The 16-byte header of a chunk stream (streams are 16-byte aligned).
 __device__ __forceinline__ bool header_matches(const uint8_t* in, int bits, int64_t chunk_symbols) {
-  uint32_t hw[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    hw[i] = (uint32_t)in[4 * i] | ((uint32_t)in[4 * i + 1] << 8) | ((uint32_t)in[4 * i + 2] << 16) |
-            ((uint32_t)in[4 * i + 3] << 24);
+  const uint4 hw = gld(reinterpret_cast<const uint4*>(in));
   const uint64_t n = (uint64_t)chunk_symbols;
-  return hw[0] == KVMI_MAGIC && hw[1] == (uint32_t)bits && hw[2] == (uint32_t)(n & 0xffffffffu) &&
-         hw[3] == (uint32_t)(n >> 32);
+  return hw.x == KVMI_MAGIC && hw.y == (uint32_t)bits && hw.z == (uint32_t)(n & 0xffffffffu) &&
+         hw.w == (uint32_t)(n >> 32);
 }
 
 __device__ __forceinline__ void write_stream_header(uint8_t* out, int bits, int64_t chunk_symbols) {
   uint32_t* o = reinterpret_cast<uint32_t*>(out);
-  o[0] = KVMI_MAGIC;
-  o[1] = (uint32_t)bits;
-  o[2] = (uint32_t)((uint64_t)chunk_symbols & 0xffffffffu);
-  o[3] = (uint32_t)((uint64_t)chunk_symbols >> 32);
+  gst(o, (uint32_t)KVMI_MAGIC);
+  gst(o + 1, (uint32_t)bits);
+  gst(o + 2, (uint32_t)((uint64_t)chunk_symbols & 0xffffffffu));
+  gst(o + 3, (uint32_t)((uint64_t)chunk_symbols >> 32));
 }
 
 // Host-side validation of a launch geometry; fills the kernel argument.

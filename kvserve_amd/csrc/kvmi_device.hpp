@@ -16,6 +16,48 @@
 
 namespace kvmi {
 
+// ---------------------------------------------------------------- global memory
+// The buffers of a job are pointers read out of a descriptor in device memory, so
+// the compiler cannot prove they are global and would emit flat_* instructions.  A
+// flat load also counts against the LDS wait counter: every LDS wait would then
+// drain the outstanding HBM loads.  All HBM accesses of the paged kernels go
+// through these address-space-1 accessors (global_* instructions) instead.
+#define KVMI_GLOBAL __attribute__((address_space(1)))
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+template <class T>
+__device__ __forceinline__ T gld(const T* p) {
+  return *(const KVMI_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ void gst(T* p, T v) {
+  *(KVMI_GLOBAL T*)p = v;
+}
+// Read-only data through the constant address space: a wave-uniform address becomes
+// a scalar load (counted by lgkmcnt, so waiting for it does not drain the streaming
+// vector loads).  Only for buffers no kernel of the launch writes.
+template <class T>
+__device__ __forceinline__ T cld(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+__device__ __forceinline__ uint4 gld(const uint4* p) {
+  const u32x4v v = *(const KVMI_GLOBAL u32x4v*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void gst(uint4* p, uint4 v) {
+  const u32x4v w = {v.x, v.y, v.z, v.w};
+  *(KVMI_GLOBAL u32x4v*)p = w;
+}
+__device__ __forceinline__ uint2 gld(const uint2* p) {
+  const u32x2v v = *(const KVMI_GLOBAL u32x2v*)p;
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ void gst(uint2* p, uint2 v) {
+  const u32x2v w = {v.x, v.y};
+  *(KVMI_GLOBAL u32x2v*)p = w;
+}
+
 // ---------------------------------------------------------------- bf16 <-> fp32
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
@@ -128,7 +170,7 @@ __device__ __forceinline__ void load_bf16_seg(const uint16_t* __restrict__ p, ui
   const uint4* p4 = reinterpret_cast<const uint4*>(p);
 #pragma unroll
   for (int i = 0; i < E / 8; ++i) {
-    uint4 t = p4[i];
+    uint4 t = gld(p4 + i);
     w[4 * i + 0] = t.x;
     w[4 * i + 1] = t.y;
     w[4 * i + 2] = t.z;
@@ -139,7 +181,7 @@ template <int E>
 __device__ __forceinline__ void store_bf16_seg(uint16_t* __restrict__ p, const uint32_t (&w)[E / 2]) {
   uint4* p4 = reinterpret_cast<uint4*>(p);
 #pragma unroll
-  for (int i = 0; i < E / 8; ++i) p4[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+  for (int i = 0; i < E / 8; ++i) gst(p4 + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
 }
 
 // Signs of the lane's E (<= 32) elements: bit i of sb set = element i negated.
@@ -205,15 +247,15 @@ __device__ __forceinline__ void store_packed(uint8_t* __restrict__ p, const Pack
   if constexpr (NB % 16 == 0) {
     uint4* p4 = reinterpret_cast<uint4*>(p);
 #pragma unroll
-    for (int i = 0; i < NB / 16; ++i) p4[i] = make_uint4(v.w[4 * i], v.w[4 * i + 1], v.w[4 * i + 2], v.w[4 * i + 3]);
+    for (int i = 0; i < NB / 16; ++i) gst(p4 + i, make_uint4(v.w[4 * i], v.w[4 * i + 1], v.w[4 * i + 2], v.w[4 * i + 3]));
   } else if constexpr (NB % 4 == 0) {
     uint32_t* p32 = reinterpret_cast<uint32_t*>(p);
 #pragma unroll
-    for (int i = 0; i < NB / 4; ++i) p32[i] = v.w[i];
+    for (int i = 0; i < NB / 4; ++i) gst(p32 + i, v.w[i]);
   } else {
     uint16_t* p16 = reinterpret_cast<uint16_t*>(p);
 #pragma unroll
-    for (int i = 0; i < NB / 2; ++i) p16[i] = (uint16_t)(v.w[i >> 1] >> ((i & 1) * 16));
+    for (int i = 0; i < NB / 2; ++i) gst(p16 + i, (uint16_t)(v.w[i >> 1] >> ((i & 1) * 16)));
   }
 }
 
@@ -224,7 +266,7 @@ __device__ __forceinline__ void load_packed(const uint8_t* __restrict__ p, Packe
     const uint4* p4 = reinterpret_cast<const uint4*>(p);
 #pragma unroll
     for (int i = 0; i < NB / 16; ++i) {
-      uint4 t = p4[i];
+      uint4 t = gld(p4 + i);
       v.w[4 * i] = t.x;
       v.w[4 * i + 1] = t.y;
       v.w[4 * i + 2] = t.z;
@@ -233,13 +275,13 @@ __device__ __forceinline__ void load_packed(const uint8_t* __restrict__ p, Packe
   } else if constexpr (NB % 4 == 0) {
     const uint32_t* p32 = reinterpret_cast<const uint32_t*>(p);
 #pragma unroll
-    for (int i = 0; i < NB / 4; ++i) v.w[i] = p32[i];
+    for (int i = 0; i < NB / 4; ++i) v.w[i] = gld(p32 + i);
   } else {
     const uint16_t* p16 = reinterpret_cast<const uint16_t*>(p);
 #pragma unroll
     for (int i = 0; i < Packed<E, BITS>::kWords; ++i) v.w[i] = 0;
 #pragma unroll
-    for (int i = 0; i < NB / 2; ++i) v.w[i >> 1] |= (uint32_t)p16[i] << ((i & 1) * 16);
+    for (int i = 0; i < NB / 2; ++i) v.w[i >> 1] |= (uint32_t)gld(p16 + i) << ((i & 1) * 16);
   }
 }
 

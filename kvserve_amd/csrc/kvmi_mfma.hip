@@ -22,11 +22,21 @@
 // before the forward transform and on the output after the inverse one, from an LDS
 // table of per-(head, element pair) masks.
 //
-// Work split: a workgroup of 4 wave64s owns a run of tokens of one (request, layer)
-// job; a tile is 32 consecutive pool rows (32/H tokens x H heads, token-major, as
-// the cache stores them), and wave w takes tiles w, w+4, ... of the run.  Because
-// 32 % H == 0, lane l always holds head (l % 32) % H, and the H heads of a token sit
-// in H neighbouring lanes of one wave.
+// Work split: a workgroup of 4 wave64s owns a run of whole blocks of one (request,
+// layer) job; a tile is 32 consecutive pool rows (32/H tokens x H heads,
+// token-major, as the cache stores them), and wave w takes tiles w, w+4, ... of the
+// run.  Because 32 % H == 0 and S*H % 32 == 0, a tile never crosses a block, lane l
+// always holds head (l % 32) % H, and the H heads of a token sit in H neighbouring
+// lanes.  Each wave issues the loads of its next section (K or V half of a tile)
+// before it computes the current one.
+//
+// Per-element VALU work is kept to the rounding chain the reference fixes:
+//   encode  y = bf16(acc*s); t = bf16(y - mn); q = bf16(t * rcp); sym = rint(q)
+//   decode  x = bf16(bf16(sym*sc) + mn)  ->  MFMA  ->  out = bf16(acc*s) ^ sign
+// with each bf16 rounding one v_cvt_pk_bf16_f32, and symbols packed four to a
+// dword by v_cvt_pk_u8_f32 before the bit-width shuffle.
+#include <atomic>
+
 #include "kvmi_common.hpp"
 
 namespace kvmi {
@@ -38,7 +48,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMW = 256;  // threads per workgroup
 constexpr int kWaves = kMW / 64;
-constexpr int kTok = 32;  // tokens per tile (MFMA rows)
+constexpr int kTok = 32;  // rows per tile (MFMA M / N)
+constexpr int kMH = 8;    // heads per shard served by these kernels (8 % H == 0)
 
 __device__ __forceinline__ bf16x8 as_b8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
@@ -53,6 +64,20 @@ __device__ __forceinline__ int opaque(int v) {
   asm volatile("" : "+v"(v));
   return v;
 }
+// A value the instruction selector may not look through (keeps byte extracts of a
+// masked word as v_cvt_f32_ubyteN instead of re-deriving them from the source).
+__device__ __forceinline__ uint32_t barrier_u(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
+// Software pipelining: the loads of the next tile are issued before the current one
+// is computed.  Pinning a buffer where its tile's work starts keeps the compiler from
+// hoisting that work (e.g. the sign flips) above the previous tile's, which would
+// make the previous tile wait for these loads.
+__device__ __forceinline__ void pin(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 
 __device__ __forceinline__ f32x16 mfma(uint4 a, uint4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(b), c, 0, 0, 0);
@@ -107,23 +132,32 @@ __device__ __forceinline__ float add_hi(uint32_t pk, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pk), sgpr_pair(0x3F800000u), c, false);
 }
 
-// Rounded-to-nearest-even integer in [0, 255] of a float, as one byte of `acc`
+// fp32 value of x rounded to bf16 (round to nearest even) in one instruction:
+// v_cvt_pk_bf16_f32 with a zero low half leaves bf16(x) << 16, which is that value.
+__device__ __forceinline__ float rbf(float x) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// Rounded-to-nearest-even integer in [0, 255] of a float, as byte BYTE of `acc`
 // (v_cvt_pk_u8_f32 rounds half to even and saturates, checked on gfx950).
 template <int BYTE>
 __device__ __forceinline__ uint32_t cvt_u8(float x, uint32_t acc) {
   return __builtin_amdgcn_cvt_pk_u8_f32(x, BYTE, acc);
 }
 
-// Symbols of an element pair (y0, y1) given per-element (mn, rcp):
-//   t = bf16(y - mn); q = bf16(t * rcp); sym = clamp(rint(q), 0, L)
-// with y rounded to bf16 first.  Returns the two rounded q values (fp32).
-__device__ __forceinline__ void quant_pair(float y0, float y1, float mn0, float mn1, float rcp0, float rcp1,
-                                           float& q0, float& q1) {
-  const uint32_t ypk = pack_bf16x2(y0, y1);
-  const uint32_t tpk = pack_bf16x2(add_lo(ypk, -mn0), add_hi(ypk, -mn1));
-  const uint32_t qpk = pack_bf16x2(bf_lo(tpk) * rcp0, bf_hi(tpk) * rcp1);
-  q0 = bf_lo(qpk);
-  q1 = bf_hi(qpk);
+// Byte BYTE of w as a float (v_cvt_f32_ubyteN).
+template <int BYTE>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+  return (float)((w >> (8 * BYTE)) & 0xffu);
+}
+
+// q = bf16(bf16(bf16(a * s) - mn) * rcp): the quantizer's value before rint
+// (quantizer_func.py:60-62; bf16(t * rcp) == bf16(t / sc) for bf16 t and sc, the
+// exact quotient being >= 2^-17 (relative) away from every bf16 midpoint).
+__device__ __forceinline__ float quant_q(float a, float s, float mn, float rcp) {
+  return rbf(rbf(rbf(a * s) - mn) * rcp);
 }
 
 // Streaming bit packer for one lane's HALF symbols (compile-time positions).
@@ -152,15 +186,15 @@ struct LanePack {
     if constexpr (kBytes % 16 == 0) {
       uint4* q = reinterpret_cast<uint4*>(p);
 #pragma unroll
-      for (int i = 0; i < kBytes / 16; ++i) q[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+      for (int i = 0; i < kBytes / 16; ++i) gst(q + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
     } else if constexpr (kBytes % 8 == 0) {
       uint2* q = reinterpret_cast<uint2*>(p);
 #pragma unroll
-      for (int i = 0; i < kBytes / 8; ++i) q[i] = make_uint2(w[2 * i], w[2 * i + 1]);
+      for (int i = 0; i < kBytes / 8; ++i) gst(q + i, make_uint2(w[2 * i], w[2 * i + 1]));
     } else {
       uint32_t* q = reinterpret_cast<uint32_t*>(p);
 #pragma unroll
-      for (int i = 0; i < kBytes / 4; ++i) q[i] = w[i];
+      for (int i = 0; i < kBytes / 4; ++i) gst(q + i, w[i]);
     }
   }
   __device__ __forceinline__ void load(const uint8_t* p) {
@@ -168,7 +202,7 @@ struct LanePack {
       const uint4* q = reinterpret_cast<const uint4*>(p);
 #pragma unroll
       for (int i = 0; i < kBytes / 16; ++i) {
-        uint4 t = q[i];
+        uint4 t = gld(q + i);
         w[4 * i] = t.x;
         w[4 * i + 1] = t.y;
         w[4 * i + 2] = t.z;
@@ -178,106 +212,277 @@ struct LanePack {
       const uint2* q = reinterpret_cast<const uint2*>(p);
 #pragma unroll
       for (int i = 0; i < kBytes / 8; ++i) {
-        uint2 t = q[i];
+        uint2 t = gld(q + i);
         w[2 * i] = t.x;
         w[2 * i + 1] = t.y;
       }
     } else {
       const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
 #pragma unroll
-      for (int i = 0; i < kBytes / 4; ++i) w[i] = q[i];
+      for (int i = 0; i < kBytes / 4; ++i) w[i] = gld(q + i);
     }
     if constexpr (kWords * 4 > kBytes) w[kWords - 1] &= 0xffffffffu >> (32 - 8 * (kBytes % 4));
   }
 };
 
+// Byte lanes of the symbols that cannot fit BITS bits (v_cvt_pk_u8_f32 saturates at
+// 255, so a symbol >= 2^BITS always shows in these bits of the OR of all bytes).
+template <int BITS>
+constexpr uint32_t overflow_mask() {
+  return 0x01010101u * (0xffu & ~((1u << BITS) - 1u));
+}
+
 // Shared per-workgroup tables.
 struct Tables {
-  uint32_t smask[kMaxH][64 + 4];  // bf16 sign-flip masks per (head, element pair), padded rows
-  float2 kc[kMaxH][128 + 4];      // K (min, 1/scale) [encode] or (min, scale) [decode], by source head
-  int posk[kMaxH], posv[kMaxH], gfirst[kMaxH];
+  uint32_t smask[kMH][64 + 4];  // bf16 sign-flip masks per (head, element pair), padded rows
+  float2 kc[kMH][128 + 4];      // K (min, 1/scale) [encode] or (min, scale) [decode], by source head
+  uint8_t prof[2][3][kMH];      // the job's profile bytes (kvmi_layer_job::profile)
+  int posk[kMH], posv[kMH], gfirst[kMH];
 };
 
-// Fill the sign-mask table: word p of head h flips elements 2p and 2p+1.
-__device__ __forceinline__ void fill_signs(Tables& T, const uint32_t* signs, int H, int D, bool transform) {
-  for (int i = threadIdx.x; i < H * (D / 2); i += kMW) {
-    const int h = i / (D / 2), p = i % (D / 2);
-    uint32_t m = 0;
-    if (transform) {
-      const uint32_t s = signs[h * (D / 32) + (2 * p) / 32] >> ((2 * p) & 31);
-      m = ((s & 1u) << 15) | ((s & 2u) << 30);
-    }
-    T.smask[h][p] = m;
+// Stage the profile bytes into LDS (one load per thread, no dependent chains).
+__device__ __forceinline__ void stage_profile(Tables& T, const uint8_t* profile, int H) {
+  if (threadIdx.x < 6u * H) {
+    const int i = threadIdx.x, part = i / (3 * H), f = (i / H) % 3, k = i % H;
+    T.prof[part][f][k] = gld(profile + i);
   }
 }
 
-__device__ __forceinline__ void fill_positions(Tables& T, const Profile& pk, const Profile& pv, int H) {
+// Fill the sign-mask table: word p of head h flips elements 2p and 2p+1.
+__device__ __forceinline__ void fill_signs(Tables& T, const uint32_t* signs, int H, int D) {
+  for (int i = threadIdx.x; i < H * (D / 2); i += kMW) {
+    const int h = i / (D / 2), p = i % (D / 2);
+    const uint32_t s = gld(signs + h * (D / 32) + (2 * p) / 32) >> ((2 * p) & 31);
+    T.smask[h][p] = ((s & 1u) << 15) | ((s & 2u) << 30);
+  }
+}
+
+// Output positions of each source head and the first head of each V group, from
+// the staged profile (after a barrier).
+__device__ __forceinline__ void fill_positions(Tables& T, int H) {
   if (threadIdx.x < (unsigned)H) {
     const int h = threadIdx.x;
     for (int k = 0; k < H; ++k) {
-      if (pk.order[k] == h) T.posk[h] = k;
-      if (pv.order[k] == h) T.posv[h] = k;
+      if (T.prof[0][0][k] == h) T.posk[h] = k;
+      if (T.prof[1][0][k] == h) T.posv[h] = k;
     }
     // first output position of V group h (if any) -> its source head
     T.gfirst[h] = -1;
     for (int k = H - 1; k >= 0; --k)
-      if (pv.group[k] == h) T.gfirst[h] = pv.order[k];
+      if (T.prof[1][2][k] == h) T.gfirst[h] = T.prof[1][0][k];
   }
 }
 
-// Tile coordinates: row r of tile t of the workgroup's run.
-struct Tile {
-  int h;           // source head (fixed per lane: r % H)
-  int tok;         // token (within the job) of this lane's row
-  bool active;     // row exists
-  int64_t row;     // pool row index (block * S*H + t_in_block*H + h)
+// K constants by source head from kmeta (stored by output position j, whose source
+// head is order[j]).  DIV: store (min, 1/scale) instead of (min, scale).
+template <bool DIV>
+__device__ __forceinline__ void fill_kconst(Tables& T, const uint16_t* kmeta, int H, int D) {
+  const int HD = H * D;
+  for (int i = threadIdx.x; i < HD; i += kMW) {
+    const int j = i / D, e = i % D, hs = T.prof[0][0][j];
+    const float m = bf16_to_f32(gld(kmeta + i));
+    const float sc = bf16_to_f32(gld(kmeta + HD + i));
+    T.kc[hs][e] = make_float2(m, DIV ? 1.0f / sc : sc);
+  }
+}
+
+// The run of tokens [tok0, tok_end) of a workgroup and its tile count.  Runs are
+// whole blocks and tiles never straddle blocks, so every row of every tile exists.
+struct Run {
+  int tok0, tok_end, tiles, nwg;
 };
-// tok_end = end of this workgroup's token run (never past the request).
-__device__ __forceinline__ Tile tile_row(const kvmi_layer_job& job, int S, int H, int tok0, int tok_end, int t, int r) {
-  Tile x;
-  const int R = t * kTok + r;  // row within the run
-  x.h = R % H;
-  x.tok = tok0 + R / H;
-  x.active = x.tok < tok_end;
-  x.row = 0;
-  if (x.active) {
-    const int b = x.tok / S;
-    x.row = ((int64_t)job.block_ids[b] * S + (x.tok % S)) * H + x.h;
-  }
-  return x;
+__device__ __forceinline__ Run wg_run(const kvmi_layer_job& job, const Geo& g) {
+  Run u;
+  const int ntok = job.num_blocks * g.S;
+  const int run = g.bpw * g.S;
+  u.nwg = (ntok + run - 1) / run;
+  u.tok0 = blockIdx.x * run;
+  u.tok_end = min(ntok, u.tok0 + run);
+  u.tiles = u.tok_end > u.tok0 ? (u.tok_end - u.tok0) * g.H / kTok : 0;
+  return u;
 }
 
-// Load (and sign) the lane's half-row of bf16 inputs.
+// Pool row of the first row of tile t (wave-uniform); lane r's row is that + r, its
+// token tile_tok(..) + r / H.
+__device__ __forceinline__ int tile_tok(int tok0, int H, int t) { return tok0 + t * (kTok / H); }
+__device__ __forceinline__ int64_t tile_row0(const kvmi_layer_job& job, int S, int H, int ta) {
+  return ((int64_t)cld(job.block_ids + ta / S) * S + (ta % S)) * H;
+}
+
+// Load (and sign) the lane's half-row of bf16 inputs of pool row `row`.
 template <int NC>
-__device__ __forceinline__ void load_half_row(const uint16_t* __restrict__ pool, const Tile& tl, int hl,
-                                              const Tables& T, uint4 (&x)[2 * NC]) {
+__device__ __forceinline__ void load_half_row(const uint16_t* __restrict__ pool, int64_t row, int hl,
+                                              uint4 (&x)[2 * NC]) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
-  if (tl.active) {
-    const uint4* src = reinterpret_cast<const uint4*>(pool + tl.row * D + HALF * hl);
+  const uint4* src = reinterpret_cast<const uint4*>(pool + row * D + HALF * hl);
 #pragma unroll
-    for (int u = 0; u < 2 * NC; ++u) x[u] = src[u];
-  } else {
-#pragma unroll
-    for (int u = 0; u < 2 * NC; ++u) x[u] = make_uint4(0, 0, 0, 0);
-  }
-  const int off = opaque(tl.h * (64 + 4) + (HALF / 2) * hl);
-  const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + off);
+  for (int u = 0; u < 2 * NC; ++u) x[u] = gld(src + u);
+}
+template <int NC>
+__device__ __forceinline__ void sign_half_row(const Tables& T, int h, int hl, uint4 (&x)[2 * NC]) {
+  constexpr int HALF = 16 * NC;
+  const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(h * (64 + 4) + (HALF / 2) * hl));
 #pragma unroll
   for (int u = 0; u < 2 * NC; ++u) x[u] = xor4(x[u], sm[u]);
 }
 
 // Forward / inverse transform, orientation T, output chunk cp (unscaled fp32).
+// The input chunks are visited in the order cp ^ k, so the chains of different
+// output chunks share no prefix (a shared prefix would keep extra accumulators live).
 template <int NC>
 __device__ __forceinline__ f32x16 transform_T(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
                                               int cp) {
   f32x16 acc = {};
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
+  for (int k = 0; k < NC; ++k) {
+    const int c = cp ^ k;
     const bool neg = __builtin_popcount(c & cp) & 1;
     acc = mfma(neg ? hn[0] : hp[0], x[2 * c], acc);
     acc = mfma(neg ? hn[1] : hp[1], x[2 * c + 1], acc);
   }
   return acc;
+}
+
+// Quantize output chunk cp (16 values of the lane's half-row) into the lane's
+// packer.  KQ: per-element (min, 1/scale) pairs from the LDS table at kq; otherwise
+// one (mn, rcp) for the row.  Widths 2, 4, 8 pack byte lanes: dword d_m holds the
+// symbols i with i % P == m (P = 8/BITS symbols per byte), and the chunk's words are
+// OR_m d_m << (m*BITS).
+template <int HALF, int BITS, bool CLAMP, bool KQ>
+__device__ __forceinline__ void quant_chunk(const f32x16& acc, int cp, float s, const float2* kq, float mn, float rcp,
+                                            float lv, LanePack<HALF, BITS>& pk, uint32_t& over) {
+  float q[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    float m0 = mn, m1 = mn, r0 = rcp, r1 = rcp;
+    if constexpr (KQ) {
+      const float4 c = *reinterpret_cast<const float4*>(kq + i);
+      m0 = c.x;
+      r0 = c.y;
+      m1 = c.z;
+      r1 = c.w;
+    }
+    q[i] = quant_q(acc[i], s, m0, r0);
+    q[i + 1] = quant_q(acc[i + 1], s, m1, r1);
+    if constexpr (CLAMP) {
+      q[i] = fminf(q[i], lv);
+      q[i + 1] = fminf(q[i + 1], lv);
+    }
+  }
+  if constexpr (BITS == 2 || BITS == 4 || BITS == 8) {
+    constexpr int P = 8 / BITS, W = BITS / 2;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int m = 0; m < P; ++m) {
+        uint32_t d = cvt_u8<0>(q[P * (4 * j) + m], 0u);
+        d = cvt_u8<1>(q[P * (4 * j + 1) + m], d);
+        d = cvt_u8<2>(q[P * (4 * j + 2) + m], d);
+        d = cvt_u8<3>(q[P * (4 * j + 3) + m], d);
+        over |= d;
+        word |= d << (m * BITS);
+      }
+      pk.w[cp * W + j] = word;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t sym = cvt_u8<0>(q[i], 0u);
+      over |= sym;
+      pk.put(16 * cp + i, sym);
+    }
+  }
+}
+
+// The 8 symbols of operand u (elements 8u .. 8u+7 of the half-row) as floats.
+template <int HALF, int BITS>
+__device__ __forceinline__ void syms8(const LanePack<HALF, BITS>& pk, int u, float (&s)[8]) {
+  if constexpr (BITS == 4) {
+    const uint32_t w = pk.w[u];
+    const uint32_t lo = barrier_u(w & 0x0F0F0F0Fu), hi = barrier_u((w >> 4) & 0x0F0F0F0Fu);
+    s[0] = ubyte<0>(lo);
+    s[1] = ubyte<0>(hi);
+    s[2] = ubyte<1>(lo);
+    s[3] = ubyte<1>(hi);
+    s[4] = ubyte<2>(lo);
+    s[5] = ubyte<2>(hi);
+    s[6] = ubyte<3>(lo);
+    s[7] = ubyte<3>(hi);
+  } else if constexpr (BITS == 8) {
+    const uint32_t a = pk.w[2 * u], b = pk.w[2 * u + 1];
+    s[0] = ubyte<0>(a);
+    s[1] = ubyte<1>(a);
+    s[2] = ubyte<2>(a);
+    s[3] = ubyte<3>(a);
+    s[4] = ubyte<0>(b);
+    s[5] = ubyte<1>(b);
+    s[6] = ubyte<2>(b);
+    s[7] = ubyte<3>(b);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = (float)pk.get(8 * u + j);
+  }
+}
+
+// Dequantized bf16 MFMA operands of the lane's half-row: x~ = bf16(bf16(sym*sc) + mn)
+// (quantizer_func.py:108-112).  KQ: per-element (min, scale) pairs from the LDS
+// table at kd; otherwise the row's (mn, sc).
+template <int NC, int BITS, bool KQ>
+__device__ __forceinline__ void dequant_half_row(const LanePack<16 * NC, BITS>& pk, const float2* kd, float mn,
+                                                 float sc, uint4 (&x)[2 * NC]) {
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) {
+    float sy[8];
+    syms8<16 * NC, BITS>(pk, u, sy);
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (KQ) {
+        // per-element constants: the pair's sums come straight out of v_dot2
+        const float4 c = *reinterpret_cast<const float4*>(&kd[8 * u + 2 * p]);
+        const uint32_t spk = pack_bf16x2(sy[2 * p] * c.y, sy[2 * p + 1] * c.w);
+        w[p] = pack_bf16x2(add_lo(spk, c.x), add_hi(spk, c.z));
+      } else {
+        // one row minimum: plain adds (v_dot2c would need a copy of it per element)
+        w[p] = pack_bf16x2(rbf(sy[2 * p] * sc) + mn, rbf(sy[2 * p + 1] * sc) + mn);
+      }
+    }
+    x[u] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// DPP lane exchange of a float (no bound_ctrl; every lane is enabled).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Min / max over the H lanes of a token (aligned groups of H in 1, 2, 4, 8):
+// quad_perm xor 1, xor 2, then row_half_mirror (lane i <-> 7 - i of each 8).
+__device__ __forceinline__ void token_minmax(float& a, float& b, int H) {
+  if (H >= 2) {
+    a = fminf(a, dpp<0xB1>(a));
+    b = fmaxf(b, dpp<0xB1>(b));
+  }
+  if (H >= 4) {
+    a = fminf(a, dpp<0x4E>(a));
+    b = fmaxf(b, dpp<0x4E>(b));
+  }
+  if (H >= 8) {
+    a = fminf(a, dpp<0x141>(a));
+    b = fmaxf(b, dpp<0x141>(b));
+  }
+}
+// Min / max of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the upper 32
+// lanes of its first operand with the lower 32 lanes of its second; with x in both,
+// result 0 holds x of lane l % 32 and result 1 x of lane 32 + l % 32.
+__device__ __forceinline__ float halves_min(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // ============================================================== K statistics (orientation N)
@@ -287,20 +492,15 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
   constexpr int D = 32 * NC;
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int S = g.S, H = g.H;
-  const int ntok = job.num_blocks * S;
-  const int run = g.bpw * S;  // tokens per workgroup (multiple of 32)
-  const int nwg = (ntok + run - 1) / run;
-  if ((int)blockIdx.x >= nwg) return;
-  const int tok0 = blockIdx.x * run;
-  const int tok_end = min(ntok, tok0 + run);
-  const int tiles = ((tok_end - tok0) * H + kTok - 1) / kTok;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
-  const bool transform = true;  // MFMA kernels serve the transform profile only
+  const Run run = wg_run(job, g);
+  if ((int)blockIdx.x >= run.nwg) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
+  const int hme = r % H;
 
   __shared__ Tables T;
-  __shared__ uint32_t lkey[2 * kMaxHD];
-  __shared__ int last;
-  fill_signs(T, job.signs, H, D, transform);
+  __shared__ uint32_t lkey[2 * kMH * 128];
+  fill_signs(T, job.signs, H, D);
   for (int i = threadIdx.x; i < H * D; i += kMW) {
     lkey[i] = 0xffffffffu;
     lkey[H * D + i] = 0u;
@@ -324,45 +524,56 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
       mx[a][c] = -__builtin_inff();
     }
   const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
-  for (int t = wave; t < tiles; t += kWaves) {
-    const Tile tl = tile_row(job, S, H, tok0, tok_end, t, r);
-    uint4 x[2 * NC];
-    load_half_row<NC>(pool, tl, hl, T, x);
-    const int valid = min(kTok, (tok_end - tok0) * H - t * kTok);  // rows of this tile that exist
+  auto accumulate = [&](uint4 (&x)[2 * NC]) {
+#pragma unroll
+    for (int u = 0; u < 2 * NC; ++u) pin(x[u]);
+    sign_half_row<NC>(T, hme, hl, x);
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
       f32x16 acc = {};
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
+      for (int k = 0; k < NC; ++k) {
+        const int c = cp ^ k;
         const bool neg = __builtin_popcount(c & cp) & 1;
         acc = mfma(x[2 * c], neg ? hn[0] : hp[0], acc);
         acc = mfma(x[2 * c + 1], neg ? hn[1] : hp[1], acc);
       }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int m = 8 * (i / 4) + 4 * hl + (i % 4);
-        if (m < valid) {
-          mn[i % 4][cp] = fminf(mn[i % 4][cp], acc[i]);
-          mx[i % 4][cp] = fmaxf(mx[i % 4][cp], acc[i]);
-        }
+      for (int a = 0; a < 4; ++a) {
+        mn[a][cp] = fminf(fminf(mn[a][cp], acc[a]), fminf(acc[a + 4], fminf(acc[a + 8], acc[a + 12])));
+        mx[a][cp] = fmaxf(fmaxf(mx[a][cp], acc[a]), fmaxf(acc[a + 4], fmaxf(acc[a + 8], acc[a + 12])));
       }
       chunk_fence();
     }
+  };
+  auto fetch = [&](int t, uint4 (&x)[2 * NC]) {
+    load_half_row<NC>(pool, tile_row0(job, S, H, tile_tok(run.tok0, H, t)) + r, hl, x);
+  };
+  // Two buffers: the loads of tile t + 4 are in flight while tile t is reduced.  The
+  // prefetch is unconditional (past the end it re-reads the current tile, a cache
+  // hit): loads issued on one path only make the compiler's wait counts conservative.
+  const int last_tile = run.tiles - 1;
+  uint4 xa[2 * NC], xb[2 * NC];
+  if (wave < run.tiles) fetch(wave, xa);
+  for (int t = wave; t < run.tiles; t += 2 * kWaves) {
+    fetch(min(t + kWaves, last_tile), xb);
+    accumulate(xa);
+    if (t + kWaves >= run.tiles) break;
+    fetch(min(t + 2 * kWaves, last_tile), xa);
+    accumulate(xb);
   }
   // Push per (head, channel): scaling by 1/sqrt(D) > 0 is monotone, so it commutes
   // with min / max (and so does the bf16 rounding applied by the finaliser).
   const int HD = H * D;
+  if (wave < run.tiles) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int h = (4 * hl + a) % H;
+    for (int a = 0; a < 4; ++a) {
+      const int h = (4 * hl + a) % H;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int f = (16 * NC) * (r >> 4) + 16 * c + (r & 15);
-      const float smn = mn[a][c] * g.scale;
-      const float smx = mx[a][c] * g.scale;
-      if (smn <= smx) {  // at least one row of this head went through the slot
-        atomicMin(&lkey[h * D + f], f2key(smn));
-        atomicMax(&lkey[HD + h * D + f], f2key(smx));
+      for (int c = 0; c < NC; ++c) {
+        const int f = (16 * NC) * (r >> 4) + 16 * c + (r & 15);
+        atomicMin(&lkey[h * D + f], f2key(mn[a][c] * g.scale));
+        atomicMax(&lkey[HD + h * D + f], f2key(mx[a][c] * g.scale));
       }
     }
   }
@@ -371,68 +582,6 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
     if (lkey[i] != 0xffffffffu) atomicMin(&job.kstats[i], lkey[i]);
     if (lkey[HD + i] != 0u) atomicMax(&job.kstats[HD + i], lkey[HD + i]);
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = (atomicAdd(job.counter, 1u) == (unsigned)(nwg - 1)) ? 1 : 0;
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const Profile pk = part_profile(job.profile, 0, H);
-  for (int i = threadIdx.x; i < HD; i += kMW) {
-    const float kmn = round_bf16(key2f(__hip_atomic_exchange(&job.kstats[i], 0xffffffffu, __ATOMIC_RELAXED,
-                                                             __HIP_MEMORY_SCOPE_AGENT)));
-    const float kmx =
-        round_bf16(key2f(__hip_atomic_exchange(&job.kstats[HD + i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
-    const int hs = i / D, e = i % D;
-    int j = 0;
-    for (int k = 0; k < H; ++k)
-      if (pk.order[k] == hs) j = k;
-    const float sc = quant_scale(kmn, kmx, pk.levels[j]);
-    job.kmeta[j * D + e] = (uint16_t)f32_to_bf16_bits(kmn);
-    job.kmeta[HD + j * D + e] = (uint16_t)f32_to_bf16_bits(sc);
-  }
-  if (threadIdx.x == 0) __hip_atomic_exchange(job.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Quantize and pack one lane's output half-row (HALF = 16*NC values in NC chunks of
-// 16) computed on the fly by transform_T.  KQ: per-element (min, 1/scale) from the
-// LDS table; otherwise one (mn, rcp) for the whole row.
-template <int NC, int BITS, bool CLAMP, bool KQ>
-__device__ __forceinline__ uint32_t quantize_half_row(const uint4 (&x)[2 * NC], const uint4 (&hp)[2],
-                                                      const uint4 (&hn)[2], float scale, const float2* kq_row,
-                                                      float mn, float rcp, float lv, LanePack<16 * NC, BITS>& pk) {
-  pk.clear();
-  uint32_t over = 0;
-#pragma unroll
-  for (int cp = 0; cp < NC; ++cp) {
-    float y[16];
-    const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) y[i] = acc[i] * scale;
-#pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      float m0 = mn, m1 = mn, r0 = rcp, r1 = rcp;
-      if (KQ) {
-        const float4 c = *reinterpret_cast<const float4*>(&kq_row[16 * cp + i]);
-        m0 = c.x;
-        r0 = c.y;
-        m1 = c.z;
-        r1 = c.w;
-      }
-      float q0, q1;
-      quant_pair(y[i], y[i + 1], m0, m1, r0, r1, q0, q1);
-      if (CLAMP) {
-        q0 = fminf(q0, lv);
-        q1 = fminf(q1, lv);
-      }
-      const uint32_t s0 = cvt_u8<0>(q0, 0u), s1 = cvt_u8<0>(q1, 0u);
-      over |= s0 | s1;
-      pk.put(16 * cp + i, s0);
-      pk.put(16 * cp + i + 1, s1);
-    }
-    chunk_fence();
-  }
-  return over;
 }
 
 // ============================================================== encode (orientation T)
@@ -443,29 +592,19 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int S = g.S, H = g.H, G = g.G, HD = H * D;
   const int ntok = job.num_blocks * S;
-  const int run = g.bpw * S;
-  const int nwg = (ntok + run - 1) / run;
-  if ((int)blockIdx.x >= nwg) return;
-  const int tok0 = blockIdx.x * run;
-  const int tok_end = min(ntok, tok0 + run);
-  const int tiles = ((tok_end - tok0) * H + kTok - 1) / kTok;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
-  const bool transform = true;  // MFMA kernels serve the transform profile only
-  const Profile pk = part_profile(job.profile, 0, H);
-  const Profile pv = part_profile(job.profile, 1, H);
+  const Run run = wg_run(job, g);
+  if ((int)blockIdx.x >= run.nwg) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
 
   __shared__ Tables T;
-  fill_signs(T, job.signs, H, D, transform);
-  fill_positions(T, pk, pv, H);
+  stage_profile(T, job.profile, H);
+  fill_signs(T, job.signs, H, D);
   if (threadIdx.x == 0 && job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER))
     write_stream_header(job.stream, BITS, job.chunk_symbols);
   __syncthreads();
-  for (int i = threadIdx.x; i < HD; i += kMW) {
-    const int hs = i / D, e = i % D, j = T.posk[hs];
-    const float m = bf16_to_f32(job.kmeta[j * D + e]);
-    const float sc = bf16_to_f32(job.kmeta[HD + j * D + e]);
-    T.kc[hs][e] = make_float2(m, 1.0f / sc);
-  }
+  fill_positions(T, H);
+  fill_kconst<true>(T, job.kmeta, H, D);
   __syncthreads();
 
   uint4 hp[2], hn[2];
@@ -477,87 +616,86 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const uint16_t* poolV = poolK + job.pool_part_stride;
   uint32_t over = 0;
 
-  // V statistic groups of this lane's head and of the H heads of its token
+  // this lane's head, its output positions and V statistic group
   const int hme = r % H;
   const int jk = T.posk[hme], jv = T.posv[hme];
-  const int gv = pv.group[jv];
-  const float lvk = (float)pk.levels[jk], lvv = (float)pv.levels[jv];
+  const int gv = T.prof[1][2][jv];
+  const float lvk = (float)T.prof[0][1][jk], lvv = (float)T.prof[1][1][jv];
   const bool rep_lane = hl == 0 && T.gfirst[gv] == hme;  // writes the V metadata of (group, token)
-  for (int t = wave; t < tiles; t += kWaves) {
-    const Tile tl = tile_row(job, S, H, tok0, tok_end, t, r);
+  const float s = g.scale;
+
+  uint4 xk[2 * NC], xv[2 * NC];
+  if (wave < run.tiles) load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, wave)) + r, hl, xk);
+  for (int t = wave; t < run.tiles; t += kWaves) {
+#pragma unroll
+    for (int u = 0; u < 2 * NC; ++u) pin(xk[u]);
+    const int ta = tile_tok(run.tok0, H, t);
+    const int64_t row = tile_row0(job, S, H, ta) + r;
+    const int tok = ta + r / H;
+    load_half_row<NC>(poolV, row, hl, xv);
     // ---------------- K: per-channel statistics from the kstats pass
     {
-      uint4 x[2 * NC];
-      load_half_row<NC>(poolK, tl, hl, T, x);
+      sign_half_row<NC>(T, hme, hl, xk);
       LanePack<HALF, BITS> pkd;
-      const float2* kq_row = &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl);
-      over |= quantize_half_row<NC, BITS, CLAMP, true>(x, hp, hn, g.scale, kq_row, 0.f, 0.f, lvk, pkd);
-      if (tl.active) pkd.store(seg_addr<BITS>(job, g, 0, jk, tl.tok, HALF * hl));
+      pkd.clear();
+      const float2* kq = &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl);
+#pragma unroll
+      for (int cp = 0; cp < NC; ++cp) {
+        const f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
+        quant_chunk<HALF, BITS, CLAMP, true>(acc, cp, s, kq + 16 * cp, 0.f, 0.f, lvk, pkd, over);
+        chunk_fence();
+      }
+      pkd.store(seg_addr<BITS>(job, g, 0, jk, tok, HALF * hl));
     }
-    chunk_fence();
+    // next tile's K (unconditional: past the end it re-reads this tile, a cache hit)
+    const int tn = min(t + kWaves, run.tiles - 1);
+    load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)) + r, hl, xk);
     // ---------------- V: per-token statistics over the heads of a group
-    uint4 x[2 * NC];
-    load_half_row<NC>(poolV, tl, hl, T, x);
-    uint32_t ypk[HALF / 2];
-    float lmn = __builtin_inff(), lmx = -__builtin_inff();
+    sign_half_row<NC>(T, hme, hl, xv);
+    float amn = __builtin_inff(), amx = -__builtin_inff();
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
-      float y[16];
-      const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
+      const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) y[i] = acc[i] * g.scale;
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) {
-        const uint32_t p = pack_bf16x2(y[i], y[i + 1]);
-        ypk[(16 * cp + i) / 2] = p;
-        lmn = fminf(lmn, fminf(bf_lo(p), bf_hi(p)));
-        lmx = fmaxf(lmx, fmaxf(bf_lo(p), bf_hi(p)));
+      for (int i = 0; i < 16; i += 4) {
+        amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
+        amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
       }
       chunk_fence();
     }
-    // whole row, then the heads of this token that share the group: lanes
-    // (r / H) * H .. + H - 1 of this half hold the token's H heads
-    lmn = fminf(lmn, __shfl_xor(lmn, 32));
-    lmx = fmaxf(lmx, __shfl_xor(lmx, 32));
-    float mn = __builtin_inff(), mx = -__builtin_inff();
+    // y = bf16(fl(acc * s)) is monotone in acc (s > 0): the row's min / max of y
+    // are those of acc pushed through the same rounding.
+    amn = halves_min(amn);
+    amx = halves_max(amx);
+    float mn = 0.f, mx = 0.f;
     for (int gg = 0; gg < G; ++gg) {
-      float a = gv == gg ? lmn : __builtin_inff();
-      float b = gv == gg ? lmx : -__builtin_inff();
-      for (int step = 1; step < H; step <<= 1) {
-        a = fminf(a, __shfl_xor(a, step));
-        b = fmaxf(b, __shfl_xor(b, step));
-      }
+      float a = gv == gg ? amn : __builtin_inff();
+      float b = gv == gg ? amx : -__builtin_inff();
+      token_minmax(a, b, H);
       if (gv == gg) {
         mn = a;
         mx = b;
       }
     }
-    const float sc = quant_scale(mn, mx, pv.levels[jv]);
+    mn = rbf(mn * s);
+    mx = rbf(mx * s);
+    const float sc = quant_scale(mn, mx, (int)lvv);
     const float rcp = 1.0f / sc;
-    if (tl.active && rep_lane) {
-      job.vmeta[(int64_t)gv * ntok + tl.tok] = (uint16_t)f32_to_bf16_bits(mn);
-      job.vmeta[(int64_t)(G + gv) * ntok + tl.tok] = (uint16_t)f32_to_bf16_bits(sc);
+    if (rep_lane) {
+      gst(job.vmeta + (int64_t)gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
+      gst(job.vmeta + (int64_t)(G + gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
     }
     LanePack<HALF, BITS> pkd;
     pkd.clear();
 #pragma unroll
-    for (int i = 0; i < HALF; i += 2) {
-      const uint32_t p = ypk[i / 2];
-      const uint32_t tpk = pack_bf16x2(add_lo(p, -mn), add_hi(p, -mn));
-      const uint32_t qpk = pack_bf16x2(bf_lo(tpk) * rcp, bf_hi(tpk) * rcp);
-      float q0 = bf_lo(qpk), q1 = bf_hi(qpk);
-      if (CLAMP) {
-        q0 = fminf(q0, lvv);
-        q1 = fminf(q1, lvv);
-      }
-      const uint32_t s0 = cvt_u8<0>(q0, 0u), s1 = cvt_u8<0>(q1, 0u);
-      over |= s0 | s1;
-      pkd.put(i, s0);
-      pkd.put(i + 1, s1);
+    for (int cp = 0; cp < NC; ++cp) {
+      const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+      quant_chunk<HALF, BITS, CLAMP, false>(acc, cp, s, nullptr, mn, rcp, lvv, pkd, over);
+      chunk_fence();
     }
-    if (tl.active) pkd.store(seg_addr<BITS>(job, g, 1, jv, tl.tok, HALF * hl));
+    pkd.store(seg_addr<BITS>(job, g, 1, jv, tok, HALF * hl));
   }
-  if (over >> BITS) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
+  if (over & overflow_mask<BITS>()) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
 }
 
 // ============================================================== decode (orientation T)
@@ -566,18 +704,12 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
                                                           int32_t* __restrict__ err) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
   const kvmi_layer_job job = jobs[blockIdx.y];
-  const int S = g.S, H = g.H, G = g.G, HD = H * D;
+  const int S = g.S, H = g.H, G = g.G;
   const int ntok = job.num_blocks * S;
-  const int run = g.bpw * S;
-  const int nwg = (ntok + run - 1) / run;
-  if ((int)blockIdx.x >= nwg) return;
-  const int tok0 = blockIdx.x * run;
-  const int tok_end = min(ntok, tok0 + run);
-  const int tiles = ((tok_end - tok0) * H + kTok - 1) / kTok;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
-  const bool transform = true;  // MFMA kernels serve the transform profile only
-  const Profile pk = part_profile(job.profile, 0, H);
-  const Profile pv = part_profile(job.profile, 1, H);
+  const Run run = wg_run(job, g);
+  if ((int)blockIdx.x >= run.nwg) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
 
   __shared__ Tables T;
   __shared__ int ok;
@@ -589,14 +721,12 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
     }
     ok = good;
   }
-  fill_signs(T, job.signs, H, D, transform);
-  fill_positions(T, pk, pv, H);
+  stage_profile(T, job.profile, H);
+  fill_signs(T, job.signs, H, D);
   __syncthreads();
   if (!ok) return;
-  for (int i = threadIdx.x; i < HD; i += kMW) {
-    const int hs = i / D, e = i % D, j = T.posk[hs];
-    T.kc[hs][e] = make_float2(bf16_to_f32(job.kmeta[j * D + e]), bf16_to_f32(job.kmeta[HD + j * D + e]));
-  }
+  fill_positions(T, H);
+  fill_kconst<false>(T, job.kmeta, H, D);
   __syncthreads();
 
   uint4 hp[2], hn[2];
@@ -605,146 +735,156 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
   hn[0] = hadamard_tile(0, false, true);
   hn[1] = hadamard_tile(1, false, true);
   uint16_t* poolK = reinterpret_cast<uint16_t*>(job.pool);
-  uint16_t* poolV = poolK + job.pool_part_stride;
+  const int hme = r % H;
+  const int jk = T.posk[hme], jv = T.posv[hme];
+  const int gv = T.prof[1][2][jv];
+  const float s = g.scale;
 
-  for (int t2 = wave; t2 < 2 * tiles; t2 += kWaves) {
-    const int part = t2 / tiles, t = t2 % tiles;
-    const Tile tl = tile_row(job, S, H, tok0, tok_end, t, r);
-    const int j = part ? T.posv[tl.h] : T.posk[tl.h];
-    // every lane takes part in the MFMAs (rows are independent columns of B);
-    // rows past the run end decode zero symbols and are not stored
-    LanePack<HALF, BITS> pkd;
-    pkd.clear();
-    if (tl.active) pkd.load(seg_addr<BITS>(job, g, part, j, tl.tok, HALF * hl));
-    float vmn = 0.f, vsc = 0.f;
-    if (part && tl.active) {
-      const int gv = pv.group[j];
-      vmn = bf16_to_f32(job.vmeta[(int64_t)gv * ntok + tl.tok]);
-      vsc = bf16_to_f32(job.vmeta[(int64_t)(G + gv) * ntok + tl.tok]);
-    }
-    const float2* kd = &T.kc[0][0] + opaque(tl.h * (128 + 4) + HALF * hl);
+  // section q = part * tiles + t: K tiles, then V tiles.  A section's inputs are its
+  // packed symbols and, for V, the row's (min, scale).
+  struct In {
+    LanePack<HALF, BITS> pk;
+    uint32_t mn, sc;  // bf16 bits of the V row's (min, scale); unused for K
+  };
+  // Loads of every section have the same shape (the V metadata of the token is read
+  // for K sections too), so no load is issued on one path only.
+  auto fetch = [&](int q, In& in) {
+    const int part = q >= run.tiles, t = q - part * run.tiles;
+    const int tok = tile_tok(run.tok0, H, t) + r / H;
+    in.pk.load(seg_addr<BITS>(job, g, part, part ? jv : jk, tok, HALF * hl));
+    in.mn = gld(job.vmeta + (int64_t)gv * ntok + tok);
+    in.sc = gld(job.vmeta + (int64_t)(G + gv) * ntok + tok);
+  };
+  auto section = [&](int q, In& in) {
+#pragma unroll
+    for (int i = 0; i < LanePack<HALF, BITS>::kWords; ++i) pin(in.pk.w[i]);
+    pin(in.mn);
+    pin(in.sc);
+    const int part = q >= run.tiles, t = q - part * run.tiles;
+    const int64_t row = tile_row0(job, S, H, tile_tok(run.tok0, H, t)) + r;
     // dequantize into bf16 MFMA operands: x~ = bf16(bf16(q * scale) + min)
     uint4 x[2 * NC];
-#pragma unroll
-    for (int u = 0; u < 2 * NC; ++u) {
-      uint32_t w[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int e = 8 * u + 2 * p;
-        float m0 = vmn, m1 = vmn, s0 = vsc, s1 = vsc;
-        if (!part) {
-          const float4 c = *reinterpret_cast<const float4*>(&kd[e]);
-          m0 = c.x;
-          s0 = c.y;
-          m1 = c.z;
-          s1 = c.w;
-        }
-        const uint32_t spk = pack_bf16x2((float)pkd.get(e) * s0, (float)pkd.get(e + 1) * s1);
-        w[p] = pack_bf16x2(add_lo(spk, m0), add_hi(spk, m1));
-      }
-      x[u] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    if (part)
+      dequant_half_row<NC, BITS, false>(in.pk, nullptr, bf16_to_f32(in.mn), bf16_to_f32(in.sc), x);
+    else
+      dequant_half_row<NC, BITS, true>(in.pk, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), 0.f, 0.f, x);
     chunk_fence();
-    uint16_t* dst = (part ? poolV : poolK) + tl.row * D + HALF * hl;
-    const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(tl.h * (64 + 4) + (HALF / 2) * hl));
-    {
+    uint16_t* dst = poolK + part * job.pool_part_stride + row * D + HALF * hl;
+    const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(hme * (64 + 4) + (HALF / 2) * hl));
 #pragma unroll
-      for (int cp = 0; cp < NC; ++cp) {
-        const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
-        uint32_t w[8];
+    for (int cp = 0; cp < NC; ++cp) {
+      const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
+      uint32_t w[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = pack_bf16x2(acc[2 * i] * g.scale, acc[2 * i + 1] * g.scale);
-        const uint4 a = xor4(make_uint4(w[0], w[1], w[2], w[3]), sm[2 * cp]);
-        const uint4 b = xor4(make_uint4(w[4], w[5], w[6], w[7]), sm[2 * cp + 1]);
-        if (tl.active) {
-          reinterpret_cast<uint4*>(dst)[2 * cp] = a;
-          reinterpret_cast<uint4*>(dst)[2 * cp + 1] = b;
-        }
-        chunk_fence();
-      }
+      for (int i = 0; i < 8; ++i) w[i] = pack_bf16x2(acc[2 * i] * s, acc[2 * i + 1] * s);
+      gst(reinterpret_cast<uint4*>(dst) + 2 * cp, xor4(make_uint4(w[0], w[1], w[2], w[3]), sm[2 * cp]));
+      gst(reinterpret_cast<uint4*>(dst) + 2 * cp + 1, xor4(make_uint4(w[4], w[5], w[6], w[7]), sm[2 * cp + 1]));
+      chunk_fence();
     }
+  };
+  // Two input buffers: section q + 4 is loading while section q is computed (past the
+  // end the prefetch re-reads the current section, a cache hit).
+  const int nsec = 2 * run.tiles, last_sec = nsec - 1;
+  In a, b;
+  if (wave < nsec) fetch(wave, a);
+  for (int q = wave; q < nsec; q += 2 * kWaves) {
+    fetch(min(q + kWaves, last_sec), b);
+    section(q, a);
+    if (q + kWaves >= nsec) break;
+    fetch(min(q + 2 * kWaves, last_sec), a);
+    section(q + kWaves, b);
   }
 }
 
 // ============================================================== launch
-// Tokens per workgroup: whole 32-token groups and whole blocks.
-int mfma_run_blocks(const Geo& g, int32_t max_blocks, int target_wgs_per_job) {
-  // blocks per workgroup: a multiple of the blocks that make up 32 tokens
-  const int unit = (kTok + g.S - 1) / g.S;  // S divides 32 or 32 divides S*? (S*H % 32 == 0 checked)
-  int bpw = unit;
-  if (target_wgs_per_job > 0) {
-    const int want = (max_blocks + target_wgs_per_job - 1) / target_wgs_per_job;
-    bpw = ((want + unit - 1) / unit) * unit;
-    if (bpw < unit) bpw = unit;
+// Workgroups that fit on the device at once for `kernel` (CUs x resident
+// workgroups per CU), per device, computed on first use.
+constexpr int kMaxDevices = 64;
+template <class K>
+int resident_wgs(K kernel) {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1024;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel), kMW, 0) !=
+        hipSuccess)
+      per = 2;
+    v = (cus > 0 ? cus : 1) * (per > 0 ? per : 1);
+    cache[dev].store(v, std::memory_order_relaxed);
   }
-  return bpw;
+  return v;
+}
+
+// Blocks per workgroup: whole multiples of the blocks that make up a 32-row tile
+// (S*H % 32 == 0), sized so that the launch is about `target` workgroups.
+int run_blocks(const Geo& g, int32_t max_blocks, int32_t num_jobs, int target) {
+  const int unit = (kTok / g.H + g.S - 1) / g.S;  // blocks per tile (1 when S >= 32/H)
+  const int64_t total = (int64_t)max_blocks * (num_jobs > 0 ? num_jobs : 1);
+  int64_t want = (total + target - 1) / (target > 0 ? target : 1);
+  if (want > max_blocks) want = max_blocks;
+  int bpw = (int)((want + unit - 1) / unit) * unit;
+  return bpw < unit ? unit : bpw;
+}
+
+// Workgroups per resident slot: more, shorter runs balance the end of a launch
+// better; each run also pays its table set-up once.
+constexpr int kWavesKstats = 1, kWavesEncode = 3, kWavesDecode = 3;
+
+template <class K>
+int launch(K kernel, Geo g, int32_t num_jobs, int32_t max_blocks, const kvmi_layer_job* jobs, int32_t* err,
+           hipStream_t st, int rounds) {
+  if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
+  g.bpw = run_blocks(g, max_blocks, num_jobs, resident_wgs(kernel) * rounds);
+  const int per_job = (max_blocks + g.bpw - 1) / g.bpw;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)per_job, (unsigned)num_jobs), dim3(kMW), 0, st, g, jobs, err);
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
 template <int NC, int BITS>
-void launch_enc(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
+int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
   if (g.flags & KVMI_F_CLAMP_LEVELS)
-    hipLaunchKernelGGL((encode_mfma_kernel<NC, BITS, true>), grid, dim3(kMW), 0, st, g, jobs, err);
-  else
-    hipLaunchKernelGGL((encode_mfma_kernel<NC, BITS, false>), grid, dim3(kMW), 0, st, g, jobs, err);
+    return launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode);
+  return launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
 }
 template <int NC, int BITS>
-void launch_dec(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
-  hipLaunchKernelGGL((decode_mfma_kernel<NC, BITS>), grid, dim3(kMW), 0, st, g, jobs, err);
+int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
+  return launch(decode_mfma_kernel<NC, BITS>, g, nj, mb, jobs, err, st, kWavesDecode);
 }
 
-#define KVMI_MFMA_BITS(FN, NC, g, grid, jobs, err, st) \
-  switch ((g).bits) {                                  \
-    case 1: FN<NC, 1>(g, grid, jobs, err, st); break;  \
-    case 2: FN<NC, 2>(g, grid, jobs, err, st); break;  \
-    case 3: FN<NC, 3>(g, grid, jobs, err, st); break;  \
-    case 4: FN<NC, 4>(g, grid, jobs, err, st); break;  \
-    case 5: FN<NC, 5>(g, grid, jobs, err, st); break;  \
-    case 6: FN<NC, 6>(g, grid, jobs, err, st); break;  \
-    case 7: FN<NC, 7>(g, grid, jobs, err, st); break;  \
-    default: FN<NC, 8>(g, grid, jobs, err, st); break; \
+#define KVMI_MFMA_BITS(FN, NC)                                 \
+  switch (g.bits) {                                            \
+    case 1: return FN<NC, 1>(g, nj, mb, jobs, err, st);        \
+    case 2: return FN<NC, 2>(g, nj, mb, jobs, err, st);        \
+    case 3: return FN<NC, 3>(g, nj, mb, jobs, err, st);        \
+    case 4: return FN<NC, 4>(g, nj, mb, jobs, err, st);        \
+    case 5: return FN<NC, 5>(g, nj, mb, jobs, err, st);        \
+    case 6: return FN<NC, 6>(g, nj, mb, jobs, err, st);        \
+    case 7: return FN<NC, 7>(g, nj, mb, jobs, err, st);        \
+    default: return FN<NC, 8>(g, nj, mb, jobs, err, st);       \
   }
 
 }  // namespace
 
-int mfma_kstats(const Geo& g0, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
-                hipStream_t st) {
-  Geo g = g0;
-  g.bpw = mfma_run_blocks(g, max_blocks, 8);  // <= ~8 workgroups per job: few global atomics
-  const int ntok = max_blocks * g.S, run = g.bpw * g.S;
-  dim3 grid((unsigned)((ntok + run - 1) / run), (unsigned)num_jobs);
-  if (g.D == 64)
-    hipLaunchKernelGGL((kstats_mfma_kernel<2>), grid, dim3(kMW), 0, st, g, jobs, err);
-  else
-    hipLaunchKernelGGL((kstats_mfma_kernel<4>), grid, dim3(kMW), 0, st, g, jobs, err);
-  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+int mfma_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
+  if (g.D == 64) return launch(kstats_mfma_kernel<2>, g, nj, mb, jobs, err, st, kWavesKstats);
+  return launch(kstats_mfma_kernel<4>, g, nj, mb, jobs, err, st, kWavesKstats);
 }
 
-int mfma_encode(const Geo& g0, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
-                hipStream_t st) {
-  Geo g = g0;
-  g.bpw = mfma_run_blocks(g, max_blocks, 0);
-  const int ntok = max_blocks * g.S, run = g.bpw * g.S;
-  dim3 grid((unsigned)((ntok + run - 1) / run), (unsigned)num_jobs);
+int mfma_encode(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
   if (g.D == 64) {
-    KVMI_MFMA_BITS(launch_enc, 2, g, grid, jobs, err, st)
-  } else {
-    KVMI_MFMA_BITS(launch_enc, 4, g, grid, jobs, err, st)
+    KVMI_MFMA_BITS(launch_enc, 2)
   }
-  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+  KVMI_MFMA_BITS(launch_enc, 4)
 }
 
-int mfma_decode(const Geo& g0, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
-                hipStream_t st) {
-  Geo g = g0;
-  g.bpw = mfma_run_blocks(g, max_blocks, 0);
-  const int ntok = max_blocks * g.S, run = g.bpw * g.S;
-  dim3 grid((unsigned)((ntok + run - 1) / run), (unsigned)num_jobs);
+int mfma_decode(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
   if (g.D == 64) {
-    KVMI_MFMA_BITS(launch_dec, 2, g, grid, jobs, err, st)
-  } else {
-    KVMI_MFMA_BITS(launch_dec, 4, g, grid, jobs, err, st)
+    KVMI_MFMA_BITS(launch_dec, 2)
   }
-  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+  KVMI_MFMA_BITS(launch_dec, 4)
 }
 
 }  // namespace kvmi

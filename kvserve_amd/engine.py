@@ -12,6 +12,8 @@ caller asks for the device error word (``check_errors``).
 
 from __future__ import annotations
 
+import dataclasses
+
 import ctypes
 import math
 import os
@@ -147,14 +149,13 @@ class FusedKVCodec:
         g.flags, g.max_groups = self._flags(max_level), groups
         return g
 
-    def _kstats_scratch(self, L: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
-        """uint32 keys [L, 2, H, D] = {0xFFFFFFFF, 0} and counters [L] = 0.  The
-        kernels leave them initialised, so a plan reuses its own set on every run."""
+    def _kstats_scratch(self, L: int, device) -> torch.Tensor:
+        """uint32 keys [L, 2, H, D] = {0xFFFFFFFF, 0}.  The kernels leave them
+        initialised, so a plan reuses its own set on every run."""
         keys = torch.empty((L, 2, self.H, self.D), dtype=torch.int32, device=device)
         keys[:, 0].fill_(-1)
         keys[:, 1].zero_()
-        cnt = torch.zeros(L, dtype=torch.int32, device=device)
-        return keys, cnt
+        return keys
 
     def _check_pools(self, pools: Sequence[torch.Tensor]) -> torch.device:
         if not pools:
@@ -189,7 +190,7 @@ class FusedKVCodec:
             raise IndexError("block id outside the KV cache")
         return torch.tensor(ids_list, dtype=torch.int32, device=device)
 
-    def _jobs(self, pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, cnt, B) -> torch.Tensor:
+    def _jobs(self, pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, B) -> torch.Tensor:
         L = len(pools)
         H, D, S = self.H, self.D, self.S
         per_layer = 2 * H * B * S * D
@@ -207,7 +208,7 @@ class FusedKVCodec:
             rows[l, 5] = _ptr(signs[l]) if signs is not None else 0
             rows[l, 6] = _ptr(prof_dev[l])
             rows[l, 7] = _ptr(keys[l])
-            rows[l, 8] = _ptr(cnt[l:l + 1])
+            rows[l, 8] = 0  # counter: unused
             rows[l, 9] = pools[l].shape[1] * S * H * D
             rows[l, 10] = (l - start) * per_layer
             rows[l, 11] = (stop - start) * per_layer
@@ -280,6 +281,11 @@ class FusedKVCodec:
                 raise ValueError("BitPackCodec payload length does not match shape and bit width")
             if st.device != dev:
                 raise ValueError("BitPackCodec decodes on the payload's CUDA device")
+        # the kernels read streams with 16-byte loads: a view at an unaligned offset is
+        # decoded from an aligned copy
+        if any(st.data_ptr() % 16 for st in packet.streams):
+            packet = dataclasses.replace(
+                packet, streams=[st.clone() if st.data_ptr() % 16 else st for st in packet.streams])
         return Plan(self, "decompress", list(pools), ids, packet)
 
     # ---------------------------------------------------------------- one-shot API
@@ -308,9 +314,9 @@ class Plan:
         if codec.transform:
             self.signs = SIGNS.table(codec.seed, packet.layer_ids, codec.H, codec.D, dev)
         self.prof = torch.from_numpy(np.stack([p.to_array() for p in packet.profiles])).to(dev)
-        self.keys, self.cnt = codec._kstats_scratch(L, dev)
+        self.keys = codec._kstats_scratch(L, dev)
         self.jobs = codec._jobs(pools, ids, packet.streams, packet.chunks, packet.kmeta, packet.vmeta,
-                                self.signs, self.prof, self.keys, self.cnt, B)
+                                self.signs, self.prof, self.keys, B)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
         self.geo = codec._geometry(packet.vmeta.shape[2], max_level)
