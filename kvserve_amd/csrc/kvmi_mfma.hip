@@ -197,6 +197,22 @@ struct LanePack {
       for (int i = 0; i < kBytes / 4; ++i) gst(q + i, w[i]);
     }
   }
+  // Store into LDS (p aligned to the largest of 16, 8, 4 that divides kBytes).
+  __device__ __forceinline__ void store_lds(uint8_t* p) const {
+    if constexpr (kBytes % 16 == 0) {
+      uint4* q = reinterpret_cast<uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 16; ++i) q[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    } else if constexpr (kBytes % 8 == 0) {
+      uint2* q = reinterpret_cast<uint2*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 8; ++i) q[i] = make_uint2(w[2 * i], w[2 * i + 1]);
+    } else {
+      uint32_t* q = reinterpret_cast<uint32_t*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 4; ++i) q[i] = w[i];
+    }
+  }
   __device__ __forceinline__ void load(const uint8_t* p) {
     if constexpr (kBytes % 16 == 0) {
       const uint4* q = reinterpret_cast<const uint4*>(p);
@@ -598,6 +614,13 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
 
   __shared__ Tables T;
+  // Per-wave staging of a section's packed symbols as the byte image of the stream
+  // runs the tile covers: H runs of 32/H tokens (permuted order) or one run of 32
+  // rows (native order).  The runs are then written lane-linear, 16 bytes a lane.
+  constexpr int RB = D * BITS / 8;            // bytes of one packed row
+  constexpr int TQ = kTok * RB / 16;          // uint4 per tile
+  __shared__ uint4 ostage[kWaves * TQ];
+  const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
   stage_profile(T, job.profile, H);
   fill_signs(T, job.signs, H, D);
   if (threadIdx.x == 0 && job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER))
@@ -624,6 +647,25 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const bool rep_lane = hl == 0 && T.gfirst[gv] == hme;  // writes the V metadata of (group, token)
   const float s = g.scale;
 
+  uint8_t* ost = reinterpret_cast<uint8_t*>(ostage + wave * TQ);
+  const int tpt = kTok / H;  // tokens per tile
+  // byte offset of this lane's half-row in the staged image, by output position
+  auto stage_off = [&](int j) { return native ? (r / H) * (H * RB) + j * RB + hl * (RB / 2)
+                                              : j * (tpt * RB) + (r / H) * RB + hl * (RB / 2); };
+  const int offk = stage_off(jk), offv = stage_off(jv);
+  // write the staged image of (part, tile starting at token ta) to the stream
+  auto flush = [&](int part, int ta) {
+    const int rq = native ? TQ : tpt * RB / 16;  // uint4 per run
+#pragma unroll
+    for (int u = 0; u < (TQ + 63) / 64; ++u) {
+      const int q = 64 * u + l;
+      if (TQ % 64 == 0 || q < TQ) {
+        const int run_j = q / rq;
+        uint8_t* dst = seg_addr<BITS>(job, g, part, native ? 0 : run_j, ta, 0) + 16 * (q - run_j * rq);
+        gst(reinterpret_cast<uint4*>(dst), ostage[wave * TQ + q]);
+      }
+    }
+  };
   uint4 xk[2 * NC], xv[2 * NC];
   if (wave < run.tiles) load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, wave)) + r, hl, xk);
   for (int t = wave; t < run.tiles; t += kWaves) {
@@ -645,7 +687,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
         quant_chunk<HALF, BITS, CLAMP, true>(acc, cp, s, kq + 16 * cp, 0.f, 0.f, lvk, pkd, over);
         chunk_fence();
       }
-      pkd.store(seg_addr<BITS>(job, g, 0, jk, tok, HALF * hl));
+      pkd.store_lds(ost + offk);
+      flush(0, ta);
     }
     // next tile's K (unconditional: past the end it re-reads this tile, a cache hit)
     const int tn = min(t + kWaves, run.tiles - 1);
@@ -693,7 +736,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
       quant_chunk<HALF, BITS, CLAMP, false>(acc, cp, s, nullptr, mn, rcp, lvv, pkd, over);
       chunk_fence();
     }
-    pkd.store(seg_addr<BITS>(job, g, 1, jv, tok, HALF * hl));
+    pkd.store_lds(ost + offv);
+    flush(1, ta);
   }
   if (over & overflow_mask<BITS>()) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
 }
@@ -713,6 +757,11 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
 
   __shared__ Tables T;
   __shared__ int ok;
+  // Per-wave staging of an output tile (32 rows, row pitch RP uint4 with one of
+  // padding): rows are written as the MFMA leaves them and stored lane-linear, so
+  // each store instruction writes 1 KB of consecutive bytes of the tile.
+  constexpr int RQ = 4 * NC, RP = RQ + 1;  // uint4 per row, pitch
+  __shared__ uint4 stage[kWaves * kTok * RP];
   if (threadIdx.x == 0) {
     int good = 1;
     if (!(g.flags & KVMI_F_NO_HEADER)) {
@@ -761,7 +810,7 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
     pin(in.mn);
     pin(in.sc);
     const int part = q >= run.tiles, t = q - part * run.tiles;
-    const int64_t row = tile_row0(job, S, H, tile_tok(run.tok0, H, t)) + r;
+    const int64_t row0 = tile_row0(job, S, H, tile_tok(run.tok0, H, t));
     // dequantize into bf16 MFMA operands: x~ = bf16(bf16(q * scale) + min)
     uint4 x[2 * NC];
     if (part)
@@ -769,17 +818,24 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
     else
       dequant_half_row<NC, BITS, true>(in.pk, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), 0.f, 0.f, x);
     chunk_fence();
-    uint16_t* dst = poolK + part * job.pool_part_stride + row * D + HALF * hl;
     const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(hme * (64 + 4) + (HALF / 2) * hl));
+    uint4* stg = stage + wave * (kTok * RP);
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
       const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
       uint32_t w[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) w[i] = pack_bf16x2(acc[2 * i] * s, acc[2 * i + 1] * s);
-      gst(reinterpret_cast<uint4*>(dst) + 2 * cp, xor4(make_uint4(w[0], w[1], w[2], w[3]), sm[2 * cp]));
-      gst(reinterpret_cast<uint4*>(dst) + 2 * cp + 1, xor4(make_uint4(w[4], w[5], w[6], w[7]), sm[2 * cp + 1]));
+      stg[r * RP + 2 * NC * hl + 2 * cp] = xor4(make_uint4(w[0], w[1], w[2], w[3]), sm[2 * cp]);
+      stg[r * RP + 2 * NC * hl + 2 * cp + 1] = xor4(make_uint4(w[4], w[5], w[6], w[7]), sm[2 * cp + 1]);
       chunk_fence();
+    }
+    // the tile's 32 rows are contiguous in the pool
+    uint4* dst = reinterpret_cast<uint4*>(poolK + part * job.pool_part_stride + row0 * D);
+#pragma unroll
+    for (int u = 0; u < RQ * kTok / 64; ++u) {
+      const int qq = 64 * u + l;
+      gst(dst + qq, stg[(qq / RQ) * RP + qq % RQ]);
     }
   };
   // Two input buffers: section q + 4 is loading while section q is computed (past the
