@@ -35,6 +35,33 @@ HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 METRIC = "compress/decompress GB/s of raw bf16 KV on 1 MI355X; % of HBM peak"
 
 
+def hip_kernel_names(codec, S: int, H: int, D: int, bits: int) -> dict:
+    """Name of the HIP kernel each entry point runs for this geometry (MFMA unless the
+    register-FWHT kernels are forced or the geometry is not MFMA-eligible)."""
+    mfma = codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
+    if mfma:
+        return {"kvmi_encode_paged": f"encode_mfma_kernel<{D // 32}, {bits}, false>",
+                "kvmi_decode_paged": f"decode_mfma_kernel<{D // 32}, {bits}>"}
+    return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>"}
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per dispatch of `kernel` on this workload from the committed rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE summaries (copy-calibrated read + write MiB), or None
+    when no summary covers this kernel."""
+    for md in sorted((Path(__file__).resolve().parent / "profiles").glob("*config2*.md")):
+        in_table = False
+        for line in md.read_text().splitlines():
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if not line.startswith("|"):
+                in_table = False
+            elif cells[-2:] == ["scaled read MiB", "scaled write MiB"]:
+                in_table = True
+            elif in_table and cells[0] == kernel:
+                return int(round((float(cells[3]) + float(cells[4])) * 2**20))
+    return None
+
+
 def cpu_model() -> str:
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
@@ -164,7 +191,7 @@ def main() -> int:
     comp_gbps, dec_gbps = R / t_c / 1e6, R / t_d / 1e6
     comp_frac, dec_frac = alg / t_c / 1e6 / HBM_PEAK_GBPS, alg / t_d / 1e6 / HBM_PEAK_GBPS
     dom = "kvmi_encode_paged" if per["kvmi_encode_paged"] >= per["kvmi_decode_paged"] else "kvmi_decode_paged"
-    dom_kernel = {"kvmi_encode_paged": "encode_kernel<128,4>", "kvmi_decode_paged": "decode_kernel<128,4>"}[dom]
+    dom_kernel = hip_kernel_names(codec, S, H, D, bits)[dom]
     achieved = alg / per[dom] / 1e6
     ms_step = wall / args.steps * 1e3
 
@@ -200,7 +227,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(dom_kernel),
             "algorithmic_bytes_per_launch": alg,
         },
         "cpu_baseline": None,
