@@ -217,7 +217,8 @@ class FusedKVCodec:
 
     # ---------------------------------------------------------------- plans
     def plan_compress(self, pools: Sequence[torch.Tensor], block_ids, profiles: Sequence[LayerProfile],
-                      layer_ids: Optional[Sequence[int]] = None, chunk_layers: Optional[int] = None) -> "Plan":
+                      layer_ids: Optional[Sequence[int]] = None, chunk_layers: Optional[int] = None,
+                      groups: Optional[int] = None) -> "Plan":
         """Allocate the outputs and device descriptors for compressing blocks
         `block_ids` of every layer cache in `pools` (one tensor [2, P, S, H, D] per
         layer, vLLM FlashAttention NHD layout).  `run` then enqueues the kernels.
@@ -225,7 +226,9 @@ class FusedKVCodec:
         layer_ids: the reference's layer index of each pool (sign seeds); by default
         0..L-1, the position in the connector's sorted layer list.
         chunk_layers: layers per stream; default = the reference's rule (one stream,
-        or 8-layer chunks above 500 MiB); 0 = one stream."""
+        or 8-layer chunks above 500 MiB); 0 = one stream.
+        groups: V statistic groups the V metadata is laid out for (default: the most any
+        layer of this request uses); plans batched together share one value."""
         dev = self._check_pools(pools)
         L = len(pools)
         if len(profiles) != L:
@@ -244,6 +247,10 @@ class FusedKVCodec:
         else:
             chunks = [(s, min(s + chunk_layers, L)) for s in range(0, L, chunk_layers)]
         G = max(p.num_v_groups() for p in profiles)
+        if groups is not None:
+            if not G <= int(groups) <= H:
+                raise ValueError("groups must cover every layer's V groups and be <= num_heads")
+            G = int(groups)
         hdr = 16 if self.header else 0
         streams = []
         for s, e in chunks:
@@ -298,6 +305,25 @@ class FusedKVCodec:
     def decompress(self, packet: Packet, pools: Sequence[torch.Tensor], block_ids) -> None:
         self.plan_decompress(packet, pools, block_ids).run()
 
+    # ---------------------------------------------------------------- batches
+    def plan_compress_batch(self, requests: Sequence[tuple], chunk_layers: Optional[int] = None) -> "BatchPlan":
+        """One plan for several requests: `requests` holds (pools, block_ids, profiles)
+        or (pools, block_ids, profiles, layer_ids) tuples, each compressed into its own
+        packet exactly as plan_compress would, with one launch per kernel for all of
+        them (requests may differ in length and profile)."""
+        reqs = [tuple(r) + (None,) * (4 - len(r)) for r in requests]
+        if not reqs:
+            raise ValueError("a batch needs at least one request")
+        G = max(p.num_v_groups() for r in reqs for p in r[2])
+        return BatchPlan([self.plan_compress(pools, ids, prof, lids, chunk_layers, groups=G)
+                          for pools, ids, prof, lids in reqs])
+
+    def plan_decompress_batch(self, items: Sequence[tuple]) -> "BatchPlan":
+        """One plan writing several packets back: `items` holds (packet, pools,
+        block_ids) tuples.  The packets must share their V metadata layout (as the
+        packets of one plan_compress_batch do)."""
+        return BatchPlan([self.plan_decompress(pk, pools, ids) for pk, pools, ids in items])
+
 
 class Plan:
     """Device descriptors of one compress or decompress of one request.  `run()`
@@ -345,6 +371,40 @@ class Plan:
 
     def check_errors(self) -> None:
         raise_device_error(self.error_code())
+
+
+class BatchPlan:
+    """Plans of one codec and direction enqueued together: their job tables are
+    concatenated, so each C entry point is launched once for every layer of every
+    request (each job keeps its own pools, block table, stream, metadata and scratch).
+    All packets of the batch report device errors through one shared error word."""
+
+    def __init__(self, plans: Sequence[Plan]):
+        plans = list(plans)
+        if not plans:
+            raise ValueError("a batch needs at least one plan")
+        p0 = plans[0]
+        for p in plans[1:]:
+            if p.codec is not p0.codec or p.kind != p0.kind or p.device != p0.device:
+                raise ValueError("batched plans must share codec, direction and device")
+            if p.geo.max_groups != p0.geo.max_groups:
+                raise ValueError("batched packets must share their V metadata layout (groups)")
+        self.plans, self.codec, self.kind, self.device = plans, p0.codec, p0.kind, p0.device
+        self.packets = [p.packet for p in plans]
+        self.num_jobs = sum(p.num_jobs for p in plans)
+        self.max_blocks = max(p.max_blocks for p in plans)
+        self.jobs = torch.cat([p.jobs for p in plans])
+        max_level = max(max(max(pr.k_levels), max(pr.v_levels)) for p in plans for pr in p.packet.profiles)
+        self.geo = p0.codec._geometry(p0.geo.max_groups, max_level)
+        self.err = torch.zeros(1, dtype=torch.int32, device=self.device)
+        for pk in self.packets:
+            pk.__dict__["_err"] = self.err
+
+    launches = Plan.launches
+    launch = Plan.launch
+    run = Plan.run
+    error_code = Plan.error_code
+    check_errors = Plan.check_errors
 
 
 def raise_device_error(code: int) -> None:
