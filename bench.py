@@ -14,7 +14,11 @@ Inputs are resident in HBM before the timed region; plans (device descriptors) a
 built before it too.  Per-direction throughput and the fraction of HBM peak are
 printed alongside.  Prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config3|config4|config5]
+
+The other BASELINE configurations can be timed with --workload (the metric is quoted
+on config2, the default; multi-request workloads run as one batched plan per
+direction, and the CPU baseline is measured for config2 only).
 """
 
 from __future__ import annotations
@@ -35,6 +39,23 @@ HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
 METRIC = "compress/decompress GB/s of raw bf16 KV on 1 MI355X; % of HBM peak"
 
 
+WORKLOADS = {
+    "config2": "config2: Llama-3-8B-shaped request, 32 layers x 8 KV heads x D=128 x 8192 tokens, "
+               "16-token blocks at seeded random ids of a 65536-block pool per layer, "
+               "Hadamard seed 0xC0FEBABE, head split (Llama-3.1-8B mask, hybrid 0.3), "
+               "16/16 levels, bitpack 4 bits, 4 streams of 8 layers; step = compress + decompress",
+    "config3": "config3: 16 requests of U[1024,16384] tokens, 32 layers x 8 heads x D=128, per-(layer, head) "
+               "levels in {6,12} for K and V, bitpack 4, seeded random blocks of a 262144-block pool (32 "
+               "logical layer pools alias 2 physical pools), one batched plan per direction; "
+               "step = compress + decompress",
+    "config4": "config4: Qwen2.5-72B-shaped request, 80 layers x 8 heads x D=128 x 32768 tokens, 2% "
+               "Student-t(3) outliers, layer split levels 12/6 alternating, bitpack 4, contiguous caches, "
+               "10 streams of 8 layers; step = compress + decompress",
+    "config5": "config5: 256 requests x 256 tokens, 16 layers x 8 heads x D=64, 6/6 levels, bitpack 3, seeded "
+               "random blocks, one batched plan per direction; step = compress + decompress",
+}
+
+
 def hip_kernel_names(codec, S: int, H: int, D: int, bits: int) -> dict:
     """Name of the HIP kernel each entry point runs for this geometry (MFMA unless the
     register-FWHT kernels are forced or the geometry is not MFMA-eligible)."""
@@ -45,11 +66,11 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int) -> dict:
     return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>"}
 
 
-def profiled_traffic(kernel: str):
+def profiled_traffic(kernel: str, workload: str = "config2"):
     """HBM bytes per dispatch of `kernel` on this workload from the committed rocprofv3
     --pmc FETCH_SIZE / WRITE_SIZE summaries (copy-calibrated read + write MiB), or None
     when no summary covers this kernel."""
-    for md in sorted((Path(__file__).resolve().parent / "profiles").glob("*config2*.md")):
+    for md in sorted((Path(__file__).resolve().parent / "profiles").glob(f"*{workload}*.md")):
         in_table = False
         for line in md.read_text().splitlines():
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
@@ -119,6 +140,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=32, help="(debug) layers of the config-2 request")
+    ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS),
+                    help="BASELINE.json configuration to time (the metric is quoted on config2)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy --steps times (scales rocprof byte counters)")
     args = ap.parse_args()
@@ -138,20 +161,29 @@ def main() -> int:
         print(json.dumps({"copy_bytes": src.numel(), "steps": args.steps}))
         return 0
 
+    from kvserve_amd import workloads
     from kvserve_amd.engine import FusedKVCodec
-    from kvserve_amd.workloads import make_config2
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    print("bench: building config-2 workload", file=sys.stderr, flush=True)
-    wl = make_config2(device=dev, num_layers=args.layers)
-    req = wl.requests[0]
-    L, B = len(req.pools), req.block_ids.numel()
+    print(f"bench: building {args.workload} workload", file=sys.stderr, flush=True)
+    if args.workload == "config2":
+        wl = workloads.make_config2(device=dev, num_layers=args.layers)
+    else:
+        wl = getattr(workloads, "make_" + args.workload)(device=dev)
+    reqs = wl.requests
     S, H, D, bits = wl.block_size, wl.num_heads, wl.head_dim, wl.bits
     codec = FusedKVCodec(H, D, S, bits, wl.seed)
-    cplan = codec.plan_compress(req.pools, req.block_ids, req.profiles, req.layer_ids)
-    packet = cplan.packet
-    dplan = codec.plan_decompress(packet, req.pools, req.block_ids)
+    if len(reqs) == 1:
+        req = reqs[0]
+        cplan = codec.plan_compress(req.pools, req.block_ids, req.profiles, req.layer_ids)
+        packets = [cplan.packet]
+        dplan = codec.plan_decompress(cplan.packet, req.pools, req.block_ids)
+    else:
+        # one launch per kernel for all requests; decompress writes back in place
+        cplan = codec.plan_compress_batch([(r.pools, r.block_ids, r.profiles, r.layer_ids) for r in reqs])
+        packets = cplan.packets
+        dplan = codec.plan_decompress_batch([(pk, r.pools, r.block_ids) for pk, r in zip(packets, reqs)])
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
@@ -183,10 +215,10 @@ def main() -> int:
     t_c = per["kvmi_kstats_paged"] + per["kvmi_encode_paged"]
     t_d = per["kvmi_decode_paged"]
 
-    R = L * 2 * B * S * H * D * 2
-    P = packet.compressed_bytes()
-    M = (packet.kmeta.numel() + packet.vmeta.numel()) * 2
-    idx = L * B * 4
+    R = sum(len(r.pools) * 2 * r.block_ids.numel() * S * H * D * 2 for r in reqs)
+    P = sum(pk.compressed_bytes() for pk in packets)
+    M = sum((pk.kmeta.numel() + pk.vmeta.numel()) * 2 for pk in packets)
+    idx = sum(len(r.pools) * r.block_ids.numel() * 4 for r in reqs)
     alg = R + P + M + idx  # one direction: read KV + write stream/meta (or the reverse)
     comp_gbps, dec_gbps = R / t_c / 1e6, R / t_d / 1e6
     comp_frac, dec_frac = alg / t_c / 1e6 / HBM_PEAK_GBPS, alg / t_d / 1e6 / HBM_PEAK_GBPS
@@ -209,11 +241,10 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
         "config": {
-            "workload": "config2: Llama-3-8B-shaped request, 32 layers x 8 KV heads x D=128 x 8192 tokens, "
-                        "16-token blocks at seeded random ids of a 65536-block pool per layer, "
-                        "Hadamard seed 0xC0FEBABE, head split (Llama-3.1-8B mask, hybrid 0.3), "
-                        "16/16 levels, bitpack 4 bits, 4 streams of 8 layers; step = compress + decompress",
-            "layers": L, "tokens": B * S, "raw_bytes": R, "packed_bytes": P, "meta_bytes": M,
+            "workload": WORKLOADS[args.workload],
+            "requests": len(reqs), "layers": len(reqs[0].pools),
+            "tokens": sum(r.block_ids.numel() for r in reqs) * S, "raw_bytes": R, "packed_bytes": P,
+            "meta_bytes": M,
         },
         "compress_gbps": round(comp_gbps, 2),
         "decompress_gbps": round(dec_gbps, 2),
@@ -227,12 +258,12 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": profiled_traffic(dom_kernel),
+            "traffic": profiled_traffic(dom_kernel, args.workload),
             "algorithmic_bytes_per_launch": alg,
         },
         "cpu_baseline": None,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload == "config2":
         print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(wl, args.cpu_budget)
     print(json.dumps(out), flush=True)
