@@ -4,6 +4,7 @@
   CompressionManager              operator-by-operator pipeline
   FusedCompressionManager         the fused gfx950 pipeline (default when a quantizer runs)
   KVServeTransformer / KVServeQuantizer / KVServeCodec / BitPackCodec   operators
+  CompressedWire, build_wire, restore_from_wire                         transport bundle
 """
 
 from .codec import BitPackCodec, KVServeCodec
@@ -13,10 +14,11 @@ from .compression_manager import (DEFAULT_COMPRESSION_CONFIG, CompressedKVData, 
 from .manager import KVCompressionAdapter
 from .quantizer import KVServeQuantizer
 from .transformer import HadamardTransform, KVServeTransformer
+from .wire import CompressedWire, build_wire, restore_from_wire
 
 __all__ = [
     "BitPackCodec", "KVServeCodec", "Codec", "Quantizer", "Transformer", "DEFAULT_COMPRESSION_CONFIG",
     "CompressedKVData", "CompressionConfig", "CompressionManager", "FusedCompressionManager",
     "get_default_compression_config", "KVCompressionAdapter", "KVServeQuantizer", "HadamardTransform",
-    "KVServeTransformer",
+    "KVServeTransformer", "CompressedWire", "build_wire", "restore_from_wire",
 ]

@@ -1,0 +1,229 @@
+"""Wire bundle of a compressed KV payload (kvserve_v1/compression/wire.py:19-289).
+
+A `CompressedKVData` is split into
+  meta         msgpack-safe dict (no tensors): sizes, ids, body layout, and the
+               metadata dicts with every tensor replaced by a placeholder
+               ``["__kvserve_aux_tensor__", index]`` (wire.py:16, :176-202);
+  body_chunks  the packed stream(s): the manager's layer chunks as they are
+               ("manager_chunks"), one stream ("single"), or one stream cut into
+               pieces of at most `max_chunk_bytes` ("byte_chunks") (wire.py:35-90);
+  aux_tensors  the metadata tensors; more than one are carried as a single byte
+               tensor plus ``meta["aux_layout"] = {"mode": "coalesced_bytes",
+               "tensors": [{storage, offset, nbytes, shape, dtype}, ...]}``
+               (wire.py:205-254).
+
+The meta layout, the placeholder and the layout table are the reference's wire
+format, so a bundle built here is read by the reference's `restore_from_wire` and
+the other way round.  Where every metadata tensor is a contiguous slice of one
+allocation -- the fused engine keeps K and V metadata in one buffer -- the aux
+tensor is a view of that allocation and nothing is copied; otherwise the tensors
+are copied into one byte tensor, each at an offset aligned to its element size.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional
+
+import torch
+
+from .compression_manager import CompressedKVData
+
+AUX_PLACEHOLDER = "__kvserve_aux_tensor__"
+
+
+@dataclass
+class CompressedWire:
+    """A compressed payload as msgpack metadata plus device tensors (wire.py:19-30)."""
+
+    meta: Dict[str, Any]
+    body_chunks: List[torch.Tensor]
+    aux_tensors: List[torch.Tensor]
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self.body_chunks + self.aux_tensors)
+
+
+# ---------------------------------------------------------------------- build
+def build_wire(compressed: CompressedKVData, max_chunk_bytes: int) -> CompressedWire:
+    """Bundle `compressed` for transport (wire.py:33-90)."""
+    aux: List[torch.Tensor] = []
+    meta: Dict[str, Any] = {
+        "is_chunked": bool(compressed.is_chunked),
+        "layer_id": compressed.layer_id,
+        "original_size": compressed.original_size,
+        "compressed_size": compressed.compressed_size,
+        "metadata": _pack_meta(compressed.metadata, aux),
+    }
+    if compressed.is_chunked:
+        if not compressed.chunks or not compressed.chunk_metadata:
+            raise ValueError("Chunked CompressedKVData is missing chunks or metadata")
+        meta["chunk_metadata"] = [_pack_meta(m, aux) for m in compressed.chunk_metadata]
+        meta["body_mode"] = "manager_chunks"
+        body = [c.contiguous() for c in compressed.chunks]
+    else:
+        if compressed.compressed_tensor is None:
+            raise ValueError("Non-chunked CompressedKVData is missing compressed_tensor")
+        t = compressed.compressed_tensor.contiguous()
+        nbytes = t.numel() * t.element_size()
+        if nbytes > max_chunk_bytes:
+            body = _byte_pieces(t, max_chunk_bytes)
+            meta["body_mode"] = "byte_chunks"
+        else:
+            body = [t]
+            meta["body_mode"] = "single"
+        meta["body_spec"] = _spec(t)
+    aux_out = _coalesce(meta, aux)
+    _no_tensors(meta)
+    return CompressedWire(meta=meta, body_chunks=body, aux_tensors=aux_out)
+
+
+def _pack_meta(obj: Any, aux: List[torch.Tensor]) -> Any:
+    # only "quantization_params" carries tensors (wire.py:140-147)
+    if not isinstance(obj, dict):
+        return obj
+    out = dict(obj)
+    if "quantization_params" in out:
+        out["quantization_params"] = _pack_tree(out["quantization_params"], aux)
+    return out
+
+
+def _pack_tree(obj: Any, aux: List[torch.Tensor]) -> Any:
+    if isinstance(obj, torch.Tensor):
+        aux.append(obj.contiguous())
+        return [AUX_PLACEHOLDER, len(aux) - 1]
+    if isinstance(obj, dict):
+        return {k: _pack_tree(v, aux) for k, v in obj.items()}
+    if isinstance(obj, (list, tuple)):
+        return [_pack_tree(v, aux) for v in obj]
+    return obj
+
+
+def _spec(t: torch.Tensor) -> Dict[str, Any]:
+    return {"shape": list(t.shape), "dtype": str(t.dtype).replace("torch.", "")}
+
+
+def _byte_pieces(t: torch.Tensor, max_chunk_bytes: int) -> List[torch.Tensor]:
+    """Consecutive pieces of at most max_chunk_bytes of t's bytes (views, wire.py:257-264)."""
+    if max_chunk_bytes <= 0:
+        raise ValueError("max_chunk_bytes must be positive")
+    b = t.reshape(-1).view(torch.uint8)
+    return [b[i:i + max_chunk_bytes] for i in range(0, b.numel(), max_chunk_bytes)]
+
+
+def _coalesce(meta: Dict[str, Any], aux: List[torch.Tensor]) -> List[torch.Tensor]:
+    """One byte tensor plus a layout table for more than one aux tensor (wire.py:205-237)."""
+    if len(aux) <= 1:
+        return aux
+    dev = aux[0].device
+    shared = _shared_storage_range(aux)
+    if shared is not None:
+        storage, lo, hi = shared
+        blob = torch.empty(0, dtype=torch.uint8, device=dev).set_(storage, lo, (hi - lo,))
+        offsets = [t.data_ptr() - storage.data_ptr() - lo for t in aux]
+    else:
+        offsets, pos = [], 0
+        for t in aux:
+            pos += (-pos) % t.element_size()
+            offsets.append(pos)
+            pos += t.numel() * t.element_size()
+        blob = torch.zeros(pos, dtype=torch.uint8, device=dev)
+        for t, off in zip(aux, offsets):
+            n = t.numel() * t.element_size()
+            if n:
+                blob[off:off + n].copy_(t.reshape(-1).view(torch.uint8))
+    meta["aux_layout"] = {
+        "mode": "coalesced_bytes",
+        "tensors": [{"storage": 0, "offset": int(off), "nbytes": t.numel() * t.element_size(),
+                     "shape": list(t.shape), "dtype": str(t.dtype).replace("torch.", "")}
+                    for t, off in zip(aux, offsets)],
+    }
+    return [blob]
+
+
+def _shared_storage_range(aux: List[torch.Tensor]):
+    """(storage, lo, hi) when every tensor is a contiguous slice of one storage at an
+    offset that is a multiple of its element size relative to lo; else None."""
+    st = aux[0].untyped_storage()
+    base = st.data_ptr()
+    spans = []
+    for t in aux:
+        if t.device != aux[0].device or not t.is_contiguous() or t.untyped_storage().data_ptr() != base:
+            return None
+        off = t.data_ptr() - base
+        spans.append((off, off + t.numel() * t.element_size(), t.element_size()))
+    lo = min(s[0] for s in spans)
+    hi = max(s[1] for s in spans)
+    if any((s[0] - lo) % s[2] for s in spans):
+        return None
+    return st, lo, hi
+
+
+def _no_tensors(obj: Any) -> None:
+    if isinstance(obj, torch.Tensor):
+        raise TypeError("CompressedWire metadata still contains a tensor; extend wire packing for this metadata field.")
+    if isinstance(obj, dict):
+        for v in obj.values():
+            _no_tensors(v)
+    elif isinstance(obj, (list, tuple)):
+        for v in obj:
+            _no_tensors(v)
+
+
+# ---------------------------------------------------------------------- restore
+def restore_from_wire(wire: CompressedWire) -> CompressedKVData:
+    """Rebuild the payload from a received bundle (wire.py:93-136).  The request id
+    comes from the inner metadata."""
+    meta = wire.meta
+    aux = _expand(wire.aux_tensors, meta.get("aux_layout"))
+    inner = _unpack_meta(meta.get("metadata"), aux)
+    rid = str(inner.get("request_id", "unknown")) if isinstance(inner, dict) else "unknown"
+    common = dict(request_id=rid, layer_id=int(meta.get("layer_id", -1)), metadata=inner,
+                  original_size=int(meta.get("original_size", 0)),
+                  compressed_size=int(meta.get("compressed_size", 0)))
+    if bool(meta["is_chunked"]):
+        return CompressedKVData(compressed_tensor=None, is_chunked=True, chunks=wire.body_chunks,
+                                chunk_metadata=[_unpack_meta(m, aux) for m in meta.get("chunk_metadata", [])],
+                                **common)
+    if meta.get("body_mode") == "byte_chunks":
+        spec = meta["body_spec"]
+        b = torch.cat([c.contiguous().view(torch.uint8).reshape(-1) for c in wire.body_chunks])
+        tensor = b.view(getattr(torch, spec["dtype"])).reshape(spec["shape"])
+    else:
+        tensor = wire.body_chunks[0]
+    return CompressedKVData(compressed_tensor=tensor, is_chunked=False, **common)
+
+
+def _expand(aux: List[torch.Tensor], layout: Optional[Dict[str, Any]]) -> List[torch.Tensor]:
+    if not layout:
+        return aux
+    if layout.get("mode") != "coalesced_bytes":
+        raise ValueError(f"Unknown aux_layout mode: {layout.get('mode')}")
+    if not aux:
+        return []
+    blob = aux[0].contiguous().view(torch.uint8).reshape(-1)
+    out = []
+    for e in layout.get("tensors", []):
+        if int(e.get("storage", 0)) != 0:
+            raise ValueError("Only single-storage aux_layout is supported")
+        a, n = int(e["offset"]), int(e["nbytes"])
+        out.append(blob[a:a + n].view(getattr(torch, e["dtype"])).reshape(e["shape"]))
+    return out
+
+
+def _unpack_meta(obj: Any, aux: List[torch.Tensor]) -> Any:
+    if isinstance(obj, dict) and "quantization_params" in obj:
+        obj = dict(obj)
+        obj["quantization_params"] = _unpack_tree(obj["quantization_params"], aux)
+    return obj
+
+
+def _unpack_tree(obj: Any, aux: List[torch.Tensor]) -> Any:
+    if isinstance(obj, list) and len(obj) == 2 and isinstance(obj[0], str) and obj[0] == AUX_PLACEHOLDER:
+        return aux[int(obj[1])]
+    if isinstance(obj, dict):
+        return {k: _unpack_tree(v, aux) for k, v in obj.items()}
+    if isinstance(obj, list):
+        return [_unpack_tree(v, aux) for v in obj]
+    return obj

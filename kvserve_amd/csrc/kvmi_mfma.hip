@@ -359,32 +359,12 @@ __device__ __forceinline__ f32x16 transform_T(const uint4 (&x)[2 * NC], const ui
   return acc;
 }
 
-// Quantize output chunk cp (16 values of the lane's half-row) into the lane's
-// packer.  KQ: per-element (min, 1/scale) pairs from the LDS table at kq; otherwise
-// one (mn, rcp) for the row.  Widths 2, 4, 8 pack byte lanes: dword d_m holds the
-// symbols i with i % P == m (P = 8/BITS symbols per byte), and the chunk's words are
-// OR_m d_m << (m*BITS).
-template <int HALF, int BITS, bool CLAMP, bool KQ>
-__device__ __forceinline__ void quant_chunk(const f32x16& acc, int cp, float s, const float2* kq, float mn, float rcp,
-                                            float lv, LanePack<HALF, BITS>& pk, uint32_t& over) {
-  float q[16];
-#pragma unroll
-  for (int i = 0; i < 16; i += 2) {
-    float m0 = mn, m1 = mn, r0 = rcp, r1 = rcp;
-    if constexpr (KQ) {
-      const float4 c = *reinterpret_cast<const float4*>(kq + i);
-      m0 = c.x;
-      r0 = c.y;
-      m1 = c.z;
-      r1 = c.w;
-    }
-    q[i] = quant_q(acc[i], s, m0, r0);
-    q[i + 1] = quant_q(acc[i + 1], s, m1, r1);
-    if constexpr (CLAMP) {
-      q[i] = fminf(q[i], lv);
-      q[i + 1] = fminf(q[i + 1], lv);
-    }
-  }
+// Pack the 16 quantized values q of output chunk cp into the lane's packer (rint,
+// saturate, and OR the bytes into `over` for the width check).  Widths 2, 4, 8 pack
+// byte lanes: dword d_m holds the symbols i with i % P == m (P = 8/BITS symbols per
+// byte), and the chunk's words are OR_m d_m << (m*BITS).
+template <int HALF, int BITS>
+__device__ __forceinline__ void pack_chunk(const float (&q)[16], int cp, LanePack<HALF, BITS>& pk, uint32_t& over) {
   if constexpr (BITS == 2 || BITS == 4 || BITS == 8) {
     constexpr int P = 8 / BITS, W = BITS / 2;
 #pragma unroll
@@ -409,6 +389,44 @@ __device__ __forceinline__ void quant_chunk(const f32x16& acc, int cp, float s, 
       pk.put(16 * cp + i, sym);
     }
   }
+}
+
+// Quantize output chunk cp (16 accumulators of the lane's half-row) with per-element
+// (min, 1/scale) pairs from the LDS table at kq (K: per-channel statistics).
+template <int HALF, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_chunk_k(const f32x16& acc, int cp, float s, const float2* kq, float lv,
+                                              LanePack<HALF, BITS>& pk, uint32_t& over) {
+  float q[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const float4 c = *reinterpret_cast<const float4*>(kq + i);
+    q[i] = quant_q(acc[i], s, c.x, c.y);
+    q[i + 1] = quant_q(acc[i + 1], s, c.z, c.w);
+    if constexpr (CLAMP) {
+      q[i] = fminf(q[i], lv);
+      q[i + 1] = fminf(q[i + 1], lv);
+    }
+  }
+  pack_chunk<HALF, BITS>(q, cp, pk, over);
+}
+
+// Quantize output chunk cp from its 16 transformed values y, kept as 8 bf16 pairs,
+// with the row's (mn, 1/scale) (V: per-token statistics).
+template <int HALF, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_chunk_v(const uint32_t* ypk, int cp, float mn, float rcp, float lv,
+                                              LanePack<HALF, BITS>& pk, uint32_t& over) {
+  float q[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const uint32_t y2 = ypk[i / 2];
+    q[i] = rbf(rbf(bf_lo(y2) - mn) * rcp);
+    q[i + 1] = rbf(rbf(bf_hi(y2) - mn) * rcp);
+    if constexpr (CLAMP) {
+      q[i] = fminf(q[i], lv);
+      q[i + 1] = fminf(q[i + 1], lv);
+    }
+  }
+  pack_chunk<HALF, BITS>(q, cp, pk, over);
 }
 
 // The 8 symbols of operand u (elements 8u .. 8u+7 of the half-row) as floats.
@@ -684,7 +702,7 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
 #pragma unroll
       for (int cp = 0; cp < NC; ++cp) {
         const f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
-        quant_chunk<HALF, BITS, CLAMP, true>(acc, cp, s, kq + 16 * cp, 0.f, 0.f, lvk, pkd, over);
+        quant_chunk_k<HALF, BITS, CLAMP>(acc, cp, s, kq + 16 * cp, lvk, pkd, over);
         chunk_fence();
       }
       pkd.store_lds(ost + offk);
@@ -695,6 +713,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
     load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)) + r, hl, xk);
     // ---------------- V: per-token statistics over the heads of a group
     sign_half_row<NC>(T, hme, hl, xv);
+    // one transform: y = bf16(acc * s) kept as bf16 pairs for the quantization below
+    uint32_t ypk[HALF / 2];
     float amn = __builtin_inff(), amx = -__builtin_inff();
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
@@ -704,6 +724,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
         amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
         amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
       }
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) ypk[8 * cp + i / 2] = pack_bf16x2(acc[i] * s, acc[i + 1] * s);
       chunk_fence();
     }
     // y = bf16(fl(acc * s)) is monotone in acc (s > 0): the row's min / max of y
@@ -732,8 +754,7 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
     pkd.clear();
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
-      const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
-      quant_chunk<HALF, BITS, CLAMP, false>(acc, cp, s, nullptr, mn, rcp, lvv, pkd, over);
+      quant_chunk_v<HALF, BITS, CLAMP>(ypk + 8 * cp, cp, mn, rcp, lvv, pkd, over);
       chunk_fence();
     }
     pkd.store_lds(ost + offv);

@@ -256,8 +256,12 @@ class FusedKVCodec:
         for s, e in chunks:
             n = (e - s) * 2 * H * B * S * D
             streams.append(torch.empty(hdr + (n * self.bits + 7) // 8, dtype=torch.uint8, device=dev))
-        kmeta = torch.empty((L, 2, H, D), dtype=torch.bfloat16, device=dev)
-        vmeta = torch.empty((L, 2, G, B * S), dtype=torch.bfloat16, device=dev)
+        # both metadata tables live in one allocation: the reference's per-section
+        # dicts are views of it, and the wire bundle ships it without a copy
+        kn, vn = L * 2 * H * D, L * 2 * G * B * S
+        meta_buf = torch.empty(kn + vn, dtype=torch.bfloat16, device=dev)
+        kmeta = meta_buf[:kn].view(L, 2, H, D)
+        vmeta = meta_buf[kn:].view(L, 2, G, B * S)
         packet = Packet(streams, chunks, kmeta, vmeta, list(profiles), B, S, H, D, self.bits, self.seed,
                         self.transform, self.layout, layer_ids)
         if B == 0 and self.header:

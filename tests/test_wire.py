@@ -1,0 +1,146 @@
+"""Wire bundle (kvserve_amd.compression.wire) against the reference's format rules
+(kvserve_v1/compression/wire.py:16-289): known answers derived by hand from those rules,
+round trips, msgpack-safety and the error contracts.  CPU tensors; the GPU case goes
+through the adapter in test_gpu_api-style at the end (marked gpu)."""
+
+import msgpack
+import pytest
+import torch
+
+from kvserve_amd.compression.compression_manager import CompressedKVData
+from kvserve_amd.compression.wire import AUX_PLACEHOLDER, CompressedWire, build_wire, restore_from_wire
+
+
+def _payload(qparams, tensor=None, **kw):
+    meta = {"request_id": "req-7", "codec_applied": True, "quantization_params": qparams}
+    return CompressedKVData("req-7", 3, tensor if tensor is not None else torch.arange(10, dtype=torch.uint8),
+                            meta, 1000, 10, **kw)
+
+
+def test_known_answer_copy_path_aligns_each_tensor():
+    a = torch.tensor([1, 2, 3], dtype=torch.uint8)                # 3 bytes at 0
+    b = torch.tensor([[1.0, -2.0]], dtype=torch.bfloat16)        # 4 bytes at 4 (pad 1)
+    c = torch.tensor(5, dtype=torch.int64)                       # 8 bytes at 8
+    qp = [{"high_key_meta": {"min_val": a, "quant_scale": b, "max_value": 16}, "original_dtype": "bfloat16"},
+          {"low_value_meta": {"min_val": c, "quant_scale": None, "max_value": 4}}]
+    w = build_wire(_payload(qp), max_chunk_bytes=1 << 20)
+    assert w.meta == {
+        "is_chunked": False, "layer_id": 3, "original_size": 1000, "compressed_size": 10,
+        "metadata": {"request_id": "req-7", "codec_applied": True, "quantization_params": [
+            {"high_key_meta": {"min_val": [AUX_PLACEHOLDER, 0], "quant_scale": [AUX_PLACEHOLDER, 1],
+                               "max_value": 16}, "original_dtype": "bfloat16"},
+            {"low_value_meta": {"min_val": [AUX_PLACEHOLDER, 2], "quant_scale": None, "max_value": 4}}]},
+        "body_mode": "single", "body_spec": {"shape": [10], "dtype": "uint8"},
+        "aux_layout": {"mode": "coalesced_bytes", "tensors": [
+            {"storage": 0, "offset": 0, "nbytes": 3, "shape": [3], "dtype": "uint8"},
+            {"storage": 0, "offset": 4, "nbytes": 4, "shape": [1, 2], "dtype": "bfloat16"},
+            {"storage": 0, "offset": 8, "nbytes": 8, "shape": [], "dtype": "int64"}]},
+    }
+    assert AUX_PLACEHOLDER == "__kvserve_aux_tensor__"
+    assert len(w.aux_tensors) == 1 and w.aux_tensors[0].dtype == torch.uint8 and w.aux_tensors[0].numel() == 16
+    blob = w.aux_tensors[0]
+    assert blob[:3].tolist() == [1, 2, 3] and blob[3].item() == 0
+    assert torch.equal(blob[4:8].view(torch.bfloat16), b.reshape(-1))
+    assert blob[8:16].view(torch.int64).item() == 5
+    assert w.nbytes == 10 + 16
+    r = restore_from_wire(w)
+    q = r.metadata["quantization_params"]
+    assert torch.equal(q[0]["high_key_meta"]["min_val"], a) and torch.equal(q[0]["high_key_meta"]["quant_scale"], b)
+    assert torch.equal(q[1]["low_value_meta"]["min_val"], c) and q[1]["low_value_meta"]["quant_scale"] is None
+    assert r.request_id == "req-7" and r.layer_id == 3 and torch.equal(r.compressed_tensor, torch.arange(10, dtype=torch.uint8))
+
+
+def test_single_aux_tensor_has_no_layout():
+    t = torch.tensor([1.5])
+    w = build_wire(_payload({"k": t}), 1 << 20)
+    assert "aux_layout" not in w.meta and w.aux_tensors[0] is t
+    assert torch.equal(restore_from_wire(w).metadata["quantization_params"]["k"], t)
+
+
+def test_scalar_and_int_metadata_roundtrip():
+    # the reference's test_wire_scalar_metadata case
+    vals = {"a": torch.tensor(1.5), "b": torch.tensor([1, 2], dtype=torch.int64)}
+    r = restore_from_wire(build_wire(_payload(vals), 1 << 20))
+    assert all(torch.equal(vals[k], r.metadata["quantization_params"][k]) for k in vals)
+
+
+def test_slices_of_one_allocation_ship_without_copy():
+    buf = torch.arange(64, dtype=torch.bfloat16)
+    qp = [{"min_val": buf[8:16].view(1, 1, 2, 4), "quant_scale": buf[16:24].view(1, 1, 2, 4)},
+          {"min_val": buf[40:48].view(8, 1, 1, 1)}]
+    w = build_wire(_payload(qp), 1 << 20)
+    blob = w.aux_tensors[0]
+    assert blob.untyped_storage().data_ptr() == buf.untyped_storage().data_ptr()
+    assert blob.numel() == (48 - 8) * 2  # from the first to the end of the last slice
+    offs = [e["offset"] for e in w.meta["aux_layout"]["tensors"]]
+    assert offs == [0, 16, 64]
+    buf[9] = 99  # a view: later writes are visible (nothing was copied)
+    r = restore_from_wire(w).metadata["quantization_params"]
+    assert r[0]["min_val"].reshape(-1)[1].item() == 99
+    assert torch.equal(r[0]["quant_scale"], qp[0]["quant_scale"]) and torch.equal(r[1]["min_val"], qp[1]["min_val"])
+
+
+def test_byte_chunks_are_views_and_restore():
+    body = torch.arange(1000, dtype=torch.int16).reshape(10, 100)
+    w = build_wire(_payload({}, tensor=body), max_chunk_bytes=300)
+    assert w.meta["body_mode"] == "byte_chunks" and w.meta["body_spec"] == {"shape": [10, 100], "dtype": "int16"}
+    assert [c.numel() for c in w.body_chunks] == [300] * 6 + [200]
+    assert all(c.untyped_storage().data_ptr() == body.untyped_storage().data_ptr() for c in w.body_chunks)
+    assert torch.equal(restore_from_wire(w).compressed_tensor, body)
+    with pytest.raises(ValueError, match="max_chunk_bytes"):
+        build_wire(_payload({}, tensor=body), max_chunk_bytes=0)
+
+
+def test_manager_chunks_and_msgpack_roundtrip():
+    chunks = [torch.arange(5, dtype=torch.uint8), torch.arange(7, dtype=torch.uint8)]
+    cm = [{"request_id": "r", "num_layers": 8, "start_layer_id": 0, "quantization_params": [{"m": torch.ones(2)}]},
+          {"request_id": "r", "num_layers": 1, "start_layer_id": 8, "quantization_params": [{"m": torch.zeros(3)}]}]
+    p = CompressedKVData("r", 8, None, {"request_id": "r", "chunked": True}, 123, 12, True, chunks, cm)
+    w = build_wire(p, max_chunk_bytes=1)
+    assert w.meta["body_mode"] == "manager_chunks" and w.body_chunks[0] is chunks[0]
+    w = CompressedWire(msgpack.unpackb(msgpack.packb(w.meta), raw=False), w.body_chunks, w.aux_tensors)
+    r = restore_from_wire(w)
+    assert r.is_chunked and r.compressed_tensor is None and r.request_id == "r"
+    assert [c.tolist() for c in r.chunks] == [c.tolist() for c in chunks]
+    assert torch.equal(r.chunk_metadata[1]["quantization_params"][0]["m"], torch.zeros(3))
+    assert r.chunk_metadata[1]["start_layer_id"] == 8
+
+
+def test_contract_errors():
+    with pytest.raises(ValueError, match="missing chunks"):
+        build_wire(CompressedKVData("r", 0, None, {}, 0, 0, True, None, None), 10)
+    with pytest.raises(ValueError, match="missing compressed_tensor"):
+        build_wire(CompressedKVData("r", 0, None, {}, 0, 0, False), 10)
+    with pytest.raises(TypeError, match="still contains a tensor"):
+        build_wire(CompressedKVData("r", 0, torch.zeros(1), {"x": torch.zeros(1)}, 0, 0), 10)
+    w = build_wire(_payload({"a": torch.ones(1), "b": torch.ones(1)}), 10)
+    w.meta["aux_layout"]["mode"] = "other"
+    with pytest.raises(ValueError, match="Unknown aux_layout"):
+        restore_from_wire(w)
+
+
+@pytest.mark.gpu
+def test_adapter_payload_over_the_wire_decodes_identically(cuda):
+    """Fused adapter packet -> wire (4 KiB body pieces, msgpack meta) -> restore ->
+    decompress equals decompressing the packet itself; the metadata ships as one
+    view of the packet's metadata allocation."""
+    from kvserve_amd.compression import KVCompressionAdapter
+
+    cfg = {"pipeline": ["transformer", "quantizer", "codec"],
+           "transformer_config": {"transform_type": "hadamard", "seed": 3237919422},
+           "quantizer_config": {"model_name": "Llama-3.1-8B-Instruct", "hybrid_ratio": 0.3,
+                                "high_key_max_value": 16, "high_value_max_value": 16,
+                                "low_key_max_value": 12, "low_value_max_value": 12},
+           "codec_config": {"codec_type": "bitpack", "bitpack_bits": 4}}
+    ad = KVCompressionAdapter(cfg, num_kv_heads=8, head_size=128)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn((3, 2, 5, 16, 8, 128), generator=g).to(torch.bfloat16).to(cuda)
+    packet = ad.compress(x, "wire")
+    w = build_wire(packet, max_chunk_bytes=4096)
+    assert len(w.body_chunks) > 1 and len(w.aux_tensors) == 1
+    qp0 = packet.metadata["quantization_params"][0]
+    some = next(v["min_val"] for v in qp0.values() if isinstance(v, dict) and v.get("min_val") is not None)
+    assert w.aux_tensors[0].untyped_storage().data_ptr() == some.untyped_storage().data_ptr()
+    w = CompressedWire(msgpack.unpackb(msgpack.packb(w.meta), raw=False), w.body_chunks, w.aux_tensors)
+    out = ad.decompress(restore_from_wire(w))
+    assert torch.equal(out, ad.decompress(packet))
