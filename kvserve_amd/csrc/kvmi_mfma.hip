@@ -856,7 +856,7 @@ __global__ __launch_bounds__(kMW) void decode_mfma_kernel(Geo g, const kvmi_laye
 #pragma unroll
     for (int u = 0; u < RQ * kTok / 64; ++u) {
       const int qq = 64 * u + l;
-      gst(dst + qq, stg[(qq / RQ) * RP + qq % RQ]);
+      gst_stream(dst + qq, stg[(qq / RQ) * RP + qq % RQ]);
     }
   };
   // Two input buffers: section q + 4 is loading while section q is computed (past the
