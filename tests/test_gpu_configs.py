@@ -301,3 +301,40 @@ def test_config5_full_size_batch_sampled_matches_oracle(cuda):
         _check_layer(bplan.packets[r], l, x[(r, l)], _bits(reqs[r].pools[l][:, reqs[r].block_ids.long()]))
     del wl, reqs, bplan, dplan
     _free()
+
+
+# ------------------------------------------------------------------ other geometries
+@pytest.mark.parametrize("H,S,D,bits", [
+    (4, 16, 128, 4),   # tensor-parallel half of 8 KV heads
+    (2, 16, 128, 4),
+    (1, 32, 128, 4),   # one head, 32-token blocks
+    (4, 32, 64, 3),
+    (8, 32, 128, 2),
+    (8, 16, 128, 8),
+    (16, 16, 128, 4),  # 8 % H != 0: register-FWHT kernels
+    (8, 16, 64, 5),
+])
+def test_geometries_match_oracle(cuda, H, S, D, bits):
+    from kvserve_amd.engine import FusedKVCodec, check_packet
+    from kvserve_amd.profiles import section_profile
+    from kvserve_amd.workloads import kv_blocks
+
+    g = torch.Generator().manual_seed(H * 1000 + S * 10 + D + bits)
+    L, B, P = 3, 7, 24
+    levels = (2 ** bits - 1, max(2, 2 ** bits - 3))
+    pools = [torch.zeros((2, P, S, H, D), dtype=torch.bfloat16) for _ in range(L)]
+    ids = torch.randperm(P, generator=g)[:B]
+    for p in pools:
+        p[:, ids] = kv_blocks(g, B, S, H, D)
+    prof = [section_profile([bool(v) for v in torch.randint(0, 2, (H,), generator=g)], levels[0], levels[0],
+                            levels[1], levels[1]) for _ in range(L)]
+    pools = [p.to(cuda) for p in pools]
+    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE)
+    packet = codec.compress(pools, ids.to(torch.int32).to(cuda), prof)
+    check_packet(packet)
+    x = [_bits(p[:, ids.to(cuda).long()]) for p in pools]
+    dst = [torch.zeros_like(p) for p in pools]
+    codec.decompress(packet, dst, ids.to(torch.int32).to(cuda))
+    torch.cuda.synchronize()
+    for l in range(L):
+        _check_layer(packet, l, x[l], _bits(dst[l][:, ids.to(cuda).long()]))
