@@ -14,11 +14,13 @@ Inputs are resident in HBM before the timed region; plans (device descriptors) a
 built before it too.  Per-direction throughput and the fraction of HBM peak are
 printed alongside.  Prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config3|config4|config5]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config3|config4|config5|connector]
 
 The other BASELINE configurations can be timed with --workload (the metric is quoted
 on config2, the default; multi-request workloads run as one batched plan per
-direction, and the CPU baseline is measured for config2 only).
+direction, and the CPU baseline is measured for config2 only).  --workload connector
+times the config-2 request through the vLLM connector (save + load, host-timed) and
+the reference connector's extract/stack/compress procedure beside it.
 """
 
 from __future__ import annotations
@@ -53,6 +55,20 @@ WORKLOADS = {
                "10 streams of 8 layers; step = compress + decompress",
     "config5": "config5: 256 requests x 256 tokens, 16 layers x 8 heads x D=64, 6/6 levels, bitpack 3, seeded "
                "random blocks, one batched plan per direction; step = compress + decompress",
+    "connector": "connector: the config2 request through CompressedKVConnector (save_kv_layer x 32 + wait_for_save "
+                 "-> LoopbackTransport -> start_load_kv into the same caches and block ids), Hadamard seed "
+                 "0xC0FEBABE, Llama-3.1-8B head split hybrid 0.3, 16/16 levels, bitpack 4; step = save + load, "
+                 "host-timed with device synchronization; the reference connector's procedure (extract, stack, "
+                 "compress, build_wire / restore, decompress, inject) on the same kernels timed beside it",
+}
+
+CONNECTOR_PROFILE = {
+    "pipeline": ["transformer", "quantizer", "codec"],
+    "transformer_config": {"transform_type": "hadamard", "seed": 0xC0FEBABE},
+    "quantizer_config": {"model_name": "Llama-3.1-8B-Instruct", "hybrid_ratio": 0.3, "high_key_max_value": 16,
+                         "high_value_max_value": 16, "low_key_max_value": 16, "low_value_max_value": 16,
+                         "axis_key": "channel", "axis_value": "token", "split_type": "head"},
+    "codec_config": {"codec_type": "bitpack", "bitpack_bits": 4},
 }
 
 
@@ -132,6 +148,126 @@ def cpu_baseline(wl, budget_s: float):
     }
 
 
+def bench_connector(args) -> dict:
+    """Time one request through the connector's worker path and, beside it, the
+    reference connector's procedure on the same operators."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from kvserve_amd import workloads
+    from kvserve_amd.compression import KVCompressionAdapter
+    from kvserve_amd.compression.wire import CompressedWire, build_wire, restore_from_wire
+    from kvserve_amd.connector import (CompressedKVConnector, CompressedKVConnectorMetadata, KVConnectorRole,
+                                       LoopbackTransport, extract_kv_from_layer_by_blocks,
+                                       inject_kv_into_layer_by_blocks)
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.make_config2(device=dev, num_layers=args.layers)
+    req = wl.requests[0]
+    L, S, H, D = len(req.pools), wl.block_size, wl.num_heads, wl.head_dim
+    names = [f"model.layers.{i}.self_attn.attn" for i in range(L)]
+    caches = dict(zip(names, req.pools))
+    ids = [int(b) for b in req.block_ids.tolist()]
+    tokens = list(range(len(ids) * S))
+
+    def cfg(producer: bool, port: int):
+        extra = {"compression": CONNECTOR_PROFILE, "transport_class": "loopback"}
+        return SimpleNamespace(
+            kv_transfer_config=SimpleNamespace(is_kv_producer=producer, kv_buffer_size=1 << 36, kv_ip="127.0.0.1",
+                                               kv_port=port, kv_connector_extra_config=extra),
+            cache_config=SimpleNamespace(block_size=S),
+            model_config=SimpleNamespace(get_num_kv_heads=lambda pc: H, get_head_size=lambda: D,
+                                         model="Llama-3.1-8B-Instruct", use_mla=False),
+            parallel_config=SimpleNamespace())
+
+    class Layer:
+        def __init__(self, cache):
+            self.kv_cache = [cache]
+
+    prod = CompressedKVConnector(cfg(True, 31000), KVConnectorRole.WORKER)
+    cons = CompressedKVConnector(cfg(False, 31000), KVConnectorRole.WORKER)
+    pm, dm = CompressedKVConnectorMetadata(), CompressedKVConnectorMetadata()
+    pm.add_request("req", "T", tokens, ids, S)
+    dm.add_request("req", "T", tokens, ids, S)
+    prod.bind_connector_metadata(pm)
+    cons.bind_connector_metadata(dm)
+    fctx = SimpleNamespace(no_compile_layers={n: Layer(c) for n, c in caches.items()}, virtual_engine=0)
+
+    def connector_step():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for n in names:
+            prod.save_kv_layer(n, caches[n], None)
+        prod.wait_for_save()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        cons.start_load_kv(fctx)
+        torch.cuda.synchronize()
+        return t1 - t0, time.perf_counter() - t1
+
+    ad = KVCompressionAdapter(CONNECTOR_PROFILE, num_kv_heads=H, head_size=D, model_name="Llama-3.1-8B-Instruct")
+    tx = LoopbackTransport(True, port=31001)
+    rx = LoopbackTransport(False, port=31001, recv_buffer_size=1 << 36)
+    order = sorted(names)
+
+    def reference_step():
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        stacked = torch.stack([extract_kv_from_layer_by_blocks(caches[n], ids) for n in order])
+        wire = build_wire(ad.compress(stacked, "req"), 512 << 20)
+        tx.send_bundle("T", ["__compressed__"] + order, wire.meta, wire.body_chunks, wire.aux_tensors)
+        tx.wait_for_sent()
+        del stacked, wire
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ((_, payload),) = rx.drain_received()["T"]
+        out = ad.decompress(restore_from_wire(CompressedWire(payload["meta"], payload["body_chunks"],
+                                                             payload["aux_tensors"])))
+        for i, n in enumerate(order):
+            inject_kv_into_layer_by_blocks(caches[n], out[i], ids)
+        torch.cuda.synchronize()
+        rx.release_received("T", rx.payload_nbytes(payload))
+        return t1 - t0, time.perf_counter() - t1
+
+    def timed(step, label):
+        print(f"bench: {label}: warmup {args.warmup} steps", file=sys.stderr, flush=True)
+        for _ in range(args.warmup):
+            step()
+        print(f"bench: {label}: timing {args.steps} steps", file=sys.stderr, flush=True)
+        ts = [step() for _ in range(args.steps)]
+        return sum(t[0] for t in ts) / len(ts), sum(t[1] for t in ts) / len(ts)
+
+    save_s, load_s = timed(connector_step, "connector")
+    wire_bytes = next(r["payload_bytes"] for r in reversed(prod._transport.stats) if r["direction"] == "send")
+    ref_save_s, ref_load_s = timed(reference_step, "reference procedure")
+    R = L * 2 * len(ids) * S * H * D * 2
+    return {
+        "metric": "connector save + load GB/s of raw bf16 KV on 1 MI355X (wait_for_save + start_load_kv)",
+        "value": round(R / (save_s + load_s) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round((save_s + load_s) * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
+        "config": {"workload": WORKLOADS["connector"], "requests": 1, "layers": L, "tokens": len(tokens),
+                   "raw_bytes": R, "wire_bytes": wire_bytes},
+        "save_ms": round(save_s * 1e3, 4),
+        "load_ms": round(load_s * 1e3, 4),
+        "save_gbps": round(R / save_s / 1e9, 2),
+        "load_gbps": round(R / load_s / 1e9, 2),
+        "reference_procedure": {"save_ms": round(ref_save_s * 1e3, 4), "load_ms": round(ref_load_s * 1e3, 4),
+                                "gbps": round(R / (ref_save_s + ref_load_s) / 1e9, 2)},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -151,6 +287,11 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.workload == "connector":
+        torch.cuda.set_device(0)
+        print(json.dumps(bench_connector(args)), flush=True)
+        return 0
 
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)

@@ -58,6 +58,9 @@ def tables_from_dicts(dicts: Sequence[Dict], H: int, D: int, B: int, S: int,
     for d in dicts:
         n = sum(1 for s in ("low_value_meta", "high_value_meta") if d[s]["min_val"] is not None)
         G = max(G, n)
+    views = _table_views(dicts, H, D, B * S, G, device)
+    if views is not None:
+        return views
     kmeta = torch.empty((L, 2, H, D), dtype=torch.bfloat16, device=device)
     vmeta = torch.zeros((L, 2, G, B * S), dtype=torch.bfloat16, device=device)
     for l, d in enumerate(dicts):
@@ -70,4 +73,58 @@ def tables_from_dicts(dicts: Sequence[Dict], H: int, D: int, B: int, S: int,
         for g, p in enumerate(parts_v):
             vmeta[l, 0, g] = p["min_val"].reshape(-1).to(device, torch.bfloat16)
             vmeta[l, 1, g] = p["quant_scale"].reshape(-1).to(device, torch.bfloat16)
+    return kmeta, vmeta
+
+
+def _table_views(dicts: Sequence[Dict], H: int, D: int, BS: int, G: int,
+                 device) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """kmeta / vmeta as views when every section tensor already sits where the
+    engine's one-allocation layout puts it (kmeta [L,2,H,D] followed by vmeta
+    [L,2,G,B*S], bf16) -- the case of a packet made by this engine, also after a
+    wire round trip that shipped the allocation whole.  Pointer arithmetic only;
+    None when any tensor is elsewhere (the caller then copies)."""
+    L = len(dicts)
+    if L == 0:
+        return None
+    first = dicts[0]["low_key_meta"]["min_val"]
+    if first is None:
+        first = dicts[0]["high_key_meta"]["min_val"]
+    if first is None or first.dtype != torch.bfloat16 or first.device != torch.device(device):
+        return None
+    st = first.untyped_storage()
+    sp, base = st.data_ptr(), first.data_ptr()
+    kn, vn = L * 2 * H * D, L * 2 * G * BS
+    if (base - sp) % 2 or base - sp + 2 * (kn + vn) > st.nbytes():
+        return None
+    vbase = base + 2 * kn
+
+    def at(t, addr, numel) -> bool:
+        return (t is not None and t.dtype == torch.bfloat16 and t.is_contiguous() and t.numel() == numel
+                and t.data_ptr() == addr and t.untyped_storage().data_ptr() == sp)
+
+    for l, d in enumerate(dicts):
+        h = 0
+        for s in ("low_key_meta", "high_key_meta"):
+            mn = d[s]["min_val"]
+            if mn is None:
+                continue
+            rows = mn.numel() // D
+            if not (at(mn, base + 2 * ((2 * l) * H + h) * D, rows * D)
+                    and at(d[s]["quant_scale"], base + 2 * ((2 * l + 1) * H + h) * D, rows * D)):
+                return None
+            h += rows
+        if h != H:
+            return None
+        g = 0
+        for s in ("low_value_meta", "high_value_meta"):
+            mn = d[s]["min_val"]
+            if mn is None:
+                continue
+            if not (at(mn, vbase + 2 * ((2 * l) * G + g) * BS, BS)
+                    and at(d[s]["quant_scale"], vbase + 2 * ((2 * l + 1) * G + g) * BS, BS)):
+                return None
+            g += 1
+    off = (base - sp) // 2
+    kmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off, (L, 2, H, D))
+    vmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off + kn, (L, 2, G, BS))
     return kmeta, vmeta

@@ -305,7 +305,8 @@ class FusedCompressionManager(CompressionManager):
         profs = self.profiles(layer_ids, H)
         codec = self._codec(H, D, S)
         packet = codec.compress(pools, block_ids, profs, layer_ids=layer_ids)
-        check_packet(packet)
+        # the metadata dicts are built while the kernels run; the error check (a
+        # synchronization) comes last
         B = packet.num_blocks
         original_size = L * 2 * B * S * H * D * 2
         transform, seed, has_codec, bits = self._settings()
@@ -329,9 +330,11 @@ class FusedCompressionManager(CompressionManager):
             m["compressed_size"] = st.numel()
         if len(streams) == 1:
             metas[0]["original_size"] = original_size
+            check_packet(packet)
             return CompressedKVData(request_id, L - 1, streams[0], metas[0], original_size, streams[0].numel())
         for ci, m in enumerate(metas):
             m.update({"chunk_index": ci, "total_chunks": len(metas)})
+        check_packet(packet)
         total = sum(st.numel() for st in streams)
         return CompressedKVData(request_id, L - 1, None,
                                 {"request_id": request_id, "original_size": original_size, "num_layers": L,

@@ -178,6 +178,15 @@ class KVCompressionAdapter:
             log.error("[KVCompressionAdapter] paged compression failed for %s: %s", request_id, e)
             return None
 
+    def update_controller(self, request_id: str, observed_latency_ms: float) -> None:
+        """Latency feedback for the online controller (manager.py:283-290); without
+        the controller mode there is nothing to update."""
+        return None
+
+    def get_controller_stats(self) -> Optional[dict]:
+        """manager.py:292-296: None outside the controller mode."""
+        return None
+
     def decompress_paged(self, compressed: CompressedKVData, kv_caches: Sequence[torch.Tensor], block_ids) -> None:
         """Decompress into the paged caches at `block_ids` (the first num_blocks ids)."""
         mgr = self._manager

@@ -16,7 +16,9 @@ The meta layout, the placeholder and the layout table are the reference's wire
 format, so a bundle built here is read by the reference's `restore_from_wire` and
 the other way round.  Where every metadata tensor is a contiguous slice of one
 allocation -- the fused engine keeps K and V metadata in one buffer -- the aux
-tensor is a view of that allocation and nothing is copied; otherwise the tensors
+tensor is a view of that allocation and nothing is copied (an allocation used from
+its start is shipped to its end when the unused tail is shorter than the used
+span, so the receiver can view the engine's tables whole); otherwise the tensors
 are copied into one byte tensor, each at an offset aligned to its element size.
 """
 
@@ -75,17 +77,21 @@ def build_wire(compressed: CompressedKVData, max_chunk_bytes: int) -> Compressed
             meta["body_mode"] = "single"
         meta["body_spec"] = _spec(t)
     aux_out = _coalesce(meta, aux)
-    _no_tensors(meta)
     return CompressedWire(meta=meta, body_chunks=body, aux_tensors=aux_out)
 
 
 def _pack_meta(obj: Any, aux: List[torch.Tensor]) -> Any:
-    # only "quantization_params" carries tensors (wire.py:140-147)
+    """Only "quantization_params" may carry tensors (wire.py:140-147); they become
+    placeholders, and a tensor anywhere else is an error."""
     if not isinstance(obj, dict):
+        _no_tensors(obj)
         return obj
     out = dict(obj)
-    if "quantization_params" in out:
-        out["quantization_params"] = _pack_tree(out["quantization_params"], aux)
+    for k, v in out.items():
+        if k == "quantization_params":
+            out[k] = _pack_tree(v, aux)
+        else:
+            _no_tensors(v)
     return out
 
 
@@ -157,6 +163,11 @@ def _shared_storage_range(aux: List[torch.Tensor]):
     hi = max(s[1] for s in spans)
     if any((s[0] - lo) % s[2] for s in spans):
         return None
+    # an allocation used from its start ships to its end when the unused tail is
+    # shorter than the used span (the engine's metadata tables: the receiver can
+    # then view them whole instead of copying section by section)
+    if lo == 0 and st.nbytes() - hi < hi:
+        hi = st.nbytes()
     return st, lo, hi
 
 

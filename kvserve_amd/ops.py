@@ -106,12 +106,19 @@ def _ids(block_ids, pool: torch.Tensor) -> torch.Tensor:
     return torch.tensor(ids_list, dtype=torch.int32, device=pool.device)
 
 
-def gather_blocks(pool: torch.Tensor, block_ids) -> torch.Tensor:
+def gather_blocks(pool: torch.Tensor, block_ids, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """extract_kv_from_layer_by_blocks (kv_utils.py:59-80), FlashAttention layout
-    [2, num_blocks, ...]: returns pool[:, block_ids] as a new contiguous tensor."""
+    [2, num_blocks, ...]: returns pool[:, block_ids] as a new contiguous tensor, or
+    writes it into `out` (contiguous, same shape and dtype; e.g. one layer's slice of
+    a stacked [L, 2, nb, ...] tensor) and returns `out`."""
     _pool_check(pool)
     ids = _ids(block_ids, pool)
-    out = torch.empty((2, ids.numel()) + tuple(pool.shape[2:]), dtype=pool.dtype, device=pool.device)
+    shape = (2, ids.numel()) + tuple(pool.shape[2:])
+    if out is None:
+        out = torch.empty(shape, dtype=pool.dtype, device=pool.device)
+    elif tuple(out.shape) != shape or out.dtype != pool.dtype or out.device != pool.device \
+            or not out.is_contiguous():
+        raise ValueError(f"gather output must be a contiguous {pool.dtype} tensor of shape {shape} on {pool.device}")
     blk = math.prod(pool.shape[2:])
     with torch.cuda.device(pool.device):
         _lib.check(_lib.load().kvmi_gather_blocks(pool.data_ptr(), pool.shape[1] * blk, ids.data_ptr(), ids.numel(),

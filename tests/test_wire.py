@@ -144,3 +144,47 @@ def test_adapter_payload_over_the_wire_decodes_identically(cuda):
     w = CompressedWire(msgpack.unpackb(msgpack.packb(w.meta), raw=False), w.body_chunks, w.aux_tensors)
     out = ad.decompress(restore_from_wire(w))
     assert torch.equal(out, ad.decompress(packet))
+
+
+def _engine_tables(L, H, D, B, S, rows, G, gen):
+    """Engine-layout metadata in one bf16 allocation and its reference-format dicts."""
+    from kvserve_amd.compression._meta import layer_dict
+    from kvserve_amd.profiles import section_profile
+
+    kn, vn = L * 2 * H * D, L * 2 * G * B * S
+    buf = torch.randn(kn + vn, generator=gen).to(torch.bfloat16)
+    kmeta, vmeta = buf[:kn].view(L, 2, H, D), buf[kn:].view(L, 2, G, B * S)
+    profs = [section_profile(row, 16, 16, 12, 12) for row in rows]
+    return buf, kmeta, vmeta, [layer_dict(kmeta[l], vmeta[l], profs[l], B, S) for l in range(L)]
+
+
+def test_engine_tables_come_back_as_views_also_over_the_wire():
+    """Dicts made from the engine's one-allocation tables give the tables back as
+    views (no copy), directly and after build_wire / restore_from_wire; dicts
+    elsewhere take the copy path and give the same values."""
+    from kvserve_amd.compression._meta import tables_from_dicts
+
+    L, H, D, B, S = 3, 4, 8, 2, 4
+    rows = [[True, False, False, True], [False] * 4, [True] * 4]   # G: 2, 1, 1 -> G = 2
+    buf, kmeta, vmeta, dicts = _engine_tables(L, H, D, B, S, rows, 2, torch.Generator().manual_seed(1))
+    k2, v2 = tables_from_dicts(dicts, H, D, B, S, "cpu")
+    assert k2.data_ptr() == kmeta.data_ptr() and v2.data_ptr() == vmeta.data_ptr()
+    assert torch.equal(k2, kmeta) and torch.equal(v2, vmeta)
+
+    # the last layer uses one of two V groups, so the used span ends before the
+    # allocation does: the wire ships the allocation to its end
+    w = build_wire(_payload(dicts), 1 << 20)
+    assert w.aux_tensors[0].numel() == buf.numel() * 2
+    received = CompressedWire(msgpack.unpackb(msgpack.packb(w.meta), raw=False), w.body_chunks,
+                              [w.aux_tensors[0].clone()])
+    q = restore_from_wire(received).metadata["quantization_params"]
+    k3, v3 = tables_from_dicts(q, H, D, B, S, "cpu")
+    assert k3.untyped_storage().data_ptr() == received.aux_tensors[0].untyped_storage().data_ptr()
+    assert torch.equal(k3, kmeta) and torch.equal(v3[0], vmeta[0]) and torch.equal(v3[1:, :, 0], vmeta[1:, :, 0])
+
+    # copies of the sections (no shared allocation): copy path, same values
+    copied = [{k: ({kk: (vv.clone() if isinstance(vv, torch.Tensor) else vv) for kk, vv in v.items()}
+                   if isinstance(v, dict) else v) for k, v in d.items()} for d in dicts]
+    k4, v4 = tables_from_dicts(copied, H, D, B, S, "cpu")
+    assert k4.data_ptr() != kmeta.data_ptr()
+    assert torch.equal(k4, kmeta) and torch.equal(v4[0], vmeta[0]) and torch.equal(v4[1:, :, 0], vmeta[1:, :, 0])
