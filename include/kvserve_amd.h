@@ -55,6 +55,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 /* Bits OR-ed into the caller's device error word. */
 #define KVMI_ERR_SYMBOL_RANGE 1 /* a symbol >= 2^bits reached the packer */
 #define KVMI_ERR_BAD_HEADER 2   /* stream header does not match the decode contract */
+#define KVMI_ERR_CORRUPT 4      /* an entropy-coded block does not decode consistently */
 
 /* Host-visible return codes. */
 #define KVMI_OK 0
@@ -191,6 +192,29 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  */
 int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
                       int32_t max_blocks, int32_t* err, kvmi_stream_t stream);
+
+/*
+ * Entropy codec (rANS) for the codec stage -- replaces the nvCOMP ANS codec that
+ * KVServe's codec stage calls (kvserve_v1/compression/codec/kvserve_codec.py:57-64,
+ * nvcomp_func.py:54-143: a uint8 view in, compressed bytes out, and back).  The
+ * stream format is this engine's own (nvCOMP's is closed); oracle/rans.c
+ * states it.  Input: n symbols of `bits` (1..8) bits packed LSB-first, i.e. a
+ * bitpack body.  All pointers 8-byte aligned.
+ *
+ * kvmi_rans_max_bytes: capacity the encoder's `out` must have.
+ * kvmi_rans_scratch_bytes: device scratch the encoder needs.
+ * kvmi_rans_encode: three launches; the stream length is written to the device u64
+ *   *out_len (read it after the stream completes).
+ * kvmi_rans_decode: one launch; writes ceil(n*bits/8) packed bytes.  A header that
+ *   does not name (bits, n) sets KVMI_ERR_BAD_HEADER; a block that does not decode
+ *   to its own end state sets KVMI_ERR_CORRUPT.
+ */
+int64_t kvmi_rans_max_bytes(int64_t n, int32_t bits);
+int64_t kvmi_rans_scratch_bytes(int64_t n, int32_t bits);
+int kvmi_rans_encode(const uint8_t* packed, int64_t n, int32_t bits, uint8_t* out, int64_t out_capacity,
+                     void* scratch, int64_t scratch_bytes, uint64_t* out_len, kvmi_stream_t stream);
+int kvmi_rans_decode(const uint8_t* stream_in, int64_t in_bytes, int64_t n, int32_t bits, uint8_t* packed_out,
+                     int32_t* err, kvmi_stream_t stream);
 
 #ifdef __cplusplus
 }

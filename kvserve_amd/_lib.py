@@ -18,6 +18,7 @@ ABI_VERSION = 1
 # Device error bits (KVMI_ERR_*) and host return codes (KVMI_*).
 ERR_SYMBOL_RANGE = 1
 ERR_BAD_HEADER = 2
+ERR_CORRUPT = 4
 OK, EINVAL, ELAUNCH = 0, -22, -5
 
 F_NO_TRANSFORM = 1
@@ -37,6 +38,10 @@ EXPORTS = (
     "kvmi_kstats_paged",
     "kvmi_encode_paged",
     "kvmi_decode_paged",
+    "kvmi_rans_max_bytes",
+    "kvmi_rans_scratch_bytes",
+    "kvmi_rans_encode",
+    "kvmi_rans_decode",
 )
 
 
@@ -76,6 +81,10 @@ _SIGNATURES = {
     "kvmi_kstats_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_encode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_decode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
+    "kvmi_rans_max_bytes": ([_i64, _i32], _i64),
+    "kvmi_rans_scratch_bytes": ([_i64, _i32], _i64),
+    "kvmi_rans_encode": ([_vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp], ctypes.c_int),
+    "kvmi_rans_decode": ([_vp, _i64, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
 }
 
 

@@ -417,6 +417,8 @@ def raise_device_error(code: int) -> None:
         raise RuntimeError("symbol exceeds bitpack_bits")
     if code & _lib.ERR_BAD_HEADER:
         raise RuntimeError("invalid bitpack header or decode configuration")
+    if code & _lib.ERR_CORRUPT:
+        raise RuntimeError("corrupt entropy-coded stream")
 
 
 def check_packet(packet: Packet, force: bool = False) -> None:

@@ -1,5 +1,5 @@
 """Torch-level wrappers of the unit C-ABI entry points (bitpack, gather / scatter,
-Hadamard).  Each enqueues on the current stream of the tensors' device.
+Hadamard, rANS).  Each enqueues on the current stream of the tensors' device.
 
 Device data errors (a symbol wider than the bit width, a header that does not match)
 are reported through a device error word.  By default the wrappers synchronize and
@@ -161,3 +161,56 @@ def hadamard(x: torch.Tensor, layer_id: int, seed: int, inverse: bool = False,
         _lib.check(_lib.load().kvmi_hadamard(src.data_ptr(), dst.data_ptr(), rows, H, D, signs.data_ptr(),
                                              1 if inverse else 0, _stream()), "kvmi_hadamard")
     return dst
+
+
+def _aligned8(t: torch.Tensor) -> torch.Tensor:
+    return t if t.data_ptr() % 8 == 0 else t.clone()
+
+
+def rans_encode(packed: torch.Tensor, n: int, bits: int) -> torch.Tensor:
+    """Entropy-code n symbols of `bits` bits packed LSB-first (a bitpack body) into
+    this engine's rANS stream -- the codec stage's nvCOMP ANS encode
+    (nvcomp_func.py:54-95).  Synchronizes once to learn the stream length; returns a
+    view of the stream's bytes."""
+    if packed.dtype != torch.uint8 or packed.dim() != 1 or not packed.is_cuda:
+        raise TypeError("rans_encode takes a 1-D uint8 CUDA tensor")
+    n, bits = int(n), _bits(bits)
+    if packed.numel() < (n * bits + 7) // 8:
+        raise ValueError("packed buffer is shorter than n symbols of this width")
+    lib = _lib.load()
+    cap, scr = int(lib.kvmi_rans_max_bytes(n, bits)), int(lib.kvmi_rans_scratch_bytes(n, bits))
+    if cap < 0 or scr < 0:
+        raise ValueError("invalid rANS size or width")
+    dev = packed.device
+    src = _aligned8(packed.contiguous())
+    out = torch.empty((cap + 7) // 8 * 8, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(max(scr, 8), dtype=torch.uint8, device=dev)
+    length = torch.empty(1, dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.kvmi_rans_encode(src.data_ptr(), n, bits, out.data_ptr(), out.numel(), scratch.data_ptr(),
+                                        scratch.numel(), length.data_ptr(), _stream()), "kvmi_rans_encode")
+    return out[: int(length.item())]
+
+
+def rans_decode(stream: torch.Tensor, n: int, bits: int, out: Optional[torch.Tensor] = None,
+                check: Optional[bool] = None) -> torch.Tensor:
+    """Inverse of rans_encode: ceil(n*bits/8) packed bytes (into `out`, an 8-byte
+    aligned uint8 tensor of at least that size, when given) -- the codec stage's
+    nvCOMP ANS decode (nvcomp_func.py:97-143)."""
+    if stream.dtype != torch.uint8 or stream.dim() != 1 or not stream.is_cuda:
+        raise TypeError("rans_decode takes a 1-D uint8 CUDA tensor")
+    n, bits = int(n), _bits(bits)
+    if stream.numel() < 32:
+        raise ValueError("rANS stream is shorter than its header")
+    nbytes = (n * bits + 7) // 8
+    if out is None:
+        out = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=stream.device)[:nbytes]
+    elif out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < nbytes or out.data_ptr() % 8:
+        raise ValueError("out must be a contiguous, 8-byte aligned uint8 tensor of ceil(n*bits/8) bytes")
+    src = _aligned8(stream.contiguous())
+    err = torch.zeros(1, dtype=torch.int32, device=stream.device)
+    with torch.cuda.device(stream.device):
+        _lib.check(_lib.load().kvmi_rans_decode(src.data_ptr(), src.numel(), n, bits, out.data_ptr(), err.data_ptr(),
+                                                _stream()), "kvmi_rans_decode")
+    _maybe_check(err, check)
+    return out

@@ -13,7 +13,7 @@ HEADER = ROOT / "include" / "kvserve_amd.h"
 
 def declared_symbols():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*int\s+(kvmi_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t)\s+(kvmi_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -62,6 +62,31 @@ def test_host_contract_errors_return_einval():
     assert lib.kvmi_encode_paged(ctypes.byref(gg), None, 1, 1, None, None) == E
     # zero jobs / zero blocks: nothing to do
     assert lib.kvmi_encode_paged(ctypes.byref(g), None, 0, 5, None, None) == 0
+
+
+def test_rans_sizes_and_contract_errors():
+    """Stream capacity is the raw-block bound of oracle/rans.c; bad arguments are
+    rejected on the host."""
+    from kvserve_amd import _lib
+    from oracle import crans
+
+    lib = _lib.load()
+    E = _lib.EINVAL
+    for n, w in ((0, 4), (1, 1), (65536, 4), (65537, 3), (3 * 65536 + 17, 8)):
+        assert lib.kvmi_rans_max_bytes(n, w) == crans.max_bytes(n, w)
+    assert lib.kvmi_rans_max_bytes(65536, 4) == 32 + 8 + 4 + 32768
+    assert lib.kvmi_rans_scratch_bytes(65536 * 2, 4) == 2 * (4 + 32 + 256 + 32768) + 8
+    assert lib.kvmi_rans_max_bytes(-1, 4) == E and lib.kvmi_rans_max_bytes(10, 0) == E
+    assert lib.kvmi_rans_max_bytes(10, 9) == E and lib.kvmi_rans_scratch_bytes(10, 9) == E
+    buf = ctypes.create_string_buffer(1 << 16)
+    a = (ctypes.addressof(buf) + 7) // 8 * 8
+    # capacity too small, misaligned pointers, missing pointers
+    assert lib.kvmi_rans_encode(a, 100, 4, a, 10, a, 1 << 12, a, None) == E
+    assert lib.kvmi_rans_encode(a, 100, 4, a + 1, 1 << 12, a, 1 << 12, a, None) == E
+    assert lib.kvmi_rans_encode(None, 100, 4, a, 1 << 12, a, 1 << 12, a, None) == E
+    assert lib.kvmi_rans_decode(a, 16, 100, 4, a, a, None) == E
+    assert lib.kvmi_rans_decode(a + 4, 64, 100, 4, a, a, None) == E
+    assert lib.kvmi_rans_decode(a, 64, 100, 0, a, a, None) == E
 
 
 def test_profiles_validate_and_serialize():
