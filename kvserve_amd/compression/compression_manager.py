@@ -26,13 +26,16 @@ import torch
 
 from ..engine import DEFAULT_SEED, FusedKVCodec, Packet, chunk_ranges, check_packet
 from ._meta import layer_dict, tables_from_dicts
+from .codec import is_entropy_codec
+from .codec.rans_codec import unpack_target
+from .. import ops
 
 log = logging.getLogger("kvserve_amd")
 
 _CODEC_LAYOUT_ENV = "KVSERVE_CODEC_LAYOUT"
 
-# The reference default (compression_manager.py:23-43) uses the closed nvCOMP ANS codec;
-# on ROCm the same quantizer profile is carried by the bitpack codec (symbols <= 11).
+# The reference default (compression_manager.py:23-43); its nvCOMP ANS codec stage is
+# served by this engine's rANS codec (same role, this engine's stream format).
 DEFAULT_COMPRESSION_CONFIG: Dict[str, Any] = {
     "enabled": True,
     "pipeline": ["quantizer", "codec"],
@@ -47,7 +50,7 @@ DEFAULT_COMPRESSION_CONFIG: Dict[str, Any] = {
         "axis_value": "token",
         "split_type": "head",
     },
-    "codec_config": {"codec_type": "bitpack", "bitpack_bits": 4},
+    "codec_config": {"codec_type": "nvcomp", "nvcomp_algorithm": "ANS", "data_type": "|u1"},
     "min_compress_size": 1024,
 }
 
@@ -77,6 +80,22 @@ class CompressedKVData:
     is_chunked: bool = False
     chunks: Optional[List[torch.Tensor]] = None
     chunk_metadata: Optional[List[Dict[str, Any]]] = None
+
+
+def symbol_bits(config: "CompressionConfig") -> int:
+    """Width of the values the codec stage codes: `bitpack_bits` for the bitpack
+    codec; for an entropy codec, bit_length of the largest level count when a
+    quantizer runs (the quantizer clamps to L inclusive, quantizer_func.py:65), else
+    8 (bytes)."""
+    cc = config.codec_config or {}
+    if not is_entropy_codec(cc):
+        return int(cc.get("bitpack_bits", 8))
+    qc = config.quantizer_config or {}
+    if "quantizer" not in (config.pipeline or []):
+        return 8
+    top = max(int(qc.get(k, d)) for k, d in (("high_key_max_value", 16), ("high_value_max_value", 16),
+                                             ("low_key_max_value", 12), ("low_value_max_value", 12)))
+    return max(1, min(8, top.bit_length()))
 
 
 def codec_layout() -> str:
@@ -174,8 +193,10 @@ class CompressionManager:
         meta["codec_dtype"] = str(buf.dtype).replace("torch.", "")
         if "codec" in pipe:
             try:
-                out = self.codec.encode(stop - 1, buf, **(self.config.codec_config or {}))
+                out = self.codec.encode(stop - 1, buf, **self._codec_kwargs())
                 meta["codec_applied"] = True
+                if is_entropy_codec(self.config.codec_config):
+                    meta["codec_symbol_bits"] = symbol_bits(self.config)
             except Exception as e:  # compression_manager.py:781-793
                 log.error("[CompressionManager] codec failed: %s", e)
                 out = buf.reshape(-1).view(torch.uint8).contiguous()
@@ -206,11 +227,17 @@ class CompressionManager:
             log.error("[CompressionManager] decompression failed for %s: %s", compressed_data.request_id, e)
             return None
 
+    def _codec_kwargs(self) -> Dict[str, Any]:
+        kw = dict(self.config.codec_config or {})
+        if is_entropy_codec(kw):
+            kw["symbol_bits"] = symbol_bits(self.config)
+        return kw
+
     def _decode_codec(self, tensor: torch.Tensor, meta: Dict) -> torch.Tensor:
         shape, dtype = meta.get("codec_shape"), meta.get("codec_dtype")
         if "codec" in self.config.pipeline and meta.get("codec_applied", False):
             return self.codec.decode(meta.get("start_layer_id", 0), tensor, dtype, shape, meta.get("device"),
-                                     **(self.config.codec_config or {}))
+                                     **self._codec_kwargs())
         return tensor.view(getattr(torch, dtype)).reshape(shape)
 
     def _decompress_range(self, tensor: torch.Tensor, meta: Dict) -> torch.Tensor:
@@ -248,8 +275,11 @@ class FusedCompressionManager(CompressionManager):
         transform = "transformer" in pipe
         seed = int(tc.get("seed", DEFAULT_SEED)) if transform else DEFAULT_SEED
         has_codec = "codec" in pipe
-        bits = int(cc.get("bitpack_bits", 8)) if has_codec else 8
+        bits = symbol_bits(self.config) if has_codec else 8
         return transform, seed, has_codec, bits
+
+    def _entropy(self) -> bool:
+        return "codec" in (self.config.pipeline or []) and is_entropy_codec(self.config.codec_config)
 
     def fusable(self, H: int, D: int, dtype) -> bool:
         pipe = self.config.pipeline or []
@@ -258,7 +288,8 @@ class FusedCompressionManager(CompressionManager):
         if "transformer" in pipe and (self.config.transformer_config or {}).get("transform_type",
                                                                                  "hadamard") != "hadamard":
             return False
-        if "codec" in pipe and (self.config.codec_config or {}).get("codec_type") != "bitpack":
+        if "codec" in pipe and (self.config.codec_config or {}).get("codec_type", "nvcomp") not in (
+                "bitpack", "rans", "nvcomp", "lc"):
             return False
         if self.quantizer.axis_key != "channel" or self.quantizer.axis_value != "token":
             return False
@@ -326,6 +357,12 @@ class FusedCompressionManager(CompressionManager):
                 m["codec_applied"] = True
             metas.append(m)
         streams = packet.streams  # without a codec: raw uint8 codec buffers (8 bits, no header)
+        if self._entropy():
+            # the codec stage: rANS over each chunk's packed symbols (the bitpack body)
+            per = 2 * H * B * S * D
+            streams = [ops.rans_encode(st[16:], (e - s) * per, bits) for (s, e), st in zip(packet.chunks, streams)]
+            for m in metas:
+                m["codec_symbol_bits"] = bits
         for m, st in zip(metas, streams):
             m["compressed_size"] = st.numel()
         if len(streams) == 1:
@@ -364,6 +401,15 @@ class FusedCompressionManager(CompressionManager):
         transform, seed, has_codec, bits = self._settings()
         if not all(m.get("codec_applied", False) == has_codec for m in metas):
             raise ValueError("packet codec does not match the pipeline")
+        if self._entropy():
+            # undo the codec stage: each chunk back to its bitpack stream
+            packed = []
+            for (s, e), st in zip(chunks, streams):
+                n = (e - s) * 2 * H * B * S * D
+                buf = unpack_target(n, bits, device)
+                ops.rans_decode(st.to(device), n, bits, out=buf[16:])
+                packed.append(buf)
+            streams = packed
         return Packet(list(streams), chunks, kmeta, vmeta, self.profiles(layer_ids, H), B, S, H, D, bits, seed,
                       transform, layout, layer_ids)
 

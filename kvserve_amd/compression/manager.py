@@ -11,7 +11,8 @@ the scatter of :83-119 fused into the kernels).
 Registry (_build_manager, manager.py:187-216):
   pipeline stages          "transformer" -> KVServeTransformer (hadamard),
                            "quantizer"   -> KVServeQuantizer,
-                           "codec"       -> KVServeCodec (codec_type "bitpack")
+                           "codec"       -> KVServeCodec (codec_type "bitpack", or "rans" /
+                                            "nvcomp" (ANS) / "lc" served by the GPU rANS codec)
   quantizer_config.impl    absent / "kvserve" / "hip_fused" -> the fused gfx950 manager
                            (same numerics as the modular torch operators);
                            "tilelang_fused" and "centered_codebook" are CUDA-only

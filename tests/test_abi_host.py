@@ -155,6 +155,45 @@ def test_codec_constructor_contracts():
         FusedKVCodec(8, 128, 16, 4, header=False)
 
 
+def test_entropy_codec_switch_and_symbol_width():
+    """codec_type "rans" / "nvcomp" (ANS) / "lc" take the rANS codec; quantized symbols
+    of a profile whose largest level count is L are coded at bit_length(L) bits
+    (the quantizer clamps to L inclusive), anything else as bytes."""
+    from kvserve_amd.compression import CompressionConfig, KVServeCodec
+    from kvserve_amd.compression.codec import BitPackCodec, RANSCodec
+    from kvserve_amd.compression.compression_manager import symbol_bits
+
+    for cc in ({"codec_type": "rans"}, {"codec_type": "nvcomp"}, {"codec_type": "nvcomp", "nvcomp_algorithm": "ANS"},
+               {"codec_type": "lc", "lc_algorithm": "TUPL8_1 BIT_8 RZE_2"}, {}):
+        assert isinstance(KVServeCodec(**cc).codec, RANSCodec), cc
+    c = KVServeCodec(codec_type="rans")
+    c.update_params(codec_type="bitpack", bitpack_bits=3)
+    assert isinstance(c.codec, BitPackCodec) and c.codec.bitpack_bits == 3
+    c.update_params(codec_type="lc")
+    assert isinstance(c.codec, RANSCodec)
+    with pytest.raises(ValueError, match="not available on the ROCm engine"):
+        KVServeCodec(codec_type="nvcomp", nvcomp_algorithm="Zstd")
+    with pytest.raises(ValueError, match="Invalid nvcomp's algorithm"):
+        KVServeCodec(codec_type="nvcomp", nvcomp_algorithm="zip")
+    with pytest.raises(ValueError, match="symbol_bits"):
+        RANSCodec(symbol_bits=9)
+
+    def cfg(pipe, cc, **levels):
+        qc = {"high_key_max_value": 16, "high_value_max_value": 16, "low_key_max_value": 12,
+              "low_value_max_value": 12, **levels}
+        return CompressionConfig(enabled=True, pipeline=pipe, quantizer_config=qc, codec_config=cc)
+
+    q = ["quantizer", "codec"]
+    assert symbol_bits(cfg(q, {"codec_type": "bitpack", "bitpack_bits": 4})) == 4
+    assert symbol_bits(cfg(q, {"codec_type": "nvcomp"})) == 5                      # L = 16 -> 0..16
+    assert symbol_bits(cfg(q, {"codec_type": "nvcomp"}, high_key_max_value=6, high_value_max_value=6,
+                           low_key_max_value=6, low_value_max_value=4)) == 3        # original_top_nvcomp.json
+    assert symbol_bits(cfg(q, {"codec_type": "lc"}, high_key_max_value=12, high_value_max_value=8,
+                           low_key_max_value=6, low_value_max_value=4)) == 4        # the reference default
+    assert symbol_bits(cfg(["codec"], {"codec_type": "nvcomp"})) == 8              # lossless over raw bytes
+    assert symbol_bits(cfg(q, {"codec_type": "rans"}, high_key_max_value=200)) == 8
+
+
 def test_adapter_registry_contracts():
     from kvserve_amd.compression import (CompressionManager, FusedCompressionManager, KVCompressionAdapter,
                                          get_default_compression_config)
@@ -173,14 +212,21 @@ def test_adapter_registry_contracts():
     for bad, exc in (({**base, "quantizer_config": {"impl": "tilelang_fused"}}, ValueError),
                      ({**base, "impl": "centered_codebook"}, ValueError),
                      ({**base, "pipeline": ["transformer", "zip"]}, ValueError),
-                     ({**base, "codec_config": {"codec_type": "nvcomp"}}, ValueError),
+                     ({**base, "codec_config": {"codec_type": "nvcomp", "nvcomp_algorithm": "LZ4"}}, ValueError),
+                     ({**base, "codec_config": {"codec_type": "nvcomp", "nvcomp_algorithm": "Brotli"}}, ValueError),
+                     ({**base, "codec_config": {"codec_type": "zip"}}, ValueError),
                      ({**base, "transformer_config": {"transform_type": "dct"}}, ValueError),
                      ({"mode": "controller", "library_path": "x"}, NotImplementedError)):
         with pytest.raises(exc):
             KVCompressionAdapter(bad, num_kv_heads=8, head_size=128)
     d = KVCompressionAdapter("default", num_kv_heads=4, head_size=128, model_name="Qwen2.5-7B-Instruct")
     assert d._config.quantizer_config["model_name"] == "Qwen2.5-7B-Instruct"
-    assert get_default_compression_config()["codec_config"]["codec_type"] == "bitpack"
+    assert get_default_compression_config()["codec_config"] == {"codec_type": "nvcomp", "nvcomp_algorithm": "ANS",
+                                                                "data_type": "|u1"}
+    for cc in ({"codec_type": "nvcomp"}, {"codec_type": "lc", "lc_algorithm": "TUPL8_1 BIT_8 RZE_2"},
+               {"codec_type": "rans"}):
+        assert isinstance(KVCompressionAdapter({**base, "codec_config": cc}, 8, 128)._manager,
+                          FusedCompressionManager)
 
 
 def test_quantizer_validation_matches_reference_asserts():
