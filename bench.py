@@ -14,13 +14,16 @@ Inputs are resident in HBM before the timed region; plans (device descriptors) a
 built before it too.  Per-direction throughput and the fraction of HBM peak are
 printed alongside.  Prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--workload config2|config3|config4|config5|connector]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+                    [--workload config2|config3|config4|config5|config2_ans|connector]
 
 The other BASELINE configurations can be timed with --workload (the metric is quoted
 on config2, the default; multi-request workloads run as one batched plan per
 direction, and the CPU baseline is measured for config2 only).  --workload connector
 times the config-2 request through the vLLM connector (save + load, host-timed) and
-the reference connector's extract/stack/compress procedure beside it.
+the reference connector's extract/stack/compress procedure beside it; --workload
+config2_ans times the same request with the reference's nvCOMP-ANS profile served by
+the GPU rANS codec.
 """
 
 from __future__ import annotations
@@ -55,6 +58,12 @@ WORKLOADS = {
                "10 streams of 8 layers; step = compress + decompress",
     "config5": "config5: 256 requests x 256 tokens, 16 layers x 8 heads x D=64, 6/6 levels, bitpack 3, seeded "
                "random blocks, one batched plan per direction; step = compress + decompress",
+    "config2_ans": "config2_ans: the config2 request with the reference's shipped nvCOMP-ANS profile "
+                   "(configs/compression/original_top_nvcomp.json: Hadamard seed 0xC0FEBABE, Llama-3.1-8B head "
+                   "split hybrid 0.9, levels 6/6/6/4) served by the GPU rANS codec over 3-bit symbols, 4 streams of "
+                   "8 layers; decompress scatters to a disjoint set of 512 block ids; step = compress (kstats, "
+                   "encode, one batched rANS encode + scan + compact for the 4 streams) + decompress (one batched "
+                   "rANS decode, decode)",
     "connector": "connector: the config2 request through CompressedKVConnector (save_kv_layer x 32 + wait_for_save "
                  "-> LoopbackTransport -> start_load_kv into the same caches and block ids), Hadamard seed "
                  "0xC0FEBABE, Llama-3.1-8B head split hybrid 0.3, 16/16 levels, bitpack 4; step = save + load, "
@@ -145,6 +154,141 @@ def cpu_baseline(wl, budget_s: float):
         "sample": f"{layers} of {len(req.pools)} layers of the config-2 request ({done_bytes / 2**20:.0f} MiB raw), "
                   f"numpy oracle compress+decompress on {cpu_model()} (os.cpu_count()={os.cpu_count()}), "
                   f"{t_total:.1f} s",
+    }
+
+
+NVCOMP_QUANTIZER = {"model_name": "Llama-3.1-8B-Instruct", "hybrid_ratio": 0.9, "high_key_max_value": 6,
+                    "high_value_max_value": 6, "low_key_max_value": 6, "low_value_max_value": 4,
+                    "axis_key": "channel", "axis_value": "token", "split_type": "head"}
+
+
+def bench_entropy(args) -> dict:
+    """The config-2 request with the entropy-coded profile: fused kernels plus the
+    rANS codec stage, every buffer allocated before the timed region."""
+    import ctypes
+    import dataclasses
+
+    import torch
+
+    from kvserve_amd import _lib, workloads
+    from kvserve_amd.compression.codec.rans_codec import unpack_target
+    from kvserve_amd.engine import FusedKVCodec
+    from kvserve_amd.profiles import profiles_from_quantizer_config
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.make_config2(device=dev, num_layers=args.layers)
+    req = wl.requests[0]
+    L, S, H, D, B = len(req.pools), wl.block_size, wl.num_heads, wl.head_dim, req.block_ids.numel()
+    bits = max(NVCOMP_QUANTIZER[k] for k in NVCOMP_QUANTIZER if k.endswith("max_value")).bit_length()
+    profiles = profiles_from_quantizer_config(NVCOMP_QUANTIZER, L, H)
+    codec = FusedKVCodec(H, D, S, bits, wl.seed)
+    cplan = codec.plan_compress(req.pools, req.block_ids, profiles, req.layer_ids)
+    packet = cplan.packet
+    perm = torch.randperm(65536, generator=torch.Generator().manual_seed(77))
+    used = set(req.block_ids.tolist())
+    dst_ids = torch.tensor([i for i in perm.tolist() if i not in used][:B], dtype=torch.int32, device=dev)
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    per = 2 * H * B * S * D
+    chunks = []
+    for (s0, e0), st in zip(packet.chunks, packet.streams):
+        n = (e0 - s0) * per
+        cap, scr = lib.kvmi_rans_max_bytes(n, bits), lib.kvmi_rans_scratch_bytes(n, bits)
+        chunks.append({"n": n, "packed": st, "out": torch.empty((cap + 7) // 8 * 8, dtype=torch.uint8, device=dev),
+                       "scratch": torch.empty(scr, dtype=torch.uint8, device=dev),
+                       "len": torch.zeros(1, dtype=torch.int64, device=dev),
+                       "target": unpack_target(n, bits, dev)})
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    enc_jobs = (_lib.RansEncJob * len(chunks))(*[
+        _lib.RansEncJob(c["packed"].data_ptr() + 16, c["n"], c["out"].data_ptr(), c["out"].numel(),
+                        c["scratch"].data_ptr(), c["scratch"].numel(), c["len"].data_ptr()) for c in chunks])
+
+    def rans_encode_all():  # every stream of the request in one launch per kernel
+        _lib.check(lib.kvmi_rans_encode_batch(enc_jobs, len(chunks), bits, sp), "kvmi_rans_encode_batch")
+
+    def rans_decode_all():
+        _lib.check(lib.kvmi_rans_decode_batch(dec_jobs, len(chunks), bits, err.data_ptr(), sp),
+                   "kvmi_rans_decode_batch")
+
+    def compress():
+        for name in cplan.launches():
+            cplan.launch(name)
+        rans_encode_all()
+
+    compress()
+    torch.cuda.synchronize()
+    cplan.check_errors()
+    for c in chunks:
+        c["nbytes"] = int(c["len"].item())
+    dec_jobs = (_lib.RansDecJob * len(chunks))(*[
+        _lib.RansDecJob(c["out"].data_ptr(), c["nbytes"], c["n"], c["target"].data_ptr() + 16) for c in chunks])
+    dpacket = dataclasses.replace(packet, streams=[c["target"] for c in chunks])
+    dplan = codec.plan_decompress(dpacket, req.pools, dst_ids)
+
+    def decompress():
+        rans_decode_all()
+        for name in dplan.launches():
+            dplan.launch(name)
+
+    print(f"bench: config2_ans: warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        compress()
+        decompress()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    print(f"bench: config2_ans: timing {args.steps} steps", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        ev[k][0].record(stream)
+        compress()
+        ev[k][1].record(stream)
+        decompress()
+        ev[k][2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    cplan.check_errors()
+    dplan.check_errors()
+    if int(err.item()):
+        raise RuntimeError(f"rANS decode reported error {int(err.item())}")
+    for c in chunks:
+        if not torch.equal(c["target"][16:], c["packed"][16:]):
+            raise RuntimeError("rANS round trip differs from the packed symbols")
+        if int(c["len"].item()) != c["nbytes"]:
+            raise RuntimeError("stream length changed between steps")
+    t_c = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    t_d = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    R = L * 2 * B * S * H * D * 2
+    nsym = L * per
+    wire = sum(c["nbytes"] for c in chunks)
+    meta = (packet.kmeta.numel() + packet.vmeta.numel()) * 2
+    return {
+        "metric": "compress/decompress GB/s of raw bf16 KV on 1 MI355X, entropy-coded profile",
+        "value": round(R / ((t_c + t_d) / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
+        "config": {"workload": WORKLOADS["config2_ans"], "requests": 1, "layers": L, "tokens": B * S,
+                   "raw_bytes": R, "symbols": nsym, "symbol_bits": bits, "packed_bytes": nsym * bits // 8,
+                   "wire_bytes": wire, "meta_bytes": meta},
+        "compress_ms": round(t_c, 4),
+        "decompress_ms": round(t_d, 4),
+        "compress_gbps": round(R / t_c / 1e6, 2),
+        "decompress_gbps": round(R / t_d / 1e6, 2),
+        "ratio_vs_uint8_symbols": round(nsym / wire, 3),
+        "ratio_vs_raw_bf16": round(R / (wire + meta), 3),
+        "bits_per_symbol": round(wire * 8 / nsym, 4),
+        "roofline": None,
+        "cpu_baseline": None,
     }
 
 
@@ -288,9 +432,10 @@ def main() -> int:
 
     import torch
 
-    if args.workload == "connector":
+    if args.workload in ("connector", "config2_ans"):
         torch.cuda.set_device(0)
-        print(json.dumps(bench_connector(args)), flush=True)
+        fn = bench_connector if args.workload == "connector" else bench_entropy
+        print(json.dumps(fn(args)), flush=True)
         return 0
 
     if args.copy_calibration:

@@ -203,18 +203,45 @@ int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  *
  * kvmi_rans_max_bytes: capacity the encoder's `out` must have.
  * kvmi_rans_scratch_bytes: device scratch the encoder needs.
- * kvmi_rans_encode: three launches; the stream length is written to the device u64
+ * kvmi_rans_encode: three launches (encode blocks, scan, compact); the stream length
+ *   is written to the device u64
  *   *out_len (read it after the stream completes).
  * kvmi_rans_decode: one launch; writes ceil(n*bits/8) packed bytes.  A header that
  *   does not name (bits, n) sets KVMI_ERR_BAD_HEADER; a block that does not decode
  *   to its own end state sets KVMI_ERR_CORRUPT.
  */
+typedef struct kvmi_rans_enc_job {
+  const uint8_t* packed; /* n symbols of `bits` bits, LSB-first */
+  int64_t n;
+  uint8_t* out;          /* >= kvmi_rans_max_bytes(n, bits) */
+  int64_t out_capacity;
+  void* scratch;         /* >= kvmi_rans_scratch_bytes(n, bits) */
+  int64_t scratch_bytes;
+  uint64_t* out_len;     /* device u64: stream length */
+} kvmi_rans_enc_job;     /* 56 bytes */
+
+typedef struct kvmi_rans_dec_job {
+  const uint8_t* stream;
+  int64_t in_bytes;
+  int64_t n;
+  uint8_t* packed_out;   /* ceil(n*bits/8) bytes */
+} kvmi_rans_dec_job;     /* 32 bytes */
+
 int64_t kvmi_rans_max_bytes(int64_t n, int32_t bits);
 int64_t kvmi_rans_scratch_bytes(int64_t n, int32_t bits);
 int kvmi_rans_encode(const uint8_t* packed, int64_t n, int32_t bits, uint8_t* out, int64_t out_capacity,
                      void* scratch, int64_t scratch_bytes, uint64_t* out_len, kvmi_stream_t stream);
 int kvmi_rans_decode(const uint8_t* stream_in, int64_t in_bytes, int64_t n, int32_t bits, uint8_t* packed_out,
                      int32_t* err, kvmi_stream_t stream);
+/*
+ * Batched forms: every stream of a request (e.g. the 8-layer chunks of a large
+ * request) coded by one launch per kernel, so that small streams still fill the
+ * GPU.  `jobs` is host memory; all jobs share `bits`.  The single-stream entry
+ * points above are one-job batches.
+ */
+int kvmi_rans_encode_batch(const kvmi_rans_enc_job* jobs, int32_t num_jobs, int32_t bits, kvmi_stream_t stream);
+int kvmi_rans_decode_batch(const kvmi_rans_dec_job* jobs, int32_t num_jobs, int32_t bits, int32_t* err,
+                           kvmi_stream_t stream);
 
 #ifdef __cplusplus
 }

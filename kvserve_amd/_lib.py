@@ -42,6 +42,8 @@ EXPORTS = (
     "kvmi_rans_scratch_bytes",
     "kvmi_rans_encode",
     "kvmi_rans_decode",
+    "kvmi_rans_encode_batch",
+    "kvmi_rans_decode_batch",
 )
 
 
@@ -55,6 +57,17 @@ class Geometry(ctypes.Structure):
         ("max_groups", ctypes.c_int32),
         ("reserved", ctypes.c_int32 * 2),
     ]
+
+
+class RansEncJob(ctypes.Structure):
+    _fields_ = [("packed", ctypes.c_void_p), ("n", ctypes.c_int64), ("out", ctypes.c_void_p),
+                ("out_capacity", ctypes.c_int64), ("scratch", ctypes.c_void_p), ("scratch_bytes", ctypes.c_int64),
+                ("out_len", ctypes.c_void_p)]
+
+
+class RansDecJob(ctypes.Structure):
+    _fields_ = [("stream", ctypes.c_void_p), ("in_bytes", ctypes.c_int64), ("n", ctypes.c_int64),
+                ("packed_out", ctypes.c_void_p)]
 
 
 # kvmi_layer_job: 9 pointers, 3 int64, 2 int32 -> 104 bytes, 8-byte aligned.  It is
@@ -85,6 +98,8 @@ _SIGNATURES = {
     "kvmi_rans_scratch_bytes": ([_i64, _i32], _i64),
     "kvmi_rans_encode": ([_vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp], ctypes.c_int),
     "kvmi_rans_decode": ([_vp, _i64, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
+    "kvmi_rans_encode_batch": ([ctypes.POINTER(RansEncJob), _i32, _i32, _vp], ctypes.c_int),
+    "kvmi_rans_decode_batch": ([ctypes.POINTER(RansDecJob), _i32, _i32, _vp, _vp], ctypes.c_int),
 }
 
 

@@ -360,7 +360,8 @@ class FusedCompressionManager(CompressionManager):
         if self._entropy():
             # the codec stage: rANS over each chunk's packed symbols (the bitpack body)
             per = 2 * H * B * S * D
-            streams = [ops.rans_encode(st[16:], (e - s) * per, bits) for (s, e), st in zip(packet.chunks, streams)]
+            streams = ops.rans_encode_batch([(st[16:], (e - s) * per) for (s, e), st in zip(packet.chunks, streams)],
+                                            bits)
             for m in metas:
                 m["codec_symbol_bits"] = bits
         for m, st in zip(metas, streams):
@@ -403,12 +404,12 @@ class FusedCompressionManager(CompressionManager):
             raise ValueError("packet codec does not match the pipeline")
         if self._entropy():
             # undo the codec stage: each chunk back to its bitpack stream
-            packed = []
+            items, packed = [], []
             for (s, e), st in zip(chunks, streams):
                 n = (e - s) * 2 * H * B * S * D
-                buf = unpack_target(n, bits, device)
-                ops.rans_decode(st.to(device), n, bits, out=buf[16:])
-                packed.append(buf)
+                packed.append(unpack_target(n, bits, device))
+                items.append((st.to(device), n, packed[-1][16:]))
+            ops.rans_decode_batch(items, bits)
             streams = packed
         return Packet(list(streams), chunks, kmeta, vmeta, self.profiles(layer_ids, H), B, S, H, D, bits, seed,
                       transform, layout, layer_ids)

@@ -100,11 +100,43 @@ __device__ __forceinline__ uint32_t sym_at(const uint32_t (&d)[W], int j) {
 
 __device__ __forceinline__ void gst16(uint16_t* p, uint32_t v) { gst(p, (uint16_t)v); }
 
+// ------------------------------------------------------------------ batches
+// Up to kMaxJobs streams per launch, passed by value: one grid covers the blocks of
+// every stream of a request (the streams of an 8-layer-chunked request are coded by
+// one launch per kernel), so small streams still fill the chip.
+constexpr int kMaxJobs = 16;
+
+struct EncBatch {
+  const uint8_t* packed[kMaxJobs];
+  uint8_t* out[kMaxJobs];
+  uint8_t* slots[kMaxJobs];
+  uint32_t* sizes[kMaxJobs];
+  uint64_t* out_len[kMaxJobs];
+  uint64_t n[kMaxJobs];
+  uint32_t first[kMaxJobs + 1];  // first grid block of each job; first[count] = total
+  int32_t count;
+};
+
+struct DecBatch {
+  const uint8_t* in[kMaxJobs];
+  uint8_t* out[kMaxJobs];
+  uint64_t in_bytes[kMaxJobs];
+  uint64_t n[kMaxJobs];
+  uint32_t first[kMaxJobs + 1];
+  int32_t count;
+};
+
+// job of grid block `g` (wave-uniform: kernel arguments live in scalar registers)
+template <class Batch>
+__device__ __forceinline__ int job_of(const Batch& bt, uint32_t g) {
+  int j = 0;
+  while (j + 1 < bt.count && g >= bt.first[j + 1]) ++j;
+  return j;
+}
+
 // ------------------------------------------------------------------ encode
 template <int W>
-__global__ __launch_bounds__(64) void rans_encode_kernel(const uint8_t* __restrict__ in, uint64_t n,
-                                                         uint8_t* __restrict__ slots,
-                                                         uint32_t* __restrict__ sizes) {
+__global__ __launch_bounds__(64) void rans_encode_kernel(const EncBatch bt) {
   using G = RansGeo<W>;
   constexpr bool kPrivate = W <= 5;  // lane-private histogram columns (no LDS contention)
   __shared__ __align__(16) uint32_t hist[kPrivate ? G::A * kLanes : G::A];
@@ -112,24 +144,32 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(const uint8_t* __restri
   __shared__ uint2 tab[G::A];
 
   const uint32_t lane = lane_id();
-  const uint64_t b = blockIdx.x;
+  const int jb = job_of(bt, blockIdx.x);
+  const uint64_t n = bt.n[jb];
+  const uint64_t b = blockIdx.x - bt.first[jb];
   const uint64_t first = b * kBlock;
   const uint32_t nb = (uint32_t)min((uint64_t)kBlock, n - first);
   const bool full = nb == kBlock;
   const uint64_t in_bytes = (n * W + 7) / 8;
-  const uint8_t* blk = in + first * W / 8;
+  const uint8_t* blk = bt.packed[jb] + first * W / 8;
   const uint64_t avail = in_bytes - first * W / 8;
-  uint8_t* slot = slots + b * G::kSlot;
+  uint8_t* slot = bt.slots[jb] + b * G::kSlot;
 
   for (uint32_t i = lane; i < (kPrivate ? G::A * kLanes : G::A); i += kLanes) hist[i] = 0;
   __syncthreads();
-  for (uint32_t r = 0; r < kRuns; ++r) {
-    uint32_t d[W];
-    load_run<W>(blk, avail, r, lane, d);
+  {
+    uint32_t d[W], dn[W];
+    load_run<W>(blk, avail, 0, lane, d);
+    for (uint32_t r = 0; r < kRuns; ++r) {
+      if (r + 1 < kRuns) load_run<W>(blk, avail, r + 1, lane, dn);  // next run in flight
 #pragma unroll
-    for (int j = 0; j < (int)kRun; ++j) {
-      const uint32_t s = sym_at<W>(d, j);
-      if (full || r * (kLanes * kRun) + lane * kRun + j < nb) atomicAdd(&hist[kPrivate ? s * kLanes + lane : s], 1u);
+      for (int j = 0; j < (int)kRun; ++j) {
+        const uint32_t s = sym_at<W>(d, j);
+        if (full || r * (kLanes * kRun) + lane * kRun + j < nb)
+          atomicAdd(&hist[kPrivate ? s * kLanes + lane : s], 1u);
+      }
+#pragma unroll
+      for (int k = 0; k < W; ++k) d[k] = dn[k];
     }
   }
   __syncthreads();
@@ -199,40 +239,46 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(const uint8_t* __restri
   int32_t pos = (int32_t)(G::kRawCap / 2);
   uint32_t x = kStateL;
   bool over = false;
-  for (int r = (int)kRuns - 1; r >= 0 && !over; --r) {
-    uint32_t d[W];
-    load_run<W>(blk, avail, (uint32_t)r, lane, d);
+  {
+    uint32_t d[W], dn[W];
+    load_run<W>(blk, avail, kRuns - 1, lane, d);
+    for (int r = (int)kRuns - 1; r >= 0 && !over; --r) {
+      if (r > 0) load_run<W>(blk, avail, (uint32_t)r - 1, lane, dn);  // next run in flight
 #pragma unroll
-    for (int j = (int)kRun - 1; j >= 0; --j) {
-      const uint32_t s = sym_at<W>(d, j);
-      const bool valid = full || (uint32_t)r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
-      const uint2 e = tab[s];
-      const uint32_t fs = e.x & 0x1fffu;
-      const bool emit = valid && (x >> 20) >= fs;
-      const uint64_t mask = __ballot(emit);
-      pos -= (int32_t)__popcll(mask);
-      if (pos < 0) {
-        over = true;
-        break;
+      for (int j = (int)kRun - 1; j >= 0; --j) {
+        const uint32_t s = sym_at<W>(d, j);
+        const bool valid = full || (uint32_t)r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
+        const uint2 e = tab[s];
+        const uint32_t fs = e.x & 0x1fffu;
+        const bool emit = valid && (x >> 20) >= fs;
+        const uint64_t mask = __ballot(emit);
+        pos -= (int32_t)__popcll(mask);
+        if (pos < 0) {
+          over = true;
+          break;
+        }
+        if (emit) {
+          gst16(words + pos + rank_in(mask), x & 0xffffu);
+          x >>= 16;
+        }
+        if (valid) {
+          const uint32_t t1 = __umulhi(e.y, x);
+          const uint32_t q = (t1 + ((x - t1) >> ((e.x >> 25) & 1u))) >> (e.x >> 26);
+          x = (q << kPB) + (x - q * fs) + ((e.x >> 13) & 0xfffu);
+        }
       }
-      if (emit) {
-        gst16(words + pos + rank_in(mask), x & 0xffffu);
-        x >>= 16;
-      }
-      if (valid) {
-        const uint32_t t1 = __umulhi(e.y, x);
-        const uint32_t q = (t1 + ((x - t1) >> ((e.x >> 25) & 1u))) >> (e.x >> 26);
-        x = (q << kPB) + (x - q * fs) + ((e.x >> 13) & 0xfffu);
-      }
+#pragma unroll
+      for (int k = 0; k < W; ++k) d[k] = dn[k];
     }
   }
   const uint32_t count = G::kRawCap / 2 - (uint32_t)pos;
   const uint64_t raw = 4u + pad4(((uint64_t)nb * W + 7) / 8);
   const uint64_t size = G::kHead + pad4(2ull * count);
+  uint32_t* sizes = bt.sizes[jb];
   if (over || size >= raw) {
     if (lane == 0) {
       gst(reinterpret_cast<uint32_t*>(slot), 1u);
-      sizes[b] = (uint32_t)raw;
+      gst(sizes + b, (uint32_t)raw);
     }
     return;
   }
@@ -240,21 +286,25 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(const uint8_t* __restri
   if (lane == 0) {
     gst(reinterpret_cast<uint32_t*>(slot), count << 1);
     if (count & 1u) gst16(words + pos - 1, 0u);
-    sizes[b] = (uint32_t)size;
+    gst(sizes + b, (uint32_t)size);
   }
 }
 
 // ------------------------------------------------------------------ scan + header
-__global__ __launch_bounds__(kScanThreads) void rans_scan_kernel(const uint32_t* __restrict__ sizes,
-                                                                 uint32_t nblk, uint64_t n, int w,
-                                                                 uint8_t* __restrict__ out,
-                                                                 uint64_t* __restrict__ out_len) {
+// One workgroup per stream: exclusive block offsets, header, stream length.
+template <int W>
+__global__ __launch_bounds__(kScanThreads) void rans_scan_kernel(const EncBatch bt) {
   __shared__ uint64_t part[kScanThreads];
+  const int jb = blockIdx.x;
+  const uint64_t n = bt.n[jb];
+  const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
+  const uint32_t* sizes = bt.sizes[jb];
+  uint8_t* out = bt.out[jb];
   const uint32_t t = threadIdx.x;
   const uint32_t per = (nblk + kScanThreads - 1) / kScanThreads;
   const uint32_t lo = min(nblk, t * per), hi = min(nblk, lo + per);
   uint64_t s = 0;
-  for (uint32_t i = lo; i < hi; ++i) s += sizes[i];
+  for (uint32_t i = lo; i < hi; ++i) s += gld(sizes + i);
   part[t] = s;
   __syncthreads();
   for (int o = 1; o < kScanThreads; o <<= 1) {
@@ -267,38 +317,40 @@ __global__ __launch_bounds__(kScanThreads) void rans_scan_kernel(const uint32_t*
   uint64_t* offs = reinterpret_cast<uint64_t*>(out + 32);
   for (uint32_t i = lo; i < hi; ++i) {
     gst(offs + i, off);
-    off += sizes[i];
+    off += gld(sizes + i);
   }
   if (t == kScanThreads - 1) {
     const uint64_t payload = part[t];
     uint32_t* h = reinterpret_cast<uint32_t*>(out);
     gst(h + 0, kRansMagic);
-    gst(h + 1, 1u | ((uint32_t)w << 8) | (kPB << 16) | (6u << 24));
+    gst(h + 1, 1u | ((uint32_t)W << 8) | (kPB << 16) | (6u << 24));
     gst(h + 2, kBlock);
     gst(h + 3, nblk);
     gst(reinterpret_cast<uint64_t*>(out + 16), n);
     gst(reinterpret_cast<uint64_t*>(out + 24), payload);
-    gst(out_len, (uint64_t)(32u + 8ull * nblk + payload));
+    gst(bt.out_len[jb], (uint64_t)(32u + 8ull * nblk + payload));
   }
 }
 
 // ------------------------------------------------------------------ compaction
 template <int W>
-__global__ __launch_bounds__(kCopyThreads) void rans_compact_kernel(const uint8_t* __restrict__ in, uint64_t n,
-                                                                    const uint8_t* __restrict__ slots,
-                                                                    uint32_t nblk, uint8_t* __restrict__ out) {
+__global__ __launch_bounds__(kCopyThreads) void rans_compact_kernel(const EncBatch bt) {
   using G = RansGeo<W>;
-  const uint64_t b = blockIdx.x;
+  const int jb = job_of(bt, blockIdx.x);
+  const uint64_t n = bt.n[jb];
+  const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
+  const uint64_t b = blockIdx.x - bt.first[jb];
+  uint8_t* out = bt.out[jb];
   const uint64_t off = gld(reinterpret_cast<const uint64_t*>(out + 32) + b);
   uint32_t* dst = reinterpret_cast<uint32_t*>(out + 32 + 8ull * nblk + off);
-  const uint8_t* slot = slots + b * G::kSlot;
+  const uint8_t* slot = bt.slots[jb] + b * G::kSlot;
   const uint32_t tag = gld(reinterpret_cast<const uint32_t*>(slot));
   const uint32_t t = threadIdx.x;
   if (tag & 1u) {
     const uint64_t first = b * kBlock;
     const uint32_t nb = (uint32_t)min((uint64_t)kBlock, n - first);
     const uint64_t rb = ((uint64_t)nb * W + 7) / 8;
-    const uint8_t* src = in + first * W / 8;
+    const uint8_t* src = bt.packed[jb] + first * W / 8;
     const uint64_t avail = (n * W + 7) / 8 - first * W / 8;
     if (t == 0) gst(dst, 1u);
     for (uint64_t i = t; i < pad4(rb) / 4; i += kCopyThreads) {
@@ -323,17 +375,27 @@ __global__ __launch_bounds__(kCopyThreads) void rans_compact_kernel(const uint8_
 }
 
 // ------------------------------------------------------------------ decode
+// The block's words are staged through a per-wave LDS ring of kRing 16-bit words,
+// refilled 256 words at a time (two coalesced dword loads per lane) whenever fewer
+// than 128 unread words remain, so a step reads its words from LDS instead of
+// waiting on a dependent global load.
+constexpr uint32_t kRing = 512;
+constexpr uint32_t kRefill = 256;
+
 template <int W>
-__global__ __launch_bounds__(64) void rans_decode_kernel(const uint8_t* __restrict__ in, uint64_t in_bytes,
-                                                         uint64_t n, uint8_t* __restrict__ out,
-                                                         int32_t* __restrict__ err) {
+__global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int32_t* __restrict__ err) {
   using G = RansGeo<W>;
   __shared__ uint8_t slot_sym[kM];
   __shared__ uint32_t sym_fc[G::A];
   __shared__ uint32_t fq[G::A];
+  __shared__ __align__(16) uint16_t ring[kRing];
 
   const uint32_t lane = lane_id();
-  const uint64_t b = blockIdx.x;
+  const int jb = job_of(bt, blockIdx.x);
+  const uint64_t n = bt.n[jb];
+  const uint64_t b = blockIdx.x - bt.first[jb];
+  const uint8_t* in = bt.in[jb];
+  const uint64_t in_bytes = bt.in_bytes[jb];
   const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
   const uint32_t* h = reinterpret_cast<const uint32_t*>(in);
   const uint64_t payload = gld(reinterpret_cast<const uint64_t*>(in + 24));
@@ -356,7 +418,7 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const uint8_t* __restri
   const uint64_t first = b * kBlock;
   const uint32_t nb = (uint32_t)min((uint64_t)kBlock, n - first);
   const uint64_t out_bytes = (n * W + 7) / 8;
-  uint8_t* dst = out + first * W / 8;
+  uint8_t* dst = bt.out[jb] + first * W / 8;
   const uint64_t room = out_bytes - first * W / 8;
 
   if (tag & 1u) {
@@ -421,19 +483,41 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const uint8_t* __restri
       slot_sym[s] = (uint8_t)v;
     }
   }
-  __syncthreads();
 
   uint32_t x = gld(reinterpret_cast<const uint32_t*>(blk + 4 + G::kTab) + lane);
-  const uint16_t* words = reinterpret_cast<const uint16_t*>(blk + G::kHead + (pad4(2ull * count) - 2ull * count));
-  uint32_t p = 0;
+  // word region: pad4(2 count) bytes, the words at its end; q counts 16-bit units
+  // from the region start, word p of the block is unit q = lead + p
+  const uint32_t* region = reinterpret_cast<const uint32_t*>(blk + G::kHead);
+  const uint32_t lead = (uint32_t)(pad4(2ull * count) / 2 - count);
+  const uint32_t units = (uint32_t)(pad4(2ull * count) / 2);
+  uint32_t q = lead;       // next unit to consume
+  uint32_t filled = 0;     // units [0, filled) have been staged (aligned to 4 units)
   bool bad = false;
   const bool full = nb == kBlock;
+
+  auto refill = [&]() {
+    while (filled < units && filled < q + kRefill / 2) {  // (q may start one unit past filled)
+      // lane l stages units [filled + 4 l, filled + 4 l + 4): two dwords
+      const uint32_t u = filled + 4u * lane;
+      uint32_t w0 = 0, w1 = 0;
+      if (u < units) w0 = gld(region + u / 2);
+      if (u + 2 < units) w1 = gld(region + u / 2 + 1);
+      uint32_t* rp = reinterpret_cast<uint32_t*>(ring + (u & (kRing - 1)));
+      rp[0] = w0;
+      rp[1] = w1;
+      filled += kRefill;
+    }
+    __syncthreads();
+  };
+  refill();
+
   for (uint32_t r = 0; r < kRuns; ++r) {
     uint32_t acc[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) acc[k] = 0;
 #pragma unroll
     for (int j = 0; j < (int)kRun; ++j) {
+      if (filled < q + kLanes && filled < units) refill();
       const bool valid = full || r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
       const uint32_t slot = x & (kM - 1u);
       const uint32_t s = slot_sym[slot];
@@ -442,12 +526,12 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const uint8_t* __restri
       const bool need = valid && y < kStateL;
       const uint64_t mask = __ballot(need);
       const uint32_t k = (uint32_t)__popcll(mask);
-      if (p + k > count) {
+      if (q + k > units) {
         bad = true;
         break;
       }
-      if (need) y = (y << 16) | (uint32_t)gld(words + p + rank_in(mask));
-      p += k;
+      if (need) y = (y << 16) | (uint32_t)ring[(q + rank_in(mask)) & (kRing - 1)];
+      q += k;
       if (valid) {
         x = y;
         const int bit = j * W, kk = bit >> 5, sh = bit & 31;
@@ -463,37 +547,28 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const uint8_t* __restri
       if (at + 4 <= room) {
         gst(reinterpret_cast<uint32_t*>(dst + at), acc[k]);
       } else {
-        for (int q = 0; q < 4; ++q)
-          if (at + q < room) gst(dst + at + q, (uint8_t)(acc[k] >> (8 * q)));
+        for (int qq = 0; qq < 4; ++qq)
+          if (at + qq < room) gst(dst + at + qq, (uint8_t)(acc[k] >> (8 * qq)));
       }
     }
   }
-  const bool ok = !bad && p == count && x == kStateL;
+  const bool ok = !bad && q == units && x == kStateL;
   if (__ballot(!ok) && lane == 0) atomicOr(err, KVMI_ERR_CORRUPT);
 }
 
 template <int W>
-int rans_encode_w(const uint8_t* in, int64_t n, uint8_t* out, void* scratch, uint64_t* out_len,
-                  hipStream_t stream) {
-  using G = RansGeo<W>;
-  const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
-  uint8_t* slots = static_cast<uint8_t*>(scratch);
-  uint32_t* sizes = reinterpret_cast<uint32_t*>(slots + (uint64_t)nblk * G::kSlot);
-  if (nblk) hipLaunchKernelGGL(rans_encode_kernel<W>, dim3(nblk), dim3(64), 0, stream, in, (uint64_t)n, slots, sizes);
-  hipLaunchKernelGGL(rans_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, sizes, nblk, (uint64_t)n, W, out,
-                     out_len);
-  if (nblk)
-    hipLaunchKernelGGL(rans_compact_kernel<W>, dim3(nblk), dim3(kCopyThreads), 0, stream, in, (uint64_t)n, slots,
-                       nblk, out);
+int rans_encode_w(const EncBatch& bt, hipStream_t stream) {
+  const uint32_t total = bt.first[bt.count];
+  if (total) hipLaunchKernelGGL(rans_encode_kernel<W>, dim3(total), dim3(64), 0, stream, bt);
+  hipLaunchKernelGGL(rans_scan_kernel<W>, dim3(bt.count), dim3(kScanThreads), 0, stream, bt);
+  if (total) hipLaunchKernelGGL(rans_compact_kernel<W>, dim3(total), dim3(kCopyThreads), 0, stream, bt);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
 template <int W>
-int rans_decode_w(const uint8_t* in, int64_t in_bytes, int64_t n, uint8_t* out, int32_t* err, hipStream_t stream) {
-  const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
-  if (nblk)
-    hipLaunchKernelGGL(rans_decode_kernel<W>, dim3(nblk), dim3(64), 0, stream, in, (uint64_t)in_bytes, (uint64_t)n,
-                       out, err);
+int rans_decode_w(const DecBatch& bt, int32_t* err, hipStream_t stream) {
+  const uint32_t total = bt.first[bt.count];
+  if (total) hipLaunchKernelGGL(rans_decode_kernel<W>, dim3(total), dim3(64), 0, stream, bt, err);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
@@ -519,42 +594,104 @@ extern "C" int64_t kvmi_rans_scratch_bytes(int64_t n, int32_t bits) {
   return (int64_t)(nblk * slot_bytes(bits) + 4u * nblk);
 }
 
+static bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) != 0; }
+
+extern "C" int kvmi_rans_encode_batch(const kvmi_rans_enc_job* jobs, int32_t num_jobs, int32_t bits,
+                                      kvmi_stream_t stream) {
+  if (num_jobs < 0 || bits < 1 || bits > 8 || (num_jobs > 0 && !jobs)) return KVMI_EINVAL;
+  for (int32_t i = 0; i < num_jobs; ++i) {
+    const kvmi_rans_enc_job& j = jobs[i];
+    if (j.n < 0 || !j.out || !j.out_len || (j.n > 0 && (!j.packed || !j.scratch))) return KVMI_EINVAL;
+    if (j.out_capacity < kvmi_rans_max_bytes(j.n, bits) || j.scratch_bytes < kvmi_rans_scratch_bytes(j.n, bits))
+      return KVMI_EINVAL;
+    if (misaligned(j.packed) || misaligned(j.out) || misaligned(j.scratch) || misaligned(j.out_len))
+      return KVMI_EINVAL;
+    if ((uint64_t)j.n > (uint64_t)kBlock * 0x7fffffffull) return KVMI_EINVAL;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int32_t base = 0; base < num_jobs; base += kMaxJobs) {
+    EncBatch bt{};
+    bt.count = min(kMaxJobs, num_jobs - base);
+    uint64_t total = 0;
+    for (int i = 0; i < bt.count; ++i) {
+      const kvmi_rans_enc_job& j = jobs[base + i];
+      const uint64_t nblk = ((uint64_t)j.n + kBlock - 1) / kBlock;
+      bt.packed[i] = j.packed;
+      bt.out[i] = j.out;
+      bt.slots[i] = static_cast<uint8_t*>(j.scratch);
+      bt.sizes[i] = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(j.scratch) + nblk * slot_bytes(bits));
+      bt.out_len[i] = j.out_len;
+      bt.n[i] = (uint64_t)j.n;
+      bt.first[i] = (uint32_t)total;
+      total += nblk;
+    }
+    if (total > 0x7fffffffull) return KVMI_EINVAL;
+    bt.first[bt.count] = (uint32_t)total;
+    int rc;
+    switch (bits) {
+      case 1: rc = rans_encode_w<1>(bt, s); break;
+      case 2: rc = rans_encode_w<2>(bt, s); break;
+      case 3: rc = rans_encode_w<3>(bt, s); break;
+      case 4: rc = rans_encode_w<4>(bt, s); break;
+      case 5: rc = rans_encode_w<5>(bt, s); break;
+      case 6: rc = rans_encode_w<6>(bt, s); break;
+      case 7: rc = rans_encode_w<7>(bt, s); break;
+      default: rc = rans_encode_w<8>(bt, s); break;
+    }
+    if (rc != KVMI_OK) return rc;
+  }
+  return KVMI_OK;
+}
+
+extern "C" int kvmi_rans_decode_batch(const kvmi_rans_dec_job* jobs, int32_t num_jobs, int32_t bits, int32_t* err,
+                                      kvmi_stream_t stream) {
+  if (num_jobs < 0 || bits < 1 || bits > 8 || !err || (num_jobs > 0 && !jobs)) return KVMI_EINVAL;
+  for (int32_t i = 0; i < num_jobs; ++i) {
+    const kvmi_rans_dec_job& j = jobs[i];
+    if (j.n < 0 || !j.stream || (j.n > 0 && !j.packed_out) || j.in_bytes < 32) return KVMI_EINVAL;
+    if (misaligned(j.stream) || misaligned(j.packed_out)) return KVMI_EINVAL;
+    if ((uint64_t)j.n > (uint64_t)kBlock * 0x7fffffffull) return KVMI_EINVAL;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int32_t base = 0; base < num_jobs; base += kMaxJobs) {
+    DecBatch bt{};
+    bt.count = min(kMaxJobs, num_jobs - base);
+    uint64_t total = 0;
+    for (int i = 0; i < bt.count; ++i) {
+      const kvmi_rans_dec_job& j = jobs[base + i];
+      bt.in[i] = j.stream;
+      bt.out[i] = j.packed_out;
+      bt.in_bytes[i] = (uint64_t)j.in_bytes;
+      bt.n[i] = (uint64_t)j.n;
+      bt.first[i] = (uint32_t)total;
+      total += ((uint64_t)j.n + kBlock - 1) / kBlock;
+    }
+    if (total > 0x7fffffffull) return KVMI_EINVAL;
+    bt.first[bt.count] = (uint32_t)total;
+    int rc;
+    switch (bits) {
+      case 1: rc = rans_decode_w<1>(bt, err, s); break;
+      case 2: rc = rans_decode_w<2>(bt, err, s); break;
+      case 3: rc = rans_decode_w<3>(bt, err, s); break;
+      case 4: rc = rans_decode_w<4>(bt, err, s); break;
+      case 5: rc = rans_decode_w<5>(bt, err, s); break;
+      case 6: rc = rans_decode_w<6>(bt, err, s); break;
+      case 7: rc = rans_decode_w<7>(bt, err, s); break;
+      default: rc = rans_decode_w<8>(bt, err, s); break;
+    }
+    if (rc != KVMI_OK) return rc;
+  }
+  return KVMI_OK;
+}
+
 extern "C" int kvmi_rans_encode(const uint8_t* packed, int64_t n, int32_t bits, uint8_t* out, int64_t out_capacity,
                                 void* scratch, int64_t scratch_bytes, uint64_t* out_len, kvmi_stream_t stream) {
-  if (n < 0 || bits < 1 || bits > 8 || !out || !out_len || (n > 0 && (!packed || !scratch))) return KVMI_EINVAL;
-  if (out_capacity < kvmi_rans_max_bytes(n, bits) || scratch_bytes < kvmi_rans_scratch_bytes(n, bits))
-    return KVMI_EINVAL;
-  if ((reinterpret_cast<uintptr_t>(packed) | reinterpret_cast<uintptr_t>(out) |
-       reinterpret_cast<uintptr_t>(scratch) | reinterpret_cast<uintptr_t>(out_len)) & 7u)
-    return KVMI_EINVAL;
-  if ((uint64_t)n > (uint64_t)kBlock * 0xffffffffull) return KVMI_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (bits) {
-    case 1: return rans_encode_w<1>(packed, n, out, scratch, out_len, s);
-    case 2: return rans_encode_w<2>(packed, n, out, scratch, out_len, s);
-    case 3: return rans_encode_w<3>(packed, n, out, scratch, out_len, s);
-    case 4: return rans_encode_w<4>(packed, n, out, scratch, out_len, s);
-    case 5: return rans_encode_w<5>(packed, n, out, scratch, out_len, s);
-    case 6: return rans_encode_w<6>(packed, n, out, scratch, out_len, s);
-    case 7: return rans_encode_w<7>(packed, n, out, scratch, out_len, s);
-    default: return rans_encode_w<8>(packed, n, out, scratch, out_len, s);
-  }
+  const kvmi_rans_enc_job j{packed, n, out, out_capacity, scratch, scratch_bytes, out_len};
+  return kvmi_rans_encode_batch(&j, 1, bits, stream);
 }
 
 extern "C" int kvmi_rans_decode(const uint8_t* stream_in, int64_t in_bytes, int64_t n, int32_t bits,
                                 uint8_t* packed_out, int32_t* err, kvmi_stream_t stream) {
-  if (n < 0 || bits < 1 || bits > 8 || !stream_in || !err || (n > 0 && !packed_out)) return KVMI_EINVAL;
-  if ((reinterpret_cast<uintptr_t>(stream_in) | reinterpret_cast<uintptr_t>(packed_out)) & 7u) return KVMI_EINVAL;
-  if (in_bytes < 32) return KVMI_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (bits) {
-    case 1: return rans_decode_w<1>(stream_in, in_bytes, n, packed_out, err, s);
-    case 2: return rans_decode_w<2>(stream_in, in_bytes, n, packed_out, err, s);
-    case 3: return rans_decode_w<3>(stream_in, in_bytes, n, packed_out, err, s);
-    case 4: return rans_decode_w<4>(stream_in, in_bytes, n, packed_out, err, s);
-    case 5: return rans_decode_w<5>(stream_in, in_bytes, n, packed_out, err, s);
-    case 6: return rans_decode_w<6>(stream_in, in_bytes, n, packed_out, err, s);
-    case 7: return rans_decode_w<7>(stream_in, in_bytes, n, packed_out, err, s);
-    default: return rans_decode_w<8>(stream_in, in_bytes, n, packed_out, err, s);
-  }
+  const kvmi_rans_dec_job j{stream_in, in_bytes, n, packed_out};
+  return kvmi_rans_decode_batch(&j, 1, bits, err, stream);
 }

@@ -167,50 +167,84 @@ def _aligned8(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 8 == 0 else t.clone()
 
 
-def rans_encode(packed: torch.Tensor, n: int, bits: int) -> torch.Tensor:
-    """Entropy-code n symbols of `bits` bits packed LSB-first (a bitpack body) into
-    this engine's rANS stream -- the codec stage's nvCOMP ANS encode
-    (nvcomp_func.py:54-95).  Synchronizes once to learn the stream length; returns a
-    view of the stream's bytes."""
-    if packed.dtype != torch.uint8 or packed.dim() != 1 or not packed.is_cuda:
-        raise TypeError("rans_encode takes a 1-D uint8 CUDA tensor")
-    n, bits = int(n), _bits(bits)
-    if packed.numel() < (n * bits + 7) // 8:
-        raise ValueError("packed buffer is shorter than n symbols of this width")
+def rans_encode_batch(items: Sequence[tuple], bits: int) -> list:
+    """Entropy-code several packed symbol buffers [(packed, n), ...] of one width in one
+    launch per kernel -- the codec stage's nvCOMP ANS encode (nvcomp_func.py:54-95)
+    for every stream of a request.  Synchronizes once to learn the stream lengths;
+    returns views of the streams' bytes."""
+    bits = _bits(bits)
     lib = _lib.load()
-    cap, scr = int(lib.kvmi_rans_max_bytes(n, bits)), int(lib.kvmi_rans_scratch_bytes(n, bits))
-    if cap < 0 or scr < 0:
-        raise ValueError("invalid rANS size or width")
-    dev = packed.device
-    src = _aligned8(packed.contiguous())
-    out = torch.empty((cap + 7) // 8 * 8, dtype=torch.uint8, device=dev)
-    scratch = torch.empty(max(scr, 8), dtype=torch.uint8, device=dev)
-    length = torch.empty(1, dtype=torch.int64, device=dev)
+    jobs = (_lib.RansEncJob * max(1, len(items)))()
+    keep = []
+    for i, (packed, n) in enumerate(items):
+        if packed.dtype != torch.uint8 or packed.dim() != 1 or not packed.is_cuda:
+            raise TypeError("rans_encode takes 1-D uint8 CUDA tensors")
+        n = int(n)
+        if packed.numel() < (n * bits + 7) // 8:
+            raise ValueError("packed buffer is shorter than n symbols of this width")
+        cap, scr = int(lib.kvmi_rans_max_bytes(n, bits)), int(lib.kvmi_rans_scratch_bytes(n, bits))
+        if cap < 0 or scr < 0:
+            raise ValueError("invalid rANS size or width")
+        dev = packed.device
+        src = _aligned8(packed.contiguous())
+        out = torch.empty((cap + 7) // 8 * 8, dtype=torch.uint8, device=dev)
+        scratch = torch.empty(max(scr, 8), dtype=torch.uint8, device=dev)
+        length = torch.empty(1, dtype=torch.int64, device=dev)
+        jobs[i] = _lib.RansEncJob(src.data_ptr() if n else None, n, out.data_ptr(), out.numel(), scratch.data_ptr(),
+                                  scratch.numel(), length.data_ptr())
+        keep.append((src, out, scratch, length))
+    if not items:
+        return []
+    devs = {k[1].device for k in keep}
+    if len(devs) != 1:
+        raise ValueError("one rANS batch runs on one device")
+    with torch.cuda.device(keep[0][1].device):
+        _lib.check(lib.kvmi_rans_encode_batch(jobs, len(items), bits, _stream()), "kvmi_rans_encode_batch")
+    lengths = torch.cat([k[3] for k in keep]).tolist()
+    return [k[1][:int(n)] for k, n in zip(keep, lengths)]
+
+
+def rans_encode(packed: torch.Tensor, n: int, bits: int) -> torch.Tensor:
+    """One stream of rans_encode_batch."""
+    return rans_encode_batch([(packed, n)], bits)[0]
+
+
+def rans_decode_batch(items: Sequence[tuple], bits: int, check: Optional[bool] = None) -> list:
+    """Inverse of rans_encode_batch for [(stream, n[, out]), ...] in one launch: the
+    ceil(n*bits/8) packed bytes of each stream (into `out`, an 8-byte aligned uint8
+    tensor of at least that size, when given) -- the codec stage's nvCOMP ANS decode
+    (nvcomp_func.py:97-143)."""
+    bits = _bits(bits)
+    jobs = (_lib.RansDecJob * max(1, len(items)))()
+    outs, keep = [], []
+    for i, item in enumerate(items):
+        stream, n = item[0], int(item[1])
+        out = item[2] if len(item) > 2 else None
+        if stream.dtype != torch.uint8 or stream.dim() != 1 or not stream.is_cuda:
+            raise TypeError("rans_decode takes 1-D uint8 CUDA tensors")
+        if stream.numel() < 32:
+            raise ValueError("rANS stream is shorter than its header")
+        nbytes = (n * bits + 7) // 8
+        if out is None:
+            out = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=stream.device)[:nbytes]
+        elif out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < nbytes or out.data_ptr() % 8:
+            raise ValueError("out must be a contiguous, 8-byte aligned uint8 tensor of ceil(n*bits/8) bytes")
+        src = _aligned8(stream.contiguous())
+        jobs[i] = _lib.RansDecJob(src.data_ptr(), src.numel(), n, out.data_ptr())
+        keep.append(src)
+        outs.append(out)
+    if not items:
+        return []
+    dev = keep[0].device
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
-        _lib.check(lib.kvmi_rans_encode(src.data_ptr(), n, bits, out.data_ptr(), out.numel(), scratch.data_ptr(),
-                                        scratch.numel(), length.data_ptr(), _stream()), "kvmi_rans_encode")
-    return out[: int(length.item())]
+        _lib.check(_lib.load().kvmi_rans_decode_batch(jobs, len(items), bits, err.data_ptr(), _stream()),
+                   "kvmi_rans_decode_batch")
+    _maybe_check(err, check)
+    return outs
 
 
 def rans_decode(stream: torch.Tensor, n: int, bits: int, out: Optional[torch.Tensor] = None,
                 check: Optional[bool] = None) -> torch.Tensor:
-    """Inverse of rans_encode: ceil(n*bits/8) packed bytes (into `out`, an 8-byte
-    aligned uint8 tensor of at least that size, when given) -- the codec stage's
-    nvCOMP ANS decode (nvcomp_func.py:97-143)."""
-    if stream.dtype != torch.uint8 or stream.dim() != 1 or not stream.is_cuda:
-        raise TypeError("rans_decode takes a 1-D uint8 CUDA tensor")
-    n, bits = int(n), _bits(bits)
-    if stream.numel() < 32:
-        raise ValueError("rANS stream is shorter than its header")
-    nbytes = (n * bits + 7) // 8
-    if out is None:
-        out = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=stream.device)[:nbytes]
-    elif out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < nbytes or out.data_ptr() % 8:
-        raise ValueError("out must be a contiguous, 8-byte aligned uint8 tensor of ceil(n*bits/8) bytes")
-    src = _aligned8(stream.contiguous())
-    err = torch.zeros(1, dtype=torch.int32, device=stream.device)
-    with torch.cuda.device(stream.device):
-        _lib.check(_lib.load().kvmi_rans_decode(src.data_ptr(), src.numel(), n, bits, out.data_ptr(), err.data_ptr(),
-                                                _stream()), "kvmi_rans_decode")
-    _maybe_check(err, check)
-    return out
+    """One stream of rans_decode_batch."""
+    return rans_decode_batch([(stream, n) if out is None else (stream, n, out)], bits, check)[0]

@@ -104,3 +104,23 @@ def test_damage_is_reported(cuda):
     bad[head + 4] ^= 0x01                            # frequency table no longer sums to 4096
     with pytest.raises(RuntimeError, match="corrupt entropy-coded stream"):
         ops.rans_decode(bad, n, w)
+
+
+@pytest.mark.parametrize("w", [3, 4, 8])
+def test_batch_of_streams_equals_oracle(cuda, w):
+    """Streams of different lengths and statistics coded by one batched launch (more
+    than one launch group of 16) equal the oracle stream by stream and decode back in
+    one batched launch."""
+    rng = np.random.default_rng(40 + w)
+    sizes = [0, 1, 65536, 65537, 3 * 65536 + 5, 2047] + [int(rng.integers(1, 300000)) for _ in range(13)]
+    kinds = ["skewed", "mixed", "uniform", "single"]
+    syms = [_symbols(rng, n, w, kinds[i % 4]) for i, n in enumerate(sizes)]
+    bodies = [crans.pack(s, w) for s in syms]
+    items = [(torch.from_numpy(b.copy()).to(cuda) if b.size else torch.empty(0, dtype=torch.uint8, device=cuda), s.size)
+             for b, s in zip(bodies, syms)]
+    streams = ops.rans_encode_batch(items, w)
+    for st, b, s in zip(streams, bodies, syms):
+        assert np.array_equal(st.cpu().numpy(), crans.encode_packed(b, s.size, w))
+    outs = ops.rans_decode_batch([(st, s.size) for st, s in zip(streams, syms)], w)
+    for o, b in zip(outs, bodies):
+        assert np.array_equal(o.cpu().numpy(), b)
