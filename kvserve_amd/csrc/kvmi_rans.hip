@@ -47,7 +47,8 @@ struct RansGeo {
   static constexpr uint32_t kTab = (uint32_t)pad4(2u * A);       // u16 frequency table
   static constexpr uint32_t kHead = 4u + kTab + 4u * kLanes;     // tag, table, states
   static constexpr uint32_t kRawCap = kBlock * W / 8;            // packed bytes of a full block
-  static constexpr uint32_t kSlot = kHead + kRawCap;             // scratch bytes per block
+  static constexpr uint32_t kGuard = 2u * kLanes * kRun;         // one run of words past the capacity
+  static constexpr uint32_t kSlot = kHead + kGuard + kRawCap;    // scratch bytes per block
   static constexpr uint32_t kPerLane = A > kLanes ? A / kLanes : 1;
 };
 
@@ -135,6 +136,40 @@ __device__ __forceinline__ int job_of(const Batch& bt, uint32_t g) {
 }
 
 // ------------------------------------------------------------------ encode
+// Steps 1023..0 of one block (FULL: every lane has a symbol at every step).  Leaves
+// pos < 0 when the words outgrow the capacity (the block is then stored raw).
+template <int W, bool FULL>
+__device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, uint32_t lane, uint32_t nb,
+                                            const uint2* tab, uint16_t* words, int32_t& pos, uint32_t& x) {
+  uint32_t d[W], dn[W];
+  load_run<W>(blk, avail, kRuns - 1, lane, d);
+  for (int r = (int)kRuns - 1; r >= 0; --r) {
+    if (r > 0) load_run<W>(blk, avail, (uint32_t)r - 1, lane, dn);  // next run in flight
+#pragma unroll
+    for (int j = (int)kRun - 1; j >= 0; --j) {
+      const uint32_t s = sym_at<W>(d, j);
+      const bool valid = FULL || (uint32_t)r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
+      const uint2 e = tab[s];
+      const uint32_t fs = e.x & 0x1fffu;
+      const bool emit = valid && (x >> 20) >= fs;
+      const uint64_t mask = __ballot(emit);
+      pos -= (int32_t)__popcll(mask);
+      if (emit) {
+        gst16(words + pos + (int32_t)rank_in(mask), x & 0xffffu);
+        x >>= 16;
+      }
+      if (valid) {
+        const uint32_t t1 = __umulhi(e.y, x);
+        const uint32_t q = (t1 + ((x - t1) >> ((e.x >> 25) & 1u))) >> (e.x >> 26);
+        x = (q << kPB) + (x - q * fs) + ((e.x >> 13) & 0xfffu);
+      }
+    }
+    if (pos < 0) return;
+#pragma unroll
+    for (int k = 0; k < W; ++k) d[k] = dn[k];
+  }
+}
+
 template <int W>
 __global__ __launch_bounds__(64) void rans_encode_kernel(const EncBatch bt) {
   using G = RansGeo<W>;
@@ -234,43 +269,15 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(const EncBatch bt) {
   }
   __syncthreads();
 
-  // encode, steps 1023..0; words fill the slot's word region from its end
-  uint16_t* words = reinterpret_cast<uint16_t*>(slot + G::kHead);
+  // encode, steps 1023..0; words fill the slot's word region from its end.  The
+  // capacity is checked once per run: a run emits at most 64 * 32 words, which the
+  // guard region in front of the word region absorbs.
+  uint16_t* words = reinterpret_cast<uint16_t*>(slot + G::kHead + G::kGuard);
   int32_t pos = (int32_t)(G::kRawCap / 2);
   uint32_t x = kStateL;
-  bool over = false;
-  {
-    uint32_t d[W], dn[W];
-    load_run<W>(blk, avail, kRuns - 1, lane, d);
-    for (int r = (int)kRuns - 1; r >= 0 && !over; --r) {
-      if (r > 0) load_run<W>(blk, avail, (uint32_t)r - 1, lane, dn);  // next run in flight
-#pragma unroll
-      for (int j = (int)kRun - 1; j >= 0; --j) {
-        const uint32_t s = sym_at<W>(d, j);
-        const bool valid = full || (uint32_t)r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
-        const uint2 e = tab[s];
-        const uint32_t fs = e.x & 0x1fffu;
-        const bool emit = valid && (x >> 20) >= fs;
-        const uint64_t mask = __ballot(emit);
-        pos -= (int32_t)__popcll(mask);
-        if (pos < 0) {
-          over = true;
-          break;
-        }
-        if (emit) {
-          gst16(words + pos + rank_in(mask), x & 0xffffu);
-          x >>= 16;
-        }
-        if (valid) {
-          const uint32_t t1 = __umulhi(e.y, x);
-          const uint32_t q = (t1 + ((x - t1) >> ((e.x >> 25) & 1u))) >> (e.x >> 26);
-          x = (q << kPB) + (x - q * fs) + ((e.x >> 13) & 0xfffu);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < W; ++k) d[k] = dn[k];
-    }
-  }
+  if (full) encode_runs<W, true>(blk, avail, lane, nb, tab, words, pos, x);
+  else encode_runs<W, false>(blk, avail, lane, nb, tab, words, pos, x);
+  const bool over = pos < 0;
   const uint32_t count = G::kRawCap / 2 - (uint32_t)pos;
   const uint64_t raw = 4u + pad4(((uint64_t)nb * W + 7) / 8);
   const uint64_t size = G::kHead + pad4(2ull * count);
@@ -375,12 +382,84 @@ __global__ __launch_bounds__(kCopyThreads) void rans_compact_kernel(const EncBat
 }
 
 // ------------------------------------------------------------------ decode
-// The block's words are staged through a per-wave LDS ring of kRing 16-bit words,
-// refilled 256 words at a time (two coalesced dword loads per lane) whenever fewer
-// than 128 unread words remain, so a step reads its words from LDS instead of
-// waiting on a dependent global load.
+// The block's words are staged through a per-wave LDS ring of kRing 16-bit units,
+// refilled 256 units at a time (two coalesced dword loads per lane) so that a step
+// reads its words from LDS instead of waiting on a dependent global load.
 constexpr uint32_t kRing = 512;
 constexpr uint32_t kRefill = 256;
+
+// Stage units [filled, ...) of the word region into the ring until `want` units
+// (or all) are staged; each pass stages 256 units, two dwords per lane.
+__device__ __forceinline__ void ring_fill(uint16_t* ring, const uint32_t* region, uint32_t units, uint32_t& filled,
+                                          uint32_t want, uint32_t lane) {
+  if (filled >= want || filled >= units) return;
+  do {
+    const uint32_t u = filled + 4u * lane;
+    uint32_t w0 = 0, w1 = 0;
+    if (u < units) w0 = gld(region + u / 2);
+    if (u + 2 < units) w1 = gld(region + u / 2 + 1);
+    uint32_t* rp = reinterpret_cast<uint32_t*>(ring + (u & (kRing - 1)));
+    rp[0] = w0;
+    rp[1] = w1;
+    filled += kRefill;
+  } while (filled < want && filled < units);
+  __syncthreads();
+}
+
+// Steps 0..1023 of one block; returns the final state.  Before each group of
+// kGroup steps (at most 64 * kGroup words) the ring holds at least that many
+// unread units.  A refill pass starts only while fewer than 64 * kGroup units are
+// staged past q, and kRing >= 64 * kGroup + kRefill, so it overwrites only units
+// below q.
+constexpr uint32_t kGroup = 4;
+static_assert(kRing >= kGroup * kLanes + kRefill, "ring too small for the refill policy");
+
+template <int W, bool FULL>
+__device__ __forceinline__ uint32_t decode_runs(const uint32_t* region, uint32_t units, uint32_t& q,
+                                                const uint8_t* slot_sym, const uint32_t* sym_fc, uint16_t* ring,
+                                                uint8_t* dst, uint64_t room, uint32_t nb, uint32_t lane, uint32_t x) {
+  uint32_t filled = 0;
+  for (uint32_t r = 0; r < kRuns; ++r) {
+    uint32_t acc[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) acc[k] = 0;
+#pragma unroll
+    for (int g = 0; g < (int)(kRun / kGroup); ++g) {
+      ring_fill(ring, region, units, filled, q + kGroup * kLanes, lane);
+#pragma unroll
+      for (int jj = 0; jj < (int)kGroup; ++jj) {
+        const int j = g * (int)kGroup + jj;
+        const bool valid = FULL || r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
+        const uint32_t slot = x & (kM - 1u);
+        const uint32_t s = slot_sym[slot];
+        const uint32_t fc = sym_fc[s];
+        uint32_t y = (fc & 0x1fffu) * (x >> kPB) + slot - (fc >> 13);
+        const bool need = valid && y < kStateL;
+        const uint64_t mask = __ballot(need);
+        if (need) y = (y << 16) | (uint32_t)ring[(q + rank_in(mask)) & (kRing - 1)];
+        q += (uint32_t)__popcll(mask);
+        if (valid) {
+          x = y;
+          const int bit = j * W, kk = bit >> 5, sh = bit & 31;
+          acc[kk] |= s << sh;
+          if (sh + W > 32) acc[kk + 1] |= s >> (32 - sh);
+        }
+      }
+    }
+    const uint64_t off = ((uint64_t)r * kLanes + lane) * (4u * W);
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const uint64_t at = off + 4u * k;
+      if (at + 4 <= room) {
+        gst(reinterpret_cast<uint32_t*>(dst + at), acc[k]);
+      } else {
+        for (int qq = 0; qq < 4; ++qq)
+          if (at + qq < room) gst(dst + at + qq, (uint8_t)(acc[k] >> (8 * qq)));
+      }
+    }
+  }
+  return x;
+}
 
 template <int W>
 __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int32_t* __restrict__ err) {
@@ -488,71 +567,14 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
   // word region: pad4(2 count) bytes, the words at its end; q counts 16-bit units
   // from the region start, word p of the block is unit q = lead + p
   const uint32_t* region = reinterpret_cast<const uint32_t*>(blk + G::kHead);
-  const uint32_t lead = (uint32_t)(pad4(2ull * count) / 2 - count);
   const uint32_t units = (uint32_t)(pad4(2ull * count) / 2);
-  uint32_t q = lead;       // next unit to consume
-  uint32_t filled = 0;     // units [0, filled) have been staged (aligned to 4 units)
-  bool bad = false;
-  const bool full = nb == kBlock;
-
-  auto refill = [&]() {
-    while (filled < units && filled < q + kRefill / 2) {  // (q may start one unit past filled)
-      // lane l stages units [filled + 4 l, filled + 4 l + 4): two dwords
-      const uint32_t u = filled + 4u * lane;
-      uint32_t w0 = 0, w1 = 0;
-      if (u < units) w0 = gld(region + u / 2);
-      if (u + 2 < units) w1 = gld(region + u / 2 + 1);
-      uint32_t* rp = reinterpret_cast<uint32_t*>(ring + (u & (kRing - 1)));
-      rp[0] = w0;
-      rp[1] = w1;
-      filled += kRefill;
-    }
-    __syncthreads();
-  };
-  refill();
-
-  for (uint32_t r = 0; r < kRuns; ++r) {
-    uint32_t acc[W];
-#pragma unroll
-    for (int k = 0; k < W; ++k) acc[k] = 0;
-#pragma unroll
-    for (int j = 0; j < (int)kRun; ++j) {
-      if (filled < q + kLanes && filled < units) refill();
-      const bool valid = full || r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
-      const uint32_t slot = x & (kM - 1u);
-      const uint32_t s = slot_sym[slot];
-      const uint32_t fc = sym_fc[s];
-      uint32_t y = (fc & 0x1fffu) * (x >> kPB) + slot - (fc >> 13);
-      const bool need = valid && y < kStateL;
-      const uint64_t mask = __ballot(need);
-      const uint32_t k = (uint32_t)__popcll(mask);
-      if (q + k > units) {
-        bad = true;
-        break;
-      }
-      if (need) y = (y << 16) | (uint32_t)ring[(q + rank_in(mask)) & (kRing - 1)];
-      q += k;
-      if (valid) {
-        x = y;
-        const int bit = j * W, kk = bit >> 5, sh = bit & 31;
-        acc[kk] |= s << sh;
-        if (sh + W > 32) acc[kk + 1] |= s >> (32 - sh);
-      }
-    }
-    if (bad) break;
-    const uint64_t off = ((uint64_t)r * kLanes + lane) * (4u * W);
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const uint64_t at = off + 4u * k;
-      if (at + 4 <= room) {
-        gst(reinterpret_cast<uint32_t*>(dst + at), acc[k]);
-      } else {
-        for (int qq = 0; qq < 4; ++qq)
-          if (at + qq < room) gst(dst + at + qq, (uint8_t)(acc[k] >> (8 * qq)));
-      }
-    }
-  }
-  const bool ok = !bad && q == units && x == kStateL;
+  uint32_t q = units - count;
+  __syncthreads();
+  if (nb == kBlock) x = decode_runs<W, true>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, lane, x);
+  else x = decode_runs<W, false>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, lane, x);
+  // a stream that is not this block's own encoding ends off its start state or
+  // off the end of its words (ring reads are masked, so none leaves the ring)
+  const bool ok = q == units && x == kStateL;
   if (__ballot(!ok) && lane == 0) atomicOr(err, KVMI_ERR_CORRUPT);
 }
 
@@ -572,7 +594,9 @@ int rans_decode_w(const DecBatch& bt, int32_t* err, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
-uint64_t slot_bytes(int w) { return 4u + pad4(2u << w) + 4u * kLanes + (uint64_t)kBlock * w / 8; }
+uint64_t slot_bytes(int w) {
+  return 4u + pad4(2u << w) + 4u * kLanes + 2u * kLanes * kRun + (uint64_t)kBlock * w / 8;
+}
 
 }  // namespace
 }  // namespace kvmi
