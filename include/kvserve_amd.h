@@ -243,6 +243,63 @@ int kvmi_rans_encode_batch(const kvmi_rans_enc_job* jobs, int32_t num_jobs, int3
 int kvmi_rans_decode_batch(const kvmi_rans_dec_job* jobs, int32_t num_jobs, int32_t bits, int32_t* err,
                            kvmi_stream_t stream);
 
+/*
+ * Fixed-profile runtime numerics (kvserve_v1/compression/runtime/pipeline.py:264-804,
+ * runtime/csrc/kvs_compress.cu), the second numerics mode:
+ *   y = rn(FWHT(x * s) * D^-1/2) with every butterfly stage rounded to bf16;
+ *   per section (axis channel / token / tensor) min, max,
+ *   scale = rn(rn(max(rn(max - min), 1e-5)) / (L - 1)), inverse = rn(1 / scale);
+ *   q = clamp(rint(rn(rn(y - min) * inverse)), 0, L - 1);  y~ = rn(rn(q * scale) + min).
+ * Caches are HND views [blocks, heads, kernel_tokens, channels]; a KV part is the
+ * channel window [channel_offset, channel_offset + head_dim).  Canonical rows are
+ * (block, token) x [H, D] in output-head order (head_order[h] = cache head).
+ */
+#define KVMI_RT_TRANSFORM 1u /* signs + FWHT (pipeline stage "transformer") */
+#define KVMI_RT_QUANTIZE 2u  /* min-max quantizer (stage "quantizer") */
+
+typedef struct kvmi_rt_geometry {
+  int32_t num_heads;
+  int32_t head_dim;       /* power of two, <= 2048 */
+  int32_t kernel_tokens;  /* tokens per physical block */
+  uint32_t flags;         /* KVMI_RT_* */
+  uint32_t axes;          /* axes present: 1 channel, 2 token, 4 tensor */
+  int32_t reserved[3];
+} kvmi_rt_geometry;       /* 32 bytes */
+
+typedef struct kvmi_rt_section {
+  int32_t head_start, head_count, levels, axis; /* axis 0 channel, 1 token, 2 tensor */
+  int64_t aux_min_offset, aux_scale_offset;     /* bytes into the aux arena */
+} kvmi_rt_section;                              /* 32 bytes */
+
+typedef struct kvmi_rt_layer {
+  void* cache;                 /* bf16 HND cache of the layer */
+  int64_t block_stride, head_stride, token_stride, channel_offset; /* elements */
+  const void* signs;           /* bf16 [H, D] by output head, or NULL */
+  const int32_t* head_order;   /* [H] */
+  int64_t u8_offset;           /* element offset of this layer-part in the payload */
+  kvmi_rt_section sections[2];
+  int32_t num_sections, reserved;
+} kvmi_rt_layer;               /* 136 bytes; an array of them in device memory */
+
+/*
+ * Encode the body of one chunk for one KV part (runtime pipeline.py:554-651): rows of
+ * `num_blocks` physical blocks (block_ids, device int64) of every layer.  Quantized:
+ * canon (device scratch, layers x rows x H x D bf16) receives the transformed rows,
+ * aux the section minima / scales (and, at +aux_half_bytes, maxima / inverses), the
+ * payload the u8 symbols at each layer's u8_offset.  Not quantized: the payload gets
+ * the (transformed) bf16 rows.
+ */
+int kvmi_rt_encode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, int32_t num_layers,
+                   const int64_t* block_ids, int64_t num_blocks, void* canon, uint8_t* packed, uint8_t* aux,
+                   int64_t aux_half_bytes, kvmi_stream_t stream);
+/* Inverse (pipeline.py:652-763): payload (+ aux) -> the caches at block_ids. */
+int kvmi_rt_decode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, int32_t num_layers,
+                   const int64_t* block_ids, int64_t num_blocks, const uint8_t* packed, const uint8_t* aux,
+                   kvmi_stream_t stream);
+/* The runtime's normalized bf16-per-stage FWHT of rows [rows, head_dim]
+ * (runtime cpp_backend.hadamard_transform); in and out may be equal, not overlap. */
+int kvmi_rt_hadamard(const void* in, void* out, int64_t rows, int32_t head_dim, kvmi_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

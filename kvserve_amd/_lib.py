@@ -44,6 +44,9 @@ EXPORTS = (
     "kvmi_rans_decode",
     "kvmi_rans_encode_batch",
     "kvmi_rans_decode_batch",
+    "kvmi_rt_encode",
+    "kvmi_rt_decode",
+    "kvmi_rt_hadamard",
 )
 
 
@@ -68,6 +71,27 @@ class RansEncJob(ctypes.Structure):
 class RansDecJob(ctypes.Structure):
     _fields_ = [("stream", ctypes.c_void_p), ("in_bytes", ctypes.c_int64), ("n", ctypes.c_int64),
                 ("packed_out", ctypes.c_void_p)]
+
+
+RT_TRANSFORM = 1
+RT_QUANTIZE = 2
+
+
+class RtGeometry(ctypes.Structure):
+    _fields_ = [("num_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32), ("kernel_tokens", ctypes.c_int32),
+                ("flags", ctypes.c_uint32), ("axes", ctypes.c_uint32), ("reserved", ctypes.c_int32 * 3)]
+
+
+class RtSection(ctypes.Structure):
+    _fields_ = [("head_start", ctypes.c_int32), ("head_count", ctypes.c_int32), ("levels", ctypes.c_int32),
+                ("axis", ctypes.c_int32), ("aux_min_offset", ctypes.c_int64), ("aux_scale_offset", ctypes.c_int64)]
+
+
+class RtLayer(ctypes.Structure):
+    _fields_ = [("cache", ctypes.c_void_p), ("block_stride", ctypes.c_int64), ("head_stride", ctypes.c_int64),
+                ("token_stride", ctypes.c_int64), ("channel_offset", ctypes.c_int64), ("signs", ctypes.c_void_p),
+                ("head_order", ctypes.c_void_p), ("u8_offset", ctypes.c_int64), ("sections", RtSection * 2),
+                ("num_sections", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
 # kvmi_layer_job: 9 pointers, 3 int64, 2 int32 -> 104 bytes, 8-byte aligned.  It is
@@ -100,6 +124,9 @@ _SIGNATURES = {
     "kvmi_rans_decode": ([_vp, _i64, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rans_encode_batch": ([ctypes.POINTER(RansEncJob), _i32, _i32, _vp], ctypes.c_int),
     "kvmi_rans_decode_batch": ([ctypes.POINTER(RansDecJob), _i32, _i32, _vp, _vp], ctypes.c_int),
+    "kvmi_rt_encode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
+    "kvmi_rt_decode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp], ctypes.c_int),
+    "kvmi_rt_hadamard": ([_vp, _vp, _i64, _i32, _vp], ctypes.c_int),
 }
 
 

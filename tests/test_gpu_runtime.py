@@ -1,0 +1,577 @@
+"""GPU parity of the fixed-profile runtime (kvserve_amd.runtime) against the oracle
+(oracle/runtime_ref.py), the reference's golden chunks, and the reference's own
+runtime contracts (tests/runtime/test_gpu.py, test_hadamard.py of the reference).
+
+Bars: payload symbols, aux, raw tails, rANS streams and restored caches bit-exact
+against the oracle; restoration tolerances of the reference tests where they hold
+for any input (atol 0.06 at 256 levels).
+"""
+
+from __future__ import annotations
+
+import json
+from concurrent.futures import ThreadPoolExecutor
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import crans
+from oracle import runtime_ref as R
+from tests._runtime_cases import MINUS_NINE, extra_config, full_caches, load_cases, physical
+
+pytestmark = pytest.mark.gpu
+
+LAYER_NAME = "model.layers.0.self_attn"
+LEVELS = ("high_key_num_levels", "low_key_num_levels", "high_value_num_levels", "low_value_num_levels")
+CASES = load_cases()
+
+
+def _runtime():
+    from kvserve_amd import runtime
+
+    return runtime
+
+
+def bits_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def to_cuda_bf16(b: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(b.view(np.int16).copy()).view(torch.bfloat16).cuda()
+
+
+# ------------------------------------------------------------------ transform
+@pytest.mark.parametrize("dim", [1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048])
+@pytest.mark.parametrize("rows", [1, 7, 33, 1025])
+def test_transform_exact_bf16_reference(dim, rows):
+    """test_hadamard.py:26-34: the kernel equals the bf16 op-order transform exactly."""
+    from kvserve_amd.runtime.pipeline import hadamard_transform
+
+    torch.manual_seed(42)
+    source = torch.randn(rows, dim, device="cuda", dtype=torch.bfloat16) * 17
+    output = torch.empty_like(source)
+    hadamard_transform(source, output)
+    expected = R.to_bits(R.fwht(R.from_bits(bits_of(source))))
+    assert np.array_equal(bits_of(output), expected)
+
+
+def test_transform_in_place_stream_and_overlap():
+    from kvserve_amd.runtime.pipeline import CompressionPipeline, hadamard_transform
+
+    source = torch.randn(1025, 128, device="cuda", dtype=torch.bfloat16)
+    expected = R.to_bits(R.fwht(R.from_bits(bits_of(source))))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        inplace = source.clone()
+        CompressionPipeline._hadamard_transform(inplace, inplace, 128)
+    stream.synchronize()
+    assert np.array_equal(bits_of(inplace), expected)
+    storage = torch.empty(129, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="overlap"):
+        hadamard_transform(storage[:128], storage[1:])
+
+
+def test_transform_matches_independent_sylvester_matrix():
+    """test_hadamard.py:72-86."""
+    from kvserve_amd.runtime.pipeline import hadamard_transform
+
+    matrix = torch.ones(1, 1, dtype=torch.float64)
+    for _ in range(7):
+        matrix = torch.cat((torch.cat((matrix, matrix), 1), torch.cat((matrix, -matrix), 1)), 0)
+    source = torch.randint(-1, 2, (33, 128), device="cuda").to(torch.bfloat16)
+    expected = ((source.cpu().double() @ matrix) / (128 ** 0.5)).to(torch.bfloat16)
+    output = torch.empty_like(source)
+    hadamard_transform(source, output)
+    assert torch.equal(output.cpu(), expected)
+
+
+# ------------------------------------------------------------------ runtime fixture
+@pytest.fixture
+def make_runtime():
+    rt = _runtime()
+    torch.manual_seed(0)
+    created = []
+
+    def factory(compression=None, num_layers=1, raw_aggregate=None, blocks_per_logical=1, block_size=16, head_size=8,
+                heads=2, scores=None, blocks=4):
+        extra = {"compression": {"enable-compression-pipeline": True, "split_type": "layer", **(compression or {})}}
+        if raw_aggregate is not None:
+            extra["raw_aggregate"] = raw_aggregate
+        config = rt.CompressionConfig.from_extra_config(extra)
+        specs = {f"model.layers.{i}.self_attn": rt.CacheSpec(i, block_size, heads, head_size, torch.bfloat16)
+                 for i in range(num_layers)}
+        plan = rt.build_memory_plan(config, specs, blocks_per_logical=blocks_per_logical, num_layers=num_layers)
+        assert plan is not None
+        runtime = rt.CompressionRuntime(plan, "LBHNC", blocks_per_logical, torch.device("cuda", 0))
+        created.append(runtime)
+        caches = {name: torch.rand(blocks * blocks_per_logical, heads, block_size // blocks_per_logical,
+                                   2 * head_size, dtype=torch.bfloat16, device="cuda") for name in specs}
+        runtime.bind_kv_caches(caches, dict.fromkeys(specs, 0))
+        return runtime, caches[LAYER_NAME]
+
+    yield factory
+    for runtime in reversed(created):
+        runtime.shutdown()
+
+
+def _copy_wire(producer, consumer, encoded, part, tokens, target_slot=None, source_slot=None):
+    source = producer.slots[part if source_slot is None else source_slot]
+    target = consumer.slots[1 - part if target_slot is None else target_slot]
+    target.arena_a[:encoded.codec_bytes].copy_(source.arena_a[:encoded.codec_bytes])
+    aux = producer.aux_bytes(part, {0: tokens})
+    target.aux[:aux].copy_(source.aux[:aux])
+    target.raw_tail[:encoded.raw_tail_bytes].copy_(source.raw_tail[:encoded.raw_tail_bytes])
+    torch.cuda.synchronize()
+
+
+def _assert_restored(producer, consumer, part, tokens, atol=0.06):
+    """test_gpu.py:103-127."""
+    factor = producer.pipelines[0].blocks_per_logical
+    block_size = producer.layout.layer_parts[0].block_size
+    count = (tokens + block_size - 1) // block_size
+    source_ids = [b * factor + i for b in [2, 0][:count] for i in range(factor)]
+    target_ids = [b * factor + i for b in [1, 3][:count] for i in range(factor)]
+    untouched = sorted(set(range(4 * factor)) - set(target_ids))
+    for name, source in producer.pipelines[0].kv_caches.items():
+        target = consumer.pipelines[0].kv_caches[name]
+        head_size = source.shape[-1] // 2
+        section = slice(part * head_size, (part + 1) * head_size)
+        expected = source[source_ids, :, :, section].permute(0, 2, 1, 3).flatten(0, 1)
+        actual = target[target_ids, :, :, section].permute(0, 2, 1, 3).flatten(0, 1)
+        stages = producer.config.pipeline
+        tolerance = atol if "quantizer" in stages or "transformer" in stages else 0
+        torch.testing.assert_close(actual[:tokens], expected[:tokens], atol=tolerance, rtol=0)
+        if "aggregate" not in stages:
+            tail = tokens // block_size * block_size
+            assert torch.equal(actual[tail:tokens], expected[tail:tokens])
+        assert (target[untouched] == -9).all()
+
+
+@pytest.mark.parametrize("stages,tokens,factor,block_size", [
+    (None, 16, 1, 16), (["aggregate"], 17, 2, 16), ([], 32, 1, 16), (["codec"], 32, 1, 16),
+    (["transformer"], 32, 1, 16), (["quantizer"], 32, 1, 16), (["transformer", "codec"], 32, 1, 16),
+    (["quantizer", "codec"], 31, 4, 16), (["transformer", "quantizer"], 31, 4, 16),
+    (["transformer", "quantizer", "codec"], 1, 1, 16), (["transformer", "quantizer", "codec"], 15, 1, 16),
+    (["transformer", "quantizer", "codec"], 16, 1, 16), (["transformer", "quantizer", "codec"], 17, 2, 16),
+    (["transformer", "quantizer", "codec"], 31, 4, 16), (["transformer", "quantizer", "codec"], 32, 1, 16),
+    (["transformer", "quantizer", "codec"], 257, 1, 256)])
+def test_peer_buffers_restore_layers_blocks_and_partial_tail(make_runtime, stages, tokens, factor, block_size):
+    """test_gpu.py:130-190."""
+    print(f"peer restore stages={stages} tokens={tokens} factor={factor} block={block_size}", flush=True)
+    config = {"logical_blocks_per_chunk": 2}
+    if stages is not None:
+        config.update(pipeline=stages, **dict.fromkeys(LEVELS, 256))
+    num_layers = 1 if stages is None else 3
+    producer, _ = make_runtime(config, num_layers=num_layers, blocks_per_logical=factor, block_size=block_size)
+    consumer, _ = make_runtime(config, num_layers=num_layers, blocks_per_logical=factor, block_size=block_size)
+    for target in consumer.pipelines[0].kv_caches.values():
+        target.fill_(-9)
+    torch.cuda.synchronize()
+    count = (tokens + block_size - 1) // block_size
+    for part in (0, 1):
+        encoded = producer.encode(part, [[2, 0][:count]], part, valid_tokens_by_group={0: tokens})
+        encoded.event.synchronize()
+        _copy_wire(producer, consumer, encoded, part, tokens)
+        consumer.decode(1 - part, [[1, 3][:count]], part, encoded.codec_bytes, encoded.u8_bytes,
+                        valid_tokens_by_group={0: tokens}).synchronize()
+        _assert_restored(producer, consumer, part, tokens, atol=0.3 if stages is None else 0.06)
+
+
+def test_nonidentity_head_order_restores_original_heads(make_runtime, tmp_path):
+    """test_gpu.py:193-229."""
+    path = tmp_path / "scores.json"
+    path.write_text(json.dumps([[1.0, 0.0]]))
+    config = {"split_type": "head", "score_path": str(path), "hybrid_ratio": 0.5, "logical_blocks_per_chunk": 2,
+              **dict.fromkeys(LEVELS, 256)}
+    producer, _ = make_runtime(config)
+    consumer, target = make_runtime(config)
+    assert producer.plan.head_selection.local_orders[0] == (1, 0)
+    target.fill_(-9)
+    torch.cuda.synchronize()
+    for part in (0, 1):
+        encoded = producer.encode(part, [[2]], part, valid_tokens_by_group={0: 16})
+        encoded.event.synchronize()
+        _copy_wire(producer, consumer, encoded, part, 16)
+        consumer.decode(1 - part, [[1]], part, encoded.codec_bytes, encoded.u8_bytes,
+                        valid_tokens_by_group={0: 16}).synchronize()
+        _assert_restored(producer, consumer, part, 16)
+
+
+def test_raw_aggregate_multiple_chunks_reuse_slots_exactly(make_runtime):
+    """test_gpu.py:232-261."""
+    runtime, cache = make_runtime(raw_aggregate={"slot_count": 2, "logical_blocks_per_chunk": 1})
+    for chunk in range(8):
+        block, part, slot = chunk // 2, chunk % 2, chunk % 2
+        section = slice(part * 8, (part + 1) * 8)
+        source = cache[block, :, :, section].clone()
+        encoded = runtime.encode(slot, [[block]], part, valid_tokens_by_group={0: 16})
+        encoded.event.synchronize()
+        cache[block, :, :, section].zero_()
+        torch.cuda.synchronize()
+        runtime.decode(slot, [[block]], part, encoded.codec_bytes, encoded.u8_bytes,
+                       valid_tokens_by_group={0: 16}).synchronize()
+        assert encoded.codec_bytes == encoded.u8_bytes and encoded.raw_tail_bytes == 0
+        assert torch.equal(cache[block, :, :, section], source)
+
+
+def test_aggregate_indices_use_slot_stream_and_sparse_group(make_runtime):
+    """test_gpu.py:264-290: work queued on the caller's stream does not race the slot."""
+    runtime, cache = make_runtime({"pipeline": ["aggregate"]})
+    runtime.bind_kv_caches({LAYER_NAME: cache}, {LAYER_NAME: 1})
+    cache[0].fill_(1)
+    cache[1].fill_(2)
+    torch.cuda.synchronize()
+    runtime.encode(0, [[], [0]], 0, valid_tokens_by_group={1: 16}).event.synchronize()
+    caller = torch.cuda.Stream()
+    with torch.cuda.stream(caller):
+        torch.cuda._sleep(20_000_000)
+        encoded = runtime.encode(0, [[], [1]], 0, valid_tokens_by_group={1: 16})
+    encoded.event.synchronize()
+    caller.synchronize()
+    with torch.cuda.stream(caller):
+        torch.cuda._sleep(20_000_000)
+        event = runtime.decode(0, [[], [3]], 0, encoded.codec_bytes, encoded.u8_bytes,
+                               valid_tokens_by_group={1: 16})
+    event.synchronize()
+    caller.synchronize()
+    assert (cache[3, :, :, :8] == 2).all()
+    assert (cache[0] == 1).all()
+
+
+def test_sparse_group_full_pipeline(make_runtime):
+    """A layer bound to cache group 1 is coded with group 1's ids and tokens."""
+    runtime, cache = make_runtime({"pipeline": ["codec"]})
+    runtime.bind_kv_caches({LAYER_NAME: cache}, {LAYER_NAME: 1})
+    expected = cache[0, :, :, :8].clone()
+    encoded = runtime.encode(0, [[], [0]], 0, valid_tokens_by_group={1: 16})
+    encoded.event.synchronize()
+    cache[1].zero_()
+    torch.cuda.synchronize()
+    runtime.decode(0, [[], [1]], 0, encoded.codec_bytes, encoded.u8_bytes,
+                   valid_tokens_by_group={1: 16}).synchronize()
+    assert torch.equal(cache[1, :, :, :8], expected)
+
+
+def test_concurrent_slots_do_not_cross_request_writes(make_runtime):
+    """test_gpu.py:293-324."""
+    runtime, cache = make_runtime({"pipeline": ["codec"], "slot_count": 2})
+    expected = cache.clone()
+    torch.cuda.synchronize()
+
+    def encode(slot):
+        with torch.cuda.device(0):
+            return runtime.encode(slot, [[slot]], 0, valid_tokens_by_group={0: 16})
+
+    def decode(slot, encoded):
+        with torch.cuda.device(0):
+            return runtime.decode(slot, [[slot]], 0, encoded.codec_bytes, encoded.u8_bytes,
+                                  valid_tokens_by_group={0: 16})
+
+    with ThreadPoolExecutor(max_workers=2) as pool:
+        chunks = list(pool.map(encode, (0, 1)))
+        for chunk in chunks:
+            chunk.event.synchronize()
+        cache[:2, :, :, :8].zero_()
+        torch.cuda.synchronize()
+        for event in pool.map(decode, (0, 1), chunks):
+            event.synchronize()
+    assert torch.equal(cache, expected)
+
+
+def test_transform_matches_independent_reference(make_runtime):
+    """test_gpu.py:370-397."""
+    runtime, cache = make_runtime({"pipeline": ["transformer"]}, head_size=128)
+    hadamard = torch.ones((1, 1), dtype=torch.float64)
+    while hadamard.shape[0] < 128:
+        hadamard = torch.cat((torch.cat((hadamard, hadamard), 1), torch.cat((hadamard, -hadamard), 1)), 0)
+    for part in (0, 1):
+        source = cache[0, :, :, part * 128:(part + 1) * 128].clone()
+        encoded = runtime.encode(0, [[0]], part, valid_tokens_by_group={0: 16})
+        encoded.event.synchronize()
+        signs = runtime.signs[(LAYER_NAME, part)].cpu().double().reshape(2, 128)
+        expected = (source.permute(1, 0, 2).cpu().double() * signs) @ hadamard / 128 ** 0.5
+        actual = runtime.slots[0].arena_a[:encoded.codec_bytes].view(torch.bfloat16).reshape(16, 2, 128).cpu().double()
+        torch.testing.assert_close(actual, expected, atol=0.04, rtol=0.03)
+
+
+@pytest.mark.parametrize("axis", ["channel", "token", "tensor"])
+def test_quantizer_matches_numpy_reference(make_runtime, axis):
+    """test_gpu.py:400-467."""
+    config = {"pipeline": ["quantizer"], "axis_key": axis, "axis_value": axis, **dict.fromkeys(LEVELS, 16)}
+    runtime, cache = make_runtime(config)
+    t = torch.arange(16, device="cuda").reshape(1, -1, 1)
+    h = torch.arange(2, device="cuda").reshape(-1, 1, 1)
+    for part in (0, 1):
+        section = slice(part * 8, (part + 1) * 8)
+        cache[0, :, :, section].mul_(1 + t).add_(h * 20)
+        x = cache[0, :, :, section].permute(1, 0, 2).float().cpu().numpy().astype(np.float64)
+        axes = {"channel": (0,), "token": (1, 2), "tensor": (0, 1, 2)}[axis]
+        low, high = x.min(axis=axes, keepdims=True), x.max(axis=axes, keepdims=True)
+        step = np.maximum(high - low, 1e-5) / 15
+        expected = np.clip(np.rint((x - low) / step), 0, 15)
+        torch.cuda.synchronize()
+        encoded = runtime.encode(0, [[0]], part, valid_tokens_by_group={0: 16})
+        encoded.event.synchronize()
+        actual = runtime.slots[0].arena_a[:encoded.u8_bytes].cpu().numpy().reshape(x.shape)
+        assert np.abs(actual.astype(np.float64) - expected).max() <= 1
+        cache[1].zero_()
+        torch.cuda.synchronize()
+        runtime.decode(0, [[1]], part, encoded.codec_bytes, encoded.u8_bytes,
+                       valid_tokens_by_group={0: 16}).synchronize()
+        result = cache[1, :, :, section].permute(1, 0, 2).float().cpu().numpy()
+        bound = step * 0.65 + np.maximum(np.abs(low), np.abs(high)) * 0.02
+        assert np.all(np.abs(result - x) <= bound)
+
+
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("pattern,levels", [("random", 4), ("random", 6), ("constant", 12), ("tiny", 8),
+                                            ("zeros", 16)])
+def test_quantization_preserves_bf16_rounding_and_aux(make_runtime, axis, pattern, levels):
+    """test_gpu.py:470-535."""
+    config = {"pipeline": ["quantizer"], "logical_blocks_per_chunk": 2, "axis_key": axis, "axis_value": axis,
+              **dict.fromkeys(LEVELS, levels)}
+    runtime, cache = make_runtime(config)
+    cache.sub_(0.5)
+    if pattern == "constant":
+        cache.fill_(-3.125)
+    elif pattern == "tiny":
+        cache.mul_(1e-6)
+    elif pattern == "zeros":
+        cache.zero_()
+        cache[..., ::2] = -0.0
+    torch.cuda.synchronize()
+    order = runtime.pipelines[0].head_orders[LAYER_NAME].cpu()
+    for part in (0, 1):
+        x = cache[:2, :, :, part * 8:(part + 1) * 8].cpu()
+        x = x.index_select(1, order).permute(0, 2, 1, 3)
+        dims = (0, 1) if axis == "channel" else (2, 3)
+        minimum = x.amin(dims, keepdim=True)
+        maximum = x.amax(dims, keepdim=True)
+        scale = ((maximum - minimum).clamp_min(1e-5).float() / (levels - 1)).to(x.dtype)
+        inverse = scale.float().reciprocal().to(x.dtype)
+        shifted = (x.float() - minimum.float()).to(x.dtype)
+        expected = (shifted.float() * inverse.float()).to(x.dtype).float()
+        expected = expected.round().clamp(0, levels - 1).to(torch.uint8)
+        encoded = runtime.encode(0, [[0, 1]], part, valid_tokens_by_group={0: 32})
+        encoded.event.synchronize()
+        actual = runtime.slots[0].arena_a[:encoded.u8_bytes].cpu().reshape(x.shape)
+        assert torch.equal(actual, expected)
+        section = runtime.layout.parts(part)[0].sections[0]
+        for offset, value in ((section.aux_min_offset, minimum), (section.aux_scale_offset, scale)):
+            actual_aux = runtime.slots[0].aux[offset:offset + value.numel() * 2].cpu()
+            if pattern == "zeros" and offset == section.aux_min_offset:
+                torch.testing.assert_close(actual_aux.view(value.dtype), value.flatten(), rtol=0, atol=0)
+            else:
+                assert torch.equal(actual_aux, value.contiguous().view(torch.uint8).flatten())
+
+
+@pytest.mark.parametrize("field,value,compatible", [("seed", 123, False), ("axis_key", "token", False),
+                                                    ("high_key_num_levels", 32, False),
+                                                    ("logical_blocks_per_chunk", 2, False), ("slot_count", 4, True)])
+def test_wire_profile_compares_representation_not_local_slots(make_runtime, field, value, compatible):
+    """test_gpu.py:538-552."""
+    producer, _ = make_runtime({"slot_count": 1})
+    consumer, _ = make_runtime({"slot_count": 1, field: value})
+    assert (producer.wire_profile == consumer.wire_profile) == compatible
+
+
+# ------------------------------------------------------------------ exact parity
+def _golden_runtime(case, drop_codec: bool, caches):
+    rt = _runtime()
+    meta = case["meta"]
+    extra = extra_config(meta)
+    config = rt.CompressionConfig.from_extra_config(extra)
+    if drop_codec:
+        extra["compression"]["pipeline"] = [s for s in config.pipeline if s != "codec"]
+        config = rt.CompressionConfig.from_extra_config(extra)
+    specs = {f"model.layers.{i}.self_attn": rt.CacheSpec(i, meta["block_size"], meta["heads"], meta["head_size"],
+                                                         torch.bfloat16, meta["head_size_v"])
+             for i in range(meta["layers"])}
+    if meta["scores"] is not None:
+        import tempfile
+        path = tempfile.NamedTemporaryFile("w", suffix=".json", delete=False)
+        json.dump(meta["scores"], path)
+        path.close()
+        extra["compression"]["score_path"] = path.name
+        config = rt.CompressionConfig.from_extra_config(extra)
+    plan = rt.build_memory_plan(config, specs, blocks_per_logical=meta["blocks_per_logical"],
+                                num_layers=meta["layers"])
+    runtime = rt.CompressionRuntime(plan, "HND", meta["blocks_per_logical"], torch.device("cuda", 0))
+    runtime.bind_kv_caches(dict(zip(specs, caches)), dict.fromkeys(specs, 0))
+    return runtime
+
+
+@pytest.mark.parametrize("drop_codec", [False, True])
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_runtime_matches_reference_golden_chunks(name, drop_codec):
+    """Symbols, aux, raw tails and restored blocks equal the reference CPU runtime's
+    bit for bit; with the codec, the stream equals the rANS oracle's."""
+    print(f"golden runtime case={name} drop_codec={drop_codec}", flush=True)
+    case = CASES[name]
+    meta = case["meta"]
+    src = [to_cuda_bf16(c) for c in full_caches(case, True)]
+    dst = [to_cuda_bf16(c) for c in full_caches(case, False)]
+    producer = _golden_runtime(case, drop_codec, src)
+    consumer = _golden_runtime(case, drop_codec, dst)
+    coded = "codec" in producer.config.pipeline
+    try:
+        for part in (0, 1):
+            encoded = producer.encode(0, [meta["src"]], part, valid_tokens_by_group={0: meta["tokens"]})
+            encoded.event.synchronize()
+            slot = producer.slots[0]
+            u8 = encoded.u8_bytes
+            payload = (slot.arena_b[producer.layout.u8_base:producer.layout.u8_base + u8] if coded and u8
+                       else slot.arena_a[:u8]).cpu().numpy()
+            assert np.array_equal(payload, case[f"p{part}_payload"])
+            aux = producer.aux_bytes(part, {0: meta["tokens"]})
+            assert np.array_equal(slot.aux[:aux].cpu().numpy(), case[f"p{part}_aux"])
+            assert encoded.raw_tail_bytes == case[f"p{part}_tail"].size
+            assert np.array_equal(slot.raw_tail[:encoded.raw_tail_bytes].cpu().numpy(), case[f"p{part}_tail"])
+            if coded and u8:
+                stream = slot.arena_a[:encoded.codec_bytes].cpu().numpy()
+                assert np.array_equal(stream, crans.encode(case[f"p{part}_payload"], 8))
+            _copy_wire(producer, consumer, encoded, part, meta["tokens"], target_slot=0, source_slot=0)
+            consumer.decode(0, [meta["dst"]], part, encoded.codec_bytes, u8,
+                            valid_tokens_by_group={0: meta["tokens"]}).synchronize()
+        dst_ids = physical(meta, meta["dst"])
+        for i, cache in enumerate(dst):
+            got = bits_of(cache)
+            assert np.array_equal(got[dst_ids], case[f"dst{i}"])
+            untouched = sorted(set(range(got.shape[0])) - set(dst_ids))
+            assert (got[untouched] == MINUS_NINE).all()
+    finally:
+        producer.shutdown()
+        consumer.shutdown()
+
+
+@pytest.mark.parametrize("split,axis_v,bpl,tokens", [("layer", "token", 1, 256), ("head", "token", 2, 250),
+                                                    ("layer", "channel", 4, 128)])
+def test_runtime_matches_oracle_at_model_shape(tmp_path, split, axis_v, bpl, tokens):
+    """8 layers x 4 KV heads x 128, both parts, against the oracle bit for bit."""
+    print(f"oracle runtime split={split} axis_v={axis_v} bpl={bpl} tokens={tokens}", flush=True)
+    rt = _runtime()
+    layers, heads, dim, block = 8, 4, 128, 16
+    blocks = (tokens + block - 1) // block
+    compression = {"enable-compression-pipeline": True, "logical_blocks_per_chunk": blocks, "split_type": split,
+                   "axis_value": axis_v}
+    if split == "head":
+        scores = np.random.default_rng(3).random((layers, heads)).astype(np.float32)
+        np.save(tmp_path / "scores.npy", scores)
+        compression["score_path"] = str(tmp_path / "scores.npy")
+    config = rt.CompressionConfig.from_extra_config({"compression": compression})
+    specs = {f"layer.{i}": rt.CacheSpec(i, block, heads, dim, torch.bfloat16) for i in range(layers)}
+    plan = rt.build_memory_plan(config, specs, blocks_per_logical=bpl, num_layers=layers)
+    runtime = rt.CompressionRuntime(plan, "HND", bpl, torch.device("cuda", 0))
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    total = 2 * blocks * bpl
+    caches = {n: torch.randn(total, heads, block // bpl, 2 * dim, device="cuda", dtype=torch.bfloat16, generator=gen)
+              for n in specs}
+    runtime.bind_kv_caches(caches, dict.fromkeys(specs, 0))
+    src_logical = list(range(blocks))[::-1]
+    dst_logical = list(range(blocks, 2 * blocks))
+    host = [bits_of(caches[n]) for n in specs]
+    target = [h.copy() for h in host]
+    try:
+        for part in (0, 1):
+            encoded = runtime.encode(part, [src_logical], part, valid_tokens_by_group={0: tokens})
+            encoded.event.synchronize()
+            slot = runtime.slots[part]
+            parts = [R.LayerPart(cache=host[p.layer_index], channel_offset=part * dim, head_size=dim,
+                                 order=plan.head_selection.local_orders[p.layer_index], u8_offset=p.u8_offset,
+                                 signs=runtime.signs[(p.layer_name, part)].reshape(heads, dim).cpu().to(torch.int8)
+                                 .numpy(), sections=[R.Section(s.head_start, s.head_count, s.num_levels, s.axis,
+                                                               s.aux_min_offset, s.aux_scale_offset)
+                                                     for s in p.sections])
+                     for p in runtime.layout.parts(part)]
+            ids = [b * bpl + i for b in src_logical for i in range(bpl)]
+            u8, aux_n = encoded.u8_bytes, runtime.aux_bytes(part, {0: tokens})
+            payload, aux, tail = R.encode_part(parts, ids, tokens, block, bpl, True, True, u8, aux_n)
+            base = runtime.layout.u8_base
+            assert np.array_equal(slot.arena_b[base:base + u8].cpu().numpy(), payload)
+            assert np.array_equal(slot.aux[:aux_n].cpu().numpy(), aux)
+            assert np.array_equal(slot.raw_tail[:encoded.raw_tail_bytes].cpu().numpy(), tail)
+            assert np.array_equal(slot.arena_a[:encoded.codec_bytes].cpu().numpy(), crans.encode(payload, 8))
+            runtime.decode(part, [dst_logical], part, encoded.codec_bytes, u8,
+                           valid_tokens_by_group={0: tokens}).synchronize()
+            targets = [replace(o, cache=target[p.layer_index]) for o, p in zip(parts, runtime.layout.parts(part))]
+            R.decode_part(targets, [b * bpl + i for b in dst_logical for i in range(bpl)], tokens, block, bpl, True,
+                          True, payload, aux, tail)
+        for n, t in zip(specs, target):
+            assert np.array_equal(bits_of(caches[n]), t)
+    finally:
+        runtime.shutdown()
+
+
+# ------------------------------------------------------------------ contracts
+def test_separate_kv_binding_equals_combined(make_runtime):
+    runtime, cache = make_runtime({"logical_blocks_per_chunk": 2}, head_size=64)
+    encoded = runtime.encode(0, [[2, 0]], 1, valid_tokens_by_group={0: 27})
+    encoded.event.synchronize()
+    combined = runtime.slots[0].arena_a[:encoded.codec_bytes].clone()
+    tail = runtime.slots[0].raw_tail[:encoded.raw_tail_bytes].clone()
+    k, v = cache[..., :64].contiguous(), cache[..., 64:].contiguous()
+    runtime.bind_kv_caches({LAYER_NAME: (k, v)}, {LAYER_NAME: 0})
+    encoded = runtime.encode(0, [[2, 0]], 1, valid_tokens_by_group={0: 27})
+    encoded.event.synchronize()
+    assert torch.equal(runtime.slots[0].arena_a[:encoded.codec_bytes], combined)
+    assert torch.equal(runtime.slots[0].raw_tail[:encoded.raw_tail_bytes], tail)
+    v.zero_()
+    runtime.decode(0, [[2, 0]], 1, encoded.codec_bytes, encoded.u8_bytes, valid_tokens_by_group={0: 27}).synchronize()
+    assert torch.equal(v[0, :, :11], cache[0, :, :11, 64:])  # raw tail of 27 - 16 tokens
+    assert (v[0, :, 11:] == 0).all()  # the rest of the tail block is cleared
+    combined_target = cache.clone()
+    combined_target[..., 64:].zero_()
+    runtime.bind_kv_caches({LAYER_NAME: combined_target}, {LAYER_NAME: 0})
+    runtime.decode(0, [[2, 0]], 1, encoded.codec_bytes, encoded.u8_bytes, valid_tokens_by_group={0: 27}).synchronize()
+    assert torch.equal(combined_target[..., 64:], v)
+
+
+def test_encode_into_output_bank_and_decode_checks(make_runtime):
+    rt = _runtime()
+    config = rt.CompressionConfig.from_extra_config({"compression": {"enable-compression-pipeline": True}})
+    specs = {LAYER_NAME: rt.CacheSpec(0, 16, 2, 64, torch.bfloat16)}
+    plan = rt.build_memory_plan(config, specs, num_layers=1)
+    runtime = rt.create_runtime(plan, "HND", 1, torch.device("cuda", 0), output_slots=2)
+    try:
+        cache = torch.randn(4, 2, 16, 128, device="cuda", dtype=torch.bfloat16)
+        runtime.bind_kv_caches({LAYER_NAME: cache}, {LAYER_NAME: 0})
+        with pytest.raises(RuntimeError, match="reserved once before binding"):
+            runtime.allocate_output_slots(1)
+        bank, aux = runtime.output_slots[1]
+        chunk = runtime.encode_into(0, [[1]], 0, valid_tokens_by_group={0: 16}, output=bank, auxiliary=aux)
+        chunk.event.synchronize()
+        plain = runtime.encode(1, [[1]], 0, valid_tokens_by_group={0: 16})
+        plain.event.synchronize()
+        assert chunk.codec_bytes == plain.codec_bytes
+        assert torch.equal(bank[:chunk.codec_bytes], runtime.slots[1].arena_a[:plain.codec_bytes])
+        with pytest.raises(ValueError, match="one Runtime-owned bank"):
+            runtime.encode_into(0, [[1]], 0, valid_tokens_by_group={0: 16}, output=bank, auxiliary=runtime.slots[0].aux)
+        with pytest.raises(ValueError, match="incompatible decoded size"):
+            runtime.decode(0, [[2]], 0, chunk.codec_bytes, chunk.u8_bytes + 1, valid_tokens_by_group={0: 16})
+        with pytest.raises(ValueError, match="exceeds receive buffer capacity"):
+            runtime.decode(0, [[2]], 0, runtime.slots[0].arena_a.numel() + 1, chunk.u8_bytes,
+                           valid_tokens_by_group={0: 16})
+        with pytest.raises(ValueError, match="out of range"):
+            runtime.encode(0, [[7]], 0, valid_tokens_by_group={0: 16})
+        with pytest.raises(ValueError, match="exceeds logical_blocks_per_chunk"):
+            runtime.encode(0, [[0, 1]], 0, valid_tokens_by_group={0: 32})
+        decode_only = rt.CompressionRuntime(plan, "HND", 1, torch.device("cuda", 0), execution="decode")
+        with pytest.raises(RuntimeError, match="decode-only runtime cannot encode"):
+            decode_only.encode(0, [[1]], 0, valid_tokens_by_group={0: 16})
+        decode_only.shutdown()
+        pointers, sizes = runtime.registered_memory()
+        assert len(pointers) == 5 and sizes[0] == runtime.bulk.numel()
+    finally:
+        runtime.shutdown()
+
+
+def test_damaged_stream_is_reported_on_synchronize(make_runtime):
+    runtime, cache = make_runtime({"pipeline": ["codec"]})
+    encoded = runtime.encode(0, [[0]], 0, valid_tokens_by_group={0: 16})
+    encoded.event.synchronize()
+    size = encoded.codec_bytes
+    runtime.slots[0].arena_a[5] = 4  # symbol width byte of the stream header
+    with pytest.raises(RuntimeError, match="invalid bitpack header"):
+        runtime.decode(0, [[1]], 0, size, encoded.u8_bytes, valid_tokens_by_group={0: 16}).synchronize()
