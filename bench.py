@@ -69,7 +69,15 @@ WORKLOADS = {
                  "0xC0FEBABE, Llama-3.1-8B head split hybrid 0.3, 16/16 levels, bitpack 4; step = save + load, "
                  "host-timed with device synchronization; the reference connector's procedure (extract, stack, "
                  "compress, build_wire / restore, decompress, inject) on the same kernels timed beside it",
+    "runtime": "runtime: fixed-profile CompressionRuntime, token view (block_size 1) 1024 tokens x 28 layers x 4 KV "
+               "heads x D=128, default profile (Hadamard, layer split, K channel / V token, levels 12/8 high "
+               "6/4 low, ANS codec = GPU rANS over bytes), slot_count 2, one 1024-block chunk per part, seeded "
+               "N(0,1) caches; step = encode K then V with completion waits, decode K then V into disjoint "
+               "blocks (the reference's scripts/bench_runtime_dispatch.py procedure)",
 }
+
+RUNTIME_REFERENCE = {"encode_gbps": 84.11, "decode_gbps": 88.92, "hardware": "H200 NVL, fused C++ + nvCOMP ANS",
+                     "source": "docs/benchmarks/h200-runtime-dispatch-20261105/README.md:23-25"}
 
 CONNECTOR_PROFILE = {
     "pipeline": ["transformer", "quantizer", "codec"],
@@ -412,6 +420,141 @@ def bench_connector(args) -> dict:
     }
 
 
+def bench_runtime(args) -> dict:
+    """The reference's runtime dispatch benchmark on the HIP runtime: wall time of
+    K then V encode (each fenced), then K then V decode, plus device time of each
+    stage from events on the slot streams."""
+    import ctypes
+
+    import torch
+
+    from kvserve_amd import _lib
+    from kvserve_amd.runtime import CacheSpec, CompressionConfig, CompressionRuntime, build_memory_plan
+
+    dev = torch.device("cuda", 0)
+    block, blocks, layers, heads, dim = args.rt_block_size, args.rt_blocks, args.rt_layers, 4, 128
+    torch.manual_seed(3817)
+    config = CompressionConfig.from_extra_config({"compression": {
+        "enable-compression-pipeline": True, "logical_blocks_per_chunk": blocks, "slot_count": 2}})
+    specs = {f"layer.{i}": CacheSpec(i, block, heads, dim, torch.bfloat16) for i in range(layers)}
+    caches = {n: torch.randn((2 * blocks, heads, block, 2 * dim), device=dev, dtype=torch.bfloat16) for n in specs}
+    plan = build_memory_plan(config, specs, blocks_per_logical=1, num_layers=layers, device=dev)
+    runtime = CompressionRuntime(plan, "HND", 1, dev)
+    runtime.bind_kv_caches(caches, dict.fromkeys(specs, 0))
+    tokens = blocks * block
+    source, destination = list(range(blocks)), list(range(blocks, 2 * blocks))
+    raw = layers * tokens * heads * dim * 2 * 2
+
+    def encode():
+        chunks = []
+        for part in (0, 1):
+            chunk = runtime.encode(part, [source], part, valid_tokens_by_group={0: tokens})
+            chunk.event.synchronize()
+            chunks.append(chunk)
+        return chunks
+
+    def decode(chunks):
+        for part, chunk in enumerate(chunks):
+            runtime.decode(part, [destination], part, chunk.codec_bytes, chunk.u8_bytes,
+                           valid_tokens_by_group={0: tokens}).synchronize()
+
+    print(f"bench: runtime: warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        decode(encode())
+    print(f"bench: runtime: timing {args.steps} steps", file=sys.stderr, flush=True)
+    enc_s, dec_s = [], []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        chunks = encode()
+        t1 = time.perf_counter()
+        decode(chunks)
+        t2 = time.perf_counter()
+        enc_s.append(t1 - t0)
+        dec_s.append(t2 - t1)
+    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+    enc, dec = med(enc_s), med(dec_s)
+    coded = [c.codec_bytes for c in chunks]
+
+    # device time per stage: the body launch set (kvmi_rt_encode / kvmi_rt_decode) and
+    # the rANS codec, each called through the C-ABI on the slot stream with events
+    lib = _lib.load()
+    stages = {}
+    for part in (0, 1):
+        pipe, slot = runtime.pipelines[part], runtime.slots[part]
+        stream = runtime.streams[part]
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        launch = pipe._launches[part][0]
+        ids = slot.block_indices[0, :blocks]
+        with torch.cuda.stream(stream):
+            ids.copy_(torch.tensor(source, dtype=torch.int64))
+        packed = slot.arena_b[runtime.layout.u8_base:]
+        u8 = chunks[part].u8_bytes
+
+        def body_enc():
+            _lib.check(lib.kvmi_rt_encode(ctypes.byref(launch.geometry), launch.table.data_ptr(), launch.num_layers,
+                                          ids.data_ptr(), blocks, slot.canonical.data_ptr(), packed.data_ptr(),
+                                          slot.aux.data_ptr(), runtime.layout.aux_arena_bytes // 2, sp), "encode")
+
+        def body_dec():
+            _lib.check(lib.kvmi_rt_decode(ctypes.byref(launch.geometry), launch.table.data_ptr(), launch.num_layers,
+                                          ids.data_ptr(), blocks, packed.data_ptr(), slot.aux.data_ptr(), sp),
+                       "decode")
+
+        codec = pipe.codec
+
+        def rans_enc():
+            codec.encode(packed, slot.arena_a, u8, torch.cuda.Event())
+
+        def rans_dec():
+            codec.decode(slot.arena_a, packed, coded[part], u8, torch.cuda.Event())
+
+        for name, fn in (("body_encode", body_enc), ("rans_encode", rans_enc), ("rans_decode", rans_dec),
+                         ("body_decode", body_dec)):
+            for _ in range(3):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(args.steps):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            stages[f"{name}_{'kv'[part]}_us"] = round(e0.elapsed_time(e1) * 1e3 / args.steps, 2)
+    runtime.shutdown()
+    body_k = stages["body_encode_k_us"]
+    part_raw = raw // 2
+    # algorithmic bytes of the K body launch set: read the bf16 part once, write u8
+    # symbols once (aux is negligible)
+    body_bytes = part_raw + part_raw // 2
+    achieved = body_bytes / (body_k * 1e-6) / 1e9
+    return {
+        "metric": "fixed-profile runtime encode GB/s of raw bf16 K+V on 1 MI355X (K then V, fenced)",
+        "value": round(raw / enc / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round((enc + dec) * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(raw / enc / 1e9 / RUNTIME_REFERENCE["encode_gbps"], 3),
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) KV)",
+        "config": {"workload": WORKLOADS["runtime"], "layers": layers, "tokens": tokens, "block_size": block,
+                   "raw_bytes": raw, "encoded_bytes": coded},
+        "encode_ms": round(enc * 1e3, 4),
+        "decode_ms": round(dec * 1e3, 4),
+        "decode_gbps": round(raw / dec / 1e9, 2),
+        "decode_vs_baseline": round(raw / dec / 1e9 / RUNTIME_REFERENCE["decode_gbps"], 3),
+        "reference": RUNTIME_REFERENCE,
+        "stages": stages,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "kvmi_rt_encode launch set, K part"},
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,6 +565,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=32, help="(debug) layers of the config-2 request")
     ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS),
                     help="BASELINE.json configuration to time (the metric is quoted on config2)")
+    ap.add_argument("--rt-block-size", type=int, default=1, help="(runtime) tokens per block; 1 = token view")
+    ap.add_argument("--rt-blocks", type=int, default=1024, help="(runtime) blocks per chunk")
+    ap.add_argument("--rt-layers", type=int, default=28, help="(runtime) layers")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy --steps times (scales rocprof byte counters)")
     args = ap.parse_args()
@@ -432,9 +578,9 @@ def main() -> int:
 
     import torch
 
-    if args.workload in ("connector", "config2_ans"):
+    if args.workload in ("connector", "config2_ans", "runtime"):
         torch.cuda.set_device(0)
-        fn = bench_connector if args.workload == "connector" else bench_entropy
+        fn = {"connector": bench_connector, "config2_ans": bench_entropy, "runtime": bench_runtime}[args.workload]
         print(json.dumps(fn(args)), flush=True)
         return 0
 

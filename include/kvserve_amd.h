@@ -256,6 +256,12 @@ int kvmi_rans_decode_batch(const kvmi_rans_dec_job* jobs, int32_t num_jobs, int3
  */
 #define KVMI_RT_TRANSFORM 1u /* signs + FWHT (pipeline stage "transformer") */
 #define KVMI_RT_QUANTIZE 2u  /* min-max quantizer (stage "quantizer") */
+/* every layer's cache pointer, strides and channel offset are multiples of 8
+ * elements: cache rows move as 16-byte vectors */
+#define KVMI_RT_ALIGNED 4u
+/* take the multi-kernel path (transformed rows through the scratch) even where
+ * the row kernels apply; the results are identical */
+#define KVMI_RT_GENERIC 8u
 
 typedef struct kvmi_rt_geometry {
   int32_t num_heads;
@@ -284,14 +290,16 @@ typedef struct kvmi_rt_layer {
 /*
  * Encode the body of one chunk for one KV part (runtime pipeline.py:554-651): rows of
  * `num_blocks` physical blocks (block_ids, device int64) of every layer.  Quantized:
- * canon (device scratch, layers x rows x H x D bf16) receives the transformed rows,
- * aux the section minima / scales (and, at +aux_half_bytes, maxima / inverses), the
- * payload the u8 symbols at each layer's u8_offset.  Not quantized: the payload gets
- * the (transformed) bf16 rows.
+ * aux receives the section minima / scales (and, at +aux_half_bytes, maxima /
+ * inverses), the payload the u8 symbols at each layer's u8_offset; `canon` is device
+ * scratch of kvmi_rt_scratch_bytes() (transformed rows, or per-workgroup column
+ * statistics).  Not quantized: the payload gets the (transformed) bf16 rows.
  */
 int kvmi_rt_encode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, int32_t num_layers,
                    const int64_t* block_ids, int64_t num_blocks, void* canon, uint8_t* packed, uint8_t* aux,
                    int64_t aux_half_bytes, kvmi_stream_t stream);
+/* Scratch bytes kvmi_rt_encode needs for `rows` rows of `num_layers` layers of H x D. */
+int64_t kvmi_rt_scratch_bytes(int32_t num_layers, int64_t rows, int32_t num_heads, int32_t head_dim);
 /* Inverse (pipeline.py:652-763): payload (+ aux) -> the caches at block_ids. */
 int kvmi_rt_decode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, int32_t num_layers,
                    const int64_t* block_ids, int64_t num_blocks, const uint8_t* packed, const uint8_t* aux,

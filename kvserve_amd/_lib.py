@@ -47,6 +47,7 @@ EXPORTS = (
     "kvmi_rt_encode",
     "kvmi_rt_decode",
     "kvmi_rt_hadamard",
+    "kvmi_rt_scratch_bytes",
 )
 
 
@@ -75,6 +76,8 @@ class RansDecJob(ctypes.Structure):
 
 RT_TRANSFORM = 1
 RT_QUANTIZE = 2
+RT_ALIGNED = 4
+RT_GENERIC = 8
 
 
 class RtGeometry(ctypes.Structure):
@@ -127,6 +130,7 @@ _SIGNATURES = {
     "kvmi_rt_encode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
     "kvmi_rt_decode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rt_hadamard": ([_vp, _vp, _i64, _i32, _vp], ctypes.c_int),
+    "kvmi_rt_scratch_bytes": ([_i32, _i64, _i32, _i32], _i64),
 }
 
 

@@ -157,8 +157,10 @@ __global__ __launch_bounds__(kRtThreads) void rt_params_channel_kernel(kvmi_rt_g
   if (c >= cols) return;
   const kvmi_rt_layer L = layers[layer];
   const int h = (int)(c / (uint32_t)g.head_dim);
-  for (int si = 0; si < L.num_sections; ++si) {
-    const kvmi_rt_section s = L.sections[si];
+#pragma unroll
+  for (int si = 0; si < 2; ++si) {
+    if (si >= L.num_sections) break;
+    const kvmi_rt_section s = si ? L.sections[1] : L.sections[0];
     if (s.axis != 0 || h < s.head_start || h >= s.head_start + s.head_count) continue;
     const uint16_t* base = canon + (uint64_t)layer * rows * cols + c;
     float mn = INFINITY, mx = -INFINITY;
@@ -180,8 +182,10 @@ __global__ __launch_bounds__(64) void rt_params_token_kernel(kvmi_rt_geometry g,
   const uint32_t lane = threadIdx.x;
   const uint32_t cols = (uint32_t)g.num_heads * (uint32_t)g.head_dim;
   const uint16_t* row = canon + ((uint64_t)ix.layer * rows + ix.row) * cols;
-  for (int si = 0; si < L.num_sections; ++si) {
-    const kvmi_rt_section s = L.sections[si];
+#pragma unroll
+  for (int si = 0; si < 2; ++si) {
+    if (si >= L.num_sections) break;
+    const kvmi_rt_section s = si ? L.sections[1] : L.sections[0];
     if (s.axis != 1) continue;
     float mn = INFINITY, mx = -INFINITY;
     const uint32_t c0 = (uint32_t)s.head_start * g.head_dim, c1 = c0 + (uint32_t)s.head_count * g.head_dim;
@@ -207,8 +211,9 @@ __global__ __launch_bounds__(kRtThreads) void rt_params_tensor_kernel(kvmi_rt_ge
   __shared__ float smn[kRtThreads], smx[kRtThreads];
   const uint32_t layer = blockIdx.x / 2, si = blockIdx.x % 2;
   const kvmi_rt_layer L = layers[layer];
-  if ((int)si >= L.num_sections || L.sections[si].axis != 2) return;  // uniform per workgroup
-  const kvmi_rt_section s = L.sections[si];
+  if ((int)si >= L.num_sections) return;  // uniform per workgroup
+  const kvmi_rt_section s = si ? L.sections[1] : L.sections[0];
+  if (s.axis != 2) return;
   const uint32_t cols = (uint32_t)g.num_heads * (uint32_t)g.head_dim;
   const uint32_t c0 = (uint32_t)s.head_start * g.head_dim, w = (uint32_t)s.head_count * g.head_dim;
   float mn = INFINITY, mx = -INFINITY;
@@ -347,6 +352,459 @@ __global__ __launch_bounds__(kRtThreads) void rt_hadamard_kernel(const uint16_t*
   }
 }
 
+// ================================================================== row kernels
+// One wave per canonical row (all heads of one token of one layer).  A head row of D
+// channels spans LH = D / E lanes holding E contiguous channels each; a wave pass
+// covers HPW = 64 / LH heads and P passes cover the row.  Loads and stores are E-wide
+// vectors, the FWHT runs in registers (in-lane stages, then lane xor stages), and the
+// transformed rows never leave the chip: the token axis reduces inside the wave, the
+// channel / tensor axes take a statistics pass (per-workgroup partials) and a small
+// reduction before the quantizing pass.
+template <int D>
+struct RowGeo {
+  static constexpr int E = D <= 8 ? D : (D / 64 > 8 ? D / 64 : 8);
+  static constexpr int LH = D / E;
+  static constexpr int HPW = 64 / LH;
+};
+
+constexpr int kStatRows = 64;     // rows per workgroup of the statistics pass
+constexpr int kMaxRowCols = 4096; // H * D held by one wave (<= 64 values per lane)
+
+template <int E>
+__device__ __forceinline__ void ld_seg(const uint16_t* p, float (&v)[E], bool vec) {
+  if (vec) {
+    if constexpr (E >= 8) {
+#pragma unroll
+      for (int i = 0; i < E / 8; ++i) {
+        const uint4 t = gld(reinterpret_cast<const uint4*>(p) + i);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[8 * i + 2 * j] = bf_lo(w[j]), v[8 * i + 2 * j + 1] = bf_hi(w[j]);
+      }
+    } else if constexpr (E == 4) {
+      const uint2 t = gld(reinterpret_cast<const uint2*>(p));
+      v[0] = bf_lo(t.x), v[1] = bf_hi(t.x), v[2] = bf_lo(t.y), v[3] = bf_hi(t.y);
+    } else if constexpr (E == 2) {
+      const uint32_t t = gld(reinterpret_cast<const uint32_t*>(p));
+      v[0] = bf_lo(t), v[1] = bf_hi(t);
+    } else {
+      v[0] = ld_bf16(p);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[k] = ld_bf16(p + k);
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void st_seg(uint16_t* p, const float (&v)[E], bool vec) {
+  if (vec) {
+    if constexpr (E >= 8) {
+#pragma unroll
+      for (int i = 0; i < E / 8; ++i)
+        gst(reinterpret_cast<uint4*>(p) + i,
+            make_uint4(pack_bf16x2(v[8 * i], v[8 * i + 1]), pack_bf16x2(v[8 * i + 2], v[8 * i + 3]),
+                       pack_bf16x2(v[8 * i + 4], v[8 * i + 5]), pack_bf16x2(v[8 * i + 6], v[8 * i + 7])));
+    } else if constexpr (E == 4) {
+      gst(reinterpret_cast<uint2*>(p), make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])));
+    } else if constexpr (E == 2) {
+      gst(reinterpret_cast<uint32_t*>(p), pack_bf16x2(v[0], v[1]));
+    } else {
+      st_bf16(p, v[0]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) st_bf16(p + k, v[k]);
+  }
+}
+
+// E u8 symbols, packed 4 per dword
+template <int E>
+__device__ __forceinline__ void ld_sym(const uint8_t* p, uint32_t (&w)[(E + 3) / 4]) {
+  if constexpr (E >= 8) {
+#pragma unroll
+    for (int i = 0; i < E / 8; ++i) {
+      const uint2 t = gld(reinterpret_cast<const uint2*>(p) + i);
+      w[2 * i] = t.x, w[2 * i + 1] = t.y;
+    }
+  } else if constexpr (E == 4) {
+    w[0] = gld(reinterpret_cast<const uint32_t*>(p));
+  } else {
+    w[0] = 0;
+#pragma unroll
+    for (int k = 0; k < E; ++k) w[0] |= (uint32_t)gld(p + k) << (8 * k);
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void st_sym(uint8_t* p, const uint32_t (&w)[(E + 3) / 4]) {
+  if constexpr (E >= 8) {
+#pragma unroll
+    for (int i = 0; i < E / 8; ++i) gst(reinterpret_cast<uint2*>(p) + i, make_uint2(w[2 * i], w[2 * i + 1]));
+  } else if constexpr (E == 4) {
+    gst(reinterpret_cast<uint32_t*>(p), w[0]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < E; ++k) gst(p + k, (uint8_t)(w[0] >> (8 * k)));
+  }
+}
+
+// Signs of a head row: bf16 +-1, applied as the exact sign flip x * s.
+template <int E>
+__device__ __forceinline__ void mul_signs(float (&v)[E], const uint16_t* s) {
+  float sg[E];
+  ld_seg<E>(s, sg, true);
+#pragma unroll
+  for (int k = 0; k < E; ++k) v[k] = __uint_as_float(__float_as_uint(v[k]) ^ (__float_as_uint(sg[k]) & 0x80000000u));
+}
+
+template <int D, int P>
+__device__ __forceinline__ void fwht_rows(float (&v)[P][RowGeo<D>::E], uint32_t lane, float scale) {
+  constexpr int E = RowGeo<D>::E, LH = RowGeo<D>::LH;
+#pragma unroll
+  for (int m = 1; m < E; m <<= 1) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        if (k & m) continue;
+        const float a = v[p][k], b = v[p][k | m];
+        v[p][k] = rn(a + b);
+        v[p][k | m] = rn(a - b);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 1; j < LH; j <<= 1) {
+    const bool hi = lane & j;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) {
+        const float o = __shfl_xor(v[p][k], j, 64);
+        v[p][k] = rn(hi ? o - v[p][k] : v[p][k] + o);
+      }
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[p][k] = rn(v[p][k] * scale);
+}
+
+struct RowLane {
+  uint32_t lane, slot, sub;  // lane, head slot of the pass, lane within the head row
+};
+
+template <int D>
+__device__ __forceinline__ RowLane row_lane() {
+  RowLane r;
+  r.lane = threadIdx.x & 63;
+  r.slot = r.lane / RowGeo<D>::LH;
+  r.sub = r.lane % RowGeo<D>::LH;
+  return r;
+}
+
+// gather -> signs -> [FWHT] of canonical row `row` of layer L into v (output-head order)
+template <int D, int P>
+__device__ __forceinline__ void load_row(const kvmi_rt_geometry& g, const kvmi_rt_layer& L, const int64_t* block_ids,
+                                         uint64_t row, const RowLane& rl, float (&v)[P][RowGeo<D>::E], bool vec,
+                                         float scale) {
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
+  const uint64_t blk = row / (uint64_t)g.kernel_tokens;
+  const uint32_t tok = (uint32_t)(row % (uint64_t)g.kernel_tokens);
+  const int64_t pb = gld(block_ids + blk);
+  const uint16_t* cache = static_cast<const uint16_t*>(L.cache) + pb * L.block_stride +
+                          (int64_t)tok * L.token_stride + L.channel_offset + rl.sub * E;
+  const uint16_t* signs = static_cast<const uint16_t*>(L.signs);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int h = p * HPW + (int)rl.slot;
+    if (h < g.num_heads) {
+      const int hc = gld(L.head_order + h);
+      ld_seg<E>(cache + (int64_t)hc * L.head_stride, v[p], vec);
+      if (signs) mul_signs<E>(v[p], signs + (int64_t)h * D + rl.sub * E);
+    } else {
+#pragma unroll
+      for (int k = 0; k < E; ++k) v[p][k] = 0.0f;
+    }
+  }
+  if (g.flags & KVMI_RT_TRANSFORM) fwht_rows<D, P>(v, rl.lane, scale);
+}
+
+__device__ __forceinline__ float wave_min(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fminf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+
+// Statistics pass: per-workgroup min / max of every column of the layer's rows
+// [r0, r0 + kStatRows), written as fp32 partials [layer][workgroup][2][cols].
+template <int D, int P>
+__global__ __launch_bounds__(kRtThreads) void rt_stats_kernel(kvmi_rt_geometry g, const kvmi_rt_layer* __restrict__ layers,
+                                                              const int64_t* __restrict__ block_ids, uint64_t rows,
+                                                              float* __restrict__ partial, uint32_t wgs_per_layer,
+                                                              bool vec, float scale) {
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
+  __shared__ float smn[kMaxRowCols], smx[kMaxRowCols];
+  const uint32_t layer = blockIdx.x / wgs_per_layer, wg = blockIdx.x % wgs_per_layer;
+  const kvmi_rt_layer L = layers[layer];
+  const RowLane rl = row_lane<D>();
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint64_t r0 = (uint64_t)wg * kStatRows;
+  const uint64_t r1 = r0 + kStatRows < rows ? r0 + kStatRows : rows;
+  float mn[P][E], mx[P][E];
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int k = 0; k < E; ++k) mn[p][k] = INFINITY, mx[p][k] = -INFINITY;
+  for (uint64_t r = r0 + wave; r < r1; r += kRtWaves) {
+    float v[P][E];
+    load_row<D, P>(g, L, block_ids, r, rl, v, vec, scale);
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int k = 0; k < E; ++k) mn[p][k] = fminf(mn[p][k], v[p][k]), mx[p][k] = fmaxf(mx[p][k], v[p][k]);
+  }
+  const uint32_t cols = (uint32_t)g.num_heads * D;
+  for (uint32_t w = 0; w < (uint32_t)kRtWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int h = p * HPW + (int)rl.slot;
+        if (h >= g.num_heads) continue;
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+          const uint32_t c = (uint32_t)h * D + rl.sub * E + k;
+          smn[c] = w ? fminf(smn[c], mn[p][k]) : mn[p][k];
+          smx[c] = w ? fmaxf(smx[c], mx[p][k]) : mx[p][k];
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* out = partial + ((uint64_t)layer * wgs_per_layer + wg) * 2 * cols;
+  for (uint32_t c = threadIdx.x; c < cols; c += kRtThreads) {
+    gst(out + c, smn[c]);
+    gst(out + cols + c, smx[c]);
+  }
+}
+
+// Reduce the partials of one layer into the channel / tensor section parameters.
+__global__ __launch_bounds__(kRtThreads) void rt_stats_reduce_kernel(kvmi_rt_geometry g,
+                                                                     const kvmi_rt_layer* __restrict__ layers,
+                                                                     const float* __restrict__ partial,
+                                                                     uint32_t wgs_per_layer, uint8_t* __restrict__ aux,
+                                                                     uint64_t half) {
+  __shared__ float tmn[2][kRtThreads], tmx[2][kRtThreads];
+  const uint32_t layer = blockIdx.x;
+  const kvmi_rt_layer L = layers[layer];
+  const uint32_t D = (uint32_t)g.head_dim, cols = (uint32_t)g.num_heads * D;
+  float smin[2] = {INFINITY, INFINITY}, smax[2] = {-INFINITY, -INFINITY};
+  const float* base = partial + (uint64_t)layer * wgs_per_layer * 2 * cols;
+  for (uint32_t c = threadIdx.x; c < cols; c += kRtThreads) {
+    float mn = INFINITY, mx = -INFINITY;
+    for (uint32_t w = 0; w < wgs_per_layer; ++w) {
+      mn = fminf(mn, gld(base + (uint64_t)w * 2 * cols + c));
+      mx = fmaxf(mx, gld(base + (uint64_t)w * 2 * cols + cols + c));
+    }
+    const int h = (int)(c / D);
+    const int si = section_of(L, h);
+    if (si >= L.num_sections) continue;
+    const kvmi_rt_section s = si ? L.sections[1] : L.sections[0];
+    if (s.axis == 0) put_params(aux, half, s, c - (uint32_t)s.head_start * D, quant_params(mn, mx, s.levels));
+    if (s.axis == 2) {
+      if (si) {
+        smin[1] = fminf(smin[1], mn), smax[1] = fmaxf(smax[1], mx);
+      } else {
+        smin[0] = fminf(smin[0], mn), smax[0] = fmaxf(smax[0], mx);
+      }
+    }
+  }
+  const bool tensor = (L.num_sections > 0 && L.sections[0].axis == 2) || (L.num_sections > 1 && L.sections[1].axis == 2);
+  if (!tensor) return;  // uniform per workgroup
+#pragma unroll
+  for (int si = 0; si < 2; ++si) tmn[si][threadIdx.x] = smin[si], tmx[si][threadIdx.x] = smax[si];
+  __syncthreads();
+  for (int o = kRtThreads / 2; o >= 1; o >>= 1) {
+    if ((int)threadIdx.x < o)
+      for (int si = 0; si < 2; ++si) {
+        tmn[si][threadIdx.x] = fminf(tmn[si][threadIdx.x], tmn[si][threadIdx.x + o]);
+        tmx[si][threadIdx.x] = fmaxf(tmx[si][threadIdx.x], tmx[si][threadIdx.x + o]);
+      }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0)
+#pragma unroll
+    for (int si = 0; si < 2; ++si) {
+      if (si >= L.num_sections) break;
+      const kvmi_rt_section s = si ? L.sections[1] : L.sections[0];
+      if (s.axis == 2) put_params(aux, half, s, 0, quant_params(tmn[si][0], tmx[si][0], s.levels));
+    }
+}
+
+// Encode pass: one wave per (layer, row).  Quantized: token sections reduce inside
+// the wave, channel / tensor sections read their parameters from aux; the u8 symbols
+// land at the layer's u8_offset.  Not quantized: the bf16 rows are the payload.
+template <int D, int P>
+__global__ __launch_bounds__(kRtThreads) void rt_row_encode_kernel(kvmi_rt_geometry g, const kvmi_rt_layer* __restrict__ layers,
+                                                                   const int64_t* __restrict__ block_ids, uint64_t rows,
+                                                                   uint32_t num_layers, uint8_t* __restrict__ packed,
+                                                                   uint8_t* __restrict__ aux, uint64_t half, bool vec,
+                                                                   float scale) {
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
+  const uint64_t task = (uint64_t)blockIdx.x * kRtWaves + (threadIdx.x >> 6);
+  const uint64_t tasks = rows * (uint64_t)num_layers;
+  if (task >= tasks) return;  // wave-uniform
+  const uint32_t layer = (uint32_t)(task / rows);
+  const uint64_t row = task % rows;
+  const kvmi_rt_layer L = layers[layer];
+  const RowLane rl = row_lane<D>();
+  float v[P][E];
+  load_row<D, P>(g, L, block_ids, row, rl, v, vec, scale);
+  const uint64_t cols = (uint64_t)g.num_heads * D;
+  if (!(g.flags & KVMI_RT_QUANTIZE)) {
+    uint16_t* out = reinterpret_cast<uint16_t*>(packed) + L.u8_offset + row * cols + rl.sub * E;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int h = p * HPW + (int)rl.slot;
+      if (h < g.num_heads) st_seg<E>(out + (int64_t)h * D, v[p], true);
+    }
+    return;
+  }
+  // token-axis statistics of the row, per section (two named sections: a local array
+  // indexed by a run-time section number would live in scratch memory)
+  float tmin0 = INFINITY, tmin1 = INFINITY, tmax0 = -INFINITY, tmax1 = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int h = p * HPW + (int)rl.slot;
+    if (h >= g.num_heads) continue;
+    float a = INFINITY, b = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < E; ++k) a = fminf(a, v[p][k]), b = fmaxf(b, v[p][k]);
+    if (section_of(L, h)) {
+      tmin1 = fminf(tmin1, a), tmax1 = fmaxf(tmax1, b);
+    } else {
+      tmin0 = fminf(tmin0, a), tmax0 = fmaxf(tmax0, b);
+    }
+  }
+  QP tp0 = {}, tp1 = {};
+  if (L.num_sections > 0 && L.sections[0].axis == 1) {  // uniform
+    tp0 = quant_params(wave_min(tmin0), wave_max(tmax0), L.sections[0].levels);
+    if (rl.lane == 0) put_params(aux, half, L.sections[0], row, tp0);
+  }
+  if (L.num_sections > 1 && L.sections[1].axis == 1) {
+    tp1 = quant_params(wave_min(tmin1), wave_max(tmax1), L.sections[1].levels);
+    if (rl.lane == 0) put_params(aux, half, L.sections[1], row, tp1);
+  }
+  uint8_t* out = packed + L.u8_offset + row * cols + rl.sub * E;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int h = p * HPW + (int)rl.slot;
+    if (h >= g.num_heads) continue;
+    const bool second = section_of(L, h);
+    const kvmi_rt_section s = second ? L.sections[1] : L.sections[0];
+    float mn[E], inv[E];
+    if (s.axis == 1) {
+      const QP& t = second ? tp1 : tp0;
+#pragma unroll
+      for (int k = 0; k < E; ++k) mn[k] = t.mn, inv[k] = t.inv;
+    } else {
+      const uint64_t pi = s.axis == 0 ? (uint64_t)(h - s.head_start) * D + rl.sub * E : 0;
+      const uint16_t* pmn = reinterpret_cast<const uint16_t*>(aux + s.aux_min_offset) + pi;
+      const uint16_t* pinv = reinterpret_cast<const uint16_t*>(aux + half + s.aux_scale_offset) + pi;
+      if (s.axis == 0) {
+        ld_seg<E>(pmn, mn, true);
+        ld_seg<E>(pinv, inv, true);
+      } else {
+        const float a = ld_bf16(pmn), b = ld_bf16(pinv);
+#pragma unroll
+        for (int k = 0; k < E; ++k) mn[k] = a, inv[k] = b;
+      }
+    }
+    const float top = (float)(s.levels - 1);
+    uint32_t w[(E + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (E + 3) / 4; ++i) w[i] = 0;
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+      float q = rintf(rn(rn(v[p][k] - mn[k]) * inv[k]));
+      q = fminf(fmaxf(q, 0.0f), top);
+      w[k / 4] |= (uint32_t)q << (8 * (k % 4));
+    }
+    st_sym<E>(out + (int64_t)h * D, w);
+  }
+}
+
+// Decode pass: one wave per (layer, row): symbols (or bf16 rows) -> dequantize ->
+// [FWHT] -> signs -> the cache, through the head order.
+template <int D, int P>
+__global__ __launch_bounds__(kRtThreads) void rt_row_decode_kernel(kvmi_rt_geometry g, const kvmi_rt_layer* __restrict__ layers,
+                                                                   const int64_t* __restrict__ block_ids, uint64_t rows,
+                                                                   uint32_t num_layers, const uint8_t* __restrict__ packed,
+                                                                   const uint8_t* __restrict__ aux, bool vec, float scale) {
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
+  const uint64_t task = (uint64_t)blockIdx.x * kRtWaves + (threadIdx.x >> 6);
+  const uint64_t tasks = rows * (uint64_t)num_layers;
+  if (task >= tasks) return;
+  const uint32_t layer = (uint32_t)(task / rows);
+  const uint64_t row = task % rows;
+  const kvmi_rt_layer L = layers[layer];
+  const RowLane rl = row_lane<D>();
+  const uint64_t cols = (uint64_t)g.num_heads * D;
+  float v[P][E];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int h = p * HPW + (int)rl.slot;
+    if (h >= g.num_heads) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) v[p][k] = 0.0f;
+      continue;
+    }
+    const uint64_t c = row * cols + (uint64_t)h * D + rl.sub * E;
+    if (!(g.flags & KVMI_RT_QUANTIZE)) {
+      ld_seg<E>(reinterpret_cast<const uint16_t*>(packed) + L.u8_offset + c, v[p], true);
+      continue;
+    }
+    uint32_t w[(E + 3) / 4];
+    ld_sym<E>(packed + L.u8_offset + c, w);
+    const kvmi_rt_section s = section_of(L, h) ? L.sections[1] : L.sections[0];
+    float mn[E], sc[E];
+    const uint64_t pi = s.axis == 0 ? (uint64_t)(h - s.head_start) * D + rl.sub * E : (s.axis == 1 ? row : 0);
+    const uint16_t* pmn = reinterpret_cast<const uint16_t*>(aux + s.aux_min_offset) + pi;
+    const uint16_t* psc = reinterpret_cast<const uint16_t*>(aux + s.aux_scale_offset) + pi;
+    if (s.axis == 0) {
+      ld_seg<E>(pmn, mn, true);
+      ld_seg<E>(psc, sc, true);
+    } else {
+      const float a = ld_bf16(pmn), b = ld_bf16(psc);
+#pragma unroll
+      for (int k = 0; k < E; ++k) mn[k] = a, sc[k] = b;
+    }
+#pragma unroll
+    for (int k = 0; k < E; ++k) v[p][k] = rn(rn((float)((w[k / 4] >> (8 * (k % 4))) & 0xffu) * sc[k]) + mn[k]);
+  }
+  if (g.flags & KVMI_RT_TRANSFORM) fwht_rows<D, P>(v, rl.lane, scale);
+  const uint64_t blk = row / (uint64_t)g.kernel_tokens;
+  const uint32_t tok = (uint32_t)(row % (uint64_t)g.kernel_tokens);
+  const int64_t pb = gld(block_ids + blk);
+  uint16_t* cache = static_cast<uint16_t*>(L.cache) + pb * L.block_stride + (int64_t)tok * L.token_stride +
+                    L.channel_offset + rl.sub * E;
+  const uint16_t* signs = static_cast<const uint16_t*>(L.signs);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int h = p * HPW + (int)rl.slot;
+    if (h >= g.num_heads) continue;
+    if (signs) mul_signs<E>(v[p], signs + (int64_t)h * D + rl.sub * E);
+    st_seg<E>(cache + (int64_t)gld(L.head_order + h) * L.head_stride, v[p], vec);
+  }
+}
+
 float rt_scale(int D) { return (float)(1.0 / __builtin_sqrt((double)D)); }
 
 template <class F>
@@ -368,6 +826,45 @@ int rt_dispatch(int D, F&& f) {
   }
 }
 
+// head sizes served by the row kernels (the others take the generic path)
+bool rt_row_head_dim(int D) { return D >= 8 && D <= 256; }
+
+// P passes of HPW heads cover a row; the row kernels hold E * P <= 64 values per lane
+int rt_row_passes(int D, int H) {
+  if (!rt_row_head_dim(D)) return 0;
+  int E = D <= 8 ? D : (D / 64 > 8 ? D / 64 : 8);
+  const int hpw = 64 / (D / E);
+  const int need = (H + hpw - 1) / hpw;
+  int P = 1;
+  while (P < need) P <<= 1;
+  if (P > 8 || E * P > 64 || (int64_t)H * D > kMaxRowCols) return 0;
+  return P;
+}
+
+template <class F>
+int rt_row_dispatch(int D, int P, F&& f) {
+  auto passes = [&](auto Dc) {
+    switch (P) {
+      case 1: return f(Dc, std::integral_constant<int, 1>{});
+      case 2: return f(Dc, std::integral_constant<int, 2>{});
+      case 4: return f(Dc, std::integral_constant<int, 4>{});
+      case 8: return f(Dc, std::integral_constant<int, 8>{});
+      default: return (int)KVMI_EINVAL;
+    }
+  };
+  switch (D) {
+    case 8: return passes(std::integral_constant<int, 8>{});
+    case 16: return passes(std::integral_constant<int, 16>{});
+    case 32: return passes(std::integral_constant<int, 32>{});
+    case 64: return passes(std::integral_constant<int, 64>{});
+    case 128: return passes(std::integral_constant<int, 128>{});
+    case 256: return passes(std::integral_constant<int, 256>{});
+    default: return (int)KVMI_EINVAL;
+  }
+}
+
+int64_t stat_wgs(uint64_t rows) { return (int64_t)((rows + kStatRows - 1) / kStatRows); }
+
 bool rt_geometry_ok(const kvmi_rt_geometry* g) {
   return g && g->num_heads >= 1 && g->num_heads <= 1024 && g->head_dim >= 1 && g->head_dim <= 2048 &&
          (g->head_dim & (g->head_dim - 1)) == 0 && g->kernel_tokens >= 1;
@@ -377,6 +874,14 @@ bool rt_geometry_ok(const kvmi_rt_geometry* g) {
 }  // namespace kvmi
 
 using namespace kvmi;
+
+extern "C" int64_t kvmi_rt_scratch_bytes(int32_t num_layers, int64_t rows, int32_t num_heads, int32_t head_dim) {
+  if (num_layers < 0 || rows < 0 || num_heads < 0 || head_dim < 0) return -1;
+  const int64_t cols = (int64_t)num_heads * head_dim;
+  const int64_t canon = (int64_t)num_layers * rows * cols * 2;
+  const int64_t stats = (int64_t)num_layers * stat_wgs((uint64_t)rows) * 2 * cols * 4;
+  return canon > stats ? canon : stats;
+}
 
 extern "C" int kvmi_rt_encode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, int32_t num_layers,
                               const int64_t* block_ids, int64_t num_blocks, void* canon, uint8_t* packed,
@@ -391,27 +896,39 @@ extern "C" int kvmi_rt_encode(const kvmi_rt_geometry* geom, const kvmi_rt_layer*
   const uint64_t rows = (uint64_t)num_blocks * (uint64_t)g.kernel_tokens;
   const uint64_t grid = rows * (uint64_t)num_layers;
   if (grid > 0x7fffffffull) return KVMI_EINVAL;
-  // not quantized: the canonical rows are the payload (bf16)
-  uint16_t* dst = quant ? static_cast<uint16_t*>(canon) : reinterpret_cast<uint16_t*>(packed);
   const float scale = rt_scale(g.head_dim);
-  if (!quant) {
-    int rc = rt_dispatch(g.head_dim, [&](auto Dc) {
-      constexpr int D = decltype(Dc)::value;
-      hipLaunchKernelGGL(rt_transform_kernel<D>, dim3((uint32_t)grid), dim3(kRtThreads), 0, s, g, layers, block_ids,
-                         rows, dst, true, scale);
-      return KVMI_OK;
+  const uint64_t half = (uint64_t)aux_half_bytes;
+  const int P = (g.flags & KVMI_RT_GENERIC) ? 0 : rt_row_passes(g.head_dim, g.num_heads);
+  const bool vec = g.flags & KVMI_RT_ALIGNED;
+  if (P) {
+    int rc = rt_row_dispatch(g.head_dim, P, [&](auto Dc, auto Pc) {
+      constexpr int D = decltype(Dc)::value, PP = decltype(Pc)::value;
+      if (quant && (g.axes & 5u)) {
+        const uint32_t wpl = (uint32_t)stat_wgs(rows);
+        float* partial = static_cast<float*>(canon);
+        hipLaunchKernelGGL((rt_stats_kernel<D, PP>), dim3(wpl * (uint32_t)num_layers), dim3(kRtThreads), 0, s, g,
+                           layers, block_ids, rows, partial, wpl, vec, scale);
+        hipLaunchKernelGGL(rt_stats_reduce_kernel, dim3((uint32_t)num_layers), dim3(kRtThreads), 0, s, g, layers,
+                           (const float*)partial, wpl, aux, half);
+      }
+      const uint32_t wgs = (uint32_t)((grid + kRtWaves - 1) / kRtWaves);
+      hipLaunchKernelGGL((rt_row_encode_kernel<D, PP>), dim3(wgs), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
+                         (uint32_t)num_layers, packed, aux, half, vec, scale);
+      return (int)KVMI_OK;
     });
     if (rc != KVMI_OK) return rc;
     return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
   }
+  // generic path: transformed rows through the scratch
+  uint16_t* dst = quant ? static_cast<uint16_t*>(canon) : reinterpret_cast<uint16_t*>(packed);
   int rc = rt_dispatch(g.head_dim, [&](auto Dc) {
     constexpr int D = decltype(Dc)::value;
     hipLaunchKernelGGL(rt_transform_kernel<D>, dim3((uint32_t)grid), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
-                       dst, false, scale);
+                       dst, !quant, scale);
     return KVMI_OK;
   });
   if (rc != KVMI_OK) return rc;
-  const uint64_t half = (uint64_t)aux_half_bytes;
+  if (!quant) return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
   const uint32_t cols = (uint32_t)g.num_heads * (uint32_t)g.head_dim;
   const uint32_t per_layer = (cols + kRtThreads - 1) / kRtThreads;
   if (g.axes & 1u)
@@ -440,12 +957,25 @@ extern "C" int kvmi_rt_decode(const kvmi_rt_geometry* geom, const kvmi_rt_layer*
   const uint64_t grid = rows * (uint64_t)num_layers;
   if (grid > 0x7fffffffull) return KVMI_EINVAL;
   const float scale = rt_scale(g.head_dim);
-  int rc = rt_dispatch(g.head_dim, [&](auto Dc) {
-    constexpr int D = decltype(Dc)::value;
-    hipLaunchKernelGGL(rt_decode_kernel<D>, dim3((uint32_t)grid), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
-                       packed, aux, scale);
-    return KVMI_OK;
-  });
+  const int P = (g.flags & KVMI_RT_GENERIC) ? 0 : rt_row_passes(g.head_dim, g.num_heads);
+  int rc;
+  if (P) {
+    const bool vec = g.flags & KVMI_RT_ALIGNED;
+    rc = rt_row_dispatch(g.head_dim, P, [&](auto Dc, auto Pc) {
+      constexpr int D = decltype(Dc)::value, PP = decltype(Pc)::value;
+      const uint32_t wgs = (uint32_t)((grid + kRtWaves - 1) / kRtWaves);
+      hipLaunchKernelGGL((rt_row_decode_kernel<D, PP>), dim3(wgs), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
+                         (uint32_t)num_layers, packed, aux, vec, scale);
+      return (int)KVMI_OK;
+    });
+  } else {
+    rc = rt_dispatch(g.head_dim, [&](auto Dc) {
+      constexpr int D = decltype(Dc)::value;
+      hipLaunchKernelGGL(rt_decode_kernel<D>, dim3((uint32_t)grid), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
+                         packed, aux, scale);
+      return KVMI_OK;
+    });
+  }
   if (rc != KVMI_OK) return rc;
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }

@@ -81,7 +81,8 @@ class CompressionRuntime:
                      + [per_slot_ws] * (self.config.slot_count if self.config.uses_codec else 0)
                      + [s for _, s in meta]):
             total = round_up(total, ALIGNMENT) + size
-        self.bulk = torch.empty(round_up(total, ALIGNMENT), dtype=torch.uint8, device=device)
+        # zeroed once; encode skips clearing the payload of chunks that fill it
+        self.bulk = torch.zeros(round_up(total, ALIGNMENT), dtype=torch.uint8, device=device)
         carver = _Carver(self.bulk)
         physical = self.config.logical_blocks_per_chunk * blocks_per_logical
         self.slots: List[CompressionSlotBuffers] = []

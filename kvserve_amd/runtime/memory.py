@@ -54,8 +54,18 @@ def codec_capacity(packed_bytes: int) -> Tuple[int, int]:
 
 
 def canonical_bytes(layout: CompressionLayout) -> int:
-    """Transformed bf16 rows of every layer of the larger KV part (quantized pipelines)."""
-    return max(sum(p.raw_bytes for p in layout.parts(k)) for k in (0, 1))
+    """Scratch of the quantizing encode (transformed rows or per-workgroup column
+    statistics, kvmi_rt_scratch_bytes) for every layer of the larger KV part at the
+    chunk's full capacity."""
+    lib = _lib.load()
+    per_part = []
+    for k in (0, 1):
+        total = 0
+        for p in layout.parts(k):
+            rows = p.raw_bytes // (2 * p.num_heads * p.head_size)
+            total += int(lib.kvmi_rt_scratch_bytes(1, rows, p.num_heads, p.head_size))
+        per_part.append(total)
+    return max(per_part)
 
 
 def index_rows(layout: CompressionLayout) -> int:

@@ -26,6 +26,7 @@ import logging
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple, Union
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -116,6 +117,9 @@ class CompressionPipeline:
         self._bases: Dict[Tuple[str, int], Tuple[torch.Tensor, int]] = {}
         self._num_blocks = 0
         self._launches: Dict[int, List[_Launch]] = {0: [], 1: []}
+        # "auto": the row kernels where they apply; "generic": the multi-kernel path
+        # everywhere (identical results; kept selectable for tests)
+        self.kernel_path = "auto"
         self._lib = _lib.load()
 
     @staticmethod
@@ -179,8 +183,11 @@ class CompressionPipeline:
             for (group, heads, size, block_size), parts in groups.items():
                 rows = (_lib.RtLayer * len(parts))()
                 axes = 0
+                aligned = True
                 for i, part in enumerate(parts):
                     base, offset = self._bases[(part.layer_name, part.kv_part)]
+                    aligned &= (base.data_ptr() % 16 == 0 and offset % 8 == 0
+                                and all(st % 8 == 0 for st in base.stride()[:3]))
                     entry = rows[i]
                     entry.cache = base.data_ptr()
                     entry.block_stride, entry.head_stride, entry.token_stride = (base.stride(0), base.stride(1),
@@ -196,53 +203,84 @@ class CompressionPipeline:
                         axes |= 1 << _AXIS[s.axis]
                 host = torch.frombuffer(bytearray(bytes(rows)), dtype=torch.uint8)
                 table = host.to(self.stream.device)
-                geometry = _lib.RtGeometry(heads, size, block_size // self.blocks_per_logical,
-                                           (_lib.RT_TRANSFORM if transform else 0) | (_lib.RT_QUANTIZE if quantize else 0),
-                                           axes)
+                flags = ((_lib.RT_TRANSFORM if transform else 0) | (_lib.RT_QUANTIZE if quantize else 0)
+                         | (_lib.RT_ALIGNED if aligned else 0) | (_lib.RT_GENERIC if self.kernel_path == "generic" else 0))
+                geometry = _lib.RtGeometry(heads, size, block_size // self.blocks_per_logical, flags, axes)
                 self._launches[kv].append(_Launch(group, block_size, geometry, table, len(parts)))
 
     # ------------------------------------------------------------------ indices
-    def _physical_ids(self, logical_ids: List[int]) -> List[int]:
+    _STAGING_DEPTH = 4  # uploads of block ids kept in flight per pipeline
+
+    def _physical_ids(self, logical_ids) -> np.ndarray:
+        if isinstance(logical_ids, torch.Tensor):
+            ids = logical_ids.detach().to("cpu", torch.int64).numpy()
+        elif isinstance(logical_ids, np.ndarray):
+            ids = logical_ids.astype(np.int64, copy=False)
+        else:
+            ids = np.fromiter(logical_ids, dtype=np.int64, count=len(logical_ids))
         f = self.blocks_per_logical
-        return [b * f + i for b in logical_ids for i in range(f)]
+        if f == 1:
+            return ids
+        return (ids[:, None] * f + np.arange(f, dtype=np.int64)[None, :]).reshape(-1)
 
-    def _index_tensor(self, slot: CompressionSlotBuffers, logical_ids: List[int], row: int = 0) -> torch.Tensor:
-        physical = self._physical_ids(logical_ids)
-        storage = slot.block_indices if slot.block_indices.ndim == 1 else slot.block_indices[row]
-        if len(physical) > storage.numel():
-            raise ValueError("Compressed chunk exceeds logical_blocks_per_chunk")
-        if min(physical) < 0 or max(physical) >= self._num_blocks:
-            raise ValueError(f"Block id out of range for KV caches of {self._num_blocks} blocks")
-        indices = storage[:len(physical)]
-        # a fresh pinned staging tensor per upload: torch's pinned-memory cache does not
-        # hand it out again before the queued copy has run, so back-to-back chunks on
-        # one slot cannot overwrite ids still in flight
-        host = torch.tensor(physical, dtype=torch.int64).pin_memory()
-        indices.copy_(host, non_blocking=True)
-        return indices
+    def _staging_rows(self, slot: CompressionSlotBuffers) -> Tuple[np.ndarray, torch.Tensor, int]:
+        """A pinned staging generation for the id uploads of one call.  A generation is
+        reused only after the copies queued from it have run (its event)."""
+        if getattr(self, "_staging", None) is None or self._staging.shape[1:] != slot.block_indices.shape:
+            self._staging = torch.empty((self._STAGING_DEPTH, *slot.block_indices.shape), dtype=torch.int64,
+                                        pin_memory=True)
+            self._staging_np = self._staging.numpy()
+            self._staging_events = [None] * self._STAGING_DEPTH
+            self._staging_next = 0
+        g = self._staging_next
+        self._staging_next = (g + 1) % self._STAGING_DEPTH
+        if self._staging_events[g] is not None:
+            self._staging_events[g].synchronize()
+        return self._staging_np[g], self._staging[g], g
 
-    def _group_indices(self, slot: CompressionSlotBuffers, logical_ids_by_group: List[List[int]]
-                       ) -> Dict[int, Tuple[torch.Tensor, List[int]]]:
-        """Device ids (one upload per group, pipeline.py:203-222) and host ids."""
+    def _group_indices(self, slot: CompressionSlotBuffers, logical_ids_by_group
+                       ) -> Dict[int, Tuple[torch.Tensor, np.ndarray]]:
+        """Device ids (one upload per group, pipeline.py:183-222) and host ids."""
         out = {}
+        staged = None
         for group, logical_ids in enumerate(logical_ids_by_group):
-            if logical_ids and group in self.layout.index_rows_by_group:
-                out[group] = (self._index_tensor(slot, logical_ids, self.layout.index_rows_by_group[group]),
-                              self._physical_ids(logical_ids))
+            if not len(logical_ids) or group not in self.layout.index_rows_by_group:
+                continue
+            row = self.layout.index_rows_by_group[group]
+            physical = self._physical_ids(logical_ids)
+            storage = slot.block_indices if slot.block_indices.ndim == 1 else slot.block_indices[row]
+            n = physical.size
+            if n > storage.numel():
+                raise ValueError("Compressed chunk exceeds logical_blocks_per_chunk")
+            if physical.min() < 0 or physical.max() >= self._num_blocks:
+                raise ValueError(f"Block id out of range for KV caches of {self._num_blocks} blocks")
+            if staged is None:
+                staged = self._staging_rows(slot)
+            host_np, host, g = staged
+            hrow_np = host_np if host_np.ndim == 1 else host_np[row]
+            hrow = host if host.ndim == 1 else host[row]
+            hrow_np[:n] = physical
+            indices = storage[:n]
+            indices.copy_(hrow[:n], non_blocking=True)
+            out[group] = (indices, physical)
+        if staged is not None:
+            event = self._staging_events[staged[2]] or torch.cuda.Event()
+            event.record(self.stream)
+            self._staging_events[staged[2]] = event
         return out
 
     # ------------------------------------------------------------------ raw tails
     def _cache_part(self, part: LayerPartLayout) -> torch.Tensor:
         return self._cache_parts[(part.layer_name, part.kv_part)]
 
-    def _tail_blocks(self, part: LayerPartLayout, physical: List[int], valid_tokens: int):
+    def _tail_blocks(self, part: LayerPartLayout, physical: np.ndarray, valid_tokens: int):
         """(physical block, token count) of the incomplete logical block."""
         tail = valid_tokens % part.block_size
         if not tail:
             return []
         kernel_tokens = part.block_size // self.blocks_per_logical
         out = []
-        for i, block in enumerate(physical[-self.blocks_per_logical:]):
+        for i, block in enumerate(physical[-self.blocks_per_logical:].tolist()):
             out.append((block, max(0, min(tail - i * kernel_tokens, kernel_tokens))))
         return out
 
@@ -342,17 +380,26 @@ class CompressionPipeline:
         coded = bool(u8_bytes) and "codec" in self.stages
         packed = slot.arena_b[self.layout.u8_base:] if coded else slot.arena_a
         tail_addr = slot.raw_tail.data_ptr() if slot.raw_tail is not None else 0
+        parts = self.layout.parts(kv_part)
+        # a chunk that fills every layer's capacity overwrites the whole payload (the
+        # layers' symbol ranges tile it); the aux arena has alignment gaps that the
+        # other KV part's sections may have written, so it is always cleared
+        full = all(valid_tokens_by_group.get(p.group_index, 0) == p.raw_bytes // (2 * p.num_heads * p.head_size)
+                   for p in parts)
         with torch.cuda.stream(self.stream):
-            # capacities are planned for the largest chunk: a short chunk must not
-            # carry the previous owner's bytes
-            packed[:u8_bytes].zero_()
+            if not full:
+                # capacities are planned for the largest chunk: a short chunk must not
+                # carry the previous owner's bytes
+                packed[:u8_bytes].zero_()
             slot.aux[:aux_bytes].zero_()
             index = self._group_indices(slot, logical_ids_by_group)
             offset = 0
-            for part in self.layout.parts(kv_part):
-                entry = index.get(part.group_index)
-                if entry is not None:
-                    offset = self._pack_raw_tail(slot, part, entry[1], valid_tokens_by_group[part.group_index], offset)
+            if raw_tail_bytes:
+                for part in parts:
+                    entry = index.get(part.group_index)
+                    if entry is not None:
+                        offset = self._pack_raw_tail(slot, part, entry[1], valid_tokens_by_group[part.group_index],
+                                                     offset)
             canonical = slot.canonical.data_ptr() if slot.canonical is not None else None
             for launch in self._launches[kv_part]:
                 body = self._body(launch, index, valid_tokens_by_group)
@@ -397,9 +444,11 @@ class CompressionPipeline:
                                               slot.aux.data_ptr() if quantized else None, self._sp())
                 _lib.check(rc, "kvmi_rt_decode")
             offset = 0
-            for part in self.layout.parts(kv_part):
-                entry = index.get(part.group_index)
-                if entry is not None:
-                    offset = self._apply_raw_tail(slot, part, entry[1], valid_tokens_by_group[part.group_index], offset)
+            if any(valid_tokens_by_group.get(p.group_index, 0) % p.block_size for p in self.layout.parts(kv_part)):
+                for part in self.layout.parts(kv_part):
+                    entry = index.get(part.group_index)
+                    if entry is not None:
+                        offset = self._apply_raw_tail(slot, part, entry[1], valid_tokens_by_group[part.group_index],
+                                                      offset)
             slot.completion_event.record(self.stream)
         return slot.completion_event
