@@ -5,19 +5,21 @@
 //
 // Input: n symbols of W bits packed LSB-first (the bitpack body).  The stream is a
 // 32-byte header, a u64 offset per block, then the blocks.  A block covers 65536
-// symbols: 64 interleaved 32-bit rANS states, one per lane of the wave that codes
-// it, lane i taking block symbol (t/32)*2048 + i*32 + t%32 at step t (t < 1024).
-// Each block carries its own 12-bit frequency table (K and V, layers and heads have
-// different statistics), renormalises in 16-bit words and is stored raw when coding
-// would not make it smaller.
+// symbols in 4 sub-blocks of 16384 that share the block's 12-bit frequency table
+// (K and V, layers and heads have different statistics).  A sub-block is coded by
+// one wave: 64 interleaved 32-bit rANS states, lane i taking sub-block symbol
+// (t/32)*2048 + i*32 + t%32 at step t (t < 256).  Blocks renormalise in 16-bit words
+// and are stored raw when coding would not make them smaller.  Four waves per block
+// keep the serial chain of a state at 256 steps, so a stream of a few hundred blocks
+// still spreads over the chip.
 //
-// Kernels (one wave per block):
-//   rans_encode_kernel   histogram -> table -> encode (steps 1023..0) into a
+// Kernels (one 256-thread workgroup per block, wave j on sub-block j):
+//   rans_encode_kernel   histogram -> table -> encode (steps 255..0) into a
 //                        per-block slot of a scratch buffer, block size out
-//   rans_scan_kernel     one workgroup: header and exclusive offsets of the blocks
+//   rans_scan_kernel     one workgroup per stream: header and exclusive offsets
 //   rans_compact_kernel  copies each block from its slot (or the raw input) to its
 //                        offset in the stream
-//   rans_decode_kernel   table -> decode (steps 0..1023) -> packed symbols
+//   rans_decode_kernel   table -> decode (steps 0..255) -> packed symbols
 // Division x / f by the 12-bit frequency uses a multiplier and two shifts per symbol
 // (T. Granlund, P. Montgomery, "Division by invariant integers using
 // multiplication", PLDI 1994, fig. 4.1).
@@ -32,9 +34,12 @@ constexpr uint32_t kPB = 12;
 constexpr uint32_t kM = 1u << kPB;
 constexpr uint32_t kLanes = 64;
 constexpr uint32_t kRun = 32;
-constexpr uint32_t kSteps = 1024;
-constexpr uint32_t kRuns = kSteps / kRun;
-constexpr uint32_t kBlock = kLanes * kSteps;
+constexpr uint32_t kSubs = 4;                       // sub-blocks (waves) per block
+constexpr uint32_t kSubSteps = 256;
+constexpr uint32_t kSubRuns = kSubSteps / kRun;     // runs of 32 steps per sub-block
+constexpr uint32_t kSub = kLanes * kSubSteps;       // 16384 symbols
+constexpr uint32_t kBlock = kSub * kSubs;           // 65536 symbols
+constexpr uint32_t kBlockThreads = kLanes * kSubs;  // workgroup of the block kernels
 constexpr uint32_t kStateL = 1u << 16;
 constexpr int kScanThreads = 1024;
 constexpr int kCopyThreads = 256;
@@ -44,12 +49,14 @@ __host__ __device__ constexpr uint64_t pad4(uint64_t b) { return (b + 3u) & ~(ui
 template <int W>
 struct RansGeo {
   static constexpr uint32_t A = 1u << W;
-  static constexpr uint32_t kTab = (uint32_t)pad4(2u * A);       // u16 frequency table
-  static constexpr uint32_t kHead = 4u + kTab + 4u * kLanes;     // tag, table, states
-  static constexpr uint32_t kRawCap = kBlock * W / 8;            // packed bytes of a full block
-  static constexpr uint32_t kGuard = 2u * kLanes * kRun;         // one run of words past the capacity
-  static constexpr uint32_t kSlot = kHead + kGuard + kRawCap;    // scratch bytes per block
-  static constexpr uint32_t kPerLane = A > kLanes ? A / kLanes : 1;
+  static constexpr uint32_t kTab = (uint32_t)pad4(2u * A);                 // u16 frequency table
+  static constexpr uint32_t kCounts = 4u + kTab;                           // u32 count[3] of sub-blocks 1..3
+  static constexpr uint32_t kStates = kCounts + 4u * (kSubs - 1u);         // u32 state[4][64]
+  static constexpr uint32_t kHead = kStates + 4u * kLanes * kSubs;         // tag, table, counts, states
+  static constexpr uint32_t kSubCap = kSub * W / 8;                        // packed bytes of a sub-block
+  static constexpr uint32_t kGuard = 2u * kLanes * kRun;                   // one run of words past the capacity
+  static constexpr uint32_t kRegion = kGuard + kSubCap;                    // word region of a sub-block
+  static constexpr uint32_t kSlot = kHead + kSubs * kRegion;               // scratch bytes per block
 };
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
@@ -67,6 +74,35 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor(v, o, 64));
   return v;
+}
+
+// Sum / max over the block's workgroup (every thread calls; red holds kSubs values).
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t* red) {
+  v = wave_sum(v);
+  if (lane_id() == 0) red[threadIdx.x / kLanes] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < kSubs; ++j) r += red[j];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
+  v = wave_max(v);
+  if (lane_id() == 0) red[threadIdx.x / kLanes] = v;
+  __syncthreads();
+  uint32_t r = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < kSubs; ++j) r = max(r, red[j]);
+  __syncthreads();
+  return r;
+}
+
+// Orders this wave's LDS accesses around a write-then-read by other lanes of the
+// same wave (the wave's LDS instructions execute in issue order).
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 }
 
 // The W dwords of run r of `lane` (32 symbols) of a block whose packed bytes start at
@@ -136,19 +172,22 @@ __device__ __forceinline__ int job_of(const Batch& bt, uint32_t g) {
 }
 
 // ------------------------------------------------------------------ encode
-// Steps 1023..0 of one block (FULL: every lane has a symbol at every step).  Leaves
-// pos < 0 when the words outgrow the capacity (the block is then stored raw).
+// Steps 255..0 of one sub-block whose runs are block runs run0 .. run0 + 7 (FULL:
+// every lane has a symbol at every step).  Leaves pos < 0 when the words outgrow the
+// capacity (the block is then stored raw).
 template <int W, bool FULL>
-__device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, uint32_t lane, uint32_t nb,
-                                            const uint2* tab, uint16_t* words, int32_t& pos, uint32_t& x) {
+__device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, uint32_t run0, uint32_t lane,
+                                            uint32_t nb, const uint2* tab, uint16_t* words, int32_t& pos,
+                                            uint32_t& x) {
   uint32_t d[W], dn[W];
-  load_run<W>(blk, avail, kRuns - 1, lane, d);
-  for (int r = (int)kRuns - 1; r >= 0; --r) {
-    if (r > 0) load_run<W>(blk, avail, (uint32_t)r - 1, lane, dn);  // next run in flight
+  load_run<W>(blk, avail, run0 + kSubRuns - 1, lane, d);
+  for (int r = (int)kSubRuns - 1; r >= 0; --r) {
+    if (r > 0) load_run<W>(blk, avail, run0 + (uint32_t)r - 1, lane, dn);  // next run in flight
+    const uint32_t base = (run0 + (uint32_t)r) * (kLanes * kRun) + lane * kRun;
 #pragma unroll
     for (int j = (int)kRun - 1; j >= 0; --j) {
       const uint32_t s = sym_at<W>(d, j);
-      const bool valid = FULL || (uint32_t)r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
+      const bool valid = FULL || base + (uint32_t)j < nb;
       const uint2 e = tab[s];
       const uint32_t fs = e.x & 0x1fffu;
       const bool emit = valid && (x >> 20) >= fs;
@@ -171,37 +210,42 @@ __device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, 
 }
 
 template <int W>
-__global__ __launch_bounds__(64) void rans_encode_kernel(const EncBatch bt) {
+__global__ __launch_bounds__(kBlockThreads) void rans_encode_kernel(const EncBatch bt) {
   using G = RansGeo<W>;
   constexpr bool kPrivate = W <= 5;  // lane-private histogram columns (no LDS contention)
-  __shared__ __align__(16) uint32_t hist[kPrivate ? G::A * kLanes : G::A];
+  constexpr uint32_t kHist = kPrivate ? G::A * kLanes : G::A;  // per wave
+  __shared__ __align__(16) uint32_t hist[kSubs * kHist];
   __shared__ uint32_t fq[G::A];
   __shared__ uint2 tab[G::A];
+  __shared__ uint32_t red[kSubs];
+  __shared__ int32_t cnt[kSubs];
 
-  const uint32_t lane = lane_id();
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kLanes, t = threadIdx.x;
   const int jb = job_of(bt, blockIdx.x);
   const uint64_t n = bt.n[jb];
   const uint64_t b = blockIdx.x - bt.first[jb];
   const uint64_t first = b * kBlock;
   const uint32_t nb = (uint32_t)min((uint64_t)kBlock, n - first);
-  const bool full = nb == kBlock;
   const uint64_t in_bytes = (n * W + 7) / 8;
   const uint8_t* blk = bt.packed[jb] + first * W / 8;
   const uint64_t avail = in_bytes - first * W / 8;
   uint8_t* slot = bt.slots[jb] + b * G::kSlot;
+  const uint32_t run0 = wave * kSubRuns;                    // this wave's sub-block
+  const bool full = (wave + 1) * kSub <= nb;
 
-  for (uint32_t i = lane; i < (kPrivate ? G::A * kLanes : G::A); i += kLanes) hist[i] = 0;
+  for (uint32_t i = t; i < kSubs * kHist; i += kBlockThreads) hist[i] = 0;
   __syncthreads();
   {
+    uint32_t* h = hist + wave * kHist;
     uint32_t d[W], dn[W];
-    load_run<W>(blk, avail, 0, lane, d);
-    for (uint32_t r = 0; r < kRuns; ++r) {
-      if (r + 1 < kRuns) load_run<W>(blk, avail, r + 1, lane, dn);  // next run in flight
+    load_run<W>(blk, avail, run0, lane, d);
+    for (uint32_t r = 0; r < kSubRuns; ++r) {
+      if (r + 1 < kSubRuns) load_run<W>(blk, avail, run0 + r + 1, lane, dn);  // next run in flight
+      const uint32_t base = (run0 + r) * (kLanes * kRun) + lane * kRun;
 #pragma unroll
       for (int j = 0; j < (int)kRun; ++j) {
         const uint32_t s = sym_at<W>(d, j);
-        if (full || r * (kLanes * kRun) + lane * kRun + j < nb)
-          atomicAdd(&hist[kPrivate ? s * kLanes + lane : s], 1u);
+        if (full || base + (uint32_t)j < nb) atomicAdd(&h[kPrivate ? s * kLanes + lane : s], 1u);
       }
 #pragma unroll
       for (int k = 0; k < W; ++k) d[k] = dn[k];
@@ -209,91 +253,74 @@ __global__ __launch_bounds__(64) void rans_encode_kernel(const EncBatch bt) {
   }
   __syncthreads();
 
-  // counts c[v] for v = lane + 64 m
-  uint32_t c[G::kPerLane];
-#pragma unroll
-  for (uint32_t m = 0; m < G::kPerLane; ++m) {
-    const uint32_t v = lane + kLanes * m;
-    uint32_t sum = 0;
-    if (v < G::A) {
+  // thread v < A: count of symbol v over the block
+  uint32_t c = 0;
+  if (t < G::A) {
+    for (uint32_t j = 0; j < kSubs; ++j) {
       if (kPrivate) {
-        const uint4* row = reinterpret_cast<const uint4*>(&hist[v * kLanes]);
+        const uint4* row = reinterpret_cast<const uint4*>(&hist[j * kHist + t * kLanes]);
         for (int q = 0; q < (int)kLanes / 4; ++q) {
-          const uint4 h = row[q];
-          sum += h.x + h.y + h.z + h.w;
+          const uint4 hv = row[q];
+          c += hv.x + hv.y + hv.z + hv.w;
         }
       } else {
-        sum = hist[v];
+        c += hist[j * kHist + t];
       }
     }
-    c[m] = sum;
   }
-  uint32_t present = 0, key = 0;
-#pragma unroll
-  for (uint32_t m = 0; m < G::kPerLane; ++m) {
-    const uint32_t v = lane + kLanes * m;
-    present += c[m] ? 1u : 0u;
-    if (v < G::A) key = max(key, (c[m] << 8) | (255u - v));  // most frequent, lowest value on ties
-  }
-  const uint32_t K = wave_sum(present);
-  const uint32_t top = 255u - (wave_max(key) & 255u);
-  uint32_t f[G::kPerLane], fsum = 0;
-#pragma unroll
-  for (uint32_t m = 0; m < G::kPerLane; ++m) {
-    f[m] = c[m] ? 1u + c[m] * (kM - K) / nb : 0u;
-    fsum += f[m];
-  }
-  fsum = wave_sum(fsum);
-#pragma unroll
-  for (uint32_t m = 0; m < G::kPerLane; ++m) {
-    const uint32_t v = lane + kLanes * m;
-    if (v == top) f[m] += kM - fsum;
-    if (v < G::A) {
-      fq[v] = f[m];
-      gst16(reinterpret_cast<uint16_t*>(slot + 4) + v, f[m]);
-    }
+  const uint32_t K = block_sum(c ? 1u : 0u, red);
+  // most frequent, lowest value on ties
+  const uint32_t top = 255u - (block_max(t < G::A ? (c << 8) | (255u - t) : 0u, red) & 255u);
+  uint32_t f = c ? 1u + c * (kM - K) / nb : 0u;
+  const uint32_t fsum = block_sum(f, red);
+  if (t == top) f += kM - fsum;
+  if (t < G::A) {
+    fq[t] = f;
+    gst16(reinterpret_cast<uint16_t*>(slot + 4) + t, f);
   }
   __syncthreads();
-#pragma unroll
-  for (uint32_t m = 0; m < G::kPerLane; ++m) {
-    const uint32_t v = lane + kLanes * m;
-    if (v < G::A) {
-      uint32_t cum = 0;
-      for (uint32_t u = 0; u < v; ++u) cum += fq[u];
-      const uint32_t fv = f[m];
-      const uint32_t l = fv <= 1u ? 0u : 32u - __clz(fv - 1u);
-      const uint32_t mul = fv ? (uint32_t)((((uint64_t)((1u << l) - fv)) << 32) / fv + 1u) : 0u;
-      const uint32_t sh1 = l ? 1u : 0u, sh2 = l ? l - 1u : 0u;
-      tab[v] = make_uint2(fv | (cum << 13) | (sh1 << 25) | (sh2 << 26), mul);
-    }
+  if (t < G::A) {
+    uint32_t cum = 0;
+    for (uint32_t u = 0; u < t; ++u) cum += fq[u];
+    const uint32_t l = f <= 1u ? 0u : 32u - __clz(f - 1u);
+    const uint32_t mul = f ? (uint32_t)((((uint64_t)((1u << l) - f)) << 32) / f + 1u) : 0u;
+    const uint32_t sh1 = l ? 1u : 0u, sh2 = l ? l - 1u : 0u;
+    tab[t] = make_uint2(f | (cum << 13) | (sh1 << 25) | (sh2 << 26), mul);
   }
   __syncthreads();
 
-  // encode, steps 1023..0; words fill the slot's word region from its end.  The
+  // encode, steps 255..0; words fill the sub-block's word region from its end.  The
   // capacity is checked once per run: a run emits at most 64 * 32 words, which the
   // guard region in front of the word region absorbs.
-  uint16_t* words = reinterpret_cast<uint16_t*>(slot + G::kHead + G::kGuard);
-  int32_t pos = (int32_t)(G::kRawCap / 2);
+  uint16_t* words = reinterpret_cast<uint16_t*>(slot + G::kHead + wave * G::kRegion + G::kGuard);
+  int32_t pos = (int32_t)(G::kSubCap / 2);
   uint32_t x = kStateL;
-  if (full) encode_runs<W, true>(blk, avail, lane, nb, tab, words, pos, x);
-  else encode_runs<W, false>(blk, avail, lane, nb, tab, words, pos, x);
-  const bool over = pos < 0;
-  const uint32_t count = G::kRawCap / 2 - (uint32_t)pos;
-  const uint64_t raw = 4u + pad4(((uint64_t)nb * W + 7) / 8);
-  const uint64_t size = G::kHead + pad4(2ull * count);
-  uint32_t* sizes = bt.sizes[jb];
-  if (over || size >= raw) {
-    if (lane == 0) {
+  if (full) encode_runs<W, true>(blk, avail, run0, lane, nb, tab, words, pos, x);
+  else encode_runs<W, false>(blk, avail, run0, lane, nb, tab, words, pos, x);
+  const uint32_t count = G::kSubCap / 2 - (uint32_t)pos;  // meaningful when pos >= 0
+  gst(reinterpret_cast<uint32_t*>(slot + G::kStates) + wave * kLanes + lane, x);
+  if (lane == 0) {
+    cnt[wave] = pos < 0 ? -1 : (int32_t)count;
+    if (pos >= 0 && (count & 1u)) gst16(words + pos - 1, 0u);
+  }
+  __syncthreads();
+  if (t == 0) {
+    bool over = false;
+    uint64_t size = G::kHead;
+    for (uint32_t j = 0; j < kSubs; ++j) {
+      over |= cnt[j] < 0;
+      size += pad4(2ull * (uint32_t)max(cnt[j], 0));
+    }
+    const uint64_t raw = 4u + pad4(((uint64_t)nb * W + 7) / 8);
+    uint32_t* sizes = bt.sizes[jb];
+    if (over || size >= raw) {
       gst(reinterpret_cast<uint32_t*>(slot), 1u);
       gst(sizes + b, (uint32_t)raw);
+    } else {
+      gst(reinterpret_cast<uint32_t*>(slot), (uint32_t)cnt[0] << 1);
+      for (uint32_t j = 1; j < kSubs; ++j) gst(reinterpret_cast<uint32_t*>(slot + G::kCounts) + (j - 1), (uint32_t)cnt[j]);
+      gst(sizes + b, (uint32_t)size);
     }
-    return;
-  }
-  gst(reinterpret_cast<uint32_t*>(slot + 4 + G::kTab) + lane, x);
-  if (lane == 0) {
-    gst(reinterpret_cast<uint32_t*>(slot), count << 1);
-    if (count & 1u) gst16(words + pos - 1, 0u);
-    gst(sizes + b, (uint32_t)size);
   }
 }
 
@@ -330,7 +357,7 @@ __global__ __launch_bounds__(kScanThreads) void rans_scan_kernel(const EncBatch 
     const uint64_t payload = part[t];
     uint32_t* h = reinterpret_cast<uint32_t*>(out);
     gst(h + 0, kRansMagic);
-    gst(h + 1, 1u | ((uint32_t)W << 8) | (kPB << 16) | (6u << 24));
+    gst(h + 1, 2u | ((uint32_t)W << 8) | (kPB << 16) | (8u << 24));
     gst(h + 2, kBlock);
     gst(h + 3, nblk);
     gst(reinterpret_cast<uint64_t*>(out + 16), n);
@@ -373,16 +400,20 @@ __global__ __launch_bounds__(kCopyThreads) void rans_compact_kernel(const EncBat
     }
     return;
   }
-  const uint32_t count = tag >> 1;
-  const uint32_t wbytes = (uint32_t)pad4(2ull * count);
   const uint32_t* head = reinterpret_cast<const uint32_t*>(slot);
   for (uint32_t i = t; i < G::kHead / 4; i += kCopyThreads) gst(dst + i, gld(head + i));
-  const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(slot + G::kSlot - wbytes);
-  for (uint32_t i = t; i < wbytes / 4; i += kCopyThreads) gst(dst + G::kHead / 4 + i, gld(wsrc + i));
+  uint32_t at = G::kHead / 4;
+  for (uint32_t j = 0; j < kSubs; ++j) {
+    const uint32_t count = j ? gld(reinterpret_cast<const uint32_t*>(slot + G::kCounts) + (j - 1)) : tag >> 1;
+    const uint32_t wbytes = (uint32_t)pad4(2ull * count);
+    const uint32_t* wsrc = reinterpret_cast<const uint32_t*>(slot + G::kHead + (j + 1) * G::kRegion - wbytes);
+    for (uint32_t i = t; i < wbytes / 4; i += kCopyThreads) gst(dst + at + i, gld(wsrc + i));
+    at += wbytes / 4;
+  }
 }
 
 // ------------------------------------------------------------------ decode
-// The block's words are staged through a per-wave LDS ring of kRing 16-bit units,
+// A sub-block's words are staged through its wave's LDS ring of kRing 16-bit units,
 // refilled 256 units at a time (two coalesced dword loads per lane) so that a step
 // reads its words from LDS instead of waiting on a dependent global load.
 constexpr uint32_t kRing = 512;
@@ -403,33 +434,35 @@ __device__ __forceinline__ void ring_fill(uint16_t* ring, const uint32_t* region
     rp[1] = w1;
     filled += kRefill;
   } while (filled < want && filled < units);
-  __syncthreads();
+  wave_lds_fence();
 }
 
-// Steps 0..1023 of one block; returns the final state.  Before each group of
-// kGroup steps (at most 64 * kGroup words) the ring holds at least that many
-// unread units.  A refill pass starts only while fewer than 64 * kGroup units are
-// staged past q, and kRing >= 64 * kGroup + kRefill, so it overwrites only units
-// below q.
+// Steps 0..255 of one sub-block (block runs run0 .. run0 + 7); returns the final
+// state.  Before each group of kGroup steps (at most 64 * kGroup words) the ring
+// holds at least that many unread units.  A refill pass starts only while fewer
+// than 64 * kGroup units are staged past q, and kRing >= 64 * kGroup + kRefill, so
+// it overwrites only units below q.
 constexpr uint32_t kGroup = 4;
 static_assert(kRing >= kGroup * kLanes + kRefill, "ring too small for the refill policy");
 
 template <int W, bool FULL>
 __device__ __forceinline__ uint32_t decode_runs(const uint32_t* region, uint32_t units, uint32_t& q,
                                                 const uint8_t* slot_sym, const uint32_t* sym_fc, uint16_t* ring,
-                                                uint8_t* dst, uint64_t room, uint32_t nb, uint32_t lane, uint32_t x) {
+                                                uint8_t* dst, uint64_t room, uint32_t nb, uint32_t run0, uint32_t lane,
+                                                uint32_t x) {
   uint32_t filled = 0;
-  for (uint32_t r = 0; r < kRuns; ++r) {
+  for (uint32_t r = run0; r < run0 + kSubRuns; ++r) {
     uint32_t acc[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) acc[k] = 0;
+    const uint32_t base = r * (kLanes * kRun) + lane * kRun;
 #pragma unroll
     for (int g = 0; g < (int)(kRun / kGroup); ++g) {
       ring_fill(ring, region, units, filled, q + kGroup * kLanes, lane);
 #pragma unroll
       for (int jj = 0; jj < (int)kGroup; ++jj) {
         const int j = g * (int)kGroup + jj;
-        const bool valid = FULL || r * (kLanes * kRun) + lane * kRun + (uint32_t)j < nb;
+        const bool valid = FULL || base + (uint32_t)j < nb;
         const uint32_t slot = x & (kM - 1u);
         const uint32_t s = slot_sym[slot];
         const uint32_t fc = sym_fc[s];
@@ -462,14 +495,15 @@ __device__ __forceinline__ uint32_t decode_runs(const uint32_t* region, uint32_t
 }
 
 template <int W>
-__global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int32_t* __restrict__ err) {
+__global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBatch bt, int32_t* __restrict__ err) {
   using G = RansGeo<W>;
   __shared__ uint8_t slot_sym[kM];
   __shared__ uint32_t sym_fc[G::A];
   __shared__ uint32_t fq[G::A];
-  __shared__ __align__(16) uint16_t ring[kRing];
+  __shared__ uint32_t red[kSubs];
+  __shared__ __align__(16) uint16_t rings[kSubs][kRing];
 
-  const uint32_t lane = lane_id();
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kLanes, t = threadIdx.x;
   const int jb = job_of(bt, blockIdx.x);
   const uint64_t n = bt.n[jb];
   const uint64_t b = blockIdx.x - bt.first[jb];
@@ -479,17 +513,18 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
   const uint32_t* h = reinterpret_cast<const uint32_t*>(in);
   const uint64_t payload = gld(reinterpret_cast<const uint64_t*>(in + 24));
   const uint64_t head = 32u + 8ull * nblk;
-  if (gld(h) != kRansMagic || gld(h + 1) != (1u | ((uint32_t)W << 8) | (kPB << 16) | (6u << 24)) ||
+  // every check below is uniform over the workgroup (it reads the same bytes)
+  if (gld(h) != kRansMagic || gld(h + 1) != (2u | ((uint32_t)W << 8) | (kPB << 16) | (8u << 24)) ||
       gld(h + 2) != kBlock || gld(h + 3) != nblk || gld(reinterpret_cast<const uint64_t*>(in + 16)) != n ||
       in_bytes != head + payload) {
-    if (lane == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
+    if (t == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
     return;
   }
   const uint64_t* offs = reinterpret_cast<const uint64_t*>(in + 32);
   const uint64_t o = gld(offs + b);
   const uint64_t e = b + 1 == nblk ? payload : gld(offs + b + 1);
   if (o > e || e > payload || e - o < 4 || (o & 3u)) {
-    if (lane == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
+    if (t == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
     return;
   }
   const uint8_t* blk = in + head + o;
@@ -503,11 +538,11 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
   if (tag & 1u) {
     const uint64_t rb = ((uint64_t)nb * W + 7) / 8;
     if (e - o != 4u + pad4(rb)) {
-      if (lane == 0) atomicOr(err, KVMI_ERR_CORRUPT);
+      if (t == 0) atomicOr(err, KVMI_ERR_CORRUPT);
       return;
     }
     const uint32_t* src = reinterpret_cast<const uint32_t*>(blk + 4);
-    for (uint64_t i = lane; i < pad4(rb) / 4; i += kLanes) {
+    for (uint64_t i = t; i < pad4(rb) / 4; i += kBlockThreads) {
       const uint32_t v = gld(src + i);
       if (4 * i + 4 <= room) {
         gst(reinterpret_cast<uint32_t*>(dst) + i, v);
@@ -518,32 +553,34 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
     }
     return;
   }
-  const uint32_t count = tag >> 1;
-  if (e - o != G::kHead + pad4(2ull * count)) {
-    if (lane == 0) atomicOr(err, KVMI_ERR_CORRUPT);
+  uint32_t count[kSubs];
+  uint64_t size = G::kHead;
+#pragma unroll
+  for (uint32_t j = 0; j < kSubs; ++j) {
+    count[j] = j ? gld(reinterpret_cast<const uint32_t*>(blk + G::kCounts) + (j - 1)) : tag >> 1;
+    size += pad4(2ull * count[j]);
+  }
+  if (e - o != size) {
+    if (t == 0) atomicOr(err, KVMI_ERR_CORRUPT);
     return;
   }
   const uint16_t* ftab = reinterpret_cast<const uint16_t*>(blk + 4);
-  uint32_t fsum = 0;
-  for (uint32_t v = lane; v < G::A; v += kLanes) {
-    const uint32_t fv = gld(ftab + v);
-    fq[v] = fv;
-    fsum += fv;
-  }
-  if (wave_sum(fsum) != kM) {
-    if (lane == 0) atomicOr(err, KVMI_ERR_CORRUPT);
+  const uint32_t fv = t < G::A ? gld(ftab + t) : 0u;
+  if (t < G::A) fq[t] = fv;
+  if (block_sum(fv, red) != kM) {
+    if (t == 0) atomicOr(err, KVMI_ERR_CORRUPT);
     return;
   }
-  __syncthreads();
-  for (uint32_t v = lane; v < G::A; v += kLanes) {
+  if (t < G::A) {
     uint32_t cum = 0;
-    for (uint32_t u = 0; u < v; ++u) cum += fq[u];
-    sym_fc[v] = fq[v] | (cum << 13);
+    for (uint32_t u = 0; u < t; ++u) cum += fq[u];
+    sym_fc[t] = fq[t] | (cum << 13);
   }
   __syncthreads();
-  // slot -> symbol: lane i fills slots [64 i, 64 i + 64), walking the cumulative table
+  // slot -> symbol: thread i fills slots [16 i, 16 i + 16), walking the cumulative table
   {
-    const uint32_t s0 = lane * (kM / kLanes);
+    constexpr uint32_t kPer = kM / kBlockThreads;
+    const uint32_t s0 = t * kPer;
     // the symbol of slot s is the last v with cum_v <= s (cum is non-decreasing, and
     // an absent symbol shares its cum with the next one, so it is never the last)
     uint32_t lo = 0, hi = G::A - 1;
@@ -554,7 +591,7 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
     }
     uint32_t v = lo;
     uint32_t end = (sym_fc[v] >> 13) + (sym_fc[v] & 0x1fffu);
-    for (uint32_t s = s0; s < s0 + kM / kLanes; ++s) {
+    for (uint32_t s = s0; s < s0 + kPer; ++s) {
       while (s >= end) {
         ++v;
         end = (sym_fc[v] >> 13) + (sym_fc[v] & 0x1fffu);
@@ -562,16 +599,23 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
       slot_sym[s] = (uint8_t)v;
     }
   }
-
-  uint32_t x = gld(reinterpret_cast<const uint32_t*>(blk + 4 + G::kTab) + lane);
-  // word region: pad4(2 count) bytes, the words at its end; q counts 16-bit units
-  // from the region start, word p of the block is unit q = lead + p
-  const uint32_t* region = reinterpret_cast<const uint32_t*>(blk + G::kHead);
-  const uint32_t units = (uint32_t)(pad4(2ull * count) / 2);
-  uint32_t q = units - count;
   __syncthreads();
-  if (nb == kBlock) x = decode_runs<W, true>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, lane, x);
-  else x = decode_runs<W, false>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, lane, x);
+
+  // sub-block `wave`: its states, and its word region (pad4(2 count) bytes, the words
+  // at its end; q counts 16-bit units from the region start)
+  uint32_t x = gld(reinterpret_cast<const uint32_t*>(blk + G::kStates) + wave * kLanes + lane);
+  uint64_t region_off = G::kHead;
+#pragma unroll
+  for (uint32_t j = 0; j < kSubs; ++j)
+    if (j < wave) region_off += pad4(2ull * count[j]);
+  const uint32_t cw = count[0] * (wave == 0) + count[1] * (wave == 1) + count[2] * (wave == 2) + count[3] * (wave == 3);
+  const uint32_t* region = reinterpret_cast<const uint32_t*>(blk + region_off);
+  const uint32_t units = (uint32_t)(pad4(2ull * cw) / 2);
+  uint32_t q = units - cw;
+  const uint32_t run0 = wave * kSubRuns;
+  uint16_t* ring = rings[wave];
+  if ((wave + 1) * kSub <= nb) x = decode_runs<W, true>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, run0, lane, x);
+  else x = decode_runs<W, false>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, run0, lane, x);
   // a stream that is not this block's own encoding ends off its start state or
   // off the end of its words (ring reads are masked, so none leaves the ring)
   const bool ok = q == units && x == kStateL;
@@ -581,7 +625,7 @@ __global__ __launch_bounds__(64) void rans_decode_kernel(const DecBatch bt, int3
 template <int W>
 int rans_encode_w(const EncBatch& bt, hipStream_t stream) {
   const uint32_t total = bt.first[bt.count];
-  if (total) hipLaunchKernelGGL(rans_encode_kernel<W>, dim3(total), dim3(64), 0, stream, bt);
+  if (total) hipLaunchKernelGGL(rans_encode_kernel<W>, dim3(total), dim3(kBlockThreads), 0, stream, bt);
   hipLaunchKernelGGL(rans_scan_kernel<W>, dim3(bt.count), dim3(kScanThreads), 0, stream, bt);
   if (total) hipLaunchKernelGGL(rans_compact_kernel<W>, dim3(total), dim3(kCopyThreads), 0, stream, bt);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
@@ -590,12 +634,13 @@ int rans_encode_w(const EncBatch& bt, hipStream_t stream) {
 template <int W>
 int rans_decode_w(const DecBatch& bt, int32_t* err, hipStream_t stream) {
   const uint32_t total = bt.first[bt.count];
-  if (total) hipLaunchKernelGGL(rans_decode_kernel<W>, dim3(total), dim3(64), 0, stream, bt, err);
+  if (total) hipLaunchKernelGGL(rans_decode_kernel<W>, dim3(total), dim3(kBlockThreads), 0, stream, bt, err);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
 uint64_t slot_bytes(int w) {
-  return 4u + pad4(2u << w) + 4u * kLanes + 2u * kLanes * kRun + (uint64_t)kBlock * w / 8;
+  const uint64_t head = 4u + pad4(2u << w) + 4u * (kSubs - 1u) + 4u * kLanes * kSubs;
+  return head + kSubs * (2u * kLanes * kRun + (uint64_t)kSub * w / 8);
 }
 
 }  // namespace

@@ -66,10 +66,12 @@ struct RtIdx {
   uint32_t tok;
 };
 
+// rows * layers <= 2^31 (checked on the host): 32-bit index arithmetic throughout
 __device__ __forceinline__ RtIdx rt_idx(uint64_t rows) {
   RtIdx r;
-  r.layer = (uint32_t)(blockIdx.x / rows);
-  r.row = blockIdx.x % rows;
+  const uint32_t n = (uint32_t)rows;
+  r.layer = blockIdx.x / n;
+  r.row = blockIdx.x - r.layer * n;
   return r;
 }
 
@@ -86,8 +88,8 @@ __global__ __launch_bounds__(kRtThreads) void rt_transform_kernel(kvmi_rt_geomet
   constexpr int HPW = D >= 64 ? 1 : 64 / D;  // head rows per wave pass
   const RtIdx ix = rt_idx(rows);
   const kvmi_rt_layer L = layers[ix.layer];
-  const uint64_t blk = ix.row / (uint64_t)g.kernel_tokens;
-  const uint32_t tok = (uint32_t)(ix.row % (uint64_t)g.kernel_tokens);
+  const uint32_t blk = (uint32_t)ix.row / (uint32_t)g.kernel_tokens;
+  const uint32_t tok = (uint32_t)ix.row - blk * (uint32_t)g.kernel_tokens;
   const int64_t pb = gld(block_ids + blk);
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint16_t* cache = static_cast<const uint16_t*>(L.cache);
@@ -280,8 +282,8 @@ __global__ __launch_bounds__(kRtThreads) void rt_decode_kernel(kvmi_rt_geometry 
   constexpr int HPW = D >= 64 ? 1 : 64 / D;
   const RtIdx ix = rt_idx(rows);
   const kvmi_rt_layer L = layers[ix.layer];
-  const uint64_t blk = ix.row / (uint64_t)g.kernel_tokens;
-  const uint32_t tok = (uint32_t)(ix.row % (uint64_t)g.kernel_tokens);
+  const uint32_t blk = (uint32_t)ix.row / (uint32_t)g.kernel_tokens;
+  const uint32_t tok = (uint32_t)ix.row - blk * (uint32_t)g.kernel_tokens;
   const int64_t pb = gld(block_ids + blk);
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   uint16_t* cache = static_cast<uint16_t*>(L.cache);
@@ -368,7 +370,7 @@ struct RowGeo {
 };
 
 constexpr int kStatRows = 64;     // rows per workgroup of the statistics pass
-constexpr int kMaxRowCols = 4096; // H * D held by one wave (<= 64 values per lane)
+constexpr int kMaxRowCols = 2048; // H * D held by one wave (<= 32 values per lane)
 
 template <int E>
 __device__ __forceinline__ void ld_seg(const uint16_t* p, float (&v)[E], bool vec) {
@@ -458,9 +460,52 @@ __device__ __forceinline__ void mul_signs(float (&v)[E], const uint16_t* s) {
   for (int k = 0; k < E; ++k) v[k] = __uint_as_float(__float_as_uint(v[k]) ^ (__float_as_uint(sg[k]) & 0x80000000u));
 }
 
+// x and y rounded to bf16 with one conversion instruction
+__device__ __forceinline__ void rn2(float& x, float& y) {
+  const uint32_t p = pack_bf16x2(x, y);
+  x = bf_lo(p);
+  y = bf_hi(p);
+}
+
+// Value of lane (lane ^ J): DPP for J = 1, 2 (quad_perm) and 8 (row_ror:8 within a
+// 16-lane row), ds_swizzle bit masks for 4 and 16, bpermute beyond.
+template <int J>
+__device__ __forceinline__ float lane_xor(float x) {
+  if constexpr (J == 1) {
+    return dpp_f<0xB1>(x);
+  } else if constexpr (J == 2) {
+    return dpp_f<0x4E>(x);
+  } else if constexpr (J == 8) {
+    return dpp_f<0x128>(x);
+  } else if constexpr (J == 4 || J == 16) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1F | (J << 10)));
+  } else {
+    return __shfl_xor(x, J, 64);
+  }
+}
+
+// Butterfly stages across lanes J, 2J, .. < LH: the lane with bit J clear holds the
+// lower element a and gets a + b, the other gets a - b = partner - own; fma(v, +-1, o)
+// is that sum with one fp32 rounding, then bf16.
+template <int J, int LH, int P, int E>
+__device__ __forceinline__ void fwht_cross(float (&v)[P][E], uint32_t lane) {
+  if constexpr (J < LH) {
+    const float sgn = (lane & J) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+#pragma unroll
+      for (int k = 0; k < E; ++k) v[p][k] = __builtin_fmaf(v[p][k], sgn, lane_xor<J>(v[p][k]));
+#pragma unroll
+      for (int k = 0; k < E; k += 2) rn2(v[p][k], v[p][k + 1]);
+    }
+    fwht_cross<J * 2, LH, P, E>(v, lane);
+  }
+}
+
 template <int D, int P>
 __device__ __forceinline__ void fwht_rows(float (&v)[P][RowGeo<D>::E], uint32_t lane, float scale) {
   constexpr int E = RowGeo<D>::E, LH = RowGeo<D>::LH;
+  static_assert(E % 2 == 0, "pairs of elements per lane");
 #pragma unroll
   for (int m = 1; m < E; m <<= 1) {
 #pragma unroll
@@ -469,27 +514,22 @@ __device__ __forceinline__ void fwht_rows(float (&v)[P][RowGeo<D>::E], uint32_t 
       for (int k = 0; k < E; ++k) {
         if (k & m) continue;
         const float a = v[p][k], b = v[p][k | m];
-        v[p][k] = rn(a + b);
-        v[p][k | m] = rn(a - b);
+        v[p][k] = a + b;
+        v[p][k | m] = a - b;
+        rn2(v[p][k], v[p][k | m]);
       }
     }
   }
+  fwht_cross<1, LH, P, E>(v, lane);
 #pragma unroll
-  for (int j = 1; j < LH; j <<= 1) {
-    const bool hi = lane & j;
+  for (int p = 0; p < P; ++p) {
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-#pragma unroll
-      for (int k = 0; k < E; ++k) {
-        const float o = __shfl_xor(v[p][k], j, 64);
-        v[p][k] = rn(hi ? o - v[p][k] : v[p][k] + o);
-      }
+    for (int k = 0; k < E; k += 2) {
+      v[p][k] *= scale;
+      v[p][k + 1] *= scale;
+      rn2(v[p][k], v[p][k + 1]);
     }
   }
-#pragma unroll
-  for (int p = 0; p < P; ++p)
-#pragma unroll
-    for (int k = 0; k < E; ++k) v[p][k] = rn(v[p][k] * scale);
 }
 
 struct RowLane {
@@ -505,31 +545,93 @@ __device__ __forceinline__ RowLane row_lane() {
   return r;
 }
 
-// gather -> signs -> [FWHT] of canonical row `row` of layer L into v (output-head order)
+// Rows whose loads a wave issues together: 4 rows of one pass, fewer for wider rows
+// (the values of R rows x P passes stay in registers).
+template <int P>
+constexpr int rows_per_wave() { return P >= 4 ? 1 : 4 / P; }
+
+// Per-wave constants of one layer: the cache head of each pass (-1: no head in this
+// slot) and the signs of the lane's channels.
 template <int D, int P>
-__device__ __forceinline__ void load_row(const kvmi_rt_geometry& g, const kvmi_rt_layer& L, const int64_t* block_ids,
-                                         uint64_t row, const RowLane& rl, float (&v)[P][RowGeo<D>::E], bool vec,
-                                         float scale) {
+struct LayerLanes {
+  int hc[P];
+  float sg[P][RowGeo<D>::E];
+};
+
+template <int D, int P>
+__device__ __forceinline__ void layer_lanes(const kvmi_rt_geometry& g, const kvmi_rt_layer& L, const RowLane& rl,
+                                            LayerLanes<D, P>& c) {
   constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
-  const uint64_t blk = row / (uint64_t)g.kernel_tokens;
-  const uint32_t tok = (uint32_t)(row % (uint64_t)g.kernel_tokens);
-  const int64_t pb = gld(block_ids + blk);
-  const uint16_t* cache = static_cast<const uint16_t*>(L.cache) + pb * L.block_stride +
-                          (int64_t)tok * L.token_stride + L.channel_offset + rl.sub * E;
   const uint16_t* signs = static_cast<const uint16_t*>(L.signs);
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int h = p * HPW + (int)rl.slot;
-    if (h < g.num_heads) {
-      const int hc = gld(L.head_order + h);
-      ld_seg<E>(cache + (int64_t)hc * L.head_stride, v[p], vec);
-      if (signs) mul_signs<E>(v[p], signs + (int64_t)h * D + rl.sub * E);
+    c.hc[p] = h < g.num_heads ? gld(L.head_order + h) : -1;
+    if (signs && h < g.num_heads) {
+      ld_seg<E>(signs + (int64_t)h * D + rl.sub * E, c.sg[p], true);
     } else {
 #pragma unroll
-      for (int k = 0; k < E; ++k) v[p][k] = 0.0f;
+      for (int k = 0; k < E; ++k) c.sg[p][k] = 1.0f;
     }
   }
-  if (g.flags & KVMI_RT_TRANSFORM) fwht_rows<D, P>(v, rl.lane, scale);
+}
+
+// Physical block and token of row row0 + lane (lanes < n), for the rows a wave
+// handles; lane j's pair is broadcast when row j is processed.
+struct RowRef {
+  int64_t pb;
+  uint32_t tok;
+};
+
+__device__ __forceinline__ RowRef row_ref(const kvmi_rt_geometry& g, const int64_t* block_ids, uint32_t row0,
+                                          uint32_t n, uint32_t lane) {
+  RowRef r = {0, 0};
+  if (lane < n) {
+    const uint32_t row = row0 + lane, kt = (uint32_t)g.kernel_tokens;
+    const uint32_t blk = row / kt;
+    r.tok = row - blk * kt;
+    r.pb = gld(block_ids + blk);
+  }
+  return r;
+}
+
+// gather -> signs -> [FWHT] of rows row0 .. row0 + n - 1 (n <= R) into v, in output-head
+// order; `pbl` holds the rows' physical blocks in lanes 0 .. n - 1.  The cache loads of
+// all R rows are issued before any of them is used.
+template <int D, int P, int R>
+__device__ __forceinline__ void load_rows(const kvmi_rt_geometry& g, const kvmi_rt_layer& L,
+                                          const LayerLanes<D, P>& c, const RowRef& ref, uint32_t n,
+                                          const RowLane& rl, float (&v)[R][P][RowGeo<D>::E], bool vec, float scale) {
+  constexpr int E = RowGeo<D>::E;
+  const uint16_t* base = static_cast<const uint16_t*>(L.cache) + L.channel_offset + rl.sub * E;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int64_t pb = __shfl(ref.pb, j, 64);
+    const uint32_t tok = (uint32_t)__shfl((int)ref.tok, j, 64);
+    const uint16_t* row = base + pb * L.block_stride + (int64_t)tok * L.token_stride;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if ((uint32_t)j < n && c.hc[p] >= 0) {
+        ld_seg<E>(row + (int64_t)c.hc[p] * L.head_stride, v[j][p], vec);
+      } else {
+#pragma unroll
+        for (int k = 0; k < E; ++k) v[j][p][k] = 0.0f;
+      }
+    }
+  }
+  if (L.signs) {
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+          v[j][p][k] = __uint_as_float(__float_as_uint(v[j][p][k]) ^ (__float_as_uint(c.sg[p][k]) & 0x80000000u));
+  }
+  if (g.flags & KVMI_RT_TRANSFORM) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) fwht_rows<D, P>(v[j], rl.lane, scale);
+  }
 }
 
 __device__ __forceinline__ float wave_min(float x) {
@@ -544,32 +646,47 @@ __device__ __forceinline__ float wave_max(float x) {
 }
 
 // Statistics pass: per-workgroup min / max of every column of the layer's rows
-// [r0, r0 + kStatRows), written as fp32 partials [layer][workgroup][2][cols].
+// [r0, r0 + kStatRows), written as fp32 partials [layer][workgroup][2][cols].  Each
+// wave takes kStatRows / 4 consecutive rows, rows_per_wave at a time.
 template <int D, int P>
 __global__ __launch_bounds__(kRtThreads) void rt_stats_kernel(kvmi_rt_geometry g, const kvmi_rt_layer* __restrict__ layers,
                                                               const int64_t* __restrict__ block_ids, uint64_t rows,
                                                               float* __restrict__ partial, uint32_t wgs_per_layer,
                                                               bool vec, float scale) {
-  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW, R = rows_per_wave<P>();
+  constexpr uint32_t kWaveRows = kStatRows / kRtWaves;
+  static_assert(kWaveRows <= 64 && kWaveRows % R == 0, "one block id per lane");
   __shared__ float smn[kMaxRowCols], smx[kMaxRowCols];
   const uint32_t layer = blockIdx.x / wgs_per_layer, wg = blockIdx.x % wgs_per_layer;
   const kvmi_rt_layer L = layers[layer];
   const RowLane rl = row_lane<D>();
   const uint32_t wave = threadIdx.x >> 6;
-  const uint64_t r0 = (uint64_t)wg * kStatRows;
-  const uint64_t r1 = r0 + kStatRows < rows ? r0 + kStatRows : rows;
+  LayerLanes<D, P> c;
+  layer_lanes<D, P>(g, L, rl, c);
+  const uint32_t nrows = (uint32_t)rows;
+  const uint32_t r0 = wg * kStatRows + wave * kWaveRows;
+  const uint32_t nw = r0 < nrows ? min(kWaveRows, nrows - r0) : 0u;
+  const RowRef all = row_ref(g, block_ids, r0, nw, rl.lane);
   float mn[P][E], mx[P][E];
 #pragma unroll
   for (int p = 0; p < P; ++p)
 #pragma unroll
     for (int k = 0; k < E; ++k) mn[p][k] = INFINITY, mx[p][k] = -INFINITY;
-  for (uint64_t r = r0 + wave; r < r1; r += kRtWaves) {
-    float v[P][E];
-    load_row<D, P>(g, L, block_ids, r, rl, v, vec, scale);
+  for (uint32_t i = 0; i < nw; i += R) {
+    const uint32_t n = min((uint32_t)R, nw - i);
+    RowRef ref;  // lane j: row r0 + i + j
+    ref.pb = __shfl(all.pb, (int)((rl.lane + i) & 63u), 64);
+    ref.tok = (uint32_t)__shfl((int)all.tok, (int)((rl.lane + i) & 63u), 64);
+    float v[R][P][E];
+    load_rows<D, P, R>(g, L, c, ref, n, rl, v, vec, scale);
 #pragma unroll
-    for (int p = 0; p < P; ++p)
+    for (int j = 0; j < R; ++j) {
+      if ((uint32_t)j >= n) break;
 #pragma unroll
-      for (int k = 0; k < E; ++k) mn[p][k] = fminf(mn[p][k], v[p][k]), mx[p][k] = fmaxf(mx[p][k], v[p][k]);
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int k = 0; k < E; ++k) mn[p][k] = fminf(mn[p][k], v[j][p][k]), mx[p][k] = fmaxf(mx[p][k], v[j][p][k]);
+    }
   }
   const uint32_t cols = (uint32_t)g.num_heads * D;
   for (uint32_t w = 0; w < (uint32_t)kRtWaves; ++w) {
@@ -580,18 +697,18 @@ __global__ __launch_bounds__(kRtThreads) void rt_stats_kernel(kvmi_rt_geometry g
         if (h >= g.num_heads) continue;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-          const uint32_t c = (uint32_t)h * D + rl.sub * E + k;
-          smn[c] = w ? fminf(smn[c], mn[p][k]) : mn[p][k];
-          smx[c] = w ? fmaxf(smx[c], mx[p][k]) : mx[p][k];
+          const uint32_t col = (uint32_t)h * D + rl.sub * E + k;
+          smn[col] = w ? fminf(smn[col], mn[p][k]) : mn[p][k];
+          smx[col] = w ? fmaxf(smx[col], mx[p][k]) : mx[p][k];
         }
       }
     }
     __syncthreads();
   }
   float* out = partial + ((uint64_t)layer * wgs_per_layer + wg) * 2 * cols;
-  for (uint32_t c = threadIdx.x; c < cols; c += kRtThreads) {
-    gst(out + c, smn[c]);
-    gst(out + cols + c, smx[c]);
+  for (uint32_t col = threadIdx.x; col < cols; col += kRtThreads) {
+    gst(out + col, smn[col]);
+    gst(out + cols + col, smx[col]);
   }
 }
 
@@ -609,7 +726,18 @@ __global__ __launch_bounds__(kRtThreads) void rt_stats_reduce_kernel(kvmi_rt_geo
   const float* base = partial + (uint64_t)layer * wgs_per_layer * 2 * cols;
   for (uint32_t c = threadIdx.x; c < cols; c += kRtThreads) {
     float mn = INFINITY, mx = -INFINITY;
-    for (uint32_t w = 0; w < wgs_per_layer; ++w) {
+    uint32_t w = 0;
+    for (; w + 8 <= wgs_per_layer; w += 8) {  // eight partials in flight
+      float a[8], b[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        a[u] = gld(base + (uint64_t)(w + u) * 2 * cols + c);
+        b[u] = gld(base + (uint64_t)(w + u) * 2 * cols + cols + c);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) mn = fminf(mn, a[u]), mx = fmaxf(mx, b[u]);
+    }
+    for (; w < wgs_per_layer; ++w) {
       mn = fminf(mn, gld(base + (uint64_t)w * 2 * cols + c));
       mx = fmaxf(mx, gld(base + (uint64_t)w * 2 * cols + cols + c));
     }
@@ -648,160 +776,263 @@ __global__ __launch_bounds__(kRtThreads) void rt_stats_reduce_kernel(kvmi_rt_geo
     }
 }
 
-// Encode pass: one wave per (layer, row).  Quantized: token sections reduce inside
-// the wave, channel / tensor sections read their parameters from aux; the u8 symbols
-// land at the layer's u8_offset.  Not quantized: the bf16 rows are the payload.
+// Quantization parameters of a lane's channels for a channel / tensor section (read
+// from aux, constant over the layer's rows), or unused for a token section.
+template <int D, int P>
+struct LaneParams {
+  float mn[P][RowGeo<D>::E], inv[P][RowGeo<D>::E];
+};
+
+// Encode pass: a wave takes rows_per_wave consecutive rows of one layer.  Quantized:
+// token sections reduce inside the wave, channel / tensor sections read their
+// parameters from aux; the u8 symbols land at the layer's u8_offset.  Not quantized:
+// the bf16 rows are the payload.
 template <int D, int P>
 __global__ __launch_bounds__(kRtThreads) void rt_row_encode_kernel(kvmi_rt_geometry g, const kvmi_rt_layer* __restrict__ layers,
                                                                    const int64_t* __restrict__ block_ids, uint64_t rows,
                                                                    uint32_t num_layers, uint8_t* __restrict__ packed,
                                                                    uint8_t* __restrict__ aux, uint64_t half, bool vec,
                                                                    float scale) {
-  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
-  const uint64_t task = (uint64_t)blockIdx.x * kRtWaves + (threadIdx.x >> 6);
-  const uint64_t tasks = rows * (uint64_t)num_layers;
-  if (task >= tasks) return;  // wave-uniform
-  const uint32_t layer = (uint32_t)(task / rows);
-  const uint64_t row = task % rows;
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW, R = rows_per_wave<P>();
+  const uint32_t nrows = (uint32_t)rows, groups = (nrows + R - 1) / R;
+  const uint32_t task = blockIdx.x * kRtWaves + (threadIdx.x >> 6);
+  if (task >= groups * num_layers) return;  // wave-uniform
+  const uint32_t layer = task / groups;
+  const uint32_t row0 = (task - layer * groups) * R;
+  const uint32_t n = min((uint32_t)R, nrows - row0);
   const kvmi_rt_layer L = layers[layer];
   const RowLane rl = row_lane<D>();
-  float v[P][E];
-  load_row<D, P>(g, L, block_ids, row, rl, v, vec, scale);
+  LayerLanes<D, P> c;
+  layer_lanes<D, P>(g, L, rl, c);
+  const RowRef ref = row_ref(g, block_ids, row0, n, rl.lane);
+  float v[R][P][E];
+  load_rows<D, P, R>(g, L, c, ref, n, rl, v, vec, scale);
   const uint64_t cols = (uint64_t)g.num_heads * D;
   if (!(g.flags & KVMI_RT_QUANTIZE)) {
-    uint16_t* out = reinterpret_cast<uint16_t*>(packed) + L.u8_offset + row * cols + rl.sub * E;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int h = p * HPW + (int)rl.slot;
-      if (h < g.num_heads) st_seg<E>(out + (int64_t)h * D, v[p], true);
+    for (int j = 0; j < R; ++j) {
+      if ((uint32_t)j >= n) break;
+      uint16_t* out = reinterpret_cast<uint16_t*>(packed) + L.u8_offset + (row0 + j) * cols + rl.sub * E;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int h = p * HPW + (int)rl.slot;
+        if (h < g.num_heads) st_seg<E>(out + (int64_t)h * D, v[j][p], true);
+      }
     }
     return;
   }
-  // token-axis statistics of the row, per section (two named sections: a local array
-  // indexed by a run-time section number would live in scratch memory)
-  float tmin0 = INFINITY, tmin1 = INFINITY, tmax0 = -INFINITY, tmax1 = -INFINITY;
+  // channel / tensor parameters of the lane's channels
+  LaneParams<D, P> lp;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int h = p * HPW + (int)rl.slot;
-    if (h >= g.num_heads) continue;
-    float a = INFINITY, b = -INFINITY;
+    const kvmi_rt_section s = (h < g.num_heads && section_of(L, h)) ? L.sections[1] : L.sections[0];
+    if (h >= g.num_heads || s.axis == 1) {
 #pragma unroll
-    for (int k = 0; k < E; ++k) a = fminf(a, v[p][k]), b = fmaxf(b, v[p][k]);
-    if (section_of(L, h)) {
-      tmin1 = fminf(tmin1, a), tmax1 = fmaxf(tmax1, b);
+      for (int k = 0; k < E; ++k) lp.mn[p][k] = 0.0f, lp.inv[p][k] = 0.0f;
+      continue;
+    }
+    const uint64_t pi = s.axis == 0 ? (uint64_t)(h - s.head_start) * D + rl.sub * E : 0;
+    const uint16_t* pmn = reinterpret_cast<const uint16_t*>(aux + s.aux_min_offset) + pi;
+    const uint16_t* pinv = reinterpret_cast<const uint16_t*>(aux + half + s.aux_scale_offset) + pi;
+    if (s.axis == 0) {
+      ld_seg<E>(pmn, lp.mn[p], true);
+      ld_seg<E>(pinv, lp.inv[p], true);
     } else {
-      tmin0 = fminf(tmin0, a), tmax0 = fmaxf(tmax0, b);
+      const float a = ld_bf16(pmn), b = ld_bf16(pinv);
+#pragma unroll
+      for (int k = 0; k < E; ++k) lp.mn[p][k] = a, lp.inv[p][k] = b;
     }
   }
-  QP tp0 = {}, tp1 = {};
-  if (L.num_sections > 0 && L.sections[0].axis == 1) {  // uniform
-    tp0 = quant_params(wave_min(tmin0), wave_max(tmax0), L.sections[0].levels);
-    if (rl.lane == 0) put_params(aux, half, L.sections[0], row, tp0);
-  }
-  if (L.num_sections > 1 && L.sections[1].axis == 1) {
-    tp1 = quant_params(wave_min(tmin1), wave_max(tmax1), L.sections[1].levels);
-    if (rl.lane == 0) put_params(aux, half, L.sections[1], row, tp1);
-  }
-  uint8_t* out = packed + L.u8_offset + row * cols + rl.sub * E;
+  const bool tok0 = L.num_sections > 0 && L.sections[0].axis == 1;
+  const bool tok1 = L.num_sections > 1 && L.sections[1].axis == 1;
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int h = p * HPW + (int)rl.slot;
-    if (h >= g.num_heads) continue;
-    const bool second = section_of(L, h);
-    const kvmi_rt_section s = second ? L.sections[1] : L.sections[0];
-    float mn[E], inv[E];
-    if (s.axis == 1) {
-      const QP& t = second ? tp1 : tp0;
+  for (int j = 0; j < R; ++j) {
+    if ((uint32_t)j >= n) break;
+    const uint64_t row = row0 + j;
+    // token-axis statistics of the row, per section (two named sections: a local
+    // array indexed by a run-time section number would live in scratch memory)
+    QP tp0 = {}, tp1 = {};
+    if (tok0 || tok1) {
+      float tmin0 = INFINITY, tmin1 = INFINITY, tmax0 = -INFINITY, tmax1 = -INFINITY;
 #pragma unroll
-      for (int k = 0; k < E; ++k) mn[k] = t.mn, inv[k] = t.inv;
-    } else {
-      const uint64_t pi = s.axis == 0 ? (uint64_t)(h - s.head_start) * D + rl.sub * E : 0;
-      const uint16_t* pmn = reinterpret_cast<const uint16_t*>(aux + s.aux_min_offset) + pi;
-      const uint16_t* pinv = reinterpret_cast<const uint16_t*>(aux + half + s.aux_scale_offset) + pi;
-      if (s.axis == 0) {
-        ld_seg<E>(pmn, mn, true);
-        ld_seg<E>(pinv, inv, true);
-      } else {
-        const float a = ld_bf16(pmn), b = ld_bf16(pinv);
+      for (int p = 0; p < P; ++p) {
+        const int h = p * HPW + (int)rl.slot;
+        if (h >= g.num_heads) continue;
+        float a = INFINITY, b = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < E; ++k) mn[k] = a, inv[k] = b;
+        for (int k = 0; k < E; ++k) a = fminf(a, v[j][p][k]), b = fmaxf(b, v[j][p][k]);
+        if (section_of(L, h)) {
+          tmin1 = fminf(tmin1, a), tmax1 = fmaxf(tmax1, b);
+        } else {
+          tmin0 = fminf(tmin0, a), tmax0 = fmaxf(tmax0, b);
+        }
+      }
+      if (tok0) {
+        tp0 = quant_params(wave_min(tmin0), wave_max(tmax0), L.sections[0].levels);
+        if (rl.lane == (uint32_t)j) put_params(aux, half, L.sections[0], row, tp0);
+      }
+      if (tok1) {
+        tp1 = quant_params(wave_min(tmin1), wave_max(tmax1), L.sections[1].levels);
+        if (rl.lane == (uint32_t)j) put_params(aux, half, L.sections[1], row, tp1);
       }
     }
-    const float top = (float)(s.levels - 1);
-    uint32_t w[(E + 3) / 4];
+    uint8_t* out = packed + L.u8_offset + row * cols + rl.sub * E;
 #pragma unroll
-    for (int i = 0; i < (E + 3) / 4; ++i) w[i] = 0;
+    for (int p = 0; p < P; ++p) {
+      const int h = p * HPW + (int)rl.slot;
+      if (h >= g.num_heads) continue;
+      const bool second = section_of(L, h);
+      const kvmi_rt_section s = second ? L.sections[1] : L.sections[0];
+      const bool token = s.axis == 1;
+      const QP& t = second ? tp1 : tp0;
+      const float top = (float)(s.levels - 1);
+      uint32_t w[(E + 3) / 4];
 #pragma unroll
-    for (int k = 0; k < E; ++k) {
-      float q = rintf(rn(rn(v[p][k] - mn[k]) * inv[k]));
-      q = fminf(fmaxf(q, 0.0f), top);
-      w[k / 4] |= (uint32_t)q << (8 * (k % 4));
+      for (int i = 0; i < (E + 3) / 4; ++i) w[i] = 0;
+#pragma unroll
+      for (int k = 0; k < E; k += 2) {
+        float a = v[j][p][k] - (token ? t.mn : lp.mn[p][k]);
+        float b = v[j][p][k + 1] - (token ? t.mn : lp.mn[p][k + 1]);
+        rn2(a, b);
+        a *= token ? t.inv : lp.inv[p][k];
+        b *= token ? t.inv : lp.inv[p][k + 1];
+        rn2(a, b);
+        a = fminf(fmaxf(rintf(a), 0.0f), top);
+        b = fminf(fmaxf(rintf(b), 0.0f), top);
+        w[k / 4] |= ((uint32_t)a | ((uint32_t)b << 8)) << (8 * (k % 4));
+      }
+      st_sym<E>(out + (int64_t)h * D, w);
     }
-    st_sym<E>(out + (int64_t)h * D, w);
   }
 }
 
-// Decode pass: one wave per (layer, row): symbols (or bf16 rows) -> dequantize ->
-// [FWHT] -> signs -> the cache, through the head order.
+// Decode pass: a wave takes rows_per_wave consecutive rows of one layer: symbols (or
+// bf16 rows) -> dequantize -> [FWHT] -> signs -> the cache, through the head order.
 template <int D, int P>
 __global__ __launch_bounds__(kRtThreads) void rt_row_decode_kernel(kvmi_rt_geometry g, const kvmi_rt_layer* __restrict__ layers,
                                                                    const int64_t* __restrict__ block_ids, uint64_t rows,
                                                                    uint32_t num_layers, const uint8_t* __restrict__ packed,
                                                                    const uint8_t* __restrict__ aux, bool vec, float scale) {
-  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW;
-  const uint64_t task = (uint64_t)blockIdx.x * kRtWaves + (threadIdx.x >> 6);
-  const uint64_t tasks = rows * (uint64_t)num_layers;
-  if (task >= tasks) return;
-  const uint32_t layer = (uint32_t)(task / rows);
-  const uint64_t row = task % rows;
+  constexpr int E = RowGeo<D>::E, HPW = RowGeo<D>::HPW, R = rows_per_wave<P>();
+  const uint32_t nrows = (uint32_t)rows, groups = (nrows + R - 1) / R;
+  const uint32_t task = blockIdx.x * kRtWaves + (threadIdx.x >> 6);
+  if (task >= groups * num_layers) return;  // wave-uniform
+  const uint32_t layer = task / groups;
+  const uint32_t row0 = (task - layer * groups) * R;
+  const uint32_t n = min((uint32_t)R, nrows - row0);
   const kvmi_rt_layer L = layers[layer];
   const RowLane rl = row_lane<D>();
   const uint64_t cols = (uint64_t)g.num_heads * D;
-  float v[P][E];
+  const bool quant = g.flags & KVMI_RT_QUANTIZE;
+  LayerLanes<D, P> c;
+  layer_lanes<D, P>(g, L, rl, c);
+  const RowRef ref = row_ref(g, block_ids, row0, n, rl.lane);
+  float v[R][P][E];
+  if (!quant) {
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int h = p * HPW + (int)rl.slot;
-    if (h >= g.num_heads) {
+    for (int j = 0; j < R; ++j)
 #pragma unroll
-      for (int k = 0; k < E; ++k) v[p][k] = 0.0f;
-      continue;
+      for (int p = 0; p < P; ++p) {
+        const int h = p * HPW + (int)rl.slot;
+        if ((uint32_t)j < n && h < g.num_heads) {
+          ld_seg<E>(reinterpret_cast<const uint16_t*>(packed) + L.u8_offset + (row0 + j) * cols + (uint64_t)h * D +
+                        rl.sub * E, v[j][p], true);
+        } else {
+#pragma unroll
+          for (int k = 0; k < E; ++k) v[j][p][k] = 0.0f;
+        }
+      }
+  } else {
+    // symbols of all rows first, then the parameters
+    uint32_t w[R][P][(E + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int h = p * HPW + (int)rl.slot;
+        if ((uint32_t)j < n && h < g.num_heads) {
+          ld_sym<E>(packed + L.u8_offset + (row0 + j) * cols + (uint64_t)h * D + rl.sub * E, w[j][p]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < (E + 3) / 4; ++i) w[j][p][i] = 0;
+        }
+      }
+    // token parameters: lane j holds row row0 + j's (min, scale) of each section
+    float tmn0 = 0.0f, tsc0 = 0.0f, tmn1 = 0.0f, tsc1 = 0.0f;
+    if (rl.lane < n) {
+      if (L.num_sections > 0 && L.sections[0].axis == 1) {
+        tmn0 = ld_bf16(reinterpret_cast<const uint16_t*>(aux + L.sections[0].aux_min_offset) + row0 + rl.lane);
+        tsc0 = ld_bf16(reinterpret_cast<const uint16_t*>(aux + L.sections[0].aux_scale_offset) + row0 + rl.lane);
+      }
+      if (L.num_sections > 1 && L.sections[1].axis == 1) {
+        tmn1 = ld_bf16(reinterpret_cast<const uint16_t*>(aux + L.sections[1].aux_min_offset) + row0 + rl.lane);
+        tsc1 = ld_bf16(reinterpret_cast<const uint16_t*>(aux + L.sections[1].aux_scale_offset) + row0 + rl.lane);
+      }
     }
-    const uint64_t c = row * cols + (uint64_t)h * D + rl.sub * E;
-    if (!(g.flags & KVMI_RT_QUANTIZE)) {
-      ld_seg<E>(reinterpret_cast<const uint16_t*>(packed) + L.u8_offset + c, v[p], true);
-      continue;
-    }
-    uint32_t w[(E + 3) / 4];
-    ld_sym<E>(packed + L.u8_offset + c, w);
-    const kvmi_rt_section s = section_of(L, h) ? L.sections[1] : L.sections[0];
-    float mn[E], sc[E];
-    const uint64_t pi = s.axis == 0 ? (uint64_t)(h - s.head_start) * D + rl.sub * E : (s.axis == 1 ? row : 0);
-    const uint16_t* pmn = reinterpret_cast<const uint16_t*>(aux + s.aux_min_offset) + pi;
-    const uint16_t* psc = reinterpret_cast<const uint16_t*>(aux + s.aux_scale_offset) + pi;
-    if (s.axis == 0) {
-      ld_seg<E>(pmn, mn, true);
-      ld_seg<E>(psc, sc, true);
-    } else {
-      const float a = ld_bf16(pmn), b = ld_bf16(psc);
 #pragma unroll
-      for (int k = 0; k < E; ++k) mn[k] = a, sc[k] = b;
-    }
+    for (int p = 0; p < P; ++p) {
+      const int h = p * HPW + (int)rl.slot;
+      const bool live = h < g.num_heads;
+      const bool second = live && section_of(L, h);
+      const kvmi_rt_section s = second ? L.sections[1] : L.sections[0];
+      float mn[E], sc[E];
+      if (live && s.axis != 1) {
+        const uint64_t pi = s.axis == 0 ? (uint64_t)(h - s.head_start) * D + rl.sub * E : 0;
+        const uint16_t* pmn = reinterpret_cast<const uint16_t*>(aux + s.aux_min_offset) + pi;
+        const uint16_t* psc = reinterpret_cast<const uint16_t*>(aux + s.aux_scale_offset) + pi;
+        if (s.axis == 0) {
+          ld_seg<E>(pmn, mn, true);
+          ld_seg<E>(psc, sc, true);
+        } else {
+          const float a = ld_bf16(pmn), b = ld_bf16(psc);
 #pragma unroll
-    for (int k = 0; k < E; ++k) v[p][k] = rn(rn((float)((w[k / 4] >> (8 * (k % 4))) & 0xffu) * sc[k]) + mn[k]);
+          for (int k = 0; k < E; ++k) mn[k] = a, sc[k] = b;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        // row j's parameters of both sections from lane j, then this lane's section
+        const float m0 = __shfl(tmn0, j, 64), m1 = __shfl(tmn1, j, 64);
+        const float s0 = __shfl(tsc0, j, 64), s1 = __shfl(tsc1, j, 64);
+        const float rmn = second ? m1 : m0, rsc = second ? s1 : s0;
+#pragma unroll
+        for (int k = 0; k < E; k += 2) {
+          const bool tok = live && s.axis == 1;
+          float a = (float)((w[j][p][k / 4] >> (8 * (k % 4))) & 0xffu) * (tok ? rsc : sc[k]);
+          float b = (float)((w[j][p][k / 4] >> (8 * (k % 4) + 8)) & 0xffu) * (tok ? rsc : sc[k + 1]);
+          rn2(a, b);
+          a += tok ? rmn : mn[k];
+          b += tok ? rmn : mn[k + 1];
+          rn2(a, b);
+          v[j][p][k] = a;
+          v[j][p][k + 1] = b;
+        }
+      }
+    }
   }
-  if (g.flags & KVMI_RT_TRANSFORM) fwht_rows<D, P>(v, rl.lane, scale);
-  const uint64_t blk = row / (uint64_t)g.kernel_tokens;
-  const uint32_t tok = (uint32_t)(row % (uint64_t)g.kernel_tokens);
-  const int64_t pb = gld(block_ids + blk);
-  uint16_t* cache = static_cast<uint16_t*>(L.cache) + pb * L.block_stride + (int64_t)tok * L.token_stride +
-                    L.channel_offset + rl.sub * E;
-  const uint16_t* signs = static_cast<const uint16_t*>(L.signs);
+  if (g.flags & KVMI_RT_TRANSFORM) {
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int h = p * HPW + (int)rl.slot;
-    if (h >= g.num_heads) continue;
-    if (signs) mul_signs<E>(v[p], signs + (int64_t)h * D + rl.sub * E);
-    st_seg<E>(cache + (int64_t)gld(L.head_order + h) * L.head_stride, v[p], vec);
+    for (int j = 0; j < R; ++j) fwht_rows<D, P>(v[j], rl.lane, scale);
+  }
+  const uint16_t* signs = static_cast<const uint16_t*>(L.signs);
+  uint16_t* base = static_cast<uint16_t*>(L.cache) + L.channel_offset + rl.sub * E;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if ((uint32_t)j >= n) break;
+    const int64_t pb = __shfl(ref.pb, j, 64);
+    const uint32_t tok = (uint32_t)__shfl((int)ref.tok, j, 64);
+    uint16_t* row = base + pb * L.block_stride + (int64_t)tok * L.token_stride;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (c.hc[p] < 0) continue;
+      if (signs) {
+#pragma unroll
+        for (int k = 0; k < E; ++k)
+          v[j][p][k] = __uint_as_float(__float_as_uint(v[j][p][k]) ^ (__float_as_uint(c.sg[p][k]) & 0x80000000u));
+      }
+      st_seg<E>(row + (int64_t)c.hc[p] * L.head_stride, v[j][p], vec);
+    }
   }
 }
 
@@ -829,7 +1060,8 @@ int rt_dispatch(int D, F&& f) {
 // head sizes served by the row kernels (the others take the generic path)
 bool rt_row_head_dim(int D) { return D >= 8 && D <= 256; }
 
-// P passes of HPW heads cover a row; the row kernels hold E * P <= 64 values per lane
+// P passes of HPW heads cover a row; the row kernels hold E * P <= 32 values per lane
+// and row; wider rows take the generic path
 int rt_row_passes(int D, int H) {
   if (!rt_row_head_dim(D)) return 0;
   int E = D <= 8 ? D : (D / 64 > 8 ? D / 64 : 8);
@@ -837,7 +1069,7 @@ int rt_row_passes(int D, int H) {
   const int need = (H + hpw - 1) / hpw;
   int P = 1;
   while (P < need) P <<= 1;
-  if (P > 8 || E * P > 64 || (int64_t)H * D > kMaxRowCols) return 0;
+  if (P > 4 || E * P > 32 || (int64_t)H * D > kMaxRowCols) return 0;
   return P;
 }
 
@@ -848,7 +1080,6 @@ int rt_row_dispatch(int D, int P, F&& f) {
       case 1: return f(Dc, std::integral_constant<int, 1>{});
       case 2: return f(Dc, std::integral_constant<int, 2>{});
       case 4: return f(Dc, std::integral_constant<int, 4>{});
-      case 8: return f(Dc, std::integral_constant<int, 8>{});
       default: return (int)KVMI_EINVAL;
     }
   };
@@ -911,7 +1142,9 @@ extern "C" int kvmi_rt_encode(const kvmi_rt_geometry* geom, const kvmi_rt_layer*
         hipLaunchKernelGGL(rt_stats_reduce_kernel, dim3((uint32_t)num_layers), dim3(kRtThreads), 0, s, g, layers,
                            (const float*)partial, wpl, aux, half);
       }
-      const uint32_t wgs = (uint32_t)((grid + kRtWaves - 1) / kRtWaves);
+      constexpr int R = rows_per_wave<PP>();
+      const uint64_t tasks = (rows + R - 1) / R * (uint64_t)num_layers;
+      const uint32_t wgs = (uint32_t)((tasks + kRtWaves - 1) / kRtWaves);
       hipLaunchKernelGGL((rt_row_encode_kernel<D, PP>), dim3(wgs), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
                          (uint32_t)num_layers, packed, aux, half, vec, scale);
       return (int)KVMI_OK;
@@ -963,7 +1196,9 @@ extern "C" int kvmi_rt_decode(const kvmi_rt_geometry* geom, const kvmi_rt_layer*
     const bool vec = g.flags & KVMI_RT_ALIGNED;
     rc = rt_row_dispatch(g.head_dim, P, [&](auto Dc, auto Pc) {
       constexpr int D = decltype(Dc)::value, PP = decltype(Pc)::value;
-      const uint32_t wgs = (uint32_t)((grid + kRtWaves - 1) / kRtWaves);
+      constexpr int R = rows_per_wave<PP>();
+      const uint64_t tasks = (rows + R - 1) / R * (uint64_t)num_layers;
+      const uint32_t wgs = (uint32_t)((tasks + kRtWaves - 1) / kRtWaves);
       hipLaunchKernelGGL((rt_row_decode_kernel<D, PP>), dim3(wgs), dim3(kRtThreads), 0, s, g, layers, block_ids, rows,
                          (uint32_t)num_layers, packed, aux, vec, scale);
       return (int)KVMI_OK;

@@ -16,28 +16,32 @@
  * [i*w, i*w + w) of a little-endian byte string) -- the bitpack body layout.
  *
  * Stream (little-endian):
- *   [0]  u32 magic 0x5352564B ("KVRS")   [4] u8 version 1, u8 w, u8 prob_bits 12, u8 log2(lanes) 6
+ *   [0]  u32 magic 0x5352564B ("KVRS")   [4] u8 version 2, u8 w, u8 prob_bits 12, u8 log2(states) 8
  *   [8]  u32 block_symbols (65536)      [12] u32 num_blocks = ceil(n / block_symbols)
  *   [16] u64 n                          [24] u64 payload_bytes
  *   [32] u64 offset[num_blocks]  (block b starts at payload + offset[b]; payload = 32 + 8*num_blocks)
  *   blocks, each a multiple of 4 bytes:
- *     u32 tag = mode | count << 1       mode 0 = rANS, 1 = raw
- *     rANS: u16 freq[2^w] (padded to 4 bytes), u32 state[64],
- *           pad4(2*count) bytes whose last 2*count are the words u16[count]
- *           (a zero u16 in front when count is odd)
+ *     u32 tag = mode | count0 << 1      mode 0 = rANS, 1 = raw
+ *     rANS: u16 freq[2^w] (padded to 4 bytes), u32 count[3] (sub-blocks 1..3),
+ *           u32 state[4][64], then for each sub-block j = 0..3 a word region of
+ *           pad4(2*count_j) bytes whose last 2*count_j are its words u16[count_j]
+ *           (a zero u16 in front when count_j is odd)
  *     raw:  the block's packed symbols, ceil(nb*w/8) bytes, zero-padded to 4
  *
- * Block b holds symbols [b*65536, b*65536 + nb).  Lane i (0..63) owns, at step t
- * (0..1023), block symbol (t/32)*2048 + i*32 + t%32 when it is < nb.  Encoding
- * runs t = 1023..0; at each step every lane with a symbol s first renormalises
- * (x >= freq[s] << 20: emit x & 0xffff, x >>= 16), the step's emitted words are
- * placed, in lane order, in front of the words of later steps, then
- * x = (x / f) << 12 | (x % f) + cum[s].  States start at 2^16; decoding runs
- * t = 0..1023 and ends with every state back at 2^16.
+ * Block b holds symbols [b*65536, b*65536 + nb) in 4 sub-blocks of 16384 symbols
+ * that share the block's frequency table and are coded independently (one GPU wave
+ * each).  In sub-block j, lane i (0..63) owns, at step t (0..255), block symbol
+ * j*16384 + (t/32)*2048 + i*32 + t%32 when it is < nb.  Encoding runs t = 255..0;
+ * at each step every lane with a symbol s first renormalises (x >= freq[s] << 20:
+ * emit x & 0xffff, x >>= 16), the step's emitted words are placed, in lane order,
+ * in front of the words of later steps, then x = (x / f) << 12 | (x % f) + cum[s].
+ * States start at 2^16; decoding runs t = 0..255 and ends with every state back at
+ * 2^16.
  * Frequencies (prob_bits 12, M = 4096): with c[v] the block's counts and K the
  * number of symbols present, f[v] = c[v] ? 1 + c[v] * (M - K) / nb : 0, and the
  * remainder M - sum(f) goes to the most frequent symbol (lowest value on ties).
- * A block is stored raw when its rANS form is not smaller than its raw form.
+ * A block is stored raw when a sub-block's words exceed 16384*w/16 (its raw size)
+ * or when its rANS form is not smaller than its raw form.
  */
 #include <stdint.h>
 #include <stdlib.h>
@@ -48,8 +52,10 @@
 #define M (1u << PB)
 #define LANES 64u
 #define RUN 32u
-#define STEPS 1024u
-#define BLOCK (LANES * STEPS)
+#define SUBS 4u
+#define SUB_STEPS 256u
+#define SUB (LANES * SUB_STEPS)
+#define BLOCK (SUB * SUBS)
 #define RANS_L (1u << 16)
 
 static uint64_t pad4(uint64_t b) { return (b + 3u) & ~(uint64_t)3u; }
@@ -73,12 +79,13 @@ static void wr64(uint8_t* p, uint64_t v) { memcpy(p, &v, 8); }
 static uint32_t rd32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
 static uint64_t rd64(const uint8_t* p) { uint64_t v; memcpy(&v, p, 8); return v; }
 
-static uint64_t block_idx(unsigned t, unsigned lane) {
-    return (uint64_t)(t / RUN) * (LANES * RUN) + (uint64_t)lane * RUN + t % RUN;
+static uint64_t block_idx(unsigned j, unsigned t, unsigned lane) {
+    return (uint64_t)j * SUB + (uint64_t)(t / RUN) * (LANES * RUN) + (uint64_t)lane * RUN + t % RUN;
 }
 
 static uint64_t raw_block_bytes(uint64_t nb, int w) { return 4u + pad4((nb * (uint64_t)w + 7u) / 8u); }
 static uint64_t table_bytes(int w) { return pad4(2u << w); }
+static uint64_t head_bytes(int w) { return 4u + table_bytes(w) + 4u * (SUBS - 1u) + 4u * LANES * SUBS; }
 
 /* Upper bound of the stream size for n symbols of w bits. */
 int64_t oracle_rans_max_bytes(uint64_t n, int w) {
@@ -108,25 +115,18 @@ static void block_freqs(const uint8_t* in, uint64_t first, uint64_t nb, int w, u
     f[top] += M - sum;
 }
 
-/* Encodes one block into dst (capacity raw_block_bytes); returns its size. */
-static uint64_t encode_block(const uint8_t* in, uint64_t first, uint64_t nb, int w, uint8_t* dst) {
-    unsigned A = 1u << w;
-    uint32_t f[256], cum[256];
-    block_freqs(in, first, nb, w, f);
-    cum[0] = 0;
-    for (unsigned v = 1; v < A; ++v) cum[v] = cum[v - 1] + f[v - 1];
-
-    uint64_t raw = raw_block_bytes(nb, w);
-    uint16_t* words = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(LANES * STEPS + 1));
-    uint64_t cap = LANES * STEPS + 1, pos = cap; /* words fill words[pos, cap) */
-    uint32_t x[LANES];
+/* Codes sub-block j of a block: words into words[*pos, cap) (front-filled), final
+ * states into x; returns the word count. */
+static uint64_t encode_sub(const uint8_t* in, uint64_t first, uint64_t nb, int w, unsigned j, const uint32_t* f,
+                           const uint32_t* cum, uint16_t* words, uint64_t cap, uint32_t* x) {
+    uint64_t pos = cap;
     for (unsigned i = 0; i < LANES; ++i) x[i] = RANS_L;
-    for (int t = (int)STEPS - 1; t >= 0; --t) {
+    for (int t = (int)SUB_STEPS - 1; t >= 0; --t) {
         unsigned s_of[LANES];
         int valid[LANES];
         unsigned emit = 0;
         for (unsigned i = 0; i < LANES; ++i) {
-            uint64_t k = block_idx((unsigned)t, i);
+            uint64_t k = block_idx(j, (unsigned)t, i);
             valid[i] = k < nb;
             if (!valid[i]) continue;
             s_of[i] = get_sym(in, first + k, w);
@@ -144,9 +144,30 @@ static uint64_t encode_block(const uint8_t* in, uint64_t first, uint64_t nb, int
             x[i] = ((x[i] / fs) << PB) + (x[i] % fs) + cum[s_of[i]];
         }
     }
-    uint64_t count = cap - pos;
-    uint64_t size = 4u + table_bytes(w) + 4u * LANES + pad4(2u * count);
-    if (size >= raw) {
+    return cap - pos;
+}
+
+/* Encodes one block into dst (capacity raw_block_bytes); returns its size. */
+static uint64_t encode_block(const uint8_t* in, uint64_t first, uint64_t nb, int w, uint8_t* dst) {
+    unsigned A = 1u << w;
+    uint32_t f[256], cum[256];
+    block_freqs(in, first, nb, w, f);
+    cum[0] = 0;
+    for (unsigned v = 1; v < A; ++v) cum[v] = cum[v - 1] + f[v - 1];
+
+    uint64_t raw = raw_block_bytes(nb, w);
+    uint64_t cap = LANES * SUB_STEPS; /* at most one word per symbol */
+    uint64_t sub_cap = (uint64_t)SUB * (uint64_t)w / 16u;
+    uint16_t* words = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(cap * SUBS));
+    uint32_t x[SUBS][LANES];
+    uint64_t count[SUBS], size = head_bytes(w);
+    int over = 0;
+    for (unsigned j = 0; j < SUBS; ++j) {
+        count[j] = encode_sub(in, first, nb, w, j, f, cum, words + (uint64_t)j * cap, cap, x[j]);
+        if (count[j] > sub_cap) over = 1;
+        size += pad4(2u * count[j]);
+    }
+    if (over || size >= raw) {
         free(words);
         memset(dst, 0, raw);
         wr32(dst, 1u);
@@ -155,13 +176,20 @@ static uint64_t encode_block(const uint8_t* in, uint64_t first, uint64_t nb, int
         return raw;
     }
     memset(dst, 0, size);
-    wr32(dst, (uint32_t)(count << 1));
+    wr32(dst, (uint32_t)(count[0] << 1));
     uint8_t* q = dst + 4;
     for (unsigned v = 0; v < A; ++v) { uint16_t fv = (uint16_t)f[v]; memcpy(q + 2u * v, &fv, 2); }
     q += table_bytes(w);
-    for (unsigned i = 0; i < LANES; ++i) wr32(q + 4u * i, x[i]);
-    q += 4u * LANES;
-    memcpy(q + (pad4(2u * count) - 2u * count), words + pos, 2u * count);
+    for (unsigned j = 1; j < SUBS; ++j) wr32(q + 4u * (j - 1u), (uint32_t)count[j]);
+    q += 4u * (SUBS - 1u);
+    for (unsigned j = 0; j < SUBS; ++j)
+        for (unsigned i = 0; i < LANES; ++i) wr32(q + 4u * (LANES * j + i), x[j][i]);
+    q += 4u * LANES * SUBS;
+    for (unsigned j = 0; j < SUBS; ++j) {
+        uint64_t region = pad4(2u * count[j]);
+        memcpy(q + (region - 2u * count[j]), words + (uint64_t)j * cap + (cap - count[j]), 2u * count[j]);
+        q += region;
+    }
     free(words);
     return size;
 }
@@ -174,7 +202,7 @@ int64_t oracle_rans_encode(const uint8_t* in, uint64_t n, int w, uint8_t* out, i
     uint32_t nblk = (uint32_t)((n + BLOCK - 1) / BLOCK);
     memset(out, 0, 32u + 8u * (uint64_t)nblk);
     wr32(out, KVRS_MAGIC);
-    out[4] = 1; out[5] = (uint8_t)w; out[6] = (uint8_t)PB; out[7] = 6;
+    out[4] = 2; out[5] = (uint8_t)w; out[6] = (uint8_t)PB; out[7] = 8;
     wr32(out + 8, BLOCK);
     wr32(out + 12, nblk);
     wr64(out + 16, n);
@@ -191,7 +219,7 @@ int64_t oracle_rans_encode(const uint8_t* in, uint64_t n, int w, uint8_t* out, i
 
 /* 0 = ok; -1 bad header / size; -2 corrupt block.  out holds ceil(n*w/8) bytes. */
 int oracle_rans_decode(const uint8_t* in, int64_t in_bytes, uint64_t n, int w, uint8_t* out) {
-    if (in_bytes < 32 || rd32(in) != KVRS_MAGIC || in[4] != 1 || in[5] != w || in[6] != PB || in[7] != 6)
+    if (in_bytes < 32 || rd32(in) != KVRS_MAGIC || in[4] != 2 || in[5] != w || in[6] != PB || in[7] != 8)
         return -1;
     uint32_t nblk = rd32(in + 12);
     if (rd32(in + 8) != BLOCK || rd64(in + 16) != n || nblk != (n + BLOCK - 1) / BLOCK) return -1;
@@ -212,37 +240,44 @@ int oracle_rans_decode(const uint8_t* in, int64_t in_bytes, uint64_t n, int w, u
             memcpy(out + (uint64_t)b * BLOCK * (uint64_t)w / 8u, blk + 4, rb);
             continue;
         }
-        uint64_t count = tag >> 1;
-        if (e - o != 4u + table_bytes(w) + 4u * LANES + pad4(2u * count)) return -2;
+        uint64_t count[SUBS], size = head_bytes(w);
+        count[0] = tag >> 1;
+        for (unsigned j = 1; j < SUBS; ++j) count[j] = rd32(blk + 4 + table_bytes(w) + 4u * (j - 1u));
+        for (unsigned j = 0; j < SUBS; ++j) size += pad4(2u * count[j]);
+        if (e - o != size) return -2;
         uint32_t f[256], cum[256], tot = 0;
         for (unsigned v = 0; v < A; ++v) { uint16_t fv; memcpy(&fv, blk + 4 + 2u * v, 2); f[v] = fv; cum[v] = tot; tot += fv; }
         if (tot != M) return -2;
         uint8_t slot_sym[M];
         for (unsigned v = 0; v < A; ++v)
             for (uint32_t k = 0; k < f[v]; ++k) slot_sym[cum[v] + k] = (uint8_t)v;
-        uint32_t x[LANES];
-        const uint8_t* st = blk + 4 + table_bytes(w);
-        for (unsigned i = 0; i < LANES; ++i) x[i] = rd32(st + 4u * i);
-        const uint8_t* wp = st + 4u * LANES + (pad4(2u * count) - 2u * count);
-        uint64_t p = 0;
-        for (unsigned t = 0; t < STEPS; ++t) {
-            for (unsigned i = 0; i < LANES; ++i) {
-                uint64_t k = block_idx(t, i);
-                if (k >= nb) continue;
-                uint32_t slot = x[i] & (M - 1u);
-                unsigned s = slot_sym[slot];
-                x[i] = f[s] * (x[i] >> PB) + slot - cum[s];
-                if (x[i] < RANS_L) {
-                    if (p >= count) return -2;
-                    uint16_t wv; memcpy(&wv, wp + 2u * p, 2); ++p;
-                    x[i] = (x[i] << 16) | wv;
+        const uint8_t* st = blk + 4 + table_bytes(w) + 4u * (SUBS - 1u);
+        const uint8_t* region = st + 4u * LANES * SUBS;
+        for (unsigned j = 0; j < SUBS; ++j) {
+            uint32_t x[LANES];
+            for (unsigned i = 0; i < LANES; ++i) x[i] = rd32(st + 4u * (LANES * j + i));
+            const uint8_t* wp = region + (pad4(2u * count[j]) - 2u * count[j]);
+            uint64_t p = 0;
+            for (unsigned t = 0; t < SUB_STEPS; ++t) {
+                for (unsigned i = 0; i < LANES; ++i) {
+                    uint64_t k = block_idx(j, t, i);
+                    if (k >= nb) continue;
+                    uint32_t slot = x[i] & (M - 1u);
+                    unsigned s = slot_sym[slot];
+                    x[i] = f[s] * (x[i] >> PB) + slot - cum[s];
+                    if (x[i] < RANS_L) {
+                        if (p >= count[j]) return -2;
+                        uint16_t wv; memcpy(&wv, wp + 2u * p, 2); ++p;
+                        x[i] = (x[i] << 16) | wv;
+                    }
+                    put_sym(out, (uint64_t)b * BLOCK + k, w, s);
                 }
-                put_sym(out, (uint64_t)b * BLOCK + k, w, s);
             }
+            if (p != count[j]) return -2;
+            for (unsigned i = 0; i < LANES; ++i)
+                if (x[i] != RANS_L) return -2;
+            region += pad4(2u * count[j]);
         }
-        if (p != count) return -2;
-        for (unsigned i = 0; i < LANES; ++i)
-            if (x[i] != RANS_L) return -2;
     }
     return 0;
 }

@@ -75,7 +75,8 @@ def test_rans_sizes_and_contract_errors():
     for n, w in ((0, 4), (1, 1), (65536, 4), (65537, 3), (3 * 65536 + 17, 8)):
         assert lib.kvmi_rans_max_bytes(n, w) == crans.max_bytes(n, w)
     assert lib.kvmi_rans_max_bytes(65536, 4) == 32 + 8 + 4 + 32768
-    assert lib.kvmi_rans_scratch_bytes(65536 * 2, 4) == 2 * (4 + 32 + 256 + 4096 + 32768) + 8
+    # per block: tag, table, 3 counts, 4 x 64 states; 4 word regions of guard + 16384 * 4 / 8
+    assert lib.kvmi_rans_scratch_bytes(65536 * 2, 4) == 2 * (4 + 32 + 12 + 1024 + 4 * (4096 + 8192)) + 8
     assert lib.kvmi_rans_max_bytes(-1, 4) == E and lib.kvmi_rans_max_bytes(10, 0) == E
     assert lib.kvmi_rans_max_bytes(10, 9) == E and lib.kvmi_rans_scratch_bytes(10, 9) == E
     buf = ctypes.create_string_buffer(1 << 16)

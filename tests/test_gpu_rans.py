@@ -80,7 +80,9 @@ def test_large_stream_equals_oracle(cuda):
     p = np.bincount(base, minlength=16) / n
     p = p[p > 0]
     entropy_bytes = -(p * np.log2(p)).sum() * n / 8
-    assert entropy_bytes <= st.numel() <= 1.01 * entropy_bytes
+    # per block: offset, tag, table, 3 counts, 4 x 64 states and word-region padding
+    per_block = 8 + 4 + 32 + 12 + 1024 + 4 * 2
+    assert entropy_bytes <= st.numel() <= 1.01 * entropy_bytes + 32 + (n // 65536) * per_block
 
 
 def test_damage_is_reported(cuda):
@@ -91,7 +93,7 @@ def test_damage_is_reported(cuda):
     nblk = 3
     head = 32 + 8 * nblk
     bad = st.clone()
-    bad[head + 4 + 16 + 1] ^= 0x10                  # a state of block 0
+    bad[head + 4 + 16 + 12 + 1] ^= 0x10             # a state of block 0
     with pytest.raises(RuntimeError, match="corrupt entropy-coded stream"):
         ops.rans_decode(bad, n, w)
     bad = st.clone()

@@ -6,8 +6,8 @@ special cases computed here without the oracle's arithmetic:
   - one symbol: the table is {s: 4096}, states never move, no words;
   - two equiprobable symbols (f = 2048 each): encoding inserts the symbol bit at
     bit 11 of the state and emits the low 16 bits once the state reaches 2^31 --
-    a bit-insertion model that fixes the lane/step symbol order, the word order
-    and the state layout;
+    a bit-insertion model that fixes the sub-block / lane / step symbol order, the
+    word order and the state and count layout;
   - normalised frequencies of a hand-counted block;
   - incompressible bytes: every block stored raw, byte for byte;
   - the coded size against the empirical entropy of each block;
@@ -37,34 +37,36 @@ def _parse(stream):
     return nblk, [stream[payload + offs[b]:payload + offs[b + 1]] for b in range(nblk)]
 
 
-def _lane_symbols(sym_block, lane):
-    """Symbols of `lane` in step order t = 0..1023: (t/32)*2048 + lane*32 + t%32."""
-    t = np.arange(1024)
-    return sym_block[(t // 32) * 2048 + lane * 32 + t % 32]
+def _lane_symbols(sym_block, sub, lane):
+    """Symbols of `lane` of sub-block `sub` in step order t = 0..255:
+    sub*16384 + (t/32)*2048 + lane*32 + t%32."""
+    t = np.arange(256)
+    return sym_block[sub * 16384 + (t // 32) * 2048 + lane * 32 + t % 32]
 
 
 def test_header_and_single_symbol_closed_form():
     w, n = 4, 65536
     st = crans.encode(np.full(n, 9, np.uint8), w)
-    assert _u32(st, 0) == MAGIC and list(st[4:8]) == [1, w, 12, 6]
+    assert _u32(st, 0) == MAGIC and list(st[4:8]) == [2, w, 12, 8]
     assert _u32(st, 8) == 65536 and _u32(st, 12) == 1 and _u64(st, 16) == n
     nblk, blocks = _parse(st)
     (blk,) = blocks
-    assert _u32(blk, 0) == 0                                        # rANS, no words
+    assert _u32(blk, 0) == 0                                        # rANS, no words in sub-block 0
     freq = np.frombuffer(blk[4:4 + 32].tobytes(), np.uint16)
     assert freq[9] == 4096 and freq.sum() == 4096
-    states = np.frombuffer(blk[36:36 + 256].tobytes(), np.uint32)
-    assert (states == 1 << 16).all() and blk.size == 4 + 32 + 256
-    assert st.size == 32 + 8 + 292
+    counts = np.frombuffer(blk[36:48].tobytes(), np.uint32)         # sub-blocks 1..3
+    states = np.frombuffer(blk[48:48 + 1024].tobytes(), np.uint32)  # 4 sub-blocks x 64 lanes
+    assert not counts.any() and (states == 1 << 16).all() and blk.size == 4 + 32 + 12 + 1024
+    assert st.size == 32 + 8 + 1072
 
 
-def _bit_insert_model(sym_block):
+def _bit_insert_model(sym_block, sub):
     """f = 2048 for both symbols: x -> (x >> 11) << 12 | s << 11 | (x & 2047), emit
-    the low 16 bits when x >= 2^31 (encoding runs t = 1023..0, lanes in order)."""
+    the low 16 bits when x >= 2^31 (encoding runs t = 255..0, lanes in order)."""
     x = np.full(64, 1 << 16, np.uint64)
     steps = []
-    lanes = [_lane_symbols(sym_block, i) for i in range(64)]
-    for t in range(1023, -1, -1):
+    lanes = [_lane_symbols(sym_block, sub, i) for i in range(64)]
+    for t in range(255, -1, -1):
         emitted = []
         for i in range(64):
             s = int(lanes[i][t])
@@ -86,14 +88,19 @@ def test_two_equiprobable_symbols_bit_insertion():
     _, (blk,) = _parse(st)
     tag = _u32(blk, 0)
     assert tag & 1 == 0
-    count = tag >> 1
+    counts = [tag >> 1] + [int(c) for c in np.frombuffer(blk[12:24].tobytes(), np.uint32)]
     freq = np.frombuffer(blk[4:12].tobytes(), np.uint16)
     assert list(freq) == [2048, 2048, 0, 0]
-    states = np.frombuffer(blk[12:12 + 256].tobytes(), np.uint32)
-    words = np.frombuffer(blk[268 + (count & 1) * 2:].tobytes(), np.uint16)
-    exp_states, exp_words = _bit_insert_model(s)
-    assert count == exp_words.size == 64 * 64       # 16 symbols per word, 1024 per lane
-    assert np.array_equal(states, exp_states) and np.array_equal(words, exp_words)
+    states = np.frombuffer(blk[24:24 + 1024].tobytes(), np.uint32).reshape(4, 64)
+    at = 24 + 1024
+    for sub in range(4):
+        exp_states, exp_words = _bit_insert_model(s, sub)
+        region = (2 * counts[sub] + 3) // 4 * 4
+        words = np.frombuffer(blk[at + region - 2 * counts[sub]:at + region].tobytes(), np.uint16)
+        assert counts[sub] == exp_words.size
+        assert np.array_equal(states[sub], exp_states) and np.array_equal(words, exp_words)
+        at += region
+    assert at == blk.size
     assert (crans.decode(st, s.size, 2) == s).all()
 
 
@@ -142,8 +149,8 @@ def test_size_tracks_the_block_entropy():
         c = np.bincount(blk, minlength=16) / blk.size
         c = c[c > 0]
         bound += -(c * np.log2(c)).sum() * blk.size / 8
-    overhead = 32 + blocks * (8 + 4 + 32 + 256)
-    assert bound <= st.size <= 1.005 * bound + overhead + 2 * blocks
+    overhead = 32 + blocks * (8 + 4 + 32 + 12 + 1024)
+    assert bound <= st.size <= 1.005 * bound + overhead + 2 * 4 * blocks
     assert (crans.decode(st, s.size, w) == s).all()
 
 
@@ -164,7 +171,7 @@ def test_corruption_and_contract_errors():
     st = crans.encode(s, 3)
     nblk = _u32(st, 12)
     bad = st.copy()
-    bad[32 + 8 * nblk + 4 + 16 + 5] ^= 0x40      # a state byte of block 0
+    bad[32 + 8 * nblk + 4 + 16 + 12 + 5] ^= 0x40  # a state byte of block 0
     with pytest.raises(ValueError, match="-2"):
         crans.decode(bad, s.size, 3)
     with pytest.raises(ValueError, match="-1"):
