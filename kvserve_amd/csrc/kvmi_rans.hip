@@ -98,6 +98,26 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* red) {
   return r;
 }
 
+// Exclusive prefix sum over the workgroup's threads (every thread calls; red holds
+// kSubs values): in-wave shuffle scan, then the totals of the lower waves.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* red) {
+  const uint32_t lane = lane_id(), wave = threadIdx.x / kLanes;
+  uint32_t incl = v;
+#pragma unroll
+  for (int o = 1; o < (int)kLanes; o <<= 1) {
+    const uint32_t u = __shfl_up(incl, o, 64);
+    if ((int)lane >= o) incl += u;
+  }
+  if (lane == kLanes - 1) red[wave] = incl;
+  __syncthreads();
+  uint32_t below = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < kSubs; ++j)
+    if (j < wave) below += red[j];
+  __syncthreads();
+  return below + incl - v;
+}
+
 // Orders this wave's LDS accesses around a write-then-read by other lanes of the
 // same wave (the wave's LDS instructions execute in issue order).
 __device__ __forceinline__ void wave_lds_fence() {
@@ -184,11 +204,15 @@ __device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, 
   for (int r = (int)kSubRuns - 1; r >= 0; --r) {
     if (r > 0) load_run<W>(blk, avail, run0 + (uint32_t)r - 1, lane, dn);  // next run in flight
     const uint32_t base = (run0 + (uint32_t)r) * (kLanes * kRun) + lane * kRun;
+    // the run's table entries depend on its symbols only: all 32 reads in flight
+    // before the first step, off the state's dependency chain
+    uint2 ent[kRun];
+#pragma unroll
+    for (int j = 0; j < (int)kRun; ++j) ent[j] = tab[sym_at<W>(d, j)];
 #pragma unroll
     for (int j = (int)kRun - 1; j >= 0; --j) {
-      const uint32_t s = sym_at<W>(d, j);
       const bool valid = FULL || base + (uint32_t)j < nb;
-      const uint2 e = tab[s];
+      const uint2 e = ent[j];
       const uint32_t fs = e.x & 0x1fffu;
       const bool emit = valid && (x >> 20) >= fs;
       const uint64_t mask = __ballot(emit);
@@ -215,7 +239,6 @@ __global__ __launch_bounds__(kBlockThreads) void rans_encode_kernel(const EncBat
   constexpr bool kPrivate = W <= 5;  // lane-private histogram columns (no LDS contention)
   constexpr uint32_t kHist = kPrivate ? G::A * kLanes : G::A;  // per wave
   __shared__ __align__(16) uint32_t hist[kSubs * kHist];
-  __shared__ uint32_t fq[G::A];
   __shared__ uint2 tab[G::A];
   __shared__ uint32_t red[kSubs];
   __shared__ int32_t cnt[kSubs];
@@ -274,14 +297,9 @@ __global__ __launch_bounds__(kBlockThreads) void rans_encode_kernel(const EncBat
   uint32_t f = c ? 1u + c * (kM - K) / nb : 0u;
   const uint32_t fsum = block_sum(f, red);
   if (t == top) f += kM - fsum;
+  if (t < G::A) gst16(reinterpret_cast<uint16_t*>(slot + 4) + t, f);
+  const uint32_t cum = block_exclusive_scan(f, red);  // f = 0 for threads >= A
   if (t < G::A) {
-    fq[t] = f;
-    gst16(reinterpret_cast<uint16_t*>(slot + 4) + t, f);
-  }
-  __syncthreads();
-  if (t < G::A) {
-    uint32_t cum = 0;
-    for (uint32_t u = 0; u < t; ++u) cum += fq[u];
     const uint32_t l = f <= 1u ? 0u : 32u - __clz(f - 1u);
     const uint32_t mul = f ? (uint32_t)((((uint64_t)((1u << l) - f)) << 32) / f + 1u) : 0u;
     const uint32_t sh1 = l ? 1u : 0u, sh2 = l ? l - 1u : 0u;
@@ -445,11 +463,12 @@ __device__ __forceinline__ void ring_fill(uint16_t* ring, const uint32_t* region
 constexpr uint32_t kGroup = 4;
 static_assert(kRing >= kGroup * kLanes + kRefill, "ring too small for the refill policy");
 
+// Decode table: slot -> symbol (bits 0..7), frequency - 1 (8..19) and the slot's
+// offset in its symbol's range (20..31); a step is one LDS read off the state.
 template <int W, bool FULL>
 __device__ __forceinline__ uint32_t decode_runs(const uint32_t* region, uint32_t units, uint32_t& q,
-                                                const uint8_t* slot_sym, const uint32_t* sym_fc, uint16_t* ring,
-                                                uint8_t* dst, uint64_t room, uint32_t nb, uint32_t run0, uint32_t lane,
-                                                uint32_t x) {
+                                                const uint32_t* slot_tab, uint16_t* ring, uint8_t* dst, uint64_t room,
+                                                uint32_t nb, uint32_t run0, uint32_t lane, uint32_t x) {
   uint32_t filled = 0;
   for (uint32_t r = run0; r < run0 + kSubRuns; ++r) {
     uint32_t acc[W];
@@ -463,10 +482,9 @@ __device__ __forceinline__ uint32_t decode_runs(const uint32_t* region, uint32_t
       for (int jj = 0; jj < (int)kGroup; ++jj) {
         const int j = g * (int)kGroup + jj;
         const bool valid = FULL || base + (uint32_t)j < nb;
-        const uint32_t slot = x & (kM - 1u);
-        const uint32_t s = slot_sym[slot];
-        const uint32_t fc = sym_fc[s];
-        uint32_t y = (fc & 0x1fffu) * (x >> kPB) + slot - (fc >> 13);
+        const uint32_t ent = slot_tab[x & (kM - 1u)];
+        const uint32_t s = ent & 0xffu;
+        uint32_t y = (((ent >> 8) & 0xfffu) + 1u) * (x >> kPB) + (ent >> 20);
         const bool need = valid && y < kStateL;
         const uint64_t mask = __ballot(need);
         if (need) y = (y << 16) | (uint32_t)ring[(q + rank_in(mask)) & (kRing - 1)];
@@ -497,9 +515,8 @@ __device__ __forceinline__ uint32_t decode_runs(const uint32_t* region, uint32_t
 template <int W>
 __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBatch bt, int32_t* __restrict__ err) {
   using G = RansGeo<W>;
-  __shared__ uint8_t slot_sym[kM];
+  __shared__ uint32_t slot_tab[kM];
   __shared__ uint32_t sym_fc[G::A];
-  __shared__ uint32_t fq[G::A];
   __shared__ uint32_t red[kSubs];
   __shared__ __align__(16) uint16_t rings[kSubs][kRing];
 
@@ -566,18 +583,15 @@ __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBat
   }
   const uint16_t* ftab = reinterpret_cast<const uint16_t*>(blk + 4);
   const uint32_t fv = t < G::A ? gld(ftab + t) : 0u;
-  if (t < G::A) fq[t] = fv;
   if (block_sum(fv, red) != kM) {
     if (t == 0) atomicOr(err, KVMI_ERR_CORRUPT);
     return;
   }
-  if (t < G::A) {
-    uint32_t cum = 0;
-    for (uint32_t u = 0; u < t; ++u) cum += fq[u];
-    sym_fc[t] = fq[t] | (cum << 13);
-  }
+  const uint32_t cum = block_exclusive_scan(fv, red);
+  if (t < G::A) sym_fc[t] = fv | (cum << 13);
   __syncthreads();
-  // slot -> symbol: thread i fills slots [16 i, 16 i + 16), walking the cumulative table
+  // slot -> (symbol, frequency, offset): thread i fills slots [16 i, 16 i + 16),
+  // walking the cumulative table
   {
     constexpr uint32_t kPer = kM / kBlockThreads;
     const uint32_t s0 = t * kPer;
@@ -596,7 +610,8 @@ __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBat
         ++v;
         end = (sym_fc[v] >> 13) + (sym_fc[v] & 0x1fffu);
       }
-      slot_sym[s] = (uint8_t)v;
+      const uint32_t fv = sym_fc[v] & 0x1fffu, cum = sym_fc[v] >> 13;
+      slot_tab[s] = v | ((fv - 1u) << 8) | ((s - cum) << 20);
     }
   }
   __syncthreads();
@@ -614,8 +629,8 @@ __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBat
   uint32_t q = units - cw;
   const uint32_t run0 = wave * kSubRuns;
   uint16_t* ring = rings[wave];
-  if ((wave + 1) * kSub <= nb) x = decode_runs<W, true>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, run0, lane, x);
-  else x = decode_runs<W, false>(region, units, q, slot_sym, sym_fc, ring, dst, room, nb, run0, lane, x);
+  if ((wave + 1) * kSub <= nb) x = decode_runs<W, true>(region, units, q, slot_tab, ring, dst, room, nb, run0, lane, x);
+  else x = decode_runs<W, false>(region, units, q, slot_tab, ring, dst, room, nb, run0, lane, x);
   // a stream that is not this block's own encoding ends off its start state or
   // off the end of its words (ring reads are masked, so none leaves the ring)
   const bool ok = q == units && x == kStateL;

@@ -16,6 +16,7 @@ from typing import Callable, Optional
 import torch
 
 from .. import _lib
+from ._hip import D2H, H2D, memcpy_async
 
 _RING = 64  # lengths kept in flight per codec
 
@@ -74,32 +75,40 @@ class ANSCodec:
         self._lengths = torch.zeros(_RING, dtype=torch.int64, device=device)
         self._host_lengths = torch.zeros(_RING, dtype=torch.int64, pin_memory=True)
         self._err = torch.zeros(1, dtype=torch.int32, device=device)
-        self._host_err = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._host_err = torch.zeros(2, dtype=torch.int32, pin_memory=True)  # [flag, zero]
         self._next = 0
-        self.capacities = {n: int(_lib.load().kvmi_rans_max_bytes(n, 8)) for n in set(packed_sizes)}
-
-    def _sp(self) -> ctypes.c_void_p:
-        return ctypes.c_void_p(self.stream.cuda_stream)
+        self._stream_ptr = ctypes.c_void_p(stream.cuda_stream)
+        self._lib = _lib.load()
+        self._enc_jobs = {}
+        self.capacities = {n: int(self._lib.kvmi_rans_max_bytes(n, 8)) for n in set(packed_sizes)}
 
     def encode(self, source: torch.Tensor, output: torch.Tensor, u8_bytes: int,
                event: torch.cuda.Event) -> EncodedChunk:
         i = self._next
         self._next = (i + 1) % _RING
-        length = self._lengths[i:i + 1]
-        job = _lib.RansEncJob(source.data_ptr(), u8_bytes, output.data_ptr(), output.numel(),
-                              self.workspace.data_ptr(), self.workspace.numel(), length.data_ptr())
-        _lib.check(_lib.load().kvmi_rans_encode_batch(ctypes.byref(job), 1, 8, self._sp()), "kvmi_rans_encode_batch")
-        self._host_lengths[i:i + 1].copy_(length, non_blocking=True)
+        length = self._lengths.data_ptr() + 8 * i
+        key = (source.data_ptr(), u8_bytes, output.data_ptr(), output.numel())
+        job = self._enc_jobs.get(key)
+        if job is None:
+            job = self._enc_jobs[key] = _lib.RansEncJob(source.data_ptr(), u8_bytes, output.data_ptr(),
+                                                        output.numel(), self.workspace.data_ptr(),
+                                                        self.workspace.numel(), length)
+        job.out_len = length
+        _lib.check(self._lib.kvmi_rans_encode_batch(ctypes.byref(job), 1, 8, self._stream_ptr),
+                   "kvmi_rans_encode_batch")
+        memcpy_async(self._host_lengths.data_ptr() + 8 * i, length, 8, D2H, self.stream.cuda_stream)
         event.record(self.stream)
         return EncodedChunk(_StreamLength(self._host_lengths, i, event), event, u8_bytes)
 
     def decode(self, source: torch.Tensor, output: torch.Tensor, codec_bytes: int, u8_bytes: int,
                event: torch.cuda.Event) -> torch.cuda.Event:
-        self._err.zero_()
+        sp = self.stream.cuda_stream
+        # the error flag starts from zero: a copy of the pinned zero word
+        memcpy_async(self._err.data_ptr(), self._host_err.data_ptr() + 4, 4, H2D, sp)
         job = _lib.RansDecJob(source.data_ptr(), codec_bytes, u8_bytes, output.data_ptr())
-        _lib.check(_lib.load().kvmi_rans_decode_batch(ctypes.byref(job), 1, 8, self._err.data_ptr(), self._sp()),
+        _lib.check(self._lib.kvmi_rans_decode_batch(ctypes.byref(job), 1, 8, self._err.data_ptr(), self._stream_ptr),
                    "kvmi_rans_decode_batch")
-        self._host_err.copy_(self._err, non_blocking=True)
+        memcpy_async(self._host_err.data_ptr(), self._err.data_ptr(), 4, D2H, sp)
         if isinstance(event, SlotEvent):
             event.check = self.check
         event.record(self.stream)

@@ -21,6 +21,8 @@ index_copy_ over the cache views.
 
 from __future__ import annotations
 
+import array
+import contextlib
 import ctypes
 import logging
 from dataclasses import dataclass
@@ -30,6 +32,7 @@ import numpy as np
 import torch
 
 from .. import _lib
+from ._hip import H2D, memcpy_async
 from .codec import ANSCodec, EncodedChunk
 from .layout import CompressionLayout, KVPart, LayerPartLayout
 
@@ -172,6 +175,17 @@ class CompressionPipeline:
     def _build_tables(self) -> None:
         transform = "transformer" in self.stages and "aggregate" not in self.stages
         quantize = "quantizer" in self.stages and "aggregate" not in self.stages
+        # per KV part and cache group: (group, block size, raw-tail bytes per token,
+        # chunk capacity in tokens), the sums layout.py's per-layer loops compute
+        self._groups = {}
+        for kv in (0, 1):
+            acc: Dict[int, List[int]] = {}
+            for part in self.layout.parts(kv):
+                entry = acc.setdefault(part.group_index, [part.block_size, 0,
+                                                           part.raw_bytes // (2 * part.num_heads * part.head_size)])
+                entry[1] += part.num_heads * part.head_size * 2
+            self._groups[kv] = tuple((g, bs, per_token, cap) for g, (bs, per_token, cap) in acc.items())
+        self._aux_clean: Dict[int, int] = {}  # slot -> KV part whose aux layout it holds, gaps zero
         self._launches = {0: [], 1: []}
         if "aggregate" in self.stages:
             return
@@ -217,7 +231,7 @@ class CompressionPipeline:
         elif isinstance(logical_ids, np.ndarray):
             ids = logical_ids.astype(np.int64, copy=False)
         else:
-            ids = np.fromiter(logical_ids, dtype=np.int64, count=len(logical_ids))
+            ids = np.frombuffer(array.array("q", logical_ids), dtype=np.int64)
         f = self.blocks_per_logical
         if f == 1:
             return ids
@@ -261,7 +275,7 @@ class CompressionPipeline:
             hrow = host if host.ndim == 1 else host[row]
             hrow_np[:n] = physical
             indices = storage[:n]
-            indices.copy_(hrow[:n], non_blocking=True)
+            memcpy_async(indices.data_ptr(), hrow.data_ptr(), 8 * n, H2D, self.stream.cuda_stream)
             out[group] = (indices, physical)
         if staged is not None:
             event = self._staging_events[staged[2]] or torch.cuda.Event()
@@ -352,8 +366,12 @@ class CompressionPipeline:
         return slot.completion_event
 
     # ------------------------------------------------------------------ body
-    def _sp(self) -> ctypes.c_void_p:
-        return ctypes.c_void_p(self.stream.cuda_stream)
+    @property
+    def _stream_ptr(self) -> ctypes.c_void_p:
+        ptr = self.__dict__.get("_stream_ptr_cache")
+        if ptr is None:
+            ptr = self.__dict__["_stream_ptr_cache"] = ctypes.c_void_p(self.stream.cuda_stream)
+        return ptr
 
     def _body(self, launch: _Launch, index, valid_tokens_by_group) -> Optional[Tuple[torch.Tensor, int]]:
         entry = index.get(launch.group_index)
@@ -366,50 +384,55 @@ class CompressionPipeline:
     def encode(self, slot_id: int, logical_ids_by_group: List[List[int]], kv_part: KVPart, *,
                valid_tokens_by_group: Dict[int, int]) -> EncodedChunk:
         slot = self.slots[slot_id]
-        raw_tail_bytes = self.layout.raw_tail_bytes(kv_part, valid_tokens_by_group)
+        tokens = valid_tokens_by_group
+        groups = self._groups[kv_part]
+        raw_tail_bytes = sum((tokens.get(g, 0) % bs) * per_token for g, bs, per_token, _ in groups)
         if logger.isEnabledFor(logging.DEBUG):
             logger.debug("KVServe runtime encode: slot=%d kv_part=%d logical_ids=%s", slot_id, kv_part,
-                         [g for g in logical_ids_by_group if g])
+                         [g for g in logical_ids_by_group if len(g)])
         if "aggregate" in self.stages:
             return self._encode_aggregate(slot, logical_ids_by_group, kv_part)
         quantized = "quantizer" in self.stages
         u8_bytes = (self.layout.u8_bytes_by_part if quantized else self.layout.raw_bytes_by_part)[kv_part]
         aux_bytes = self.layout.aux_bytes_by_part[kv_part] if quantized else 0
-        if not self.layout.has_body(valid_tokens_by_group):
+        if not any(tokens.get(g, 0) >= bs for g, bs, _, _ in self._groups[0]):  # layout.has_body
             u8_bytes = aux_bytes = 0
         coded = bool(u8_bytes) and "codec" in self.stages
         packed = slot.arena_b[self.layout.u8_base:] if coded else slot.arena_a
         tail_addr = slot.raw_tail.data_ptr() if slot.raw_tail is not None else 0
-        parts = self.layout.parts(kv_part)
-        # a chunk that fills every layer's capacity overwrites the whole payload (the
-        # layers' symbol ranges tile it); the aux arena has alignment gaps that the
-        # other KV part's sections may have written, so it is always cleared
-        full = all(valid_tokens_by_group.get(p.group_index, 0) == p.raw_bytes // (2 * p.num_heads * p.head_size)
-                   for p in parts)
-        with torch.cuda.stream(self.stream):
+        # A chunk that fills every layer's capacity overwrites the whole payload (the
+        # layers' symbol ranges tile it) and every aux entry; the aux arena's
+        # alignment gaps stay zero unless the other KV part's sections or a received
+        # chunk were written there since it was last cleared.
+        full = all(tokens.get(g, 0) == cap for g, _, _, cap in groups)
+        clear_aux = bool(aux_bytes) and not (full and self._aux_clean.get(slot_id) == kv_part)
+        torch_ops = not full or clear_aux or raw_tail_bytes
+        with torch.cuda.stream(self.stream) if torch_ops else contextlib.nullcontext():
             if not full:
                 # capacities are planned for the largest chunk: a short chunk must not
                 # carry the previous owner's bytes
                 packed[:u8_bytes].zero_()
-            slot.aux[:aux_bytes].zero_()
+            if clear_aux:
+                slot.aux[:aux_bytes].zero_()
+            if aux_bytes:
+                self._aux_clean[slot_id] = kv_part
             index = self._group_indices(slot, logical_ids_by_group)
             offset = 0
             if raw_tail_bytes:
-                for part in parts:
+                for part in self.layout.parts(kv_part):
                     entry = index.get(part.group_index)
                     if entry is not None:
-                        offset = self._pack_raw_tail(slot, part, entry[1], valid_tokens_by_group[part.group_index],
-                                                     offset)
+                        offset = self._pack_raw_tail(slot, part, entry[1], tokens[part.group_index], offset)
             canonical = slot.canonical.data_ptr() if slot.canonical is not None else None
             for launch in self._launches[kv_part]:
-                body = self._body(launch, index, valid_tokens_by_group)
+                body = self._body(launch, index, tokens)
                 if body is None:
                     continue
                 ids, blocks = body
                 rc = self._lib.kvmi_rt_encode(ctypes.byref(launch.geometry), launch.table.data_ptr(), launch.num_layers,
                                               ids.data_ptr(), blocks, canonical, packed.data_ptr(),
                                               slot.aux.data_ptr() if quantized else None,
-                                              self.layout.aux_arena_bytes // 2, self._sp())
+                                              self.layout.aux_arena_bytes // 2, self._stream_ptr)
                 _lib.check(rc, "kvmi_rt_encode")
             if not coded:
                 slot.completion_event.record(self.stream)
@@ -430,25 +453,27 @@ class CompressionPipeline:
         quantized = "quantizer" in self.stages
         coded = bool(u8_bytes) and "codec" in self.stages
         packed = slot.arena_b[self.layout.u8_base:] if coded else slot.arena_a
-        with torch.cuda.stream(self.stream):
+        tokens = valid_tokens_by_group
+        tails = any(tokens.get(g, 0) % bs for g, bs, _, _ in self._groups[kv_part])
+        self._aux_clean.pop(slot_id, None)  # the received aux replaced the slot's own
+        with torch.cuda.stream(self.stream) if tails else contextlib.nullcontext():
             if coded:
                 self.codec.decode(slot.arena_a, packed, codec_bytes, u8_bytes, slot.completion_event)
             index = self._group_indices(slot, logical_ids_by_group)
             for launch in self._launches[kv_part]:
-                body = self._body(launch, index, valid_tokens_by_group)
+                body = self._body(launch, index, tokens)
                 if body is None:
                     continue
                 ids, blocks = body
                 rc = self._lib.kvmi_rt_decode(ctypes.byref(launch.geometry), launch.table.data_ptr(), launch.num_layers,
                                               ids.data_ptr(), blocks, packed.data_ptr(),
-                                              slot.aux.data_ptr() if quantized else None, self._sp())
+                                              slot.aux.data_ptr() if quantized else None, self._stream_ptr)
                 _lib.check(rc, "kvmi_rt_decode")
             offset = 0
-            if any(valid_tokens_by_group.get(p.group_index, 0) % p.block_size for p in self.layout.parts(kv_part)):
+            if tails:
                 for part in self.layout.parts(kv_part):
                     entry = index.get(part.group_index)
                     if entry is not None:
-                        offset = self._apply_raw_tail(slot, part, entry[1], valid_tokens_by_group[part.group_index],
-                                                      offset)
+                        offset = self._apply_raw_tail(slot, part, entry[1], tokens[part.group_index], offset)
             slot.completion_event.record(self.stream)
         return slot.completion_event
