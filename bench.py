@@ -521,12 +521,14 @@ def bench_runtime(args) -> dict:
             e1.synchronize()
             stages[f"{name}_{'kv'[part]}_us"] = round(e0.elapsed_time(e1) * 1e3 / args.steps, 2)
     runtime.shutdown()
-    body_k = stages["body_encode_k_us"]
     part_raw = raw // 2
-    # algorithmic bytes of the K body launch set: read the bf16 part once, write u8
-    # symbols once (aux is negligible)
-    body_bytes = part_raw + part_raw // 2
-    achieved = body_bytes / (body_k * 1e-6) / 1e9
+    # dominant launch set: the K part's rANS encode (encode + compaction kernels);
+    # algorithmic bytes = the u8 symbols read once + the stream written once
+    rans_k = stages["rans_encode_k_us"]
+    rans_bytes = chunks[0].u8_bytes + coded[0]
+    achieved = rans_bytes / (rans_k * 1e-6) / 1e9
+    traffic = [profiled_traffic(k, "runtime") for k in ("rans_encode_kernel<8>", "rans_compact_kernel<8, true>")]
+    cpu = None if args.no_cpu_baseline else runtime_cpu_baseline(plan, caches, source, args.cpu_budget)
     return {
         "metric": "fixed-profile runtime encode GB/s of raw bf16 K+V on 1 MI355X (K then V, fenced)",
         "value": round(raw / enc / 1e9, 2),
@@ -549,9 +551,59 @@ def bench_runtime(args) -> dict:
         "reference": RUNTIME_REFERENCE,
         "stages": stages,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "kvmi_rt_encode launch set, K part"},
-        "cpu_baseline": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None if None in traffic else sum(traffic),
+                     "kernel": "rANS encode launch set of the K part (rans_encode_kernel<8> + "
+                               "rans_compact_kernel<8, true>); latency-bound, not HBM-bound"},
+        "cpu_baseline": cpu,
+    }
+
+
+def runtime_cpu_baseline(plan, caches, source, budget_s: float):
+    """The runtime oracle (numpy, one thread) encoding and decoding whole layers of the
+    same chunk, with the rANS oracle as the codec, until `budget_s` is spent."""
+    import numpy as np
+    import torch
+
+    from kvserve_amd.runtime import build_signs
+    from oracle import crans
+    from oracle import runtime_ref as R
+
+    cfg, layout = plan.config, plan.layout
+    orders = plan.head_selection.local_orders
+    done, t_total, layers = 0, 0.0, 0
+    for name in caches:
+        cache = caches[name].cpu().view(torch.int16).numpy().view(np.uint16)
+        target = np.zeros_like(cache)
+        for kv in (0, 1):
+            part = next(p for p in layout.parts(kv) if p.layer_name == name)
+            sections = [R.Section(s.head_start, s.head_count, s.num_levels, s.axis, s.aux_min_offset,
+                                  s.aux_scale_offset) for s in part.sections]
+            signs = build_signs(part, orders[part.layer_index], cfg.seed).reshape(part.num_heads, -1)
+            mk = lambda c: R.LayerPart(cache=c, channel_offset=kv * part.head_size, head_size=part.head_size,  # noqa
+                                       order=orders[part.layer_index], u8_offset=0,
+                                       signs=signs.to(torch.int8).numpy(), sections=sections)
+            tokens = len(source) * part.block_size
+            n = part.raw_bytes // 2
+            t0 = time.perf_counter()
+            payload, aux, tail = R.encode_part([mk(cache)], source, tokens, part.block_size, 1, True, True, n,
+                                               layout.aux_bytes_by_part[kv])
+            stream = crans.encode(payload, 8)
+            back = crans.decode(stream, n, 8)
+            R.decode_part([mk(target)], source, tokens, part.block_size, 1, True, True, back, aux, tail)
+            t_total += time.perf_counter() - t0
+            done += part.raw_bytes
+        layers += 1
+        if t_total >= budget_s:
+            break
+    return {
+        "value": round(done / t_total / 1e9, 5),
+        "unit": "GB/s (encode + decode, raw bf16 K+V)",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{layers} of {len(caches)} layers, K and V parts of the 1024-token chunk "
+                  f"({done / 2**20:.0f} MiB raw), numpy runtime oracle + C rANS oracle encode and decode on "
+                  f"{cpu_model()} (os.cpu_count()={os.cpu_count()}), {t_total:.1f} s",
     }
 
 

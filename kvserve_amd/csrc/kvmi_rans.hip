@@ -192,6 +192,8 @@ __device__ __forceinline__ int job_of(const Batch& bt, uint32_t g) {
 }
 
 // ------------------------------------------------------------------ encode
+constexpr uint32_t kEncGroup = 8;  // steps whose table reads are issued together
+
 // Steps 255..0 of one sub-block whose runs are block runs run0 .. run0 + 7 (FULL:
 // every lane has a symbol at every step).  Leaves pos < 0 when the words outgrow the
 // capacity (the block is then stored raw).
@@ -204,15 +206,18 @@ __device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, 
   for (int r = (int)kSubRuns - 1; r >= 0; --r) {
     if (r > 0) load_run<W>(blk, avail, run0 + (uint32_t)r - 1, lane, dn);  // next run in flight
     const uint32_t base = (run0 + (uint32_t)r) * (kLanes * kRun) + lane * kRun;
-    // the run's table entries depend on its symbols only: all 32 reads in flight
-    // before the first step, off the state's dependency chain
-    uint2 ent[kRun];
 #pragma unroll
-    for (int j = 0; j < (int)kRun; ++j) ent[j] = tab[sym_at<W>(d, j)];
+    for (int g = (int)kRun / kEncGroup - 1; g >= 0; --g) {
+    // a group's table entries depend on its symbols only: their reads are in flight
+    // before its first step, off the state's dependency chain
+    uint2 ent[kEncGroup];
 #pragma unroll
-    for (int j = (int)kRun - 1; j >= 0; --j) {
+    for (int jj = 0; jj < (int)kEncGroup; ++jj) ent[jj] = tab[sym_at<W>(d, g * (int)kEncGroup + jj)];
+#pragma unroll
+    for (int jj = (int)kEncGroup - 1; jj >= 0; --jj) {
+      const int j = g * (int)kEncGroup + jj;
       const bool valid = FULL || base + (uint32_t)j < nb;
-      const uint2 e = ent[j];
+      const uint2 e = ent[jj];
       const uint32_t fs = e.x & 0x1fffu;
       const bool emit = valid && (x >> 20) >= fs;
       const uint64_t mask = __ballot(emit);
@@ -226,6 +231,7 @@ __device__ __forceinline__ void encode_runs(const uint8_t* blk, uint64_t avail, 
         const uint32_t q = (t1 + ((x - t1) >> ((e.x >> 25) & 1u))) >> (e.x >> 26);
         x = (q << kPB) + (x - q * fs) + ((e.x >> 13) & 0xfffu);
       }
+    }
     }
     if (pos < 0) return;
 #pragma unroll
@@ -385,15 +391,44 @@ __global__ __launch_bounds__(kScanThreads) void rans_scan_kernel(const EncBatch 
 }
 
 // ------------------------------------------------------------------ compaction
-template <int W>
+// SCAN: the workgroup sums the sizes of the blocks in front of its own (streams of
+// at most kFusedScanBlocks blocks), writes its offset, and the last block's
+// workgroup writes the header and the length; otherwise rans_scan_kernel ran first.
+constexpr uint32_t kFusedScanBlocks = 512;
+static_assert(kCopyThreads == kBlockThreads, "block_sum covers the compaction workgroup");
+
+template <int W, bool SCAN>
 __global__ __launch_bounds__(kCopyThreads) void rans_compact_kernel(const EncBatch bt) {
   using G = RansGeo<W>;
+  __shared__ uint32_t red[kSubs];
   const int jb = job_of(bt, blockIdx.x);
   const uint64_t n = bt.n[jb];
   const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
   const uint64_t b = blockIdx.x - bt.first[jb];
   uint8_t* out = bt.out[jb];
-  const uint64_t off = gld(reinterpret_cast<const uint64_t*>(out + 32) + b);
+  uint64_t off;
+  if (SCAN) {
+    const uint32_t* sizes = bt.sizes[jb];
+    uint32_t part = 0;  // block sizes are < 2^17 and b < kFusedScanBlocks: no overflow
+    for (uint32_t i = threadIdx.x; i < (uint32_t)b; i += kCopyThreads) part += gld(sizes + i);
+    off = block_sum(part, red);
+    if (threadIdx.x == 0) {
+      gst(reinterpret_cast<uint64_t*>(out + 32) + b, off);
+      if (b + 1 == nblk) {
+        const uint64_t payload = off + gld(sizes + b);
+        uint32_t* h = reinterpret_cast<uint32_t*>(out);
+        gst(h + 0, kRansMagic);
+        gst(h + 1, 2u | ((uint32_t)W << 8) | (kPB << 16) | (8u << 24));
+        gst(h + 2, kBlock);
+        gst(h + 3, nblk);
+        gst(reinterpret_cast<uint64_t*>(out + 16), n);
+        gst(reinterpret_cast<uint64_t*>(out + 24), payload);
+        gst(bt.out_len[jb], (uint64_t)(32u + 8ull * nblk + payload));
+      }
+    }
+  } else {
+    off = gld(reinterpret_cast<const uint64_t*>(out + 32) + b);
+  }
   uint32_t* dst = reinterpret_cast<uint32_t*>(out + 32 + 8ull * nblk + off);
   const uint8_t* slot = bt.slots[jb] + b * G::kSlot;
   const uint32_t tag = gld(reinterpret_cast<const uint32_t*>(slot));
@@ -640,9 +675,19 @@ __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBat
 template <int W>
 int rans_encode_w(const EncBatch& bt, hipStream_t stream) {
   const uint32_t total = bt.first[bt.count];
+  // streams with no block (n = 0) get their header from the scan kernel
+  bool fused = true;
+  for (int i = 0; i < bt.count; ++i) {
+    const uint32_t nblk = bt.first[i + 1] - bt.first[i];
+    fused = fused && nblk >= 1 && nblk <= kFusedScanBlocks;
+  }
   if (total) hipLaunchKernelGGL(rans_encode_kernel<W>, dim3(total), dim3(kBlockThreads), 0, stream, bt);
-  hipLaunchKernelGGL(rans_scan_kernel<W>, dim3(bt.count), dim3(kScanThreads), 0, stream, bt);
-  if (total) hipLaunchKernelGGL(rans_compact_kernel<W>, dim3(total), dim3(kCopyThreads), 0, stream, bt);
+  if (fused) {
+    hipLaunchKernelGGL((rans_compact_kernel<W, true>), dim3(total), dim3(kCopyThreads), 0, stream, bt);
+  } else {
+    hipLaunchKernelGGL(rans_scan_kernel<W>, dim3(bt.count), dim3(kScanThreads), 0, stream, bt);
+    if (total) hipLaunchKernelGGL((rans_compact_kernel<W, false>), dim3(total), dim3(kCopyThreads), 0, stream, bt);
+  }
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
