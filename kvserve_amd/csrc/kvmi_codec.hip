@@ -157,7 +157,12 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int B = job.num_blocks;
   const int nwg = (B + g.bpw - 1) / g.bpw;
-  if ((int)blockIdx.x >= nwg) return;
+  if ((int)blockIdx.x >= nwg) {
+    // a job without blocks still heads its chunk (the stream of N = 0 symbols)
+    if (nwg == 0 && blockIdx.x == 0 && threadIdx.x == 0 && job.write_header && !(g.flags & KVMI_F_NO_HEADER))
+      write_stream_header(job.stream, BITS, job.chunk_symbols);
+    return;
+  }
   const int H = g.H, S = g.S, HD = H * D, G = g.G;
   const int blk0 = blockIdx.x * g.bpw;
   const int blk1 = min(B, blk0 + g.bpw);

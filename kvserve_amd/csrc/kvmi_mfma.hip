@@ -519,6 +519,138 @@ __device__ __forceinline__ float halves_max(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// ============================================================== tile helpers
+// K statistics of one signed tile, orientation N: output register i of chunk c holds
+// row m = 8*(i/4) + 4*hl + i%4 of the tile and channel f(r, c) = HALF*(r>>4) + 16*c +
+// (r & 15); row m has head m % H, which depends only on s = i%4 (32 % H == 0 and
+// H <= 8).  Running min / max per (s, c) of the unscaled accumulators.
+template <int NC>
+__device__ __forceinline__ void kstats_tile(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                            float (&mn)[4][NC], float (&mx)[4][NC]) {
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    f32x16 acc = {};
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int c = cp ^ k;
+      const bool neg = __builtin_popcount(c & cp) & 1;
+      acc = mfma(x[2 * c], neg ? hn[0] : hp[0], acc);
+      acc = mfma(x[2 * c + 1], neg ? hn[1] : hp[1], acc);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      mn[a][cp] = fminf(fminf(mn[a][cp], acc[a]), fminf(acc[a + 4], fminf(acc[a + 8], acc[a + 12])));
+      mx[a][cp] = fmaxf(fmaxf(mx[a][cp], acc[a]), fmaxf(acc[a + 4], fmaxf(acc[a + 8], acc[a + 12])));
+    }
+    chunk_fence();
+  }
+}
+
+// Push a wave's running K min / max into the workgroup's LDS keys [2][H][D] (by
+// source head and channel).  Scaling by 1/sqrt(D) > 0 is monotone, so it commutes
+// with min / max (and so does the bf16 rounding applied when the keys are finalised).
+template <int NC>
+__device__ __forceinline__ void push_lkeys(uint32_t* lkey, const float (&mn)[4][NC], const float (&mx)[4][NC],
+                                           int H, float scale) {
+  constexpr int D = 32 * NC;
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31, HD = H * D;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int h = (4 * hl + a) % H;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int f = (16 * NC) * (r >> 4) + 16 * c + (r & 15);
+      atomicMin(&lkey[h * D + f], f2key(mn[a][c] * scale));
+      atomicMax(&lkey[HD + h * D + f], f2key(mx[a][c] * scale));
+    }
+  }
+}
+
+// The lane's fixed V / K profile values within a job (after fill_positions).
+struct LaneProfile {
+  int jk, jv, gv;
+  float lvk, lvv;
+  bool rep_lane;  // writes the V metadata of (group, token)
+};
+__device__ __forceinline__ LaneProfile lane_profile(const Tables& T, int hme, int hl) {
+  LaneProfile p;
+  p.jk = T.posk[hme];
+  p.jv = T.posv[hme];
+  p.gv = T.prof[1][2][p.jv];
+  p.lvk = (float)T.prof[0][1][p.jk];
+  p.lvv = (float)T.prof[1][1][p.jv];
+  p.rep_lane = hl == 0 && T.gfirst[p.gv] == hme;
+  return p;
+}
+
+// K section of a signed tile (orientation T): transform and quantize with the
+// per-channel (min, 1/scale) pairs at kq into pkd.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_k_tile(const uint4 (&xk)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                             const float2* kq, float s, float lvk, LanePack<16 * NC, BITS>& pkd,
+                                             uint32_t& over) {
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
+    quant_chunk_k<16 * NC, BITS, CLAMP>(acc, cp, s, kq + 16 * cp, lvk, pkd, over);
+    chunk_fence();
+  }
+}
+
+// V section of a signed tile (per-token statistics over the heads of a group):
+// transform once, keeping y = bf16(acc * s) as bf16 pairs, reduce the group's
+// min / max over the token's lanes, write the (group, token) metadata from the
+// representative lane and quantize into pkd.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_v_tile(const uint4 (&xv)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                             const LaneProfile& lp, const kvmi_layer_job& job, int ntok, int tok,
+                                             int G, int H, float s, LanePack<16 * NC, BITS>& pkd, uint32_t& over) {
+  constexpr int HALF = 16 * NC;
+  uint32_t ypk[HALF / 2];
+  float amn = __builtin_inff(), amx = -__builtin_inff();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
+      amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) ypk[8 * cp + i / 2] = pack_bf16x2(acc[i] * s, acc[i + 1] * s);
+    chunk_fence();
+  }
+  // y = bf16(fl(acc * s)) is monotone in acc (s > 0): the row's min / max of y
+  // are those of acc pushed through the same rounding.
+  amn = halves_min(amn);
+  amx = halves_max(amx);
+  float mn = 0.f, mx = 0.f;
+  for (int gg = 0; gg < G; ++gg) {
+    float a = lp.gv == gg ? amn : __builtin_inff();
+    float b = lp.gv == gg ? amx : -__builtin_inff();
+    token_minmax(a, b, H);
+    if (lp.gv == gg) {
+      mn = a;
+      mx = b;
+    }
+  }
+  mn = rbf(mn * s);
+  mx = rbf(mx * s);
+  const float sc = quant_scale(mn, mx, (int)lp.lvv);
+  const float rcp = 1.0f / sc;
+  if (lp.rep_lane) {
+    gst(job.vmeta + (int64_t)lp.gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
+    gst(job.vmeta + (int64_t)(G + lp.gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
+  }
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    quant_chunk_v<HALF, BITS, CLAMP>(ypk + 8 * cp, cp, mn, rcp, lp.lvv, pkd, over);
+    chunk_fence();
+  }
+}
+
 // ============================================================== K statistics (orientation N)
 template <int NC>
 __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
@@ -546,9 +678,7 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
   hp[1] = hadamard_tile(1, true, false);
   hn[0] = hadamard_tile(0, true, true);
   hn[1] = hadamard_tile(1, true, true);
-  // Output register i of chunk c holds row m = 8*(i/4) + 4*hl + i%4 of the tile and
-  // channel f(r, c) = HALF*(r>>4) + 16*c + (r & 15); row m has head m % H, which
-  // depends only on s = i%4 (32 % H == 0 and H <= 8).  Running min/max per (s, c).
+  // running min / max per (output register % 4, chunk): see kstats_tile
   float mn[4][NC], mx[4][NC];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -562,23 +692,7 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(x[u]);
     sign_half_row<NC>(T, hme, hl, x);
-#pragma unroll
-    for (int cp = 0; cp < NC; ++cp) {
-      f32x16 acc = {};
-#pragma unroll
-      for (int k = 0; k < NC; ++k) {
-        const int c = cp ^ k;
-        const bool neg = __builtin_popcount(c & cp) & 1;
-        acc = mfma(x[2 * c], neg ? hn[0] : hp[0], acc);
-        acc = mfma(x[2 * c + 1], neg ? hn[1] : hp[1], acc);
-      }
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        mn[a][cp] = fminf(fminf(mn[a][cp], acc[a]), fminf(acc[a + 4], fminf(acc[a + 8], acc[a + 12])));
-        mx[a][cp] = fmaxf(fmaxf(mx[a][cp], acc[a]), fmaxf(acc[a + 4], fmaxf(acc[a + 8], acc[a + 12])));
-      }
-      chunk_fence();
-    }
+    kstats_tile<NC>(x, hp, hn, mn, mx);
   };
   auto fetch = [&](int t, uint4 (&x)[2 * NC]) {
     load_half_row<NC>(pool, tile_row0(job, S, H, tile_tok(run.tok0, H, t)) + r, hl, x);
@@ -596,21 +710,8 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
     fetch(min(t + 2 * kWaves, last_tile), xa);
     accumulate(xb);
   }
-  // Push per (head, channel): scaling by 1/sqrt(D) > 0 is monotone, so it commutes
-  // with min / max (and so does the bf16 rounding applied by the finaliser).
   const int HD = H * D;
-  if (wave < run.tiles) {
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int h = (4 * hl + a) % H;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int f = (16 * NC) * (r >> 4) + 16 * c + (r & 15);
-        atomicMin(&lkey[h * D + f], f2key(mn[a][c] * g.scale));
-        atomicMax(&lkey[HD + h * D + f], f2key(mx[a][c] * g.scale));
-      }
-    }
-  }
+  if (wave < run.tiles) push_lkeys<NC>(lkey, mn, mx, H, g.scale);
   __syncthreads();
   for (int i = threadIdx.x; i < HD; i += kMW) {
     if (lkey[i] != 0xffffffffu) atomicMin(&job.kstats[i], lkey[i]);
@@ -627,7 +728,12 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const int S = g.S, H = g.H, G = g.G, HD = H * D;
   const int ntok = job.num_blocks * S;
   const Run run = wg_run(job, g);
-  if ((int)blockIdx.x >= run.nwg) return;
+  if ((int)blockIdx.x >= run.nwg) {
+    // a job without blocks still heads its chunk (the stream of N = 0 symbols)
+    if (run.nwg == 0 && blockIdx.x == 0 && threadIdx.x == 0 && job.write_header && !(g.flags & KVMI_F_NO_HEADER))
+      write_stream_header(job.stream, BITS, job.chunk_symbols);
+    return;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
 
@@ -659,10 +765,7 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
 
   // this lane's head, its output positions and V statistic group
   const int hme = r % H;
-  const int jk = T.posk[hme], jv = T.posv[hme];
-  const int gv = T.prof[1][2][jv];
-  const float lvk = (float)T.prof[0][1][jk], lvv = (float)T.prof[1][1][jv];
-  const bool rep_lane = hl == 0 && T.gfirst[gv] == hme;  // writes the V metadata of (group, token)
+  const LaneProfile lp = lane_profile(T, hme, hl);
   const float s = g.scale;
 
   uint8_t* ost = reinterpret_cast<uint8_t*>(ostage + wave * TQ);
@@ -670,7 +773,7 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   // byte offset of this lane's half-row in the staged image, by output position
   auto stage_off = [&](int j) { return native ? (r / H) * (H * RB) + j * RB + hl * (RB / 2)
                                               : j * (tpt * RB) + (r / H) * RB + hl * (RB / 2); };
-  const int offk = stage_off(jk), offv = stage_off(jv);
+  const int offk = stage_off(lp.jk), offv = stage_off(lp.jv);
   // write the staged image of (part, tile starting at token ta) to the stream
   auto flush = [&](int part, int ta) {
     const int rq = native ? TQ : tpt * RB / 16;  // uint4 per run
@@ -697,14 +800,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
     {
       sign_half_row<NC>(T, hme, hl, xk);
       LanePack<HALF, BITS> pkd;
-      pkd.clear();
-      const float2* kq = &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl);
-#pragma unroll
-      for (int cp = 0; cp < NC; ++cp) {
-        const f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
-        quant_chunk_k<HALF, BITS, CLAMP>(acc, cp, s, kq + 16 * cp, lvk, pkd, over);
-        chunk_fence();
-      }
+      quant_k_tile<NC, BITS, CLAMP>(xk, hp, hn, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), s, lp.lvk, pkd,
+                                    over);
       pkd.store_lds(ost + offk);
       flush(0, ta);
     }
@@ -713,50 +810,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
     load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)) + r, hl, xk);
     // ---------------- V: per-token statistics over the heads of a group
     sign_half_row<NC>(T, hme, hl, xv);
-    // one transform: y = bf16(acc * s) kept as bf16 pairs for the quantization below
-    uint32_t ypk[HALF / 2];
-    float amn = __builtin_inff(), amx = -__builtin_inff();
-#pragma unroll
-    for (int cp = 0; cp < NC; ++cp) {
-      const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
-        amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
-      }
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) ypk[8 * cp + i / 2] = pack_bf16x2(acc[i] * s, acc[i + 1] * s);
-      chunk_fence();
-    }
-    // y = bf16(fl(acc * s)) is monotone in acc (s > 0): the row's min / max of y
-    // are those of acc pushed through the same rounding.
-    amn = halves_min(amn);
-    amx = halves_max(amx);
-    float mn = 0.f, mx = 0.f;
-    for (int gg = 0; gg < G; ++gg) {
-      float a = gv == gg ? amn : __builtin_inff();
-      float b = gv == gg ? amx : -__builtin_inff();
-      token_minmax(a, b, H);
-      if (gv == gg) {
-        mn = a;
-        mx = b;
-      }
-    }
-    mn = rbf(mn * s);
-    mx = rbf(mx * s);
-    const float sc = quant_scale(mn, mx, (int)lvv);
-    const float rcp = 1.0f / sc;
-    if (rep_lane) {
-      gst(job.vmeta + (int64_t)gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
-      gst(job.vmeta + (int64_t)(G + gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
-    }
     LanePack<HALF, BITS> pkd;
-    pkd.clear();
-#pragma unroll
-    for (int cp = 0; cp < NC; ++cp) {
-      quant_chunk_v<HALF, BITS, CLAMP>(ypk + 8 * cp, cp, mn, rcp, lvv, pkd, over);
-      chunk_fence();
-    }
+    quant_v_tile<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, pkd, over);
     pkd.store_lds(ost + offv);
     flush(1, ta);
   }

@@ -338,3 +338,30 @@ def test_geometries_match_oracle(cuda, H, S, D, bits):
     torch.cuda.synchronize()
     for l in range(L):
         _check_layer(packet, l, x[l], _bits(dst[l][:, ids.to(cuda).long()]))
+
+
+@pytest.mark.parametrize("fwht", ["mfma", "valu"])
+def test_batch_with_empty_request_writes_its_header(cuda, fwht):
+    """A request without blocks in a batch still gets a valid 16-byte header for N = 0
+    from the encode launch (the C-ABI contract, independent of the host's plan-time
+    header), and the other requests are unaffected."""
+    from kvserve_amd.engine import FusedKVCodec, check_packet
+
+    g = torch.Generator().manual_seed(41)
+    L, H, D, S, P = 2, 8, 128, 16, 32
+    pools, reqs = _small_requests(cuda, g, [5, 0, 3], L, H, D, S, P)
+    codec = FusedKVCodec(H, D, S, 4, 0xC0FEBABE, fwht=fwht)
+    bplan = codec.plan_compress_batch([(pools, ids.to(cuda), prof) for ids, prof in reqs])
+    for pk in bplan.packets:
+        for st in pk.streams:
+            st.zero_()
+    bplan.run()
+    bplan.check_errors()
+    for (ids, prof), pk in zip(reqs, bplan.packets):
+        for (s, e), st in zip(pk.chunks, pk.streams):
+            n = (e - s) * 2 * H * pk.num_blocks * S * D
+            assert np.array_equal(st[:16].cpu().numpy(), _header(4, n))
+        for l in range(L):
+            if pk.num_blocks:
+                _check_layer(pk, l, _bits(pools[l][:, ids.long().to(cuda)]))
+    assert bplan.packets[1].num_blocks == 0
