@@ -194,6 +194,33 @@ int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
                       int32_t max_blocks, int32_t* err, kvmi_stream_t stream);
 
 /*
+ * Fused Hadamard quantizer with fp32 statistics: quantizer_config.impl
+ * "tilelang_fused", replacing KVHadamardQuantOp.compress_v3 / decompress_v3
+ * (kvserve_v1/tilelang_ops/kv_hadamard_quant.py:1519-1599, :1645-1750) behind
+ * TileLangFusedQuantizer.quantize / .dequantize
+ * (kvserve_v1/compression/quantizer/tilelang_quantizer.py:142-181).
+ * One dense layer x = bf16 [2][rows][H][D] (rows = blocks * block_size, D in
+ * {64, 128}, H dividing 64): y = FWHT_fp32(x * s) / sqrt(D) in the reference's
+ * butterfly order; K per-(head, channel) and V per-(row, head) min / max of the fp32
+ * y (V reduced over the heads of each group), scale = max(max - min, 1e-5) / (L - 1),
+ * q = clamp(roundf((bf16(y) - min) / scale), 0, L) as uint8 [2][rows][H][D] (natural
+ * head order).  levels: fp32 [2][H] (K then V), vgroup: int32 [H] group of each head
+ * (heads with equal V levels).  Outputs fp32 kmeta [2][H][D] and vmeta [2][rows][H]
+ * (min, scale).  `scratch` holds kvmi_v3_scratch_bytes(rows, H, D) bytes.  x, q and
+ * out (below) are 16-byte aligned.
+ */
+int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim, const uint32_t* signs,
+                     const float* levels, const int32_t* vgroup, uint8_t* q, float* kmeta, float* vmeta,
+                     void* scratch, kvmi_stream_t stream);
+/* Scratch bytes of kvmi_v3_compress (-1 for an unsupported shape). */
+int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim);
+/* Inverse: x = fma(q, scale, min) with float16 metadata (the wire form: kmeta16
+ * [2][H][D], vmeta16 [2][rows][H]), FWHT_fp32, bf16((y / sqrt(D)) * s) -> out
+ * bf16 [2][rows][H][D]. */
+int kvmi_v3_decompress(const uint8_t* q, int64_t rows, int32_t num_heads, int32_t head_dim, const uint32_t* signs,
+                       const uint16_t* kmeta16, const uint16_t* vmeta16, void* out, kvmi_stream_t stream);
+
+/*
  * Entropy codec (rANS) for the codec stage -- replaces the nvCOMP ANS codec that
  * KVServe's codec stage calls (kvserve_v1/compression/codec/kvserve_codec.py:57-64,
  * nvcomp_func.py:54-143: a uint8 view in, compressed bytes out, and back).  The

@@ -44,6 +44,9 @@ EXPORTS = (
     "kvmi_rans_decode",
     "kvmi_rans_encode_batch",
     "kvmi_rans_decode_batch",
+    "kvmi_v3_compress",
+    "kvmi_v3_scratch_bytes",
+    "kvmi_v3_decompress",
     "kvmi_rt_encode",
     "kvmi_rt_decode",
     "kvmi_rt_hadamard",
@@ -127,6 +130,9 @@ _SIGNATURES = {
     "kvmi_rans_decode": ([_vp, _i64, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rans_encode_batch": ([ctypes.POINTER(RansEncJob), _i32, _i32, _vp], ctypes.c_int),
     "kvmi_rans_decode_batch": ([ctypes.POINTER(RansDecJob), _i32, _i32, _vp, _vp], ctypes.c_int),
+    "kvmi_v3_compress": ([_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "kvmi_v3_scratch_bytes": ([_i64, _i32, _i32], _i64),
+    "kvmi_v3_decompress": ([_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rt_encode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
     "kvmi_rt_decode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rt_hadamard": ([_vp, _vp, _i64, _i32, _vp], ctypes.c_int),

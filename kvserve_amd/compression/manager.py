@@ -15,8 +15,12 @@ Registry (_build_manager, manager.py:187-216):
                                             "nvcomp" (ANS) / "lc" served by the GPU rANS codec)
   quantizer_config.impl    absent / "kvserve" / "hip_fused" -> the fused gfx950 manager
                            (same numerics as the modular torch operators);
-                           "tilelang_fused" and "centered_codebook" are CUDA-only
-                           implementations with other numerics and are rejected.
+                           "tilelang_fused" (also as top-level "impl" / "quantizer_impl")
+                           -> FusedHadamardQuantizer (the compress_v3 numerics) in the
+                           operator pipeline, with the normalisation of manager.py:151-185
+                           (the transformer stage is folded into the quantizer);
+                           "centered_codebook" is a CUDA-only implementation and is
+                           rejected.
   The controller mode (online bandit profile selection) is outside this engine.
 """
 
@@ -31,14 +35,15 @@ import torch
 from .codec import KVServeCodec
 from .compression_manager import (CompressedKVData, CompressionConfig, CompressionManager,
                                   FusedCompressionManager, get_default_compression_config)
-from .quantizer import KVServeQuantizer
+from .quantizer import FusedHadamardQuantizer, KVServeQuantizer
 from .transformer import KVServeTransformer
 
 log = logging.getLogger("kvserve_amd")
 
 _COMPRESSED_SENTINEL = "__compressed__"
 FUSED_IMPLS = (None, "kvserve", "hip_fused")
-_CUDA_ONLY = ("tilelang_fused", "centered_codebook")
+_CUDA_ONLY = ("centered_codebook",)
+TILELANG_IMPL = "tilelang_fused"
 
 
 def is_compressed_layer_names(layer_names: list) -> bool:
@@ -86,10 +91,47 @@ class KVCompressionAdapter:
             return cfg.get("quantizer_impl")
         return (cfg.get("quantizer_config") or {}).get("impl")
 
+    @staticmethod
+    def _is_tilelang_fused(cfg: dict) -> bool:
+        """manager.py:151-158."""
+        if cfg.get("impl") == TILELANG_IMPL or cfg.get("quantizer_impl") == TILELANG_IMPL:
+            return True
+        return (cfg.get("quantizer_config") or {}).get("impl") == TILELANG_IMPL
+
+    @classmethod
+    def _normalize_tilelang(cls, cfg: dict) -> dict:
+        """manager.py:160-185: one fused configuration at construction and per request
+        -- the quantizer carries the Hadamard seed and the transformer stage goes."""
+        if (cfg.get("quantizer_config") or {}).get("impl") == "centered_codebook":
+            raise ValueError("centered_codebook cannot use the tilelang_fused implementation")
+        pipeline = list(cfg.get("pipeline", []))
+        if "quantizer" not in pipeline:
+            raise ValueError("tilelang_fused requires a quantizer pipeline stage")
+        qc = dict(cfg.get("quantizer_config") or {})
+        qc["impl"] = TILELANG_IMPL
+        if "transformer" in pipeline:
+            tc = dict(cfg.get("transformer_config") or {})
+            if tc.get("transform_type", "hadamard") != "hadamard":
+                raise ValueError("tilelang_fused only fuses the Hadamard transformer")
+            seed = tc.get("seed", 0x3333)
+            explicit = qc.get("base_seed", qc.get("seed"))
+            if "seed" in tc and explicit is not None and int(explicit) != int(seed):
+                raise ValueError("Conflicting transformer seed and fused quantizer seed")
+            qc.setdefault("base_seed", explicit if explicit is not None else seed)
+            pipeline = [p for p in pipeline if p != "transformer"]
+        cfg["quantizer_config"] = qc
+        cfg["pipeline"] = pipeline
+        for stage in pipeline:
+            if stage not in ("quantizer", "codec"):
+                raise ValueError(f"unknown pipeline stage '{stage}'")
+        return cfg
+
     @classmethod
     def _normalize_config(cls, cfg: dict) -> dict:
         """Validate the implementation choice and the pipeline stages."""
         cfg = dict(cfg)
+        if cls._is_tilelang_fused(cfg):
+            return cls._normalize_tilelang(cfg)
         impl = cls._impl(cfg)
         if impl in _CUDA_ONLY:
             raise ValueError(f"quantizer impl '{impl}' is a CUDA-only implementation; use 'hip_fused'")
@@ -107,7 +149,7 @@ class KVCompressionAdapter:
         cfg = self._normalize_config(cfg)
         qc = cfg.get("quantizer_config")
         if qc is not None:
-            qc = {k: v for k, v in qc.items() if k != "impl"}
+            qc = {k: v for k, v in qc.items() if k != "impl" or v == TILELANG_IMPL}
             qc["tp_rank"] = self._tp_rank
             qc["tensor_parallel_size"] = self._tp_size
         return CompressionConfig(enabled=cfg.get("enabled", True), pipeline=cfg.get("pipeline", []),
@@ -120,8 +162,11 @@ class KVCompressionAdapter:
         pipeline = list(cfg.get("pipeline", []))
         config = self._make_config(cfg)
         transformer = KVServeTransformer if "transformer" in pipeline else None
-        quantizer = KVServeQuantizer if "quantizer" in pipeline else None
         codec = KVServeCodec if "codec" in pipeline else None
+        if self._is_tilelang_fused(cfg):
+            return CompressionManager(config=config, transformer=transformer, quantizer=FusedHadamardQuantizer,
+                                      codec=codec)
+        quantizer = KVServeQuantizer if "quantizer" in pipeline else None
         cls = FusedCompressionManager if "quantizer" in pipeline else CompressionManager
         return cls(config=config, transformer=transformer, quantizer=quantizer, codec=codec)
 

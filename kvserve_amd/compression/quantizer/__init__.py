@@ -1,4 +1,6 @@
-"""Quantizers: KVServe's hybrid min-max quantizer on gfx950."""
+"""Quantizers: KVServe's hybrid min-max quantizer and the fused Hadamard quantizer
+(impl "tilelang_fused") on gfx950."""
+from .fused_quantizer import FusedHadamardQuantizer, TileLangFusedQuantizer
 from .kvserve_quantizer import KVServeQuantizer
 
-__all__ = ["KVServeQuantizer"]
+__all__ = ["FusedHadamardQuantizer", "KVServeQuantizer", "TileLangFusedQuantizer"]

@@ -1,0 +1,346 @@
+// Fused Hadamard quantizer with fp32 statistics (quantizer_config.impl
+// "tilelang_fused"): the arithmetic of KVHadamardQuantOp.compress_v3 /
+// decompress_v3 (kvserve_v1/tilelang_ops/kv_hadamard_quant.py:1519-1599,
+// :1645-1750) on one dense layer [2, R, H, D] (R rows = blocks * block_size).
+//
+// A head-row (one token of one head, D contiguous bf16) is held by a quad of lanes,
+// lane q owning elements [q*E, (q+1)*E), E = D/4; a 256-thread workgroup covers 64
+// consecutive head-rows per pass, and since 64 % H == 0 a lane always sees the same
+// head.  The FWHT is the reference's radix-2 butterfly in fp32 (natural order, lowest
+// index bit first: fwht_row), so y = FWHT(x*s) * (1/sqrt(D)) is bit-identical to the
+// TileLang kernels' values (:521-596).
+//
+// Compress is three launches:
+//   stats:  y of every head-row; K: per-lane running min / max per channel, reduced
+//           over the workgroup in LDS (order-preserving keys) into a per-workgroup
+//           partial [wg][2][H][D]; V: per-head-row min / max over D (:652-659);
+//   kfinal: K min / max over the partials, scale = max(max - min, 1e-5) / (L - 1);
+//   quant:  y again, had = bf16(y); K with the channel constants, V with the
+//           per-(row, head) statistics reduced over the heads of its group (equal L,
+//           :1143-1163); q = clamp(roundf((had - min) / scale), 0, L) as uint8.
+// Decompress is one launch: x = fma(q, scale16, min16), fp32 butterflies,
+// bf16((y * (1/sqrt(D))) * s) (:685-716).
+#include "kvmi_common.hpp"
+
+namespace kvmi {
+namespace {
+
+constexpr int kV3WG = 256;
+constexpr int kV3Rows = kV3WG / 4;  // head-rows per pass
+constexpr int kV3MaxH = 64;
+constexpr int kV3KGrid = 256;       // workgroups of the K statistics pass (partials)
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// Sign bits of lane q's E elements of head h (bit i set = element i negated).
+template <int D>
+__device__ __forceinline__ uint32_t v3_lane_signs(const uint32_t* signs, int h, int q) {
+  constexpr int E = D / 4;
+  const uint32_t* sg = signs + h * (D / 32);
+  if constexpr (E == 32) {
+    return gld(sg + q);
+  } else {  // E == 16
+    return (gld(sg + (q >> 1)) >> ((q & 1) * 16)) & 0xffffu;
+  }
+}
+
+// y = FWHT_fp32(x * s) * (1/sqrt(D)) of the lane's E elements.
+template <int D>
+__device__ __forceinline__ void v3_transform(const uint16_t* src, uint32_t sb, float scale, int q,
+                                             float (&y)[D / 4]) {
+  constexpr int E = D / 4;
+  uint32_t w[E / 2];
+  load_bf16_seg<E>(src, w);
+  apply_sign_bf16<E>(w, sb);
+  unpack_bf16<E>(w, y);
+  fwht_row<E>(y, q);
+#pragma unroll
+  for (int i = 0; i < E; ++i) y[i] *= scale;
+}
+
+// roundf (ties away from zero), clamped to [0, L], as an integer.
+__device__ __forceinline__ uint32_t v3_symbol(float had, float mn, float sc, float lv) {
+  const float r = __builtin_roundf((had - mn) / sc);
+  return (uint32_t)fminf(fmaxf(r, 0.0f), lv);
+}
+
+struct V3Shape {
+  int64_t rows;  // R
+  int H;
+  float scale;   // fp32 1/sqrt(D)
+};
+
+// ------------------------------------------------------------------ stats
+// part 0 (K) writes one partial per workgroup: its grid must not exceed kV3KGrid.
+template <int D>
+__global__ __launch_bounds__(kV3WG) void v3_stats_kernel(V3Shape sh, int part, const uint16_t* __restrict__ x,
+                                                         const uint32_t* __restrict__ signs,
+                                                         uint32_t* __restrict__ kpart, float* __restrict__ vrow) {
+  constexpr int E = D / 4;
+  const int H = sh.H, HD = H * D;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3, h = Q % H;
+  const int64_t hrows = sh.rows * H;
+  const uint16_t* src = x + part * hrows * D;
+  const uint32_t sb = v3_lane_signs<D>(signs, h, q);
+  const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
+  if (part == 1) {  // V: min / max of every head-row over D
+    for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
+      const int64_t hr = p * kV3Rows + Q;
+      if (hr >= hrows) continue;
+      float y[E];
+      v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
+      float mn = y[0], mx = y[0];
+#pragma unroll
+      for (int i = 1; i < E; ++i) {
+        mn = fminf(mn, y[i]);
+        mx = fmaxf(mx, y[i]);
+      }
+      mn = quad_min(mn);
+      mx = quad_max(mx);
+      if (q == 0) {
+        gst(vrow + hr, mn);
+        gst(vrow + hrows + hr, mx);
+      }
+    }
+    return;
+  }
+  // K: running per-channel min / max of the lane's rows
+  __shared__ uint32_t lkey[2 * kV3MaxH * 128];
+  for (int i = tid; i < HD; i += kV3WG) {
+    lkey[i] = 0xffffffffu;
+    lkey[HD + i] = 0u;
+  }
+  float mn[E], mx[E];
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    mn[i] = __builtin_inff();
+    mx[i] = -__builtin_inff();
+  }
+  bool any = false;
+  for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
+    const int64_t hr = p * kV3Rows + Q;
+    if (hr >= hrows) continue;
+    any = true;
+    float y[E];
+    v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      mn[i] = fminf(mn[i], y[i]);
+      mx[i] = fmaxf(mx[i], y[i]);
+    }
+  }
+  __syncthreads();
+  if (any) {
+#pragma unroll
+    for (int i = 0; i < E; ++i) {
+      atomicMin(&lkey[h * D + q * E + i], f2key(mn[i]));
+      atomicMax(&lkey[HD + h * D + q * E + i], f2key(mx[i]));
+    }
+  }
+  __syncthreads();
+  uint32_t* out = kpart + (int64_t)blockIdx.x * 2 * HD;
+  for (int i = tid; i < 2 * HD; i += kV3WG) gst(out + i, lkey[i]);
+}
+
+// K statistics over the partials -> kmeta [2][H][D] = (min, scale).
+__global__ __launch_bounds__(kV3WG) void v3_kfinal_kernel(int HD, int D, int nparts, const uint32_t* __restrict__ kpart,
+                                                          const float* __restrict__ levels, float* __restrict__ kmeta) {
+  const int i = blockIdx.x * kV3WG + threadIdx.x;
+  if (i >= HD) return;
+  uint32_t a = 0xffffffffu, b = 0u;
+  for (int w = 0; w < nparts; ++w) {
+    a = min(a, gld(kpart + (int64_t)w * 2 * HD + i));
+    b = max(b, gld(kpart + (int64_t)w * 2 * HD + HD + i));
+  }
+  const float mn = key2f(a), mx = key2f(b);
+  const float lv = gld(levels + i / D);
+  gst(kmeta + i, mn);
+  gst(kmeta + HD + i, fmaxf(mx - mn, 1e-5f) / (lv - 1.0f));
+}
+
+// ------------------------------------------------------------------ quantize
+template <int D>
+__global__ __launch_bounds__(kV3WG) void v3_quant_kernel(V3Shape sh, const uint16_t* __restrict__ x,
+                                                         const uint32_t* __restrict__ signs,
+                                                         const float* __restrict__ levels,
+                                                         const int32_t* __restrict__ vgroup,
+                                                         const float* __restrict__ kmeta,
+                                                         const float* __restrict__ vrow, uint8_t* __restrict__ qout,
+                                                         float* __restrict__ vmeta) {
+  constexpr int E = D / 4;
+  const int part = blockIdx.y;
+  const int H = sh.H, HD = H * D;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3, h = Q % H;
+  const int64_t hrows = sh.rows * H;
+  const uint16_t* src = x + part * hrows * D;
+  uint8_t* dst = qout + part * hrows * D;
+  const uint32_t sb = v3_lane_signs<D>(signs, h, q);
+  const float lv = gld(levels + part * H + h);
+  const int grp = gld(vgroup + h);
+  const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
+  for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
+    const int64_t hr = p * kV3Rows + Q;
+    if (hr >= hrows) continue;
+    float y[E];
+    v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
+    uint32_t sym[E];
+    if (part == 0) {
+      const float* kmn = kmeta + h * D + q * E;
+#pragma unroll
+      for (int i = 0; i < E; ++i) sym[i] = v3_symbol(round_bf16(y[i]), gld(kmn + i), gld(kmn + HD + i), lv);
+    } else {
+      // the row's statistics over the heads of this head's group
+      const int64_t r = hr / H;
+      float gmn = __builtin_inff(), gmx = -__builtin_inff();
+      for (int k = 0; k < H; ++k) {
+        if (gld(vgroup + k) != grp) continue;
+        gmn = fminf(gmn, gld(vrow + r * H + k));
+        gmx = fmaxf(gmx, gld(vrow + hrows + r * H + k));
+      }
+      const float sc = fmaxf(gmx - gmn, 1e-5f) / (lv - 1.0f);
+      if (q == 0) {
+        gst(vmeta + hr, gmn);
+        gst(vmeta + hrows + hr, sc);
+      }
+#pragma unroll
+      for (int i = 0; i < E; ++i) sym[i] = v3_symbol(round_bf16(y[i]), gmn, sc, lv);
+    }
+    uint32_t w[E / 4];
+#pragma unroll
+    for (int i = 0; i < E / 4; ++i)
+      w[i] = sym[4 * i] | (sym[4 * i + 1] << 8) | (sym[4 * i + 2] << 16) | (sym[4 * i + 3] << 24);
+    uint4* o = reinterpret_cast<uint4*>(dst + hr * D + q * E);
+#pragma unroll
+    for (int i = 0; i < E / 16; ++i) gst(o + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
+  }
+}
+
+// ------------------------------------------------------------------ dequantize
+template <int D>
+__global__ __launch_bounds__(kV3WG) void v3_dequant_kernel(V3Shape sh, const uint8_t* __restrict__ qin,
+                                                           const uint32_t* __restrict__ signs,
+                                                           const uint16_t* __restrict__ kmeta16,
+                                                           const uint16_t* __restrict__ vmeta16,
+                                                           uint16_t* __restrict__ out) {
+  constexpr int E = D / 4;
+  const int part = blockIdx.y;
+  const int H = sh.H, HD = H * D;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3, h = Q % H;
+  const int64_t hrows = sh.rows * H;
+  const uint8_t* src = qin + part * hrows * D;
+  uint16_t* dst = out + part * hrows * D;
+  const uint32_t sb = v3_lane_signs<D>(signs, h, q);
+  const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
+  for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
+    const int64_t hr = p * kV3Rows + Q;
+    if (hr >= hrows) continue;
+    uint32_t w[E / 4];
+    const uint4* s4 = reinterpret_cast<const uint4*>(src + hr * D + q * E);
+#pragma unroll
+    for (int i = 0; i < E / 16; ++i) {
+      const uint4 t = gld(s4 + i);
+      w[4 * i] = t.x;
+      w[4 * i + 1] = t.y;
+      w[4 * i + 2] = t.z;
+      w[4 * i + 3] = t.w;
+    }
+    float v[E];
+    if (part == 0) {
+      const uint16_t* mn = kmeta16 + h * D + q * E;
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        const float sym = (float)((w[i / 4] >> (8 * (i % 4))) & 0xffu);
+        v[i] = __builtin_fmaf(sym, f16_to_f32(gld(mn + HD + i)), f16_to_f32(gld(mn + i)));
+      }
+    } else {
+      const float mn = f16_to_f32(gld(vmeta16 + hr)), sc = f16_to_f32(gld(vmeta16 + hrows + hr));
+#pragma unroll
+      for (int i = 0; i < E; ++i) v[i] = __builtin_fmaf((float)((w[i / 4] >> (8 * (i % 4))) & 0xffu), sc, mn);
+    }
+    fwht_row<E>(v, q);
+    uint32_t o[E / 2];
+#pragma unroll
+    for (int i = 0; i < E / 2; ++i) o[i] = pack_bf16x2(v[2 * i] * sh.scale, v[2 * i + 1] * sh.scale);
+    apply_sign_bf16<E>(o, sb);  // (y * (1/sqrt(D))) * s: the sign is exact after rounding
+    store_bf16_seg<E>(dst + hr * D + q * E, o);
+  }
+}
+
+// ------------------------------------------------------------------ launch
+int v3_check(int64_t rows, int32_t H, int32_t D) {
+  if (rows < 0 || H < 1 || H > kV3MaxH || (kV3Rows % H) != 0 || (D != 64 && D != 128)) return KVMI_EINVAL;
+  if (rows * H > (int64_t)1 << 31) return KVMI_EINVAL;
+  return KVMI_OK;
+}
+
+int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
+unsigned v3_grid(int64_t rows, int H) {
+  const int64_t passes = (rows * H + kV3Rows - 1) / kV3Rows;
+  return (unsigned)(passes < 4096 ? (passes > 0 ? passes : 1) : 4096);
+}
+
+}  // namespace
+}  // namespace kvmi
+
+extern "C" int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim) {
+  using namespace kvmi;
+  if (v3_check(rows, num_heads, head_dim)) return -1;
+  return align256((int64_t)kV3KGrid * 2 * num_heads * head_dim * 4) + align256(2 * rows * num_heads * 4);
+}
+
+extern "C" int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,
+                                const uint32_t* signs, const float* levels, const int32_t* vgroup, uint8_t* q,
+                                float* kmeta, float* vmeta, void* scratch, kvmi_stream_t stream) {
+  using namespace kvmi;
+  int rc = v3_check(rows, num_heads, head_dim);
+  if (rc) return rc;
+  if (rows == 0) return KVMI_OK;
+  if (!x || !signs || !levels || !vgroup || !q || !kmeta || !vmeta || !scratch) return KVMI_EINVAL;
+  if (((uintptr_t)x | (uintptr_t)q) & 15) return KVMI_EINVAL;  // 16-byte row segments
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int H = num_heads, D = head_dim;
+  V3Shape sh{rows, H, (float)(1.0 / __builtin_sqrt((double)D))};
+  uint32_t* kpart = static_cast<uint32_t*>(scratch);
+  float* vrow = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch) +
+                                         align256((int64_t)kV3KGrid * 2 * H * D * 4));
+  const unsigned g = v3_grid(rows, H);
+  const unsigned gk = g < (unsigned)kV3KGrid ? g : (unsigned)kV3KGrid;  // K partials: at most kV3KGrid
+  const uint16_t* xs = static_cast<const uint16_t*>(x);
+  const unsigned gf = (unsigned)((H * D + kV3WG - 1) / kV3WG);
+  if (D == 64) {
+    hipLaunchKernelGGL((v3_stats_kernel<64>), dim3(gk), dim3(kV3WG), 0, st, sh, 0, xs, signs, kpart, vrow);
+    hipLaunchKernelGGL((v3_stats_kernel<64>), dim3(g), dim3(kV3WG), 0, st, sh, 1, xs, signs, kpart, vrow);
+  } else {
+    hipLaunchKernelGGL((v3_stats_kernel<128>), dim3(gk), dim3(kV3WG), 0, st, sh, 0, xs, signs, kpart, vrow);
+    hipLaunchKernelGGL((v3_stats_kernel<128>), dim3(g), dim3(kV3WG), 0, st, sh, 1, xs, signs, kpart, vrow);
+  }
+  hipLaunchKernelGGL(v3_kfinal_kernel, dim3(gf), dim3(kV3WG), 0, st, H * D, D, (int)gk, kpart, levels, kmeta);
+  if (D == 64)
+    hipLaunchKernelGGL((v3_quant_kernel<64>), dim3(g, 2), dim3(kV3WG), 0, st, sh, xs, signs, levels, vgroup, kmeta,
+                       vrow, q, vmeta);
+  else
+    hipLaunchKernelGGL((v3_quant_kernel<128>), dim3(g, 2), dim3(kV3WG), 0, st, sh, xs, signs, levels, vgroup, kmeta,
+                       vrow, q, vmeta);
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+extern "C" int kvmi_v3_decompress(const uint8_t* q, int64_t rows, int32_t num_heads, int32_t head_dim,
+                                  const uint32_t* signs, const uint16_t* kmeta16, const uint16_t* vmeta16, void* out,
+                                  kvmi_stream_t stream) {
+  using namespace kvmi;
+  int rc = v3_check(rows, num_heads, head_dim);
+  if (rc) return rc;
+  if (rows == 0) return KVMI_OK;
+  if (!q || !signs || !kmeta16 || !vmeta16 || !out) return KVMI_EINVAL;
+  if (((uintptr_t)q | (uintptr_t)out) & 15) return KVMI_EINVAL;  // 16-byte row segments
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  V3Shape sh{rows, num_heads, (float)(1.0 / __builtin_sqrt((double)head_dim))};
+  const unsigned g = v3_grid(rows, num_heads);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (head_dim == 64)
+    hipLaunchKernelGGL((v3_dequant_kernel<64>), dim3(g, 2), dim3(kV3WG), 0, st, sh, q, signs, kmeta16, vmeta16, o);
+  else
+    hipLaunchKernelGGL((v3_dequant_kernel<128>), dim3(g, 2), dim3(kV3WG), 0, st, sh, q, signs, kmeta16, vmeta16, o);
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}

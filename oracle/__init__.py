@@ -13,6 +13,8 @@ Modules
            file:line it follows).
   cbitpack ctypes wrapper of ``bitpack.c``, a C restatement of the bitpack codec
            used for full-size streams.
+  fused_v3 the arithmetic of quantizer impl "tilelang_fused" (compress_v3 /
+           decompress_v3: fp32 statistics, grouped V, roundf, float16 metadata).
 
 Pins (what fixes each function independently of this restatement):
   signs           torch CPU Generator recipe + committed fixture (tests/golden)
@@ -24,6 +26,10 @@ Pins (what fixes each function independently of this restatement):
   layout/chunking golden vectors from the reference's CompressionManager
   bitpack         np.packbits closed form + hand-derived known answers
   gather/scatter  closed form on integer-valued pools
+  fused_v3        float64 derivation on exactly representable inputs, half-step
+                  reconstruction bound, planted bf16-statistics mistake
 Parity unpinned: the summation order inside the third-party fast_hadamard_transform
-(not vendored); this oracle uses the natural radix-2 order, lowest bit first.
+(not vendored); this oracle uses the natural radix-2 order, lowest bit first.  In
+fused_v3, the tie rule of T.round (taken as roundf) and the FMA contraction of the
+dequant (taken as one fma) are TileLang / nvcc lowering choices.
 """

@@ -210,8 +210,11 @@ def test_adapter_registry_contracts():
     assert isinstance(hip._manager, FusedCompressionManager)
     codec_only = KVCompressionAdapter({"pipeline": ["codec"], "codec_config": {"codec_type": "bitpack"}}, 8, 128)
     assert type(codec_only._manager) is CompressionManager
-    for bad, exc in (({**base, "quantizer_config": {"impl": "tilelang_fused"}}, ValueError),
-                     ({**base, "impl": "centered_codebook"}, ValueError),
+    # impl "tilelang_fused": the operator pipeline with the fused Hadamard quantizer
+    tl = KVCompressionAdapter({**base, "quantizer_config": {"impl": "tilelang_fused"}}, 8, 128)
+    assert type(tl._manager) is CompressionManager and tl._config.pipeline == ["quantizer", "codec"]
+    assert type(tl._manager.quantizer).__name__ == "FusedHadamardQuantizer"
+    for bad, exc in (({**base, "impl": "centered_codebook"}, ValueError),
                      ({**base, "pipeline": ["transformer", "zip"]}, ValueError),
                      ({**base, "codec_config": {"codec_type": "nvcomp", "nvcomp_algorithm": "LZ4"}}, ValueError),
                      ({**base, "codec_config": {"codec_type": "nvcomp", "nvcomp_algorithm": "Brotli"}}, ValueError),
@@ -240,3 +243,22 @@ def test_quantizer_validation_matches_reference_asserts():
     q = KVServeQuantizer(split_type="layer", low_key_max_value=6, high_key_max_value=12)
     assert q.layer_profile(31, 8).k_levels == [6] * 8 and q.layer_profile(0, 8).k_levels == [12] * 8
     assert q.layer_profile(31, 8).n_low == 8 and q.layer_profile(0, 8).n_low == 0
+
+
+def test_v3_sizes_and_contract_errors():
+    """The fused quantizer's scratch: 256 K partials [2][H][D] uint32 + V row stats
+    [2][rows][H] fp32, each 256-byte aligned; unsupported shapes and misaligned
+    buffers are rejected on the host."""
+    from kvserve_amd import _lib
+
+    lib = _lib.load()
+    E = _lib.EINVAL
+    assert lib.kvmi_v3_scratch_bytes(100, 8, 128) == 256 * 2 * 8 * 128 * 4 + 6400
+    assert lib.kvmi_v3_scratch_bytes(3, 4, 64) == 256 * 2 * 4 * 64 * 4 + 256
+    for bad in ((5, 8, 96), (5, 3, 128), (5, 128, 128), (-1, 8, 128)):
+        assert lib.kvmi_v3_scratch_bytes(*bad) == -1
+    assert lib.kvmi_v3_compress(None, 4, 8, 96, None, None, None, None, None, None, None, None) == E
+    assert lib.kvmi_v3_compress(None, 0, 8, 128, None, None, None, None, None, None, None, None) == 0
+    assert lib.kvmi_v3_compress(None, 4, 8, 128, None, None, None, None, None, None, None, None) == E
+    assert lib.kvmi_v3_compress(8, 4, 8, 128, 16, 16, 16, 24, 16, 16, 16, None) == E  # q misaligned
+    assert lib.kvmi_v3_decompress(16, 4, 8, 128, 16, 16, 16, 8, None) == E  # out misaligned
