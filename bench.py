@@ -95,8 +95,22 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int) -> dict:
     mfma = codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
     if mfma:
         return {"kvmi_encode_paged": f"encode_mfma_kernel<{D // 32}, {bits}, false>",
-                "kvmi_decode_paged": f"decode_mfma_kernel<{D // 32}, {bits}>"}
-    return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>"}
+                "kvmi_decode_paged": f"decode_mfma_kernel<{D // 32}, {bits}>",
+                "kvmi_kstats_paged": f"kstats_mfma_kernel<{D // 32}>"}
+    return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>",
+            "kvmi_kstats_paged": f"kstats_kernel<{D}>"}
+
+
+def traffic_frac(kernels, seconds: float, workload: str):
+    """Fraction of HBM peak moved by `kernels` (profiled bytes per dispatch, summed)
+    in `seconds`, or None when a kernel has no committed profile."""
+    total = 0
+    for k in kernels:
+        t = profiled_traffic(k, workload)
+        if t is None:
+            return None
+        total += t
+    return round(total / seconds / 1e9 / HBM_PEAK_GBPS, 4)
 
 
 def profiled_traffic(kernel: str, workload: str = "config2"):
@@ -707,7 +721,8 @@ def main() -> int:
     comp_gbps, dec_gbps = R / t_c / 1e6, R / t_d / 1e6
     comp_frac, dec_frac = alg / t_c / 1e6 / HBM_PEAK_GBPS, alg / t_d / 1e6 / HBM_PEAK_GBPS
     dom = "kvmi_encode_paged" if per["kvmi_encode_paged"] >= per["kvmi_decode_paged"] else "kvmi_decode_paged"
-    dom_kernel = hip_kernel_names(codec, S, H, D, bits)[dom]
+    names = hip_kernel_names(codec, S, H, D, bits)
+    dom_kernel = names[dom]
     achieved = alg / per[dom] / 1e6
     ms_step = wall / args.steps * 1e3
 
@@ -734,6 +749,12 @@ def main() -> int:
         "decompress_gbps": round(dec_gbps, 2),
         "compress_hbm_frac": round(comp_frac, 4),
         "decompress_hbm_frac": round(dec_frac, 4),
+        # the same times over the bytes the kernels actually move (rocprofv3 FETCH_SIZE /
+        # WRITE_SIZE per dispatch, copy-calibrated): compress reads K twice
+        "compress_traffic_hbm_frac": traffic_frac(
+            [names["kvmi_kstats_paged"], "kstats_finalize_kernel", names["kvmi_encode_paged"]], t_c / 1e3,
+            args.workload),
+        "decompress_traffic_hbm_frac": traffic_frac([names["kvmi_decode_paged"]], t_d / 1e3, args.workload),
         "kernel_ms": {k: round(v, 4) for k, v in per.items()},
         "roofline": {
             "bound": "hbm",
