@@ -69,7 +69,8 @@ WORKLOADS = {
                  "0xC0FEBABE, Llama-3.1-8B head split hybrid 0.3, 16/16 levels, bitpack 4; step = save + load, "
                  "host-timed with device synchronization; the reference connector's procedure (extract, stack, "
                  "compress, build_wire / restore, decompress, inject) on the same kernels timed beside it",
-    "runtime": "runtime: fixed-profile CompressionRuntime, token view (block_size 1) 1024 tokens x 28 layers x 4 KV "
+    "runtime": "runtime: fixed-profile runtime (create_runtime backend 'fused'), token view (block_size 1) 1024 "
+               "tokens x 28 layers x 4 KV "
                "heads x D=128, default profile (Hadamard, layer split, K channel / V token, levels 12/8 high "
                "6/4 low, ANS codec = GPU rANS over bytes), slot_count 2, one 1024-block chunk per part, seeded "
                "N(0,1) caches; step = encode K then V with completion waits, decode K then V into disjoint "
@@ -443,7 +444,7 @@ def bench_runtime(args) -> dict:
     import torch
 
     from kvserve_amd import _lib
-    from kvserve_amd.runtime import CacheSpec, CompressionConfig, CompressionRuntime, build_memory_plan
+    from kvserve_amd.runtime import CacheSpec, CompressionConfig, build_memory_plan, create_runtime
 
     dev = torch.device("cuda", 0)
     block, blocks, layers, heads, dim = args.rt_block_size, args.rt_blocks, args.rt_layers, 4, 128
@@ -453,7 +454,8 @@ def bench_runtime(args) -> dict:
     specs = {f"layer.{i}": CacheSpec(i, block, heads, dim, torch.bfloat16) for i in range(layers)}
     caches = {n: torch.randn((2 * blocks, heads, block, 2 * dim), device=dev, dtype=torch.bfloat16) for n in specs}
     plan = build_memory_plan(config, specs, blocks_per_logical=1, num_layers=layers, device=dev)
-    runtime = CompressionRuntime(plan, "HND", 1, dev)
+    # the reference's number is its fused backend (scripts/bench_runtime_dispatch.py:92-93)
+    runtime = create_runtime(plan, "HND", 1, dev, backend="fused")
     runtime.bind_kv_caches(caches, dict.fromkeys(specs, 0))
     tokens = blocks * block
     source, destination = list(range(blocks)), list(range(blocks, 2 * blocks))

@@ -233,9 +233,11 @@ int kvmi_v3_decompress(const uint8_t* q, int64_t rows, int32_t num_heads, int32_
  * kvmi_rans_encode: three launches (encode blocks, scan, compact); the stream length
  *   is written to the device u64
  *   *out_len (read it after the stream completes).
- * kvmi_rans_decode: one launch; writes ceil(n*bits/8) packed bytes.  A header that
- *   does not name (bits, n) sets KVMI_ERR_BAD_HEADER; a block that does not decode
- *   to its own end state sets KVMI_ERR_CORRUPT.
+ * kvmi_rans_decode: one launch; writes ceil(n*bits/8) packed bytes.  `in_bytes` is
+ *   the size of the buffer holding the stream (at least the stream's length, which
+ *   its header states; more is allowed).  A header that does not name (bits, n) or a
+ *   stream longer than in_bytes sets KVMI_ERR_BAD_HEADER; a block that does not
+ *   decode to its own end state sets KVMI_ERR_CORRUPT.
  */
 typedef struct kvmi_rans_enc_job {
   const uint8_t* packed; /* n symbols of `bits` bits, LSB-first */

@@ -568,7 +568,7 @@ __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBat
   // every check below is uniform over the workgroup (it reads the same bytes)
   if (gld(h) != kRansMagic || gld(h + 1) != (2u | ((uint32_t)W << 8) | (kPB << 16) | (8u << 24)) ||
       gld(h + 2) != kBlock || gld(h + 3) != nblk || gld(reinterpret_cast<const uint64_t*>(in + 16)) != n ||
-      in_bytes != head + payload) {
+      in_bytes < head + payload) {  // the stream (its header states the length) fits in the buffer
     if (t == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
     return;
   }

@@ -106,6 +106,13 @@ def test_damage_is_reported(cuda):
     bad[head + 4] ^= 0x01                            # frequency table no longer sums to 4096
     with pytest.raises(RuntimeError, match="corrupt entropy-coded stream"):
         ops.rans_decode(bad, n, w)
+    # the stream may sit in a larger buffer (its header states its length); a buffer
+    # shorter than the stream is rejected
+    roomy = torch.zeros(st.numel() + 4096, dtype=torch.uint8, device=cuda)
+    roomy[:st.numel()] = st
+    assert torch.equal(ops.rans_decode(roomy, n, w), ops.rans_decode(st, n, w))
+    with pytest.raises(RuntimeError, match="invalid bitpack header"):
+        ops.rans_decode(st[:-4].clone(), n, w)
 
 
 @pytest.mark.parametrize("w", [3, 4, 8])

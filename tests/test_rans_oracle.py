@@ -178,3 +178,6 @@ def test_corruption_and_contract_errors():
         crans.decode(st, s.size, 4)              # width differs from the header
     with pytest.raises(ValueError, match="-1"):
         crans.decode(st[:-4], s.size, 3)         # truncated
+    # a receive buffer longer than the stream (its header states the length) decodes
+    roomy = np.concatenate([st, np.full(100, 0xAB, np.uint8)])
+    assert np.array_equal(crans.decode(roomy, s.size, 3), s)
