@@ -23,7 +23,8 @@ direction, and the CPU baseline is measured for config2 only).  --workload conne
 times the config-2 request through the vLLM connector (save + load, host-timed) and
 the reference connector's extract/stack/compress procedure beside it; --workload
 config2_ans times the same request with the reference's nvCOMP-ANS profile served by
-the GPU rANS codec.
+the GPU rANS codec.  --workload config2_v3 times the request's layers through the fused
+Hadamard quantizer (impl "tilelang_fused", kvmi_v3_*).
 """
 
 from __future__ import annotations
@@ -69,6 +70,10 @@ WORKLOADS = {
                  "0xC0FEBABE, Llama-3.1-8B head split hybrid 0.3, 16/16 levels, bitpack 4; step = save + load, "
                  "host-timed with device synchronization; the reference connector's procedure (extract, stack, "
                  "compress, build_wire / restore, decompress, inject) on the same kernels timed beside it",
+    "config2_v3": "config2_v3: the config2 request's 32 layers, gathered dense [2, 512, 16, 8, 128] outside the "
+                  "timed region, through impl 'tilelang_fused' (kvmi_v3_compress / kvmi_v3_decompress: fp32 FWHT and "
+                  "statistics, uint8 symbols, fp32 metadata out, float16 metadata in), Hadamard seed 0xC0FEBABE, "
+                  "Llama-3.1-8B head split hybrid 0.3, 16/16 levels; step = compress + decompress of every layer",
     "runtime": "runtime: fixed-profile runtime (create_runtime backend 'fused'), token view (block_size 1) 1024 "
                "tokens x 28 layers x 4 KV "
                "heads x D=128, default profile (Hadamard, layer split, K channel / V token, levels 12/8 high "
@@ -470,6 +475,127 @@ def bench_connector(args) -> dict:
     }
 
 
+def bench_fused_v3(args) -> dict:
+    """impl "tilelang_fused" (kvmi_v3_* through the C-ABI) on the config-2 request's
+    layers.  The operator takes the dense layer [2, B, 16, H, D] that the reference's
+    connector gathers before calling it, so the layers are gathered once outside the
+    timed region; every output buffer is allocated before it."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from kvserve_amd import _lib, workloads
+    from kvserve_amd.compression.quantizer import FusedHadamardQuantizer
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.make_config2(device=dev, num_layers=args.layers)
+    req = wl.requests[0]
+    L, S, H, D, B = len(req.pools), wl.block_size, wl.num_heads, wl.head_dim, req.block_ids.numel()
+    rows = B * S
+    idx = req.block_ids.long()
+    x = torch.stack([p[:, idx].reshape(2, rows, H, D) for p in req.pools])  # [L, 2, rows, H, D]
+    del idx
+    qz = FusedHadamardQuantizer(base_seed=wl.seed, **CONNECTOR_PROFILE["quantizer_config"])
+    tables = [qz._device_tables(l, H, D, dev) for l in range(L)]
+    lib = _lib.load()
+    q = torch.empty((L, 2, rows, H, D), dtype=torch.uint8, device=dev)
+    kmeta = torch.empty((L, 2, H, D), dtype=torch.float32, device=dev)
+    vmeta = torch.empty((L, 2, rows, H), dtype=torch.float32, device=dev)
+    scratch = torch.empty(int(lib.kvmi_v3_scratch_bytes(rows, H, D)), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(x)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def compress():
+        for l in range(L):
+            lv, grp, sg = tables[l]
+            _lib.check(lib.kvmi_v3_compress(x[l].data_ptr(), rows, H, D, sg.data_ptr(), lv.data_ptr(),
+                                            grp.data_ptr(), q[l].data_ptr(), kmeta[l].data_ptr(),
+                                            vmeta[l].data_ptr(), scratch.data_ptr(), sp), "kvmi_v3_compress")
+
+    compress()
+    km16, vm16 = kmeta.to(torch.float16), vmeta.to(torch.float16)  # the wire form of the metadata
+
+    def decompress():
+        for l in range(L):
+            _lib.check(lib.kvmi_v3_decompress(q[l].data_ptr(), rows, H, D, tables[l][2].data_ptr(),
+                                              km16[l].data_ptr(), vm16[l].data_ptr(), out[l].data_ptr(), sp),
+                       "kvmi_v3_decompress")
+
+    print(f"bench: warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        compress()
+        decompress()
+    torch.cuda.synchronize()
+    print(f"bench: timing {args.steps} steps", file=sys.stderr, flush=True)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e in ev:
+        e[0].record(stream)
+        compress()
+        e[1].record(stream)
+        decompress()
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_c = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    t_d = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    R = x.numel() * 2
+    Q = q.numel()
+    M32, M16 = (kmeta.numel() + vmeta.numel()) * 4, (km16.numel() + vm16.numel()) * 2
+    alg_c, alg_d = R + Q + M32, Q + M16 + R  # read KV, write symbols + meta (or the reverse)
+    res = {
+        "metric": "compress/decompress GB/s of raw bf16 KV on 1 MI355X, impl tilelang_fused",
+        "value": round(R / ((t_c + t_d) / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
+        "config": {"workload": WORKLOADS["config2_v3"], "requests": 1, "layers": L, "tokens": rows,
+                   "raw_bytes": R, "symbol_bytes": Q, "meta_bytes_fp32": M32, "meta_bytes_fp16": M16},
+        "compress_ms": round(t_c, 4),
+        "decompress_ms": round(t_d, 4),
+        "compress_gbps": round(R / t_c / 1e6, 2),
+        "decompress_gbps": round(R / t_d / 1e6, 2),
+        "compress_hbm_frac": round(alg_c / t_c / 1e6 / HBM_PEAK_GBPS, 4),
+        "decompress_hbm_frac": round(alg_d / t_d / 1e6 / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "kernel": "v3_dequant_kernel<128> (one launch per layer)",
+                     "achieved": round(alg_d / L / (t_d / L / 1e3) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(alg_d / t_d / 1e6 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": alg_d // L},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import fused_v3 as fv
+        from oracle import kvpipe as kp
+
+        print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
+        xb = x[0].cpu().view(torch.int16).numpy().view(np.uint16)
+        k_lv, v_lv = qz.levels(0, H)
+        signs = kp.rademacher_signs(wl.seed, 0, H, D)
+        n, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_budget / 2 and n < L:
+            t1 = time.perf_counter()
+            rq, rm = fv.compress_layer(xb, signs, k_lv, v_lv)
+            fv.decompress_layer(rq, rm["kmin"].astype(np.float16), rm["kscale"].astype(np.float16),
+                                rm["vmin"].astype(np.float16), rm["vscale"].astype(np.float16), signs)
+            t_cpu += time.perf_counter() - t1
+            n += 1
+        res["cpu_baseline"] = {"value": round(n * (R // L) / t_cpu / 1e9, 4), "unit": "GB/s (round trip, raw bf16 KV)",
+                               "cores": 1, "kind": "port",
+                               "sample": f"{n} x layer 0 of the request ({R // L >> 20} MiB raw) in {t_cpu:.1f} s; "
+                                         f"numpy oracle (oracle/fused_v3.py) compress+decompress, one thread, on "
+                                         f"{cpu_model()}"}
+    return res
+
+
 def bench_runtime(args) -> dict:
     """The reference's runtime dispatch benchmark on the HIP runtime: wall time of
     K then V encode (each fenced), then K then V decode, plus device time of each
@@ -681,9 +807,10 @@ def main() -> int:
 
     import torch
 
-    if args.workload in ("connector", "config2_ans", "runtime"):
+    if args.workload in ("connector", "config2_ans", "runtime", "config2_v3"):
         torch.cuda.set_device(0)
-        fn = {"connector": bench_connector, "config2_ans": bench_entropy, "runtime": bench_runtime}[args.workload]
+        fn = {"connector": bench_connector, "config2_ans": bench_entropy, "runtime": bench_runtime,
+              "config2_v3": bench_fused_v3}[args.workload]
         print(json.dumps(fn(args)), flush=True)
         return 0
 

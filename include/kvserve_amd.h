@@ -206,13 +206,14 @@ int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  * q = clamp(roundf((bf16(y) - min) / scale), 0, L) as uint8 [2][rows][H][D] (natural
  * head order).  levels: fp32 [2][H] (K then V), vgroup: int32 [H] group of each head
  * (heads with equal V levels).  Outputs fp32 kmeta [2][H][D] and vmeta [2][rows][H]
- * (min, scale).  `scratch` holds kvmi_v3_scratch_bytes(rows, H, D) bytes.  x, q and
- * out (below) are 16-byte aligned.
+ * (min, scale).  `scratch` holds kvmi_v3_scratch_bytes(rows, H, D) bytes.  x, q, kmeta
+ * and, below, out and kmeta16 are 16-byte aligned.
  */
 int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim, const uint32_t* signs,
                      const float* levels, const int32_t* vgroup, uint8_t* q, float* kmeta, float* vmeta,
                      void* scratch, kvmi_stream_t stream);
-/* Scratch bytes of kvmi_v3_compress (-1 for an unsupported shape). */
+/* Scratch bytes of kvmi_v3_compress: up to 256 per-workgroup K partials of 2*H*D*4
+ * bytes, not depending on rows (-1 for an unsupported shape). */
 int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim);
 /* Inverse: x = fma(q, scale, min) with float16 metadata (the wire form: kmeta16
  * [2][H][D], vmeta16 [2][rows][H]), FWHT_fp32, bf16((y / sqrt(D)) * s) -> out

@@ -11,13 +11,14 @@
 // TileLang kernels' values (:521-596).
 //
 // Compress is three launches:
-//   stats:  y of every head-row; K: per-lane running min / max per channel, reduced
+//   kstats: y of every K head-row; per-lane running min / max per channel, reduced
 //           over the workgroup in LDS (order-preserving keys) into a per-workgroup
-//           partial [wg][2][H][D]; V: per-head-row min / max over D (:652-659);
+//           partial [wg][2][H][D];
 //   kfinal: K min / max over the partials, scale = max(max - min, 1e-5) / (L - 1);
-//   quant:  y again, had = bf16(y); K with the channel constants, V with the
-//           per-(row, head) statistics reduced over the heads of its group (equal L,
-//           :1143-1163); q = clamp(roundf((had - min) / scale), 0, L) as uint8.
+//   quant:  y again, had = bf16(y); K with the channel constants; V with the
+//           per-head-row min / max over D (:652-659) reduced over the heads of its
+//           group (equal L, :1143-1163) in LDS -- a pass holds 64 / H whole rows, so
+//           V is read once; q = clamp(roundf((had - min) / scale), 0, L) as uint8.
 // Decompress is one launch: x = fma(q, scale16, min16), fp32 butterflies,
 // bf16((y * (1/sqrt(D))) * s) (:685-716).
 #include "kvmi_common.hpp"
@@ -28,7 +29,8 @@ namespace {
 constexpr int kV3WG = 256;
 constexpr int kV3Rows = kV3WG / 4;  // head-rows per pass
 constexpr int kV3MaxH = 64;
-constexpr int kV3KGrid = 256;       // workgroups of the K statistics pass (partials)
+constexpr int kV3KGrid = 256;       // most workgroups of the K statistics pass (partials)
+constexpr int kV3Ahead = 4;         // K statistics: passes loaded before any is transformed
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
@@ -44,24 +46,29 @@ __device__ __forceinline__ uint32_t v3_lane_signs(const uint32_t* signs, int h, 
   }
 }
 
-// y = FWHT_fp32(x * s) * (1/sqrt(D)) of the lane's E elements.
+// y = FWHT_fp32(x * s) * (1/sqrt(D)) of the lane's E elements (w: their bf16 pairs).
 template <int D>
-__device__ __forceinline__ void v3_transform(const uint16_t* src, uint32_t sb, float scale, int q,
-                                             float (&y)[D / 4]) {
+__device__ __forceinline__ void v3_transform_w(uint32_t (&w)[D / 8], uint32_t sb, float scale, int q,
+                                               float (&y)[D / 4]) {
   constexpr int E = D / 4;
-  uint32_t w[E / 2];
-  load_bf16_seg<E>(src, w);
   apply_sign_bf16<E>(w, sb);
   unpack_bf16<E>(w, y);
   fwht_row<E>(y, q);
 #pragma unroll
   for (int i = 0; i < E; ++i) y[i] *= scale;
 }
+template <int D>
+__device__ __forceinline__ void v3_transform(const uint16_t* src, uint32_t sb, float scale, int q,
+                                             float (&y)[D / 4]) {
+  uint32_t w[D / 8];
+  load_bf16_seg<D / 4>(src, w);
+  v3_transform_w<D>(w, sb, scale, q, y);
+}
 
-// roundf (ties away from zero), clamped to [0, L], as an integer.
+// clamp(roundf((had - mn) / sc), 0, L) as an integer (roundf: ties away from zero;
+// the division is the correctly rounded fp32 one).
 __device__ __forceinline__ uint32_t v3_symbol(float had, float mn, float sc, float lv) {
-  const float r = __builtin_roundf((had - mn) / sc);
-  return (uint32_t)fminf(fmaxf(r, 0.0f), lv);
+  return (uint32_t)fminf(fmaxf(__builtin_roundf((had - mn) / sc), 0.0f), lv);
 }
 
 struct V3Shape {
@@ -70,42 +77,23 @@ struct V3Shape {
   float scale;   // fp32 1/sqrt(D)
 };
 
-// ------------------------------------------------------------------ stats
-// part 0 (K) writes one partial per workgroup: its grid must not exceed kV3KGrid.
+// ------------------------------------------------------------------ K statistics
+// One partial per workgroup: the grid must not exceed kV3KGrid.  With about one
+// workgroup per CU a lane loads kV3Ahead passes before transforming any of them, so
+// that enough bytes are in flight; the LDS holds the layer's 2 * H * D keys (dynamic
+// size).  (Up to 1024 workgroups of 2 passes ahead measured faster on 128 Ki-row layers
+// and slower on 8 Ki-row ones, where the partials cost more than the overlap gains.)
 template <int D>
-__global__ __launch_bounds__(kV3WG) void v3_stats_kernel(V3Shape sh, int part, const uint16_t* __restrict__ x,
-                                                         const uint32_t* __restrict__ signs,
-                                                         uint32_t* __restrict__ kpart, float* __restrict__ vrow) {
+__global__ __launch_bounds__(kV3WG) void v3_kstats_kernel(V3Shape sh, const uint16_t* __restrict__ x,
+                                                          const uint32_t* __restrict__ signs,
+                                                          uint32_t* __restrict__ kpart) {
   constexpr int E = D / 4;
   const int H = sh.H, HD = H * D;
   const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3, h = Q % H;
   const int64_t hrows = sh.rows * H;
-  const uint16_t* src = x + part * hrows * D;
   const uint32_t sb = v3_lane_signs<D>(signs, h, q);
   const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
-  if (part == 1) {  // V: min / max of every head-row over D
-    for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
-      const int64_t hr = p * kV3Rows + Q;
-      if (hr >= hrows) continue;
-      float y[E];
-      v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
-      float mn = y[0], mx = y[0];
-#pragma unroll
-      for (int i = 1; i < E; ++i) {
-        mn = fminf(mn, y[i]);
-        mx = fmaxf(mx, y[i]);
-      }
-      mn = quad_min(mn);
-      mx = quad_max(mx);
-      if (q == 0) {
-        gst(vrow + hr, mn);
-        gst(vrow + hrows + hr, mx);
-      }
-    }
-    return;
-  }
-  // K: running per-channel min / max of the lane's rows
-  __shared__ uint32_t lkey[2 * kV3MaxH * 128];
+  extern __shared__ uint32_t lkey[];  // [2][H * D]
   for (int i = tid; i < HD; i += kV3WG) {
     lkey[i] = 0xffffffffu;
     lkey[HD + i] = 0u;
@@ -117,16 +105,26 @@ __global__ __launch_bounds__(kV3WG) void v3_stats_kernel(V3Shape sh, int part, c
     mx[i] = -__builtin_inff();
   }
   bool any = false;
-  for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
-    const int64_t hr = p * kV3Rows + Q;
-    if (hr >= hrows) continue;
-    any = true;
-    float y[E];
-    v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
+  const int64_t stride = gridDim.x;
+  for (int64_t p0 = blockIdx.x; p0 < passes; p0 += kV3Ahead * stride) {
+    uint32_t w[kV3Ahead][E / 2];
 #pragma unroll
-    for (int i = 0; i < E; ++i) {
-      mn[i] = fminf(mn[i], y[i]);
-      mx[i] = fmaxf(mx[i], y[i]);
+    for (int u = 0; u < kV3Ahead; ++u) {
+      const int64_t hr = (p0 + u * stride) * kV3Rows + Q;
+      if (hr < hrows) load_bf16_seg<E>(x + hr * D + q * E, w[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kV3Ahead; ++u) {
+      const int64_t hr = (p0 + u * stride) * kV3Rows + Q;
+      if (hr >= hrows) continue;  // a quad's lanes share hr: the quad shuffles stay whole
+      any = true;
+      float y[E];
+      v3_transform_w<D>(w[u], sb, sh.scale, q, y);
+#pragma unroll
+      for (int i = 0; i < E; ++i) {
+        mn[i] = fminf(mn[i], y[i]);
+        mx[i] = fmaxf(mx[i], y[i]);
+      }
     }
   }
   __syncthreads();
@@ -142,30 +140,67 @@ __global__ __launch_bounds__(kV3WG) void v3_stats_kernel(V3Shape sh, int part, c
   for (int i = tid; i < 2 * HD; i += kV3WG) gst(out + i, lkey[i]);
 }
 
-// K statistics over the partials -> kmeta [2][H][D] = (min, scale).
+// K statistics over the partials -> kmeta [2][H][D] = (min, scale).  A workgroup
+// takes 4 channels: lane j = tid & 3 of every quad reads channel 4 * blockIdx.x + j
+// of the partials s, s + 64, ... (s = tid >> 2, so every load of a lane is
+// independent), then the 64 slices are reduced across the wave and the 4 waves.
 __global__ __launch_bounds__(kV3WG) void v3_kfinal_kernel(int HD, int D, int nparts, const uint32_t* __restrict__ kpart,
                                                           const float* __restrict__ levels, float* __restrict__ kmeta) {
-  const int i = blockIdx.x * kV3WG + threadIdx.x;
-  if (i >= HD) return;
+  const int j = threadIdx.x & 3, s = threadIdx.x >> 2;
+  const int c = blockIdx.x * 4 + j;
   uint32_t a = 0xffffffffu, b = 0u;
-  for (int w = 0; w < nparts; ++w) {
-    a = min(a, gld(kpart + (int64_t)w * 2 * HD + i));
-    b = max(b, gld(kpart + (int64_t)w * 2 * HD + HD + i));
+  if (c < HD) {
+    for (int w = s; w < nparts; w += kV3WG / 4) {
+      a = min(a, gld(kpart + (int64_t)w * 2 * HD + c));
+      b = max(b, gld(kpart + (int64_t)w * 2 * HD + HD + c));
+    }
+  }
+#pragma unroll
+  for (int m = 4; m < 64; m <<= 1) {  // lanes of equal j within the wave
+    a = min(a, (uint32_t)__shfl_xor((int)a, m));
+    b = max(b, (uint32_t)__shfl_xor((int)b, m));
+  }
+  __shared__ uint32_t la[kV3WG / 64][4], lb[kV3WG / 64][4];
+  const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+  if (ln < 4) {
+    la[wv][ln] = a;
+    lb[wv][ln] = b;
+  }
+  __syncthreads();
+  if (threadIdx.x >= 4 || c >= HD) return;
+#pragma unroll
+  for (int v = 1; v < kV3WG / 64; ++v) {
+    a = min(a, la[v][j]);
+    b = max(b, lb[v][j]);
   }
   const float mn = key2f(a), mx = key2f(b);
-  const float lv = gld(levels + i / D);
-  gst(kmeta + i, mn);
-  gst(kmeta + HD + i, fmaxf(mx - mn, 1e-5f) / (lv - 1.0f));
+  const float lv = gld(levels + c / D);
+  gst(kmeta + c, mn);
+  gst(kmeta + HD + c, fmaxf(mx - mn, 1e-5f) / (lv - 1.0f));
 }
 
 // ------------------------------------------------------------------ quantize
+template <int E>
+__device__ __forceinline__ void v3_store_symbols(uint8_t* p, const uint32_t (&sym)[E]) {
+  uint32_t w[E / 4];
+#pragma unroll
+  for (int i = 0; i < E / 4; ++i)
+    w[i] = sym[4 * i] | (sym[4 * i + 1] << 8) | (sym[4 * i + 2] << 16) | (sym[4 * i + 3] << 24);
+  uint4* o = reinterpret_cast<uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < E / 16; ++i) gst(o + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
+}
+
+// blockIdx.y = part (0 = K, 1 = V).  hrows is a multiple of H and 64 % H == 0, so a
+// pass of 64 consecutive head-rows holds whole rows, each entirely inside or entirely
+// past the layer; lanes past it load and store nothing but still reach the V branch's
+// barriers (the pass count is uniform over the workgroup).
 template <int D>
 __global__ __launch_bounds__(kV3WG) void v3_quant_kernel(V3Shape sh, const uint16_t* __restrict__ x,
                                                          const uint32_t* __restrict__ signs,
                                                          const float* __restrict__ levels,
                                                          const int32_t* __restrict__ vgroup,
-                                                         const float* __restrict__ kmeta,
-                                                         const float* __restrict__ vrow, uint8_t* __restrict__ qout,
+                                                         const float* __restrict__ kmeta, uint8_t* __restrict__ qout,
                                                          float* __restrict__ vmeta) {
   constexpr int E = D / 4;
   const int part = blockIdx.y;
@@ -176,26 +211,54 @@ __global__ __launch_bounds__(kV3WG) void v3_quant_kernel(V3Shape sh, const uint1
   uint8_t* dst = qout + part * hrows * D;
   const uint32_t sb = v3_lane_signs<D>(signs, h, q);
   const float lv = gld(levels + part * H + h);
-  const int grp = gld(vgroup + h);
   const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
+  // heads of this head's V group (equal L), as a bit set over the row's heads
+  uint64_t same = 0;
+  if (part == 1) {
+    const int grp = gld(vgroup + h);
+    for (int k = 0; k < H; ++k)
+      if (gld(vgroup + k) == grp) same |= (uint64_t)1 << k;
+  }
+  __shared__ float lmn[kV3Rows], lmx[kV3Rows];
+  const int row0 = Q - h;  // this pass's LDS slot of head 0 of the lane's row
   for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
     const int64_t hr = p * kV3Rows + Q;
-    if (hr >= hrows) continue;
+    const bool live = hr < hrows;
     float y[E];
-    v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
+    if (live) {
+      v3_transform<D>(src + hr * D + q * E, sb, sh.scale, q, y);
+    } else {
+#pragma unroll
+      for (int i = 0; i < E; ++i) y[i] = 0.0f;
+    }
     uint32_t sym[E];
     if (part == 0) {
+      if (!live) continue;
       const float* kmn = kmeta + h * D + q * E;
 #pragma unroll
       for (int i = 0; i < E; ++i) sym[i] = v3_symbol(round_bf16(y[i]), gld(kmn + i), gld(kmn + HD + i), lv);
     } else {
+      float mn = y[0], mx = y[0];
+#pragma unroll
+      for (int i = 1; i < E; ++i) {
+        mn = fminf(mn, y[i]);
+        mx = fmaxf(mx, y[i]);
+      }
+      mn = quad_min(mn);
+      mx = quad_max(mx);
+      __syncthreads();  // the previous pass's readers are done
+      if (q == 0) {
+        lmn[Q] = mn;
+        lmx[Q] = mx;
+      }
+      __syncthreads();
+      if (!live) continue;  // no barrier follows in this pass
       // the row's statistics over the heads of this head's group
-      const int64_t r = hr / H;
       float gmn = __builtin_inff(), gmx = -__builtin_inff();
-      for (int k = 0; k < H; ++k) {
-        if (gld(vgroup + k) != grp) continue;
-        gmn = fminf(gmn, gld(vrow + r * H + k));
-        gmx = fmaxf(gmx, gld(vrow + hrows + r * H + k));
+      for (uint64_t m = same; m; m &= m - 1) {
+        const int k = __builtin_ctzll(m);
+        gmn = fminf(gmn, lmn[row0 + k]);
+        gmx = fmaxf(gmx, lmx[row0 + k]);
       }
       const float sc = fmaxf(gmx - gmn, 1e-5f) / (lv - 1.0f);
       if (q == 0) {
@@ -205,17 +268,40 @@ __global__ __launch_bounds__(kV3WG) void v3_quant_kernel(V3Shape sh, const uint1
 #pragma unroll
       for (int i = 0; i < E; ++i) sym[i] = v3_symbol(round_bf16(y[i]), gmn, sc, lv);
     }
-    uint32_t w[E / 4];
-#pragma unroll
-    for (int i = 0; i < E / 4; ++i)
-      w[i] = sym[4 * i] | (sym[4 * i + 1] << 8) | (sym[4 * i + 2] << 16) | (sym[4 * i + 3] << 24);
-    uint4* o = reinterpret_cast<uint4*>(dst + hr * D + q * E);
-#pragma unroll
-    for (int i = 0; i < E / 16; ++i) gst(o + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
+    v3_store_symbols<E>(dst + hr * D + q * E, sym);
   }
 }
 
 // ------------------------------------------------------------------ dequantize
+template <int E>
+__device__ __forceinline__ void v3_load_symbols(const uint8_t* p, uint32_t (&w)[E / 4]) {
+  const uint4* s4 = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < E / 16; ++i) {
+    const uint4 t = gld(s4 + i);
+    w[4 * i] = t.x;
+    w[4 * i + 1] = t.y;
+    w[4 * i + 2] = t.z;
+    w[4 * i + 3] = t.w;
+  }
+}
+
+// fp32 butterflies of the lane's reconstructed values, bf16((y * (1/sqrt(D))) * s):
+// the sign is exact after rounding.
+template <int D>
+__device__ __forceinline__ void v3_inverse_store(float (&v)[D / 4], uint32_t sb, float scale, int q, uint16_t* p) {
+  constexpr int E = D / 4;
+  fwht_row<E>(v, q);
+  uint32_t o[E / 2];
+#pragma unroll
+  for (int i = 0; i < E / 2; ++i) o[i] = pack_bf16x2(v[2 * i] * scale, v[2 * i + 1] * scale);
+  apply_sign_bf16<E>(o, sb);
+  store_bf16_seg<E>(p, o);
+}
+
+// K passes are head-major: a pass is 64 rows of one head, so the quads of a wave read
+// the same channel constants (one broadcast line per lane position, not one copy per
+// quad).  V passes are 64 consecutive head-rows.
 template <int D>
 __global__ __launch_bounds__(kV3WG) void v3_dequant_kernel(V3Shape sh, const uint8_t* __restrict__ qin,
                                                            const uint32_t* __restrict__ signs,
@@ -225,44 +311,50 @@ __global__ __launch_bounds__(kV3WG) void v3_dequant_kernel(V3Shape sh, const uin
   constexpr int E = D / 4;
   const int part = blockIdx.y;
   const int H = sh.H, HD = H * D;
-  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3, h = Q % H;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3;
   const int64_t hrows = sh.rows * H;
   const uint8_t* src = qin + part * hrows * D;
   uint16_t* dst = out + part * hrows * D;
-  const uint32_t sb = v3_lane_signs<D>(signs, h, q);
+  if (part == 0) {
+    const int64_t kpasses = (sh.rows + kV3Rows - 1) / kV3Rows * H;
+    for (int64_t p = blockIdx.x; p < kpasses; p += gridDim.x) {
+      const int hk = (int)(p % H);
+      const int64_t r = (p / H) * kV3Rows + Q;
+      if (r >= sh.rows) continue;
+      const int64_t hr = r * H + hk;
+      uint32_t w[E / 4];
+      v3_load_symbols<E>(src + hr * D + q * E, w);
+      const uint4* mn = reinterpret_cast<const uint4*>(kmeta16 + hk * D + q * E);  // 16-byte aligned
+      const uint4* sc = reinterpret_cast<const uint4*>(kmeta16 + HD + hk * D + q * E);
+      float v[E];
+#pragma unroll
+      for (int i8 = 0; i8 < E / 8; ++i8) {
+        const uint4 m4 = gld(mn + i8), c4 = gld(sc + i8);
+        const uint32_t mw[4] = {m4.x, m4.y, m4.z, m4.w}, cw[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int i = 8 * i8 + k;
+          const float sym = (float)((w[i / 4] >> (8 * (i % 4))) & 0xffu);
+          v[i] = __builtin_fmaf(sym, f16_to_f32((uint16_t)(cw[k / 2] >> (16 * (k & 1)))),
+                                f16_to_f32((uint16_t)(mw[k / 2] >> (16 * (k & 1)))));
+        }
+      }
+      v3_inverse_store<D>(v, v3_lane_signs<D>(signs, hk, q), sh.scale, q, dst + hr * D + q * E);
+    }
+    return;
+  }
+  const uint32_t sb = v3_lane_signs<D>(signs, Q % H, q);
   const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
   for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
     const int64_t hr = p * kV3Rows + Q;
     if (hr >= hrows) continue;
     uint32_t w[E / 4];
-    const uint4* s4 = reinterpret_cast<const uint4*>(src + hr * D + q * E);
-#pragma unroll
-    for (int i = 0; i < E / 16; ++i) {
-      const uint4 t = gld(s4 + i);
-      w[4 * i] = t.x;
-      w[4 * i + 1] = t.y;
-      w[4 * i + 2] = t.z;
-      w[4 * i + 3] = t.w;
-    }
+    v3_load_symbols<E>(src + hr * D + q * E, w);
+    const float mn = f16_to_f32(gld(vmeta16 + hr)), sc = f16_to_f32(gld(vmeta16 + hrows + hr));
     float v[E];
-    if (part == 0) {
-      const uint16_t* mn = kmeta16 + h * D + q * E;
 #pragma unroll
-      for (int i = 0; i < E; ++i) {
-        const float sym = (float)((w[i / 4] >> (8 * (i % 4))) & 0xffu);
-        v[i] = __builtin_fmaf(sym, f16_to_f32(gld(mn + HD + i)), f16_to_f32(gld(mn + i)));
-      }
-    } else {
-      const float mn = f16_to_f32(gld(vmeta16 + hr)), sc = f16_to_f32(gld(vmeta16 + hrows + hr));
-#pragma unroll
-      for (int i = 0; i < E; ++i) v[i] = __builtin_fmaf((float)((w[i / 4] >> (8 * (i % 4))) & 0xffu), sc, mn);
-    }
-    fwht_row<E>(v, q);
-    uint32_t o[E / 2];
-#pragma unroll
-    for (int i = 0; i < E / 2; ++i) o[i] = pack_bf16x2(v[2 * i] * sh.scale, v[2 * i + 1] * sh.scale);
-    apply_sign_bf16<E>(o, sb);  // (y * (1/sqrt(D))) * s: the sign is exact after rounding
-    store_bf16_seg<E>(dst + hr * D + q * E, o);
+    for (int i = 0; i < E; ++i) v[i] = __builtin_fmaf((float)((w[i / 4] >> (8 * (i % 4))) & 0xffu), sc, mn);
+    v3_inverse_store<D>(v, sb, sh.scale, q, dst + hr * D + q * E);
   }
 }
 
@@ -272,8 +364,6 @@ int v3_check(int64_t rows, int32_t H, int32_t D) {
   if (rows * H > (int64_t)1 << 31) return KVMI_EINVAL;
   return KVMI_OK;
 }
-
-int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
 unsigned v3_grid(int64_t rows, int H) {
   const int64_t passes = (rows * H + kV3Rows - 1) / kV3Rows;
@@ -286,7 +376,7 @@ unsigned v3_grid(int64_t rows, int H) {
 extern "C" int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim) {
   using namespace kvmi;
   if (v3_check(rows, num_heads, head_dim)) return -1;
-  return align256((int64_t)kV3KGrid * 2 * num_heads * head_dim * 4) + align256(2 * rows * num_heads * 4);
+  return (int64_t)kV3KGrid * 2 * num_heads * head_dim * 4;
 }
 
 extern "C" int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,
@@ -297,31 +387,27 @@ extern "C" int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, 
   if (rc) return rc;
   if (rows == 0) return KVMI_OK;
   if (!x || !signs || !levels || !vgroup || !q || !kmeta || !vmeta || !scratch) return KVMI_EINVAL;
-  if (((uintptr_t)x | (uintptr_t)q) & 15) return KVMI_EINVAL;  // 16-byte row segments
+  if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)kmeta) & 15) return KVMI_EINVAL;  // 16-byte vectors
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int H = num_heads, D = head_dim;
   V3Shape sh{rows, H, (float)(1.0 / __builtin_sqrt((double)D))};
   uint32_t* kpart = static_cast<uint32_t*>(scratch);
-  float* vrow = reinterpret_cast<float*>(static_cast<uint8_t*>(scratch) +
-                                         align256((int64_t)kV3KGrid * 2 * H * D * 4));
   const unsigned g = v3_grid(rows, H);
   const unsigned gk = g < (unsigned)kV3KGrid ? g : (unsigned)kV3KGrid;  // K partials: at most kV3KGrid
+  const size_t klds = (size_t)2 * H * D * 4;
   const uint16_t* xs = static_cast<const uint16_t*>(x);
-  const unsigned gf = (unsigned)((H * D + kV3WG - 1) / kV3WG);
-  if (D == 64) {
-    hipLaunchKernelGGL((v3_stats_kernel<64>), dim3(gk), dim3(kV3WG), 0, st, sh, 0, xs, signs, kpart, vrow);
-    hipLaunchKernelGGL((v3_stats_kernel<64>), dim3(g), dim3(kV3WG), 0, st, sh, 1, xs, signs, kpart, vrow);
-  } else {
-    hipLaunchKernelGGL((v3_stats_kernel<128>), dim3(gk), dim3(kV3WG), 0, st, sh, 0, xs, signs, kpart, vrow);
-    hipLaunchKernelGGL((v3_stats_kernel<128>), dim3(g), dim3(kV3WG), 0, st, sh, 1, xs, signs, kpart, vrow);
-  }
+  const unsigned gf = (unsigned)((H * D + 3) / 4);  // 4 channels per workgroup
+  if (D == 64)
+    hipLaunchKernelGGL((v3_kstats_kernel<64>), dim3(gk), dim3(kV3WG), klds, st, sh, xs, signs, kpart);
+  else
+    hipLaunchKernelGGL((v3_kstats_kernel<128>), dim3(gk), dim3(kV3WG), klds, st, sh, xs, signs, kpart);
   hipLaunchKernelGGL(v3_kfinal_kernel, dim3(gf), dim3(kV3WG), 0, st, H * D, D, (int)gk, kpart, levels, kmeta);
   if (D == 64)
     hipLaunchKernelGGL((v3_quant_kernel<64>), dim3(g, 2), dim3(kV3WG), 0, st, sh, xs, signs, levels, vgroup, kmeta,
-                       vrow, q, vmeta);
+                       q, vmeta);
   else
     hipLaunchKernelGGL((v3_quant_kernel<128>), dim3(g, 2), dim3(kV3WG), 0, st, sh, xs, signs, levels, vgroup, kmeta,
-                       vrow, q, vmeta);
+                       q, vmeta);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
@@ -333,7 +419,7 @@ extern "C" int kvmi_v3_decompress(const uint8_t* q, int64_t rows, int32_t num_he
   if (rc) return rc;
   if (rows == 0) return KVMI_OK;
   if (!q || !signs || !kmeta16 || !vmeta16 || !out) return KVMI_EINVAL;
-  if (((uintptr_t)q | (uintptr_t)out) & 15) return KVMI_EINVAL;  // 16-byte row segments
+  if (((uintptr_t)q | (uintptr_t)out | (uintptr_t)kmeta16) & 15) return KVMI_EINVAL;  // 16-byte vectors
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   V3Shape sh{rows, num_heads, (float)(1.0 / __builtin_sqrt((double)head_dim))};
   const unsigned g = v3_grid(rows, num_heads);

@@ -246,19 +246,22 @@ def test_quantizer_validation_matches_reference_asserts():
 
 
 def test_v3_sizes_and_contract_errors():
-    """The fused quantizer's scratch: 256 K partials [2][H][D] uint32 + V row stats
-    [2][rows][H] fp32, each 256-byte aligned; unsupported shapes and misaligned
-    buffers are rejected on the host."""
+    """The fused quantizer's scratch: up to 256 K partials [2][H][D] uint32,
+    whatever the row count; unsupported shapes and misaligned buffers are rejected on the host
+    (no kernel runs: every pointer below is a small integer)."""
     from kvserve_amd import _lib
 
     lib = _lib.load()
     E = _lib.EINVAL
-    assert lib.kvmi_v3_scratch_bytes(100, 8, 128) == 256 * 2 * 8 * 128 * 4 + 6400
-    assert lib.kvmi_v3_scratch_bytes(3, 4, 64) == 256 * 2 * 4 * 64 * 4 + 256
+    assert lib.kvmi_v3_scratch_bytes(100, 8, 128) == 256 * 2 * 8 * 128 * 4
+    assert lib.kvmi_v3_scratch_bytes(3, 4, 64) == 256 * 2 * 4 * 64 * 4
     for bad in ((5, 8, 96), (5, 3, 128), (5, 128, 128), (-1, 8, 128)):
         assert lib.kvmi_v3_scratch_bytes(*bad) == -1
     assert lib.kvmi_v3_compress(None, 4, 8, 96, None, None, None, None, None, None, None, None) == E
     assert lib.kvmi_v3_compress(None, 0, 8, 128, None, None, None, None, None, None, None, None) == 0
     assert lib.kvmi_v3_compress(None, 4, 8, 128, None, None, None, None, None, None, None, None) == E
-    assert lib.kvmi_v3_compress(8, 4, 8, 128, 16, 16, 16, 24, 16, 16, 16, None) == E  # q misaligned
+    assert lib.kvmi_v3_compress(8, 4, 8, 128, 16, 16, 16, 16, 16, 16, 16, None) == E  # x misaligned
+    assert lib.kvmi_v3_compress(16, 4, 8, 128, 16, 16, 16, 24, 16, 16, 16, None) == E  # q misaligned
+    assert lib.kvmi_v3_compress(16, 4, 8, 128, 16, 16, 16, 16, 8, 16, 16, None) == E  # kmeta misaligned
     assert lib.kvmi_v3_decompress(16, 4, 8, 128, 16, 16, 16, 8, None) == E  # out misaligned
+    assert lib.kvmi_v3_decompress(16, 4, 8, 128, 16, 8, 16, 16, None) == E  # kmeta16 misaligned
