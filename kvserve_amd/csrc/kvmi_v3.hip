@@ -180,6 +180,8 @@ __global__ __launch_bounds__(kV3WG) void v3_kfinal_kernel(int HD, int D, int npa
 }
 
 // ------------------------------------------------------------------ quantize
+// Symbols leave through streaming stores: 3-4 % faster compress than cached stores
+// (the same stores for dequant's bf16 output were 1.6x slower, so that one stays cached).
 template <int E>
 __device__ __forceinline__ void v3_store_symbols(uint8_t* p, const uint32_t (&sym)[E]) {
   uint32_t w[E / 4];
@@ -188,7 +190,7 @@ __device__ __forceinline__ void v3_store_symbols(uint8_t* p, const uint32_t (&sy
     w[i] = sym[4 * i] | (sym[4 * i + 1] << 8) | (sym[4 * i + 2] << 16) | (sym[4 * i + 3] << 24);
   uint4* o = reinterpret_cast<uint4*>(p);
 #pragma unroll
-  for (int i = 0; i < E / 16; ++i) gst(o + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
+  for (int i = 0; i < E / 16; ++i) gst_stream(o + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
 }
 
 // blockIdx.y = part (0 = K, 1 = V).  hrows is a multiple of H and 64 % H == 0, so a
@@ -365,9 +367,11 @@ int v3_check(int64_t rows, int32_t H, int32_t D) {
   return KVMI_OK;
 }
 
+// One pass per workgroup (rows * H <= 2^31, so at most 2^25 workgroups): capping the
+// grid at 4096 and looping measured 12-14 % slower for dequant at 128-512 Ki rows.
 unsigned v3_grid(int64_t rows, int H) {
   const int64_t passes = (rows * H + kV3Rows - 1) / kV3Rows;
-  return (unsigned)(passes < 4096 ? (passes > 0 ? passes : 1) : 4096);
+  return (unsigned)(passes > 0 ? passes : 1);
 }
 
 }  // namespace
