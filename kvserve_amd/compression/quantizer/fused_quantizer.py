@@ -171,7 +171,8 @@ class FusedHadamardQuantizer(Quantizer):
         if scratch_n < 0:
             raise ValueError(f"unsupported geometry for the fused quantizer: heads={H}, head_dim={D}")
         levels, group, signs = self._device_tables(layer_id, H, D, dev)
-        kmeta = torch.empty((2, H, D), dtype=torch.float32, device=dev)
+        # no rows: no statistics are computed, and the K metadata is defined as zeros
+        kmeta = (torch.zeros if rows == 0 else torch.empty)((2, H, D), dtype=torch.float32, device=dev)
         vmeta = torch.empty((2, rows, H), dtype=torch.float32, device=dev)
         scratch = torch.empty(max(scratch_n, 1), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):

@@ -41,6 +41,8 @@ CASES = [
     (1, 5, 16, 128, None, 1),
     (256, 16, 8, 128, "Llama-3.1-8B-Instruct", 17),   # 4096 rows: many passes per workgroup
     (9, 16, 2, 64, "Llama-3.1-8B-Instruct", 3),
+    (3, 16, 64, 128, None, 0),   # most heads: 64 KiB of LDS keys in the K statistics
+    (5, 3, 32, 64, None, 4),     # ragged block size, last pass partly past the layer
 ]
 
 
@@ -133,3 +135,19 @@ def test_adapter_tilelang_fused_roundtrip_through_wire(cuda):
         for part in range(2):
             rel = np.abs(got[part] - want[part]).max() / np.abs(want[part]).max()
             assert rel <= 1e-2, (l, part, rel)
+
+
+def test_fused_quantizer_empty_layer(cuda):
+    """A layer with no blocks quantizes to empty symbols and metadata and back."""
+    from kvserve_amd.compression.quantizer import FusedHadamardQuantizer
+
+    q = FusedHadamardQuantizer(base_seed=0xC0FEBABE)
+    x = torch.empty((2, 0, 16, 8, 128), dtype=torch.bfloat16, device=cuda)
+    sym, meta = q.quantize(0, x)
+    assert sym.shape == x.shape and sym.dtype == torch.uint8
+    assert tuple(meta["key_meta"]["min_val"].shape) == (8, 128)
+    assert not meta["key_meta"]["min_val"].any() and not meta["key_meta"]["quant_scale"].any()
+    assert tuple(meta["value_meta"]["min_val"].shape) == (0, 8)
+    out = q.dequantize(0, sym, meta)
+    torch.cuda.synchronize()
+    assert out.shape == x.shape and out.dtype == torch.bfloat16
