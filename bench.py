@@ -545,6 +545,11 @@ def bench_fused_v3(args) -> dict:
     Q = q.numel()
     M32, M16 = (kmeta.numel() + vmeta.numel()) * 4, (km16.numel() + vm16.numel()) * 2
     alg_c, alg_d = R + Q + M32, Q + M16 + R  # read KV, write symbols + meta (or the reverse)
+    # profiled HBM bytes per dispatch (committed rocprofv3 --pmc summary), per layer
+    dk = f"v3_dequant_kernel<{D}>"
+    ct = [profiled_traffic(k, "config2_v3") for k in (f"v3_kstats_kernel<{D}>", "v3_kfinal_kernel",
+                                                     f"v3_quant_kernel<{D}>")]
+    dt = profiled_traffic(dk, "config2_v3")
     res = {
         "metric": "compress/decompress GB/s of raw bf16 KV on 1 MI355X, impl tilelang_fused",
         "value": round(R / ((t_c + t_d) / 1e3) / 1e9, 2),
@@ -566,9 +571,13 @@ def bench_fused_v3(args) -> dict:
         "decompress_gbps": round(R / t_d / 1e6, 2),
         "compress_hbm_frac": round(alg_c / t_c / 1e6 / HBM_PEAK_GBPS, 4),
         "decompress_hbm_frac": round(alg_d / t_d / 1e6 / HBM_PEAK_GBPS, 4),
-        "roofline": {"bound": "hbm", "kernel": "v3_dequant_kernel<128> (one launch per layer)",
+        "compress_traffic_hbm_frac": (round(L * sum(ct) / (t_c / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)
+                                      if None not in ct else None),
+        "decompress_traffic_hbm_frac": (round(L * dt / (t_d / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)
+                                        if dt is not None else None),
+        "roofline": {"bound": "hbm", "kernel": f"{dk} (one launch per layer)",
                      "achieved": round(alg_d / L / (t_d / L / 1e3) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(alg_d / t_d / 1e6 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(alg_d / t_d / 1e6 / HBM_PEAK_GBPS, 4), "traffic": dt,
                      "algorithmic_bytes_per_launch": alg_d // L},
         "cpu_baseline": None,
     }
