@@ -93,7 +93,9 @@ __global__ __launch_bounds__(kV3WG) void v3_kstats_kernel(V3Shape sh, const uint
   const int64_t hrows = sh.rows * H;
   const uint32_t sb = v3_lane_signs<D>(signs, h, q);
   const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
-  extern __shared__ uint32_t lkey[];  // [2][H * D]
+  // [2][H * D] keys; channel c = seg * E + k sits at seg * E + (k + seg) % E, so that the
+  // lanes of one atomic instruction (same k, different segments) use different banks.
+  extern __shared__ uint32_t lkey[];
   for (int i = tid; i < HD; i += kV3WG) {
     lkey[i] = 0xffffffffu;
     lkey[HD + i] = 0u;
@@ -131,13 +133,18 @@ __global__ __launch_bounds__(kV3WG) void v3_kstats_kernel(V3Shape sh, const uint
   if (any) {
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      atomicMin(&lkey[h * D + q * E + i], f2key(mn[i]));
-      atomicMax(&lkey[HD + h * D + q * E + i], f2key(mx[i]));
+      const int seg = h * 4 + q, slot = seg * E + ((i + seg) & (E - 1));
+      atomicMin(&lkey[slot], f2key(mn[i]));
+      atomicMax(&lkey[HD + slot], f2key(mx[i]));
     }
   }
   __syncthreads();
   uint32_t* out = kpart + (int64_t)blockIdx.x * 2 * HD;
-  for (int i = tid; i < 2 * HD; i += kV3WG) gst(out + i, lkey[i]);
+  for (int i = tid; i < HD; i += kV3WG) {
+    const int seg = i / E, slot = seg * E + ((i + seg) & (E - 1));
+    gst(out + i, lkey[slot]);
+    gst(out + HD + i, lkey[HD + slot]);
+  }
 }
 
 // K statistics over the partials -> kmeta [2][H][D] = (min, scale).  A workgroup
