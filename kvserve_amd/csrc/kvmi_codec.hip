@@ -106,18 +106,22 @@ __global__ __launch_bounds__(kWG) void kstats_kernel(Geo g, const kvmi_layer_job
     }
   }
   __syncthreads();
+  // channel c = seg * E + k (seg = h * 4 + q) sits at seg * E + (k + seg) % E, so that
+  // the lanes of one atomic instruction (same k, different segments) use different banks
   if (Q < (int)((rows < kRows) ? rows : kRows)) {
+    const int seg = h * 4 + q;
 #pragma unroll
     for (int i = 0; i < E; ++i) {
-      const int c = h * D + q * E + i;
-      atomicMin(&lkey[c], f2key(mn[i]));
-      atomicMax(&lkey[HD + c], f2key(mx[i]));
+      const int slot = seg * E + ((i + seg) & (E - 1));
+      atomicMin(&lkey[slot], f2key(mn[i]));
+      atomicMax(&lkey[HD + slot], f2key(mx[i]));
     }
   }
   __syncthreads();
   for (int i = tid; i < HD; i += kWG) {
-    atomicMin(&job.kstats[i], lkey[i]);
-    atomicMax(&job.kstats[HD + i], lkey[HD + i]);
+    const int seg = i / E, slot = seg * E + ((i + seg) & (E - 1));
+    atomicMin(&job.kstats[i], lkey[slot]);
+    atomicMax(&job.kstats[HD + i], lkey[HD + slot]);
   }
 }
 
