@@ -154,7 +154,12 @@ __global__ __launch_bounds__(kV3WG) void v3_kstats_kernel(V3Shape sh, const uint
 __global__ __launch_bounds__(kV3WG) void v3_kfinal_kernel(int HD, int D, int nparts, const uint32_t* __restrict__ kpart,
                                                           const float* __restrict__ levels, float* __restrict__ kmeta) {
   const int j = threadIdx.x & 3, s = threadIdx.x >> 2;
-  const int c = blockIdx.x * 4 + j;
+  // The 8 workgroups whose channels share a 128-byte line of the partials take ids
+  // equal mod 8, i.e. the same XCD under round-robin dispatch, so that one L2 fetch
+  // serves them all (when the grid is a multiple of 64; else the plain order).
+  const int wg = blockIdx.x;
+  const int grp = (gridDim.x % 64 == 0) ? 8 * ((wg % 8) + 8 * (wg / 64)) + (wg / 8) % 8 : wg;
+  const int c = grp * 4 + j;
   uint32_t a = 0xffffffffu, b = 0u;
   if (c < HD) {
     for (int w = s; w < nparts; w += kV3WG / 4) {
