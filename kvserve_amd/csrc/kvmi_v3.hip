@@ -300,75 +300,120 @@ __device__ __forceinline__ void v3_load_symbols(const uint8_t* p, uint32_t (&w)[
   }
 }
 
-// fp32 butterflies of the lane's reconstructed values, bf16((y * (1/sqrt(D))) * s):
-// the sign is exact after rounding.
+// fp32 butterflies of the lane's reconstructed values, bf16((y * (1/sqrt(D))) * s) as
+// E/2 words: the sign is exact after rounding.
 template <int D>
-__device__ __forceinline__ void v3_inverse_store(float (&v)[D / 4], uint32_t sb, float scale, int q, uint16_t* p) {
+__device__ __forceinline__ void v3_inverse_words(float (&v)[D / 4], uint32_t sb, float scale, int q,
+                                                 uint32_t (&o)[D / 8]) {
   constexpr int E = D / 4;
   fwht_row<E>(v, q);
-  uint32_t o[E / 2];
 #pragma unroll
   for (int i = 0; i < E / 2; ++i) o[i] = pack_bf16x2(v[2 * i] * scale, v[2 * i + 1] * scale);
   apply_sign_bf16<E>(o, sb);
-  store_bf16_seg<E>(p, o);
+}
+
+// The output leaves through a per-wave LDS stage: lane l puts its W = E/2 words at row
+// l (rows padded to W + 4 words against bank conflicts), then the wave stores 16-byte
+// chunk f = c * 64 + lane, i.e. chunk f % (W/4) of lane f / (W/4)'s segment, so that
+// consecutive lanes store consecutive bytes of each head-row (a lane's own segment at
+// a 2E-byte lane stride writes at a far lower rate).
+template <int W>
+__device__ __forceinline__ void v3_stage_put(uint32_t* ws, int lane, const uint32_t (&o)[W]) {
+  uint4* row = reinterpret_cast<uint4*>(ws + lane * (W + 4));
+#pragma unroll
+  for (int i = 0; i < W / 4; ++i) row[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
 }
 
 // K passes are head-major: a pass is 64 rows of one head, so the quads of a wave read
 // the same channel constants (one broadcast line per lane position, not one copy per
-// quad).  V passes are 64 consecutive head-rows.
+// quad).  V passes are 64 consecutive head-rows.  Every lane takes part in the staged
+// store (a chunk is written only if its head-row exists), so no lane leaves a pass
+// early.
 template <int D>
 __global__ __launch_bounds__(kV3WG) void v3_dequant_kernel(V3Shape sh, const uint8_t* __restrict__ qin,
                                                            const uint32_t* __restrict__ signs,
                                                            const uint16_t* __restrict__ kmeta16,
                                                            const uint16_t* __restrict__ vmeta16,
                                                            uint16_t* __restrict__ out) {
-  constexpr int E = D / 4;
+  constexpr int E = D / 4, W = E / 2, CH = W / 4;  // words and 16-byte chunks of a segment
   const int part = blockIdx.y;
   const int H = sh.H, HD = H * D;
-  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3;
+  const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3, lane = tid & 63, qw = (tid >> 6) * 16;
   const int64_t hrows = sh.rows * H;
   const uint8_t* src = qin + part * hrows * D;
   uint16_t* dst = out + part * hrows * D;
+  __shared__ __align__(16) uint32_t stage[kV3WG / 64][64 * (W + 4)];
+  uint32_t* ws = stage[tid >> 6];
   if (part == 0) {
     const int64_t kpasses = (sh.rows + kV3Rows - 1) / kV3Rows * H;
     for (int64_t p = blockIdx.x; p < kpasses; p += gridDim.x) {
       const int hk = (int)(p % H);
-      const int64_t r = (p / H) * kV3Rows + Q;
-      if (r >= sh.rows) continue;
-      const int64_t hr = r * H + hk;
-      uint32_t w[E / 4];
-      v3_load_symbols<E>(src + hr * D + q * E, w);
-      const uint4* mn = reinterpret_cast<const uint4*>(kmeta16 + hk * D + q * E);  // 16-byte aligned
-      const uint4* sc = reinterpret_cast<const uint4*>(kmeta16 + HD + hk * D + q * E);
-      float v[E];
+      const int64_t r0 = (p / H) * kV3Rows;  // row of quad 0 of the pass
+      const int64_t r = r0 + Q;
+      if (r < sh.rows) {
+        const int64_t hr = r * H + hk;
+        uint32_t w[E / 4];
+        v3_load_symbols<E>(src + hr * D + q * E, w);
+        const uint4* mn = reinterpret_cast<const uint4*>(kmeta16 + hk * D + q * E);  // 16-byte aligned
+        const uint4* sc = reinterpret_cast<const uint4*>(kmeta16 + HD + hk * D + q * E);
+        float v[E];
 #pragma unroll
-      for (int i8 = 0; i8 < E / 8; ++i8) {
-        const uint4 m4 = gld(mn + i8), c4 = gld(sc + i8);
-        const uint32_t mw[4] = {m4.x, m4.y, m4.z, m4.w}, cw[4] = {c4.x, c4.y, c4.z, c4.w};
+        for (int i8 = 0; i8 < E / 8; ++i8) {
+          const uint4 m4 = gld(mn + i8), c4 = gld(sc + i8);
+          const uint32_t mw[4] = {m4.x, m4.y, m4.z, m4.w}, cw[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int i = 8 * i8 + k;
-          const float sym = (float)((w[i / 4] >> (8 * (i % 4))) & 0xffu);
-          v[i] = __builtin_fmaf(sym, f16_to_f32((uint16_t)(cw[k / 2] >> (16 * (k & 1)))),
-                                f16_to_f32((uint16_t)(mw[k / 2] >> (16 * (k & 1)))));
+          for (int k = 0; k < 8; ++k) {
+            const int i = 8 * i8 + k;
+            const float sym = (float)((w[i / 4] >> (8 * (i % 4))) & 0xffu);
+            v[i] = __builtin_fmaf(sym, f16_to_f32((uint16_t)(cw[k / 2] >> (16 * (k & 1)))),
+                                  f16_to_f32((uint16_t)(mw[k / 2] >> (16 * (k & 1)))));
+          }
+        }
+        uint32_t o[W];
+        v3_inverse_words<D>(v, v3_lane_signs<D>(signs, hk, q), sh.scale, q, o);
+        v3_stage_put<W>(ws, lane, o);
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int f = c * 64 + lane, sl = f / CH, k = f % CH;  // source lane, its chunk
+        const int64_t rs = r0 + qw + (sl >> 2);
+        if (rs < sh.rows) {
+          const uint4 t = *reinterpret_cast<const uint4*>(ws + sl * (W + 4) + 4 * k);
+          gst(reinterpret_cast<uint4*>(dst + (rs * H + hk) * D + (sl & 3) * E + 8 * k), t);
         }
       }
-      v3_inverse_store<D>(v, v3_lane_signs<D>(signs, hk, q), sh.scale, q, dst + hr * D + q * E);
+      __builtin_amdgcn_wave_barrier();
     }
     return;
   }
   const uint32_t sb = v3_lane_signs<D>(signs, Q % H, q);
   const int64_t passes = (hrows + kV3Rows - 1) / kV3Rows;
   for (int64_t p = blockIdx.x; p < passes; p += gridDim.x) {
-    const int64_t hr = p * kV3Rows + Q;
-    if (hr >= hrows) continue;
-    uint32_t w[E / 4];
-    v3_load_symbols<E>(src + hr * D + q * E, w);
-    const float mn = f16_to_f32(gld(vmeta16 + hr)), sc = f16_to_f32(gld(vmeta16 + hrows + hr));
-    float v[E];
+    const int64_t h0 = p * kV3Rows;  // head-row of quad 0 of the pass
+    const int64_t hr = h0 + Q;
+    if (hr < hrows) {
+      uint32_t w[E / 4];
+      v3_load_symbols<E>(src + hr * D + q * E, w);
+      const float mn = f16_to_f32(gld(vmeta16 + hr)), sc = f16_to_f32(gld(vmeta16 + hrows + hr));
+      float v[E];
 #pragma unroll
-    for (int i = 0; i < E; ++i) v[i] = __builtin_fmaf((float)((w[i / 4] >> (8 * (i % 4))) & 0xffu), sc, mn);
-    v3_inverse_store<D>(v, sb, sh.scale, q, dst + hr * D + q * E);
+      for (int i = 0; i < E; ++i) v[i] = __builtin_fmaf((float)((w[i / 4] >> (8 * (i % 4))) & 0xffu), sc, mn);
+      uint32_t o[W];
+      v3_inverse_words<D>(v, sb, sh.scale, q, o);
+      v3_stage_put<W>(ws, lane, o);
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int f = c * 64 + lane, sl = f / CH, k = f % CH;
+      const int64_t hs = h0 + qw + (sl >> 2);
+      if (hs < hrows) {
+        const uint4 t = *reinterpret_cast<const uint4*>(ws + sl * (W + 4) + 4 * k);
+        gst(reinterpret_cast<uint4*>(dst + hs * D + (sl & 3) * E + 8 * k), t);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
