@@ -61,6 +61,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_OK 0
 #define KVMI_EINVAL (-22)
 #define KVMI_ELAUNCH (-5)
+#define KVMI_ENOSPC (-28) /* the call needs more than a fixed scratch array holds */
 
 /* Stream format constants (bitpack_codec.py:20-21). */
 #define KVMI_HEADER_BYTES 16
@@ -215,6 +216,22 @@ int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t hea
 /* Scratch bytes of kvmi_v3_compress: up to 256 per-workgroup K partials of 2*H*D*4
  * bytes, not depending on rows (-1 for an unsupported shape). */
 int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim);
+/*
+ * kvmi_v3_compress without the `scratch` argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops and harnesses that
+ * forbid allocation).  No counterpart in the reference.  It allocates nothing: the K
+ * partials live in a fixed device array of KVMI_V3_NOALLOC_SCRATCH_BYTES per GPU,
+ * held from the library's first use on that GPU until the process ends.  A call needs
+ * min(ceil(rows*H/64), 256) * 8*H*D bytes of it (every H*D <= 2048 fits); larger
+ * calls return KVMI_ENOSPC before enqueueing anything.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (different streams, or threads
+ * without stream order) race; calls ordered on one stream do not.  Results are
+ * identical to kvmi_v3_compress.
+ */
+#define KVMI_V3_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)
+int kvmi_v3_compress_noalloc(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,
+                             const uint32_t* signs, const float* levels, const int32_t* vgroup, uint8_t* q,
+                             float* kmeta, float* vmeta, kvmi_stream_t stream);
 /* Inverse: x = fma(q, scale, min) with float16 metadata (the wire form: kmeta16
  * [2][H][D], vmeta16 [2][rows][H]), FWHT_fp32, bf16((y / sqrt(D)) * s) -> out
  * bf16 [2][rows][H][D]. */

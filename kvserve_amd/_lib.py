@@ -19,7 +19,9 @@ ABI_VERSION = 1
 ERR_SYMBOL_RANGE = 1
 ERR_BAD_HEADER = 2
 ERR_CORRUPT = 4
-OK, EINVAL, ELAUNCH = 0, -22, -5
+OK, EINVAL, ELAUNCH, ENOSPC = 0, -22, -5, -28
+# Bytes of the fixed device array behind kvmi_v3_compress_noalloc (per GPU).
+V3_NOALLOC_SCRATCH_BYTES = 4 * 1024 * 1024
 
 F_NO_TRANSFORM = 1
 F_NATIVE_LAYOUT = 2
@@ -47,6 +49,7 @@ EXPORTS = (
     "kvmi_v3_compress",
     "kvmi_v3_scratch_bytes",
     "kvmi_v3_decompress",
+    "kvmi_v3_compress_noalloc",
     "kvmi_rt_encode",
     "kvmi_rt_decode",
     "kvmi_rt_hadamard",
@@ -133,6 +136,7 @@ _SIGNATURES = {
     "kvmi_v3_compress": ([_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_v3_scratch_bytes": ([_i64, _i32, _i32], _i64),
     "kvmi_v3_decompress": ([_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "kvmi_v3_compress_noalloc": ([_vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rt_encode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
     "kvmi_rt_decode": ([ctypes.POINTER(RtGeometry), _vp, _i32, _vp, _i64, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rt_hadamard": ([_vp, _vp, _i64, _i32, _vp], ctypes.c_int),
@@ -171,4 +175,6 @@ def check(rc: int, what: str) -> None:
         return
     if rc == EINVAL:
         raise ValueError(f"{what}: invalid arguments (KVMI_EINVAL)")
+    if rc == ENOSPC:
+        raise ValueError(f"{what}: the call needs more scratch than the fixed device array holds (KVMI_ENOSPC)")
     raise KvmiError(f"{what}: failed with code {rc}")

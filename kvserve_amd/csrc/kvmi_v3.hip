@@ -21,6 +21,8 @@
 //           V is read once; q = clamp(roundf((had - min) / scale), 0, L) as uint8.
 // Decompress is one launch: x = fma(q, scale16, min16), fp32 butterflies,
 // bf16((y * (1/sqrt(D))) * s) (:685-716).
+#include <mutex>
+
 #include "kvmi_common.hpp"
 
 namespace kvmi {
@@ -418,43 +420,35 @@ __global__ __launch_bounds__(kV3WG) void v3_dequant_kernel(V3Shape sh, const uin
 }
 
 // ------------------------------------------------------------------ launch
+// rows * H <= 2^29 head-rows: at most 2^23 workgroups of 256 threads, so the grid stays
+// below HIP's 2^32 work-items per dimension.
 int v3_check(int64_t rows, int32_t H, int32_t D) {
   if (rows < 0 || H < 1 || H > kV3MaxH || (kV3Rows % H) != 0 || (D != 64 && D != 128)) return KVMI_EINVAL;
-  if (rows * H > (int64_t)1 << 31) return KVMI_EINVAL;
+  if (rows * H > (int64_t)1 << 29) return KVMI_EINVAL;
   return KVMI_OK;
 }
 
-// One pass per workgroup (rows * H <= 2^31, so at most 2^25 workgroups): capping the
-// grid at 4096 and looping measured 12-14 % slower for dequant at 128-512 Ki rows.
+// One pass per workgroup (at most 2^23 workgroups, see v3_check): capping the grid at
+// 4096 and looping measured 12-14 % slower for dequant at 128-512 Ki rows.
 unsigned v3_grid(int64_t rows, int H) {
   const int64_t passes = (rows * H + kV3Rows - 1) / kV3Rows;
   return (unsigned)(passes > 0 ? passes : 1);
 }
 
-}  // namespace
-}  // namespace kvmi
-
-extern "C" int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim) {
-  using namespace kvmi;
-  if (v3_check(rows, num_heads, head_dim)) return -1;
-  return (int64_t)kV3KGrid * 2 * num_heads * head_dim * 4;
+// Workgroups of the K statistics pass, i.e. the K partials one call writes and reads.
+unsigned v3_kgrid(int64_t rows, int H) {
+  const unsigned g = v3_grid(rows, H);
+  return g < (unsigned)kV3KGrid ? g : (unsigned)kV3KGrid;
 }
 
-extern "C" int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,
-                                const uint32_t* signs, const float* levels, const int32_t* vgroup, uint8_t* q,
-                                float* kmeta, float* vmeta, void* scratch, kvmi_stream_t stream) {
-  using namespace kvmi;
-  int rc = v3_check(rows, num_heads, head_dim);
-  if (rc) return rc;
-  if (rows == 0) return KVMI_OK;
-  if (!x || !signs || !levels || !vgroup || !q || !kmeta || !vmeta || !scratch) return KVMI_EINVAL;
-  if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)kmeta) & 15) return KVMI_EINVAL;  // 16-byte vectors
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int H = num_heads, D = head_dim;
+// The three launches of compress with the K partials at `kpart`
+// (v3_kgrid(rows, H) * 2 * H * D uint32; every one is written before it is read).
+int v3_compress_launch(const void* x, int64_t rows, int32_t H, int32_t D, const uint32_t* signs,
+                       const float* levels, const int32_t* vgroup, uint8_t* q, float* kmeta, float* vmeta,
+                       uint32_t* kpart, hipStream_t st) {
   V3Shape sh{rows, H, (float)(1.0 / __builtin_sqrt((double)D))};
-  uint32_t* kpart = static_cast<uint32_t*>(scratch);
   const unsigned g = v3_grid(rows, H);
-  const unsigned gk = g < (unsigned)kV3KGrid ? g : (unsigned)kV3KGrid;  // K partials: at most kV3KGrid
+  const unsigned gk = v3_kgrid(rows, H);
   const size_t klds = (size_t)2 * H * D * 4;
   const uint16_t* xs = static_cast<const uint16_t*>(x);
   const unsigned gf = (unsigned)((H * D + 3) / 4);  // 4 channels per workgroup
@@ -470,6 +464,78 @@ extern "C" int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, 
     hipLaunchKernelGGL((v3_quant_kernel<128>), dim3(g, 2), dim3(kV3WG), 0, st, sh, xs, signs, levels, vgroup, kmeta,
                        q, vmeta);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+int v3_compress_args(const void* x, int64_t rows, int32_t H, int32_t D, const uint32_t* signs, const float* levels,
+                     const int32_t* vgroup, const uint8_t* q, const float* kmeta, const float* vmeta) {
+  if (!x || !signs || !levels || !vgroup || !q || !kmeta || !vmeta) return KVMI_EINVAL;
+  if (((uintptr_t)x | (uintptr_t)q | (uintptr_t)kmeta) & 15) return KVMI_EINVAL;  // 16-byte vectors
+  return KVMI_OK;
+}
+
+// ------------------------------------------------------------------ no-allocation variant
+// The K partials of kvmi_v3_compress_noalloc live in this fixed device array (one copy
+// per GPU, held until the process ends).  Host code never passes the array's name to a
+// kernel: the name is a host-side stand-in, and the device address of each GPU's copy
+// comes from hipGetSymbolAddress (with that GPU current), once per device.
+static __device__ __align__(256) uint8_t scratch[KVMI_V3_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of the current GPU's copy of `scratch` (null on failure).
+void* noalloc_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace kvmi
+
+extern "C" int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim) {
+  using namespace kvmi;
+  if (v3_check(rows, num_heads, head_dim)) return -1;
+  return (int64_t)kV3KGrid * 2 * num_heads * head_dim * 4;
+}
+
+extern "C" int kvmi_v3_compress(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,
+                                const uint32_t* signs, const float* levels, const int32_t* vgroup, uint8_t* q,
+                                float* kmeta, float* vmeta, void* workspace, kvmi_stream_t stream) {
+  using namespace kvmi;
+  int rc = v3_check(rows, num_heads, head_dim);
+  if (rc) return rc;
+  if (rows == 0) return KVMI_OK;
+  rc = v3_compress_args(x, rows, num_heads, head_dim, signs, levels, vgroup, q, kmeta, vmeta);
+  if (rc) return rc;
+  if (!workspace) return KVMI_EINVAL;
+  return v3_compress_launch(x, rows, num_heads, head_dim, signs, levels, vgroup, q, kmeta, vmeta,
+                            static_cast<uint32_t*>(workspace), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int kvmi_v3_compress_noalloc(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,
+                                        const uint32_t* signs, const float* levels, const int32_t* vgroup,
+                                        uint8_t* q, float* kmeta, float* vmeta, kvmi_stream_t stream) {
+  using namespace kvmi;
+  int rc = v3_check(rows, num_heads, head_dim);
+  if (rc) return rc;
+  if (rows == 0) return KVMI_OK;
+  rc = v3_compress_args(x, rows, num_heads, head_dim, signs, levels, vgroup, q, kmeta, vmeta);
+  if (rc) return rc;
+  // K partials of this call: v3_kgrid workgroups x 2 x H x D keys
+  const int64_t need = (int64_t)v3_kgrid(rows, num_heads) * 2 * num_heads * head_dim * 4;
+  if (need > KVMI_V3_NOALLOC_SCRATCH_BYTES) return KVMI_ENOSPC;
+  void* kpart = noalloc_scratch();
+  if (!kpart) return KVMI_ELAUNCH;
+  return v3_compress_launch(x, rows, num_heads, head_dim, signs, levels, vgroup, q, kmeta, vmeta,
+                            static_cast<uint32_t*>(kpart), reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int kvmi_v3_decompress(const uint8_t* q, int64_t rows, int32_t num_heads, int32_t head_dim,

@@ -265,3 +265,23 @@ def test_v3_sizes_and_contract_errors():
     assert lib.kvmi_v3_compress(16, 4, 8, 128, 16, 16, 16, 16, 8, 16, 16, None) == E  # kmeta misaligned
     assert lib.kvmi_v3_decompress(16, 4, 8, 128, 16, 16, 16, 8, None) == E  # out misaligned
     assert lib.kvmi_v3_decompress(16, 4, 8, 128, 16, 8, 16, 16, None) == E  # kmeta16 misaligned
+
+
+def test_v3_noalloc_contract_errors():
+    """kvmi_v3_compress_noalloc checks shapes, pointers and its fixed scratch capacity on
+    the host before any HIP call (every pointer below is a small integer)."""
+    from kvserve_amd import _lib
+
+    lib = _lib.load()
+    f = lib.kvmi_v3_compress_noalloc
+    assert f(16, 4, 8, 96, 16, 16, 16, 16, 16, 16, None) == _lib.EINVAL  # head_dim
+    assert f(16, 0, 8, 128, 16, 16, 16, 16, 16, 16, None) == _lib.OK  # nothing to do
+    assert f(None, 4, 8, 128, 16, 16, 16, 16, 16, 16, None) == _lib.EINVAL
+    assert f(8, 4, 8, 128, 16, 16, 16, 16, 16, 16, None) == _lib.EINVAL  # x misaligned
+    # 64 heads x 128: 256 partials of 64 KiB = 16 MiB > the 4 MiB array
+    assert f(16, 1024, 64, 128, 16, 16, 16, 16, 16, 16, None) == _lib.ENOSPC
+    # few rows: fewer partials, and 8 partials of 64 KiB fit
+    need = lambda rows, H, D: min(-(-rows * H // 64), 256) * 8 * H * D
+    assert need(8, 64, 128) <= _lib.V3_NOALLOC_SCRATCH_BYTES < need(1024, 64, 128)
+    with pytest.raises(ValueError, match="KVMI_ENOSPC"):
+        _lib.check(_lib.ENOSPC, "kvmi_v3_compress_noalloc")
