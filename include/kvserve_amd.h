@@ -56,6 +56,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_ERR_SYMBOL_RANGE 1 /* a symbol >= 2^bits reached the packer */
 #define KVMI_ERR_BAD_HEADER 2   /* stream header does not match the decode contract */
 #define KVMI_ERR_CORRUPT 4      /* an entropy-coded block does not decode consistently */
+#define KVMI_ERR_SYNC 8         /* a one-pass compress barrier timed out or met another call's keys */
 
 /* Host-visible return codes. */
 #define KVMI_OK 0
@@ -73,6 +74,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_F_NO_HEADER 4u     /* raw symbol buffer: no 16-byte header (bits must be 8) */
 #define KVMI_F_VALU_FWHT 8u     /* force the register (VALU) FWHT kernels instead of MFMA */
 #define KVMI_F_CLAMP_LEVELS 16u /* some level count exceeds 128: clamp symbols to the level */
+#define KVMI_F_TWO_PASS 32u     /* kvmi_compress_paged: statistics pass + encode pass (K read twice) */
 
 /* Launch-wide geometry shared by every job of one call. */
 typedef struct kvmi_geometry {
@@ -184,6 +186,35 @@ int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  */
 int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
                       int32_t max_blocks, int32_t* err, kvmi_stream_t stream);
+
+/*
+ * Compress in one call: the gather, transform, quantization and bitpack of
+ * kvmi_kstats_paged + kvmi_encode_paged (same outputs, bit for bit), reading every
+ * K value from HBM once.  Replaces the same reference path as those two
+ * (compression_manager.py:200-537 with kv_utils.py:59-80).
+ *
+ * Where the one-pass kernel applies (MFMA geometry, cooperative launch, and each
+ * job's K fits the LDS of the workgroups sharing it: num_blocks*S*H*D*2 <= 64 KiB
+ * per CU, e.g. 8192 tokens x 8 heads x 128 on 256 CUs), one cooperative launch keeps
+ * every workgroup's share of a job's K on chip from the statistics to the
+ * quantization.  Otherwise, or with KVMI_F_TWO_PASS, it runs kvmi_kstats_paged then
+ * kvmi_encode_paged (which use each job's `kstats`).
+ *
+ * workspace: kvmi_compress_workspace_bytes(geom, num_jobs) bytes of device memory,
+ *   256-byte aligned, zeroed once by the caller before its first use and then passed
+ *   unchanged to every call for the same jobs (per job: barrier counters and 64-bit
+ *   min / max keys tagged with the call's epoch, so nothing is cleared between
+ *   calls).  NULL selects the two-pass kernels.
+ * epoch: host pointer to the workspace's call counter, 0 before the first call; it
+ *   is incremented when (and only when) the one-pass kernel is enqueued.  Calls
+ *   sharing a workspace must be ordered on one stream.
+ * A barrier that does not complete within about 0.3 s sets KVMI_ERR_SYNC (the
+ * kernel still ends; later barriers of the launch then no longer wait).
+ */
+int64_t kvmi_compress_workspace_bytes(const kvmi_geometry* geom, int32_t num_jobs);
+int kvmi_compress_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
+                        int32_t max_blocks, void* workspace, uint32_t* epoch, int32_t* err,
+                        kvmi_stream_t stream);
 
 /*
  * Decompress: check each chunk header, unpack, dequantize

@@ -19,6 +19,7 @@ ABI_VERSION = 1
 ERR_SYMBOL_RANGE = 1
 ERR_BAD_HEADER = 2
 ERR_CORRUPT = 4
+ERR_SYNC = 8
 OK, EINVAL, ELAUNCH, ENOSPC = 0, -22, -5, -28
 # Bytes of the fixed device array behind kvmi_v3_compress_noalloc (per GPU).
 V3_NOALLOC_SCRATCH_BYTES = 4 * 1024 * 1024
@@ -28,6 +29,7 @@ F_NATIVE_LAYOUT = 2
 F_NO_HEADER = 4
 F_VALU_FWHT = 8
 F_CLAMP_LEVELS = 16
+F_TWO_PASS = 32
 
 # Every symbol include/kvserve_amd.h declares.
 EXPORTS = (
@@ -40,6 +42,8 @@ EXPORTS = (
     "kvmi_kstats_paged",
     "kvmi_encode_paged",
     "kvmi_decode_paged",
+    "kvmi_compress_paged",
+    "kvmi_compress_workspace_bytes",
     "kvmi_rans_max_bytes",
     "kvmi_rans_scratch_bytes",
     "kvmi_rans_encode",
@@ -127,6 +131,9 @@ _SIGNATURES = {
     "kvmi_kstats_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_encode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_decode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
+    "kvmi_compress_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, ctypes.POINTER(ctypes.c_uint32), _vp,
+                             _vp], ctypes.c_int),
+    "kvmi_compress_workspace_bytes": ([ctypes.POINTER(Geometry), _i32], _i64),
     "kvmi_rans_max_bytes": ([_i64, _i32], _i64),
     "kvmi_rans_scratch_bytes": ([_i64, _i32], _i64),
     "kvmi_rans_encode": ([_vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp], ctypes.c_int),

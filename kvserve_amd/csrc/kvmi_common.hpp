@@ -100,7 +100,7 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
   if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
   if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
   if (geom->flags & ~(KVMI_F_NO_TRANSFORM | KVMI_F_NATIVE_LAYOUT | KVMI_F_NO_HEADER | KVMI_F_VALU_FWHT |
-                      KVMI_F_CLAMP_LEVELS))
+                      KVMI_F_CLAMP_LEVELS | KVMI_F_TWO_PASS))
     return KVMI_EINVAL;
   out->S = S;
   out->H = H;

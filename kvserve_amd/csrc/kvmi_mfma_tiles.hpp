@@ -1,0 +1,756 @@
+// Device helpers of the MFMA paged kernels (gfx950): Hadamard tiles, rounding
+// chains, bit packers, lane reductions and the per-tile K / V work shared by the
+// two-pass kernels (kvmi_mfma.hip) and the one-pass compress (kvmi_compress.hip).
+//
+// Paged compress / decompress kernels with the Hadamard transform on MFMA (gfx950).
+//
+// The D-point transform of a row is a dense product with the +-1 Sylvester matrix,
+// issued as v_mfma_f32_32x32x16_bf16 tiles: bf16 inputs times +-1 are exact and the
+// products accumulate in fp32 (the reference runs its FWHT in fp32 with one bf16
+// rounding at the end, hadamard_func.py:97-99).  Element index e (7 bits at D=128,
+// 6 at D=64) is split as
+//     e = HALF*hl + 16*c + 8*kt + j      (HALF = D/2, hl = lane half, j = 0..7)
+// so a lane always holds one contiguous half-row: the 16-byte MFMA operand of
+// k-tile (c, kt) is uint4 number 2c+kt of that half-row.  The output element f has
+// the same split, and the Sylvester sign of (e, f) factorises into a sign per
+// 32x16 tile (chunk bits c, c') times one of two 32x16 base tiles (kt = 0, 1):
+//   H[e][f] = (-1)^(popc(c & c')) * Hb_kt[m(f)][k(e)],
+// so output chunk c' accumulates 2*NC MFMAs with +Hb or -Hb.  One accumulator
+// (16 fp32 per lane) is live at a time.
+//
+// Orientation T (encode, decode): A = Hb, B = X^T -> lane holds output half-row of
+// its row.  Orientation N (K statistics): A = X, B = Hb^T -> lane holds 16 rows of
+// one output channel, so per-channel min/max reduce in registers.
+//
+// Rademacher signs are applied by flipping bf16 sign bits (exact): on the input
+// before the forward transform and on the output after the inverse one, from an LDS
+// table of per-(head, element pair) masks.
+//
+// Work split: a workgroup of 4 wave64s owns a run of whole blocks of one (request,
+// layer) job; a tile is 32 consecutive pool rows (32/H tokens x H heads,
+// token-major, as the cache stores them), and wave w takes tiles w, w+4, ... of the
+// run.  Because 32 % H == 0 and S*H % 32 == 0, a tile never crosses a block, lane l
+// always holds head (l % 32) % H, and the H heads of a token sit in H neighbouring
+// lanes.  Each wave issues the loads of its next section (K or V half of a tile)
+// before it computes the current one.
+//
+// Per-element VALU work is kept to the rounding chain the reference fixes:
+//   encode  y = bf16(acc*s); t = bf16(y - mn); q = bf16(t * rcp); sym = rint(q)
+//   decode  x = bf16(bf16(sym*sc) + mn)  ->  MFMA  ->  out = bf16(acc*s) ^ sign
+// with each bf16 rounding one v_cvt_pk_bf16_f32, and symbols packed four to a
+// dword by v_cvt_pk_u8_f32 before the bit-width shuffle.
+#pragma once
+
+#include <atomic>
+
+
+#include "kvmi_common.hpp"
+
+namespace kvmi {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMW = 256;  // threads per workgroup
+constexpr int kWaves = kMW / 64;
+constexpr int kTok = 32;  // rows per tile (MFMA M / N)
+constexpr int kMH = 8;    // heads per shard served by these kernels (8 % H == 0)
+
+__device__ __forceinline__ bf16x8 as_b8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Keeps the scheduler from interleaving work across output chunks (or K / V
+// sections), which would keep several chunks' accumulators and constants alive.
+__device__ __forceinline__ void chunk_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// A per-lane LDS offset the compiler must re-read every iteration: the per-head
+// tables are loop-invariant for a lane, and hoisting their reads out of the tile
+// loop would pin ~160 VGPRs for the whole kernel.
+__device__ __forceinline__ int opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+// A value the instruction selector may not look through (keeps byte extracts of a
+// masked word as v_cvt_f32_ubyteN instead of re-deriving them from the source).
+__device__ __forceinline__ uint32_t barrier_u(uint32_t v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
+// Software pipelining: the loads of the next tile are issued before the current one
+// is computed.  Pinning a buffer where its tile's work starts keeps the compiler from
+// hoisting that work (e.g. the sign flips) above the previous tile's, which would
+// make the previous tile wait for these loads.
+__device__ __forceinline__ void pin(uint4& v) { asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w)); }
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+
+__device__ __forceinline__ f32x16 mfma(uint4 a, uint4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_b8(a), as_b8(b), c, 0, 0, 0);
+}
+
+// Base tile kt of the 32-point factor as this lane's MFMA operand (8 bf16 = uint4).
+// orient_n == false: A[m][k], lane = m + 32*(k/8); output bits (f_top, f3, f2, f1, f0)
+//   = (m2, m4, m3, m1, m0) so that lane l ends up with row l%32, outputs
+//   HALF*hl + 16*c' + i in accumulator register i.
+// orient_n == true:  B[k][n], lane = n + 32*(k/8); output channel bits
+//   (f_top, f3, f2, f1, f0) = (n4, n3, n2, n1, n0).
+// Input bits (e_top, e3, e2, e1, e0) = (k/8, kt, j2, j1, j0) in both.
+__device__ __forceinline__ uint4 hadamard_tile(int l, int kt, bool orient_n, bool negate) {
+  const int hl = l >> 5, r = l & 31;
+  uint32_t w[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int j = 2 * p + s;
+      int par;
+      if (!orient_n)
+        par = ((r >> 2) & hl) ^ ((r >> 4) & kt) ^ ((r >> 3) & (j >> 2)) ^ ((r >> 1) & (j >> 1) & 1) ^ (r & j & 1);
+      else
+        par = (hl & (r >> 4)) ^ (kt & (r >> 3)) ^ ((j >> 2) & (r >> 2)) ^ ((j >> 1) & (r >> 1) & 1) ^ (j & r & 1);
+      par = (par ^ (negate ? 1 : 0)) & 1;
+      v |= (uint32_t)(par ? 0xBF80u : 0x3F80u) << (16 * s);
+    }
+    w[p] = v;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ uint4 hadamard_tile(int kt, bool orient_n, bool negate) {
+  return hadamard_tile((int)(threadIdx.x & 63), kt, orient_n, negate);
+}
+
+__device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) { return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w); }
+
+// A bf16-pair constant held in an SGPR.  Left to itself the compiler encodes the
+// pair (1.0, 0) = 0x00003F80 as the inline constant "1.0" of v_dot2c_f32_bf16, which
+// the hardware reads as the f32 1.0 = 0x3F800000, i.e. the pair (0, 1.0).  The asm
+// is not volatile, so the value is materialised once and shared.
+__device__ __forceinline__ bf16x2v sgpr_pair(uint32_t v) {
+  asm("" : "+s"(v));
+  return __builtin_bit_cast(bf16x2v, v);
+}
+
+// RN(lo(bf16 pair) + c) and RN(hi(bf16 pair) + c): v_dot2_f32_bf16 against (1, 0) /
+// (0, 1) is exactly one fp32 rounding of the sum (checked on gfx950 hardware).
+__device__ __forceinline__ float add_lo(uint32_t pk, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pk), sgpr_pair(0x00003F80u), c, false);
+}
+__device__ __forceinline__ float add_hi(uint32_t pk, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pk), sgpr_pair(0x3F800000u), c, false);
+}
+
+// fp32 value of x rounded to bf16 (round to nearest even) in one instruction:
+// v_cvt_pk_bf16_f32 with a zero low half leaves bf16(x) << 16, which is that value.
+__device__ __forceinline__ float rbf(float x) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// Rounded-to-nearest-even integer in [0, 255] of a float, as byte BYTE of `acc`
+// (v_cvt_pk_u8_f32 rounds half to even and saturates, checked on gfx950).
+template <int BYTE>
+__device__ __forceinline__ uint32_t cvt_u8(float x, uint32_t acc) {
+  return __builtin_amdgcn_cvt_pk_u8_f32(x, BYTE, acc);
+}
+
+// Byte BYTE of w as a float (v_cvt_f32_ubyteN).
+template <int BYTE>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+  return (float)((w >> (8 * BYTE)) & 0xffu);
+}
+
+// q = bf16(bf16(bf16(a * s) - mn) * rcp): the quantizer's value before rint
+// (quantizer_func.py:60-62; bf16(t * rcp) == bf16(t / sc) for bf16 t and sc, the
+// exact quotient being >= 2^-17 (relative) away from every bf16 midpoint).
+__device__ __forceinline__ float quant_q(float a, float s, float mn, float rcp) {
+  return rbf(rbf(rbf(a * s) - mn) * rcp);
+}
+
+// Streaming bit packer for one lane's HALF symbols (compile-time positions).
+template <int HALF, int BITS>
+struct LanePack {
+  static constexpr int kWords = (HALF * BITS + 31) / 32;
+  static constexpr int kBytes = HALF * BITS / 8;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) w[i] = 0;
+  }
+  __device__ __forceinline__ void put(int idx, uint32_t s) {  // idx compile-time after unrolling
+    const int bit = idx * BITS, wi = bit >> 5, sh = bit & 31;
+    w[wi] |= s << sh;
+    if (sh + BITS > 32) w[wi + 1] |= s >> (32 - sh);
+  }
+  __device__ __forceinline__ uint32_t get(int idx) const {
+    const int bit = idx * BITS, wi = bit >> 5, sh = bit & 31;
+    uint32_t v = w[wi] >> sh;
+    if (sh + BITS > 32) v |= w[wi + 1] << (32 - sh);
+    return v & ((1u << BITS) - 1u);
+  }
+  // kBytes is a multiple of 4 (HALF >= 32), and of 8 when HALF == 64.
+  __device__ __forceinline__ void store(uint8_t* p) const {
+    if constexpr (kBytes % 16 == 0) {
+      uint4* q = reinterpret_cast<uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 16; ++i) gst(q + i, make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]));
+    } else if constexpr (kBytes % 8 == 0) {
+      uint2* q = reinterpret_cast<uint2*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 8; ++i) gst(q + i, make_uint2(w[2 * i], w[2 * i + 1]));
+    } else {
+      uint32_t* q = reinterpret_cast<uint32_t*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 4; ++i) gst(q + i, w[i]);
+    }
+  }
+  // Store into LDS (p aligned to the largest of 16, 8, 4 that divides kBytes).
+  __device__ __forceinline__ void store_lds(uint8_t* p) const {
+    if constexpr (kBytes % 16 == 0) {
+      uint4* q = reinterpret_cast<uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 16; ++i) q[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+    } else if constexpr (kBytes % 8 == 0) {
+      uint2* q = reinterpret_cast<uint2*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 8; ++i) q[i] = make_uint2(w[2 * i], w[2 * i + 1]);
+    } else {
+      uint32_t* q = reinterpret_cast<uint32_t*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 4; ++i) q[i] = w[i];
+    }
+  }
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    if constexpr (kBytes % 16 == 0) {
+      const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 16; ++i) {
+        uint4 t = gld(q + i);
+        w[4 * i] = t.x;
+        w[4 * i + 1] = t.y;
+        w[4 * i + 2] = t.z;
+        w[4 * i + 3] = t.w;
+      }
+    } else if constexpr (kBytes % 8 == 0) {
+      const uint2* q = reinterpret_cast<const uint2*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 8; ++i) {
+        uint2 t = gld(q + i);
+        w[2 * i] = t.x;
+        w[2 * i + 1] = t.y;
+      }
+    } else {
+      const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+      for (int i = 0; i < kBytes / 4; ++i) w[i] = gld(q + i);
+    }
+    if constexpr (kWords * 4 > kBytes) w[kWords - 1] &= 0xffffffffu >> (32 - 8 * (kBytes % 4));
+  }
+};
+
+// Byte lanes of the symbols that cannot fit BITS bits (v_cvt_pk_u8_f32 saturates at
+// 255, so a symbol >= 2^BITS always shows in these bits of the OR of all bytes).
+template <int BITS>
+constexpr uint32_t overflow_mask() {
+  return 0x01010101u * (0xffu & ~((1u << BITS) - 1u));
+}
+
+// Shared per-workgroup tables.
+struct Tables {
+  uint32_t smask[kMH][64 + 4];  // bf16 sign-flip masks per (head, element pair), padded rows
+  float2 kc[kMH][128 + 4];      // K (min, 1/scale) [encode] or (min, scale) [decode], by source head
+  uint8_t prof[2][3][kMH];      // the job's profile bytes (kvmi_layer_job::profile)
+  int posk[kMH], posv[kMH], gfirst[kMH];
+};
+
+// Stage the profile bytes into LDS (one load per thread, no dependent chains).
+__device__ __forceinline__ void stage_profile(Tables& T, const uint8_t* profile, int H) {
+  if (threadIdx.x < 6u * H) {
+    const int i = threadIdx.x, part = i / (3 * H), f = (i / H) % 3, k = i % H;
+    T.prof[part][f][k] = gld(profile + i);
+  }
+}
+
+// Fill the sign-mask table: word p of head h flips elements 2p and 2p+1.
+__device__ __forceinline__ void fill_signs(Tables& T, const uint32_t* signs, int H, int D) {
+  for (int i = threadIdx.x; i < H * (D / 2); i += (int)blockDim.x) {
+    const int h = i / (D / 2), p = i % (D / 2);
+    const uint32_t s = gld(signs + h * (D / 32) + (2 * p) / 32) >> ((2 * p) & 31);
+    T.smask[h][p] = ((s & 1u) << 15) | ((s & 2u) << 30);
+  }
+}
+
+// Output positions of each source head and the first head of each V group, from
+// the staged profile (after a barrier).
+__device__ __forceinline__ void fill_positions(Tables& T, int H) {
+  if (threadIdx.x < (unsigned)H) {
+    const int h = threadIdx.x;
+    for (int k = 0; k < H; ++k) {
+      if (T.prof[0][0][k] == h) T.posk[h] = k;
+      if (T.prof[1][0][k] == h) T.posv[h] = k;
+    }
+    // first output position of V group h (if any) -> its source head
+    T.gfirst[h] = -1;
+    for (int k = H - 1; k >= 0; --k)
+      if (T.prof[1][2][k] == h) T.gfirst[h] = T.prof[1][0][k];
+  }
+}
+
+// K constants by source head from kmeta (stored by output position j, whose source
+// head is order[j]).  DIV: store (min, 1/scale) instead of (min, scale).
+template <bool DIV>
+__device__ __forceinline__ void fill_kconst(Tables& T, const uint16_t* kmeta, int H, int D) {
+  const int HD = H * D;
+  for (int i = threadIdx.x; i < HD; i += (int)blockDim.x) {
+    const int j = i / D, e = i % D, hs = T.prof[0][0][j];
+    const float m = bf16_to_f32(gld(kmeta + i));
+    const float sc = bf16_to_f32(gld(kmeta + HD + i));
+    T.kc[hs][e] = make_float2(m, DIV ? 1.0f / sc : sc);
+  }
+}
+
+// The run of tokens [tok0, tok_end) of a workgroup and its tile count.  Runs are
+// whole blocks and tiles never straddle blocks, so every row of every tile exists.
+struct Run {
+  int tok0, tok_end, tiles, nwg;
+};
+__device__ __forceinline__ Run wg_run(const kvmi_layer_job& job, const Geo& g) {
+  Run u;
+  const int ntok = job.num_blocks * g.S;
+  const int run = g.bpw * g.S;
+  u.nwg = (ntok + run - 1) / run;
+  u.tok0 = blockIdx.x * run;
+  u.tok_end = min(ntok, u.tok0 + run);
+  u.tiles = u.tok_end > u.tok0 ? (u.tok_end - u.tok0) * g.H / kTok : 0;
+  return u;
+}
+
+// Pool row of the first row of tile t (wave-uniform); lane r's row is that + r, its
+// token tile_tok(..) + r / H.
+__device__ __forceinline__ int tile_tok(int tok0, int H, int t) { return tok0 + t * (kTok / H); }
+__device__ __forceinline__ int64_t tile_row0(const kvmi_layer_job& job, int S, int H, int ta) {
+  return ((int64_t)cld(job.block_ids + ta / S) * S + (ta % S)) * H;
+}
+
+// Load (and sign) the lane's half-row of bf16 inputs of pool row `row`.
+template <int NC>
+__device__ __forceinline__ void load_half_row(const uint16_t* __restrict__ pool, int64_t row, int hl,
+                                              uint4 (&x)[2 * NC]) {
+  constexpr int D = 32 * NC, HALF = 16 * NC;
+  const uint4* src = reinterpret_cast<const uint4*>(pool + row * D + HALF * hl);
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) x[u] = gld(src + u);
+}
+// The same from a sign-mask table laid out like Tables::smask.
+template <int NC>
+__device__ __forceinline__ void sign_half_row(const uint32_t (*smask)[64 + 4], int h, int hl, uint4 (&x)[2 * NC]) {
+  constexpr int HALF = 16 * NC;
+  const uint4* sm = reinterpret_cast<const uint4*>(&smask[0][0] + opaque(h * (64 + 4) + (HALF / 2) * hl));
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) x[u] = xor4(x[u], sm[u]);
+}
+template <int NC>
+__device__ __forceinline__ void sign_half_row(const Tables& T, int h, int hl, uint4 (&x)[2 * NC]) {
+  constexpr int HALF = 16 * NC;
+  const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(h * (64 + 4) + (HALF / 2) * hl));
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) x[u] = xor4(x[u], sm[u]);
+}
+
+// Forward / inverse transform, orientation T, output chunk cp (unscaled fp32).
+// The input chunks are visited in the order cp ^ k, so the chains of different
+// output chunks share no prefix (a shared prefix would keep extra accumulators live).
+template <int NC>
+__device__ __forceinline__ f32x16 transform_T(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                              int cp) {
+  f32x16 acc = {};
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = cp ^ k;
+    const bool neg = __builtin_popcount(c & cp) & 1;
+    acc = mfma(neg ? hn[0] : hp[0], x[2 * c], acc);
+    acc = mfma(neg ? hn[1] : hp[1], x[2 * c + 1], acc);
+  }
+  return acc;
+}
+
+// Pack the 16 quantized values q of output chunk cp into the lane's packer (rint,
+// saturate, and OR the bytes into `over` for the width check).  Widths 2, 4, 8 pack
+// byte lanes: dword d_m holds the symbols i with i % P == m (P = 8/BITS symbols per
+// byte), and the chunk's words are OR_m d_m << (m*BITS).
+template <int HALF, int BITS>
+__device__ __forceinline__ void pack_chunk(const float (&q)[16], int cp, LanePack<HALF, BITS>& pk, uint32_t& over) {
+  if constexpr (BITS == 2 || BITS == 4 || BITS == 8) {
+    constexpr int P = 8 / BITS, W = BITS / 2;
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int m = 0; m < P; ++m) {
+        uint32_t d = cvt_u8<0>(q[P * (4 * j) + m], 0u);
+        d = cvt_u8<1>(q[P * (4 * j + 1) + m], d);
+        d = cvt_u8<2>(q[P * (4 * j + 2) + m], d);
+        d = cvt_u8<3>(q[P * (4 * j + 3) + m], d);
+        over |= d;
+        word |= d << (m * BITS);
+      }
+      pk.w[cp * W + j] = word;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t sym = cvt_u8<0>(q[i], 0u);
+      over |= sym;
+      pk.put(16 * cp + i, sym);
+    }
+  }
+}
+
+// Quantize output chunk cp (16 accumulators of the lane's half-row) with per-element
+// (min, 1/scale) pairs from the LDS table at kq (K: per-channel statistics).
+template <int HALF, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_chunk_k(const f32x16& acc, int cp, float s, const float2* kq, float lv,
+                                              LanePack<HALF, BITS>& pk, uint32_t& over) {
+  float q[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const float4 c = *reinterpret_cast<const float4*>(kq + i);
+    q[i] = quant_q(acc[i], s, c.x, c.y);
+    q[i + 1] = quant_q(acc[i + 1], s, c.z, c.w);
+    if constexpr (CLAMP) {
+      q[i] = fminf(q[i], lv);
+      q[i + 1] = fminf(q[i + 1], lv);
+    }
+  }
+  pack_chunk<HALF, BITS>(q, cp, pk, over);
+}
+
+// Quantize output chunk cp from its 16 transformed values y, kept as 8 bf16 pairs,
+// with the row's (mn, 1/scale) (V: per-token statistics).
+template <int HALF, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_chunk_v(const uint32_t* ypk, int cp, float mn, float rcp, float lv,
+                                              LanePack<HALF, BITS>& pk, uint32_t& over) {
+  float q[16];
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const uint32_t y2 = ypk[i / 2];
+    q[i] = rbf(rbf(bf_lo(y2) - mn) * rcp);
+    q[i + 1] = rbf(rbf(bf_hi(y2) - mn) * rcp);
+    if constexpr (CLAMP) {
+      q[i] = fminf(q[i], lv);
+      q[i + 1] = fminf(q[i + 1], lv);
+    }
+  }
+  pack_chunk<HALF, BITS>(q, cp, pk, over);
+}
+
+// The 8 symbols of operand u (elements 8u .. 8u+7 of the half-row) as floats.
+template <int HALF, int BITS>
+__device__ __forceinline__ void syms8(const LanePack<HALF, BITS>& pk, int u, float (&s)[8]) {
+  if constexpr (BITS == 4) {
+    const uint32_t w = pk.w[u];
+    const uint32_t lo = barrier_u(w & 0x0F0F0F0Fu), hi = barrier_u((w >> 4) & 0x0F0F0F0Fu);
+    s[0] = ubyte<0>(lo);
+    s[1] = ubyte<0>(hi);
+    s[2] = ubyte<1>(lo);
+    s[3] = ubyte<1>(hi);
+    s[4] = ubyte<2>(lo);
+    s[5] = ubyte<2>(hi);
+    s[6] = ubyte<3>(lo);
+    s[7] = ubyte<3>(hi);
+  } else if constexpr (BITS == 8) {
+    const uint32_t a = pk.w[2 * u], b = pk.w[2 * u + 1];
+    s[0] = ubyte<0>(a);
+    s[1] = ubyte<1>(a);
+    s[2] = ubyte<2>(a);
+    s[3] = ubyte<3>(a);
+    s[4] = ubyte<0>(b);
+    s[5] = ubyte<1>(b);
+    s[6] = ubyte<2>(b);
+    s[7] = ubyte<3>(b);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = (float)pk.get(8 * u + j);
+  }
+}
+
+// Dequantized bf16 MFMA operands of the lane's half-row: x~ = bf16(bf16(sym*sc) + mn)
+// (quantizer_func.py:108-112).  KQ: per-element (min, scale) pairs from the LDS
+// table at kd; otherwise the row's (mn, sc).
+template <int NC, int BITS, bool KQ>
+__device__ __forceinline__ void dequant_half_row(const LanePack<16 * NC, BITS>& pk, const float2* kd, float mn,
+                                                 float sc, uint4 (&x)[2 * NC]) {
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) {
+    float sy[8];
+    syms8<16 * NC, BITS>(pk, u, sy);
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (KQ) {
+        // per-element constants: the pair's sums come straight out of v_dot2
+        const float4 c = *reinterpret_cast<const float4*>(&kd[8 * u + 2 * p]);
+        const uint32_t spk = pack_bf16x2(sy[2 * p] * c.y, sy[2 * p + 1] * c.w);
+        w[p] = pack_bf16x2(add_lo(spk, c.x), add_hi(spk, c.z));
+      } else {
+        // one row minimum: plain adds (v_dot2c would need a copy of it per element)
+        w[p] = pack_bf16x2(rbf(sy[2 * p] * sc) + mn, rbf(sy[2 * p + 1] * sc) + mn);
+      }
+    }
+    x[u] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// DPP lane exchange of a float (no bound_ctrl; every lane is enabled).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Min / max over the H lanes of a token (aligned groups of H in 1, 2, 4, 8):
+// quad_perm xor 1, xor 2, then row_half_mirror (lane i <-> 7 - i of each 8).
+__device__ __forceinline__ void token_minmax(float& a, float& b, int H) {
+  if (H >= 2) {
+    a = fminf(a, dpp<0xB1>(a));
+    b = fmaxf(b, dpp<0xB1>(b));
+  }
+  if (H >= 4) {
+    a = fminf(a, dpp<0x4E>(a));
+    b = fmaxf(b, dpp<0x4E>(b));
+  }
+  if (H >= 8) {
+    a = fminf(a, dpp<0x141>(a));
+    b = fmaxf(b, dpp<0x141>(b));
+  }
+}
+// Min / max of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the upper 32
+// lanes of its first operand with the lower 32 lanes of its second; with x in both,
+// result 0 holds x of lane l % 32 and result 1 x of lane 32 + l % 32.
+__device__ __forceinline__ float halves_min(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// ============================================================== tile helpers
+// K statistics of one signed tile, orientation N: output register i of chunk c holds
+// row m = 8*(i/4) + 4*hl + i%4 of the tile and channel f(r, c) = HALF*(r>>4) + 16*c +
+// (r & 15); row m has head m % H, which depends only on s = i%4 (32 % H == 0 and
+// H <= 8).  Running min / max per (s, c) of the unscaled accumulators.
+template <int NC>
+__device__ __forceinline__ void kstats_tile(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                            float (&mn)[4][NC], float (&mx)[4][NC]) {
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    f32x16 acc = {};
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int c = cp ^ k;
+      const bool neg = __builtin_popcount(c & cp) & 1;
+      acc = mfma(x[2 * c], neg ? hn[0] : hp[0], acc);
+      acc = mfma(x[2 * c + 1], neg ? hn[1] : hp[1], acc);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      mn[a][cp] = fminf(fminf(mn[a][cp], acc[a]), fminf(acc[a + 4], fminf(acc[a + 8], acc[a + 12])));
+      mx[a][cp] = fmaxf(fmaxf(mx[a][cp], acc[a]), fmaxf(acc[a + 4], fmaxf(acc[a + 8], acc[a + 12])));
+    }
+    chunk_fence();
+  }
+}
+
+// Push a wave's running K min / max into the workgroup's LDS keys [2][H][D] (by
+// source head and channel).  Scaling by 1/sqrt(D) > 0 is monotone, so it commutes
+// with min / max (and so does the bf16 rounding applied when the keys are finalised).
+template <int NC>
+__device__ __forceinline__ void push_lkeys(uint32_t* lkey, const float (&mn)[4][NC], const float (&mx)[4][NC],
+                                           int H, float scale) {
+  constexpr int D = 32 * NC;
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31, HD = H * D;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int h = (4 * hl + a) % H;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int f = (16 * NC) * (r >> 4) + 16 * c + (r & 15);
+      atomicMin(&lkey[h * D + f], f2key(mn[a][c] * scale));
+      atomicMax(&lkey[HD + h * D + f], f2key(mx[a][c] * scale));
+    }
+  }
+}
+
+// The lane's fixed V / K profile values within a job (after fill_positions).
+struct LaneProfile {
+  int jk, jv, gv;
+  float lvk, lvv;
+  bool rep_lane;  // writes the V metadata of (group, token)
+};
+__device__ __forceinline__ LaneProfile lane_profile(const Tables& T, int hme, int hl) {
+  LaneProfile p;
+  p.jk = T.posk[hme];
+  p.jv = T.posv[hme];
+  p.gv = T.prof[1][2][p.jv];
+  p.lvk = (float)T.prof[0][1][p.jk];
+  p.lvv = (float)T.prof[1][1][p.jv];
+  p.rep_lane = hl == 0 && T.gfirst[p.gv] == hme;
+  return p;
+}
+
+// K section of a signed tile (orientation T): transform and quantize with the
+// per-channel (min, 1/scale) pairs at kq into pkd.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_k_tile(const uint4 (&xk)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                             const float2* kq, float s, float lvk, LanePack<16 * NC, BITS>& pkd,
+                                             uint32_t& over) {
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
+    quant_chunk_k<16 * NC, BITS, CLAMP>(acc, cp, s, kq + 16 * cp, lvk, pkd, over);
+    chunk_fence();
+  }
+}
+
+// V section of a signed tile (per-token statistics over the heads of a group):
+// transform once, keeping y = bf16(acc * s) as bf16 pairs, reduce the group's
+// min / max over the token's lanes, write the (group, token) metadata from the
+// representative lane and quantize into pkd.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_v_tile(const uint4 (&xv)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                             const LaneProfile& lp, const kvmi_layer_job& job, int ntok, int tok,
+                                             int G, int H, float s, LanePack<16 * NC, BITS>& pkd, uint32_t& over) {
+  constexpr int HALF = 16 * NC;
+  uint32_t ypk[HALF / 2];
+  float amn = __builtin_inff(), amx = -__builtin_inff();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
+      amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) ypk[8 * cp + i / 2] = pack_bf16x2(acc[i] * s, acc[i + 1] * s);
+    chunk_fence();
+  }
+  // y = bf16(fl(acc * s)) is monotone in acc (s > 0): the row's min / max of y
+  // are those of acc pushed through the same rounding.
+  amn = halves_min(amn);
+  amx = halves_max(amx);
+  float mn = 0.f, mx = 0.f;
+  for (int gg = 0; gg < G; ++gg) {
+    float a = lp.gv == gg ? amn : __builtin_inff();
+    float b = lp.gv == gg ? amx : -__builtin_inff();
+    token_minmax(a, b, H);
+    if (lp.gv == gg) {
+      mn = a;
+      mx = b;
+    }
+  }
+  mn = rbf(mn * s);
+  mx = rbf(mx * s);
+  const float sc = quant_scale(mn, mx, (int)lp.lvv);
+  const float rcp = 1.0f / sc;
+  if (lp.rep_lane) {
+    gst(job.vmeta + (int64_t)lp.gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
+    gst(job.vmeta + (int64_t)(G + lp.gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
+  }
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    quant_chunk_v<HALF, BITS, CLAMP>(ypk + 8 * cp, cp, mn, rcp, lp.lvv, pkd, over);
+    chunk_fence();
+  }
+}
+
+// V section of a signed tile (per-token statistics over the heads of a group) like
+// quant_v_tile, with the transform run twice (statistics, then quantization) instead
+// of keeping the rounded outputs in registers: the same values, 32 fewer VGPRs.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_v_tile_twice(const uint4 (&xv)[2 * NC], const uint4 (&hp)[2],
+                                                   const uint4 (&hn)[2], const LaneProfile& lp,
+                                                   const kvmi_layer_job& job, int ntok, int tok, int G, int H,
+                                                   float s, LanePack<16 * NC, BITS>& pkd, uint32_t& over) {
+  constexpr int HALF = 16 * NC;
+  float amn = __builtin_inff(), amx = -__builtin_inff();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
+      amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
+    }
+    chunk_fence();
+  }
+  amn = halves_min(amn);
+  amx = halves_max(amx);
+  float mn = 0.f, mx = 0.f;
+  for (int gg = 0; gg < G; ++gg) {
+    float a = lp.gv == gg ? amn : __builtin_inff();
+    float b = lp.gv == gg ? amx : -__builtin_inff();
+    token_minmax(a, b, H);
+    if (lp.gv == gg) {
+      mn = a;
+      mx = b;
+    }
+  }
+  mn = rbf(mn * s);
+  mx = rbf(mx * s);
+  const float sc = quant_scale(mn, mx, (int)lp.lvv);
+  const float rcp = 1.0f / sc;
+  if (lp.rep_lane) {
+    gst(job.vmeta + (int64_t)lp.gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
+    gst(job.vmeta + (int64_t)(G + lp.gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
+  }
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+    float q[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      q[i] = quant_q(acc[i], s, mn, rcp);
+      if constexpr (CLAMP) q[i] = fminf(q[i], lp.lvv);
+    }
+    pack_chunk<HALF, BITS>(q, cp, pkd, over);
+    chunk_fence();
+  }
+}
+
+// Counters in LDS between the waves of a workgroup.  Everything these counters
+// publish (keys, constants, tables) lives in LDS, and the LDS executes each wave's
+// operations in order: a wave that sees another wave's increment also sees that
+// wave's earlier LDS writes.  So the only ordering needed is the compiler's (and a
+// wait for the wave's own LDS operations); a workgroup-scope fence would also wait for
+// every outstanding global load and store of the wave, i.e. for the prefetched tiles.
+__device__ __forceinline__ void lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Spin (the whole wave) until an LDS counter reaches `target`.  Bounded: after about
+// half a second it gives up and returns false.
+constexpr uint32_t kMaxLdsPolls = 1u << 22;
+__device__ __forceinline__ bool lds_wait(uint32_t* ctr, uint32_t target) {
+  bool ok = false;
+  for (uint32_t polls = 0; polls < kMaxLdsPolls; ++polls) {
+    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) {
+      ok = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  lds_order();
+  return ok;
+}
+__device__ __forceinline__ void lds_signal(uint32_t* ctr) {
+  lds_order();
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+}  // namespace
+}  // namespace kvmi

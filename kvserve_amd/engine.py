@@ -111,7 +111,7 @@ class FusedKVCodec:
 
     def __init__(self, num_heads: int, head_dim: int, block_size: int, bits: int = 4,
                  seed: int = DEFAULT_SEED, transform: bool = True, layout: str = "permuted",
-                 header: bool = True, fwht: Optional[str] = None):
+                 header: bool = True, fwht: Optional[str] = None, compress_path: Optional[str] = None):
         if type(bits) is not int or not 1 <= bits <= 8:
             raise ValueError("bitpack_bits must be an integer in [1, 8]")
         if head_dim not in (64, 128):
@@ -126,6 +126,12 @@ class FusedKVCodec:
         self.fwht = (fwht or os.environ.get("KVSERVE_AMD_FWHT", "mfma")).strip().lower()
         if self.fwht not in ("mfma", "valu"):
             raise ValueError("fwht must be 'mfma' or 'valu'")
+        # compress: "two_pass" (kvmi_kstats_paged + kvmi_encode_paged, the faster on
+        # MI355X) or "one_pass" (kvmi_compress_paged: every K value read from HBM once
+        # where the jobs fit the one-pass kernel; KVSERVE_AMD_COMPRESS=one_pass)
+        self.compress_path = (compress_path or os.environ.get("KVSERVE_AMD_COMPRESS", "two_pass")).strip().lower()
+        if self.compress_path not in ("one_pass", "two_pass"):
+            raise ValueError("compress_path must be 'one_pass' or 'two_pass'")
         self._lib = _lib.load()
 
     # ---------------------------------------------------------------- helpers
@@ -351,17 +357,40 @@ class Plan:
         max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
         self.geo = codec._geometry(packet.vmeta.shape[2], max_level)
         packet.__dict__["_err"] = self.err
+        self._init_workspace()
+
+    def _init_workspace(self) -> None:
+        """Device workspace of kvmi_compress_paged (barrier counters and epoch-tagged
+        keys), zeroed once; the host-side epoch counts the one-pass launches on it."""
+        self.workspace, self.epoch = None, ctypes.c_uint32(0)
+        if self.kind == "compress" and self.codec.compress_path == "one_pass":
+            n = int(self.codec._lib.kvmi_compress_workspace_bytes(ctypes.byref(self.geo), self.num_jobs))
+            if n < 0:
+                raise ValueError("geometry not supported by kvmi_compress_paged")
+            self.workspace = torch.zeros(max(n, 256), dtype=torch.uint8, device=self.device)
 
     def launches(self) -> List[str]:
         """Names of the C entry points one run() enqueues, in order."""
         if self.max_blocks == 0:
             return []
-        return ["kvmi_kstats_paged", "kvmi_encode_paged"] if self.kind == "compress" else ["kvmi_decode_paged"]
+        if self.kind == "compress":
+            if self.workspace is not None:
+                return ["kvmi_compress_paged"]
+            return ["kvmi_kstats_paged", "kvmi_encode_paged"]
+        return ["kvmi_decode_paged"]
 
     def launch(self, name: str) -> None:
         """Enqueue one of launches() on the current stream."""
         fn = getattr(self.codec._lib, name)
         with torch.cuda.device(self.device):
+            if name == "kvmi_compress_paged":
+                if self.epoch.value >= 1 << 31:  # epoch tags are 32-bit: start the workspace afresh
+                    self.workspace.zero_()
+                    self.epoch.value = 0
+                _lib.check(fn(ctypes.byref(self.geo), _ptr(self.jobs), self.num_jobs, self.max_blocks,
+                              _ptr(self.workspace), ctypes.byref(self.epoch), _ptr(self.err), _stream_handle()),
+                           name)
+                return
             _lib.check(fn(ctypes.byref(self.geo), _ptr(self.jobs), self.num_jobs, self.max_blocks, _ptr(self.err),
                           _stream_handle()), name)
 
@@ -403,7 +432,9 @@ class BatchPlan:
         self.err = torch.zeros(1, dtype=torch.int32, device=self.device)
         for pk in self.packets:
             pk.__dict__["_err"] = self.err
+        self._init_workspace()
 
+    _init_workspace = Plan._init_workspace
     launches = Plan.launches
     launch = Plan.launch
     run = Plan.run
@@ -419,6 +450,8 @@ def raise_device_error(code: int) -> None:
         raise RuntimeError("invalid bitpack header or decode configuration")
     if code & _lib.ERR_CORRUPT:
         raise RuntimeError("corrupt entropy-coded stream")
+    if code & _lib.ERR_SYNC:
+        raise RuntimeError("one-pass compress: a workgroup barrier timed out or met keys of another call")
 
 
 def check_packet(packet: Packet, force: bool = False) -> None:

@@ -1,0 +1,159 @@
+"""One-pass compress (kvmi_compress_paged, K read once) against the two-pass kernels
+(kvmi_kstats_paged + kvmi_encode_paged) through the C-ABI: packed streams, K and V
+metadata must be identical, bit for bit, on every call.  The two-pass path is itself
+pinned to the oracle (test_gpu_codec.py, test_gpu_configs.py; those tests run the
+default one-pass path too)."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _requests(g, lens_blocks, L, H, D, S, P, levels):
+    from kvserve_amd.profiles import per_head_profile
+    from kvserve_amd.workloads import kv_blocks
+
+    pools = [torch.zeros((2, P, S, H, D), dtype=torch.bfloat16) for _ in range(L)]
+    perm = torch.randperm(P, generator=g)
+    reqs, off = [], 0
+    for B in lens_blocks:
+        ids = perm[off:off + B]
+        off += B
+        for p in pools:
+            p[:, ids] = kv_blocks(g, B, S, H, D)
+        kl = [[levels[int(i)] for i in torch.randint(0, len(levels), (H,), generator=g)] for _ in range(L)]
+        vl = [[levels[int(i)] for i in torch.randint(0, len(levels), (H,), generator=g)] for _ in range(L)]
+        reqs.append((ids.to(torch.int32), [per_head_profile(kl[l], vl[l]) for l in range(L)]))
+    return pools, reqs
+
+
+def _outputs(plan):
+    """Streams, K metadata and the V metadata rows each layer uses (a layer with fewer
+    V groups than the plan's table leaves the other rows unwritten, on either path)."""
+    pks = plan.packets if hasattr(plan, "packets") else [plan.packet]
+    out = []
+    for pk in pks:
+        vm = torch.cat([pk.vmeta[l, :, :p.num_v_groups()].reshape(-1) for l, p in enumerate(pk.profiles)])
+        out.append(([s.clone() for s in pk.streams], pk.kmeta.clone(), vm))
+    return out
+
+
+def _assert_same(a, b):
+    assert len(a) == len(b)
+    for (sa, ka, va), (sb, kb, vb) in zip(a, b):
+        for x, y in zip(sa, sb):
+            assert torch.equal(x, y)
+        assert torch.equal(ka.view(torch.int16), kb.view(torch.int16))
+        assert torch.equal(va.view(torch.int16), vb.view(torch.int16))
+
+
+def _compare(cuda, pools, reqs, H, D, S, bits, layout="permuted", runs=3, expect_one_pass=True):
+    from kvserve_amd.engine import FusedKVCodec
+
+    pools = [p.to(cuda) for p in pools]
+    args = [(pools, ids.to(cuda), prof) for ids, prof in reqs]
+    ref_codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path="two_pass")
+    one_codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path="one_pass")
+    ref = ref_codec.plan_compress_batch(args)
+    one = one_codec.plan_compress_batch(args)
+    assert one.launches() == ["kvmi_compress_paged"]
+    ref.run()
+    ref.check_errors()
+    want = _outputs(ref)
+    for k in range(runs):
+        for j, pk in enumerate(one.packets):  # poison the outputs: every byte must be written again
+            for s in pk.streams:
+                s.fill_(0xA5)
+            if pk.num_blocks:  # a request without blocks keeps its K metadata (C-ABI contract)
+                pk.kmeta.view(torch.int16).fill_(-1)
+            else:
+                pk.kmeta.copy_(ref.packets[j].kmeta)
+        one.run()
+        one.check_errors()
+        _assert_same(_outputs(one), want)
+    # the host-side epoch counts the one-pass launches (it stays 0 on the fallback)
+    assert one.epoch.value == (runs if expect_one_pass else 0)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("H,S,D,bits,layout", [
+    (8, 16, 128, 4, "permuted"),
+    (8, 16, 128, 4, "native"),
+    (8, 16, 64, 3, "permuted"),   # two tiles per wave
+    (4, 16, 128, 5, "permuted"),
+    (2, 16, 128, 4, "native"),
+    (1, 32, 128, 2, "permuted"),
+    (8, 32, 64, 6, "permuted"),
+])
+def test_one_pass_equals_two_pass_on_ragged_batches(cuda, H, S, D, bits, layout):
+    g = torch.Generator().manual_seed(H * 131 + S * 7 + D + bits)
+    top = 2 ** bits - 1
+    pools, reqs = _requests(g, [9, 0, 3, 40, 1], 3, H, D, S, 64, (top, max(2, top - 2)))
+    print(f"one-pass H={H} S={S} D={D} bits={bits} {layout}", flush=True)
+    _compare(cuda, pools, reqs, H, D, S, bits, layout)
+
+
+def test_one_pass_with_levels_above_128(cuda):
+    g = torch.Generator().manual_seed(5)
+    pools, reqs = _requests(g, [7, 12], 2, 8, 128, 16, 32, (200, 255))
+    _compare(cuda, pools, reqs, 8, 128, 16, 8)
+
+
+def test_one_pass_config2_shape_whole_grid(cuda):
+    """32 layers x 512 blocks of 16 tokens x 8 heads x 128: each job spans the whole
+    grid (one group), as on the benchmark's configuration."""
+    from kvserve_amd.workloads import kv_blocks, llama_row_profiles
+
+    g = torch.Generator().manual_seed(2)
+    L, B, S, H, D = 32, 512, 16, 8, 128
+    pools = []
+    for _ in range(L):
+        pools.append(kv_blocks(g, B, S, H, D))
+    ids = torch.randperm(B, generator=g).to(torch.int32)
+    prof = llama_row_profiles(L, H)
+    print("one-pass config-2 shape", flush=True)
+    _compare(cuda, pools, [(ids, prof)], H, D, S, 4, runs=2)
+
+
+def test_job_too_large_for_one_pass_falls_back(cuda):
+    """A job whose K exceeds the LDS of the whole grid runs the two passes inside
+    kvmi_compress_paged (and leaves the epoch alone)."""
+    g = torch.Generator().manual_seed(9)
+    pools, reqs = _requests(g, [4096], 1, 8, 128, 16, 4096, (16, 16))
+    _compare(cuda, pools, reqs, 8, 128, 16, 4, runs=1, expect_one_pass=False)
+
+
+def test_workspace_contract_through_the_c_abi(cuda):
+    """Direct C-ABI use: a zeroed workspace, a host epoch counter advanced by the call."""
+    from kvserve_amd import _lib
+    from kvserve_amd.engine import FusedKVCodec
+
+    g = torch.Generator().manual_seed(3)
+    pools, reqs = _requests(g, [6], 2, 8, 128, 16, 16, (16, 12))
+    pools = [p.to(cuda) for p in pools]
+    codec = FusedKVCodec(8, 128, 16, 4, 0xC0FEBABE, compress_path="two_pass")
+    plan = codec.plan_compress(pools, reqs[0][0].to(cuda), reqs[0][1])
+    plan.run()
+    want = _outputs(plan)
+    lib = _lib.load()
+    n = lib.kvmi_compress_workspace_bytes(ctypes.byref(plan.geo), plan.num_jobs)
+    assert n == 256 * ((plan.num_jobs * 1024 + 255) // 256) + plan.num_jobs * 2 * 8 * 128 * 8
+    ws = torch.zeros(n, dtype=torch.uint8, device=cuda)
+    epoch = ctypes.c_uint32(0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for k in range(2):
+        rc = lib.kvmi_compress_paged(ctypes.byref(plan.geo), plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks,
+                                     ws.data_ptr(), ctypes.byref(epoch), plan.err.data_ptr(), stream)
+        assert rc == 0 and epoch.value == k + 1
+        plan.check_errors()
+        _assert_same(_outputs(plan), want)
+    # misaligned workspace / missing epoch pointer: rejected on the host
+    assert lib.kvmi_compress_paged(ctypes.byref(plan.geo), plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks,
+                                   ws.data_ptr() + 16, ctypes.byref(epoch), plan.err.data_ptr(), stream) == _lib.EINVAL
+    assert lib.kvmi_compress_paged(ctypes.byref(plan.geo), plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks,
+                                   ws.data_ptr(), None, plan.err.data_ptr(), stream) == _lib.EINVAL
+    assert epoch.value == 2
