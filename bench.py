@@ -33,6 +33,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import subprocess
 import sys
 import time
@@ -129,20 +130,31 @@ def traffic_frac(kernels, seconds: float, workload: str):
     return round(total / seconds / 1e9 / HBM_PEAK_GBPS, 4)
 
 
-def profiled_traffic(kernel: str, workload: str = "config2"):
+def profiled_traffic(kernel: str, workload: str = "config2", root: Path = None):
     """HBM bytes per dispatch of `kernel` on this workload from the committed rocprofv3
     --pmc FETCH_SIZE / WRITE_SIZE summaries (copy-calibrated read + write MiB), or None
-    when no summary covers this kernel."""
-    for md in sorted((Path(__file__).resolve().parent / "profiles").glob(f"*{workload}*.md")):
+    when no summary covers this kernel.  A row is used only if its scaled MiB follow
+    from its KiB columns and the summary's stated calibration factors."""
+    cal = re.compile(r"FETCH_SIZE is scaled by ([0-9]+\.[0-9]+) and WRITE_SIZE by ([0-9]+\.[0-9]+)")
+    root = Path(__file__).resolve().parent / "profiles" if root is None else Path(root)
+    for md in sorted(root.glob(f"*{workload}*.md")):
+        text = md.read_text()
+        m = cal.search(text)
+        if not m:
+            continue
+        fs, ws = float(m.group(1)), float(m.group(2))
         in_table = False
-        for line in md.read_text().splitlines():
+        for line in text.splitlines():
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
             if not line.startswith("|"):
                 in_table = False
             elif cells[-2:] == ["scaled read MiB", "scaled write MiB"]:
                 in_table = True
             elif in_table and cells[0] == kernel:
-                return int(round((float(cells[3]) + float(cells[4])) * 2**20))
+                fk, wk, rm, wm = (float(c) for c in cells[1:5])
+                if abs(fk * fs / 1024 - rm) > 0.1 or abs(wk * ws / 1024 - wm) > 0.1:
+                    return None  # inconsistent row: not evidence
+                return int(round((rm + wm) * 2**20))
     return None
 
 

@@ -1,0 +1,35 @@
+"""bench.py host logic that needs no GPU: reading profiled HBM traffic from the
+committed rocprofv3 summaries."""
+
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+
+TABLE = """Calibration: a 1 GiB device copy reads FETCH_SIZE = 524302 KiB and WRITE_SIZE = 1048576 KiB, so FETCH_SIZE is scaled by 2.000 and WRITE_SIZE by 1.000.
+
+| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled read MiB | scaled write MiB |
+|---|---|---|---|---|
+| good_kernel | 1024 | 512 | 2.0 | 0.5 |
+| bad_kernel | 6 | 4.2 | 4.1 | 4.7 |
+"""
+
+
+def test_profiled_traffic_uses_consistent_rows_only(tmp_path):
+    (tmp_path / "k_wlx.md").write_text(TABLE)
+    assert bench.profiled_traffic("good_kernel", "wlx", tmp_path) == int(round(2.5 * 2**20))
+    # a row whose scaled MiB do not follow from its KiB columns is not evidence
+    assert bench.profiled_traffic("bad_kernel", "wlx", tmp_path) is None
+    assert bench.profiled_traffic("missing", "wlx", tmp_path) is None
+    # no calibration statement: nothing is read
+    (tmp_path / "k_wly.md").write_text(TABLE.split("\n", 1)[1])
+    assert bench.profiled_traffic("good_kernel", "wly", tmp_path) is None
+
+
+def test_committed_config2_summary_is_consistent():
+    for k in ("encode_mfma_kernel<4, 4, false>", "kstats_mfma_kernel<4>", "kstats_finalize_kernel"):
+        assert bench.profiled_traffic(k, "config2") is not None, k
