@@ -32,7 +32,7 @@
  *       kvserve_v1/compression/compression_manager.py:200-537 (compress_all_layers and
  *       its chunked variant: transform -> KVServeQuantizer.quantize
  *       (quantizer/kvserve_quantizer.py:171-233) -> codec-buffer permute (:155-164)
- *       -> KVServeCodec.encode (codec/kvserve_codec.py:289-313)), fused with the
+ *       -> KVServeCodec.encode (codec/kvserve_codec.py:154-178)), fused with the
  *       gather of kv_utils.py:59-80
  *   kvmi_decode_paged
  *       kvserve_v1/compression/compression_manager.py:539-757 (decompress_all_layers

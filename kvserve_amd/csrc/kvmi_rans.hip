@@ -563,15 +563,19 @@ __global__ __launch_bounds__(kBlockThreads) void rans_decode_kernel(const DecBat
   const uint64_t in_bytes = bt.in_bytes[jb];
   const uint32_t nblk = (uint32_t)((n + kBlock - 1) / kBlock);
   const uint32_t* h = reinterpret_cast<const uint32_t*>(in);
-  const uint64_t payload = gld(reinterpret_cast<const uint64_t*>(in + 24));
   const uint64_t head = 32u + 8ull * nblk;
-  // every check below is uniform over the workgroup (it reads the same bytes)
-  if (gld(h) != kRansMagic || gld(h + 1) != (2u | ((uint32_t)W << 8) | (kPB << 16) | (8u << 24)) ||
-      gld(h + 2) != kBlock || gld(h + 3) != nblk || gld(reinterpret_cast<const uint64_t*>(in + 16)) != n ||
-      in_bytes < head + payload) {  // the stream (its header states the length) fits in the buffer
+  // Every check below is uniform over the workgroup (it reads the same bytes).  The
+  // buffer must hold the header and offset table before any of it is read, and the
+  // stated payload is compared with what is left of the buffer (never head + payload,
+  // which a payload near 2^64 would wrap).
+  if (in_bytes < head || gld(h) != kRansMagic ||
+      gld(h + 1) != (2u | ((uint32_t)W << 8) | (kPB << 16) | (8u << 24)) || gld(h + 2) != kBlock ||
+      gld(h + 3) != nblk || gld(reinterpret_cast<const uint64_t*>(in + 16)) != n ||
+      gld(reinterpret_cast<const uint64_t*>(in + 24)) > in_bytes - head) {
     if (t == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
     return;
   }
+  const uint64_t payload = gld(reinterpret_cast<const uint64_t*>(in + 24));
   const uint64_t* offs = reinterpret_cast<const uint64_t*>(in + 32);
   const uint64_t o = gld(offs + b);
   const uint64_t e = b + 1 == nblk ? payload : gld(offs + b + 1);

@@ -224,7 +224,8 @@ int oracle_rans_decode(const uint8_t* in, int64_t in_bytes, uint64_t n, int w, u
     uint32_t nblk = rd32(in + 12);
     if (rd32(in + 8) != BLOCK || rd64(in + 16) != n || nblk != (n + BLOCK - 1) / BLOCK) return -1;
     uint64_t head = 32u + 8u * (uint64_t)nblk, pay = rd64(in + 24);
-    if ((uint64_t)in_bytes < head + pay) return -1;  /* the stream may sit in a larger buffer */
+    /* the stream may sit in a larger buffer; compare without forming head + pay (wraps) */
+    if ((uint64_t)in_bytes < head || pay > (uint64_t)in_bytes - head) return -1;
     const uint8_t* payload = in + head;
     unsigned A = 1u << w;
     memset(out, 0, (size_t)((n * (uint64_t)w + 7u) / 8u));

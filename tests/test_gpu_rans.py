@@ -113,6 +113,13 @@ def test_damage_is_reported(cuda):
     assert torch.equal(ops.rans_decode(roomy, n, w), ops.rans_decode(st, n, w))
     with pytest.raises(RuntimeError, match="invalid bitpack header"):
         ops.rans_decode(st[:-4].clone(), n, w)
+    # a stated payload near 2^64 must not wrap the kernel's length check
+    bad = st.clone()
+    bad[24:32] = torch.from_numpy(np.frombuffer(np.uint64(2**64 - 8).tobytes(), np.uint8).copy()).to(cuda)
+    with pytest.raises(RuntimeError, match="invalid bitpack header"):
+        ops.rans_decode(bad, n, w)
+    with pytest.raises(RuntimeError, match="invalid bitpack header"):
+        ops.rans_decode(st[:head - 8].clone(), n, w)   # offset table cut short
 
 
 @pytest.mark.parametrize("w", [3, 4, 8])

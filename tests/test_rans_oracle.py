@@ -181,3 +181,10 @@ def test_corruption_and_contract_errors():
     # a receive buffer longer than the stream (its header states the length) decodes
     roomy = np.concatenate([st, np.full(100, 0xAB, np.uint8)])
     assert np.array_equal(crans.decode(roomy, s.size, 3), s)
+    # a stated payload near 2^64 must not wrap the length check (head + payload)
+    huge = st.copy()
+    huge[24:32] = np.frombuffer(np.uint64(2**64 - 8).tobytes(), np.uint8)
+    with pytest.raises(ValueError, match="-1"):
+        crans.decode(huge, s.size, 3)
+    with pytest.raises(ValueError, match="-1"):
+        crans.decode(st[:32 + 8 * nblk - 1], s.size, 3)  # offset table cut short
