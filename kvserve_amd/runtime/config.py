@@ -1,15 +1,20 @@
-"""Fixed-profile runtime configuration (kvserve_v1/compression/runtime/config.py:14-221).
+"""Fixed-profile runtime configuration: the ``kv_connector_extra_config`` contract of
+kvserve_v1/compression/runtime/config.py:14-221.
 
-Same fields, defaults, JSON keys (``enable-compression-pipeline``, ``raw_aggregate`` /
-``raw_agg``) and validation messages as the reference.  ``codec = "ans"`` selects this
-engine's GPU rANS codec (nvCOMP ANS is closed NVIDIA code).
+What peers depend on is kept as the reference has it: the dataclass fields and their
+defaults, the JSON keys (``compression`` / ``enable-compression-pipeline``,
+``raw_aggregate`` and its alias ``raw_agg``), the stage names and the error texts'
+substance.  The parsing is this module's own: the aggregate request and the compression
+object are each checked against a table of rules, and every rule carries the text of its
+error.  ``codec = "ans"`` names this engine's GPU rANS codec (nvCOMP's ANS is closed
+NVIDIA code).
 """
 
 from __future__ import annotations
 
 import logging
-from dataclasses import dataclass
-from typing import Any, Dict, Literal, Optional, Tuple
+from dataclasses import dataclass, fields
+from typing import Any, Callable, Dict, Literal, Optional, Tuple
 
 logger = logging.getLogger("kvserve_amd.runtime")
 
@@ -22,42 +27,85 @@ RAW_AGGREGATE_ALIAS = "raw_agg"
 RAW_AGGREGATE_SLOT_COUNT = 2
 RAW_AGGREGATE_LOGICAL_BLOCKS_PER_CHUNK = 160
 
-_raw_aggregate_warned = False
+ENABLE_KEY = "enable-compression-pipeline"
+CODED_STAGES = ("transformer", "quantizer", "codec")  # the only order they may appear in
+STAGES = frozenset(CODED_STAGES + ("aggregate",))
+AXES = ("channel", "token", "tensor")
+LEVEL_FIELDS = ("high_key_num_levels", "high_value_num_levels", "low_key_num_levels", "low_value_num_levels")
+
+# Several components parse the same extra config (memory plan, connector); each
+# warning below is logged once per process.
+_warned: set = set()
 
 
-def _parse_raw_aggregate(extra_config: Dict[str, Any]) -> Optional[Tuple[int, int]]:
-    """(slot_count, logical_blocks_per_chunk), or None when the key is absent or
-    disabled; ``raw_aggregate`` wins over ``raw_agg`` (config.py:28-62)."""
-    if RAW_AGGREGATE_KEY in extra_config:
-        raw = extra_config[RAW_AGGREGATE_KEY]
-    elif RAW_AGGREGATE_ALIAS in extra_config:
-        raw = extra_config[RAW_AGGREGATE_ALIAS]
-    else:
+def _warn_once(key: str, msg: str, *args) -> None:
+    if key not in _warned:
+        _warned.add(key)
+        logger.warning(msg, *args)
+
+
+def _count(value: Any) -> bool:
+    """A positive int that is not a bool."""
+    return type(value) is int and value >= 1
+
+
+def _aggregate_request(extra: Dict[str, Any]) -> Optional[Tuple[int, int]]:
+    """(slot_count, logical_blocks_per_chunk) when the lossless aggregate transport is
+    requested, else None.  The canonical key shadows its alias; ``false`` / ``null``
+    mean "not requested" and ``true`` means "with the defaults"."""
+    key = next((k for k in (RAW_AGGREGATE_KEY, RAW_AGGREGATE_ALIAS) if k in extra), None)
+    value = extra[key] if key else None
+    if value is None or value is False:
         return None
-    if raw is None or raw is False:
-        return None
-    if raw is True:
-        raw = {}
-    if not isinstance(raw, dict):
+    params = {} if value is True else value
+    if not isinstance(params, dict):
         raise ValueError(f"{RAW_AGGREGATE_KEY} must be true or an object with "
                          f"{RAW_AGGREGATE_SLOT_COUNT}/{RAW_AGGREGATE_LOGICAL_BLOCKS_PER_CHUNK}")
-    unknown = set(raw) - {"slot_count", "logical_blocks_per_chunk"}
-    if unknown:
-        raise ValueError(f"Unknown {RAW_AGGREGATE_KEY} parameters: {sorted(unknown)}; "
+    defaults = {"slot_count": RAW_AGGREGATE_SLOT_COUNT,
+                "logical_blocks_per_chunk": RAW_AGGREGATE_LOGICAL_BLOCKS_PER_CHUNK}
+    extra_keys = sorted(set(params) - set(defaults))
+    if extra_keys:
+        raise ValueError(f"Unknown {RAW_AGGREGATE_KEY} parameters: {extra_keys}; "
                          "supported: slot_count, logical_blocks_per_chunk")
-    slot_count = int(raw.get("slot_count", RAW_AGGREGATE_SLOT_COUNT))
-    blocks = int(raw.get("logical_blocks_per_chunk", RAW_AGGREGATE_LOGICAL_BLOCKS_PER_CHUNK))
-    if slot_count < 1:
-        raise ValueError(f"{RAW_AGGREGATE_KEY}.slot_count must be >= 1")
-    if blocks < 1:
-        raise ValueError(f"{RAW_AGGREGATE_KEY}.logical_blocks_per_chunk must be >= 1")
-    return slot_count, blocks
+    got = {name: int(params.get(name, default)) for name, default in defaults.items()}
+    for name, value in got.items():
+        if value < 1:
+            raise ValueError(f"{RAW_AGGREGATE_KEY}.{name} must be >= 1")
+    return got["slot_count"], got["logical_blocks_per_chunk"]
+
+
+def _stage_order_ok(pipeline: Tuple[str, ...]) -> bool:
+    """Without the aggregate stage the coded stages keep transformer < quantizer < codec."""
+    if "aggregate" in pipeline:
+        return True
+    ranks = [CODED_STAGES.index(s) for s in pipeline]
+    return ranks == sorted(ranks)
+
+
+# (field, accepts(value), error text).  Checked in this order on an enabled
+# configuration; an error text may use {value}.
+_RULES: Tuple[Tuple[str, Callable[[Any], bool], str], ...] = (
+    ("transformer", lambda v: v == "hadamard", "KVServe compression only supports transformer='hadamard'."),
+    ("codec", lambda v: v == "ans", "KVServe compression only supports codec='ans'."),
+    ("slot_count", _count, "KVServe compression slot_count must be >= 1."),
+    ("logical_blocks_per_chunk", _count, "KVServe compression logical_blocks_per_chunk must be >= 1."),
+    ("pipeline", lambda v: set(v) <= STAGES,
+     "Unknown KVServe compression stages: {unknown}; supported stages: " + str(sorted(STAGES))),
+    ("pipeline", lambda v: len(set(v)) == len(v), "KVServe compression stages must be unique."),
+    ("pipeline", _stage_order_ok, "KVServe compression stages must follow transformer, quantizer, codec order."),
+    ("hybrid_ratio", lambda v: 0.0 <= v <= 1.0, "KVServe compression hybrid_ratio must be in [0, 1]."),
+    *((name, lambda v: type(v) is int and 2 <= v <= 256, f"KVServe compression {name} must be an integer in [2, 256].")
+      for name in LEVEL_FIELDS),
+    ("split_type", lambda v: v in ("head", "layer"), "Unsupported KVServe compression split_type: {value}"),
+    ("axis_key", lambda v: v in AXES, "Unsupported KVServe key quantization axis: {value}"),
+    ("axis_value", lambda v: v in AXES, "Unsupported KVServe value quantization axis: {value}"),
+)
 
 
 @dataclass(frozen=True)
 class CompressionConfig:
-    enabled: bool = False
-    transport: Transport = "compression"
+    enabled: bool = False  # JSON key: enable-compression-pipeline
+    transport: Transport = "compression"  # "raw" only for a disabled configuration
     transformer: Literal["hadamard"] = "hadamard"
     seed: int = 3237919422
     split_type: SplitType = "layer"
@@ -72,7 +120,7 @@ class CompressionConfig:
     codec: Literal["ans"] = "ans"
     slot_count: int = 2
     logical_blocks_per_chunk: int = 1
-    pipeline: Tuple[str, ...] = ("transformer", "quantizer", "codec")
+    pipeline: Tuple[str, ...] = CODED_STAGES
 
     @property
     def available(self) -> bool:
@@ -86,72 +134,55 @@ class CompressionConfig:
     def uses_aggregate(self) -> bool:
         return "aggregate" in self.pipeline
 
+    def _uses(self, stage: str) -> bool:
+        # the aggregate stage replaces every coded stage
+        return stage in self.pipeline and not self.uses_aggregate
+
     @property
     def uses_transformer(self) -> bool:
-        return not self.uses_aggregate and "transformer" in self.pipeline
+        return self._uses("transformer")
 
     @property
     def uses_quantizer(self) -> bool:
-        return not self.uses_aggregate and "quantizer" in self.pipeline
+        return self._uses("quantizer")
 
     @property
     def uses_codec(self) -> bool:
-        return not self.uses_aggregate and "codec" in self.pipeline
+        return self._uses("codec")
+
+    def _validate(self) -> None:
+        for name, accepts, text in _RULES:
+            value = getattr(self, name)
+            if not accepts(value):
+                unknown = sorted(set(value) - STAGES) if name == "pipeline" else None
+                raise ValueError(text.format(value=value, unknown=unknown))
+        if self.uses_aggregate and len(self.pipeline) > 1:
+            _warn_once("aggregate-stage", "The aggregate stage takes precedence over other compression "
+                       "stages; configure raw_aggregate for the preferred spelling.")
 
     @classmethod
-    def from_extra_config(cls, extra_config: Dict[str, Any]) -> "CompressionConfig":
-        """Parse ``kv_connector_extra_config`` (config.py:110-221)."""
-        global _raw_aggregate_warned
-        extra_config = extra_config or {}
-        agg = _parse_raw_aggregate(extra_config)
-        if agg is not None:
-            compression = extra_config.get("compression") or {}
-            if compression.get("enable-compression-pipeline", False) and not _raw_aggregate_warned:
-                _raw_aggregate_warned = True
-                logger.warning("raw_aggregate transport selected; ignoring compression parameters: %s",
-                               ", ".join(sorted(str(k) for k in compression)))
-            return cls(enabled=True, transport="raw_aggregate", pipeline=("aggregate",), slot_count=agg[0],
-                       logical_blocks_per_chunk=agg[1])
-        raw = extra_config.get("compression", {}) or {}
-        if not raw.get("enable-compression-pipeline", False):
-            return cls(enabled=False, transport="raw")
-        normalized = dict(raw)
-        normalized.pop("enable-compression-pipeline")
-        if "pipeline" in normalized:
-            normalized["pipeline"] = tuple(normalized["pipeline"])
-        config = cls(enabled=True, transport="compression", **normalized)
-        if config.transformer != "hadamard":
-            raise ValueError("Mooncake compression only supports transformer='hadamard'.")
-        if config.codec != "ans":
-            raise ValueError("Mooncake compression only supports codec='ans'.")
-        if type(config.slot_count) is not int or config.slot_count < 1:
-            raise ValueError("Mooncake compression slot_count must be >= 1.")
-        if type(config.logical_blocks_per_chunk) is not int or config.logical_blocks_per_chunk < 1:
-            raise ValueError("Mooncake compression logical_blocks_per_chunk must be >= 1.")
-        supported = {"aggregate", "transformer", "quantizer", "codec"}
-        unknown = set(config.pipeline) - supported
-        if unknown:
-            raise ValueError(f"Unknown Mooncake compression stages: {sorted(unknown)}; "
-                             f"supported stages: {sorted(supported)}")
-        if len(set(config.pipeline)) != len(config.pipeline):
-            raise ValueError("Mooncake compression stages must be unique.")
-        if "aggregate" not in config.pipeline:
-            ordered = tuple(s for s in ("transformer", "quantizer", "codec") if s in config.pipeline)
-            if config.pipeline != ordered:
-                raise ValueError("Mooncake compression stages must follow transformer, quantizer, codec order.")
-        if "aggregate" in config.pipeline and len(config.pipeline) > 1:
-            logger.warning("The aggregate stage takes precedence over other compression stages; "
-                           "configure raw_aggregate for the preferred spelling.")
-        if not 0.0 <= config.hybrid_ratio <= 1.0:
-            raise ValueError("Mooncake compression hybrid_ratio must be in [0, 1].")
-        for name in ("high_key_num_levels", "high_value_num_levels", "low_key_num_levels", "low_value_num_levels"):
-            levels = getattr(config, name)
-            if type(levels) is not int or not 2 <= levels <= 256:
-                raise ValueError(f"Mooncake compression {name} must be an integer in [2, 256].")
-        if config.split_type not in ("head", "layer"):
-            raise ValueError(f"Unsupported Mooncake compression split_type: {config.split_type}")
-        if config.axis_key not in ("channel", "token", "tensor"):
-            raise ValueError(f"Unsupported Mooncake key quantization axis: {config.axis_key}")
-        if config.axis_value not in ("channel", "token", "tensor"):
-            raise ValueError(f"Unsupported Mooncake value quantization axis: {config.axis_value}")
+    def from_extra_config(cls, extra_config: Optional[Dict[str, Any]]) -> "CompressionConfig":
+        """Parse ``kv_connector_extra_config``: the aggregate transport when requested
+        (any compression object is then ignored, with a warning), else the compression
+        object when enabled, else the raw transport."""
+        extra = extra_config or {}
+        compression = extra.get("compression") or {}
+        aggregate = _aggregate_request(extra)
+        if aggregate is not None:
+            if compression.get(ENABLE_KEY, False):
+                _warn_once("aggregate-shadows", "raw_aggregate transport selected; ignoring compression "
+                           "parameters: %s", ", ".join(sorted(map(str, compression))))
+            return cls(enabled=True, transport="raw_aggregate", pipeline=("aggregate",),
+                       slot_count=aggregate[0], logical_blocks_per_chunk=aggregate[1])
+        if not compression.get(ENABLE_KEY, False):
+            return cls(enabled=False, transport="raw")  # the rest of the object is ignored
+        params = {k: v for k, v in compression.items() if k != ENABLE_KEY}
+        known = {f.name for f in fields(cls)}
+        stray = sorted(set(params) - known)
+        if stray:
+            raise TypeError(f"unknown compression parameters: {stray}")
+        if "pipeline" in params:
+            params["pipeline"] = tuple(params["pipeline"])
+        config = cls(enabled=True, transport="compression", **params)
+        config._validate()
         return config

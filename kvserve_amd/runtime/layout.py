@@ -1,18 +1,31 @@
 """Arena layout of the fixed-profile runtime (kvserve_v1/compression/runtime/layout.py:16-285).
 
-The offsets are the reference's: per KV part, every layer's packed rows at a
-``u8_offset`` sized for the full chunk capacity; per quantization section, a min and a
-scale array at 256-byte aligned ``aux`` offsets (channel axis: [heads, head_size];
-token axis: one per token; tensor axis: one), the aux arena holding these in its first
-half and the maxima / inverses at the same offsets in its second half.  Callers and
-peers address the arenas through these numbers, so they are kept identical.
+Peers address a slot's arenas by these offsets, so the numbers are the reference's;
+the builder below derives them from the layout rules, stated here:
+
+* Chunk capacity: ``C = logical_blocks_per_chunk`` blocks of ``block_size`` tokens.  A
+  (layer, part) of ``h`` heads of size ``d`` holds ``n = C * block_size * h * d``
+  elements (``2n`` raw bf16 bytes).
+* Arena A holds two raw scratch regions of ``scratch_stride`` bytes each (the largest
+  ``2n`` over layers and both head sizes, 256-aligned) that successive layers reuse.
+* Arena B: the packed u8 stream starts at ``u8_base = 2 * scratch_stride``; within it
+  each part (K = 0, V = 1) lays its layers out back to back in layer order, ``n`` bytes
+  each (``u8_offset``), so the K and V streams are two independent sequences.
+* Aux arena, per part: layers in order, and within a layer its quantization sections
+  (low heads, then high heads; an empty group has no section).  A section stores a min
+  table and then a scale table, each starting on a 256-byte boundary and holding one
+  bf16 per statistic: ``h_s * d`` on the channel axis, ``C * block_size`` on the token
+  axis, one on the tensor axis.  The maxima / inverse scales of the same sections sit at
+  the same offsets in the second half of the aux arena (``aux_arena_bytes`` is twice the
+  larger part).
+* Layer split: the last ``round(0.33 * num_model_layers)`` layers are all-low, the
+  others all-high; head split: the selection's low count per layer.
 """
 
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from math import prod
-from typing import Dict, FrozenSet, Literal, Optional, Tuple
+from typing import Dict, FrozenSet, List, Literal, Optional, Tuple
 
 import torch
 
@@ -48,6 +61,11 @@ class LayerPartLayout:
     u8_offset: int
     sections: Tuple[QuantSection, ...]
 
+    @property
+    def token_bytes(self) -> int:
+        """Raw bf16 bytes of one token of this (layer, part)."""
+        return self.num_heads * self.head_size * 2
+
 
 @dataclass(frozen=True)
 class CompressionLayout:
@@ -69,98 +87,106 @@ class CompressionLayout:
 
     @property
     def raw_tail_capacity(self) -> int:
-        """bf16 bytes of at most block_size - 1 tokens per layer of the larger part."""
+        """Bytes for the partial last block (at most block_size - 1 tokens) of every
+        layer of the larger part; the aggregate transport sends whole blocks only."""
         if self.aggregate:
             return 0
-        return round_up(max(sum((p.block_size - 1) * p.num_heads * p.head_size * 2 for p in self.parts(k))
-                            for k in (0, 1)), ALIGNMENT)
+        per_part = [sum((p.block_size - 1) * p.token_bytes for p in self.parts(k)) for k in (0, 1)]
+        return round_up(max(per_part), ALIGNMENT)
 
     def raw_tail_bytes(self, kv_part: KVPart, tokens: Dict[int, int]) -> int:
-        return sum((tokens[p.group_index] % p.block_size) * p.num_heads * p.head_size * 2
-                   for p in self.parts(kv_part))
+        return sum((tokens[p.group_index] % p.block_size) * p.token_bytes for p in self.parts(kv_part))
 
     def has_body(self, tokens: Dict[int, int]) -> bool:
         return any(tokens[p.group_index] >= p.block_size for p in self.parts(0))
 
 
-def _reduction_shape(axis: str, shape: Tuple[int, int, int, int]) -> Tuple[int, ...]:
-    blocks, tokens, heads, head_size = shape
-    if axis == "channel":
-        return (1, 1, heads, head_size)
-    if axis == "token":
-        return (blocks, tokens, 1, 1)
-    return (1, 1, 1, 1)
+def _stat_count(axis: str, tokens: int, heads: int, head_size: int) -> int:
+    """Statistics (bf16 each) one section stores per table."""
+    return {"channel": heads * head_size, "token": tokens}.get(axis, 1)
 
 
-def _split_counts(config: CompressionConfig, layer_index: int, num_heads: int, low_head_counts: Dict[int, int],
-                  num_model_layers: int) -> Tuple[int, int]:
-    """(low heads, high heads): head split from the selection; layer split makes the
-    last round(0.33 L) layers low (layout.py:110-124)."""
+class _Cursor:
+    """Bump allocator over one part's aux half: 256-aligned tables."""
+
+    def __init__(self):
+        self.end = 0
+
+    def table(self, nbytes: int) -> int:
+        start = round_up(self.end, ALIGNMENT)
+        self.end = start + nbytes
+        return start
+
+
+def _check_specs(ordered: List[Tuple[str, CacheSpec]], config: CompressionConfig) -> None:
+    if not ordered:
+        raise ValueError("KVServe compression requires FullAttention KV caches")
+    if len({s.block_size for _, s in ordered}) > 1:
+        raise ValueError("KVServe compression requires a common logical block size across FullAttention "
+                         "cache groups.")
+    for name, s in ordered:
+        sizes = (s.head_size, s.head_size_v)
+        if config.uses_transformer and not all(d >= 1 and d & (d - 1) == 0 for d in sizes):
+            raise ValueError("Hadamard compression requires power-of-two head sizes")
+        if s.dtype is not torch.bfloat16:
+            raise ValueError(f"KVServe compression currently supports only BF16 KV caches; layer {name} uses "
+                             f"{s.dtype}.")
+
+
+def _low_heads(config: CompressionConfig, layer: int, heads: int, low_head_counts: Dict[int, int],
+               num_model_layers: int) -> int:
     if config.split_type == "head":
-        low = low_head_counts[layer_index]
-        return low, num_heads - low
-    n_low = round(num_model_layers * 0.33)
-    is_low = n_low > 0 and layer_index >= num_model_layers - n_low
-    return (num_heads, 0) if is_low else (0, num_heads)
+        return low_head_counts[layer]
+    n_low_layers = round(num_model_layers * 0.33)
+    return heads if n_low_layers and layer >= num_model_layers - n_low_layers else 0
 
 
 def build_compression_layout(specs: Dict[str, CacheSpec], config: CompressionConfig,
                              low_head_counts: Dict[int, int], num_model_layers: int,
                              group_indices: Optional[Dict[str, int]] = None) -> CompressionLayout:
-    group_indices = group_indices or {}
-    items = sorted(specs.items(), key=lambda kv: kv[1].layer_index)
-    if not items:
-        raise ValueError("Mooncake compression requires FullAttention KV caches")
-    if len({s.block_size for _, s in items}) != 1:
-        raise ValueError("Mooncake compression requires a common logical block size across FullAttention "
-                         "cache groups.")
-    for name, spec in items:
-        if config.uses_transformer and any(sz < 1 or sz & (sz - 1) for sz in (spec.head_size, spec.head_size_v)):
-            raise ValueError("Hadamard compression requires power-of-two head sizes")
-        if spec.dtype is not torch.bfloat16:
-            raise ValueError(f"Mooncake compression currently supports only BF16 KV caches; layer {name} uses "
-                             f"{spec.dtype}.")
-    cb = config.logical_blocks_per_chunk
-    scratch_stride = round_up(max(cb * s.block_size * s.num_kv_heads * hs * 2 for _, s in items
-                                  for hs in (s.head_size, s.head_size_v)), ALIGNMENT)
-    u8_base = round_up(2 * scratch_stride, ALIGNMENT)
-    raw_off, u8_off, aux_off = [0, 0], [0, 0], [0, 0]
-    parts, groups = [], set()
-    for name, spec in items:
-        li = spec.layer_index
-        gi = group_indices.get(name, 0)
-        groups.add(gi)
-        low, high = _split_counts(config, li, spec.num_kv_heads, low_head_counts, num_model_layers)
-        for kv, hs, axis, lo_lv, hi_lv in ((0, spec.head_size, config.axis_key, config.low_key_num_levels,
-                                             config.high_key_num_levels),
-                                            (1, spec.head_size_v, config.axis_value, config.low_value_num_levels,
-                                             config.high_value_num_levels)):
-            numel = cb * spec.block_size * spec.num_kv_heads * hs
-            sections, start = [], 0
-            for count, levels in ((low, lo_lv), (high, hi_lv)):
-                if count == 0:
-                    continue
-                nbytes = prod(_reduction_shape(axis, (cb, spec.block_size, count, hs))) * 2
-                mo = round_up(aux_off[kv], ALIGNMENT)
-                so = round_up(mo + nbytes, ALIGNMENT)
-                aux_off[kv] = so + nbytes
-                sections.append(QuantSection(start, count, levels, axis, mo, so))
-                start += count
-            parts.append(LayerPartLayout(name, li, kv, gi, spec.block_size, spec.num_kv_heads, hs, spec.dtype, 0,
-                                         numel * 2, u8_off[kv], tuple(sections)))
-            raw_off[kv] += numel * 2
-            u8_off[kv] += numel
-    raw_by = (raw_off[0], raw_off[1])
-    u8_by = (u8_off[0], u8_off[1])
-    aux_by = (round_up(aux_off[0], ALIGNMENT), round_up(aux_off[1], ALIGNMENT))
-    aggregate = "aggregate" in config.pipeline
-    quant = "quantizer" in config.pipeline and not aggregate
-    packed_by = u8_by if quant else raw_by
-    arena = (round_up(max(*raw_by), ALIGNMENT) if aggregate
-             else round_up(max(2 * scratch_stride, u8_base + max(*packed_by)), ALIGNMENT))
-    return CompressionLayout(layer_parts=tuple(parts), raw_bytes_by_part=raw_by, u8_bytes_by_part=u8_by,
-                             packed_bytes_by_part=packed_by, aux_bytes_by_part=aux_by, arena_bytes=arena,
-                             scratch_stride=scratch_stride, u8_base=u8_base,
-                             aux_arena_bytes=0 if (aggregate or not quant) else 2 * max(aux_by),
-                             fa_group_indices=frozenset(groups),
-                             index_rows_by_group={g: r for r, g in enumerate(sorted(groups))}, aggregate=aggregate)
+    ordered = sorted(specs.items(), key=lambda item: item[1].layer_index)
+    _check_specs(ordered, config)
+    groups = {name: (group_indices or {}).get(name, 0) for name, _ in ordered}
+    chunk_tokens = config.logical_blocks_per_chunk * ordered[0][1].block_size
+    # per part: (head size, quantization axis, (low levels, high levels))
+    part_rules = ((lambda s: s.head_size, config.axis_key, (config.low_key_num_levels, config.high_key_num_levels)),
+                  (lambda s: s.head_size_v, config.axis_value,
+                   (config.low_value_num_levels, config.high_value_num_levels)))
+
+    per_part: List[List[LayerPartLayout]] = [[], []]
+    raw_total, u8_total, aux_end = [0, 0], [0, 0], [0, 0]
+    for kv, (head_size_of, axis, levels) in enumerate(part_rules):
+        cursor, u8_at = _Cursor(), 0
+        for name, s in ordered:
+            d = head_size_of(s)
+            elems = chunk_tokens * s.num_kv_heads * d
+            low = _low_heads(config, s.layer_index, s.num_kv_heads, low_head_counts, num_model_layers)
+            sections, first = [], 0
+            for count, lv in zip((low, s.num_kv_heads - low), levels):
+                if count:
+                    nbytes = 2 * _stat_count(axis, chunk_tokens, count, d)
+                    mn = cursor.table(nbytes)
+                    sections.append(QuantSection(first, count, lv, axis, mn, cursor.table(nbytes)))
+                    first += count
+            per_part[kv].append(LayerPartLayout(name, s.layer_index, kv, groups[name], s.block_size, s.num_kv_heads,
+                                                d, s.dtype, 0, 2 * elems, u8_at, tuple(sections)))
+            u8_at += elems
+        raw_total[kv], u8_total[kv], aux_end[kv] = 2 * u8_at, u8_at, round_up(cursor.end, ALIGNMENT)
+
+    scratch_stride = round_up(max(chunk_tokens * s.num_kv_heads * d * 2 for _, s in ordered
+                                  for d in (s.head_size, s.head_size_v)), ALIGNMENT)
+    u8_base = 2 * scratch_stride
+    aggregate = config.uses_aggregate
+    quantized = config.uses_quantizer
+    packed = u8_total if quantized else raw_total
+    if aggregate:
+        arena = round_up(max(raw_total), ALIGNMENT)
+    else:
+        arena = round_up(max(2 * scratch_stride, u8_base + max(packed)), ALIGNMENT)
+    group_ids = sorted(set(groups.values()))
+    return CompressionLayout(
+        layer_parts=tuple(p for pair in zip(*per_part) for p in pair),  # layer order, K before V
+        raw_bytes_by_part=tuple(raw_total), u8_bytes_by_part=tuple(u8_total), packed_bytes_by_part=tuple(packed),
+        aux_bytes_by_part=tuple(aux_end), arena_bytes=arena, scratch_stride=scratch_stride, u8_base=u8_base,
+        aux_arena_bytes=2 * max(aux_end) if quantized else 0, fa_group_indices=frozenset(group_ids),
+        index_rows_by_group={g: row for row, g in enumerate(group_ids)}, aggregate=aggregate)

@@ -102,7 +102,7 @@ class CompressionPipeline:
         if kv_cache_layout == "LBHNC":
             kv_cache_layout = "HND"
         if kv_cache_layout != "HND":
-            raise ValueError("Mooncake compression requires LBHNC/HND KV cache layout.")
+            raise ValueError("KVServe compression requires LBHNC/HND KV cache layout.")
         self.layout = layout
         self.kv_cache_layout = kv_cache_layout
         self.blocks_per_logical = blocks_per_logical

@@ -1,10 +1,18 @@
-"""Head selection of the fixed-profile runtime (kvserve_v1/compression/runtime/scores.py:16-112).
+"""Head selection of the fixed-profile runtime: which KV heads of each bound layer take
+the low-precision levels (kvserve_v1/compression/runtime/scores.py:16-112).
 
-The low-precision heads are the lowest ``round(candidates * hybrid_ratio)`` scores
-over all (layer, head) pairs of the bound layers (stable order); each layer's heads
-are reordered [low ascending, high ascending].  Score tables wider than the local
-heads are sliced by tensor-parallel rank, and a score column is shared by replicated
-KV heads.
+The rule, which peers must reproduce exactly because it fixes the head order on the
+wire:
+
+* ``split_type = "layer"``: no head is low here (the layer split is applied by the
+  layout) and every layer keeps its natural head order.
+* ``split_type = "head"``: the score table has one row per model layer and one column
+  per KV head of the whole model (or of this rank).  The candidates are the full rows of
+  the bound layers, taken in binding order; the ``round(candidates * hybrid_ratio)``
+  lowest scores (ties broken by candidate order) are low.  Each rank then looks at its
+  own window of a row -- the whole row, its tensor-parallel slice, or the one column it
+  shares with other ranks when KV heads are replicated -- and orders its heads
+  [low ascending, high ascending].
 """
 
 from __future__ import annotations
@@ -12,7 +20,7 @@ from __future__ import annotations
 import json
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Dict, Optional, Tuple
+from typing import Callable, Dict, Optional, Tuple
 
 import numpy as np
 import torch
@@ -27,67 +35,82 @@ class HeadSelection:
     local_orders: Dict[int, Tuple[int, ...]]
 
 
+def _scores_from_torch(path: Path) -> np.ndarray:
+    obj = torch.load(path, map_location="cpu", weights_only=True)  # tensors only, nothing executed
+    if isinstance(obj, dict):
+        obj = obj.get("scores", obj.get("head_scores"))
+    return obj.float().numpy()
+
+
+def _scores_from_text(path: Path) -> np.ndarray:
+    table = np.genfromtxt(path, delimiter=",", dtype=np.float32)
+    if table.ndim == 2:  # drop rows and columns that hold no number (headers, trailing commas)
+        table = table[~np.isnan(table).all(axis=1)]
+        table = table[:, ~np.isnan(table).all(axis=0)]
+    return table
+
+
+_LOADERS: Dict[str, Callable[[Path], np.ndarray]] = {
+    ".npy": lambda p: np.load(p, allow_pickle=False),
+    ".pt": _scores_from_torch,
+    ".pth": _scores_from_torch,
+    ".json": lambda p: np.asarray(json.loads(p.read_text()), dtype=np.float32),
+}
+
+
 def load_scores(path: str) -> np.ndarray:
-    """.npy (no pickles), .pt / .pth (weights only), .json, or CSV."""
+    """A score table from .npy (no pickles), .pt / .pth (weights only; a tensor or a dict
+    with "scores" / "head_scores"), .json, or comma-separated text (any other suffix)."""
     p = Path(path)
-    suffix = p.suffix.lower()
-    if suffix == ".npy":
-        values = np.load(p, allow_pickle=False)
-    elif suffix in (".pt", ".pth"):
-        loaded = torch.load(p, map_location="cpu", weights_only=True)
-        if isinstance(loaded, dict):
-            loaded = loaded.get("scores", loaded.get("head_scores"))
-        values = loaded.float().numpy()
-    elif suffix == ".json":
-        values = np.asarray(json.loads(p.read_text()), dtype=np.float32)
-    else:
-        values = np.genfromtxt(p, delimiter=",", dtype=np.float32)
-        if values.ndim == 2:
-            values = values[~np.all(np.isnan(values), axis=1)]
-            values = values[:, ~np.all(np.isnan(values), axis=0)]
-    return np.asarray(values, dtype=np.float32)
+    return np.asarray(_LOADERS.get(p.suffix.lower(), _scores_from_text)(p), dtype=np.float32)
+
+
+def _window_start(width: int, local: int, tp_rank: int, tp_size: int) -> int:
+    """First score column of this rank's heads in a row of `width` columns."""
+    if width == local:                        # the table already holds this rank's heads
+        return 0
+    if width == local * tp_size:              # the model's heads, sliced by rank
+        return tp_rank * local
+    replicas = tp_size // width if 0 < width < tp_size else 0
+    if local == 1 and replicas and width * replicas == tp_size:
+        return tp_rank // replicas            # one KV head shared by `replicas` ranks
+    raise ValueError(f"Head score width {width} is incompatible with {local} local KV heads and "
+                     f"TP size {tp_size}.")
+
+
+def _low_mask(scores: np.ndarray, rows: list, ratio: float) -> np.ndarray:
+    """Boolean table shaped like `scores`: True where a candidate is among the lowest."""
+    mask = np.zeros(scores.shape, dtype=bool)
+    cand = scores[rows]                        # candidate rows in binding order (repeats allowed)
+    n_low = round(cand.size * ratio)
+    if n_low:
+        flat = np.argsort(cand.reshape(-1), kind="stable")[:n_low]
+        r, c = np.divmod(flat, scores.shape[1])
+        mask[np.asarray(rows)[r], c] = True
+    return mask
 
 
 def build_head_selection(specs: Dict[str, CacheSpec], config: CompressionConfig, tp_rank: int, tp_size: int,
                          scores: Optional[np.ndarray] = None) -> HeadSelection:
-    items = list(specs.items())
+    bound = list(specs.values())
     if config.split_type == "layer":
-        return HeadSelection(low_counts={s.layer_index: 0 for _, s in items},
-                             local_orders={s.layer_index: tuple(range(s.num_kv_heads)) for _, s in items})
+        return HeadSelection(low_counts={s.layer_index: 0 for s in bound},
+                             local_orders={s.layer_index: tuple(range(s.num_kv_heads)) for s in bound})
     if scores is None:
         if not config.score_path:
             raise ValueError("Head split requires a score_path or head scores.")
         scores = load_scores(config.score_path)
     if scores.ndim != 2 or not np.isfinite(scores).all():
         raise ValueError("Head scores must be a finite 2D array of layers and KV heads.")
-    rows, width = scores.shape
-    candidates = []
-    for _, spec in items:
-        li = spec.layer_index
-        if not 0 <= li < rows:
-            raise ValueError(f"Head scores have no row for layer {li}.")
-        candidates.extend(range(li * width, (li + 1) * width))
-    cand = np.asarray(candidates, dtype=np.int64)
-    mask = np.zeros(scores.size, dtype=bool)
-    n_low = round(cand.size * config.hybrid_ratio)
-    if n_low:
-        picked = np.argsort(scores.reshape(-1)[cand], kind="stable")[:n_low]
-        mask[cand[picked]] = True
-    mask = mask.reshape(scores.shape)
+    missing = next((s.layer_index for s in bound if not 0 <= s.layer_index < scores.shape[0]), None)
+    if missing is not None:
+        raise ValueError(f"Head scores have no row for layer {missing}.")
+    mask = _low_mask(scores, [s.layer_index for s in bound], config.hybrid_ratio)
     low_counts, orders = {}, {}
-    for _, spec in items:
-        li, local = spec.layer_index, spec.num_kv_heads
-        if width == local:
-            start = 0
-        elif width == local * tp_size:
-            start = tp_rank * local
-        elif local == 1 and 0 < width < tp_size and tp_size % width == 0:
-            start = tp_rank // (tp_size // width)
-        else:
-            raise ValueError(f"Head score width {width} is incompatible with {local} local KV heads and "
-                             f"TP size {tp_size}.")
-        row = mask[li, start:start + local]
-        low, high = np.flatnonzero(row).tolist(), np.flatnonzero(~row).tolist()
-        low_counts[li] = len(low)
-        orders[li] = tuple(low + high)
+    for s in bound:
+        start = _window_start(scores.shape[1], s.num_kv_heads, tp_rank, tp_size)
+        is_low = mask[s.layer_index, start:start + s.num_kv_heads]
+        heads = np.arange(s.num_kv_heads)
+        low_counts[s.layer_index] = int(is_low.sum())
+        orders[s.layer_index] = tuple(int(h) for h in np.concatenate([heads[is_low], heads[~is_low]]))
     return HeadSelection(low_counts=low_counts, local_orders=orders)

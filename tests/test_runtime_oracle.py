@@ -8,6 +8,7 @@ quantizer formulas (tests/runtime/test_gpu.py:412-535, test_hadamard.py:14-23).
 
 from __future__ import annotations
 
+import json
 import numpy as np
 import pytest
 import torch
@@ -229,11 +230,11 @@ def test_signs_follow_the_fixture_generator_recipe():
     ({"logical_blocks_per_chunk": 0}, "logical_blocks_per_chunk must be >= 1"),
     ({"pipeline": ["quantizer", "transformer"]}, "must follow transformer, quantizer, codec order"),
     ({"pipeline": ["codec", "codec"]}, "must be unique"),
-    ({"pipeline": ["squeeze"]}, "Unknown Mooncake compression stages"),
+    ({"pipeline": ["squeeze"]}, "Unknown KVServe compression stages"),
     ({"hybrid_ratio": 1.5}, "hybrid_ratio must be in"),
     ({"high_key_num_levels": 1}, "must be an integer in"),
-    ({"split_type": "row"}, "Unsupported Mooncake compression split_type"),
-    ({"axis_key": "row"}, "Unsupported Mooncake key quantization axis"),
+    ({"split_type": "row"}, "Unsupported KVServe compression split_type"),
+    ({"axis_key": "row"}, "Unsupported KVServe key quantization axis"),
 ])
 def test_config_rejects_like_the_reference(bad, message):
     with pytest.raises(ValueError, match=message):
@@ -283,3 +284,62 @@ def test_head_selection_tp_slices_and_replicated_kv_heads():
     with pytest.raises(ValueError, match="finite 2D"):
         build_head_selection(one, config, 0, 1, np.array([[np.nan, 1.0]], dtype=np.float32))
 
+
+
+def test_layout_layer_split_and_arena_invariants():
+    """Layer split: of 10 layers the last round(3.3) = 3 are low.  Every aux table is
+    256-aligned, disjoint from the others and inside its part's aux bytes; the u8 stream
+    of each part is gap-free in layer order; K and V alternate per layer."""
+    config = CompressionConfig.from_extra_config({"compression": {"enable-compression-pipeline": True,
+                                                                  "axis_value": "tensor",
+                                                                  "logical_blocks_per_chunk": 2}})
+    specs = {f"m.{i}": CacheSpec(i, 16, 4, 64 if i % 2 else 128, torch.bfloat16, head_size_v=64) for i in range(10)}
+    layout = build_compression_layout(specs, config, {}, 10)
+    assert [p.kv_part for p in layout.layer_parts] == [0, 1] * 10
+    for kv in (0, 1):
+        parts = layout.parts(kv)
+        assert [p.layer_index for p in parts] == list(range(10))
+        assert [p.sections[0].num_levels for p in parts] == (
+            [config.high_key_num_levels] * 7 + [config.low_key_num_levels] * 3 if kv == 0
+            else [config.high_value_num_levels] * 7 + [config.low_value_num_levels] * 3)
+        at, tables = 0, []
+        for p in parts:
+            assert p.u8_offset == at and p.raw_bytes == 2 * 32 * 4 * p.head_size
+            at += 32 * 4 * p.head_size
+            (s,) = p.sections
+            n = 2 * (4 * p.head_size if s.axis == "channel" else 1)
+            tables += [(s.aux_min_offset, n), (s.aux_scale_offset, n)]
+        assert layout.u8_bytes_by_part[kv] == at
+        for (o, n), (o2, _) in zip(tables, tables[1:]):
+            assert o % 256 == 0 and o + n <= o2
+        assert tables[-1][0] + tables[-1][1] <= layout.aux_bytes_by_part[kv]
+    assert layout.aux_arena_bytes == 2 * max(layout.aux_bytes_by_part)
+    assert layout.scratch_stride == 2 * 32 * 4 * 128 and layout.u8_base == 2 * layout.scratch_stride
+    agg = build_compression_layout(specs, CompressionConfig.from_extra_config({"raw_agg": True}), {}, 10)
+    assert agg.aggregate and agg.aux_arena_bytes == 0 and agg.raw_tail_capacity == 0
+    assert agg.arena_bytes == max(agg.raw_bytes_by_part)
+
+
+def test_head_selection_ties_follow_binding_order():
+    """Equal scores: the earlier candidate (binding order, then column) is low first."""
+    config = CompressionConfig(enabled=True, split_type="head", hybrid_ratio=0.25)
+    scores = np.ones((3, 4), dtype=np.float32)
+    specs = {"b": CacheSpec(2, 16, 4, 8, torch.bfloat16), "a": CacheSpec(0, 16, 4, 8, torch.bfloat16)}
+    sel = build_head_selection(specs, config, 0, 1, scores)
+    assert sel.low_counts == {2: 2, 0: 0} and sel.local_orders[2] == (0, 1, 2, 3)
+    with pytest.raises(ValueError, match="no row for layer 5"):
+        build_head_selection({"x": CacheSpec(5, 16, 4, 8, torch.bfloat16)}, config, 0, 1, scores)
+
+
+def test_score_loaders_read_every_supported_format(tmp_path):
+    from kvserve_amd.runtime.scores import load_scores
+
+    table = np.array([[0.5, 2.0, 1.0], [3.0, 0.25, 4.0]], dtype=np.float32)
+    np.save(tmp_path / "s.npy", table)
+    torch.save({"head_scores": torch.from_numpy(table)}, tmp_path / "s.pt")
+    torch.save(torch.from_numpy(table), tmp_path / "s.pth")
+    (tmp_path / "s.json").write_text(json.dumps(table.tolist()))
+    (tmp_path / "s.csv").write_text("layer,h0,h1,h2\n" + "\n".join("," + ",".join(map(str, r)) for r in table.tolist()))
+    for name in ("s.npy", "s.pt", "s.pth", "s.json", "s.csv"):
+        got = load_scores(str(tmp_path / name))
+        assert got.dtype == np.float32 and np.array_equal(got, table), name
