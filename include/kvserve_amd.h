@@ -79,8 +79,10 @@ typedef struct ihipStream_t* kvmi_stream_t;
 /* Launch-wide geometry shared by every job of one call. */
 typedef struct kvmi_geometry {
   int32_t block_size; /* S: tokens per paged block (vLLM block_size) */
-  int32_t num_heads;  /* H: KV heads of this worker's shard */
-  int32_t head_dim;   /* D: 64, 128 or 256 */
+  int32_t num_heads;  /* H: KV heads of this worker's shard, 1..64 */
+  int32_t head_dim;   /* D: a multiple of 16 in [16, 256], with H * next_pow2(D) <= 8192; a D
+                         that is not a power of two is transformed in descending
+                         power-of-two chunks (hadamard_func.py:50-103) */
   int32_t bits;       /* bitpack width in [1, 8] */
   uint32_t flags;     /* KVMI_F_* */
   int32_t max_groups; /* G: V statistic groups per layer (<= H) */
@@ -109,7 +111,7 @@ typedef struct kvmi_layer_job {
   uint8_t* stream;           /* packed chunk stream this layer belongs to (16-byte aligned) */
   uint16_t* kmeta;
   uint16_t* vmeta;
-  const uint32_t* signs;     /* [H][D/32] Rademacher sign bits per source head (1 = -1) */
+  const uint32_t* signs;     /* [H][ceil(D/32)] Rademacher sign bits per source head (1 = -1) */
   const uint8_t* profile;
   uint32_t* kstats;
   uint32_t* counter;
@@ -160,10 +162,12 @@ int kvmi_scatter_blocks(void* pool, int64_t pool_part_stride, const int32_t* blo
 
 /*
  * Random-sign Hadamard transform of contiguous bf16 rows [rows, D], row r
- * belonging to head r % num_heads (hadamard_func.py:161-231).
- *   forward: out = bf16( FWHT_fp32(x * s) * (1/sqrt(D)) )
- *   inverse: out = bf16( FWHT_fp32(x) * (1/sqrt(D)) ) * s
- * signs: [num_heads][D/32] bits (1 = -1).  in and out may alias.
+ * belonging to head r % num_heads (hadamard_func.py:161-231), D a multiple of 16 in
+ * [16, 256].  Each power-of-two chunk c of D (descending, hadamard_func.py:50-103) is
+ * transformed on its own:
+ *   forward: out = bf16( FWHT_fp32(x * s) * (1/sqrt(c)) )
+ *   inverse: out = bf16( FWHT_fp32(x) * (1/sqrt(c)) ) * s
+ * signs: [num_heads][ceil(D/32)] bits (1 = -1).  in and out may alias.
  */
 int kvmi_hadamard(const void* in, void* out, int64_t rows, int32_t num_heads,
                   int32_t head_dim, const uint32_t* signs, int32_t inverse,

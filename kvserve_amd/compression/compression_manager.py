@@ -24,7 +24,7 @@ from typing import Any, Dict, List, Optional, Sequence
 
 import torch
 
-from ..engine import DEFAULT_SEED, FusedKVCodec, Packet, chunk_ranges, check_packet
+from ..engine import DEFAULT_SEED, FusedKVCodec, Packet, check_packet, chunk_ranges, supported_geometry
 from ._meta import layer_dict, tables_from_dicts
 from .codec import is_entropy_codec
 from .codec.rans_codec import unpack_target
@@ -293,7 +293,7 @@ class FusedCompressionManager(CompressionManager):
             return False
         if self.quantizer.axis_key != "channel" or self.quantizer.axis_value != "token":
             return False
-        return dtype == torch.bfloat16 and D in (64, 128) and 128 % H == 0 and H <= 16
+        return dtype == torch.bfloat16 and supported_geometry(H, D)
 
     def _codec(self, H, D, S) -> FusedKVCodec:
         transform, seed, has_codec, bits = self._settings()

@@ -1,10 +1,10 @@
 """Random-sign normalized FWHT (kvserve_v1/compression/transformer/hadamard_func.py:11-231).
 
-transform: y = bf16(FWHT_fp32(x * s) / sqrt(D));  inverse: x = bf16(FWHT_fp32(y) / sqrt(D)) * s,
-with Rademacher signs s from a CPU torch.Generator seeded base_seed ^ (layer << 16) ^ head
-(:33-48, :137-152).  The transform itself runs in the kvmi_hadamard kernel.
-head_dim must be 64 or 128 (the reference splits other sizes into power-of-two chunks,
-:50-103; those are not supported here).
+transform: y = bf16(FWHT_fp32(x * s) / sqrt(c));  inverse: x = bf16(FWHT_fp32(y) / sqrt(c)) * s,
+per power-of-two chunk c of head_dim (descending, :50-103; c = D for a power of two), with
+Rademacher signs s from a CPU torch.Generator seeded base_seed ^ (layer << 16) ^ head
+(:33-48, :137-152).  The transform itself runs in the kvmi_hadamard kernel; head_dim is a
+multiple of 16 up to 256.
 """
 
 from __future__ import annotations
@@ -28,7 +28,7 @@ class HadamardTransform:
         key = (layer_idx, num_heads, head_dim, str(device), dtype)
         if key not in self.signs_cache:
             b = rademacher_sign_bits(self.base_seed, layer_idx, num_heads, head_dim)
-            neg = ((b[:, :, None] >> torch.arange(32).numpy()) & 1).reshape(num_heads, head_dim)
+            neg = ((b[:, :, None] >> torch.arange(32).numpy()) & 1).reshape(num_heads, -1)[:, :head_dim]
             s = torch.from_numpy(1.0 - 2.0 * neg).to(device=device, dtype=dtype)
             self.signs_cache[key] = s.view(1, 1, num_heads, head_dim)
         return self.signs_cache[key]

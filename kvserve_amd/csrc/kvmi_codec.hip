@@ -1,4 +1,6 @@
-// Fused paged compress / decompress kernels for gfx950.
+// Fused paged compress / decompress kernels for gfx950, register FWHT, one quad of
+// lanes per row (D in {64, 128}, H dividing 128, H <= 16; other geometries run the
+// generic row kernels of kvmi_rows.hip, the transform profile mostly the MFMA kernels).
 //
 // Work unit: a workgroup of 512 threads (8 wave64s) owns a run of paged blocks of
 // one (request, layer) job.  The run's rows (one row = one token x one KV head =
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(kWG) void kstats_kernel(Geo g, const kvmi_layer_job
   const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
   const uint32_t sb = transform ? lane_signs<D>(job.signs, h, q) : 0u;
 
-  __shared__ uint32_t lkey[2 * kMaxHD];
+  __shared__ uint32_t lkey[2 * kMaxQuadHD];
   for (int i = tid; i < HD; i += kWG) {
     lkey[i] = 0xffffffffu;
     lkey[HD + i] = 0u;
@@ -133,8 +135,8 @@ __global__ __launch_bounds__(kWG) void kstats_finalize_kernel(Geo g, const kvmi_
   const kvmi_layer_job job = jobs[blockIdx.x];
   if (job.num_blocks <= 0) return;  // nothing accumulated: kmeta is left as it is
   const int H = g.H, D = g.D, HD = H * D;
-  __shared__ int pos[kMaxH];
-  __shared__ uint8_t lev[kMaxH];
+  __shared__ int pos[kMaxHeads];
+  __shared__ uint8_t lev[kMaxHeads];
   if (threadIdx.x < (unsigned)H) {
     const int k = threadIdx.x;
     pos[gld(job.profile + k)] = k;  // order[k] = source head at output position k
@@ -178,8 +180,8 @@ __global__ __launch_bounds__(kWG) void encode_kernel(Geo g, const kvmi_layer_job
   const Profile pk = part_profile(job.profile, 0, H);
   const Profile pv = part_profile(job.profile, 1, H);
 
-  __shared__ float2 kq[kMaxHD];     // (min, 1/scale) by source head and channel
-  __shared__ int posk[kMaxH], posv[kMaxH];
+  __shared__ float2 kq[kMaxQuadHD];     // (min, 1/scale) by source head and channel
+  __shared__ int posk[kMaxQuadH], posv[kMaxQuadH];
   __shared__ float2 rowmm[kRows];   // V row (min, max)
   __shared__ float2 tokq[kRows];    // V (min, 1/scale) by (token of pass, group)
   __shared__ int ngv;
@@ -300,8 +302,8 @@ __global__ __launch_bounds__(kWG) void decode_kernel(Geo g, const kvmi_layer_job
   const int H = g.H, S = g.S, HD = H * D, G = g.G;
   const int tid = threadIdx.x, Q = tid >> 2, q = tid & 3;
 
-  __shared__ float2 kd[kMaxHD];  // (min, scale) by source head and channel
-  __shared__ int posk[kMaxH], posv[kMaxH];
+  __shared__ float2 kd[kMaxQuadHD];  // (min, scale) by source head and channel
+  __shared__ int posk[kMaxQuadH], posv[kMaxQuadH];
   __shared__ int ok;
   const Profile pk = part_profile(job.profile, 0, H);
   const Profile pv = part_profile(job.profile, 1, H);
@@ -420,6 +422,9 @@ extern "C" int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (mfma_eligible(g)) {
     rc = mfma_kstats(g, jobs, num_jobs, max_blocks, err, st);
     if (rc) return rc;
+  } else if (!quad_eligible(g)) {
+    rc = rows_kstats(g, jobs, num_jobs, max_blocks, err, st);
+    if (rc) return rc;
   } else {
     // Statistics need only K: give each workgroup enough blocks that a job has at
     // most ~16 workgroups, which keeps the global atomics per channel small.
@@ -447,6 +452,7 @@ extern "C" int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (mfma_eligible(g)) return mfma_encode(g, jobs, num_jobs, max_blocks, err, st);
+  if (!quad_eligible(g)) return rows_encode(g, jobs, num_jobs, max_blocks, err, st);
   set_valu_bpw(&g);
   dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   if (g.D == 64) {
@@ -467,6 +473,7 @@ extern "C" int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (mfma_eligible(g)) return mfma_decode(g, jobs, num_jobs, max_blocks, err, st);
+  if (!quad_eligible(g)) return rows_decode(g, jobs, num_jobs, max_blocks, err, st);
   set_valu_bpw(&g);
   dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   if (g.D == 64) {

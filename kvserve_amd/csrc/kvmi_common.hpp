@@ -6,8 +6,16 @@
 
 namespace kvmi {
 
-constexpr int kMaxH = 16;  // heads per worker shard supported by the LDS tables
-constexpr int kMaxHD = kMaxH * 128;
+constexpr int kMaxHeads = 64;     // heads per worker shard (profile and finalize tables)
+constexpr int kMaxRowSlots = 8192; // H * next_pow2(D): the generic row kernels' pass holds a whole token
+constexpr int kMaxQuadH = 16;     // heads of the quad-per-row kernels' LDS tables
+constexpr int kMaxQuadHD = kMaxQuadH * 128;
+
+__host__ __device__ constexpr int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
 
 // Launch geometry (kernel argument).
 struct Geo {
@@ -94,8 +102,8 @@ __device__ __forceinline__ void write_stream_header(uint8_t* out, int bits, int6
 inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_blocks, Geo* out) {
   if (!geom || num_jobs < 0 || max_blocks < 0) return KVMI_EINVAL;
   const int S = geom->block_size, H = geom->num_heads, D = geom->head_dim, bits = geom->bits;
-  if (S < 1 || H < 1 || H > kMaxH || (128 % H) != 0) return KVMI_EINVAL;
-  if (D != 64 && D != 128) return KVMI_EINVAL;
+  if (S < 1 || H < 1 || H > kMaxHeads) return KVMI_EINVAL;
+  if (D < 16 || D > 256 || D % 16 || H * next_pow2(D) > kMaxRowSlots) return KVMI_EINVAL;
   if (bits < 1 || bits > 8) return KVMI_EINVAL;
   if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
   if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
@@ -113,12 +121,30 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
   return KVMI_OK;
 }
 
-// MFMA variants (kvmi_mfma.hip).  They serve the transform profile for geometries
-// with H dividing 8 and S*H a multiple of 32, unless the caller forces the register
-// FWHT (KVMI_F_VALU_FWHT); everything else runs the register-FWHT kernels.
+// Kernel families, by geometry:
+//  * MFMA (kvmi_mfma.hip): the transform profile with D in {64, 128}, H dividing 8 and
+//    S*H a multiple of 32, unless the caller forces the register FWHT
+//    (KVMI_F_VALU_FWHT);
+//  * quad-per-row register FWHT (kvmi_codec.hip): D in {64, 128}, H dividing 128,
+//    H <= 16;
+//  * generic rows (kvmi_rows.hip): every other geometry check_geo admits (D a
+//    multiple of 16 up to 256, split into power-of-two chunks when it is not one;
+//    H up to 64).
 inline bool mfma_eligible(const Geo& g) {
-  return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_NO_TRANSFORM)) && (8 % g.H) == 0 && ((g.S * g.H) % 32) == 0;
+  return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_NO_TRANSFORM)) && (g.D == 64 || g.D == 128) && (8 % g.H) == 0 &&
+         ((g.S * g.H) % 32) == 0;
 }
+inline bool quad_eligible(const Geo& g) {
+  return (g.D == 64 || g.D == 128) && g.H <= kMaxQuadH && (128 % g.H) == 0;
+}
+int rows_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
+                hipStream_t st);
+int rows_encode(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
+                hipStream_t st);
+int rows_decode(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
+                hipStream_t st);
+int rows_hadamard(const void* in, void* out, int64_t rows, int32_t H, int32_t D, const uint32_t* signs,
+                  int32_t inverse, hipStream_t st);
 int mfma_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
                 hipStream_t st);
 int mfma_encode(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,

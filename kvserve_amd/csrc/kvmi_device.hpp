@@ -160,6 +160,23 @@ __device__ __forceinline__ void fwht_row(float (&v)[E], int q) {
   fwht_cross_quad<E>(v, q);
 }
 
+// Value of lane (lane ^ J): DPP for J = 1, 2 (quad_perm) and 8 (row_ror:8 within a
+// 16-lane row), ds_swizzle bit masks for 4 and 16, bpermute beyond.
+template <int J>
+__device__ __forceinline__ float lane_xor(float x) {
+  if constexpr (J == 1) {
+    return dpp_f<0xB1>(x);
+  } else if constexpr (J == 2) {
+    return dpp_f<0x4E>(x);
+  } else if constexpr (J == 8) {
+    return dpp_f<0x128>(x);
+  } else if constexpr (J == 4 || J == 16) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1F | (J << 10)));
+  } else {
+    return __shfl_xor(x, J, 64);
+  }
+}
+
 // Min / max of a value across the 4 lanes of a quad.
 __device__ __forceinline__ float quad_min(float x) {
   x = fminf(x, dpp_f<0xB1>(x));

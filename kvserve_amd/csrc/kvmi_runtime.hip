@@ -467,23 +467,6 @@ __device__ __forceinline__ void rn2(float& x, float& y) {
   y = bf_hi(p);
 }
 
-// Value of lane (lane ^ J): DPP for J = 1, 2 (quad_perm) and 8 (row_ror:8 within a
-// 16-lane row), ds_swizzle bit masks for 4 and 16, bpermute beyond.
-template <int J>
-__device__ __forceinline__ float lane_xor(float x) {
-  if constexpr (J == 1) {
-    return dpp_f<0xB1>(x);
-  } else if constexpr (J == 2) {
-    return dpp_f<0x4E>(x);
-  } else if constexpr (J == 8) {
-    return dpp_f<0x128>(x);
-  } else if constexpr (J == 4 || J == 16) {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1F | (J << 10)));
-  } else {
-    return __shfl_xor(x, J, 64);
-  }
-}
-
 // Butterfly stages across lanes J, 2J, .. < LH: the lane with bit J clear holds the
 // lower element a and gets a + b, the other gets a - b = partner - own; fma(v, +-1, o)
 // is that sum with one fp32 rounding, then bf16.

@@ -2,8 +2,7 @@
 // Hadamard transform.  They serve the operator-level API (one stage at a time,
 // as KVServe's CompressionManager calls its operators) and stage-by-stage parity
 // checks; the fused path in kvmi_codec.hip does not use them.
-#include "kvmi_device.hpp"
-#include "../../include/kvserve_amd.h"
+#include "kvmi_common.hpp"
 
 namespace kvmi {
 namespace {
@@ -91,14 +90,16 @@ extern "C" int kvmi_scatter_blocks(void* pool, int64_t pool_part_stride, const i
 extern "C" int kvmi_hadamard(const void* in, void* out, int64_t rows, int32_t num_heads, int32_t head_dim,
                              const uint32_t* signs, int32_t inverse, kvmi_stream_t stream) {
   using namespace kvmi;
-  if (rows < 0 || num_heads < 1 || (head_dim != 64 && head_dim != 128)) return KVMI_EINVAL;
+  if (rows < 0 || num_heads < 1 || head_dim < 16 || head_dim > 256 || head_dim % 16) return KVMI_EINVAL;
   if (rows == 0) return KVMI_OK;
   if (!in || !out || !signs) return KVMI_EINVAL;
   if ((uintptr_t)in % 16 || (uintptr_t)out % 16) return KVMI_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (head_dim != 64 && head_dim != 128)  // power-of-two chunks, one row per 16-channel lane group
+    return rows_hadamard(in, out, rows, num_heads, head_dim, signs, inverse, st);
   const int64_t grid = (rows + kHadWG / 4 - 1) / (kHadWG / 4);
   if (grid > 0x7fffffffLL) return KVMI_EINVAL;
   const float scale = (float)(1.0 / __builtin_sqrt((double)head_dim));
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (head_dim == 64)
     hipLaunchKernelGGL((hadamard_kernel<64>), dim3((unsigned)grid), dim3(kHadWG), 0, st,
                        static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), rows, num_heads, signs, inverse,

@@ -99,6 +99,27 @@ class Packet:
         return sum(int(s.numel()) for s in self.streams)
 
 
+MAX_HEADS = 64        # kvmi_common.hpp kMaxHeads
+MAX_ROW_SLOTS = 8192  # kvmi_common.hpp kMaxRowSlots: H * next_pow2(D)
+
+
+def supported_geometry(num_heads: int, head_dim: int) -> bool:
+    """The geometries the paged kernels take (kvmi_common.hpp check_geo): head_dim a
+    multiple of 16 in [16, 256] (split into power-of-two chunks when it is not one,
+    hadamard_func.py:50-103), 1..64 heads, and heads * next_pow2(head_dim) <= 8192."""
+    if type(num_heads) is not int or type(head_dim) is not int:
+        return False
+    if not 1 <= num_heads <= MAX_HEADS or not 16 <= head_dim <= 256 or head_dim % 16:
+        return False
+    return num_heads * (1 << (head_dim - 1).bit_length()) <= MAX_ROW_SLOTS
+
+
+def check_geometry(num_heads: int, head_dim: int) -> None:
+    if not supported_geometry(num_heads, head_dim):
+        raise ValueError(f"unsupported geometry: {num_heads} heads of head_dim {head_dim} (head_dim a multiple "
+                         f"of 16 in [16, 256], 1..{MAX_HEADS} heads, heads * next_pow2(head_dim) <= {MAX_ROW_SLOTS})")
+
+
 class FusedKVCodec:
     """Fused compress / decompress of paged KV for one worker's geometry.
 
@@ -114,8 +135,7 @@ class FusedKVCodec:
                  header: bool = True, fwht: Optional[str] = None, compress_path: Optional[str] = None):
         if type(bits) is not int or not 1 <= bits <= 8:
             raise ValueError("bitpack_bits must be an integer in [1, 8]")
-        if head_dim not in (64, 128):
-            raise ValueError("head_dim must be 64 or 128")
+        check_geometry(num_heads, head_dim)
         if layout not in ("permuted", "native"):
             raise ValueError("layout must be 'permuted' or 'native'")
         if not header and bits != 8:

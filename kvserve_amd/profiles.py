@@ -25,7 +25,8 @@ DUO_DIR = Path(__file__).resolve().parent / "compression" / "config" / "duo_conf
 
 # ------------------------------------------------------------------ signs
 def rademacher_sign_bits(base_seed: int, layer_id: int, num_heads: int, head_dim: int) -> np.ndarray:
-    """uint32 [H, D/32]: bit d%32 of word d//32 is set where the sign is -1.
+    """uint32 [H, ceil(D/32)]: bit d%32 of word d//32 is set where the sign is -1 (bits
+    past D are 0).
 
     Recipe of HadamardTransform.get_rademacher_signs (hadamard_func.py:33-48,
     :137-152): one CPU torch.Generator re-seeded per head with
@@ -33,15 +34,17 @@ def rademacher_sign_bits(base_seed: int, layer_id: int, num_heads: int, head_dim
     """
     import torch
 
-    if head_dim % 32:
-        raise ValueError("head_dim must be a multiple of 32")
+    if head_dim < 1:
+        raise ValueError("head_dim must be positive")
     gen = torch.Generator(device="cpu")
-    out = np.zeros((num_heads, head_dim // 32), dtype=np.uint32)
+    W = (head_dim + 31) // 32
+    out = np.zeros((num_heads, W), dtype=np.uint32)
     for h in range(num_heads):
         gen.manual_seed(base_seed ^ (layer_id << 16) ^ h)
         s = torch.randint(0, 2, (head_dim,), generator=gen, dtype=torch.int8).numpy()
-        neg = (s == 0).astype(np.uint64)  # 0 -> -1
-        words = (neg.reshape(-1, 32) << np.arange(32, dtype=np.uint64)).sum(axis=1)
+        neg = np.zeros(W * 32, np.uint64)
+        neg[:head_dim] = s == 0  # 0 -> -1
+        words = (neg.reshape(W, 32) << np.arange(32, dtype=np.uint64)).sum(axis=1)
         out[h] = words.astype(np.uint32)
     return out
 

@@ -53,10 +53,13 @@ def rademacher_signs(base_seed: int, layer_id: int, num_heads: int, head_dim: in
 
 
 def sign_bits(signs: np.ndarray) -> np.ndarray:
-    """[H, D] +-1 -> [H, D/32] uint32, bit (d % 32) of word d // 32 set when sign is -1."""
-    neg = (signs < 0).astype(np.uint64)
+    """[H, D] +-1 -> [H, ceil(D/32)] uint32, bit (d % 32) of word d // 32 set when the
+    sign is -1 (bits past D are 0)."""
     H, D = signs.shape
-    w = neg.reshape(H, D // 32, 32) << np.arange(32, dtype=np.uint64)
+    W = (D + 31) // 32
+    neg = np.zeros((H, W * 32), np.uint64)
+    neg[:, :D] = signs < 0
+    w = neg.reshape(H, W, 32) << np.arange(32, dtype=np.uint64)
     return w.sum(axis=2).astype(np.uint32)
 
 
@@ -83,19 +86,31 @@ def _scale(D: int) -> np.float32:
     return np.float32(1.0 / math.sqrt(D))  # hadamard_func.py:98 scale=1/sqrt(size)
 
 
+def pow2_chunks(D: int) -> List[int]:
+    """hadamard_func.py:50-71: D as descending powers of two (96 -> [64, 32])."""
+    return [1 << b for b in range(D.bit_length() - 1, -1, -1) if D >> b & 1]
+
+
+def fwht_scaled_f32(x: np.ndarray) -> np.ndarray:
+    """hadamard_func.py:73-103 before the bf16 rounding: each power-of-two chunk of the
+    last axis transformed on its own (fwht_f32) and scaled by 1/sqrt(chunk)."""
+    out, start = [], 0
+    for c in pow2_chunks(x.shape[-1]):
+        out.append(fwht_f32(x[..., start:start + c]) * _scale(c))
+        start += c
+    return np.concatenate(out, axis=-1)
+
+
 def hadamard_forward(x_bits: np.ndarray, signs: np.ndarray) -> np.ndarray:
-    """bf16 [..., H, D] -> bf16.  hadamard_func.py:161-197: x*s (exact in bf16), FWHT
-    with scale 1/sqrt(D) in fp32, one bf16 rounding."""
+    """bf16 [..., H, D] -> bf16.  hadamard_func.py:161-197: x*s (exact in bf16), FWHT of
+    each power-of-two chunk with scale 1/sqrt(chunk) in fp32, one bf16 rounding."""
     x = bf16_to_f32(x_bits) * signs
-    D = x.shape[-1]
-    return f32_to_bf16(fwht_f32(x) * _scale(D))
+    return f32_to_bf16(fwht_scaled_f32(x))
 
 
 def hadamard_inverse(y_bits: np.ndarray, signs: np.ndarray) -> np.ndarray:
-    """hadamard_func.py:199-231: FWHT (rounded to bf16) first, then * signs."""
-    y = bf16_to_f32(y_bits)
-    D = y.shape[-1]
-    z = rbf(fwht_f32(y) * _scale(D))
+    """hadamard_func.py:199-231: chunked FWHT (rounded to bf16) first, then * signs."""
+    z = rbf(fwht_scaled_f32(bf16_to_f32(y_bits)))
     return f32_to_bf16(z * signs)
 
 

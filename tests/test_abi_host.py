@@ -52,11 +52,21 @@ def test_host_contract_errors_return_einval():
     assert lib.kvmi_hadamard(None, None, 4, 8, 96, None, 0, None) == E
     g = _lib.Geometry()
     g.block_size, g.num_heads, g.head_dim, g.bits, g.max_groups = 16, 8, 128, 4, 2
-    for field, bad in (("head_dim", 96), ("bits", 0), ("num_heads", 3), ("max_groups", 9), ("num_heads", 32)):
+    # head_dim: a multiple of 16 in [16, 256]; heads: 1..64 with heads * next_pow2(head_dim) <= 8192
+    for bad in ({"head_dim": 100}, {"head_dim": 8}, {"head_dim": 272}, {"bits": 0}, {"num_heads": 0},
+                {"num_heads": 65}, {"max_groups": 9}, {"num_heads": 64, "head_dim": 256, "max_groups": 2},
+                {"num_heads": 48, "head_dim": 160}):
         gg = _lib.Geometry.from_buffer_copy(g)
-        setattr(gg, field, bad)
+        for field, value in bad.items():
+            setattr(gg, field, value)
         for fn in (lib.kvmi_kstats_paged, lib.kvmi_encode_paged, lib.kvmi_decode_paged):
-            assert fn(ctypes.byref(gg), None, 1, 1, None, None) == E, (field, bad)
+            assert fn(ctypes.byref(gg), None, 1, 1, None, None) == E, bad
+    for good in ({"head_dim": 96}, {"num_heads": 3}, {"num_heads": 64}, {"head_dim": 256, "num_heads": 32}):
+        gg = _lib.Geometry.from_buffer_copy(g)
+        for field, value in good.items():
+            setattr(gg, field, value)
+        # a valid geometry with zero jobs returns before touching any pointer
+        assert lib.kvmi_encode_paged(ctypes.byref(gg), None, 0, 1, None, None) == 0, good
     gg = _lib.Geometry.from_buffer_copy(g)
     gg.flags = _lib.F_NO_HEADER  # raw symbols need 8 bits
     assert lib.kvmi_encode_paged(ctypes.byref(gg), None, 1, 1, None, None) == E
@@ -150,8 +160,10 @@ def test_codec_constructor_contracts():
     for bits in (0, 9, True, 3.5, None):
         with pytest.raises(ValueError, match="bitpack_bits"):
             FusedKVCodec(8, 128, 16, bits)
-    with pytest.raises(ValueError):
-        FusedKVCodec(8, 96, 16, 4)
+    for H, D in ((8, 100), (8, 272), (65, 64), (64, 256), (0, 128)):
+        with pytest.raises(ValueError, match="unsupported geometry"):
+            FusedKVCodec(H, D, 16, 4)
+    FusedKVCodec(6, 96, 16, 4)  # D split into power-of-two chunks, H not dividing 128
     with pytest.raises(ValueError):
         FusedKVCodec(8, 128, 16, 4, header=False)
 

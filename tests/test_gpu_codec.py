@@ -102,15 +102,19 @@ def test_gather_scatter_bit_exact(cuda):
         ops.gather_blocks(pool.to(cuda), [40])
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_hadamard_unit_matches_oracle(cuda, D):
+@pytest.mark.parametrize("D,H", [(64, 8), (128, 8), (96, 8), (256, 4), (80, 6), (16, 3), (224, 2)])
+def test_hadamard_unit_matches_oracle(cuda, D, H):
+    """Power-of-two D and D split into power-of-two chunks (hadamard_func.py:50-103):
+    bit-exact with the oracle, whose chunked transform is pinned to the Sylvester
+    matrices (tests/test_oracle.py)."""
     from kvserve_amd import ops
 
     g = torch.Generator().manual_seed(D)
-    x = torch.randn((3, 16, 8, D), generator=g).to(torch.bfloat16)
+    x = torch.randn((3, 16, H, D), generator=g).to(torch.bfloat16)
     seed, layer = 0xC0FEBABE, 5
+    print(f"hadamard unit D={D} H={H}", flush=True)
     y = ops.hadamard(x.to(cuda), layer, seed)
-    sg = kp.rademacher_signs(seed, layer, 8, D)
+    sg = kp.rademacher_signs(seed, layer, H, D)
     ref = kp.hadamard_forward(_bits(x), sg)
     assert np.array_equal(_bits(y), ref)
     z = ops.hadamard(y, layer, seed, inverse=True)

@@ -340,6 +340,55 @@ def test_geometries_match_oracle(cuda, H, S, D, bits):
         _check_layer(packet, l, x[l], _bits(dst[l][:, ids.to(cuda).long()]))
 
 
+@pytest.mark.parametrize("H,S,D,bits,layout", [
+    (32, 16, 128, 4, "permuted"),  # 32 KV heads (MHA model, one rank)
+    (6, 16, 128, 4, "permuted"),   # H not dividing 128
+    (8, 16, 256, 4, "permuted"),   # D = 256
+    (8, 16, 96, 4, "permuted"),    # D = 64 + 32
+    (12, 16, 80, 3, "native"),     # D = 64 + 16, odd bit width
+    (64, 16, 128, 2, "permuted"),  # 64 heads: one token per pass
+    (5, 32, 224, 5, "native"),     # D = 128 + 64 + 32
+    (3, 16, 16, 8, "permuted"),    # D = 16: one lane per row
+    (24, 16, 160, 6, "permuted"),  # D = 128 + 32
+])
+def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
+    """The generic row kernels (kvmi_rows.hip) run the oracle's FWHT stage order, so
+    symbols, metadata and the decompressed KV are bit-exact with the oracle."""
+    from kvserve_amd.engine import FusedKVCodec, check_packet
+    from kvserve_amd.profiles import section_profile
+    from kvserve_amd.workloads import kv_blocks
+
+    g = torch.Generator().manual_seed(H * 1000 + S * 10 + D + bits)
+    L, B, P = 2, 5, 16
+    levels = (2 ** bits - 1, max(2, 2 ** bits - 3))
+    pools = [torch.zeros((2, P, S, H, D), dtype=torch.bfloat16) for _ in range(L)]
+    ids = torch.randperm(P, generator=g)[:B]
+    for p in pools:
+        p[:, ids] = kv_blocks(g, B, S, H, D)
+    prof = [section_profile([bool(v) for v in torch.randint(0, 2, (H,), generator=g)], levels[0], levels[0],
+                            levels[1], levels[1]) for _ in range(L)]
+    print(f"generic geometry H={H} S={S} D={D} bits={bits} {layout}", flush=True)
+    pools = [p.to(cuda) for p in pools]
+    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout)
+    dev_ids = ids.to(torch.int32).to(cuda)
+    packet = codec.compress(pools, dev_ids, prof)
+    check_packet(packet)
+    dst = [torch.zeros_like(p) for p in pools]
+    codec.decompress(packet, dst, dev_ids)
+    torch.cuda.synchronize()
+    for l in range(L):
+        x = _bits(pools[l][:, dev_ids.long()])
+        oprof = _oracle_profile(packet.profiles[l])
+        ch = kp.compress_request([x], list(range(B)), [oprof], packet.seed, bits, layout=layout,
+                                 layer_ids=[packet.layer_ids[l]], chunks=[(0, 1)])[0]
+        assert np.array_equal(_layer_symbols(packet, l), ch.symbols.reshape(-1)), l
+        _check_layer(packet, l, x)
+        ref = np.zeros_like(x)
+        kp.decompress_request([ch], [ref], list(range(B)), [oprof], packet.seed, bits, layout=layout,
+                              layer_ids=[packet.layer_ids[l]])
+        assert np.array_equal(_bits(dst[l][:, dev_ids.long()]), ref), l
+
+
 @pytest.mark.parametrize("fwht", ["mfma", "valu"])
 def test_batch_with_empty_request_writes_its_header(cuda, fwht):
     """A request without blocks in a batch still gets a valid 16-byte header for N = 0

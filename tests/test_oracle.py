@@ -159,6 +159,35 @@ def test_hadamard_roundtrip_and_signs_on_exact_inputs():
     assert np.max(np.abs(back - x)) <= 2 ** -6  # one bf16 rounding in each direction
 
 
+def test_pow2_chunks_follow_the_reference_examples():
+    # hadamard_func.py:63-64 docstring: 96 -> [64, 32], 100 -> [64, 32, 4]
+    assert kp.pow2_chunks(96) == [64, 32] and kp.pow2_chunks(100) == [64, 32, 4]
+    assert kp.pow2_chunks(128) == [128] and kp.pow2_chunks(80) == [64, 16]
+
+
+@pytest.mark.parametrize("D", [96, 80, 224, 256])
+def test_chunked_transform_is_sylvester_per_chunk(D):
+    """Each unit vector inside chunk [a, a + c) maps to a Walsh row of H_c / sqrt(c) at
+    [a, a + c) and zero elsewhere: the chunks are transformed independently, with
+    their own scale (Sylvester closed form, scipy.linalg.hadamard)."""
+    eye = np.eye(D, dtype=np.float32)
+    y = kp.fwht_scaled_f32(eye)
+    start = 0
+    for c in kp.pow2_chunks(D):
+        blk = scipy.linalg.hadamard(c).astype(np.float32) * np.float32(1.0 / np.sqrt(c))
+        assert np.array_equal(y[start:start + c, start:start + c], blk)
+        assert not y[start:start + c, :start].any() and not y[start:start + c, start + c:].any()
+        start += c
+    # signs and rounding: forward then inverse restores exact {-1, 0, 1} inputs within
+    # one bf16 rounding each way
+    rng = np.random.default_rng(D)
+    x = rng.integers(-1, 2, (4, 3, D)).astype(np.float32)
+    s = kp.rademacher_signs(9, 1, 3, D)
+    back = kp.bf16_to_f32(kp.hadamard_inverse(kp.hadamard_forward(kp.f32_to_bf16(x), s), s))
+    assert np.max(np.abs(back - x)) <= 2 ** -6
+    assert kp.sign_bits(s).shape == (3, (D + 31) // 32)
+
+
 def test_fwht_random_close_to_float64():
     rng = np.random.default_rng(5)
     x = rng.standard_normal((64, 128)).astype(np.float32)
