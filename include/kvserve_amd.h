@@ -75,6 +75,13 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_F_VALU_FWHT 8u     /* force the register (VALU) FWHT kernels instead of MFMA */
 #define KVMI_F_CLAMP_LEVELS 16u /* some level count exceeds 128: clamp symbols to the level */
 #define KVMI_F_TWO_PASS 32u     /* kvmi_compress_paged: statistics pass + encode pass (K read twice) */
+/* Quantization axes (quantizer_func.py:41-49; KVServeQuantizer axis_key / axis_value,
+ * kvserve_quantizer.py:136-139).  Default (no flag): K per channel, V per token.  At most
+ * one flag per part; any of them selects the generic row kernels. */
+#define KVMI_F_K_TOKEN 64u    /* K statistics per token over the heads of a K group */
+#define KVMI_F_K_TENSOR 128u  /* one K statistic pair per K group */
+#define KVMI_F_V_CHANNEL 256u /* V statistics per channel of each head */
+#define KVMI_F_V_TENSOR 512u  /* one V statistic pair per V group */
 
 /* Launch-wide geometry shared by every job of one call. */
 typedef struct kvmi_geometry {
@@ -97,12 +104,15 @@ typedef struct kvmi_geometry {
  *             ascending, then high heads: kvserve_quantizer.py:216-220)
  *   [p][1][j] quantization levels (max_value) of output position j, in [2, 255]
  *   [p][2][j] statistic group of output position j; groups are contiguous runs of
- *             positions. Only the V part uses groups (per-token stats are shared by
- *             the heads of a group, quantizer_func.py:44-53 with axis "token").
- * kmeta: bf16 [2][H][D]: [0] = per-channel min, [1] = scale, by output position.
- * vmeta: bf16 [2][G][num_blocks*S]: [0] = per-token min, [1] = scale, by group.
- * kstats: uint32 [2][H][D] order-preserving keys of the running K min / max,
- *         initialised to {0xFFFFFFFF, 0}; kvmi_kstats_paged leaves it initialised.
+ *             positions sharing one level count.  A part on the token or tensor axis
+ *             shares its statistics over the heads of a group (quantizer_func.py:44-53);
+ *             on the channel axis groups only label the sections.
+ * kmeta / vmeta: bf16 metadata of the K / V part, [0] = min, [1] = scale, laid out by
+ *   the part's axis: channel [2][H][D] by output position (K's default), token
+ *   [2][G][num_blocks*S] by group (V's default), tensor [2][G] by group.
+ * kstats: uint32 [2][H][D] order-preserving keys of the running K min / max; with
+ *   KVMI_F_V_CHANNEL or KVMI_F_V_TENSOR, [2 parts][2][H][D] (V's keys after K's);
+ *   initialised to {0xFFFFFFFF, 0}; kvmi_kstats_paged leaves it initialised.
  * counter: unused (may be null; kept for the layout of this struct).
  */
 typedef struct kvmi_layer_job {

@@ -30,6 +30,10 @@ F_NO_HEADER = 4
 F_VALU_FWHT = 8
 F_CLAMP_LEVELS = 16
 F_TWO_PASS = 32
+F_K_TOKEN = 64
+F_K_TENSOR = 128
+F_V_CHANNEL = 256
+F_V_TENSOR = 512
 
 # Every symbol include/kvserve_amd.h declares.
 EXPORTS = (

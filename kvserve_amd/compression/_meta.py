@@ -1,15 +1,18 @@
 """Conversion between the engine's flat metadata tables and the reference's
 per-layer quantization dicts.
 
-Engine tables (kvserve_amd.engine.Packet):
-  kmeta bf16 [L, 2, H, D]   [l, 0] = per-channel min, [l, 1] = scale, by output position
-  vmeta bf16 [L, 2, G, B*S] [l, 0] = per-token min, [l, 1] = scale, by V group
+Engine tables (kvserve_amd.engine.Packet), one per part, laid out by the part's axis:
+  channel  bf16 [L, 2, H, D]    [l, 0] = per-channel min, [l, 1] = scale, by output position
+  token    bf16 [L, 2, G, B*S]  per-token min / scale, by statistic group
+  tensor   bf16 [L, 2, G, 1]    one min / scale per group
+(K is on the channel axis and V on the token axis by default.)
 Reference dict of one layer (kvserve_quantizer.py:224-231, quantizer_func.py:67-73):
   {"high_key_meta", "high_value_meta", "low_key_meta", "low_value_meta": {
-       "min_val": bf16 [1,1,Hg,D] (K) or [B,S,1,1] (V) | None, "quant_scale": same,
+       "min_val": bf16 keepdim tensor -- [1,1,Hg,D] (channel), [B,S,1,1] (token),
+                  [1,1,1,1] (tensor) -- or None, "quant_scale": same,
        "original_dtype": "bfloat16", "quant_dtype": "uint8"},
    "original_dtype": "bfloat16"}
-The "low" section is the first n_low output positions and V group 0 when it exists.
+The "low" section is the first n_low output positions and group 0 when it exists.
 """
 
 from __future__ import annotations
@@ -18,9 +21,11 @@ from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
+from ..engine import DEFAULT_AXES, meta_shape
 from ..profiles import LayerProfile
 
 _SECTIONS = ("high_key_meta", "high_value_meta", "low_key_meta", "low_value_meta")
+_PARTS = (("low_key_meta", "high_key_meta"), ("low_value_meta", "high_value_meta"))
 
 
 def _empty(dtype: str = "bfloat16") -> Dict:
@@ -31,58 +36,79 @@ def _sec(mn: torch.Tensor, sc: torch.Tensor) -> Dict:
     return {"min_val": mn, "quant_scale": sc, "original_dtype": "bfloat16", "quant_dtype": "uint8"}
 
 
-def layer_dict(kmeta_l: torch.Tensor, vmeta_l: torch.Tensor, prof: LayerProfile, B: int, S: int) -> Dict:
-    """Reference-format metadata of one layer (views into the engine tables)."""
-    H, D = kmeta_l.shape[1], kmeta_l.shape[2]
+def _keepdim(axis: str, rows: int, D: int, B: int, S: int) -> Tuple[int, ...]:
+    """Reference shape of a section's min / scale (quantizer_func.py:52-53, keepdim)."""
+    return {"channel": (1, 1, rows, D), "token": (B, S, 1, 1), "tensor": (1, 1, 1, 1)}[axis]
+
+
+def _sections(prof: LayerProfile, H: int) -> List[Tuple[str, int, int, int]]:
+    """(name, first position, last position + 1, group) of the layer's sections."""
+    n_low = prof.n_low if prof.n_low is not None else 0
+    out = []
+    if n_low > 0:
+        out.append(("low", 0, n_low, 0))
+    if n_low < H:
+        out.append(("high", n_low, H, 1 if n_low > 0 else 0))
+    return out
+
+
+def layer_dict(kmeta_l: torch.Tensor, vmeta_l: torch.Tensor, prof: LayerProfile, B: int, S: int,
+               axes: Tuple[str, str] = DEFAULT_AXES) -> Dict:
+    """Reference-format metadata of one layer (views into the engine tables; a
+    table of one layer is [2, rows, cols] as laid out by its part's axis)."""
+    H = len(prof.k_order)
+    D = kmeta_l.shape[2] if axes[0] == "channel" else vmeta_l.shape[2] if axes[1] == "channel" else None
     n_low = prof.n_low if prof.n_low is not None else 0
     if prof.num_v_groups() > (2 if 0 < n_low < H else 1) or prof.k_order != prof.v_order:
         raise ValueError("this profile has no reference-format metadata (more than two sections)")
     out = {k: _empty() for k in _SECTIONS}
     out["original_dtype"] = "bfloat16"
-    if n_low > 0:
-        out["low_key_meta"] = _sec(kmeta_l[0, :n_low].view(1, 1, n_low, D), kmeta_l[1, :n_low].view(1, 1, n_low, D))
-        out["low_value_meta"] = _sec(vmeta_l[0, 0].view(B, S, 1, 1), vmeta_l[1, 0].view(B, S, 1, 1))
-    if n_low < H:
-        nh = H - n_low
-        g = 1 if n_low > 0 else 0
-        out["high_key_meta"] = _sec(kmeta_l[0, n_low:].view(1, 1, nh, D), kmeta_l[1, n_low:].view(1, 1, nh, D))
-        out["high_value_meta"] = _sec(vmeta_l[0, g].view(B, S, 1, 1), vmeta_l[1, g].view(B, S, 1, 1))
+    for (low_name, high_name), table, axis in zip(_PARTS, (kmeta_l, vmeta_l), axes):
+        for sec, lo, hi, g in _sections(prof, H):
+            name = low_name if sec == "low" else high_name
+            shape = _keepdim(axis, hi - lo, D, B, S)
+            rows = slice(lo, hi) if axis == "channel" else g
+            out[name] = _sec(table[0, rows].reshape(shape), table[1, rows].reshape(shape))
     return out
 
 
-def tables_from_dicts(dicts: Sequence[Dict], H: int, D: int, B: int, S: int,
-                      device) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Inverse of layer_dict for a list of layers: (kmeta [L,2,H,D], vmeta [L,2,G,B*S])."""
+def tables_from_dicts(dicts: Sequence[Dict], H: int, D: int, B: int, S: int, device,
+                      axes: Tuple[str, str] = DEFAULT_AXES) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Inverse of layer_dict for a list of layers: (kmeta, vmeta), each
+    [L, 2, rows, cols] as laid out by its part's axis."""
     L = len(dicts)
     G = 1
     for d in dicts:
-        n = sum(1 for s in ("low_value_meta", "high_value_meta") if d[s]["min_val"] is not None)
-        G = max(G, n)
-    views = _table_views(dicts, H, D, B * S, G, device)
+        for names in _PARTS:
+            G = max(G, sum(1 for s in names if d[s]["min_val"] is not None))
+    views = _table_views(dicts, H, D, B * S, G, axes, device)
     if views is not None:
         return views
-    kmeta = torch.empty((L, 2, H, D), dtype=torch.bfloat16, device=device)
-    vmeta = torch.zeros((L, 2, G, B * S), dtype=torch.bfloat16, device=device)
-    for l, d in enumerate(dicts):
-        parts_k = [d[s] for s in ("low_key_meta", "high_key_meta") if d[s]["min_val"] is not None]
-        parts_v = [d[s] for s in ("low_value_meta", "high_value_meta") if d[s]["min_val"] is not None]
-        if not parts_k or not parts_v:
-            raise ValueError("Missing quantization params")
-        kmeta[l, 0] = torch.cat([p["min_val"].reshape(-1, D) for p in parts_k]).to(device, torch.bfloat16)
-        kmeta[l, 1] = torch.cat([p["quant_scale"].reshape(-1, D) for p in parts_k]).to(device, torch.bfloat16)
-        for g, p in enumerate(parts_v):
-            vmeta[l, 0, g] = p["min_val"].reshape(-1).to(device, torch.bfloat16)
-            vmeta[l, 1, g] = p["quant_scale"].reshape(-1).to(device, torch.bfloat16)
-    return kmeta, vmeta
+    tables = []
+    for names, axis in zip(_PARTS, axes):
+        rows, cols = meta_shape(axis, H, D, G, B * S)
+        t = torch.zeros((L, 2, rows, cols), dtype=torch.bfloat16, device=device)
+        for l, d in enumerate(dicts):
+            secs = [d[s] for s in names if d[s]["min_val"] is not None]
+            if not secs:
+                raise ValueError("Missing quantization params")
+            for which, key in ((0, "min_val"), (1, "quant_scale")):
+                if axis == "channel":
+                    t[l, which] = torch.cat([p[key].reshape(-1, D) for p in secs]).to(device, torch.bfloat16)
+                else:
+                    for g, p in enumerate(secs):
+                        t[l, which, g] = p[key].reshape(-1).to(device, torch.bfloat16)
+        tables.append(t)
+    return tables[0], tables[1]
 
 
-def _table_views(dicts: Sequence[Dict], H: int, D: int, BS: int, G: int,
+def _table_views(dicts: Sequence[Dict], H: int, D: int, BS: int, G: int, axes: Tuple[str, str],
                  device) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
     """kmeta / vmeta as views when every section tensor already sits where the
-    engine's one-allocation layout puts it (kmeta [L,2,H,D] followed by vmeta
-    [L,2,G,B*S], bf16) -- the case of a packet made by this engine, also after a
-    wire round trip that shipped the allocation whole.  Pointer arithmetic only;
-    None when any tensor is elsewhere (the caller then copies)."""
+    engine's one-allocation layout puts it (the K table followed by the V table, bf16)
+    -- the case of a packet made by this engine, also after a wire round trip that
+    shipped the allocation whole.  Pointer arithmetic only; None when any tensor is
+    elsewhere (the caller then copies)."""
     L = len(dicts)
     if L == 0:
         return None
@@ -93,38 +119,31 @@ def _table_views(dicts: Sequence[Dict], H: int, D: int, BS: int, G: int,
         return None
     st = first.untyped_storage()
     sp, base = st.data_ptr(), first.data_ptr()
-    kn, vn = L * 2 * H * D, L * 2 * G * BS
-    if (base - sp) % 2 or base - sp + 2 * (kn + vn) > st.nbytes():
+    shapes = [meta_shape(a, H, D, G, BS) for a in axes]
+    sizes = [L * 2 * r * c for r, c in shapes]
+    if (base - sp) % 2 or base - sp + 2 * sum(sizes) > st.nbytes():
         return None
-    vbase = base + 2 * kn
+    bases = (base, base + 2 * sizes[0])
 
     def at(t, addr, numel) -> bool:
         return (t is not None and t.dtype == torch.bfloat16 and t.is_contiguous() and t.numel() == numel
                 and t.data_ptr() == addr and t.untyped_storage().data_ptr() == sp)
 
     for l, d in enumerate(dicts):
-        h = 0
-        for s in ("low_key_meta", "high_key_meta"):
-            mn = d[s]["min_val"]
-            if mn is None:
-                continue
-            rows = mn.numel() // D
-            if not (at(mn, base + 2 * ((2 * l) * H + h) * D, rows * D)
-                    and at(d[s]["quant_scale"], base + 2 * ((2 * l + 1) * H + h) * D, rows * D)):
+        for names, axis, (rows, cols), pbase in zip(_PARTS, axes, shapes, bases):
+            r = 0  # next table row: a position (channel axis) or a group
+            for s in names:
+                mn = d[s]["min_val"]
+                if mn is None:
+                    continue
+                n = mn.numel() // cols if axis == "channel" else 1
+                if not (at(mn, pbase + 2 * ((2 * l) * rows + r) * cols, n * cols)
+                        and at(d[s]["quant_scale"], pbase + 2 * ((2 * l + 1) * rows + r) * cols, n * cols)):
+                    return None
+                r += n
+            if axis == "channel" and r != H:
                 return None
-            h += rows
-        if h != H:
-            return None
-        g = 0
-        for s in ("low_value_meta", "high_value_meta"):
-            mn = d[s]["min_val"]
-            if mn is None:
-                continue
-            if not (at(mn, vbase + 2 * ((2 * l) * G + g) * BS, BS)
-                    and at(d[s]["quant_scale"], vbase + 2 * ((2 * l + 1) * G + g) * BS, BS)):
-                return None
-            g += 1
     off = (base - sp) // 2
-    kmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off, (L, 2, H, D))
-    vmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off + kn, (L, 2, G, BS))
+    kmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off, (L, 2) + shapes[0])
+    vmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off + sizes[0], (L, 2) + shapes[1])
     return kmeta, vmeta

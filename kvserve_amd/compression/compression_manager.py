@@ -291,16 +291,17 @@ class FusedCompressionManager(CompressionManager):
         if "codec" in pipe and (self.config.codec_config or {}).get("codec_type", "nvcomp") not in (
                 "bitpack", "rans", "nvcomp", "lc"):
             return False
-        if self.quantizer.axis_key != "channel" or self.quantizer.axis_value != "token":
-            return False
         return dtype == torch.bfloat16 and supported_geometry(H, D)
+
+    def _axes(self):
+        return (self.quantizer.axis_key, self.quantizer.axis_value)
 
     def _codec(self, H, D, S) -> FusedKVCodec:
         transform, seed, has_codec, bits = self._settings()
-        key = (H, D, S, transform, seed, has_codec, bits, codec_layout())
+        key = (H, D, S, transform, seed, has_codec, bits, codec_layout(), self._axes())
         if key not in self._codecs:
             self._codecs[key] = FusedKVCodec(H, D, S, bits, seed, transform=transform, layout=codec_layout(),
-                                             header=has_codec)
+                                             header=has_codec, axes=self._axes())
         return self._codecs[key]
 
     def profiles(self, layer_ids: Sequence[int], H: int):
@@ -349,7 +350,7 @@ class FusedCompressionManager(CompressionManager):
             if transform:
                 m["transformer_applied"] = True
             m["quantization_applied"] = True
-            m["quantization_params"] = [layer_dict(packet.kmeta[l], packet.vmeta[l], profs[l], B, S)
+            m["quantization_params"] = [layer_dict(packet.kmeta[l], packet.vmeta[l], profs[l], B, S, packet.axes)
                                         for l in range(s, e)]
             m["codec_shape"] = [e - s, 2, H, B, S, D] if layout == "permuted" else [e - s, 2, B, S, H, D]
             m["codec_dtype"] = "uint8"
@@ -398,7 +399,7 @@ class FusedCompressionManager(CompressionManager):
         if len(dicts) != off:
             raise ValueError("Missing quantization params")
         layer_ids = list(range(start, start + off))
-        kmeta, vmeta = tables_from_dicts(dicts, H, D, B, S, device)
+        kmeta, vmeta = tables_from_dicts(dicts, H, D, B, S, device, self._axes())
         transform, seed, has_codec, bits = self._settings()
         if not all(m.get("codec_applied", False) == has_codec for m in metas):
             raise ValueError("packet codec does not match the pipeline")
@@ -412,7 +413,7 @@ class FusedCompressionManager(CompressionManager):
             ops.rans_decode_batch(items, bits)
             streams = packed
         return Packet(list(streams), chunks, kmeta, vmeta, self.profiles(layer_ids, H), B, S, H, D, bits, seed,
-                      transform, layout, layer_ids)
+                      transform, layout, layer_ids, self._axes())
 
     def _fused_decodable(self, metas) -> bool:
         m = metas[0]

@@ -1,11 +1,10 @@
 """KVServeQuantizer on gfx950 (kvserve_v1/compression/quantizer/kvserve_quantizer.py:17-294).
 
 Same configuration keys, validation, head / layer masks and metadata dicts as the
-reference; the arithmetic (bf16 per-op min-max, K per channel, V per token, heads
-reordered [low, high]) runs in the fused kernels with the transform switched off
-and 8-bit raw symbols in native order, i.e. the operator-level entry of the same
-code the fused pipeline uses.  Only axis_key="channel" and axis_value="token" run
-on the GPU kernels.
+reference; the arithmetic (bf16 per-op min-max on each part's axis -- channel, token
+or tensor, quantizer_func.py:41-49 -- heads reordered [low, high]) runs in the fused
+kernels with the transform switched off and 8-bit raw symbols in native order, i.e.
+the operator-level entry of the same code the fused pipeline uses.
 """
 
 from __future__ import annotations
@@ -67,8 +66,6 @@ class KVServeQuantizer(Quantizer):
     # ---------------------------------------------------------------- profiles
     def layer_profile(self, layer_id: int, num_heads: int):
         """Profile of `layer_id` for this worker's `num_heads` KV heads."""
-        if self.axis_key != "channel" or self.axis_value != "token":
-            raise NotImplementedError("the gfx950 quantizer computes K per channel and V per token")
         if self.split_type == "head":
             mask = tp_head_slice(self.head_scores_mask, num_heads, self.tensor_parallel_size, self.tp_rank)
             return section_profile(mask[layer_id], self.high_key_max_value, self.high_value_max_value,
@@ -78,9 +75,10 @@ class KVServeQuantizer(Quantizer):
                                    self.low_value_max_value if low else self.high_value_max_value, low)
 
     def _codec(self, H: int, D: int, S: int) -> FusedKVCodec:
-        key = (H, D, S)
+        key = (H, D, S, self.axis_key, self.axis_value)
         if key not in self._codecs:
-            self._codecs[key] = FusedKVCodec(H, D, S, bits=8, transform=False, layout="native", header=False)
+            self._codecs[key] = FusedKVCodec(H, D, S, bits=8, transform=False, layout="native", header=False,
+                                             axes=(self.axis_key, self.axis_value))
         return self._codecs[key]
 
     # ---------------------------------------------------------------- operator API
@@ -97,17 +95,18 @@ class KVServeQuantizer(Quantizer):
         packet = codec.compress([x], ids, [prof], layer_ids=[layer_id], chunk_layers=0)
         check_packet(packet)
         sym = packet.streams[0].view(2, B, S, H, D)
-        return sym, layer_dict(packet.kmeta[0], packet.vmeta[0], prof, B, S)
+        return sym, layer_dict(packet.kmeta[0], packet.vmeta[0], prof, B, S, packet.axes)
 
     def dequantize(self, layer_id: int, tensor: torch.Tensor, meta_data: Any, **kwargs) -> torch.Tensor:
         if tensor.dim() != 5 or tensor.shape[0] != 2 or tensor.dtype != torch.uint8:
             raise ValueError("expected uint8 symbols [2, num_blocks, block_size, num_heads, head_size]")
         _, B, S, H, D = tensor.shape
         prof = self.layer_profile(layer_id, H)
-        kmeta, vmeta = tables_from_dicts([meta_data], H, D, B, S, tensor.device)
+        axes = (self.axis_key, self.axis_value)
+        kmeta, vmeta = tables_from_dicts([meta_data], H, D, B, S, tensor.device, axes)
         codec = self._codec(H, D, S)
         packet = Packet([tensor.contiguous().view(-1)], [(0, 1)], kmeta, vmeta, [prof], B, S, H, D, 8, codec.seed,
-                        False, "native", [layer_id])
+                        False, "native", [layer_id], axes)
         out = torch.empty((2, B, S, H, D), dtype=torch.bfloat16, device=tensor.device)
         codec.decompress(packet, [out], torch.arange(B, dtype=torch.int32, device=tensor.device))
         check_packet(packet)

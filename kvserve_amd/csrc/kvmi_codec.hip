@@ -423,8 +423,7 @@ extern "C" int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job
     rc = mfma_kstats(g, jobs, num_jobs, max_blocks, err, st);
     if (rc) return rc;
   } else if (!quad_eligible(g)) {
-    rc = rows_kstats(g, jobs, num_jobs, max_blocks, err, st);
-    if (rc) return rc;
+    return rows_kstats(g, jobs, num_jobs, max_blocks, err, st);  // statistics of both parts + their finalize
   } else {
     // Statistics need only K: give each workgroup enough blocks that a job has at
     // most ~16 workgroups, which keeps the global atomics per channel small.

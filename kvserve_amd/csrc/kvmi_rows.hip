@@ -16,8 +16,11 @@
 // cross-lane butterflies are lane-xor exchanges inside the chunk; the FWHT stage order
 // is the oracle's (index bits from the lowest up: 4 in-lane, then across lanes).
 //
-// Compress is kstats (this file) + kstats_finalize (kvmi_codec.hip) + encode; decode
-// is one launch -- the same passes, metadata and stream layout as the other families.
+// Every quantization axis runs here (quantizer_func.py:41-49): a part on the channel
+// or tensor axis takes its statistics in a pass of its own over the job (reduced per
+// (head, channel) or per group) before encode; a part on the token axis takes them
+// inside encode, per token over the heads of a group.  Compress is stats + finalize
+// (both parts) + encode; decode is one launch.
 #include "kvmi_common.hpp"
 
 namespace kvmi {
@@ -147,11 +150,83 @@ __device__ __forceinline__ Pass pass_of(int H, const Lane& l) {
   return p;
 }
 
-// ============================================================== K statistics
+// ============================================================== per-part context
+// What a lane needs to quantize its head of one part: the part's axis, the output
+// position and statistic group of its head, the level count, the cache half and the
+// metadata table (laid out by the axis: channel [2][H][D], token [2][G][ntok],
+// tensor [2][G]).
+struct PartCtx {
+  int axis, j, grp;
+  float level;
+  Profile prof;
+  uint16_t* meta;
+};
+
+__device__ __forceinline__ PartCtx part_ctx(const Geo& g, const kvmi_layer_job& job, int part, const int* pos,
+                                            int h) {
+  PartCtx c;
+  c.axis = part_axis(g.flags, part);
+  c.prof = part_profile(job.profile, part, g.H);
+  c.j = pos[h];
+  c.grp = gld(c.prof.group + c.j);
+  c.level = (float)gld(c.prof.levels + c.j);
+  c.meta = part ? job.vmeta : job.kmeta;
+  return c;
+}
+
+// Source head -> output position of both parts, in LDS; statistic groups per part.
+__device__ __forceinline__ void positions(const kvmi_layer_job& job, int H, int* posk, int* posv) {
+  const Profile pk = part_profile(job.profile, 0, H);
+  const Profile pv = part_profile(job.profile, 1, H);
+  if ((int)threadIdx.x < H) {
+    posk[gld(pk.order + threadIdx.x)] = threadIdx.x;
+    posv[gld(pv.order + threadIdx.x)] = threadIdx.x;
+  }
+}
+__device__ __forceinline__ int group_count(const Profile& p, int H) {
+  int n = 1;
+  for (int k = 0; k < H; ++k) n = max(n, (int)gld(p.group + k) + 1);
+  return n;
+}
+
+// The lane's quantization constants of a channel- or tensor-axis part: (min, x) per
+// channel, x = 1/scale (encode) or scale (decode).
+template <bool RCP>
+__device__ __forceinline__ void part_consts(const Geo& g, const PartCtx& c, const Lane& l, float (&mn)[kSeg],
+                                            float (&x)[kSeg]) {
+  if (c.axis == kAxChannel) {
+    const int HD = g.H * g.D, e0 = l.seg_ok ? l.sub * kSeg : 0;
+    uint32_t wm[kSeg / 2], ws[kSeg / 2];
+    load_bf16_seg<kSeg>(c.meta + c.j * g.D + e0, wm);
+    load_bf16_seg<kSeg>(c.meta + HD + c.j * g.D + e0, ws);
+    unpack_bf16<kSeg>(wm, mn);
+    unpack_bf16<kSeg>(ws, x);
+  } else if (c.axis == kAxTensor) {
+    const float m = bf16_to_f32(gld(c.meta + c.grp)), s = bf16_to_f32(gld(c.meta + g.G + c.grp));
+#pragma unroll
+    for (int i = 0; i < kSeg; ++i) {
+      mn[i] = m;
+      x[i] = s;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kSeg; ++i) mn[i] = x[i] = 1.0f;  // token axis: per-token, not per-lane
+  }
+  if (RCP) {
+#pragma unroll
+    for (int i = 0; i < kSeg; ++i) x[i] = 1.0f / x[i];
+  }
+}
+
+// ============================================================== statistics
+// Pass 1 of compress for every part on the channel or tensor axis: min / max over all
+// tokens of the job, per (head, channel) or per group, reduced through LDS atomics and
+// then global atomics on order-preserving keys (part p at kstats + p * 2*H*D).
 template <int LPR>
-__global__ __launch_bounds__(kRWG) void rows_kstats_kernel(Geo g, ChunkScales cs,
-                                                           const kvmi_layer_job* __restrict__ jobs) {
-  extern __shared__ uint32_t lkey[];  // [2][H*D]: min keys, then max keys
+__global__ __launch_bounds__(kRWG) void rows_stats_kernel(Geo g, ChunkScales cs,
+                                                          const kvmi_layer_job* __restrict__ jobs) {
+  extern __shared__ uint32_t lkey[];  // [2][H*D]: min keys, then max keys (one part at a time)
+  __shared__ int pos[2][kMaxHeads];
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int B = job.num_blocks;
   const int nwg = (B + g.bpw - 1) / g.bpw;
@@ -163,64 +238,185 @@ __global__ __launch_bounds__(kRWG) void rows_kstats_kernel(Geo g, ChunkScales cs
   const Pass ps = pass_of<LPR>(H, l);
   const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
   const uint32_t sb = transform ? seg_signs(job.signs, ps.h, D, l) : 0u;
+  positions(job, H, pos[0], pos[1]);
 
-  for (int i = threadIdx.x; i < HD; i += kRWG) {
-    lkey[i] = 0xffffffffu;
-    lkey[HD + i] = 0u;
-  }
-  float mn[kSeg], mx[kSeg];
 #pragma unroll
-  for (int i = 0; i < kSeg; ++i) {
-    mn[i] = __builtin_inff();
-    mx[i] = -__builtin_inff();
-  }
-  const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
-  bool any = false;
-  for (int64_t r0 = 0; r0 < rows; r0 += ps.RP) {
-    const RowPos rp = row_pos(job, blk0, rows, r0 + l.slot, S, H);
-    if (ps.on && rp.active) {
-      float y[kSeg];
-      load_transform<LPR, false>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
-      any = true;
-#pragma unroll
-      for (int i = 0; i < kSeg; ++i) {
-        mn[i] = fminf(mn[i], y[i]);
-        mx[i] = fmaxf(mx[i], y[i]);
-      }
-    }
-  }
-  __syncthreads();
-  // channel c = seg * 16 + i (seg = c / 16) sits at seg * 16 + (i + seg) % 16, so that
-  // the lanes of one atomic instruction (same i, different segments) use different banks
-  if (any && l.seg_ok) {
-    const int seg = (ps.h * D) / kSeg + l.sub;
+  for (int part = 0; part < 2; ++part) {
+    const int axis = part_axis(g.flags, part);
+    if (axis == kAxToken) continue;  // uniform: per-token statistics are taken in encode
+    float mn[kSeg], mx[kSeg];
 #pragma unroll
     for (int i = 0; i < kSeg; ++i) {
-      const int slot = seg * kSeg + ((i + seg) & (kSeg - 1));
-      atomicMin(&lkey[slot], f2key(mn[i]));
-      atomicMax(&lkey[HD + slot], f2key(mx[i]));
+      mn[i] = __builtin_inff();
+      mx[i] = -__builtin_inff();
     }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < HD; i += kRWG) {
-    const int seg = i / kSeg, slot = seg * kSeg + ((i + seg) & (kSeg - 1));
-    const uint32_t kmn = lkey[slot], kmx = lkey[HD + slot];
-    if (kmn != 0xffffffffu) atomicMin(&job.kstats[i], kmn);
-    if (kmx != 0u) atomicMax(&job.kstats[HD + i], kmx);
+    const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool) + part * job.pool_part_stride;
+    bool any = false;
+    for (int64_t r0 = 0; r0 < rows; r0 += ps.RP) {
+      const RowPos rp = row_pos(job, blk0, rows, r0 + l.slot, S, H);
+      if (ps.on && rp.active) {
+        float y[kSeg];
+        load_transform<LPR, false>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
+        any = true;
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+          mn[i] = fminf(mn[i], y[i]);
+          mx[i] = fmaxf(mx[i], y[i]);
+        }
+      }
+    }
+    __syncthreads();  // the previous part's flush has read the LDS keys; positions are visible
+    const int nkeys = axis == kAxChannel ? HD : g.G;
+    for (int i = threadIdx.x; i < nkeys; i += kRWG) {
+      lkey[i] = 0xffffffffu;
+      lkey[HD + i] = 0u;
+    }
+    __syncthreads();
+    if (axis == kAxChannel) {
+      // channel c = seg * 16 + i (seg = c / 16) sits at seg * 16 + (i + seg) % 16, so
+      // that the lanes of one atomic (same i, different segments) use different banks
+      if (any && l.seg_ok) {
+        const int seg = (ps.h * D) / kSeg + l.sub;
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+          const int slot = seg * kSeg + ((i + seg) & (kSeg - 1));
+          atomicMin(&lkey[slot], f2key(mn[i]));
+          atomicMax(&lkey[HD + slot], f2key(mx[i]));
+        }
+      }
+    } else {
+      float a = __builtin_inff(), b = -__builtin_inff();
+      if (l.seg_ok) {
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+          a = fminf(a, mn[i]);
+          b = fmaxf(b, mx[i]);
+        }
+      }
+      if (any) {  // rows are whole: every lane of a row has the same `any`
+        a = row_min<LPR>(a);
+        b = row_max<LPR>(b);
+        if (l.sub == 0) {
+          const Profile pr = part_profile(job.profile, part, H);
+          const int grp = gld(pr.group + pos[part][ps.h]);
+          atomicMin(&lkey[grp], f2key(a));
+          atomicMax(&lkey[HD + grp], f2key(b));
+        }
+      }
+    }
+    __syncthreads();
+    uint32_t* keys = job.kstats + part * 2 * HD;
+    for (int i = threadIdx.x; i < nkeys; i += kRWG) {
+      const int slot = axis == kAxChannel ? (i / kSeg) * kSeg + ((i + i / kSeg) & (kSeg - 1)) : i;
+      const uint32_t kmn = lkey[slot], kmx = lkey[HD + slot];
+      if (kmn != 0xffffffffu) atomicMin(&keys[i], kmn);
+      if (kmx != 0u) atomicMax(&keys[HD + i], kmx);
+    }
   }
 }
 
-// Source head -> output position of both parts, in LDS.
-__device__ __forceinline__ void positions(const kvmi_layer_job& job, int H, int* posk, int* posv) {
-  const Profile pk = part_profile(job.profile, 0, H);
-  const Profile pv = part_profile(job.profile, 1, H);
-  if ((int)threadIdx.x < H) {
-    posk[gld(pk.order + threadIdx.x)] = threadIdx.x;
-    posv[gld(pv.order + threadIdx.x)] = threadIdx.x;
+// Pass 1b, one workgroup per job: keys -> metadata of every channel- or tensor-axis
+// part (bf16 min and scale), keys re-initialised.  Its own launch, so every
+// workgroup's atomics of pass 1 are visible without a device-wide fence.
+__global__ __launch_bounds__(kRWG) void rows_finalize_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs) {
+  const kvmi_layer_job job = jobs[blockIdx.x];
+  if (job.num_blocks <= 0) return;  // nothing accumulated: the metadata is left as it is
+  const int H = g.H, D = g.D, HD = H * D;
+  __shared__ int pos[kMaxHeads];
+  __shared__ uint8_t lev[kMaxHeads];
+  __shared__ uint8_t glev[kMaxHeads];
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const int axis = part_axis(g.flags, part);
+    if (axis == kAxToken) continue;
+    const Profile pr = part_profile(job.profile, part, H);
+    __syncthreads();  // the previous part is done with the tables
+    if ((int)threadIdx.x < H) {
+      const int k = threadIdx.x;
+      pos[gld(pr.order + k)] = k;
+      lev[k] = gld(pr.levels + k);
+      glev[gld(pr.group + k)] = gld(pr.levels + k);  // one level count per group
+    }
+    __syncthreads();
+    uint32_t* keys = job.kstats + part * 2 * HD;
+    uint16_t* meta = part ? job.vmeta : job.kmeta;
+    if (axis == kAxChannel) {
+      for (int i = threadIdx.x; i < HD; i += kRWG) {
+        const int j = pos[i / D], e = i % D;
+        const float kmn = round_bf16(key2f(gld(keys + i)));
+        const float kmx = round_bf16(key2f(gld(keys + HD + i)));
+        gst(meta + j * D + e, (uint16_t)f32_to_bf16_bits(kmn));
+        gst(meta + HD + j * D + e, (uint16_t)f32_to_bf16_bits(quant_scale(kmn, kmx, lev[j])));
+        gst(keys + i, 0xffffffffu);
+        gst(keys + HD + i, 0u);
+      }
+    } else {
+      const int ng = group_count(pr, H);
+      for (int i = threadIdx.x; i < ng; i += kRWG) {
+        const float kmn = round_bf16(key2f(gld(keys + i)));
+        const float kmx = round_bf16(key2f(gld(keys + HD + i)));
+        gst(meta + i, (uint16_t)f32_to_bf16_bits(kmn));
+        gst(meta + g.G + i, (uint16_t)f32_to_bf16_bits(quant_scale(kmn, kmx, glev[i])));
+        gst(keys + i, 0xffffffffu);
+        gst(keys + HD + i, 0u);
+      }
+    }
   }
 }
 
 // ============================================================== encode
+// Per-token statistics of one part over the heads of each group (token axis): row
+// min / max -> LDS, then one thread per (token of the pass, group) forms (min, 1/scale)
+// and writes the part's token table.  Every thread of the workgroup calls this.
+template <int LPR>
+__device__ __forceinline__ float2 token_stats(const Geo& g, const kvmi_layer_job& job, const PartCtx& c,
+                                              const Lane& l, const Pass& ps, const float (&y)[kSeg], bool act,
+                                              int64_t r0, int64_t rows, int blk0, int ngroups, float2* rowmm,
+                                              float2* tokq) {
+  const int H = g.H, G = g.G, tid = threadIdx.x;
+  if (act) {
+    float lmn = __builtin_inff(), lmx = -__builtin_inff();
+    if (l.seg_ok) {
+#pragma unroll
+      for (int i = 0; i < kSeg; ++i) {
+        lmn = fminf(lmn, y[i]);
+        lmx = fmaxf(lmx, y[i]);
+      }
+    }
+    lmn = row_min<LPR>(lmn);
+    lmx = row_max<LPR>(lmx);
+    if (l.sub == 0) rowmm[l.slot] = make_float2(lmn, lmx);
+  }
+  __syncthreads();
+  const int tpp = ps.RP / H;  // tokens per pass
+  if (tid < tpp * G) {
+    const int tp = tid / G, gg = tid % G;
+    const int64_t rr = r0 + (int64_t)tp * H;
+    if (gg < ngroups && rr < rows) {
+      float mn = __builtin_inff(), mx = -__builtin_inff();
+      int lv = 2;
+      for (int k = 0; k < H; ++k) {
+        if (gld(c.prof.group + k) == gg) {
+          const float2 m = rowmm[tp * H + gld(c.prof.order + k)];
+          mn = fminf(mn, m.x);
+          mx = fmaxf(mx, m.y);
+          lv = gld(c.prof.levels + k);
+        }
+      }
+      const float sc = quant_scale(mn, mx, lv);
+      tokq[tid] = make_float2(mn, 1.0f / sc);
+      const int64_t ntok = (int64_t)job.num_blocks * g.S;
+      const RowPos tpz = row_pos(job, blk0, rows, rr, g.S, H);
+      gst(c.meta + (int64_t)gg * ntok + tpz.tok, (uint16_t)f32_to_bf16_bits(mn));
+      gst(c.meta + (int64_t)(G + gg) * ntok + tpz.tok, (uint16_t)f32_to_bf16_bits(sc));
+    }
+  }
+  __syncthreads();
+  const float2 q = act ? tokq[(l.slot / H) * G + c.grp] : make_float2(0.0f, 1.0f);
+  __syncthreads();  // rowmm / tokq are reused by the next call
+  return q;
+}
+
 template <int LPR, int BITS>
 __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs,
                                                            const kvmi_layer_job* __restrict__ jobs,
@@ -235,123 +431,62 @@ __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs
       write_stream_header(job.stream, BITS, job.chunk_symbols);
     return;
   }
-  const int H = g.H, S = g.S, D = g.D, HD = H * D, G = g.G;
+  const int H = g.H, S = g.S, D = g.D;
   const int blk0 = blockIdx.x * g.bpw;
   const int64_t rows = (int64_t)(min(B, blk0 + g.bpw) - blk0) * S * H;
   const Lane l = lane_of<LPR>(D, cs);
   const Pass ps = pass_of<LPR>(H, l);
-  const int tid = threadIdx.x;
   const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
   const uint32_t sb = transform ? seg_signs(job.signs, ps.h, D, l) : 0u;
-  const Profile pk = part_profile(job.profile, 0, H);
-  const Profile pv = part_profile(job.profile, 1, H);
 
-  __shared__ int posk[kMaxHeads], posv[kMaxHeads];
-  __shared__ float2 rowmm[P];  // V row (min, max) by slot
-  __shared__ float2 tokq[P];   // V (min, 1/scale) by (token of pass, group)
-  positions(job, H, posk, posv);
-  if (tid == 0 && job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER))
+  __shared__ int pos[2][kMaxHeads];
+  __shared__ float2 rowmm[P];  // row (min, max) by slot
+  __shared__ float2 tokq[P];   // (min, 1/scale) by (token of pass, group)
+  positions(job, H, pos[0], pos[1]);
+  if (threadIdx.x == 0 && job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER))
     write_stream_header(job.stream, BITS, job.chunk_symbols);
-  int ngroups = 1;
-  for (int k = 0; k < H; ++k) ngroups = max(ngroups, (int)gld(pv.group + k) + 1);
   __syncthreads();
 
-  const int jk = posk[ps.h], jv = posv[ps.h];
-  // K constants of the lane's 16 channels: (min, 1/scale) of output position jk
-  float kmn[kSeg], krc[kSeg];
-  {
-    const int e0 = l.seg_ok ? l.sub * kSeg : 0;
-    uint32_t wm[kSeg / 2], ws[kSeg / 2];
-    load_bf16_seg<kSeg>(job.kmeta + jk * D + e0, wm);
-    load_bf16_seg<kSeg>(job.kmeta + HD + jk * D + e0, ws);
+  PartCtx ctx[2];
+  float cmn[2][kSeg], crc[2][kSeg];
+  int ngroups[2];
 #pragma unroll
-    for (int i = 0; i < kSeg / 2; ++i) {
-      kmn[2 * i] = bf_lo(wm[i]);
-      kmn[2 * i + 1] = bf_hi(wm[i]);
-      krc[2 * i] = 1.0f / bf_lo(ws[i]);
-      krc[2 * i + 1] = 1.0f / bf_hi(ws[i]);
-    }
+  for (int part = 0; part < 2; ++part) {
+    ctx[part] = part_ctx(g, job, part, pos[part], ps.h);
+    part_consts<true>(g, ctx[part], l, cmn[part], crc[part]);
+    ngroups[part] = group_count(ctx[part].prof, H);
   }
-  const float lk = (float)gld(pk.levels + jk);
-  const float lvv = (float)gld(pv.levels + jv);
-  const int gv = gld(pv.group + jv);
-  const int tpp = ps.RP / H;  // tokens per pass
-  const uint16_t* poolK = reinterpret_cast<const uint16_t*>(job.pool);
-  const uint16_t* poolV = poolK + job.pool_part_stride;
-  const int64_t ntok = (int64_t)B * S;
   uint32_t over = 0;
 
   for (int64_t r0 = 0; r0 < rows; r0 += ps.RP) {
     const RowPos rp = row_pos(job, blk0, rows, r0 + l.slot, S, H);
     const bool act = ps.on && rp.active;  // uniform over the lanes of a row
-    // ---------------- K: per-channel statistics from the kstats pass
-    if (act) {
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+      const PartCtx& c = ctx[part];
+      const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool) + part * job.pool_part_stride;
       float y[kSeg];
-      load_transform<LPR, true>(poolK + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
-      if (l.seg_ok) {
+      if (act) load_transform<LPR, true>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
+      if (c.axis == kAxToken) {  // uniform over the workgroup
+        const float2 q = token_stats<LPR>(g, job, c, l, ps, y, act, r0, rows, blk0, ngroups[part], rowmm, tokq);
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) {
+          cmn[part][i] = q.x;
+          crc[part][i] = q.y;
+        }
+      }
+      if (act && l.seg_ok) {
         uint32_t s[kSeg];
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
-          s[i] = (uint32_t)quant_value(y[i], kmn[i], krc[i], lk);
+          s[i] = (uint32_t)quant_value(y[i], cmn[part][i], crc[part][i], c.level);
           over |= s[i];
         }
         Packed<kSeg, BITS> pkd;
         pack_syms<kSeg, BITS>(s, pkd);
-        store_packed<kSeg, BITS>(seg_addr<BITS>(job, g, 0, jk, rp.tok, l.sub * kSeg), pkd);
+        store_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), pkd);
       }
     }
-    // ---------------- V: per-token statistics over the heads of a group
-    float y[kSeg];
-    if (act) {
-      load_transform<LPR, true>(poolV + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
-      float lmn = __builtin_inff(), lmx = -__builtin_inff();
-      if (l.seg_ok) {
-#pragma unroll
-        for (int i = 0; i < kSeg; ++i) {
-          lmn = fminf(lmn, y[i]);
-          lmx = fmaxf(lmx, y[i]);
-        }
-      }
-      lmn = row_min<LPR>(lmn);
-      lmx = row_max<LPR>(lmx);
-      if (l.sub == 0) rowmm[l.slot] = make_float2(lmn, lmx);
-    }
-    __syncthreads();
-    if (tid < tpp * G) {
-      const int tp = tid / G, gg = tid % G;
-      const int64_t rr = r0 + (int64_t)tp * H;
-      if (gg < ngroups && rr < rows) {
-        float mn = __builtin_inff(), mx = -__builtin_inff();
-        int lv = 2;
-        for (int k = 0; k < H; ++k) {
-          if (gld(pv.group + k) == gg) {
-            const float2 m = rowmm[tp * H + gld(pv.order + k)];
-            mn = fminf(mn, m.x);
-            mx = fmaxf(mx, m.y);
-            lv = gld(pv.levels + k);
-          }
-        }
-        const float sc = quant_scale(mn, mx, lv);
-        tokq[tid] = make_float2(mn, 1.0f / sc);
-        const RowPos tpz = row_pos(job, blk0, rows, rr, S, H);
-        gst(job.vmeta + (int64_t)gg * ntok + tpz.tok, (uint16_t)f32_to_bf16_bits(mn));
-        gst(job.vmeta + (int64_t)(G + gg) * ntok + tpz.tok, (uint16_t)f32_to_bf16_bits(sc));
-      }
-    }
-    __syncthreads();
-    if (act && l.seg_ok) {
-      const float2 c = tokq[(l.slot / H) * G + gv];
-      uint32_t s[kSeg];
-#pragma unroll
-      for (int i = 0; i < kSeg; ++i) {
-        s[i] = (uint32_t)quant_value(y[i], c.x, c.y, lvv);
-        over |= s[i];
-      }
-      Packed<kSeg, BITS> pkd;
-      pack_syms<kSeg, BITS>(s, pkd);
-      store_packed<kSeg, BITS>(seg_addr<BITS>(job, g, 1, jv, rp.tok, l.sub * kSeg), pkd);
-    }
-    __syncthreads();
   }
   if (over >> BITS) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
 }
@@ -365,11 +500,10 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
   const int B = job.num_blocks;
   const int nwg = (B + g.bpw - 1) / g.bpw;
   if ((int)blockIdx.x >= nwg) return;
-  const int H = g.H, S = g.S, D = g.D, HD = H * D, G = g.G;
-  const int tid = threadIdx.x;
-  __shared__ int posk[kMaxHeads], posv[kMaxHeads];
+  const int H = g.H, S = g.S, D = g.D, G = g.G;
+  __shared__ int pos[2][kMaxHeads];
   __shared__ int ok;
-  if (tid == 0) {
+  if (threadIdx.x == 0) {
     int good = 1;
     if (!(g.flags & KVMI_F_NO_HEADER)) {
       good = header_matches(job.stream, BITS, job.chunk_symbols);
@@ -377,7 +511,7 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
     }
     ok = good;
   }
-  positions(job, H, posk, posv);
+  positions(job, H, pos[0], pos[1]);
   __syncthreads();
   if (!ok) return;
 
@@ -387,20 +521,13 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
   const Pass ps = pass_of<LPR>(H, l);
   const bool transform = !(g.flags & KVMI_F_NO_TRANSFORM);
   const uint32_t sb = transform ? seg_signs(job.signs, ps.h, D, l) : 0u;
-  const int jk = posk[ps.h], jv = posv[ps.h];
-  const Profile pv = part_profile(job.profile, 1, H);
-  const int gv = gld(pv.group + jv);
-  float kmn[kSeg], ksc[kSeg];
-  {
-    const int e0 = l.seg_ok ? l.sub * kSeg : 0;
-    uint32_t wm[kSeg / 2], ws[kSeg / 2];
-    load_bf16_seg<kSeg>(job.kmeta + jk * D + e0, wm);
-    load_bf16_seg<kSeg>(job.kmeta + HD + jk * D + e0, ws);
-    unpack_bf16<kSeg>(wm, kmn);
-    unpack_bf16<kSeg>(ws, ksc);
+  PartCtx ctx[2];
+  float cmn[2][kSeg], csc[2][kSeg];
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    ctx[part] = part_ctx(g, job, part, pos[part], ps.h);
+    part_consts<false>(g, ctx[part], l, cmn[part], csc[part]);
   }
-  uint16_t* poolK = reinterpret_cast<uint16_t*>(job.pool);
-  uint16_t* poolV = poolK + job.pool_part_stride;
   const int64_t ntok = (int64_t)B * S;
 
   for (int64_t r0 = 0; r0 < rows; r0 += ps.RP) {
@@ -408,24 +535,25 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
     if (!(ps.on && rp.active)) continue;  // rows are whole: every lane of a row agrees
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
+      const PartCtx& c = ctx[part];
       uint32_t s[kSeg];
       if (l.seg_ok) {
         Packed<kSeg, BITS> pkd;
-        load_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, part ? jv : jk, rp.tok, l.sub * kSeg), pkd);
+        load_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), pkd);
         unpack_syms<kSeg, BITS>(pkd, s);
       } else {
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) s[i] = 0u;
       }
       float x[kSeg];
-      if (part == 0) {
-#pragma unroll
-        for (int i = 0; i < kSeg; ++i) x[i] = dequant_value((float)s[i], kmn[i], ksc[i]);
-      } else {
-        const float mn = bf16_to_f32(gld(job.vmeta + (int64_t)gv * ntok + rp.tok));
-        const float sc = bf16_to_f32(gld(job.vmeta + (int64_t)(G + gv) * ntok + rp.tok));
+      if (c.axis == kAxToken) {
+        const float mn = bf16_to_f32(gld(c.meta + (int64_t)c.grp * ntok + rp.tok));
+        const float sc = bf16_to_f32(gld(c.meta + (int64_t)(G + c.grp) * ntok + rp.tok));
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) x[i] = dequant_value((float)s[i], mn, sc);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kSeg; ++i) x[i] = dequant_value((float)s[i], cmn[part][i], csc[part][i]);
       }
       uint32_t w[kSeg / 2];
       if (transform) {
@@ -437,7 +565,10 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
 #pragma unroll
         for (int i = 0; i < kSeg / 2; ++i) w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
       }
-      if (l.seg_ok) store_bf16_seg<kSeg>((part ? poolV : poolK) + rp.pool_row * D + l.sub * kSeg, w);
+      if (l.seg_ok)
+        store_bf16_seg<kSeg>(reinterpret_cast<uint16_t*>(job.pool) + part * job.pool_part_stride +
+                                 rp.pool_row * D + l.sub * kSeg,
+                             w);
     }
   }
 }
@@ -488,9 +619,9 @@ void set_rows_bpw(Geo* g, int32_t max_blocks, bool stats) {
 }
 
 template <int LPR>
-void launch_kstats(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, hipStream_t st) {
+void launch_stats(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, hipStream_t st) {
   const size_t lds = (size_t)2 * g.H * g.D * sizeof(uint32_t);
-  hipLaunchKernelGGL((rows_kstats_kernel<LPR>), grid, dim3(kRWG), lds, st, g, chunk_scales(), jobs);
+  hipLaunchKernelGGL((rows_stats_kernel<LPR>), grid, dim3(kRWG), lds, st, g, chunk_scales(), jobs);
 }
 template <int LPR, int BITS>
 void launch_encode(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
@@ -567,13 +698,16 @@ int rows_kstats(const Geo& g0, const kvmi_layer_job* jobs, int32_t num_jobs, int
   Geo g = g0;
   set_rows_bpw(&g, max_blocks, true);
   const dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
+  if (part_axis(g.flags, 0) == kAxToken && part_axis(g.flags, 1) == kAxToken) return KVMI_OK;  // nothing to reduce
   switch (next_pow2(g.D / kSeg)) {
-    case 1: launch_kstats<1>(g, grid, jobs, st); break;
-    case 2: launch_kstats<2>(g, grid, jobs, st); break;
-    case 4: launch_kstats<4>(g, grid, jobs, st); break;
-    case 8: launch_kstats<8>(g, grid, jobs, st); break;
-    default: launch_kstats<16>(g, grid, jobs, st); break;
+    case 1: launch_stats<1>(g, grid, jobs, st); break;
+    case 2: launch_stats<2>(g, grid, jobs, st); break;
+    case 4: launch_stats<4>(g, grid, jobs, st); break;
+    case 8: launch_stats<8>(g, grid, jobs, st); break;
+    default: launch_stats<16>(g, grid, jobs, st); break;
   }
+  if (hipGetLastError() != hipSuccess) return KVMI_ELAUNCH;
+  hipLaunchKernelGGL(rows_finalize_kernel, dim3((unsigned)num_jobs), dim3(kRWG), 0, st, g, jobs);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 

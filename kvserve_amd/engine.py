@@ -46,6 +46,9 @@ def _stream_handle() -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+DEFAULT_AXES = ("channel", "token")  # (axis_key, axis_value): kvserve_quantizer.py defaults
+
+
 class _SignCache:
     """Per-(seed, layer, H, D) device sign tables, like the reference's signs_cache
     (hadamard_func.py:130-159)."""
@@ -87,6 +90,7 @@ class Packet:
     transform: bool
     layout: str
     layer_ids: List[int]
+    axes: Tuple[str, str] = DEFAULT_AXES  # (axis_key, axis_value): how kmeta / vmeta are laid out
 
     @property
     def num_layers(self) -> int:
@@ -97,6 +101,15 @@ class Packet:
 
     def compressed_bytes(self) -> int:
         return sum(int(s.numel()) for s in self.streams)
+
+
+AXES = ("channel", "token", "tensor")
+
+
+def meta_shape(axis: str, H: int, D: int, G: int, ntok: int) -> Tuple[int, int]:
+    """(rows, cols) of one layer's [min, scale] table of a part on `axis`: per channel
+    by output position, per token by group, or one pair per group."""
+    return {"channel": (H, D), "token": (G, ntok), "tensor": (G, 1)}[axis]
 
 
 MAX_HEADS = 64        # kvmi_common.hpp kMaxHeads
@@ -132,7 +145,8 @@ class FusedKVCodec:
 
     def __init__(self, num_heads: int, head_dim: int, block_size: int, bits: int = 4,
                  seed: int = DEFAULT_SEED, transform: bool = True, layout: str = "permuted",
-                 header: bool = True, fwht: Optional[str] = None, compress_path: Optional[str] = None):
+                 header: bool = True, fwht: Optional[str] = None, compress_path: Optional[str] = None,
+                 axes: Tuple[str, str] = DEFAULT_AXES):
         if type(bits) is not int or not 1 <= bits <= 8:
             raise ValueError("bitpack_bits must be an integer in [1, 8]")
         check_geometry(num_heads, head_dim)
@@ -140,6 +154,10 @@ class FusedKVCodec:
             raise ValueError("layout must be 'permuted' or 'native'")
         if not header and bits != 8:
             raise ValueError("a stream without header carries raw 8-bit symbols")
+        axes = tuple(axes)
+        if len(axes) != 2 or any(a not in AXES for a in axes):
+            raise ValueError("axes must be (axis_key, axis_value), each 'channel', 'token' or 'tensor'")
+        self.axes = axes
         self.H, self.D, self.S, self.bits = num_heads, head_dim, block_size, bits
         self.seed, self.transform, self.layout, self.header = int(seed), transform, layout, header
         # Hadamard on MFMA (default) or the register FWHT kernels (KVSERVE_AMD_FWHT=valu)
@@ -167,7 +185,17 @@ class FusedKVCodec:
             f |= _lib.F_VALU_FWHT
         if max_level > 128:
             f |= _lib.F_CLAMP_LEVELS
+        f |= {"channel": 0, "token": _lib.F_K_TOKEN, "tensor": _lib.F_K_TENSOR}[self.axes[0]]
+        f |= {"token": 0, "channel": _lib.F_V_CHANNEL, "tensor": _lib.F_V_TENSOR}[self.axes[1]]
         return f
+
+    def _groups_of(self, p: LayerProfile) -> int:
+        """Statistic groups the metadata of profile p needs: V's groups, and K's when K
+        shares statistics over groups (token / tensor axis)."""
+        n = p.num_v_groups()
+        if self.axes[0] != "channel":
+            n = max(n, max(p.k_groups()) + 1)
+        return n
 
     def _geometry(self, groups: int, max_level: int) -> _lib.Geometry:
         g = _lib.Geometry()
@@ -176,11 +204,13 @@ class FusedKVCodec:
         return g
 
     def _kstats_scratch(self, L: int, device) -> torch.Tensor:
-        """uint32 keys [L, 2, H, D] = {0xFFFFFFFF, 0}.  The kernels leave them
-        initialised, so a plan reuses its own set on every run."""
-        keys = torch.empty((L, 2, self.H, self.D), dtype=torch.int32, device=device)
-        keys[:, 0].fill_(-1)
-        keys[:, 1].zero_()
+        """uint32 keys [L, 2, H, D] = {0xFFFFFFFF, 0} ([L, 2 parts, 2, H, D] when V takes
+        a statistics pass too).  The kernels leave them initialised, so a plan reuses
+        its own set on every run."""
+        parts = 2 if self.axes[1] != "token" else 1
+        keys = torch.empty((L, parts, 2, self.H, self.D), dtype=torch.int32, device=device)
+        keys[:, :, 0].fill_(-1)
+        keys[:, :, 1].zero_()
         return keys
 
     def _check_pools(self, pools: Sequence[torch.Tensor]) -> torch.device:
@@ -260,7 +290,7 @@ class FusedKVCodec:
         if len(profiles) != L:
             raise ValueError("one profile per layer is required")
         for p in profiles:
-            p.validate(self.H)
+            p.validate(self.H, k_groups=self.axes[0] != "channel")
         layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
         ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
         B = int(ids.numel())
@@ -272,10 +302,10 @@ class FusedKVCodec:
             chunks = [(0, L)]
         else:
             chunks = [(s, min(s + chunk_layers, L)) for s in range(0, L, chunk_layers)]
-        G = max(p.num_v_groups() for p in profiles)
+        G = max(self._groups_of(p) for p in profiles)
         if groups is not None:
             if not G <= int(groups) <= H:
-                raise ValueError("groups must cover every layer's V groups and be <= num_heads")
+                raise ValueError("groups must cover every layer's statistic groups and be <= num_heads")
             G = int(groups)
         hdr = 16 if self.header else 0
         streams = []
@@ -284,12 +314,14 @@ class FusedKVCodec:
             streams.append(torch.empty(hdr + (n * self.bits + 7) // 8, dtype=torch.uint8, device=dev))
         # both metadata tables live in one allocation: the reference's per-section
         # dicts are views of it, and the wire bundle ships it without a copy
-        kn, vn = L * 2 * H * D, L * 2 * G * B * S
+        kshape = meta_shape(self.axes[0], H, D, G, B * S)
+        vshape = meta_shape(self.axes[1], H, D, G, B * S)
+        kn, vn = L * 2 * kshape[0] * kshape[1], L * 2 * vshape[0] * vshape[1]
         meta_buf = torch.empty(kn + vn, dtype=torch.bfloat16, device=dev)
-        kmeta = meta_buf[:kn].view(L, 2, H, D)
-        vmeta = meta_buf[kn:].view(L, 2, G, B * S)
+        kmeta = meta_buf[:kn].view(L, 2, *kshape)
+        vmeta = meta_buf[kn:].view(L, 2, *vshape)
         packet = Packet(streams, chunks, kmeta, vmeta, list(profiles), B, S, H, D, self.bits, self.seed,
-                        self.transform, self.layout, layer_ids)
+                        self.transform, self.layout, layer_ids, self.axes)
         if B == 0 and self.header:
             for st in streams:
                 st.copy_(torch.from_numpy(_header_bytes(self.bits, 0)).to(dev))
@@ -305,6 +337,14 @@ class FusedKVCodec:
             raise ValueError("packet geometry does not match this codec")
         if (packet.seed, packet.transform, packet.layout) != (self.seed, self.transform, self.layout):
             raise ValueError("packet transform / layout does not match this codec")
+        if tuple(packet.axes) != self.axes:
+            raise ValueError("packet quantization axes do not match this codec")
+        G = packet.vmeta.shape[2] if self.axes[1] != "channel" else (
+            packet.kmeta.shape[2] if self.axes[0] != "channel" else 1)
+        for name, t, axis in (("kmeta", packet.kmeta, self.axes[0]), ("vmeta", packet.vmeta, self.axes[1])):
+            want = (packet.num_layers, 2) + meta_shape(axis, self.H, self.D, G, packet.num_blocks * self.S)
+            if tuple(t.shape) != want:
+                raise ValueError(f"{name} must be {list(want)} for axis {axis!r}, got {list(t.shape)}")
         ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
         if ids.numel() < packet.num_blocks:
             raise ValueError("fewer block ids than compressed blocks")
@@ -375,7 +415,7 @@ class Plan:
                                 self.signs, self.prof, self.keys, B)
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
-        self.geo = codec._geometry(packet.vmeta.shape[2], max_level)
+        self.geo = codec._geometry(packet_groups(packet), max_level)
         packet.__dict__["_err"] = self.err
         self._init_workspace()
 
@@ -460,6 +500,15 @@ class BatchPlan:
     run = Plan.run
     error_code = Plan.error_code
     check_errors = Plan.check_errors
+
+
+def packet_groups(packet: Packet) -> int:
+    """G of a packet's metadata layout: the group rows of a token- or tensor-axis table
+    (1 when both parts are on the channel axis)."""
+    for t, axis in ((packet.vmeta, packet.axes[1]), (packet.kmeta, packet.axes[0])):
+        if axis != "channel":
+            return int(t.shape[2])
+    return 1
 
 
 def raise_device_error(code: int) -> None:

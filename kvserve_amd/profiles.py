@@ -140,20 +140,24 @@ class LayerProfile:
         a[1, 0], a[1, 1], a[1, 2] = self.v_order, self.v_levels, self.v_group
         return a
 
-    def validate(self, H: int) -> None:
+    def validate(self, H: int, k_groups: bool = False) -> None:
+        """k_groups: K shares statistics over its groups too (token / tensor axis), so
+        its groups obey the rules of V's."""
         for name, arr in (("k_order", self.k_order), ("v_order", self.v_order)):
             if sorted(arr) != list(range(H)):
                 raise ValueError(f"{name} must be a permutation of range({H})")
         for lv in list(self.k_levels) + list(self.v_levels):
             if not 2 <= int(lv) <= 255:
                 raise ValueError("levels (max_value) must be in [2, 255]")
-        g = list(self.v_group)
-        if g[0] != 0 or any(b not in (a, a + 1) for a, b in zip(g, g[1:])):
-            raise ValueError("V groups must be contiguous runs numbered from 0")
-        for gi in set(g):
-            lv = {self.v_levels[j] for j in range(H) if g[j] == gi}
-            if len(lv) != 1:
-                raise ValueError("all heads of a V group share one level count")
+        parts = [("V", list(self.v_group), self.v_levels)]
+        if k_groups:
+            parts.append(("K", list(self.k_groups()), self.k_levels))
+        for name, g, levels in parts:
+            if len(g) != H or g[0] != 0 or any(b not in (a, a + 1) for a, b in zip(g, g[1:])):
+                raise ValueError(f"{name} groups must be contiguous runs numbered from 0")
+            for gi in set(g):
+                if len({levels[j] for j in range(H) if g[j] == gi}) != 1:
+                    raise ValueError(f"all heads of a {name} group share one level count")
 
 
 def section_profile(low_mask_row: Sequence[bool], hk: int, hv: int, lk: int, lv: int) -> LayerProfile:

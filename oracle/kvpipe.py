@@ -205,10 +205,15 @@ def layer_split_profile(is_low: bool, H: int, hk: int, hv: int, lk: int, lv: int
 
 
 # ------------------------------------------------------------------ one layer
+AXES = ("channel", "token", "tensor")
+DEFAULT_AXES = ("channel", "token")  # (axis_key, axis_value), kvserve_quantizer.py defaults
+
+
 @dataclass
 class LayerMeta:
-    """Quantization metadata of one layer as bf16 values (float32 arrays).
-    kmin/kscale: [H', D] by output position.  vmin/vscale: [G, B*S] by group."""
+    """Quantization metadata of one layer as bf16 values (float32 arrays), per part by
+    its axis: "channel" [H', D] by output position; "token" [G, B*S] by statistic
+    group; "tensor" [G, 1] by group.  (kmin, kscale) for K, (vmin, vscale) for V."""
 
     kmin: np.ndarray
     kscale: np.ndarray
@@ -216,49 +221,74 @@ class LayerMeta:
     vscale: np.ndarray
 
 
-def quantize_layer(y: np.ndarray, prof: LayerProfile) -> Tuple[np.ndarray, LayerMeta]:
+def _group_runs(part: PartProfile) -> List[Tuple[int, int]]:
+    """[lo, hi) output positions of each statistic group, in group order."""
+    runs = []
+    for g in sorted(set(part.group)):
+        js = [j for j, gg in enumerate(part.group) if gg == g]
+        assert js == list(range(js[0], js[-1] + 1)), "groups are contiguous runs of output positions"
+        runs.append((js[0], js[-1] + 1))
+    return runs
+
+
+def quantize_part(x: np.ndarray, part: PartProfile, axis: str) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """KVServeQuantizer.quantize's section loop (kvserve_quantizer.py:202-214) for one
+    part: x bf16-valued float32 [B, S, H, D] in output order; quantizer_func.quantize on
+    each section with its axis (quantizer_func.py:41-49).  A channel-axis section has
+    per-(head, channel) statistics, so each head is its own section there."""
+    B, S, H, D = x.shape
+    out = np.empty(x.shape, np.uint8)
+    if axis == "channel":
+        mn_t, sc_t = np.empty((H, D), np.float32), np.empty((H, D), np.float32)
+        for j in range(H):
+            sym, mn, sc = quantize(part.levels[j], x[:, :, j:j + 1, :], "channel")
+            out[:, :, j:j + 1, :] = sym
+            mn_t[j], sc_t[j] = mn[0, 0, 0], sc[0, 0, 0]
+        return out, mn_t, sc_t
+    runs = _group_runs(part)
+    n = B * S if axis == "token" else 1
+    mn_t, sc_t = np.empty((len(runs), n), np.float32), np.empty((len(runs), n), np.float32)
+    for g, (lo, hi) in enumerate(runs):
+        sym, mn, sc = quantize(part.levels[lo], x[:, :, lo:hi, :], axis)
+        out[:, :, lo:hi, :] = sym
+        mn_t[g], sc_t[g] = mn.reshape(-1), sc.reshape(-1)
+    return out, mn_t, sc_t
+
+
+def dequantize_part(sym: np.ndarray, part: PartProfile, axis: str, mn_t: np.ndarray,
+                    sc_t: np.ndarray) -> np.ndarray:
+    """quantizer_func.dequantize (quantizer_func.py:77-113) of each section of one part;
+    returns bf16-valued float32 [B, S, H, D] in output order."""
+    B, S, H, D = sym.shape
+    if axis == "channel":
+        return dequantize(sym, mn_t[None, None], sc_t[None, None])
+    out = np.empty(sym.shape, np.float32)
+    for g, (lo, hi) in enumerate(_group_runs(part)):
+        shape = (B, S, 1, 1) if axis == "token" else (1, 1, 1, 1)
+        out[:, :, lo:hi, :] = dequantize(sym[:, :, lo:hi, :], mn_t[g].reshape(shape), sc_t[g].reshape(shape))
+    return out
+
+
+def quantize_layer(y: np.ndarray, prof: LayerProfile,
+                   axes: Tuple[str, str] = DEFAULT_AXES) -> Tuple[np.ndarray, LayerMeta]:
     """KVServeQuantizer.quantize (kvserve_quantizer.py:171-233) generalised to any
-    number of contiguous statistic groups: K per channel (stats per output position),
-    V per token over the heads of a group.  y: bf16-valued float32 [2, B, S, H, D].
-    Returns uint8 [2, B, S, H', D] with heads in output order, and metadata."""
-    _, B, S, H, D = y.shape
+    number of contiguous statistic groups: K with axes[0], V with axes[1] (default K
+    per channel, V per token over the heads of a group).  y: bf16-valued float32
+    [2, B, S, H, D].  Returns uint8 [2, B, S, H', D] with heads in output order, and
+    metadata."""
     out = np.empty(y.shape, dtype=np.uint8)
-    kmin = np.empty((H, D), np.float32)
-    ksc = np.empty((H, D), np.float32)
-    kx = y[0][:, :, prof.k.order, :]
-    # K: channel stats are per head, levels per output position
-    for j in range(H):
-        sym, mn, sc = quantize(prof.k.levels[j], kx[:, :, j : j + 1, :], "channel")
-        out[0, :, :, j : j + 1, :] = sym
-        kmin[j], ksc[j] = mn[0, 0, 0], sc[0, 0, 0]
-    vx = y[1][:, :, prof.v.order, :]
-    groups = sorted(set(prof.v.group))
-    vmin = np.empty((len(groups), B * S), np.float32)
-    vsc = np.empty((len(groups), B * S), np.float32)
-    for g in groups:
-        js = [j for j in range(H) if prof.v.group[j] == g]
-        lo, hi = js[0], js[-1] + 1
-        assert js == list(range(lo, hi)), "groups are contiguous runs of output positions"
-        sym, mn, sc = quantize(prof.v.levels[lo], vx[:, :, lo:hi, :], "token")
-        out[1, :, :, lo:hi, :] = sym
-        vmin[g], vsc[g] = mn.reshape(-1), sc.reshape(-1)
+    out[0], kmin, ksc = quantize_part(y[0][:, :, prof.k.order, :], prof.k, axes[0])
+    out[1], vmin, vsc = quantize_part(y[1][:, :, prof.v.order, :], prof.v, axes[1])
     return out, LayerMeta(kmin, ksc, vmin, vsc)
 
 
-def dequantize_layer(sym: np.ndarray, meta: LayerMeta, prof: LayerProfile) -> np.ndarray:
+def dequantize_layer(sym: np.ndarray, meta: LayerMeta, prof: LayerProfile,
+                     axes: Tuple[str, str] = DEFAULT_AXES) -> np.ndarray:
     """KVServeQuantizer.dequantize (kvserve_quantizer.py:235-294): returns bf16-valued
     float32 [2, B, S, H, D] in source head order."""
-    _, B, S, H, D = sym.shape
     out = np.empty(sym.shape, np.float32)
-    kx = dequantize(sym[0], meta.kmin[None, None], meta.kscale[None, None])
-    out[0][:, :, prof.k.order, :] = kx
-    vd = np.empty((B, S, H, D), np.float32)
-    for g in range(meta.vmin.shape[0]):
-        js = [j for j in range(H) if prof.v.group[j] == g]
-        mn = meta.vmin[g].reshape(B, S, 1, 1)
-        sc = meta.vscale[g].reshape(B, S, 1, 1)
-        vd[:, :, js, :] = dequantize(sym[1][:, :, js, :], mn, sc)
-    out[1][:, :, prof.v.order, :] = vd
+    out[0][:, :, prof.k.order, :] = dequantize_part(sym[0], prof.k, axes[0], meta.kmin, meta.kscale)
+    out[1][:, :, prof.v.order, :] = dequantize_part(sym[1], prof.v, axes[1], meta.vmin, meta.vscale)
     return out
 
 
@@ -335,6 +365,7 @@ def compress_request(
     layout: str = "permuted",
     layer_ids: Optional[Sequence[int]] = None,
     chunks: Optional[Sequence[Tuple[int, int]]] = None,
+    axes: Tuple[str, str] = DEFAULT_AXES,
 ) -> List[Chunk]:
     """Gather every layer (kv_utils.py:59-80), then compress_all_layers
     (compression_manager.py:200-537): per layer transform (KVServeTransformer,
@@ -356,7 +387,7 @@ def compress_request(
                 y = np.stack([bf16_to_f32(hadamard_forward(x[p], sg)) for p in (0, 1)])
             else:
                 y = bf16_to_f32(x)
-            sym, meta = quantize_layer(y, profiles[l])
+            sym, meta = quantize_layer(y, profiles[l], axes)
             syms.append(sym.transpose(0, 3, 1, 2, 4) if layout == "permuted" else sym)
             metas.append(meta)
         buf = np.ascontiguousarray(np.stack(syms))
@@ -374,6 +405,7 @@ def decompress_request(
     transform: bool = True,
     layout: str = "permuted",
     layer_ids: Optional[Sequence[int]] = None,
+    axes: Tuple[str, str] = DEFAULT_AXES,
 ) -> None:
     """decompress_all_layers (compression_manager.py:539-757) then
     inject_kv_into_layer_by_blocks (kv_utils.py:83-119), into `pools` in place."""
@@ -383,7 +415,7 @@ def decompress_request(
         buf = bitpack_decode(ch.stream, int(np.prod(shape)), bits).reshape(shape)
         for i, l in enumerate(range(ch.start, ch.stop)):
             sym = buf[i].transpose(0, 2, 3, 1, 4) if layout == "permuted" else buf[i]
-            x = dequantize_layer(sym, ch.metas[i], profiles[l])
+            x = dequantize_layer(sym, ch.metas[i], profiles[l], axes)
             H, D = x.shape[-2], x.shape[-1]
             if transform:
                 sg = rademacher_signs(base_seed, lids[l], H, D)

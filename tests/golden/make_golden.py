@@ -4,9 +4,9 @@ Run in the build container only (the reference tree is absent on GPU boxes):
 
     python tests/golden/make_golden.py /root/reference
 
-Nothing pins the bf16 op order of KVServe's quantizer except the reference code
-itself (no golden data ships with it), so this script imports the reference's own
-pure-torch modules -- quantizer_func.py, split_func.py, kvserve_quantizer.py and
+Nothing pins the bf16 op order of KVServe's quantizer (on every quantization axis)
+except the reference code itself (no golden data ships with it), so this script
+imports the reference's own pure-torch modules -- quantizer_func.py, split_func.py, kvserve_quantizer.py and
 compression_manager.py -- and records inputs and outputs as small .npz fixtures.
 The transform (hadamard_func.py) is not imported: it needs the absent third-party
 fast_hadamard_transform, and the FWHT is pinned by the Sylvester closed form
@@ -117,6 +117,43 @@ def main(ref_root: str) -> None:
             rows.append(torch.randint(0, 2, (D,), generator=g, dtype=torch.int8).numpy())
         sg[f"s_{seed}_{layer}_{H}_{D}"] = np.stack(rows)
     np.savez_compressed(OUT / "signs.npz", **sg)
+
+    # (e) quantization axes (quantizer_func.py:41-49, kvserve_quantizer.py:202-214): the
+    # tensor axis of quantizer_func, and KVServeQuantizer with every non-default
+    # (axis_key, axis_value) pair.  A generator of its own, so (a)-(d) stay as they were.
+    gen = torch.Generator().manual_seed(20261202)
+    ax = {}
+    for i, (shape, mv) in enumerate([((3, 16, 2, 128), 16), ((2, 16, 3, 64), 6), ((1, 16, 1, 128), 200)]):
+        x = kv(gen, shape)
+        if i == 1:
+            x[:] = x[0, 0, 0, 0]  # a constant section: the scale falls to the 1e-5 floor
+        q, meta = qf.quantize(mv, x, "tensor")
+        ax[f"t{i}_x"] = bits(x)
+        ax[f"t{i}_q"] = q.numpy()
+        ax[f"t{i}_min"] = bits(meta["min_val"])
+        ax[f"t{i}_scale"] = bits(meta["quant_scale"])
+        ax[f"t{i}_deq"] = bits(qf.dequantize(q, meta))
+        ax[f"t{i}_mv"] = np.array([mv])
+    pairs = [(a, b) for a in ("channel", "token", "tensor") for b in ("channel", "token", "tensor")
+             if (a, b) != ("channel", "token")]
+    for pi, (ak, av) in enumerate(pairs):
+        # head split (two sections) on layer 0, layer split (the low layer 31)
+        for ci, layer_id in ((1, 0), (2, 31)):
+            quant = KVServeQuantizer(**cfgs[ci], axis_key=ak, axis_value=av)
+            x = kv(gen, (2, 1, 8, 8, 64))
+            q, meta = quant.quantize(layer_id, x)
+            d = quant.dequantize(layer_id, q, meta)
+            key = f"a{pi}_q{ci}_l{layer_id}"
+            ax[key + "_x"] = bits(x)
+            ax[key + "_q"] = q.numpy()
+            ax[key + "_deq"] = bits(d)
+            for sec in ("high_key_meta", "high_value_meta", "low_key_meta", "low_value_meta"):
+                m = meta[sec]
+                if m["min_val"] is not None:
+                    ax[f"{key}_{sec}_min"] = bits(m["min_val"])
+                    ax[f"{key}_{sec}_scale"] = bits(m["quant_scale"])
+        ax[f"a{pi}_axes"] = np.array([["channel", "token", "tensor"].index(a) for a in (ak, av)])
+    np.savez_compressed(OUT / "quantizer_axes.npz", **ax)
     for p in sorted(OUT.glob("*.npz")):
         print(p.name, p.stat().st_size)
 

@@ -297,3 +297,36 @@ def test_v3_noalloc_contract_errors():
     assert need(8, 64, 128) <= _lib.V3_NOALLOC_SCRATCH_BYTES < need(1024, 64, 128)
     with pytest.raises(ValueError, match="KVMI_ENOSPC"):
         _lib.check(_lib.ENOSPC, "kvmi_v3_compress_noalloc")
+
+
+@pytest.mark.parametrize("axes", [("channel", "token"), ("token", "channel"), ("tensor", "tensor"),
+                                  ("channel", "channel"), ("token", "tensor")])
+def test_metadata_dicts_follow_each_axis_and_round_trip(axes):
+    """Reference-format section dicts are views of the engine tables with the keepdim
+    shapes of quantizer_func.py:52-53 on every axis; tables_from_dicts returns views of
+    the same allocation, and a copy elsewhere still converts back to equal tables."""
+    import torch
+
+    from kvserve_amd.compression._meta import layer_dict, tables_from_dicts
+    from kvserve_amd.engine import meta_shape
+    from kvserve_amd.profiles import section_profile
+
+    H, D, B, S, L, G = 4, 32, 3, 16, 2, 2
+    prof = section_profile([True, False, True, False], 12, 8, 6, 4)
+    shapes = [meta_shape(a, H, D, G, B * S) for a in axes]
+    sizes = [L * 2 * r * c for r, c in shapes]
+    buf = torch.arange(sum(sizes), dtype=torch.float32).to(torch.bfloat16)
+    kmeta = buf[:sizes[0]].view(L, 2, *shapes[0])
+    vmeta = buf[sizes[0]:].view(L, 2, *shapes[1])
+    dicts = [layer_dict(kmeta[l], vmeta[l], prof, B, S, axes) for l in range(L)]
+    want = {"channel": (1, 1, 2, D), "token": (B, S, 1, 1), "tensor": (1, 1, 1, 1)}
+    for d in dicts:
+        for name, axis in (("low_key_meta", axes[0]), ("high_value_meta", axes[1])):
+            assert tuple(d[name]["min_val"].shape) == want[axis], (name, axis)
+            assert d[name]["min_val"].untyped_storage().data_ptr() == buf.untyped_storage().data_ptr()
+    k2, v2 = tables_from_dicts(dicts, H, D, B, S, "cpu", axes)
+    assert k2.data_ptr() == kmeta.data_ptr() and torch.equal(k2, kmeta) and torch.equal(v2, vmeta)
+    copies = [{k: ({f: (t.clone() if isinstance(t, torch.Tensor) else t) for f, t in v.items()}
+                   if isinstance(v, dict) else v) for k, v in d.items()} for d in dicts]
+    k3, v3 = tables_from_dicts(copies, H, D, B, S, "cpu", axes)
+    assert k3.data_ptr() != kmeta.data_ptr() and torch.equal(k3, kmeta) and torch.equal(v3, vmeta)

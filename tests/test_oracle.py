@@ -103,6 +103,49 @@ def test_kvserve_quantizer_matches_reference_golden(cfg_idx, layer):
     assert np.array_equal(kp.f32_to_bf16(deq), z[key + "_deq"])
 
 
+# ------------------------------------------------------------------ quantization axes golden
+def test_tensor_axis_matches_reference_golden():
+    z = np.load(GOLDEN / "quantizer_axes.npz")
+    for i in range(3):
+        mv = int(z[f"t{i}_mv"][0])
+        sym, mn, sc = kp.quantize(mv, f(z[f"t{i}_x"]), "tensor")
+        assert mn.shape == (1, 1, 1, 1) and np.array_equal(sym, z[f"t{i}_q"]), i
+        assert np.array_equal(kp.f32_to_bf16(mn), z[f"t{i}_min"]), i
+        assert np.array_equal(kp.f32_to_bf16(sc), z[f"t{i}_scale"]), i
+        assert np.array_equal(kp.f32_to_bf16(kp.dequantize(sym, mn, sc)), z[f"t{i}_deq"]), i
+
+
+def _axis_cases():
+    z = np.load(GOLDEN / "quantizer_axes.npz")
+    return sorted({k.rsplit("_x", 1)[0] for k in z.files if k.startswith("a") and k.endswith("_x")})
+
+
+@pytest.mark.parametrize("key", _axis_cases())
+def test_kvserve_quantizer_axes_match_reference_golden(key):
+    """KVServeQuantizer with every non-default (axis_key, axis_value): symbols, each
+    section's metadata in the reference's keepdim layout, and the dequantized layer."""
+    z = np.load(GOLDEN / "quantizer_axes.npz")
+    pi, ci, layer = key.split("_")
+    axes = tuple(kp.AXES[int(a)] for a in z[f"{pi}_axes"])
+    prof = _profiles_for(int(ci[1:]), int(layer[1:]))
+    x = f(z[key + "_x"])
+    sym, meta = kp.quantize_layer(x, prof, axes)
+    assert np.array_equal(sym, z[key + "_q"]), axes
+    groups = sorted(set(prof.v.group))
+    nl = prof.v.group.count(0) if len(groups) == 2 else None
+    names = ["low", "high"] if nl is not None else (["low"] if f"{key}_low_key_meta_min" in z.files else ["high"])
+    for si, name in enumerate(names):
+        hs = slice(None) if nl is None else (slice(0, nl) if si == 0 else slice(nl, None))
+        for part, (mn_t, sc_t), axis in (("key", (meta.kmin, meta.kscale), axes[0]),
+                                         ("value", (meta.vmin, meta.vscale), axes[1])):
+            sel = hs if axis == "channel" else si  # channel: rows of the section; else: its group
+            for t, what in ((mn_t, "min"), (sc_t, "scale")):
+                want = z[f"{key}_{name}_{part}_meta_{what}"]
+                assert np.array_equal(kp.f32_to_bf16(t[sel]).reshape(-1), want.reshape(-1)), (axes, name, part, what)
+    deq = kp.dequantize_layer(sym, meta, prof, axes)
+    assert np.array_equal(kp.f32_to_bf16(deq), z[key + "_deq"]), axes
+
+
 @pytest.mark.parametrize("layout", ["permuted", "native"])
 def test_manager_layout_matches_reference_golden(layout):
     """CompressionManager without codec: the byte stream is the uint8 codec buffer."""
