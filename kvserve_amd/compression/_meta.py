@@ -17,7 +17,8 @@ The "low" section is the first n_low output positions and group 0 when it exists
 
 from __future__ import annotations
 
-from typing import Dict, List, Optional, Sequence, Tuple
+from collections.abc import Sequence as _SequenceABC
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -147,3 +148,101 @@ def _table_views(dicts: Sequence[Dict], H: int, D: int, BS: int, G: int, axes: T
     kmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off, (L, 2) + shapes[0])
     vmeta = torch.empty(0, dtype=torch.bfloat16, device=device).set_(st, off + sizes[0], (L, 2) + shapes[1])
     return kmeta, vmeta
+
+
+class QuantParams(_SequenceABC):
+    """A layer range's "quantization_params" list in the reference's format, each dict
+    built on first access (a dict per layer of four sections is most of the host time
+    of a request otherwise).  `tables` = (kmeta, vmeta, start, stop): the engine tables
+    of the whole request the range belongs to, when known -- the decoder and the wire
+    then use them directly and never build the dicts."""
+
+    def __init__(self, n: int, make: Callable[[int], Dict],
+                 tables: Optional[Tuple[torch.Tensor, torch.Tensor, int, int]] = None, template=None):
+        self._n, self._make, self._dicts = n, make, [None] * n
+        self.tables, self.template = tables, template
+
+    def __len__(self) -> int:
+        return self._n
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return [self[j] for j in range(*i.indices(self._n))]
+        if i < 0:
+            i += self._n
+        if not 0 <= i < self._n:
+            raise IndexError("quantization_params index out of range")
+        if self._dicts[i] is None:
+            self._dicts[i] = self._make(i)
+        return self._dicts[i]
+
+    def __eq__(self, other) -> bool:
+        return isinstance(other, (list, tuple, QuantParams)) and list(self) == list(other)
+
+    def __repr__(self) -> str:
+        return f"QuantParams({self._n} layers)"
+
+
+def packet_params(kmeta: torch.Tensor, vmeta: torch.Tensor, profiles: Sequence[LayerProfile], B: int, S: int,
+                  axes: Tuple[str, str], start: int, stop: int) -> QuantParams:
+    """Layers [start, stop) of a packet's tables as a QuantParams."""
+    return QuantParams(stop - start,
+                       lambda i: layer_dict(kmeta[start + i], vmeta[start + i], profiles[start + i], B, S, axes),
+                       (kmeta, vmeta, start, stop), (profiles, B, S, axes))
+
+
+def joined_tables(params: Sequence) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """(kmeta, vmeta) of a request whose chunks' QuantParams cover the layers of one
+    pair of tables in order; None otherwise (the caller converts dicts)."""
+    pos, base = 0, None
+    for qp in params:
+        t = getattr(qp, "tables", None)
+        if t is None:
+            return None
+        kmeta, vmeta, start, stop = t
+        if base is None:
+            base = (kmeta, vmeta)
+        elif kmeta is not base[0] or vmeta is not base[1]:
+            return None
+        if start != pos:
+            return None
+        pos = stop
+    if base is None or pos != base[0].shape[0]:
+        return None
+    return base
+
+
+def section_entries(profiles: Sequence[LayerProfile], start: int, stop: int, B: int, S: int, axes: Tuple[str, str],
+                    kshape: Tuple[int, ...], vshape: Tuple[int, ...]) -> Tuple[List, List]:
+    """The wire image of layers [start, stop): for each layer the dict of placeholders
+    (index relative to the first section) and, per section tensor in placeholder
+    order, (byte offset in the metadata allocation, nbytes, keepdim shape) -- the K
+    table [L,2,r,c] at offset 0 followed by the V table.  Sections of layer_dict."""
+    H = len(profiles[0].k_order)
+    D = kshape[3] if axes[0] == "channel" else vshape[3]
+    tree, entries = [], []
+    vbase = 2 * kshape[0] * kshape[1] * kshape[2] * kshape[3]
+    for l in range(start, stop):
+        prof = profiles[l]
+        where = {}  # section name -> ((offset, nbytes, shape) of min, of scale)
+        for (low_name, high_name), (base, shape), axis in zip(_PARTS, ((0, kshape), (vbase, vshape)), axes):
+            _, _, rows, cols = shape
+            for sec, lo, hi, g in _sections(prof, H):
+                r0, n = (lo, hi - lo) if axis == "channel" else (g, 1)
+                where[low_name if sec == "low" else high_name] = tuple(
+                    (base + 2 * (((l * 2 + which) * rows + r0) * cols), 2 * n * cols,
+                     list(_keepdim(axis, hi - lo, D, B, S))) for which in (0, 1))
+        # placeholders are numbered in the order a walk of layer_dict's dict meets them
+        out = {}
+        for name in _SECTIONS:
+            if name not in where:
+                out[name] = _empty()
+                continue
+            idx = []
+            for e in where[name]:
+                entries.append(e)
+                idx.append(len(entries) - 1)
+            out[name] = {"min_val": idx[0], "quant_scale": idx[1], "original_dtype": "bfloat16", "quant_dtype": "uint8"}
+        out["original_dtype"] = "bfloat16"
+        tree.append(out)
+    return tree, entries

@@ -25,7 +25,7 @@ from typing import Any, Dict, List, Optional, Sequence
 import torch
 
 from ..engine import DEFAULT_SEED, FusedKVCodec, Packet, check_packet, chunk_ranges, supported_geometry
-from ._meta import layer_dict, tables_from_dicts
+from ._meta import joined_tables, packet_params, tables_from_dicts
 from .codec import is_entropy_codec
 from .codec.rans_codec import unpack_target
 from .. import ops
@@ -305,7 +305,22 @@ class FusedCompressionManager(CompressionManager):
         return self._codecs[key]
 
     def profiles(self, layer_ids: Sequence[int], H: int):
-        return [self.quantizer.layer_profile(l, H) for l in layer_ids]
+        """Layer profiles, cached per (layers, heads, quantizer settings): the same list
+        object for every request of one shape (the wire caches its image by it)."""
+        q = self.quantizer
+        state = tuple(getattr(q, k, None) for k in (
+            "split_type", "hybrid_ratio", "high_key_max_value", "high_value_max_value", "low_key_max_value",
+            "low_value_max_value", "tensor_parallel_size", "tp_rank", "model_name"))
+        key = (tuple(layer_ids), H, state, id(getattr(q, "head_scores_mask", None)),
+               id(getattr(q, "layer_scores_mask", None)))
+        cache = self.__dict__.setdefault("_profile_cache", {})
+        hit = cache.get(key)
+        if hit is None:
+            if len(cache) > 64:
+                cache.clear()
+            hit = [q.layer_profile(l, H) for l in layer_ids]
+            cache[key] = hit
+        return hit
 
     # ---------------------------------------------------------------- compress
     def compress_all_layers(self, all_layers_data, request_id, config, metadata):
@@ -350,8 +365,7 @@ class FusedCompressionManager(CompressionManager):
             if transform:
                 m["transformer_applied"] = True
             m["quantization_applied"] = True
-            m["quantization_params"] = [layer_dict(packet.kmeta[l], packet.vmeta[l], profs[l], B, S, packet.axes)
-                                        for l in range(s, e)]
+            m["quantization_params"] = packet_params(packet.kmeta, packet.vmeta, profs, B, S, packet.axes, s, e)
             m["codec_shape"] = [e - s, 2, H, B, S, D] if layout == "permuted" else [e - s, 2, B, S, H, D]
             m["codec_dtype"] = "uint8"
             if has_codec:
@@ -389,17 +403,21 @@ class FusedCompressionManager(CompressionManager):
             _, _, H, B, S, D = shape
         else:
             _, _, B, S, H, D = shape
-        chunks, dicts, start = [], [], m0.get("start_layer_id", 0)
+        chunks, start = [], m0.get("start_layer_id", 0)
         off = 0
         for m in metas:
             n = m["num_layers"]
             chunks.append((off, off + n))
             off += n
-            dicts += list(m.get("quantization_params") or [])
-        if len(dicts) != off:
+        params = [m.get("quantization_params") or [] for m in metas]
+        if sum(len(p) for p in params) != off:
             raise ValueError("Missing quantization params")
         layer_ids = list(range(start, start + off))
-        kmeta, vmeta = tables_from_dicts(dicts, H, D, B, S, device, self._axes())
+        tables = joined_tables(params)  # tables of this engine's packet or bundle, as they are
+        if tables is not None and tables[0].device == torch.device(device):
+            kmeta, vmeta = tables
+        else:
+            kmeta, vmeta = tables_from_dicts([d for p in params for d in p], H, D, B, S, device, self._axes())
         transform, seed, has_codec, bits = self._settings()
         if not all(m.get("codec_applied", False) == has_codec for m in metas):
             raise ValueError("packet codec does not match the pipeline")

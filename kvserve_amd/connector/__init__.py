@@ -2,7 +2,7 @@
 
   CompressedKVConnector            the connector; compresses and decompresses on the paged caches
   CompressedKVConnectorMetadata    per-step requests (ReqMeta) handed from scheduler to workers
-  LoopbackTransport                in-process transport with the NcclTransport method surface
+  LoopbackTransport                in-process hand-off with the NcclTransport method surface
   extract / inject_kv_*_by_blocks  block-level copies between paged caches and stacked tensors
 """
 

@@ -19,10 +19,13 @@ A received bundle is the dict ``{"__bundle__": True, "meta", "body_chunks",
 The ZMQ + NCCL transport itself (a socket control channel and a send thread) is
 network plumbing and not part of this engine; a deployment plugs its own class in
 through ``kv_connector_extra_config["transport_class"]``.  `LoopbackTransport`
-connects a producer and a consumer inside one process (tests, single-process
-disaggregation, benchmarks): a send copies the payload into receive buffers on the
-consumer's device and delivers it once the consumer has staging credit, with the
-credit rules of nccl_transport.py:508-560.
+hands payloads from a producer to a consumer inside one process (single-process
+disaggregation, benchmarks): the consumer receives the producer's tensors themselves
+(copied only when the consumer names another device) and the metadata dict itself.
+`CreditLoopbackTransport` is test infrastructure: it adds what a network transport
+does on the way -- the metadata through msgpack, staging copies on the receiver and
+the receive-credit rules of nccl_transport.py:508-560 -- so the connector's load loop
+and the wire's msgpack safety are tested against them.
 """
 
 from __future__ import annotations
@@ -71,12 +74,12 @@ class _Channel:
 
 
 class LoopbackTransport:
-    """In-process transport between a producer and a consumer connector.
+    """In-process hand-off between a producer and a consumer connector.
 
-    Both ends name the same (host, port, channel_rank); the consumer's
-    `recv_buffer_size` is the staging capacity.  `device` is where received
-    tensors live (the consumer's GPU).  Sends are copies enqueued on the current
-    stream, so the producer may reuse its buffers once `wait_for_sent` returns.
+    Both ends name the same (host, port, channel_rank).  `device` is where the
+    consumer wants received tensors (its GPU); a payload already there is handed
+    over as it is, so the producer must not write a sent buffer again (the
+    connector sends freshly allocated ones).  Every send is admitted at once.
     """
 
     _registry: Dict[Tuple[str, int, int], _Channel] = {}
@@ -106,8 +109,8 @@ class LoopbackTransport:
     @classmethod
     def reset_channels(cls) -> None:
         """Forget every channel (between tests)."""
-        with cls._registry_lock:
-            cls._registry.clear()
+        with LoopbackTransport._registry_lock:
+            LoopbackTransport._registry.clear()
 
     # ------------------------------------------------------------------ stats
     def record_stat(self, row: Dict[str, Any]) -> None:
@@ -135,16 +138,20 @@ class LoopbackTransport:
 
     # ------------------------------------------------------------------ producer
     def _stage(self, tensors: List[torch.Tensor]) -> List[torch.Tensor]:
-        """Receive buffers on the consumer's device holding copies of `tensors`."""
+        """The tensors as the consumer receives them: themselves on its device, else
+        copies there (enqueued on the current stream)."""
         out = []
         for t in tensors:
+            if t.device == self.device:
+                out.append(t)
+                continue
             r = torch.empty(t.shape, dtype=t.dtype, device=self.device)
             r.copy_(t.contiguous(), non_blocking=True)
             out.append(r)
-        if self.device.type == "cuda":
-            ev = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.device))
-            self._copy_events.append(ev)
+            if t.device.type == "cuda" or self.device.type == "cuda":
+                ev = torch.cuda.Event()
+                ev.record(torch.cuda.current_stream(t.device if t.device.type == "cuda" else self.device))
+                self._copy_events.append(ev)
         return out
 
     def _post(self, request_id: str, layer_names: List[str], payload: Any, nbytes: int, kind: str) -> None:
@@ -153,9 +160,9 @@ class LoopbackTransport:
             ch.pending.append((request_id, list(layer_names), payload, nbytes))
             ch.pending_bytes += nbytes
             depth, queued = len(ch.pending), ch.pending_bytes
+            self._stat_locked({"direction": "send", "kind": kind, "request_id": request_id, "payload_bytes": nbytes,
+                               "queue_depth_at_submit": depth, "queued_bytes_at_submit": queued})
             ch.cv.notify_all()
-        self.record_stat({"direction": "send", "kind": kind, "request_id": request_id, "payload_bytes": nbytes,
-                          "queue_depth_at_submit": depth, "queued_bytes_at_submit": queued})
 
     def send(self, request_id: str, layer_names: List[str], stacked_kv: torch.Tensor) -> None:
         """Queue a raw stacked KV tensor (nccl_transport.py:181-197)."""
@@ -163,16 +170,16 @@ class LoopbackTransport:
         (t,) = self._stage([stacked_kv])
         self._post(request_id, layer_names, t, _tensor_nbytes(t), "tensor")
 
+    def _meta(self, meta: Dict[str, Any]) -> Dict[str, Any]:
+        """The metadata as the consumer receives it: the dict itself (a hand-off)."""
+        return meta
+
     def send_bundle(self, request_id: str, layer_names: List[str], meta: Dict[str, Any],
                     body_chunks: List[torch.Tensor], aux_tensors: List[torch.Tensor]) -> None:
-        """Queue a compressed bundle (nccl_transport.py:199-223).  The metadata goes
-        through msgpack as on the network transport's control channel, so a
-        bundle that would not serialize fails here."""
+        """Queue a compressed bundle (nccl_transport.py:199-223)."""
         assert self.is_sender
-        meta = msgpack.unpackb(msgpack.packb(meta, use_bin_type=True), raw=False)
-        body = self._stage(list(body_chunks))
-        aux = self._stage(list(aux_tensors))
-        payload = {"__bundle__": True, "meta": meta, "body_chunks": body, "aux_tensors": aux}
+        payload = {"__bundle__": True, "meta": self._meta(meta), "body_chunks": self._stage(list(body_chunks)),
+                   "aux_tensors": self._stage(list(aux_tensors))}
         self._post(request_id, layer_names, payload, payload_nbytes(payload), "bundle")
 
     def wait_for_sent(self) -> None:
@@ -183,8 +190,8 @@ class LoopbackTransport:
         self._copy_events.clear()
 
     def wait_for_below(self, max_pending_bytes: int, timeout_s: Optional[float] = None) -> float:
-        """Block while more than `max_pending_bytes` wait for receiver credit
-        (nccl_transport.py:232-239); the consumer admits them from another thread."""
+        """Block while more than `max_pending_bytes` wait for the receiver
+        (nccl_transport.py:232-239); the consumer takes them from another thread."""
         assert self.is_sender
         t0 = time.perf_counter()
         with self._ch.cv:
@@ -202,33 +209,12 @@ class LoopbackTransport:
             self._ch.received[request_id].append((list(FAILED_LAYER_NAMES), FAILED_PAYLOAD))
 
     # ------------------------------------------------------------------ consumer
-    def _try_reserve(self, request_id: str, nbytes: int) -> bool:
-        """Credit rule of nccl_transport.py:519-560 without waiting: admitted when
-        the staging is empty, when it fits, or once as the scheduled request
-        allowed past the budget.  Called with the channel lock held."""
-        ch = self._ch
-        over = ch.reserved > 0 and ch.reserved + nbytes > ch.capacity
-        if over:
-            if request_id in ch.expected and ch.priority is None:
-                ch.priority = request_id
-            else:
-                return False
-        before = ch.reserved
-        ch.reserved += nbytes
-        self._stat_locked({"direction": "recv_credit", "kind": "reserve", "request_id": request_id,
-                         "payload_bytes": nbytes, "blocked": over, "reserved_before_bytes": before,
-                         "reserved_after_bytes": ch.reserved, "capacity_bytes": ch.capacity,
-                         "oversize": nbytes > ch.capacity, "priority_overflow": request_id == ch.priority})
-        return True
-
     def _admit(self) -> None:
-        """Move sent payloads into the received set, in order, while credit lasts."""
+        """Move sent payloads into the received set, in order (all of them: a
+        hand-off needs no staging credit).  Called with the channel lock held."""
         ch = self._ch
         while ch.pending:
-            rid, names, payload, nbytes = ch.pending[0]
-            if not self._try_reserve(rid, nbytes):
-                break
-            ch.pending.popleft()
+            rid, names, payload, nbytes = ch.pending.popleft()
             ch.pending_bytes -= nbytes
             ch.received[rid].append((names, payload))
         ch.cv.notify_all()
@@ -247,6 +233,70 @@ class LoopbackTransport:
         return payload_nbytes(payload)
 
     def release_received(self, request_id: str, payload_bytes: int) -> None:
+        """A payload has been consumed (nccl_transport.py:485-506); a hand-off holds
+        no staging to give back."""
+        assert not self.is_sender
+
+    def set_expected_requests(self, request_ids: List[str]) -> None:
+        """The requests of this step (nccl_transport.py:508-517)."""
+        with self._ch.cv:
+            self._ch.expected = set(request_ids)
+            self._admit()
+
+
+class CreditLoopbackTransport(LoopbackTransport):
+    """Test infrastructure: a loopback whose consumer copies every payload into
+    staging on its device and admits it only with receive credit, by the rules of
+    nccl_transport.py:508-560 -- admitted when the staging is empty, when it fits, or
+    once as the scheduled request allowed past the budget (`recv_buffer_size` is the
+    staging capacity).  The metadata goes through msgpack as on the network
+    transport's control channel, so a bundle that would not serialize fails here.
+    The connector's load loop is tested against these rules."""
+
+    def _meta(self, meta: Dict[str, Any]) -> Dict[str, Any]:
+        return msgpack.unpackb(msgpack.packb(meta, use_bin_type=True), raw=False)
+
+    def _stage(self, tensors: List[torch.Tensor]) -> List[torch.Tensor]:
+        out = []
+        for t in tensors:
+            r = torch.empty(t.shape, dtype=t.dtype, device=self.device)
+            r.copy_(t.contiguous(), non_blocking=True)
+            out.append(r)
+        if self.device.type == "cuda":
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self._copy_events.append(ev)
+        return out
+
+    def _try_reserve(self, request_id: str, nbytes: int) -> bool:
+        """Called with the channel lock held."""
+        ch = self._ch
+        over = ch.reserved > 0 and ch.reserved + nbytes > ch.capacity
+        if over:
+            if request_id in ch.expected and ch.priority is None:
+                ch.priority = request_id
+            else:
+                return False
+        before = ch.reserved
+        ch.reserved += nbytes
+        self._stat_locked({"direction": "recv_credit", "kind": "reserve", "request_id": request_id,
+                           "payload_bytes": nbytes, "blocked": over, "reserved_before_bytes": before,
+                           "reserved_after_bytes": ch.reserved, "capacity_bytes": ch.capacity,
+                           "oversize": nbytes > ch.capacity, "priority_overflow": request_id == ch.priority})
+        return True
+
+    def _admit(self) -> None:
+        ch = self._ch
+        while ch.pending:
+            rid, names, payload, nbytes = ch.pending[0]
+            if not self._try_reserve(rid, nbytes):
+                break
+            ch.pending.popleft()
+            ch.pending_bytes -= nbytes
+            ch.received[rid].append((names, payload))
+        ch.cv.notify_all()
+
+    def release_received(self, request_id: str, payload_bytes: int) -> None:
         """Return staging credit once a payload has been consumed (nccl_transport.py:485-506)."""
         assert not self.is_sender
         if payload_bytes <= 0:
@@ -258,12 +308,6 @@ class LoopbackTransport:
             if request_id == ch.priority:
                 ch.priority = None
             self._stat_locked({"direction": "recv_credit_release", "kind": "release", "request_id": request_id,
-                             "payload_bytes": int(payload_bytes), "reserved_before_bytes": before,
-                             "reserved_after_bytes": ch.reserved, "capacity_bytes": ch.capacity})
-            self._admit()
-
-    def set_expected_requests(self, request_ids: List[str]) -> None:
-        """The requests of this step; one of them may pass the budget (nccl_transport.py:508-517)."""
-        with self._ch.cv:
-            self._ch.expected = set(request_ids)
+                               "payload_bytes": int(payload_bytes), "reserved_before_bytes": before,
+                               "reserved_after_bytes": ch.reserved, "capacity_bytes": ch.capacity})
             self._admit()

@@ -171,6 +171,8 @@ class FusedKVCodec:
         if self.compress_path not in ("one_pass", "two_pass"):
             raise ValueError("compress_path must be 'one_pass' or 'two_pass'")
         self._lib = _lib.load()
+        self._prof_cache: Dict[tuple, tuple] = {}
+        self._pools_ok: Dict[tuple, tuple] = {}
 
     # ---------------------------------------------------------------- helpers
     def _flags(self, max_level: int) -> int:
@@ -214,6 +216,20 @@ class FusedKVCodec:
         return keys
 
     def _check_pools(self, pools: Sequence[torch.Tensor]) -> torch.device:
+        """Device of the per-layer caches after checking dtype, shape, layout and
+        placement; the caches of a deployment are the same tensors on every request,
+        so a passing set is remembered by identity and address."""
+        key = tuple((id(p), p.data_ptr()) for p in pools)
+        hit = self._pools_ok.get(key)
+        if hit is not None and all(a is b for a, b in zip(hit[0], pools)):
+            return hit[1]
+        dev = self._check_pools_once(pools)
+        if len(self._pools_ok) > 16:
+            self._pools_ok.clear()
+        self._pools_ok[key] = (tuple(pools), dev)
+        return dev
+
+    def _check_pools_once(self, pools: Sequence[torch.Tensor]) -> torch.device:
         if not pools:
             raise ValueError("at least one layer is required")
         dev = pools[0].device
@@ -228,11 +244,12 @@ class FusedKVCodec:
                 raise ValueError("KV caches must live on one GPU")
         return dev
 
-    def _block_table(self, block_ids, device, pool_blocks: int) -> torch.Tensor:
-        """int32 device block table; every id is checked against the cache size on
-        the host before a kernel dereferences it (a plan is built once, so the
-        synchronization of a device-tensor check is off the hot path)."""
-        if isinstance(block_ids, torch.Tensor):
+    def _block_table(self, block_ids, device, pool_blocks: int):
+        """The block table, every id checked against the cache size on the host
+        before a kernel dereferences it: an int32 device tensor for device input (a
+        plan is built once, so the synchronization of that check is off the hot
+        path), else a host int32 array that the plan uploads with its job table."""
+        if isinstance(block_ids, torch.Tensor) and block_ids.is_cuda:
             if block_ids.dim() != 1:
                 raise ValueError("block_ids must be 1-D")
             ids = block_ids.to(device=device, dtype=torch.int32).contiguous()
@@ -241,35 +258,79 @@ class FusedKVCodec:
                 if lo < 0 or hi >= pool_blocks:
                     raise IndexError("block id outside the KV cache")
             return ids
-        ids_list = [int(b) for b in block_ids]
-        if ids_list and (min(ids_list) < 0 or max(ids_list) >= pool_blocks):
+        ids = np.asarray(block_ids.numpy() if isinstance(block_ids, torch.Tensor) else block_ids, dtype=np.int64)
+        if ids.ndim != 1:
+            raise ValueError("block_ids must be 1-D")
+        if ids.size and (int(ids.min()) < 0 or int(ids.max()) >= pool_blocks):
             raise IndexError("block id outside the KV cache")
-        return torch.tensor(ids_list, dtype=torch.int32, device=device)
+        return ids.astype(np.int32)
 
     def _jobs(self, pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, B) -> torch.Tensor:
+        """The kvmi_layer_job table: one row per layer, built with array arithmetic
+        (per-layer pointers are base + l * layer stride of each table).  `ids` is the
+        device block table, or a host int32 array: it is then uploaded in the same copy
+        as the table (returned as the table's `block_ids` attribute)."""
+        dev = pools[0].device
+        up = None
+        if not isinstance(ids, torch.Tensor):
+            L = len(pools)
+            jb = L * _lib.JOB_INT64S * 8
+            up = torch.empty(jb + 4 * max(1, ids.size), dtype=torch.uint8, device=dev)
+            host_ids = ids
+            ids = up[jb:jb + 4 * ids.size].view(torch.int32)
+        rows = self._job_rows(pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, B)
+        if up is None:
+            return torch.from_numpy(rows).to(dev, non_blocking=False)
+        host = np.zeros(up.numel(), np.uint8)
+        host[:rows.nbytes] = rows.view(np.uint8).reshape(-1)
+        host[rows.nbytes:rows.nbytes + host_ids.nbytes] = host_ids.view(np.uint8)
+        up.copy_(torch.from_numpy(host))
+        table = up[:rows.nbytes].view(torch.int64).view(rows.shape)
+        table.block_ids = ids
+        return table
+
+    def _job_rows(self, pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, B) -> np.ndarray:
         L = len(pools)
         H, D, S = self.H, self.D, self.S
         per_layer = 2 * H * B * S * D
+        lay = np.arange(L, dtype=np.int64)
+        start = np.empty(L, np.int64)
+        stop = np.empty(L, np.int64)
+        stream = np.empty(L, np.int64)
+        for (s, e), st in zip(chunks, streams):
+            start[s:e], stop[s:e], stream[s:e] = s, e, _ptr(st)
+
+        def strided(t):  # address of t[l] for every l (t contiguous along its first axis)
+            return _ptr(t) + lay * (t.stride(0) * t.element_size()) if t is not None else np.zeros(L, np.int64)
+
         rows = np.zeros((L, _lib.JOB_INT64S), dtype=np.int64)
-        ci = 0
-        for l in range(L):
-            while not (chunks[ci][0] <= l < chunks[ci][1]):
-                ci += 1
-            start, stop = chunks[ci]
-            rows[l, 0] = _ptr(pools[l])
-            rows[l, 1] = _ptr(ids)
-            rows[l, 2] = _ptr(streams[ci])
-            rows[l, 3] = _ptr(kmeta[l])
-            rows[l, 4] = _ptr(vmeta[l])
-            rows[l, 5] = _ptr(signs[l]) if signs is not None else 0
-            rows[l, 6] = _ptr(prof_dev[l])
-            rows[l, 7] = _ptr(keys[l])
-            rows[l, 8] = 0  # counter: unused
-            rows[l, 9] = pools[l].shape[1] * S * H * D
-            rows[l, 10] = (l - start) * per_layer
-            rows[l, 11] = (stop - start) * per_layer
-            rows[l, 12] = B | ((1 if l == start else 0) << 32)
-        return torch.from_numpy(rows).to(pools[0].device, non_blocking=False)
+        rows[:, 0] = [_ptr(p) for p in pools]
+        rows[:, 1] = _ptr(ids)
+        rows[:, 2] = stream
+        rows[:, 3] = strided(kmeta)
+        rows[:, 4] = strided(vmeta)
+        rows[:, 5] = strided(signs)
+        rows[:, 6] = strided(prof_dev)
+        rows[:, 7] = strided(keys)
+        rows[:, 9] = [p.shape[1] * S * H * D for p in pools]
+        rows[:, 10] = (lay - start) * per_layer
+        rows[:, 11] = (stop - start) * per_layer
+        rows[:, 12] = B | ((lay == start).astype(np.int64) << 32)
+        return rows
+
+    def _profile_table(self, profiles: Sequence[LayerProfile], device) -> torch.Tensor:
+        """uint8 [L, 2, 3, H] device copy of the profiles, cached per profile objects
+        (a caller that keeps its profile list, as the compression manager does, uploads
+        it once)."""
+        key = (tuple(map(id, profiles)), str(device))
+        hit = self._prof_cache.get(key)
+        if hit is not None and all(a is b for a, b in zip(hit[0], profiles)):
+            return hit[1]
+        t = torch.from_numpy(np.stack([p.to_array() for p in profiles])).to(device)
+        if len(self._prof_cache) > 64:
+            self._prof_cache.clear()
+        self._prof_cache[key] = (tuple(profiles), t)
+        return t
 
     # ---------------------------------------------------------------- plans
     def plan_compress(self, pools: Sequence[torch.Tensor], block_ids, profiles: Sequence[LayerProfile],
@@ -293,7 +354,7 @@ class FusedKVCodec:
             p.validate(self.H, k_groups=self.axes[0] != "channel")
         layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
         ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
-        B = int(ids.numel())
+        B = int(ids.numel()) if isinstance(ids, torch.Tensor) else int(ids.size)
         H, D, S = self.H, self.D, self.S
         raw = L * 2 * B * S * H * D * 2
         if chunk_layers is None:
@@ -346,9 +407,10 @@ class FusedKVCodec:
             if tuple(t.shape) != want:
                 raise ValueError(f"{name} must be {list(want)} for axis {axis!r}, got {list(t.shape)}")
         ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
-        if ids.numel() < packet.num_blocks:
+        if (ids.numel() if isinstance(ids, torch.Tensor) else ids.size) < packet.num_blocks:
             raise ValueError("fewer block ids than compressed blocks")
-        ids = ids[: packet.num_blocks].contiguous()
+        ids = ids[: packet.num_blocks]
+        ids = ids.contiguous() if isinstance(ids, torch.Tensor) else np.ascontiguousarray(ids)
         hdr = 16 if self.header else 0
         for (s, e), st in zip(packet.chunks, packet.streams):
             n = (e - s) * 2 * self.H * packet.num_blocks * self.S * self.D
@@ -409,10 +471,12 @@ class Plan:
         self.signs = None
         if codec.transform:
             self.signs = SIGNS.table(codec.seed, packet.layer_ids, codec.H, codec.D, dev)
-        self.prof = torch.from_numpy(np.stack([p.to_array() for p in packet.profiles])).to(dev)
+        self.prof = codec._profile_table(packet.profiles, dev)
         self.keys = codec._kstats_scratch(L, dev)
         self.jobs = codec._jobs(pools, ids, packet.streams, packet.chunks, packet.kmeta, packet.vmeta,
                                 self.signs, self.prof, self.keys, B)
+        if not isinstance(ids, torch.Tensor):
+            self.ids = self.jobs.block_ids  # uploaded with the job table
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
         self.geo = codec._geometry(packet_groups(packet), max_level)

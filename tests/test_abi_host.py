@@ -330,3 +330,34 @@ def test_metadata_dicts_follow_each_axis_and_round_trip(axes):
                    if isinstance(v, dict) else v) for k, v in d.items()} for d in dicts]
     k3, v3 = tables_from_dicts(copies, H, D, B, S, "cpu", axes)
     assert k3.data_ptr() != kmeta.data_ptr() and torch.equal(k3, kmeta) and torch.equal(v3, vmeta)
+
+
+def test_job_table_rows_address_each_layer():
+    """The vectorised job table holds, per layer, the address of that layer's slice of
+    every table (as indexing the tensors gives it), its chunk's stream and offsets."""
+    import torch
+
+    from kvserve_amd import _lib
+    from kvserve_amd.engine import FusedKVCodec
+
+    codec = FusedKVCodec(4, 64, 16, 4, axes=("channel", "tensor"))
+    L, B = 5, 3
+    pools = [torch.zeros((2, 7, 16, 4, 64), dtype=torch.bfloat16) for _ in range(L)]
+    ids = torch.arange(B, dtype=torch.int32)
+    chunks = [(0, 2), (2, 5)]
+    streams = [torch.empty(100, dtype=torch.uint8), torch.empty(200, dtype=torch.uint8)]
+    buf = torch.empty(L * 2 * 4 * 64 + L * 2 * 2, dtype=torch.bfloat16)
+    kmeta, vmeta = buf[:L * 2 * 4 * 64].view(L, 2, 4, 64), buf[L * 2 * 4 * 64:].view(L, 2, 2, 1)
+    signs = torch.zeros((L, 4, 2), dtype=torch.int32)
+    prof = torch.zeros((L, 2, 3, 4), dtype=torch.uint8)
+    keys = torch.zeros((L, 2, 2, 4, 64), dtype=torch.int32)
+    rows = codec._jobs(pools, ids, streams, chunks, kmeta, vmeta, signs, prof, keys, B).numpy()
+    assert rows.shape == (L, _lib.JOB_INT64S)
+    per = 2 * 4 * B * 16 * 64
+    for l in range(L):
+        ci = 0 if l < 2 else 1
+        s, e = chunks[ci]
+        want = [pools[l].data_ptr(), ids.data_ptr(), streams[ci].data_ptr(), kmeta[l].data_ptr(), vmeta[l].data_ptr(),
+                signs[l].data_ptr(), prof[l].data_ptr(), keys[l].data_ptr(), 0, 7 * 16 * 4 * 64, (l - s) * per,
+                (e - s) * per, B | ((1 if l == s else 0) << 32)]
+        assert rows[l].tolist() == want, l

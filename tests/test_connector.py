@@ -14,7 +14,7 @@ import torch
 import kvserve_amd.connector.compressed_kv_connector as connector_module
 from kvserve_amd.connector import (CompressedKVConnector, CompressedKVConnectorMetadata, KVConnectorRole,
                                    LoopbackTransport, ReqMeta, make_slot_mapping)
-from kvserve_amd.connector.transport import payload_nbytes
+from kvserve_amd.connector.transport import CreditLoopbackTransport, payload_nbytes
 
 PROFILE = {"pipeline": ["transformer", "quantizer", "codec"],
            "transformer_config": {"transform_type": "hadamard", "seed": 3237919422},
@@ -96,8 +96,8 @@ def test_one_scheduled_overflow_unblocks_next_decode_step():
     """Credit rule of the reference's test: with the staging held by a future
     request, one scheduled request may pass the budget; the next is admitted once
     that one releases its credit."""
-    tx = LoopbackTransport(True, port=1)
-    rx = LoopbackTransport(False, port=1, recv_buffer_size=100, device="cpu")
+    tx = CreditLoopbackTransport(True, port=1)
+    rx = CreditLoopbackTransport(False, port=1, recv_buffer_size=100, device="cpu")
     for rid in ["future", "current-1", "current-2"]:
         tx.send(rid, ["l"], torch.zeros(100, dtype=torch.uint8))
     assert list(rx.drain_received()) == ["future"]
@@ -116,16 +116,16 @@ def test_one_scheduled_overflow_unblocks_next_decode_step():
 
 
 def test_oversize_payload_admitted_into_empty_staging():
-    tx = LoopbackTransport(True, port=2)
-    rx = LoopbackTransport(False, port=2, recv_buffer_size=10, device="cpu")
+    tx = CreditLoopbackTransport(True, port=2)
+    rx = CreditLoopbackTransport(False, port=2, recv_buffer_size=10, device="cpu")
     tx.send("big", ["l"], torch.zeros(64, dtype=torch.uint8))
     got = rx.drain_received()
     assert list(got) == ["big"] and [r for r in rx.stats if r.get("oversize")]
 
 
 def test_wait_for_below_blocks_until_the_consumer_admits():
-    tx = LoopbackTransport(True, port=3)
-    rx = LoopbackTransport(False, port=3, recv_buffer_size=100, device="cpu")
+    tx = CreditLoopbackTransport(True, port=3)
+    rx = CreditLoopbackTransport(False, port=3, recv_buffer_size=100, device="cpu")
     tx.send("a", ["l"], torch.zeros(80, dtype=torch.uint8))
     tx.send("b", ["l"], torch.zeros(80, dtype=torch.uint8))
     rx.drain_received()                      # admits a; b waits for credit
@@ -137,17 +137,25 @@ def test_wait_for_below_blocks_until_the_consumer_admits():
     assert tx.pending_bytes() == 0 and 0.03 < waited < 5.0
 
 
-def test_bundle_meta_goes_through_msgpack_and_payload_nbytes():
+def test_bundle_hand_off_and_payload_nbytes():
+    """The loopback hands over the tensors and the metadata dict themselves; the
+    test-only credit transport sends the metadata through msgpack (a tensor in it
+    fails there) and stages copies."""
     tx = LoopbackTransport(True, port=4)
     rx = LoopbackTransport(False, port=4, device="cpu")
     body, aux = [torch.arange(10, dtype=torch.uint8)], [torch.ones(3, dtype=torch.bfloat16)]
-    tx.send_bundle("r", ["__compressed__", "l0"], {"a": [1, 2], "b": {"c": "x"}}, body, aux)
+    meta = {"a": [1, 2], "b": {"c": "x"}}
+    tx.send_bundle("r", ["__compressed__", "l0"], meta, body, aux)
     ((names, payload),) = rx.drain_received()["r"]
-    assert names == ["__compressed__", "l0"] and payload["__bundle__"] and payload["meta"] == {"a": [1, 2], "b": {"c": "x"}}
-    assert payload_nbytes(payload) == 16 and payload["body_chunks"][0] is not body[0]
-    assert torch.equal(payload["body_chunks"][0], body[0])
+    assert names == ["__compressed__", "l0"] and payload["__bundle__"] and payload["meta"] is meta
+    assert payload_nbytes(payload) == 16 and payload["body_chunks"][0] is body[0]
+    ctx, crx = CreditLoopbackTransport(True, port=14), CreditLoopbackTransport(False, port=14, device="cpu")
+    ctx.send_bundle("r", ["__compressed__", "l0"], meta, body, aux)
+    ((_, staged),) = crx.drain_received()["r"]
+    assert staged["meta"] == meta and staged["meta"] is not meta
+    assert staged["body_chunks"][0] is not body[0] and torch.equal(staged["body_chunks"][0], body[0])
     with pytest.raises(TypeError):
-        tx.send_bundle("r", [], {"t": torch.zeros(1)}, body, aux)
+        ctx.send_bundle("r", [], {"t": torch.zeros(1)}, body, aux)
     assert payload_nbytes(None) == 0
 
 

@@ -30,8 +30,11 @@ def profile(min_size=0, hybrid=0.3):
             "codec_config": {"codec_type": "bitpack", "bitpack_bits": 4}, "min_compress_size": min_size}
 
 
-def vllm_config(producer, port, compression, heads=8, head=128, tp=(0, 1)):
-    extra = {"compression": compression, "transport_class": "loopback", "tp_rank": tp[0], "tp_size": tp[1]}
+CREDIT = "kvserve_amd.connector.transport:CreditLoopbackTransport"  # msgpack metadata, staging copies, credit
+
+
+def vllm_config(producer, port, compression, heads=8, head=128, tp=(0, 1), transport="loopback"):
+    extra = {"compression": compression, "transport_class": transport, "tp_rank": tp[0], "tp_size": tp[1]}
     return SimpleNamespace(
         kv_transfer_config=SimpleNamespace(is_kv_producer=producer, kv_buffer_size=1 << 34, kv_ip="127.0.0.1",
                                            kv_port=port, kv_connector_extra_config=extra),
@@ -68,11 +71,11 @@ def _caches(cuda, names, P, H, D, seed, fill=None):
     return out
 
 
-def _run(cuda, compression, prod, cons, p_ids, d_ids, port, heads, skip_layers=(), tp=(0, 1)):
+def _run(cuda, compression, prod, cons, p_ids, d_ids, port, heads, skip_layers=(), tp=(0, 1), transport="loopback"):
     names = list(prod)
     H, D = prod[names[0]].shape[3:]
-    p = CompressedKVConnector(vllm_config(True, port, compression, heads, D, tp), KVConnectorRole.WORKER)
-    d = CompressedKVConnector(vllm_config(False, port, compression, heads, D, tp), KVConnectorRole.WORKER)
+    p = CompressedKVConnector(vllm_config(True, port, compression, heads, D, tp, transport), KVConnectorRole.WORKER)
+    d = CompressedKVConnector(vllm_config(False, port, compression, heads, D, tp, transport), KVConnectorRole.WORKER)
     pm, dm = CompressedKVConnectorMetadata(), CompressedKVConnectorMetadata()
     pm.add_request("p-req", "T", list(range(16 * len(p_ids))), p_ids, 16)
     dm.add_request("d-req", "T", list(range(16 * len(d_ids))), d_ids, 16)
@@ -114,17 +117,20 @@ def _assert_written(cons, names, d_ids, expect, skip=()):
         assert (c[:, mask] == SENTINEL).all(), n
 
 
-def test_compressed_transfer_equals_reference_procedure(cuda):
+@pytest.mark.parametrize("transport", ["loopback", CREDIT])
+def test_compressed_transfer_equals_reference_procedure(cuda, transport):
     """5 layers whose names sort out of numeric order, 40 blocks at random producer
     ids, written at the first 40 of 48 consumer ids; the sent stream is byte-equal to
-    the stacked path's and the decode cache holds the stacked path's round trip."""
+    the stacked path's and the decode cache holds the stacked path's round trip.  Over
+    the hand-off, and over the credit transport, whose msgpack hop and staging copies
+    stand for a network's (the bundle is restored from msgpack'd metadata)."""
     P, H, D = 96, 8, 128
     g = torch.Generator().manual_seed(11)
     p_ids = torch.randperm(P, generator=g)[:40].tolist()
     d_ids = torch.randperm(P, generator=g)[:48].tolist()
     prod = _caches(cuda, NAMES, P, H, D, 5)
     cons = _caches(cuda, NAMES, P, H, D, 0, fill=SENTINEL)
-    p, d = _run(cuda, profile(), prod, cons, p_ids, d_ids, 20, H)
+    p, d = _run(cuda, profile(), prod, cons, p_ids, d_ids, 20, H, transport=transport)
     names, stacked, ref_packet, ref_out = _reference_procedure(profile(), prod, p_ids, H)
     assert names[2:] == ["model.layers.10.self_attn.attn", "model.layers.11.self_attn.attn",
                          "model.layers.2.self_attn.attn"]

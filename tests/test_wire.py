@@ -188,3 +188,65 @@ def test_engine_tables_come_back_as_views_also_over_the_wire():
     k4, v4 = tables_from_dicts(copied, H, D, B, S, "cpu")
     assert k4.data_ptr() != kmeta.data_ptr()
     assert torch.equal(k4, kmeta) and torch.equal(v4[0], vmeta[0]) and torch.equal(v4[1:, :, 0], vmeta[1:, :, 0])
+
+
+def _axis_tables(L, H, D, G, BS, axes):
+    from kvserve_amd.engine import meta_shape
+
+    ks, vs = meta_shape(axes[0], H, D, G, BS), meta_shape(axes[1], H, D, G, BS)
+    kn, vn = L * 2 * ks[0] * ks[1], L * 2 * vs[0] * vs[1]
+    buf = torch.randn(kn + vn).to(torch.bfloat16)
+    return buf[:kn].view(L, 2, *ks), buf[kn:].view(L, 2, *vs)
+
+
+@pytest.mark.parametrize("axes", [("channel", "token"), ("token", "tensor"), ("tensor", "channel")])
+@pytest.mark.parametrize("chunked", [False, True])
+def test_table_backed_params_pack_like_their_dicts(axes, chunked):
+    """QuantParams straight from the engine tables go on the wire exactly as their
+    materialised dicts would (same placeholder tree, aux layout and blob bytes, plus the
+    tables key), and come back as QuantParams over the received tables whose dicts
+    equal the sender's."""
+    import msgpack
+
+    from kvserve_amd.compression._meta import QuantParams, joined_tables, packet_params
+    from kvserve_amd.compression.wire import TABLES_KEY
+    from kvserve_amd.profiles import section_profile, whole_layer_profile
+
+    L, H, D, B, S = 6, 4, 32, 3, 16
+    kmeta, vmeta = _axis_tables(L, H, D, 2, B * S, axes)
+    profs = [section_profile([l % 2 == 0, True, False, l % 3 == 0], 12, 8, 6, 4) for l in range(L - 1)]
+    profs.append(whole_layer_profile(H, 6, 4, is_low=True))
+    ranges = [(0, 4), (4, 6)] if chunked else [(0, L)]
+
+    def payload(lazy):
+        def qp(s, e):
+            p = packet_params(kmeta, vmeta, profs, B, S, axes, s, e)
+            return p if lazy else list(p)
+        if not chunked:
+            return _payload(qp(0, L))
+        metas = [{"request_id": "req-7", "num_layers": e - s, "quantization_params": qp(s, e)} for s, e in ranges]
+        return CompressedKVData("req-7", L - 1, None, {"request_id": "req-7", "is_chunked": True}, 1000, 10, True,
+                                [torch.arange(4, dtype=torch.uint8) for _ in ranges], metas)
+
+    fast, slow = build_wire(payload(True), 1 << 20), build_wire(payload(False), 1 << 20)
+    fm = dict(fast.meta)
+    assert fm.pop(TABLES_KEY) == {"k_offset": 0, "k_shape": list(kmeta.shape), "v_offset": 2 * kmeta.numel(),
+                                  "v_shape": list(vmeta.shape)}
+    assert fm == slow.meta
+    assert torch.equal(fast.aux_tensors[0], slow.aux_tensors[0])
+    assert fast.aux_tensors[0].data_ptr() == kmeta.data_ptr()  # shipped without a copy
+    wire = CompressedWire(msgpack.unpackb(msgpack.packb(fast.meta)), fast.body_chunks,
+                          [fast.aux_tensors[0].clone()])
+    back = restore_from_wire(wire)
+    metas = back.chunk_metadata if chunked else [back.metadata]
+    params = [m["quantization_params"] for m in metas]
+    assert all(isinstance(p, QuantParams) for p in params)
+    k2, v2 = joined_tables(params)
+    assert torch.equal(k2, kmeta) and torch.equal(v2, vmeta)
+    want = [d for s, e in ranges for d in packet_params(kmeta, vmeta, profs, B, S, axes, s, e)]
+    got = [d for p in params for d in p]
+    for a, b in zip(got, want):
+        for sec in ("high_key_meta", "high_value_meta", "low_key_meta", "low_value_meta"):
+            for f in ("min_val", "quant_scale"):
+                x, y = a[sec][f], b[sec][f]
+                assert (x is None and y is None) or (x.shape == y.shape and torch.equal(x, y)), (sec, f)
