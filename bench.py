@@ -99,23 +99,30 @@ CONNECTOR_PROFILE = {
 def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> dict:
     """Name of the HIP kernel each entry point runs for this geometry (MFMA unless the
     register-FWHT kernels are forced or the geometry is not MFMA-eligible)."""
-    mfma = codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
+    default_axes = tuple(getattr(codec, "axes", ("channel", "token"))) == ("channel", "token")
+    pow2 = D in (64, 128) and default_axes
+    mfma = pow2 and codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
     if mfma:
         names = {"kvmi_encode_paged": f"encode_mfma_kernel<{D // 32}, {bits}, false>",
-                 "kvmi_decode_paged": f"decode_mfma_kernel<{D // 32}, {bits}>",
-                 "kvmi_kstats_paged": f"kstats_mfma_kernel<{D // 32}>"}
+                 "kvmi_decode_paged": f"decode_mfma_kernel<{D // 32}, {bits}, 8>",
+                 "kvmi_kstats_paged": f"kstats_mfma_kernel<{D // 32}>", "finalize": "kstats_finalize_kernel"}
         if cplan is not None and cplan.epoch.value > 0:  # the one-pass kernel ran
             names["kvmi_compress_paged"] = f"compress_pass_kernel<{D // 32}, {bits}, false>"
         return names
-    return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>",
-            "kvmi_kstats_paged": f"kstats_kernel<{D}>"}
+    if pow2 and H <= 16 and 128 % H == 0:  # quad-per-row register FWHT
+        return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>",
+                "kvmi_kstats_paged": f"kstats_kernel<{D}>", "finalize": "kstats_finalize_kernel"}
+    lpr = 1 << max(0, (D // 16 - 1).bit_length())  # generic rows: next_pow2(D / 16) lanes per row
+    return {"kvmi_encode_paged": f"rows_encode_kernel<{lpr}, {bits}>", "kvmi_decode_paged":
+            f"rows_decode_kernel<{lpr}, {bits}>", "kvmi_kstats_paged": f"rows_stats_kernel<{lpr}>",
+            "finalize": "rows_finalize_kernel"}
 
 
 def compress_kernels(names: dict, cplan) -> list:
     """HIP kernels of one compress of `cplan`, in launch order."""
     if "kvmi_compress_paged" in names:
         return [names["kvmi_compress_paged"]]
-    return [names["kvmi_kstats_paged"], "kstats_finalize_kernel", names["kvmi_encode_paged"]]
+    return [names["kvmi_kstats_paged"], names["finalize"], names["kvmi_encode_paged"]]
 
 
 def traffic_frac(kernels, seconds: float, workload: str):
@@ -469,6 +476,29 @@ def bench_connector(args) -> dict:
 
     save_s, load_s = timed(connector_step, "connector")
     wire_bytes = next(r["payload_bytes"] for r in reversed(prod._transport.stats) if r["direction"] == "send")
+
+    # the kernels alone on the same request: the producer's codec, plans built outside
+    # the timed region, HIP events on the launch stream
+    mgr = prod._get_compressor()._manager
+    codec = mgr._codec(H, D, S)
+    profs = mgr.profiles(list(range(L)), H)
+    cplan = codec.plan_compress([caches[n] for n in order], ids, profs)
+    dplan = codec.plan_decompress(cplan.packet, [caches[n] for n in order], ids)
+    for _ in range(args.warmup):
+        cplan.run()
+        dplan.run()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    kc = kd = 0.0
+    for _ in range(args.steps):
+        ev[0].record()
+        cplan.run()
+        ev[1].record()
+        dplan.run()
+        ev[2].record()
+        ev[2].synchronize()
+        kc += ev[0].elapsed_time(ev[1])
+        kd += ev[1].elapsed_time(ev[2])
+    kernel_ms = (kc + kd) / args.steps
     ref_save_s, ref_load_s = timed(reference_step, "reference procedure")
     R = L * 2 * len(ids) * S * H * D * 2
     return {
@@ -488,6 +518,8 @@ def bench_connector(args) -> dict:
                    "raw_bytes": R, "wire_bytes": wire_bytes},
         "save_ms": round(save_s * 1e3, 4),
         "load_ms": round(load_s * 1e3, 4),
+        "kernel_ms": {"compress": round(kc / args.steps, 4), "decompress": round(kd / args.steps, 4)},
+        "connector_over_kernels": round((save_s + load_s) * 1e3 / kernel_ms, 3),
         "save_gbps": round(R / save_s / 1e9, 2),
         "load_gbps": round(R / load_s / 1e9, 2),
         "reference_procedure": {"save_ms": round(ref_save_s * 1e3, 4), "load_ms": round(ref_load_s * 1e3, 4),

@@ -173,6 +173,9 @@ class FusedKVCodec:
         self._lib = _lib.load()
         self._prof_cache: Dict[tuple, tuple] = {}
         self._pools_ok: Dict[tuple, tuple] = {}
+        self._stage_ring: List[tuple] = [(None, None)] * 4  # pinned upload buffers and their last copy's event
+        self._stage_next = 0
+        self._stage_last = 0
 
     # ---------------------------------------------------------------- helpers
     def _flags(self, max_level: int) -> int:
@@ -219,15 +222,24 @@ class FusedKVCodec:
         """Device of the per-layer caches after checking dtype, shape, layout and
         placement; the caches of a deployment are the same tensors on every request,
         so a passing set is remembered by identity and address."""
+        hit = self._pool_entry(pools)
+        if hit[1] is None:
+            self._pools_ok[hit[4]] = hit = hit[:1] + (self._check_pools_once(pools),) + hit[2:]
+        return hit[1]
+
+    def _pool_entry(self, pools: Sequence[torch.Tensor]) -> tuple:
+        """(pools, device once checked or None, base addresses, elements per part, key)
+        of a set of caches, remembered by identity and address."""
         key = tuple((id(p), p.data_ptr()) for p in pools)
         hit = self._pools_ok.get(key)
         if hit is not None and all(a is b for a, b in zip(hit[0], pools)):
-            return hit[1]
-        dev = self._check_pools_once(pools)
+            return hit
         if len(self._pools_ok) > 16:
             self._pools_ok.clear()
-        self._pools_ok[key] = (tuple(pools), dev)
-        return dev
+        hit = (tuple(pools), None, np.array([k[1] for k in key], np.int64),
+               np.array([p.shape[1] * self.S * self.H * self.D for p in pools], np.int64), key)
+        self._pools_ok[key] = hit
+        return hit
 
     def _check_pools_once(self, pools: Sequence[torch.Tensor]) -> torch.device:
         if not pools:
@@ -281,10 +293,12 @@ class FusedKVCodec:
         rows = self._job_rows(pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, B)
         if up is None:
             return torch.from_numpy(rows).to(dev, non_blocking=False)
-        host = np.zeros(up.numel(), np.uint8)
+        stage = self._staging(up.numel())
+        host = stage.numpy()
         host[:rows.nbytes] = rows.view(np.uint8).reshape(-1)
         host[rows.nbytes:rows.nbytes + host_ids.nbytes] = host_ids.view(np.uint8)
-        up.copy_(torch.from_numpy(host))
+        up.copy_(stage, non_blocking=True)
+        self._staged(dev)
         table = up[:rows.nbytes].view(torch.int64).view(rows.shape)
         table.block_ids = ids
         return table
@@ -303,8 +317,9 @@ class FusedKVCodec:
         def strided(t):  # address of t[l] for every l (t contiguous along its first axis)
             return _ptr(t) + lay * (t.stride(0) * t.element_size()) if t is not None else np.zeros(L, np.int64)
 
+        _, _, pool_ptrs, part_elems, _ = self._pool_entry(pools)
         rows = np.zeros((L, _lib.JOB_INT64S), dtype=np.int64)
-        rows[:, 0] = [_ptr(p) for p in pools]
+        rows[:, 0] = pool_ptrs
         rows[:, 1] = _ptr(ids)
         rows[:, 2] = stream
         rows[:, 3] = strided(kmeta)
@@ -312,11 +327,33 @@ class FusedKVCodec:
         rows[:, 5] = strided(signs)
         rows[:, 6] = strided(prof_dev)
         rows[:, 7] = strided(keys)
-        rows[:, 9] = [p.shape[1] * S * H * D for p in pools]
+        rows[:, 9] = part_elems
         rows[:, 10] = (lay - start) * per_layer
         rows[:, 11] = (stop - start) * per_layer
         rows[:, 12] = B | ((lay == start).astype(np.int64) << 32)
         return rows
+
+    def _staging(self, nbytes: int) -> torch.Tensor:
+        """A pinned host buffer of `nbytes` for an asynchronous upload: the next slot of
+        a small ring, waited on if its previous copy has not finished."""
+        i = self._stage_next
+        self._stage_next = (i + 1) % len(self._stage_ring)
+        buf, ev = self._stage_ring[i]
+        if ev is not None:
+            ev.synchronize()
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, pin_memory=True)
+        self._stage_ring[i] = (buf, None)
+        self._stage_last = i
+        return buf[:nbytes]
+
+    def _staged(self, device) -> None:
+        """Record the end of the upload (on `device`'s current stream) from the staging
+        slot just filled."""
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(device))
+        buf, _ = self._stage_ring[self._stage_last]
+        self._stage_ring[self._stage_last] = (buf, ev)
 
     def _profile_table(self, profiles: Sequence[LayerProfile], device) -> torch.Tensor:
         """uint8 [L, 2, 3, H] device copy of the profiles, cached per profile objects
