@@ -44,24 +44,27 @@ def hipcc() -> str:
     return exe
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path, defines=()) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *(f"-D{d}" for d in defines), f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
+def build(verbose: bool = False, defines=()) -> Path:
+    """Compile every HIP source and link the shared library; returns its path.
+    `defines`: preprocessor symbols for every source (KVMI_ORDINARY_LAUNCH: the one-pass
+    compress launched as an ordinary kernel, for profilers that cannot follow a
+    cooperative launch; its waits are bounded either way)."""
     OBJ.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
     with cf.ThreadPoolExecutor(max_workers=workers) as pool:
-        objs = list(pool.map(_compile, sources))
+        objs = list(pool.map(lambda src: _compile(src, defines), sources))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -74,5 +77,5 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, defines=["KVMI_ORDINARY_LAUNCH"] if "--ordinary-launch" in sys.argv[1:] else [])
     sys.exit(0)

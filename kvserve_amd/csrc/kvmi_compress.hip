@@ -541,8 +541,17 @@ int launch_pass(const PassArgs& in, int32_t mb, hipStream_t st, bool* taken) {
   }
   *taken = true;
   void* args[] = {&a};
+#ifdef KVMI_ORDINARY_LAUNCH
+  // profiling build (python -m kvserve_amd.build --ordinary-launch): the same grid of
+  // resident workgroups as an ordinary launch, which rocprofv3 can follow; every wait of
+  // the kernel is bounded, so a workgroup that would not be resident ends in
+  // KVMI_ERR_SYNC, never in a hang
+  const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(kernel), dim3((unsigned)(a.gsize * a.ngroups)),
+                                       dim3(kPW), args, 0, st);
+#else
   const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kernel),
                                                   dim3((unsigned)(a.gsize * a.ngroups)), dim3(kPW), args, 0, st);
+#endif
   return e == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 
