@@ -209,16 +209,16 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  *
  * Where the one-pass kernel applies (MFMA geometry, cooperative launch, and each
  * job's K fits the LDS of the workgroups sharing it: num_blocks*S*H*D*2 <= 64 KiB
- * per CU, e.g. 8192 tokens x 8 heads x 128 on 256 CUs), one cooperative launch keeps
- * every workgroup's share of a job's K on chip from the statistics to the
- * quantization.  Otherwise, or with KVMI_F_TWO_PASS, it runs kvmi_kstats_paged then
- * kvmi_encode_paged (which use each job's `kstats`).
+ * per CU on at most 256 CUs, e.g. 8192 tokens x 8 heads x 128), one cooperative
+ * launch keeps every workgroup's share of a job's K on chip from the statistics to
+ * the quantization.  Otherwise, or with KVMI_F_TWO_PASS, it runs kvmi_kstats_paged
+ * then kvmi_encode_paged (which use each job's `kstats`).
  *
  * workspace: kvmi_compress_workspace_bytes(geom, num_jobs) bytes of device memory,
  *   256-byte aligned, zeroed once by the caller before its first use and then passed
- *   unchanged to every call for the same jobs (per job: barrier counters and 64-bit
- *   min / max keys tagged with the call's epoch, so nothing is cleared between
- *   calls).  NULL selects the two-pass kernels.
+ *   unchanged to every call for the same jobs (per job: one barrier flag per
+ *   workgroup and 64-bit min / max keys, both holding the call's epoch, so nothing
+ *   is cleared between calls).  NULL selects the two-pass kernels.
  * epoch: host pointer to the workspace's call counter, 0 before the first call; it
  *   is incremented when (and only when) the one-pass kernel is enqueued.  Calls
  *   sharing a workspace must be ordered on one stream.
