@@ -75,6 +75,10 @@ WORKLOADS = {
                   "timed region, through impl 'tilelang_fused' (kvmi_v3_compress / kvmi_v3_decompress: fp32 FWHT and "
                   "statistics, uint8 symbols, fp32 metadata out, float16 metadata in), Hadamard seed 0xC0FEBABE, "
                   "Llama-3.1-8B head split hybrid 0.3, 16/16 levels; step = compress + decompress of every layer",
+    "bitpack": "bitpack: the operator-path BitPackCodec alone (kvmi_bitpack_encode / kvmi_bitpack_decode), "
+               "the config-2 request's 2^29 uint8 symbols (32 layers x 2 x 8192 tokens x 8 heads x 128) of "
+               "seeded values < 16 at 4 bits, all buffers allocated outside the timed region; step = encode + "
+               "decode",
     "runtime": "runtime: fixed-profile runtime (create_runtime backend 'fused'), token view (block_size 1) 1024 "
                "tokens x 28 layers x 4 KV "
                "heads x D=128, default profile (Hadamard, layer split, K channel / V token, levels 12/8 high "
@@ -659,6 +663,103 @@ def bench_fused_v3(args) -> dict:
     return res
 
 
+def bench_bitpack(args) -> dict:
+    """BitPackCodec of the operator path (bitpack_codec.py:100-135) through the C-ABI on
+    the config-2 symbol count; every buffer is allocated before the timed region."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from kvserve_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    bits, n = 4, 1 << 29
+    g = torch.Generator(device=dev).manual_seed(7)
+    sym = torch.randint(0, 1 << bits, (n,), dtype=torch.uint8, device=dev, generator=g)
+    nbytes = 16 + (n * bits + 7) // 8
+    stream_buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    back = torch.empty(n, dtype=torch.uint8, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    st = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(st.cuda_stream)
+
+    def encode():
+        _lib.check(lib.kvmi_bitpack_encode(sym.data_ptr(), n, bits, stream_buf.data_ptr(), err.data_ptr(), sp),
+                   "kvmi_bitpack_encode")
+
+    def decode():
+        _lib.check(lib.kvmi_bitpack_decode(stream_buf.data_ptr(), nbytes, n, bits, back.data_ptr(), err.data_ptr(),
+                                           sp), "kvmi_bitpack_decode")
+
+    print(f"bench: warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        encode()
+        decode()
+    torch.cuda.synchronize()
+    if err.item() != 0 or not torch.equal(back, sym):
+        raise RuntimeError("bitpack round trip failed")
+    print(f"bench: timing {args.steps} steps", file=sys.stderr, flush=True)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e in ev:
+        e[0].record(st)
+        encode()
+        e[1].record(st)
+        decode()
+        e[2].record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    t_e = sum(e[0].elapsed_time(e[1]) for e in ev) / args.steps
+    t_d = sum(e[1].elapsed_time(e[2]) for e in ev) / args.steps
+    alg = n + nbytes  # read the symbols, write the stream (or the reverse)
+    k_e, k_d = f"bitpack_encode_kernel<{bits}, true>", f"bitpack_decode_kernel<{bits}, true>"
+    te, td = profiled_traffic(k_e, "bitpack"), profiled_traffic(k_d, "bitpack")
+    dom, t_dom, tr_dom = (k_e, t_e, te) if t_e >= t_d else (k_d, t_d, td)
+    res = {
+        "metric": "bitpack encode/decode GB/s of uint8 symbols on 1 MI355X",
+        "value": round(n / ((t_e + t_d) / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic (seeded uniform symbols < 16)",
+        "config": {"workload": WORKLOADS["bitpack"], "symbols": n, "bits": bits, "stream_bytes": nbytes},
+        "encode_ms": round(t_e, 4),
+        "decode_ms": round(t_d, 4),
+        "encode_hbm_frac": round(alg / t_e / 1e6 / HBM_PEAK_GBPS, 4),
+        "decode_hbm_frac": round(alg / t_d / 1e6 / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(alg / t_dom / 1e6, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(alg / t_dom / 1e6 / HBM_PEAK_GBPS, 4), "traffic": tr_dom,
+                     "algorithmic_bytes_per_launch": alg},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        from oracle import cbitpack
+
+        print("bench: CPU oracle baseline", file=sys.stderr, flush=True)
+        m = 1 << 26
+        host = sym[:m].cpu().numpy()
+        k, t_cpu = 0, 0.0
+        while t_cpu < args.cpu_budget and k < 64:
+            t1 = time.perf_counter()
+            body = cbitpack.encode(host, bits)
+            cbitpack.decode(body, m, bits)
+            t_cpu += time.perf_counter() - t1
+            k += 1
+        res["cpu_baseline"] = {"value": round(k * m / t_cpu / 1e9, 4), "unit": "GB/s (encode + decode, symbols)",
+                               "cores": 1, "kind": "port",
+                               "sample": f"{k} x {m >> 20} Mi symbols in {t_cpu:.1f} s; the C oracle "
+                                         f"(oracle/cbitpack.py) encode + decode, one thread, on {cpu_model()}"}
+    return res
+
+
 def bench_runtime(args) -> dict:
     """The reference's runtime dispatch benchmark on the HIP runtime: wall time of
     K then V encode (each fenced), then K then V decode, plus device time of each
@@ -872,10 +973,10 @@ def main() -> int:
 
     import torch
 
-    if args.workload in ("connector", "config2_ans", "runtime", "config2_v3"):
+    if args.workload in ("connector", "config2_ans", "runtime", "config2_v3", "bitpack"):
         torch.cuda.set_device(0)
         fn = {"connector": bench_connector, "config2_ans": bench_entropy, "runtime": bench_runtime,
-              "config2_v3": bench_fused_v3}[args.workload]
+              "config2_v3": bench_fused_v3, "bitpack": bench_bitpack}[args.workload]
         print(json.dumps(fn(args)), flush=True)
         return 0
 

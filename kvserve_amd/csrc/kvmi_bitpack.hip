@@ -9,7 +9,7 @@
 //               bytes filled LSB first; pad bits are zero.
 //
 // Work split: one thread owns 32 consecutive symbols, i.e. exactly 4*bits payload
-// bytes, so every thread writes whole dwords and no two threads share a byte.
+// bytes, so no two threads share a byte; a workgroup's bytes are contiguous.
 #include "kvmi_device.hpp"
 #include "../../include/kvserve_amd.h"
 
@@ -36,16 +36,27 @@ __device__ __forceinline__ bool header_ok(const uint8_t* in, int bits, uint64_t 
          h[3] == (uint32_t)(n >> 32);
 }
 
-// VEC: input symbols 16-byte aligned and output 4-byte aligned (the usual case for
-// torch allocations); otherwise bytes are moved one at a time.
+// A workgroup's payload: kThreads chunks of 32 symbols, 4*BITS bytes each, contiguous
+// in the stream.  On the encoder's VEC path (symbols and stream 16-byte aligned, the
+// usual case for torch allocations) it passes through LDS, so that the stream is
+// written lane-linear in 16-byte pieces (each store instruction writes 1 KiB of
+// consecutive bytes) rather than as BITS dwords per lane at a 4*BITS-byte stride;
+// otherwise bytes move one at a time.  The decoder reads its 4*BITS bytes per lane
+// directly (reads do not depend on the lane stride here).
+template <int BITS>
+constexpr int wg_dwords() {
+  return kThreads * BITS;
+}
+
 template <int BITS, bool VEC>
 __global__ __launch_bounds__(kThreads) void bitpack_encode_kernel(const uint8_t* __restrict__ sym, int64_t n,
                                                                   uint8_t* __restrict__ out,
                                                                   int32_t* __restrict__ err) {
+  __shared__ uint4 stage[wg_dwords<BITS>() / 4];
   const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;  // chunk of 32 symbols
   if (c == 0) write_header(out, BITS, (uint64_t)n);
   const int64_t s0 = c * 32;
-  if (s0 >= n) return;
+  if (!VEC && s0 >= n) return;
   uint32_t s[32];
   if (VEC && s0 + 32 <= n) {
     const uint4* p = reinterpret_cast<const uint4*>(sym + s0);
@@ -63,14 +74,27 @@ __global__ __launch_bounds__(kThreads) void bitpack_encode_kernel(const uint8_t*
   if (ov >> BITS) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
   Packed<32, BITS> pk;
   pack_syms<32, BITS>(s, pk);
-  uint8_t* dst = out + KVMI_HEADER_BYTES + c * (4 * BITS);
   const int64_t payload = (n * BITS + 7) / 8;
-  const int64_t rem = payload - c * (4 * BITS);  // bytes this thread may write
-  if (VEC && rem >= 4 * BITS) {
-    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+  if constexpr (VEC) {
+    uint32_t* sw = reinterpret_cast<uint32_t*>(stage);
 #pragma unroll
-    for (int i = 0; i < BITS; ++i) d[i] = pk.w[i];
+    for (int i = 0; i < BITS; ++i) sw[threadIdx.x * BITS + i] = pk.w[i];
+    __syncthreads();
+    const int64_t base = (int64_t)blockIdx.x * (4 * wg_dwords<BITS>());  // payload bytes before this workgroup
+    const int64_t rem = payload - base;                                   // bytes this workgroup writes
+    uint8_t* dst = out + KVMI_HEADER_BYTES + base;
+    for (int q = threadIdx.x; q < wg_dwords<BITS>() / 4; q += kThreads) {
+      const int64_t off = 16 * (int64_t)q;
+      if (off + 16 <= rem) {
+        reinterpret_cast<uint4*>(dst)[q] = stage[q];
+      } else if (off < rem) {  // the stream's last, partial 16 bytes
+        const uint8_t* sb = reinterpret_cast<const uint8_t*>(stage);
+        for (int64_t b = off; b < rem; ++b) dst[b] = sb[b];
+      }
+    }
   } else {
+    uint8_t* dst = out + KVMI_HEADER_BYTES + c * (4 * BITS);
+    const int64_t rem = payload - c * (4 * BITS);  // bytes this thread may write
     const int nb = rem < 4 * BITS ? (int)rem : 4 * BITS;
     for (int i = 0; i < nb; ++i) dst[i] = (uint8_t)(pk.w[i >> 2] >> ((i & 3) * 8));
   }
@@ -123,7 +147,7 @@ template <int BITS>
 int launch_encode(const uint8_t* sym, int64_t n, uint8_t* out, int32_t* err, hipStream_t st) {
   const int64_t chunks = (n + 31) / 32;
   const int64_t grid = chunks > 0 ? (chunks + kThreads - 1) / kThreads : 1;
-  const bool vec = ((uintptr_t)sym % 16 == 0) && ((uintptr_t)out % 4 == 0);
+  const bool vec = ((uintptr_t)sym % 16 == 0) && ((uintptr_t)out % 16 == 0);
   if (vec)
     hipLaunchKernelGGL((bitpack_encode_kernel<BITS, true>), dim3((unsigned)grid), dim3(kThreads), 0, st, sym, n, out, err);
   else
