@@ -25,6 +25,9 @@
  *       kvserve_v1/utils/kv_utils.py:59-80 (extract_kv_from_layer_by_blocks)
  *   kvmi_scatter_blocks
  *       kvserve_v1/utils/kv_utils.py:83-119 (inject_kv_into_layer_by_blocks)
+ *   kvmi_gather_blocks_kv_adjacent / kvmi_scatter_blocks_kv_adjacent
+ *       kvserve_v1/utils/kv_utils.py:76-79 and :108-114 (the [num_blocks, 2, ...]
+ *       branches of the same two functions)
  *   kvmi_hadamard
  *       kvserve_v1/compression/transformer/hadamard_func.py:161-231
  *       (HadamardTransform.transform / .inverse)
@@ -169,6 +172,18 @@ int kvmi_gather_blocks(const void* pool, int64_t pool_part_stride, const int32_t
 int kvmi_scatter_blocks(void* pool, int64_t pool_part_stride, const int32_t* block_ids,
                         int32_t num_blocks, int64_t block_elems, const void* src,
                         kvmi_stream_t stream);
+
+/*
+ * The MLA / FlashInfer branch of the same two functions (kv_utils.py:76-79 and
+ * :108-114), cache layout [P, 2, S, H, D] with a block's K and V adjacent:
+ * gather out[i] = pool[block_ids[i]] into a contiguous [num_blocks, 2, S, H, D];
+ * scatter pool[block_ids[i]] = src[i] for i < num_blocks.  `block_elems` = S*H*D
+ * (one part of a block); element size 2 bytes.
+ */
+int kvmi_gather_blocks_kv_adjacent(const void* pool, const int32_t* block_ids, int32_t num_blocks,
+                                   int64_t block_elems, void* out, kvmi_stream_t stream);
+int kvmi_scatter_blocks_kv_adjacent(void* pool, const int32_t* block_ids, int32_t num_blocks,
+                                    int64_t block_elems, const void* src, kvmi_stream_t stream);
 
 /*
  * Random-sign Hadamard transform of contiguous bf16 rows [rows, D], row r

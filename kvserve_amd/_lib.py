@@ -42,6 +42,8 @@ EXPORTS = (
     "kvmi_bitpack_decode",
     "kvmi_gather_blocks",
     "kvmi_scatter_blocks",
+    "kvmi_gather_blocks_kv_adjacent",
+    "kvmi_scatter_blocks_kv_adjacent",
     "kvmi_hadamard",
     "kvmi_kstats_paged",
     "kvmi_encode_paged",
@@ -131,6 +133,8 @@ _SIGNATURES = {
     "kvmi_bitpack_decode": ([_vp, _i64, _i64, _i32, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_gather_blocks": ([_vp, _i64, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
     "kvmi_scatter_blocks": ([_vp, _i64, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
+    "kvmi_gather_blocks_kv_adjacent": ([_vp, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
+    "kvmi_scatter_blocks_kv_adjacent": ([_vp, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
     "kvmi_hadamard": ([_vp, _vp, _i64, _i32, _i32, _vp, _i32, _vp], ctypes.c_int),
     "kvmi_kstats_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_encode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),

@@ -1,9 +1,11 @@
 """Block-level KV extract / inject for the connector (kvserve_v1/utils/kv_utils.py:6-119).
 
-FlashAttention NHD caches ``[2, num_blocks, block_size, H, D]`` go through the HIP
-gather / scatter kernels.  The MLA / FlashInfer layout ``[num_blocks, 2, ...]``,
-which the compression path never takes (the reference does not request a layout
-for MLA and compresses only NHD), is copied with device-side tensor indexing.
+FlashAttention caches ``[2, num_blocks, ...]`` and MLA / FlashInfer caches
+``[num_blocks, 2, ...]`` that are contiguous 16-bit CUDA tensors go through the HIP
+gather / scatter kernels (kvmi_gather_blocks / kvmi_gather_blocks_kv_adjacent and
+the scatters); anything else is copied with device-side tensor indexing.  Only the
+FlashAttention NHD layout takes the fused compression path (the reference requests
+NHD, compressed_kv_connector.py:217-230).
 """
 
 from __future__ import annotations
@@ -30,6 +32,12 @@ def is_flash_layout(kv_layer: torch.Tensor) -> bool:
             and kv_layer.is_contiguous() and kv_layer.is_cuda)
 
 
+def _hip_copyable(kv_layer: torch.Tensor) -> bool:
+    """A contiguous 16-bit CUDA cache whose blocks are whole 16-byte vectors."""
+    return (kv_layer.dim() >= 3 and kv_layer.element_size() == 2 and kv_layer.is_contiguous() and kv_layer.is_cuda
+            and (kv_layer[0, 0].numel() * 2) % 16 == 0)
+
+
 def extract_kv_from_layer_by_blocks(kv_layer: torch.Tensor, block_ids: Sequence[int],
                                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """kv[:, block_ids] (FlashAttention) or kv[block_ids] (MLA) as a new tensor, or
@@ -43,8 +51,13 @@ def extract_kv_from_layer_by_blocks(kv_layer: torch.Tensor, block_ids: Sequence[
             idx = torch.tensor(list(block_ids), dtype=torch.long, device=kv_layer.device)
             res = kv_layer[:, idx]
     elif kv_layer.dim() > 1 and kv_layer.shape[1] == 2:
-        idx = torch.tensor(list(block_ids), dtype=torch.long, device=kv_layer.device)
-        res = kv_layer[idx]
+        if len(block_ids) == 0:
+            res = kv_layer[:0].clone()
+        elif _hip_copyable(kv_layer):
+            return ops.gather_blocks(kv_layer, block_ids, out=out)
+        else:
+            idx = torch.tensor(list(block_ids), dtype=torch.long, device=kv_layer.device)
+            res = kv_layer[idx]
     else:
         raise RuntimeError(f"Unsupported KV layout shape: {tuple(kv_layer.shape)}")
     if out is None:
@@ -68,6 +81,9 @@ def inject_kv_into_layer_by_blocks(kv_cache_layer: torch.Tensor, kv_data: torch.
         kv_cache_layer[:, idx[: payload.shape[1]]] = payload
         return
     if kv_cache_layer.dim() > 1 and kv_cache_layer.shape[1] == 2:
+        if _hip_copyable(kv_cache_layer):
+            ops.scatter_blocks(kv_cache_layer, kv_data, block_ids)
+            return
         payload = kv_data.to(kv_cache_layer.device)
         idx = torch.tensor(list(block_ids), dtype=torch.long, device=kv_cache_layer.device)
         kv_cache_layer[idx[: payload.shape[0]]] = payload

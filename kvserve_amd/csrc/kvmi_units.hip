@@ -9,8 +9,9 @@ namespace {
 
 constexpr int kCopyThreads = 256;
 
-// One workgroup copies one block of one part: 16-byte vectors when the block size
-// allows it (S*H*D*2 is a multiple of 16 for every D in {64, 128}).
+// One workgroup copies one block of one part (both parts of a block at once for the
+// [P, 2, ...] layout) in 16-byte vectors; the entry points require block sizes that
+// are multiples of 16 bytes.
 __global__ __launch_bounds__(kCopyThreads) void gather_kernel(const uint4* __restrict__ pool, int64_t part_stride16,
                                                               const int32_t* __restrict__ ids, int64_t blk16,
                                                               int32_t nblocks, uint4* __restrict__ out) {
@@ -84,6 +85,36 @@ extern "C" int kvmi_scatter_blocks(void* pool, int64_t pool_part_stride, const i
   hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)num_blocks, 2), dim3(kCopyThreads), 0, st,
                      static_cast<uint4*>(pool), pool_part_stride * 2 / 16, block_ids, block_elems * 2 / 16,
                      num_blocks, static_cast<const uint4*>(src));
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+// The MLA / FlashInfer cache layout [P, 2, S, H, D]: a block's K and V are adjacent,
+// so a block is one unit of 2*block_elems elements (one part per workgroup column).
+extern "C" int kvmi_gather_blocks_kv_adjacent(const void* pool, const int32_t* block_ids, int32_t num_blocks,
+                                              int64_t block_elems, void* out, kvmi_stream_t stream) {
+  using namespace kvmi;
+  if (num_blocks < 0 || block_elems <= 0) return KVMI_EINVAL;
+  if (num_blocks == 0) return KVMI_OK;
+  if (!pool || !block_ids || !out) return KVMI_EINVAL;
+  if ((block_elems * 2) % 16 || (uintptr_t)pool % 16 || (uintptr_t)out % 16) return KVMI_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(gather_kernel, dim3((unsigned)num_blocks, 1), dim3(kCopyThreads), 0, st,
+                     static_cast<const uint4*>(pool), (int64_t)0, block_ids, block_elems * 4 / 16, num_blocks,
+                     static_cast<uint4*>(out));
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+extern "C" int kvmi_scatter_blocks_kv_adjacent(void* pool, const int32_t* block_ids, int32_t num_blocks,
+                                               int64_t block_elems, const void* src, kvmi_stream_t stream) {
+  using namespace kvmi;
+  if (num_blocks < 0 || block_elems <= 0) return KVMI_EINVAL;
+  if (num_blocks == 0) return KVMI_OK;
+  if (!pool || !block_ids || !src) return KVMI_EINVAL;
+  if ((block_elems * 2) % 16 || (uintptr_t)pool % 16 || (uintptr_t)src % 16) return KVMI_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)num_blocks, 1), dim3(kCopyThreads), 0, st,
+                     static_cast<uint4*>(pool), (int64_t)0, block_ids, block_elems * 4 / 16, num_blocks,
+                     static_cast<const uint4*>(src));
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 

@@ -87,61 +87,86 @@ def bitpack_decode(stream: torch.Tensor, shape: Sequence[int], bits: int, check:
     return out
 
 
-def _pool_check(pool: torch.Tensor) -> None:
-    if pool.dim() < 3 or pool.shape[0] != 2:
+def _pool_layout(pool: torch.Tensor) -> str:
+    """"flash" for [2, num_blocks, ...], "kv_adjacent" for [num_blocks, 2, ...] (the
+    reference tests the first before the second, kv_utils.py:74-80)."""
+    if pool.dim() >= 3 and pool.shape[0] == 2:
+        layout = "flash"
+    elif pool.dim() >= 3 and pool.shape[1] == 2:
+        layout = "kv_adjacent"
+    else:
         raise RuntimeError(f"Unsupported KV layout shape: {tuple(pool.shape)}")
     if pool.element_size() != 2 or not pool.is_contiguous() or not pool.is_cuda:
         raise ValueError("paged gather/scatter needs a contiguous 16-bit CUDA KV cache")
+    return layout
 
 
-def _ids(block_ids, pool: torch.Tensor) -> torch.Tensor:
+def _ids(block_ids, num_blocks: int, device) -> torch.Tensor:
     if isinstance(block_ids, torch.Tensor):
-        ids = block_ids.to(device=pool.device, dtype=torch.int32).contiguous()
-        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= pool.shape[1]):
+        ids = block_ids.to(device=device, dtype=torch.int32).contiguous()
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= num_blocks):
             raise IndexError("block id outside the KV cache")
         return ids
     ids_list = [int(b) for b in block_ids]
-    if ids_list and (min(ids_list) < 0 or max(ids_list) >= pool.shape[1]):
+    if ids_list and (min(ids_list) < 0 or max(ids_list) >= num_blocks):
         raise IndexError("block id outside the KV cache")
-    return torch.tensor(ids_list, dtype=torch.int32, device=pool.device)
+    return torch.tensor(ids_list, dtype=torch.int32, device=device)
 
 
 def gather_blocks(pool: torch.Tensor, block_ids, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """extract_kv_from_layer_by_blocks (kv_utils.py:59-80), FlashAttention layout
-    [2, num_blocks, ...]: returns pool[:, block_ids] as a new contiguous tensor, or
-    writes it into `out` (contiguous, same shape and dtype; e.g. one layer's slice of
-    a stacked [L, 2, nb, ...] tensor) and returns `out`."""
-    _pool_check(pool)
-    ids = _ids(block_ids, pool)
-    shape = (2, ids.numel()) + tuple(pool.shape[2:])
+    """extract_kv_from_layer_by_blocks (kv_utils.py:59-80): pool[:, block_ids] of a
+    FlashAttention cache [2, num_blocks, ...], or pool[block_ids] of a [num_blocks, 2,
+    ...] cache (MLA / FlashInfer branch), as a new contiguous tensor, or written into
+    `out` (contiguous, same shape and dtype; e.g. one layer's slice of a stacked
+    tensor) and returned."""
+    layout = _pool_layout(pool)
+    flash = layout == "flash"
+    P = pool.shape[1] if flash else pool.shape[0]
+    ids = _ids(block_ids, P, pool.device)
+    shape = ((2, ids.numel()) if flash else (ids.numel(), 2)) + tuple(pool.shape[2:])
     if out is None:
         out = torch.empty(shape, dtype=pool.dtype, device=pool.device)
     elif tuple(out.shape) != shape or out.dtype != pool.dtype or out.device != pool.device \
             or not out.is_contiguous():
         raise ValueError(f"gather output must be a contiguous {pool.dtype} tensor of shape {shape} on {pool.device}")
     blk = math.prod(pool.shape[2:])
+    lib = _lib.load()
     with torch.cuda.device(pool.device):
-        _lib.check(_lib.load().kvmi_gather_blocks(pool.data_ptr(), pool.shape[1] * blk, ids.data_ptr(), ids.numel(),
-                                                  blk, out.data_ptr(), _stream()), "kvmi_gather_blocks")
+        if flash:
+            _lib.check(lib.kvmi_gather_blocks(pool.data_ptr(), P * blk, ids.data_ptr(), ids.numel(), blk,
+                                              out.data_ptr(), _stream()), "kvmi_gather_blocks")
+        else:
+            _lib.check(lib.kvmi_gather_blocks_kv_adjacent(pool.data_ptr(), ids.data_ptr(), ids.numel(), blk,
+                                                          out.data_ptr(), _stream()), "kvmi_gather_blocks_kv_adjacent")
     return out
 
 
 def scatter_blocks(pool: torch.Tensor, payload: torch.Tensor, block_ids) -> None:
-    """inject_kv_into_layer_by_blocks (kv_utils.py:83-119): pool[:, ids[:nb]] = payload."""
-    _pool_check(pool)
+    """inject_kv_into_layer_by_blocks (kv_utils.py:83-119): pool[:, ids[:nb]] =
+    payload for a FlashAttention cache, pool[ids[:nb]] = payload for a [num_blocks, 2,
+    ...] cache; nb = the payload's block count."""
+    layout = _pool_layout(pool)
+    flash = layout == "flash"
     n_ids = block_ids.numel() if isinstance(block_ids, torch.Tensor) else len(block_ids)
     if n_ids == 0:
         return
-    ids = _ids(block_ids, pool)
+    P = pool.shape[1] if flash else pool.shape[0]
+    ids = _ids(block_ids, P, pool.device)
     src = payload.to(device=pool.device, dtype=pool.dtype).contiguous()
-    nb = src.shape[1]
+    nb = src.shape[1] if flash else src.shape[0]
     ids = ids[:nb].contiguous()
-    if ids.numel() < nb or tuple(src.shape[2:]) != tuple(pool.shape[2:]):
+    if ids.numel() < nb or tuple(src.shape[2:]) != tuple(pool.shape[2:]) or (not flash and src.shape[1] != 2) \
+            or (flash and src.shape[0] != 2):
         raise ValueError("payload does not match the KV cache blocks")
     blk = math.prod(pool.shape[2:])
+    lib = _lib.load()
     with torch.cuda.device(pool.device):
-        _lib.check(_lib.load().kvmi_scatter_blocks(pool.data_ptr(), pool.shape[1] * blk, ids.data_ptr(), nb, blk,
-                                                   src.data_ptr(), _stream()), "kvmi_scatter_blocks")
+        if flash:
+            _lib.check(lib.kvmi_scatter_blocks(pool.data_ptr(), P * blk, ids.data_ptr(), nb, blk, src.data_ptr(),
+                                               _stream()), "kvmi_scatter_blocks")
+        else:
+            _lib.check(lib.kvmi_scatter_blocks_kv_adjacent(pool.data_ptr(), ids.data_ptr(), nb, blk, src.data_ptr(),
+                                                           _stream()), "kvmi_scatter_blocks_kv_adjacent")
 
 
 def hadamard(x: torch.Tensor, layer_id: int, seed: int, inverse: bool = False,

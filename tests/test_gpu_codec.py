@@ -102,6 +102,41 @@ def test_gather_scatter_bit_exact(cuda):
         ops.gather_blocks(pool.to(cuda), [40])
 
 
+@pytest.mark.parametrize("shape", [(40, 2, 16, 8, 128), (33, 2, 16, 4, 64), (12, 2, 3, 8)])
+def test_gather_scatter_kv_adjacent_bit_exact(cuda, shape):
+    """The [num_blocks, 2, ...] branch (kv_utils.py:76-79, :108-114) on the HIP kernels:
+    kv[ids] and kv[ids[:nb]] = payload, directly and through the connector's helpers."""
+    from kvserve_amd import ops
+    from kvserve_amd.connector.kv_utils import extract_kv_from_layer_by_blocks, inject_kv_into_layer_by_blocks
+
+    g = torch.Generator().manual_seed(shape[0])
+    pool = torch.randint(-30000, 30000, shape, generator=g, dtype=torch.int16).view(torch.bfloat16)
+    P = shape[0]
+    ids = [5, 0, P - 1, 7, 3]
+    print(f"kv-adjacent gather/scatter {shape}", flush=True)
+    got = ops.gather_blocks(pool.to(cuda), ids)
+    assert got.shape == (len(ids),) + shape[1:]
+    assert torch.equal(got.cpu().view(torch.int16), pool[ids].view(torch.int16))
+    via = extract_kv_from_layer_by_blocks(pool.to(cuda), ids)
+    assert torch.equal(via.cpu().view(torch.int16), pool[ids].view(torch.int16))
+    out = torch.empty_like(got)
+    assert ops.gather_blocks(pool.to(cuda), torch.tensor(ids, device=cuda), out=out) is out
+    assert torch.equal(out.view(torch.int16), got.view(torch.int16))  # bit patterns (NaNs included)
+    dst = torch.zeros_like(pool).to(cuda)
+    ops.scatter_blocks(dst, got, ids + [1, 2])  # more ids than payload blocks: overlap only
+    ref = torch.zeros_like(pool)
+    ref[ids] = pool[ids]
+    assert torch.equal(dst.cpu().view(torch.int16), ref.view(torch.int16))
+    dst2 = torch.zeros_like(pool).to(cuda)
+    inject_kv_into_layer_by_blocks(dst2, got, ids)
+    assert torch.equal(dst2.cpu().view(torch.int16), ref.view(torch.int16))
+    assert extract_kv_from_layer_by_blocks(pool.to(cuda), []).shape == (0,) + shape[1:]
+    with pytest.raises(IndexError):
+        ops.gather_blocks(pool.to(cuda), [P])
+    with pytest.raises(ValueError):
+        ops.scatter_blocks(dst, got[:, :1], ids)  # not a [nb, 2, ...] payload
+
+
 @pytest.mark.parametrize("D,H", [(64, 8), (128, 8), (96, 8), (256, 4), (80, 6), (16, 3), (224, 2)])
 def test_hadamard_unit_matches_oracle(cuda, D, H):
     """Power-of-two D and D split into power-of-two chunks (hadamard_func.py:50-103):
