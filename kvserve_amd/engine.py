@@ -171,7 +171,8 @@ class FusedKVCodec:
         if self.compress_path not in ("one_pass", "two_pass"):
             raise ValueError("compress_path must be 'one_pass' or 'two_pass'")
         self._lib = _lib.load()
-        self._prof_cache: Dict[tuple, tuple] = {}
+        self._prof_cache: Dict[tuple, torch.Tensor] = {}
+        self._prof_valid: set = set()
         self._pools_ok: Dict[tuple, tuple] = {}
         self._stage_ring: List[tuple] = [(None, None)] * 4  # pinned upload buffers and their last copy's event
         self._stage_next = 0
@@ -355,18 +356,35 @@ class FusedKVCodec:
         buf, _ = self._stage_ring[self._stage_last]
         self._stage_ring[self._stage_last] = (buf, ev)
 
-    def _profile_table(self, profiles: Sequence[LayerProfile], device) -> torch.Tensor:
-        """uint8 [L, 2, 3, H] device copy of the profiles, cached per profile objects
-        (a caller that keeps its profile list, as the compression manager does, uploads
-        it once)."""
-        key = (tuple(map(id, profiles)), str(device))
-        hit = self._prof_cache.get(key)
-        if hit is not None and all(a is b for a, b in zip(hit[0], profiles)):
-            return hit[1]
+    @staticmethod
+    def _profile_key(profiles: Sequence[LayerProfile]) -> tuple:
+        """The content of the profiles that validation and the device table depend on
+        (a snapshot: a profile edited in place gets a new key)."""
+        return tuple((tuple(p.k_order), tuple(p.k_levels), tuple(p.v_order), tuple(p.v_levels),
+                      tuple(p.v_group), None if p.k_group is None else tuple(p.k_group)) for p in profiles)
+
+    def _validate_profiles(self, profiles: Sequence[LayerProfile], key: tuple) -> None:
+        """LayerProfile.validate on every profile, once per distinct content."""
+        if key in self._prof_valid:
+            return
+        for p in profiles:
+            p.validate(self.H, k_groups=self.axes[0] != "channel")
+        if len(self._prof_valid) > 64:
+            self._prof_valid.clear()
+        self._prof_valid.add(key)
+
+    def _profile_table(self, profiles: Sequence[LayerProfile], device, key: Optional[tuple] = None) -> torch.Tensor:
+        """uint8 [L, 2, 3, H] device copy of the profiles, cached by their content (a
+        caller that keeps its profile list, as the compression manager does, uploads it
+        once)."""
+        ck = (self._profile_key(profiles) if key is None else key, str(device))
+        t = self._prof_cache.get(ck)
+        if t is not None:
+            return t
         t = torch.from_numpy(np.stack([p.to_array() for p in profiles])).to(device)
         if len(self._prof_cache) > 64:
             self._prof_cache.clear()
-        self._prof_cache[key] = (tuple(profiles), t)
+        self._prof_cache[ck] = t
         return t
 
     # ---------------------------------------------------------------- plans
@@ -387,8 +405,7 @@ class FusedKVCodec:
         L = len(pools)
         if len(profiles) != L:
             raise ValueError("one profile per layer is required")
-        for p in profiles:
-            p.validate(self.H, k_groups=self.axes[0] != "channel")
+        self._validate_profiles(profiles, self._profile_key(profiles))
         layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
         ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
         B = int(ids.numel()) if isinstance(ids, torch.Tensor) else int(ids.size)

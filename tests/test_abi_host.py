@@ -361,3 +361,27 @@ def test_job_table_rows_address_each_layer():
                 signs[l].data_ptr(), prof[l].data_ptr(), keys[l].data_ptr(), 0, 7 * 16 * 4 * 64, (l - s) * per,
                 (e - s) * per, B | ((1 if l == s else 0) << 32)]
         assert rows[l].tolist() == want, l
+
+
+def test_profile_validation_and_table_follow_content():
+    """Validation and the device profile table are cached by profile content: a
+    profile edited in place after a successful plan is validated (and uploaded) again."""
+    import torch
+
+    from kvserve_amd.engine import FusedKVCodec
+    from kvserve_amd.profiles import section_profile
+
+    codec = FusedKVCodec(4, 64, 16, 4)
+    profs = [section_profile([True, False, False, True], 16, 16, 12, 12) for _ in range(3)]
+    key = codec._profile_key(profs)
+    codec._validate_profiles(profs, key)
+    t0 = codec._profile_table(profs, "cpu")
+    assert codec._profile_table(profs, "cpu") is t0
+    assert torch.equal(t0, torch.from_numpy(np.stack([p.to_array() for p in profs])))
+    profs[1].v_order[0] = profs[1].v_order[1]  # no longer a permutation
+    with pytest.raises(ValueError, match="permutation"):
+        codec._validate_profiles(profs, codec._profile_key(profs))
+    profs[1].v_order[:] = [3, 0, 1, 2]
+    codec._validate_profiles(profs, codec._profile_key(profs))
+    t1 = codec._profile_table(profs, "cpu")
+    assert t1 is not t0 and t1[1, 1, 0].tolist() == [3, 0, 1, 2]
