@@ -194,6 +194,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
   // each store instruction writes 1 KB of consecutive bytes of the tile.
   constexpr int RQ = 4 * NC, RP = RQ + 1;  // uint4 per row, pitch
   __shared__ uint4 stage[NW * kTok * RP];
+  static_assert(!kVTable<BITS> || vtab_bytes<BITS>() <= kTok * RP * 16, "V table fits a wave's staging space");
   if (threadIdx.x == 0) {
     int good = 1;
     if (!(g.flags & KVMI_F_NO_HEADER)) {
@@ -245,13 +246,17 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
     const int64_t row0 = tile_row0(job, S, H, tile_tok(run.tok0, H, t));
     // dequantize into bf16 MFMA operands: x~ = bf16(bf16(q * scale) + min)
     uint4 x[2 * NC];
-    if (part)
-      dequant_half_row<NC, BITS, false>(in.pk, nullptr, bf16_to_f32(in.mn), bf16_to_f32(in.sc), x);
-    else
+    uint4* stg = stage + wave * (kTok * RP);
+    if (part) {
+      // V: the row table lives in the wave's staging space (free until the transform)
+      if constexpr (kVTable<BITS>)
+        dequant_v_table<NC, BITS>(in.pk, bf16_to_f32(in.mn), bf16_to_f32(in.sc), stg, x);
+      else
+        dequant_half_row<NC, BITS, false>(in.pk, nullptr, bf16_to_f32(in.mn), bf16_to_f32(in.sc), x);
+    } else
       dequant_half_row<NC, BITS, true>(in.pk, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), 0.f, 0.f, x);
     chunk_fence();
     const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(hme * (64 + 4) + (HALF / 2) * hl));
-    uint4* stg = stage + wave * (kTok * RP);
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
       const f32x16 acc = transform_T<NC>(x, hp, hn, cp);

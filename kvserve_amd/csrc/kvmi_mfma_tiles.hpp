@@ -504,6 +504,109 @@ __device__ __forceinline__ void dequant_half_row(const LanePack<16 * NC, BITS>& 
   }
 }
 
+// ---------------------------------------------------------------- V by table lookup
+// A V row has one (mn, sc) pair, so at widths 2 and 4 its dequantized values
+// x~(q) = bf16(bf16(q * sc) + mn) take 2^BITS values: the wave stages them per row in
+// LDS and each element becomes one LDS read instead of the convert / multiply / round /
+// add / round chain.  Layout of a wave's table (32 rows): entry (row r, symbol q) at
+// byte (r / 8) * G + 16 * q + 2 * (r % 8), G = 16 * 2^BITS + 16 (the pad turns each
+// group of 8 rows by four banks).  The address of a symbol is then the row's base
+// plus 16 * q, formed from the packed word with one byte-select add per element.
+template <int BITS>
+constexpr bool kVTable = BITS == 2 || BITS == 4;
+template <int BITS>
+constexpr int vtab_group() { return 16 * (1 << BITS) + 16; }
+template <int BITS>
+constexpr int vtab_bytes() { return 4 * vtab_group<BITS>(); }
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_u8*)p; }
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t a) { return *(const lds_u16*)(uintptr_t)a; }
+__device__ __forceinline__ void lds_write_u16(uint32_t a, uint32_t v) { *(lds_u16*)(uintptr_t)a = (uint16_t)v; }
+
+// base + byte B of packed (v_add_u32 with an SDWA byte select: one instruction).
+template <int B>
+__device__ __forceinline__ uint32_t add_byte(uint32_t packed, uint32_t base) {
+  uint32_t r;
+  if constexpr (B == 0)
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0 src1_sel:DWORD"
+        : "=v"(r) : "v"(packed), "v"(base));
+  else if constexpr (B == 1)
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:DWORD"
+        : "=v"(r) : "v"(packed), "v"(base));
+  else if constexpr (B == 2)
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2 src1_sel:DWORD"
+        : "=v"(r) : "v"(packed), "v"(base));
+  else
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3 src1_sel:DWORD"
+        : "=v"(r) : "v"(packed), "v"(base));
+  return r;
+}
+
+// 16 * (symbol of element e) in the byte lanes of word w, for the elements e of w
+// with e % P == M (P symbols per byte; byte b holds element P * b + M).
+template <int BITS, int M>
+__device__ __forceinline__ uint32_t sym16(uint32_t w) {
+  constexpr int sh = 4 - BITS * M;
+  constexpr uint32_t mask = 0x01010101u * (((1u << BITS) - 1u) << 4);
+  return (sh >= 0 ? (w << sh) : (w >> -sh)) & mask;
+}
+
+// Fill the table of the lane's row (lanes r and r + 32 take half the symbols each).
+template <int BITS>
+__device__ __forceinline__ void fill_v_table(uint32_t row_base, float mn, float sc) {
+  constexpr int EH = (1 << BITS) / 2;
+  const int hl = (threadIdx.x >> 5) & 1;
+#pragma unroll
+  for (int k = 0; k < EH; k += 2) {
+    const float q0 = (float)(EH * hl + k);
+    const uint32_t w = pack_bf16x2(rbf(q0 * sc) + mn, rbf((q0 + 1.f) * sc) + mn);
+    const uint32_t a = row_base + 16u * (uint32_t)(EH * hl + k);
+    lds_write_u16(a, w);
+    lds_write_u16(a + 16u, w >> 16);
+  }
+}
+
+// Dequantized bf16 MFMA operands of the lane's half-row of a V section from the
+// wave's table at `tab` (filled here): the values of dequant_half_row<NC, BITS, false>.
+template <int NC, int BITS>
+__device__ __forceinline__ void dequant_v_table(const LanePack<16 * NC, BITS>& pk, float mn, float sc, void* tab,
+                                                uint4 (&x)[2 * NC]) {
+  static_assert(kVTable<BITS>, "table lookup serves widths 2 and 4");
+  const int r = threadIdx.x & 31;
+  const uint32_t row_base = lds_addr(tab) + (uint32_t)((r >> 3) * vtab_group<BITS>() + 2 * (r & 7));
+  fill_v_table<BITS>(row_base, mn, sc);
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) {
+    uint32_t w[4];
+    if constexpr (BITS == 4) {
+      // word u: elements 8u + 2b in the low nibbles of byte b, 8u + 2b + 1 in the high
+      const uint32_t ev = sym16<4, 0>(pk.w[u]), od = sym16<4, 1>(pk.w[u]);
+      w[0] = lds_read_u16(add_byte<0>(ev, row_base)) | lds_read_u16(add_byte<0>(od, row_base)) << 16;
+      w[1] = lds_read_u16(add_byte<1>(ev, row_base)) | lds_read_u16(add_byte<1>(od, row_base)) << 16;
+      w[2] = lds_read_u16(add_byte<2>(ev, row_base)) | lds_read_u16(add_byte<2>(od, row_base)) << 16;
+      w[3] = lds_read_u16(add_byte<3>(ev, row_base)) | lds_read_u16(add_byte<3>(od, row_base)) << 16;
+    } else {
+      // word u / 2: element 4b + m in bits 2m of byte b; x[u] takes bytes 2(u % 2), +1
+      const uint32_t pw = pk.w[u / 2];
+      const uint32_t s0 = sym16<2, 0>(pw), s1 = sym16<2, 1>(pw), s2 = sym16<2, 2>(pw), s3 = sym16<2, 3>(pw);
+      if (u % 2 == 0) {
+        w[0] = lds_read_u16(add_byte<0>(s0, row_base)) | lds_read_u16(add_byte<0>(s1, row_base)) << 16;
+        w[1] = lds_read_u16(add_byte<0>(s2, row_base)) | lds_read_u16(add_byte<0>(s3, row_base)) << 16;
+        w[2] = lds_read_u16(add_byte<1>(s0, row_base)) | lds_read_u16(add_byte<1>(s1, row_base)) << 16;
+        w[3] = lds_read_u16(add_byte<1>(s2, row_base)) | lds_read_u16(add_byte<1>(s3, row_base)) << 16;
+      } else {
+        w[0] = lds_read_u16(add_byte<2>(s0, row_base)) | lds_read_u16(add_byte<2>(s1, row_base)) << 16;
+        w[1] = lds_read_u16(add_byte<2>(s2, row_base)) | lds_read_u16(add_byte<2>(s3, row_base)) << 16;
+        w[2] = lds_read_u16(add_byte<3>(s0, row_base)) | lds_read_u16(add_byte<3>(s1, row_base)) << 16;
+        w[3] = lds_read_u16(add_byte<3>(s2, row_base)) | lds_read_u16(add_byte<3>(s3, row_base)) << 16;
+      }
+    }
+    x[u] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // DPP lane exchange of a float (no bound_ctrl; every lane is enabled).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
