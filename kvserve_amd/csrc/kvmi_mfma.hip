@@ -99,6 +99,9 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   constexpr int RB = D * BITS / 8;            // bytes of one packed row
   constexpr int TQ = kTok * RB / 16;          // uint4 per tile
   __shared__ uint4 ostage[kWaves * TQ];
+  // per-wave parking of a V tile's rounded outputs between its statistics and its
+  // quantization (2*NC uint4 per lane)
+  __shared__ uint4 ypark[kWaves * 2 * NC * 64];
   const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
   stage_profile(T, job.profile, H);
   fill_signs(T, job.signs, H, D);
@@ -166,7 +169,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
     // ---------------- V: per-token statistics over the heads of a group
     sign_half_row<NC>(T, hme, hl, xv);
     LanePack<HALF, BITS> pkd;
-    quant_v_tile_twice<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, pkd, over);
+    quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, ypark + wave * (2 * NC * 64) + l, pkd,
+                                      over);
     pkd.store_lds(ost + offv);
     flush(1, ta);
   }

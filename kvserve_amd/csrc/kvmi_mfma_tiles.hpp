@@ -133,8 +133,13 @@ __device__ __forceinline__ bf16x2v sgpr_pair(uint32_t v) {
   return __builtin_bit_cast(bf16x2v, v);
 }
 
-// RN(lo(bf16 pair) + c) and RN(hi(bf16 pair) + c): v_dot2_f32_bf16 against (1, 0) /
-// (0, 1) is exactly one fp32 rounding of the sum (checked on gfx950 hardware).
+// lo(bf16 pair) + c and hi(bf16 pair) + c by v_dot2_f32_bf16 against (1, 0) / (0, 1).
+// On gfx950 the sum is exact when it fits fp32 and is otherwise rounded toward -inf
+// (measured: ~0.015 % of random bf16 + bf16-valued operand pairs differ from the fp32
+// add by one ulp).  Used only where both terms are bf16 values and the sum is rounded
+// to bf16 next: then the fp32 sum is exact when the exponents differ by at most 15, and
+// otherwise the smaller term is below 2^-15 of the larger, so both roundings of the
+// sum land on the larger term in bf16 -- the result equals bf16(fl(a + c)).
 __device__ __forceinline__ float add_lo(uint32_t pk, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pk), sgpr_pair(0x00003F80u), c, false);
 }
@@ -768,6 +773,63 @@ __device__ __forceinline__ void quant_v_tile(const uint4 (&xv)[2 * NC], const ui
 #pragma unroll
   for (int cp = 0; cp < NC; ++cp) {
     quant_chunk_v<HALF, BITS, CLAMP>(ypk + 8 * cp, cp, mn, rcp, lp.lvv, pkd, over);
+    chunk_fence();
+  }
+}
+
+// V section of a signed tile like quant_v_tile, with the rounded outputs y parked in
+// LDS between the statistics and the quantization instead of in registers (or a second
+// transform): `ylane` is the lane's slot of a wave buffer of 2*NC x 64 uint4 (stride 64
+// uint4, so every access of the wave is 1 KB of consecutive LDS).
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_v_tile_lds(const uint4 (&xv)[2 * NC], const uint4 (&hp)[2],
+                                                 const uint4 (&hn)[2], const LaneProfile& lp,
+                                                 const kvmi_layer_job& job, int ntok, int tok, int G, int H,
+                                                 float s, uint4* ylane, LanePack<16 * NC, BITS>& pkd,
+                                                 uint32_t& over) {
+  constexpr int HALF = 16 * NC;
+  float amn = __builtin_inff(), amx = -__builtin_inff();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
+      amx = fmaxf(fmaxf(amx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
+    }
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) w[i / 2] = pack_bf16x2(acc[i] * s, acc[i + 1] * s);
+    ylane[(2 * cp) * 64] = make_uint4(w[0], w[1], w[2], w[3]);
+    ylane[(2 * cp + 1) * 64] = make_uint4(w[4], w[5], w[6], w[7]);
+    chunk_fence();
+  }
+  amn = halves_min(amn);
+  amx = halves_max(amx);
+  float mn = 0.f, mx = 0.f;
+  for (int gg = 0; gg < G; ++gg) {
+    float a = lp.gv == gg ? amn : __builtin_inff();
+    float b = lp.gv == gg ? amx : -__builtin_inff();
+    token_minmax(a, b, H);
+    if (lp.gv == gg) {
+      mn = a;
+      mx = b;
+    }
+  }
+  mn = rbf(mn * s);
+  mx = rbf(mx * s);
+  const float sc = quant_scale(mn, mx, (int)lp.lvv);
+  const float rcp = 1.0f / sc;
+  if (lp.rep_lane) {
+    gst(job.vmeta + (int64_t)lp.gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
+    gst(job.vmeta + (int64_t)(G + lp.gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
+  }
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const uint4 a = ylane[(2 * cp) * 64], b = ylane[(2 * cp + 1) * 64];
+    const uint32_t ypk[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    quant_chunk_v<HALF, BITS, CLAMP>(ypk, cp, mn, rcp, lp.lvv, pkd, over);
     chunk_fence();
   }
 }
