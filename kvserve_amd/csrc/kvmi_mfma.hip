@@ -293,6 +293,136 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
   }
 }
 
+// ============================================================== decode, K by table (D = 128, 4 bits)
+// decode_mfma_kernel<4, 4, NW> with K dequantized by LDS lookups too.  A K element has
+// per-channel constants, so its table covers every (source head, channel): 34 KiB per
+// workgroup, made room for by staging half a row at a time.  That needs the element
+// split of hadamard_tile_d, where a lane's outputs of chunks 0-1 (2-3) are the row's
+// first (second) 128 bytes: the lane's inputs are then elements 16 s + 8 hl + (0..7),
+// which the lane pair (r, r + 32) trades from their loaded half-rows with one
+// v_permlane32_swap per two words.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void decode_kt_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                            int32_t* __restrict__ err) {
+  constexpr int NC = 4, BITS = 4, D = 128, HALF = 64;
+  const kvmi_layer_job job = jobs[blockIdx.y];
+  const int S = g.S, H = g.H, G = g.G;
+  const int ntok = job.num_blocks * S;
+  const Run run = wg_run(job, g);
+  if ((int)blockIdx.x >= run.nwg) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
+
+  __shared__ __attribute__((aligned(16))) DecTables T;
+  __shared__ int ok;
+  // Per-wave staging of half an output tile (32 rows x 128 bytes, pitch RP uint4 with
+  // one of padding), stored lane-linear: every store instruction writes eight full
+  // 128-byte lines.  The V row table lives in the same space until the transform.
+  constexpr int RH = 8, RP = RH + 1;
+  __shared__ uint4 stage[NW * kTok * RP];
+  __shared__ __attribute__((aligned(16))) uint8_t ktab[D * kKtabRow];
+  static_assert(vtab_bytes<BITS>() <= kTok * RP * 16, "V table fits a wave's staging space");
+  if (threadIdx.x == 0) {
+    int good = 1;
+    if (!(g.flags & KVMI_F_NO_HEADER)) {
+      good = header_matches(job.stream, BITS, job.chunk_symbols);
+      if (!good && blockIdx.x == 0) atomicOr(err, KVMI_ERR_BAD_HEADER);
+    }
+    ok = good;
+  }
+  stage_profile(T, job.profile, H);
+  fill_signs(T, job.signs, H, D);
+  __syncthreads();
+  if (!ok) return;
+  fill_positions(T, H);
+  fill_k_table(ktab, T, job.kmeta, H, D);
+  __syncthreads();
+
+  uint4 hp[2], hn[2];
+  hp[0] = hadamard_tile_d(0, false);
+  hp[1] = hadamard_tile_d(1, false);
+  hn[0] = hadamard_tile_d(0, true);
+  hn[1] = hadamard_tile_d(1, true);
+  uint16_t* poolK = reinterpret_cast<uint16_t*>(job.pool);
+  const int hme = r % H;
+  const int jk = T.posk[hme], jv = T.posv[hme];
+  const int gv = T.prof[1][2][jv];
+  const float s = g.scale;
+  const uint32_t kbase = lds_addr(ktab) + (uint32_t)(8 * hl * kKtabRow + 2 * hme);
+
+  struct In {
+    LanePack<HALF, BITS> pk;
+    uint32_t mn, sc;  // bf16 bits of the V row's (min, scale); unused for K
+  };
+  auto fetch = [&](int q, In& in) {
+    const int part = q >= run.tiles, t = q - part * run.tiles;
+    const int tok = tile_tok(run.tok0, H, t) + r / H;
+    in.pk.load(seg_addr<BITS>(job, g, part, part ? jv : jk, tok, HALF * hl));
+    in.mn = gld(job.vmeta + (int64_t)gv * ntok + tok);
+    in.sc = gld(job.vmeta + (int64_t)(G + gv) * ntok + tok);
+  };
+  auto section = [&](int q, In& in) {
+#pragma unroll
+    for (int i = 0; i < LanePack<HALF, BITS>::kWords; ++i) pin(in.pk.w[i]);
+    pin(in.mn);
+    pin(in.sc);
+    const int part = q >= run.tiles, t = q - part * run.tiles;
+    const int64_t row0 = tile_row0(job, S, H, tile_tok(run.tok0, H, t));
+    // word s: the symbols of elements 16 s + 8 hl + (0..7).  Lane half 0 holds words
+    // (2u, 2u + 1) = elements 16u + (0..15) of its row, half 1 the same of 64 + 16u:
+    // the swap leaves half 0 with (its 2u, the partner's 2u) and half 1 with (the
+    // partner's 2u + 1, its 2u + 1).
+    LanePack<HALF, BITS> W;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const auto pr = __builtin_amdgcn_permlane32_swap(in.pk.w[2 * u], in.pk.w[2 * u + 1], false, false);
+      W.w[u] = pr[0];
+      W.w[u + 4] = pr[1];
+    }
+    uint4 x[2 * NC];
+    uint4* stg = stage + wave * (kTok * RP);
+    if (part)
+      dequant_v_table<NC, BITS>(W, bf16_to_f32(in.mn), bf16_to_f32(in.sc), stg, x);
+    else
+      dequant_k_table(W.w, kbase, x);
+    chunk_fence();
+    // output signs of (head, element pair 16 c' + 8 hl + (0..7)): uint4 4 c' and 4 c' + 1
+    const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(hme * (64 + 4) + 8 * hl));
+    // the tile's 32 rows are contiguous in the pool; half h of a row is its bytes
+    // [128 h, 128 h + 128) = uint4 8 h .. 8 h + 7
+    uint4* dst = reinterpret_cast<uint4*>(poolK + part * job.pool_part_stride + row0 * D);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const int cp = 2 * h + c2;
+        const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = pack_bf16x2(acc[2 * i] * s, acc[2 * i + 1] * s);
+        stg[r * RP + 4 * c2 + 2 * hl] = xor4(make_uint4(w[0], w[1], w[2], w[3]), sm[4 * cp]);
+        stg[r * RP + 4 * c2 + 2 * hl + 1] = xor4(make_uint4(w[4], w[5], w[6], w[7]), sm[4 * cp + 1]);
+        chunk_fence();
+      }
+#pragma unroll
+      for (int u = 0; u < RH * kTok / 64; ++u) {
+        const int qq = 64 * u + l, row = qq / RH, j = qq % RH;
+        gst_stream(dst + row * (4 * NC) + RH * h + j, stg[row * RP + j]);
+      }
+    }
+  };
+  const int nsec = 2 * run.tiles, last_sec = nsec - 1;
+  In a, b;
+  if (wave < nsec) fetch(wave, a);
+  for (int q = wave; q < nsec; q += 2 * NW) {
+    fetch(min(q + NW, last_sec), b);
+    section(q, a);
+    if (q + NW >= nsec) break;
+    fetch(min(q + 2 * NW, last_sec), a);
+    section(q + NW, b);
+  }
+}
+
 // ============================================================== launch
 // Workgroups that fit on the device at once for `kernel` (CUs x resident
 // workgroups per CU), per device, computed on first use.
@@ -349,8 +479,11 @@ int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
 constexpr int kDecodeWaves = 8;  // waves per decode workgroup (two workgroups per CU)
 template <int NC, int BITS>
 int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
-  return launch(decode_mfma_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode,
-                64 * kDecodeWaves);
+  if constexpr (NC == 4 && BITS == 4)
+    return launch(decode_kt_kernel<kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode, 64 * kDecodeWaves);
+  else
+    return launch(decode_mfma_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode,
+                  64 * kDecodeWaves);
 }
 
 #define KVMI_MFMA_BITS(FN, NC)                                 \

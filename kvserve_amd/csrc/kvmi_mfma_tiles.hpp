@@ -122,6 +122,31 @@ __device__ __forceinline__ uint4 hadamard_tile(int kt, bool orient_n, bool negat
   return hadamard_tile((int)(threadIdx.x & 63), kt, orient_n, negate);
 }
 
+// Base tile kt for the split of decode_kt_kernel (D = 128, orientation T):
+//   input  e = 16*s + 8*hl + j    (k-step s = 2*t + kt, lane half hl = k/8, j = 0..7)
+//   output f = 32*c' + 16*m2 + i  (chunk c', MFMA row bit m2 = lane half, i = register)
+// so a lane's outputs of chunk c' are 16 consecutive elements and chunks 0-1 / 2-3 are
+// the two 128-byte halves of a row.  popc(f & e) = popc(c' & t) + the in-tile part
+// (m2 & kt) ^ (m4 & kh) ^ (m3 & j2) ^ (m1 & j1) ^ (m0 & j0) (i = 8 m4 + 4 m3 + 2 m1 + m0),
+// so transform_T over k-step operands x[2t + kt] gives this split's outputs.
+__device__ __forceinline__ uint4 hadamard_tile_d(int kt, bool negate) {
+  const int l = (int)(threadIdx.x & 63), kh = l >> 5, m = l & 31;
+  uint32_t w[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int j = 2 * p + s;
+      int par = ((m >> 2) & kt) ^ ((m >> 4) & kh) ^ ((m >> 3) & (j >> 2)) ^ ((m >> 1) & (j >> 1) & 1) ^ (m & j & 1);
+      par = (par ^ (negate ? 1 : 0)) & 1;
+      v |= (uint32_t)(par ? 0xBF80u : 0x3F80u) << (16 * s);
+    }
+    w[p] = v;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 __device__ __forceinline__ uint4 xor4(uint4 a, uint4 b) { return make_uint4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w); }
 
 // A bf16-pair constant held in an SGPR.  Left to itself the compiler encodes the
@@ -271,8 +296,17 @@ struct Tables {
   int posk[kMH], posv[kMH], gfirst[kMH];
 };
 
+// Decode tables of the K-table decode: the per-channel K pairs are replaced by the
+// table of dequantized values (decode_kt_kernel).
+struct DecTables {
+  uint32_t smask[kMH][64 + 4];
+  uint8_t prof[2][3][kMH];
+  int posk[kMH], posv[kMH], gfirst[kMH];
+};
+
 // Stage the profile bytes into LDS (one load per thread, no dependent chains).
-__device__ __forceinline__ void stage_profile(Tables& T, const uint8_t* profile, int H) {
+template <class TT>
+__device__ __forceinline__ void stage_profile(TT& T, const uint8_t* profile, int H) {
   if (threadIdx.x < 6u * H) {
     const int i = threadIdx.x, part = i / (3 * H), f = (i / H) % 3, k = i % H;
     T.prof[part][f][k] = gld(profile + i);
@@ -280,7 +314,8 @@ __device__ __forceinline__ void stage_profile(Tables& T, const uint8_t* profile,
 }
 
 // Fill the sign-mask table: word p of head h flips elements 2p and 2p+1.
-__device__ __forceinline__ void fill_signs(Tables& T, const uint32_t* signs, int H, int D) {
+template <class TT>
+__device__ __forceinline__ void fill_signs(TT& T, const uint32_t* signs, int H, int D) {
   for (int i = threadIdx.x; i < H * (D / 2); i += (int)blockDim.x) {
     const int h = i / (D / 2), p = i % (D / 2);
     const uint32_t s = gld(signs + h * (D / 32) + (2 * p) / 32) >> ((2 * p) & 31);
@@ -290,7 +325,8 @@ __device__ __forceinline__ void fill_signs(Tables& T, const uint32_t* signs, int
 
 // Output positions of each source head and the first head of each V group, from
 // the staged profile (after a barrier).
-__device__ __forceinline__ void fill_positions(Tables& T, int H) {
+template <class TT>
+__device__ __forceinline__ void fill_positions(TT& T, int H) {
   if (threadIdx.x < (unsigned)H) {
     const int h = threadIdx.x;
     for (int k = 0; k < H; ++k) {
@@ -609,6 +645,50 @@ __device__ __forceinline__ void dequant_v_table(const LanePack<16 * NC, BITS>& p
       }
     }
     x[u] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ---------------------------------------------------------------- K by table lookup
+// K table of decode_kt_kernel (D = 128, 4-bit symbols): the 16 dequantized values
+// bf16(bf16(q * sc) + mn) of every (source head hs, channel c) at byte
+// c * kKtabRow + 16 * q + 2 * hs.  kKtabRow = 272 turns the banks of channels eight
+// apart (the two lane halves of one k-step) by 32.
+constexpr int kKtabRow = 16 * 16 + 16;
+
+// Fill the table from the K metadata (stored by output position j, whose source head
+// is prof[0][0][j]); after the profile is staged.
+template <class TT>
+__device__ __forceinline__ void fill_k_table(uint8_t* ktab, const TT& T, const uint16_t* kmeta, int H, int D) {
+  const int HD = H * D;
+  const uint32_t base = lds_addr(ktab);
+  for (int i = threadIdx.x; i < HD; i += (int)blockDim.x) {
+    const int j = i / D, c = i % D, hs = T.prof[0][0][j];
+    const float mn = bf16_to_f32(gld(kmeta + i));
+    const float sc = bf16_to_f32(gld(kmeta + HD + i));
+    const uint32_t a = base + (uint32_t)(c * kKtabRow + 2 * hs);
+#pragma unroll
+    for (int q = 0; q < 16; q += 2) {
+      const uint32_t w = pack_bf16x2(rbf((float)q * sc) + mn, rbf((float)(q + 1) * sc) + mn);
+      lds_write_u16(a + 16u * q, w);
+      lds_write_u16(a + 16u * (q + 1), w >> 16);
+    }
+  }
+}
+
+// Dequantized bf16 MFMA operands of a K section of decode_kt_kernel: word W[s] holds
+// the symbols of elements 16 s + 8 hl + (0..7) (nibble j = element j), `base` is the
+// table address of the lane's (source head, channel 8 hl).
+__device__ __forceinline__ void dequant_k_table(const uint32_t (&W)[8], uint32_t base, uint4 (&x)[8]) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const uint32_t ev = sym16<4, 0>(W[s]), od = sym16<4, 1>(W[s]);
+    constexpr int R = kKtabRow;
+    const uint32_t o = (uint32_t)(16 * s * R);
+    const uint32_t w0 = lds_read_u16(add_byte<0>(ev, base) + o) | lds_read_u16(add_byte<0>(od, base) + o + R) << 16;
+    const uint32_t w1 = lds_read_u16(add_byte<1>(ev, base) + o + 2 * R) | lds_read_u16(add_byte<1>(od, base) + o + 3 * R) << 16;
+    const uint32_t w2 = lds_read_u16(add_byte<2>(ev, base) + o + 4 * R) | lds_read_u16(add_byte<2>(od, base) + o + 5 * R) << 16;
+    const uint32_t w3 = lds_read_u16(add_byte<3>(ev, base) + o + 6 * R) | lds_read_u16(add_byte<3>(od, base) + o + 7 * R) << 16;
+    x[s] = make_uint4(w0, w1, w2, w3);
   }
 }
 
