@@ -108,7 +108,8 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> di
     mfma = pow2 and codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
     if mfma:
         names = {"kvmi_encode_paged": f"encode_mfma_kernel<{D // 32}, {bits}, false>",
-                 "kvmi_decode_paged": f"decode_mfma_kernel<{D // 32}, {bits}, 8>",
+                 "kvmi_decode_paged": ("decode_kt_kernel<8>" if (D, bits) == (128, 4)
+                                       else f"decode_mfma_kernel<{D // 32}, {bits}, 8>"),
                  "kvmi_kstats_paged": f"kstats_mfma_kernel<{D // 32}>", "finalize": "kstats_finalize_kernel"}
         if cplan is not None and cplan.epoch.value > 0:  # the one-pass kernel ran
             names["kvmi_compress_paged"] = f"compress_pass_kernel<{D // 32}, {bits}, false>"
