@@ -21,6 +21,9 @@ pytestmark = pytest.mark.gpu
 
 SYM_MISMATCH_FRAC = 1e-4
 DEQ_REL_TOL = 1e-2
+# decode of the same stream by the GPU and by the oracle: bf16 neighbours (the inverse
+# transform's fp32 summation order) on at most this fraction of the elements
+OWN_DECODE_ULP_FRAC = 1e-3
 
 
 def _bits(t: torch.Tensor) -> np.ndarray:
@@ -47,6 +50,27 @@ def _layer_symbols(packet, l: int) -> np.ndarray:
     return cbitpack.decode(np.concatenate([_header(packet.bits, per), seg]), per, packet.bits)
 
 
+def _layer_stream(packet, l: int) -> np.ndarray:
+    """Layer l's byte-aligned segment of its chunk stream, behind a header of its own."""
+    ci = next(i for i, (s, e) in enumerate(packet.chunks) if s <= l < e)
+    per = 2 * packet.num_heads * packet.num_blocks * packet.block_size * packet.head_dim
+    nb = per * packet.bits // 8
+    off = 16 + (l - packet.chunks[ci][0]) * nb
+    return np.concatenate([_header(packet.bits, per), packet.streams[ci][off:off + nb].cpu().numpy()])
+
+
+def _assert_within_one_ulp(got_bits: np.ndarray, ref_bits: np.ndarray, frac: float, what):
+    """bf16 arrays (as uint16) equal except for neighbours (one ulp apart, same sign) on
+    at most `frac` of the elements."""
+    a, b = got_bits.view(np.int16).astype(np.int32), ref_bits.view(np.int16).astype(np.int32)
+    diff = a != b
+    n = int(np.count_nonzero(diff))
+    if n:
+        da, db = a[diff], b[diff]
+        assert np.all((da ^ db) >= 0) and np.abs(da - db).max() <= 1, (what, "more than one ulp apart")
+    assert n <= frac * a.size, (what, n, a.size)
+
+
 def _check_layer(packet, l: int, x_bits: np.ndarray, out_bits=None):
     """Layer l of `packet` against the oracle on that layer's gathered blocks x_bits
     [2, B, S, H, D]; out_bits: the GPU's decompressed blocks of the layer, if any."""
@@ -71,6 +95,14 @@ def _check_layer(packet, l: int, x_bits: np.ndarray, out_bits=None):
         for part in range(2):
             rel = np.abs(x[part] - xr[part]).max() / np.abs(xr[part]).max()
             assert rel <= DEQ_REL_TOL, (l, part, rel)
+        # the GPU's own stream and metadata decoded by the oracle: the same symbols and
+        # constants, so only the fp32 summation order of the inverse transform differs
+        own = kp.Chunk(0, 1, np.empty(ch.symbols.shape, np.uint8), _layer_stream(packet, l),
+                       [kp.LayerMeta(km[0], km[1], vm[0, :G], vm[1, :G])])
+        mine = np.zeros_like(x_bits)
+        kp.decompress_request([own], [mine], list(range(B)), [prof], packet.seed, packet.bits, layout=packet.layout,
+                              layer_ids=[lid])
+        _assert_within_one_ulp(out_bits, mine, OWN_DECODE_ULP_FRAC, l)
 
 
 def _free():
@@ -313,6 +345,8 @@ def test_config5_full_size_batch_sampled_matches_oracle(cuda):
     (8, 16, 128, 8),
     (16, 16, 128, 4),  # 8 % H != 0: register-FWHT kernels
     (8, 16, 64, 5),
+    (8, 16, 64, 4),    # D = 64 with the V row table
+    (4, 16, 64, 2),
 ])
 def test_geometries_match_oracle(cuda, H, S, D, bits):
     from kvserve_amd.engine import FusedKVCodec, check_packet
