@@ -33,3 +33,15 @@ def test_profiled_traffic_uses_consistent_rows_only(tmp_path):
 def test_committed_config2_summary_is_consistent():
     for k in ("encode_mfma_kernel<4, 4, false>", "kstats_mfma_kernel<4>", "kstats_finalize_kernel"):
         assert bench.profiled_traffic(k, "config2") is not None, k
+
+
+def test_config2_kernel_names_have_committed_profiles():
+    """Every kernel the default bench line names for config 2 has a consistent row in the
+    committed summary (the roofline's traffic field reads it)."""
+    from types import SimpleNamespace
+
+    codec = SimpleNamespace(axes=("channel", "token"), fwht="mfma", transform=True)
+    names = bench.hip_kernel_names(codec, 16, 8, 128, 4)
+    assert names["kvmi_decode_paged"] == "decode_kt_kernel<8>"
+    for k in names.values():
+        assert bench.profiled_traffic(k, "config2") is not None, k
