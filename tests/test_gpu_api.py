@@ -258,3 +258,23 @@ def test_streams_threads_and_graph_capture(cuda):
         assert all(torch.equal(a, b) for a, b in zip(eager, plan.packet.streams))
         assert torch.equal(km, plan.packet.kmeta)
     plan.check_errors()
+
+    # the decompress plan (the K-table decode at D = 128, 4 bits) replayed into cleared caches
+    dplan = fc.plan_decompress(plan.packet, req.pools, req.block_ids)
+    dplan.run()
+    torch.cuda.synchronize()
+    ids = req.block_ids.long()
+    want = [p[:, ids].clone() for p in req.pools]
+    dgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        torch.cuda.synchronize()
+        with torch.cuda.graph(dgraph, stream=st):
+            dplan.run()
+    for _ in range(3):
+        for p in req.pools:
+            p[:, ids] = 0
+        torch.cuda.synchronize()
+        dgraph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(p[:, ids].view(torch.int16), w.view(torch.int16)) for p, w in zip(req.pools, want))
+    dplan.check_errors()
