@@ -60,6 +60,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_ERR_BAD_HEADER 2   /* stream header does not match the decode contract */
 #define KVMI_ERR_CORRUPT 4      /* an entropy-coded block does not decode consistently */
 #define KVMI_ERR_SYNC 8         /* a one-pass compress barrier timed out or met another call's keys */
+#define KVMI_ERR_BLOCK_ID 16    /* a block id outside its pool (kvmi_check_block_ids) */
 
 /* Host-visible return codes. */
 #define KVMI_OK 0
@@ -116,7 +117,7 @@ typedef struct kvmi_geometry {
  * kstats: uint32 [2][H][D] order-preserving keys of the running K min / max; with
  *   KVMI_F_V_CHANNEL or KVMI_F_V_TENSOR, [2 parts][2][H][D] (V's keys after K's);
  *   initialised to {0xFFFFFFFF, 0}; kvmi_kstats_paged leaves it initialised.
- * counter: unused (may be null; kept for the layout of this struct).
+ * pool_blocks: P, the blocks of `pool`; read only by kvmi_check_block_ids.
  */
 typedef struct kvmi_layer_job {
   void* pool;                /* bf16 [2, P, S, H, D] paged KV of this layer (NHD) */
@@ -127,7 +128,7 @@ typedef struct kvmi_layer_job {
   const uint32_t* signs;     /* [H][ceil(D/32)] Rademacher sign bits per source head (1 = -1) */
   const uint8_t* profile;
   uint32_t* kstats;
-  uint32_t* counter;
+  int64_t pool_blocks;       /* P: block ids must lie in [0, P) */
   int64_t pool_part_stride;  /* elements between the K and V halves of `pool` */
   int64_t symbol_offset;     /* index of this layer's first symbol in the chunk */
   int64_t chunk_symbols;     /* symbol count N of the chunk (header bytes 8..15) */
@@ -184,6 +185,17 @@ int kvmi_gather_blocks_kv_adjacent(const void* pool, const int32_t* block_ids, i
                                    int64_t block_elems, void* out, kvmi_stream_t stream);
 int kvmi_scatter_blocks_kv_adjacent(void* pool, const int32_t* block_ids, int32_t num_blocks,
                                     int64_t block_elems, const void* src, kvmi_stream_t stream);
+
+/*
+ * Device-side check of the block tables of a job table, for callers whose block ids
+ * are a device tensor and who must not synchronize to check them on the host.  No
+ * counterpart in the reference (its torch indexing faults or raises on a bad id).  If
+ * any job holds an id outside [0, pool_blocks), sets KVMI_ERR_BLOCK_ID and sets
+ * num_blocks of every job to 0, so that the kernels enqueued after it on the stream
+ * (kvmi_kstats_paged, kvmi_encode_paged, kvmi_decode_paged) touch no pool memory.
+ * One workgroup per job; `jobs` is written, so it is the job table of one call.
+ */
+int kvmi_check_block_ids(kvmi_layer_job* jobs, int32_t num_jobs, int32_t* err, kvmi_stream_t stream);
 
 /*
  * Random-sign Hadamard transform of contiguous bf16 rows [rows, D], row r

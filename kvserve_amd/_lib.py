@@ -20,6 +20,7 @@ ERR_SYMBOL_RANGE = 1
 ERR_BAD_HEADER = 2
 ERR_CORRUPT = 4
 ERR_SYNC = 8
+ERR_BLOCK_ID = 16
 OK, EINVAL, ELAUNCH, ENOSPC = 0, -22, -5, -28
 # Bytes of the fixed device array behind kvmi_v3_compress_noalloc (per GPU).
 V3_NOALLOC_SCRATCH_BYTES = 4 * 1024 * 1024
@@ -44,6 +45,7 @@ EXPORTS = (
     "kvmi_scatter_blocks",
     "kvmi_gather_blocks_kv_adjacent",
     "kvmi_scatter_blocks_kv_adjacent",
+    "kvmi_check_block_ids",
     "kvmi_hadamard",
     "kvmi_kstats_paged",
     "kvmi_encode_paged",
@@ -113,11 +115,11 @@ class RtLayer(ctypes.Structure):
                 ("num_sections", ctypes.c_int32), ("reserved", ctypes.c_int32)]
 
 
-# kvmi_layer_job: 9 pointers, 3 int64, 2 int32 -> 104 bytes, 8-byte aligned.  It is
+# kvmi_layer_job: 8 pointers, 4 int64, 2 int32 -> 104 bytes, 8-byte aligned.  It is
 # written as 13 int64 words; the last word carries num_blocks (low half) and
 # write_header (high half).
 JOB_FIELDS = (
-    "pool", "block_ids", "stream", "kmeta", "vmeta", "signs", "profile", "kstats", "counter",
+    "pool", "block_ids", "stream", "kmeta", "vmeta", "signs", "profile", "kstats", "pool_blocks",
     "pool_part_stride", "symbol_offset", "chunk_symbols", "num_blocks_and_header",
 )
 JOB_INT64S = 13
@@ -134,6 +136,7 @@ _SIGNATURES = {
     "kvmi_gather_blocks": ([_vp, _i64, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
     "kvmi_scatter_blocks": ([_vp, _i64, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
     "kvmi_gather_blocks_kv_adjacent": ([_vp, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
+    "kvmi_check_block_ids": ([_vp, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_scatter_blocks_kv_adjacent": ([_vp, _vp, _i32, _i64, _vp, _vp], ctypes.c_int),
     "kvmi_hadamard": ([_vp, _vp, _i64, _i32, _i32, _vp, _i32, _vp], ctypes.c_int),
     "kvmi_kstats_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),

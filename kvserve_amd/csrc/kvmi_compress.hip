@@ -98,7 +98,7 @@ __device__ __forceinline__ kvmi_layer_job load_job(const kvmi_layer_job* jobs, i
   j.signs = cld(&q->signs);
   j.profile = cld(&q->profile);
   j.kstats = nullptr;
-  j.counter = nullptr;
+  j.pool_blocks = 0;
   j.pool_part_stride = cld(&q->pool_part_stride);
   j.symbol_offset = cld(&q->symbol_offset);
   j.chunk_symbols = cld(&q->chunk_symbols);

@@ -30,6 +30,24 @@ __global__ __launch_bounds__(kCopyThreads) void scatter_kernel(uint4* __restrict
   for (int64_t k = threadIdx.x; k < blk16; k += kCopyThreads) dst[k] = s[k];
 }
 
+// One workgroup per job: if any block id of the job lies outside [0, pool_blocks),
+// flag it and clear num_blocks of every job, so that the kernels enqueued after this
+// one on the stream run with nothing to do and touch no pool memory.
+__global__ __launch_bounds__(kCopyThreads) void check_blocks_kernel(kvmi_layer_job* __restrict__ jobs,
+                                                                    int32_t num_jobs, int32_t* __restrict__ err) {
+  const int32_t* ids = jobs[blockIdx.x].block_ids;
+  const int n = jobs[blockIdx.x].num_blocks;
+  const int64_t P = jobs[blockIdx.x].pool_blocks;
+  int mine = 0;
+  for (int i = threadIdx.x; i < n; i += kCopyThreads) {
+    const int32_t b = ids[i];
+    mine |= b < 0 || b >= P;
+  }
+  if (!__syncthreads_or(mine)) return;
+  if (threadIdx.x == 0) atomicOr(err, KVMI_ERR_BLOCK_ID);
+  for (int k = threadIdx.x; k < num_jobs; k += kCopyThreads) jobs[k].num_blocks = 0;
+}
+
 constexpr int kHadWG = 512;
 
 template <int D>
@@ -115,6 +133,16 @@ extern "C" int kvmi_scatter_blocks_kv_adjacent(void* pool, const int32_t* block_
   hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)num_blocks, 1), dim3(kCopyThreads), 0, st,
                      static_cast<uint4*>(pool), (int64_t)0, block_ids, block_elems * 4 / 16, num_blocks,
                      static_cast<const uint4*>(src));
+  return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
+}
+
+extern "C" int kvmi_check_block_ids(kvmi_layer_job* jobs, int32_t num_jobs, int32_t* err, kvmi_stream_t stream) {
+  using namespace kvmi;
+  if (num_jobs < 0) return KVMI_EINVAL;
+  if (num_jobs == 0) return KVMI_OK;
+  if (!jobs || !err) return KVMI_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(check_blocks_kernel, dim3((unsigned)num_jobs), dim3(kCopyThreads), 0, st, jobs, num_jobs, err);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
 

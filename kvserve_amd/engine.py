@@ -257,16 +257,18 @@ class FusedKVCodec:
                 raise ValueError("KV caches must live on one GPU")
         return dev
 
-    def _block_table(self, block_ids, device, pool_blocks: int):
-        """The block table, every id checked against the cache size on the host
-        before a kernel dereferences it: an int32 device tensor for device input (a
-        plan is built once, so the synchronization of that check is off the hot
-        path), else a host int32 array that the plan uploads with its job table."""
+    def _block_table(self, block_ids, device, pool_blocks: int, host_check: bool = False):
+        """The block table: a host int32 array, every id checked against the cache size
+        here and uploaded with the plan's job table; or, for a device tensor, the int32
+        device tensor, checked by the plan's first launch (kvmi_check_block_ids: a bad
+        id sets the error the plan reports and leaves the caches untouched), so that
+        building a plan does not synchronize.  `host_check` checks a device tensor here
+        too (the one-pass compress wants jobs that cannot be cleared under it)."""
         if isinstance(block_ids, torch.Tensor) and block_ids.is_cuda:
             if block_ids.dim() != 1:
                 raise ValueError("block_ids must be 1-D")
             ids = block_ids.to(device=device, dtype=torch.int32).contiguous()
-            if ids.numel():
+            if host_check and ids.numel():
                 lo, hi = int(ids.min().item()), int(ids.max().item())
                 if lo < 0 or hi >= pool_blocks:
                     raise IndexError("block id outside the KV cache")
@@ -284,20 +286,21 @@ class FusedKVCodec:
         device block table, or a host int32 array: it is then uploaded in the same copy
         as the table (returned as the table's `block_ids` attribute)."""
         dev = pools[0].device
-        up = None
-        if not isinstance(ids, torch.Tensor):
-            L = len(pools)
-            jb = L * _lib.JOB_INT64S * 8
+        L = len(pools)
+        jb = L * _lib.JOB_INT64S * 8
+        host_ids = None
+        if isinstance(ids, torch.Tensor):
+            up = torch.empty(jb, dtype=torch.uint8, device=dev)
+        else:
             up = torch.empty(jb + 4 * max(1, ids.size), dtype=torch.uint8, device=dev)
             host_ids = ids
             ids = up[jb:jb + 4 * ids.size].view(torch.int32)
         rows = self._job_rows(pools, ids, streams, chunks, kmeta, vmeta, signs, prof_dev, keys, B)
-        if up is None:
-            return torch.from_numpy(rows).to(dev, non_blocking=False)
         stage = self._staging(up.numel())
         host = stage.numpy()
         host[:rows.nbytes] = rows.view(np.uint8).reshape(-1)
-        host[rows.nbytes:rows.nbytes + host_ids.nbytes] = host_ids.view(np.uint8)
+        if host_ids is not None:
+            host[rows.nbytes:rows.nbytes + host_ids.nbytes] = host_ids.view(np.uint8)
         up.copy_(stage, non_blocking=True)
         self._staged(dev)
         table = up[:rows.nbytes].view(torch.int64).view(rows.shape)
@@ -328,6 +331,7 @@ class FusedKVCodec:
         rows[:, 5] = strided(signs)
         rows[:, 6] = strided(prof_dev)
         rows[:, 7] = strided(keys)
+        rows[:, 8] = part_elems // (S * H * D)  # pool blocks P of each layer
         rows[:, 9] = part_elems
         rows[:, 10] = (lay - start) * per_layer
         rows[:, 11] = (stop - start) * per_layer
@@ -407,7 +411,8 @@ class FusedKVCodec:
             raise ValueError("one profile per layer is required")
         self._validate_profiles(profiles, self._profile_key(profiles))
         layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
-        ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
+        ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools),
+                                host_check=self.compress_path == "one_pass")
         B = int(ids.numel()) if isinstance(ids, torch.Tensor) else int(ids.size)
         H, D, S = self.H, self.D, self.S
         raw = L * 2 * B * S * H * D * 2
@@ -529,7 +534,10 @@ class Plan:
         self.keys = codec._kstats_scratch(L, dev)
         self.jobs = codec._jobs(pools, ids, packet.streams, packet.chunks, packet.kmeta, packet.vmeta,
                                 self.signs, self.prof, self.keys, B)
-        if not isinstance(ids, torch.Tensor):
+        # a device block table is checked by the first launch of the plan's first run
+        # (the table is the plan's, as a host table would be checked once at build)
+        self.check_ids, self._ids_checked = isinstance(ids, torch.Tensor), False
+        if not self.check_ids:
             self.ids = self.jobs.block_ids  # uploaded with the job table
         self.err = torch.zeros(1, dtype=torch.int32, device=dev)
         max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
@@ -551,16 +559,22 @@ class Plan:
         """Names of the C entry points one run() enqueues, in order."""
         if self.max_blocks == 0:
             return []
+        first = ["kvmi_check_block_ids"] if self.check_ids and not self._ids_checked else []
         if self.kind == "compress":
             if self.workspace is not None:
-                return ["kvmi_compress_paged"]
-            return ["kvmi_kstats_paged", "kvmi_encode_paged"]
-        return ["kvmi_decode_paged"]
+                return first + ["kvmi_compress_paged"]
+            return first + ["kvmi_kstats_paged", "kvmi_encode_paged"]
+        return first + ["kvmi_decode_paged"]
 
     def launch(self, name: str) -> None:
         """Enqueue one of launches() on the current stream."""
         fn = getattr(self.codec._lib, name)
         with torch.cuda.device(self.device):
+            if name == "kvmi_check_block_ids":
+                if not self._ids_checked:  # once per plan
+                    _lib.check(fn(_ptr(self.jobs), self.num_jobs, _ptr(self.err), _stream_handle()), name)
+                    self._ids_checked = True
+                return
             if name == "kvmi_compress_paged":
                 if self.epoch.value >= 1 << 31:  # epoch tags are 32-bit: start the workspace afresh
                     self.workspace.zero_()
@@ -605,6 +619,7 @@ class BatchPlan:
         self.num_jobs = sum(p.num_jobs for p in plans)
         self.max_blocks = max(p.max_blocks for p in plans)
         self.jobs = torch.cat([p.jobs for p in plans])
+        self.check_ids, self._ids_checked = any(p.check_ids for p in plans), False
         max_level = max(max(max(pr.k_levels), max(pr.v_levels)) for p in plans for pr in p.packet.profiles)
         self.geo = p0.codec._geometry(p0.geo.max_groups, max_level)
         self.err = torch.zeros(1, dtype=torch.int32, device=self.device)
@@ -637,6 +652,8 @@ def raise_device_error(code: int) -> None:
         raise RuntimeError("invalid bitpack header or decode configuration")
     if code & _lib.ERR_CORRUPT:
         raise RuntimeError("corrupt entropy-coded stream")
+    if code & _lib.ERR_BLOCK_ID:
+        raise IndexError("block id outside the KV cache")
     if code & _lib.ERR_SYNC:
         raise RuntimeError("one-pass compress: a workgroup barrier timed out or met keys of another call")
 

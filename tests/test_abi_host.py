@@ -351,14 +351,14 @@ def test_job_table_rows_address_each_layer():
     signs = torch.zeros((L, 4, 2), dtype=torch.int32)
     prof = torch.zeros((L, 2, 3, 4), dtype=torch.uint8)
     keys = torch.zeros((L, 2, 2, 4, 64), dtype=torch.int32)
-    rows = codec._jobs(pools, ids, streams, chunks, kmeta, vmeta, signs, prof, keys, B).numpy()
+    rows = codec._job_rows(pools, ids, streams, chunks, kmeta, vmeta, signs, prof, keys, B)
     assert rows.shape == (L, _lib.JOB_INT64S)
     per = 2 * 4 * B * 16 * 64
     for l in range(L):
         ci = 0 if l < 2 else 1
         s, e = chunks[ci]
         want = [pools[l].data_ptr(), ids.data_ptr(), streams[ci].data_ptr(), kmeta[l].data_ptr(), vmeta[l].data_ptr(),
-                signs[l].data_ptr(), prof[l].data_ptr(), keys[l].data_ptr(), 0, 7 * 16 * 4 * 64, (l - s) * per,
+                signs[l].data_ptr(), prof[l].data_ptr(), keys[l].data_ptr(), 7, 7 * 16 * 4 * 64, (l - s) * per,
                 (e - s) * per, B | ((1 if l == s else 0) << 32)]
         assert rows[l].tolist() == want, l
 

@@ -305,3 +305,47 @@ def test_fused_bad_header_leaves_pool_untouched(cuda):
     with pytest.raises(RuntimeError, match="invalid bitpack header"):
         check_packet(packet)
     assert int(torch.count_nonzero(dst.view(torch.int16))) == 0
+
+
+def test_device_block_ids_checked_on_the_device(cuda):
+    """A device block table is checked by the plan's first launch instead of a host
+    synchronization: an id outside the cache (or negative) is reported as the
+    IndexError a host table raises, no kernel touches the caches, and a decompress
+    with such a table leaves them as they were; batches report it for all requests."""
+    from kvserve_amd.engine import FusedKVCodec, check_packet
+    from kvserve_amd.workloads import make_config1
+
+    wl = make_config1(device=cuda)
+    req = wl.requests[0]
+    fc = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed)
+    P = req.pools[0].shape[1]
+    good = fc.plan_compress(req.pools, req.block_ids, req.profiles)
+    assert good.launches() == ["kvmi_check_block_ids", "kvmi_kstats_paged", "kvmi_encode_paged"]
+    good.run()
+    good.check_errors()
+    assert good.launches() == ["kvmi_kstats_paged", "kvmi_encode_paged"]  # checked once per plan
+    for bad_id in (P, -1):
+        bad = req.block_ids.clone()
+        bad[1] = bad_id
+        print(f"device block table with id {bad_id}", flush=True)
+        plan = fc.plan_compress(req.pools, bad, req.profiles)  # builds without a host check
+        plan.run()
+        with pytest.raises(IndexError, match="block id outside the KV cache"):
+            check_packet(plan.packet)
+        before = [p.clone() for p in req.pools]
+        d = fc.plan_decompress(good.packet, req.pools, bad)
+        d.run()
+        with pytest.raises(IndexError):
+            d.check_errors()
+        assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(before, req.pools))
+    # one bad request in a batch: the batch's shared error word reports it
+    bad = req.block_ids.clone()
+    bad[0] = P + 5
+    bp = fc.plan_compress_batch([(req.pools, req.block_ids, req.profiles), (req.pools, bad, req.profiles)])
+    bp.run()
+    with pytest.raises(IndexError):
+        bp.check_errors()
+    # a good device table after all this still round-trips
+    d = fc.plan_decompress(good.packet, req.pools, req.block_ids)
+    d.run()
+    d.check_errors()

@@ -140,7 +140,8 @@ def test_batch_of_variable_requests_equals_single_plans_and_oracle(cuda):
     pools, reqs = _small_requests(cuda, g, [3, 7, 12, 1], L, H, D, S, P)
     codec = FusedKVCodec(H, D, S, 4, 0xC0FEBABE)
     bplan = codec.plan_compress_batch([(pools, ids.to(cuda), prof) for ids, prof in reqs])
-    assert bplan.launches() == ["kvmi_kstats_paged", "kvmi_encode_paged"] and bplan.num_jobs == L * len(reqs)
+    assert bplan.launches() == ["kvmi_check_block_ids", "kvmi_kstats_paged", "kvmi_encode_paged"]
+    assert bplan.num_jobs == L * len(reqs)
     bplan.run()
     for pk in bplan.packets:
         check_packet(pk)
@@ -157,7 +158,7 @@ def test_batch_of_variable_requests_equals_single_plans_and_oracle(cuda):
     # batched decompress into fresh pools equals the oracle's round trip
     dst = [torch.zeros_like(p) for p in pools]
     dplan = codec.plan_decompress_batch([(pk, dst, ids.to(cuda)) for (ids, _), pk in zip(reqs, bplan.packets)])
-    assert dplan.launches() == ["kvmi_decode_paged"]
+    assert dplan.launches() == ["kvmi_check_block_ids", "kvmi_decode_paged"]
     dplan.run()
     dplan.check_errors()
     for (ids, _), pk in zip(reqs, bplan.packets):

@@ -60,7 +60,7 @@ def _compare(cuda, pools, reqs, H, D, S, bits, layout="permuted", runs=3, expect
     one_codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path="one_pass")
     ref = ref_codec.plan_compress_batch(args)
     one = one_codec.plan_compress_batch(args)
-    assert one.launches() == ["kvmi_compress_paged"]
+    assert one.launches() == ["kvmi_check_block_ids", "kvmi_compress_paged"]
     ref.run()
     ref.check_errors()
     want = _outputs(ref)
