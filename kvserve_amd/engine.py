@@ -42,6 +42,16 @@ def _ptr(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else int(t.data_ptr())
 
 
+def _upload(host: torch.Tensor, device) -> torch.Tensor:
+    """Device copy of a host tensor that does not wait for the device: a pinned copy of
+    it sent by a non-blocking copy on the current stream (the caching host allocator
+    keeps the pinned buffer until that copy has run)."""
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return host.to(dev)
+    return host.pin_memory().to(dev, non_blocking=True)
+
+
 def _stream_handle() -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
@@ -63,7 +73,7 @@ class _SignCache:
             t = self._cache.get(key)
         if t is None:
             host = np.stack([rademacher_sign_bits(seed, l, H, D) for l in layer_ids])
-            t = torch.from_numpy(host.view(np.int32)).to(device)
+            t = _upload(torch.from_numpy(host.view(np.int32)), device)
             with self._lock:
                 self._cache[key] = t
         return t
@@ -385,7 +395,7 @@ class FusedKVCodec:
         t = self._prof_cache.get(ck)
         if t is not None:
             return t
-        t = torch.from_numpy(np.stack([p.to_array() for p in profiles])).to(device)
+        t = _upload(torch.from_numpy(np.stack([p.to_array() for p in profiles])), device)
         if len(self._prof_cache) > 64:
             self._prof_cache.clear()
         self._prof_cache[ck] = t
@@ -444,7 +454,7 @@ class FusedKVCodec:
                         self.transform, self.layout, layer_ids, self.axes)
         if B == 0 and self.header:
             for st in streams:
-                st.copy_(torch.from_numpy(_header_bytes(self.bits, 0)).to(dev))
+                st.copy_(_upload(torch.from_numpy(_header_bytes(self.bits, 0)), dev))
         return Plan(self, "compress", list(pools), ids, packet)
 
     def plan_decompress(self, packet: Packet, pools: Sequence[torch.Tensor], block_ids) -> "Plan":
