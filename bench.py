@@ -102,7 +102,8 @@ CONNECTOR_PROFILE = {
 
 def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> dict:
     """Name of the HIP kernel each entry point runs for this geometry (MFMA unless the
-    register-FWHT kernels are forced or the geometry is not MFMA-eligible)."""
+    register-FWHT kernels are forced, quad-per-row or generic rows, or the geometry is
+    not MFMA-eligible)."""
     default_axes = tuple(getattr(codec, "axes", ("channel", "token"))) == ("channel", "token")
     pow2 = D in (64, 128) and default_axes
     mfma = pow2 and codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
@@ -114,7 +115,7 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> di
         if cplan is not None and cplan.epoch.value > 0:  # the one-pass kernel ran
             names["kvmi_compress_paged"] = f"compress_pass_kernel<{D // 32}, {bits}, false>"
         return names
-    if pow2 and H <= 16 and 128 % H == 0:  # quad-per-row register FWHT
+    if pow2 and H <= 16 and 128 % H == 0 and codec.fwht != "rows":  # quad-per-row register FWHT
         return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>",
                 "kvmi_kstats_paged": f"kstats_kernel<{D}>", "finalize": "kstats_finalize_kernel"}
     lpr = 1 << max(0, (D // 16 - 1).bit_length())  # generic rows: next_pow2(D / 16) lanes per row

@@ -86,6 +86,9 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_F_K_TENSOR 128u  /* one K statistic pair per K group */
 #define KVMI_F_V_CHANNEL 256u /* V statistics per channel of each head */
 #define KVMI_F_V_TENSOR 512u  /* one V statistic pair per V group */
+/* Force the generic row kernels (register FWHT with DPP exchanges over next_pow2(D)/16
+ * lanes of a row) instead of MFMA or the quad-per-row kernels. */
+#define KVMI_F_ROW_FWHT 1024u
 
 /* Launch-wide geometry shared by every job of one call. */
 typedef struct kvmi_geometry {

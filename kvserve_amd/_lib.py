@@ -35,6 +35,7 @@ F_K_TOKEN = 64
 F_K_TENSOR = 128
 F_V_CHANNEL = 256
 F_V_TENSOR = 512
+F_ROW_FWHT = 1024
 
 # Every symbol include/kvserve_amd.h declares.
 EXPORTS = (

@@ -117,7 +117,7 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
   if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
   if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
   if (geom->flags & ~(KVMI_F_NO_TRANSFORM | KVMI_F_NATIVE_LAYOUT | KVMI_F_NO_HEADER | KVMI_F_VALU_FWHT |
-                      KVMI_F_CLAMP_LEVELS | KVMI_F_TWO_PASS | kAxisFlags))
+                      KVMI_F_CLAMP_LEVELS | KVMI_F_TWO_PASS | KVMI_F_ROW_FWHT | kAxisFlags))
     return KVMI_EINVAL;
   if ((geom->flags & KVMI_F_K_TOKEN) && (geom->flags & KVMI_F_K_TENSOR)) return KVMI_EINVAL;
   if ((geom->flags & KVMI_F_V_CHANNEL) && (geom->flags & KVMI_F_V_TENSOR)) return KVMI_EINVAL;
@@ -140,13 +140,15 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
 //    H <= 16;
 //  * generic rows (kvmi_rows.hip): every other geometry check_geo admits (D a
 //    multiple of 16 up to 256, split into power-of-two chunks when it is not one;
-//    H up to 64), and every non-default quantization axis.
+//    H up to 64), every non-default quantization axis, and any geometry when the
+//    caller forces them (KVMI_F_ROW_FWHT).
 inline bool mfma_eligible(const Geo& g) {
-  return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_NO_TRANSFORM | kAxisFlags)) && (g.D == 64 || g.D == 128) &&
-         (8 % g.H) == 0 && ((g.S * g.H) % 32) == 0;
+  return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_ROW_FWHT | KVMI_F_NO_TRANSFORM | kAxisFlags)) &&
+         (g.D == 64 || g.D == 128) && (8 % g.H) == 0 && ((g.S * g.H) % 32) == 0;
 }
 inline bool quad_eligible(const Geo& g) {
-  return !(g.flags & kAxisFlags) && (g.D == 64 || g.D == 128) && g.H <= kMaxQuadH && (128 % g.H) == 0;
+  return !(g.flags & (KVMI_F_ROW_FWHT | kAxisFlags)) && (g.D == 64 || g.D == 128) && g.H <= kMaxQuadH &&
+         (128 % g.H) == 0;
 }
 int rows_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t num_jobs, int32_t max_blocks, int32_t* err,
                 hipStream_t st);

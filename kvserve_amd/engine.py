@@ -170,10 +170,12 @@ class FusedKVCodec:
         self.axes = axes
         self.H, self.D, self.S, self.bits = num_heads, head_dim, block_size, bits
         self.seed, self.transform, self.layout, self.header = int(seed), transform, layout, header
-        # Hadamard on MFMA (default) or the register FWHT kernels (KVSERVE_AMD_FWHT=valu)
+        # Hadamard on MFMA (default), or forced onto the register FWHT kernels:
+        # "valu" the quad-per-row kernels, "rows" the generic row kernels
+        # (KVSERVE_AMD_FWHT=valu|rows)
         self.fwht = (fwht or os.environ.get("KVSERVE_AMD_FWHT", "mfma")).strip().lower()
-        if self.fwht not in ("mfma", "valu"):
-            raise ValueError("fwht must be 'mfma' or 'valu'")
+        if self.fwht not in ("mfma", "valu", "rows"):
+            raise ValueError("fwht must be 'mfma', 'valu' or 'rows'")
         # compress: "two_pass" (kvmi_kstats_paged + kvmi_encode_paged, the faster on
         # MI355X) or "one_pass" (kvmi_compress_paged: every K value read from HBM once
         # where the jobs fit the one-pass kernel; KVSERVE_AMD_COMPRESS=one_pass)
@@ -199,6 +201,8 @@ class FusedKVCodec:
             f |= _lib.F_NO_HEADER
         if self.fwht == "valu":
             f |= _lib.F_VALU_FWHT
+        elif self.fwht == "rows":
+            f |= _lib.F_ROW_FWHT
         if max_level > 128:
             f |= _lib.F_CLAMP_LEVELS
         f |= {"channel": 0, "token": _lib.F_K_TOKEN, "tensor": _lib.F_K_TENSOR}[self.axes[0]]

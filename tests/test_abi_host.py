@@ -385,3 +385,29 @@ def test_profile_validation_and_table_follow_content():
     codec._validate_profiles(profs, codec._profile_key(profs))
     t1 = codec._profile_table(profs, "cpu")
     assert t1 is not t0 and t1[1, 1, 0].tolist() == [3, 0, 1, 2]
+
+
+def test_flag_and_error_constants_match_the_header():
+    """The Python mirror's KVMI_F_* and KVMI_ERR_* values are the header's."""
+    from kvserve_amd import _lib
+
+    text = HEADER.read_text()
+    flags = dict(re.findall(r"#define KVMI_F_(\w+) (\d+)u", text))
+    errs = dict(re.findall(r"#define KVMI_ERR_(\w+) (\d+)", text))
+    assert "ROW_FWHT" in flags and "BLOCK_ID" in errs
+    for name, v in flags.items():
+        assert getattr(_lib, "F_" + name) == int(v), name
+    for name, v in errs.items():
+        assert getattr(_lib, "ERR_" + name) == int(v), name
+
+
+def test_fwht_choice_sets_its_flag():
+    """fwht='valu' / 'rows' force the quad-per-row / generic row kernels through their flags."""
+    from kvserve_amd import _lib
+    from kvserve_amd.engine import FusedKVCodec
+
+    assert FusedKVCodec(8, 128, 16, 4, fwht="mfma")._flags(16) & (_lib.F_VALU_FWHT | _lib.F_ROW_FWHT) == 0
+    assert FusedKVCodec(8, 128, 16, 4, fwht="valu")._flags(16) & _lib.F_VALU_FWHT
+    assert FusedKVCodec(8, 128, 16, 4, fwht="rows")._flags(16) & _lib.F_ROW_FWHT
+    with pytest.raises(ValueError):
+        FusedKVCodec(8, 128, 16, 4, fwht="dpp")

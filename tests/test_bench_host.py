@@ -45,3 +45,12 @@ def test_config2_kernel_names_have_committed_profiles():
     assert names["kvmi_decode_paged"] == "decode_kt_kernel<8>"
     for k in names.values():
         assert bench.profiled_traffic(k, "config2") is not None, k
+
+
+def test_kernel_names_follow_the_forced_fwht():
+    """The bench names the kernels the forced register-FWHT families launch."""
+    from types import SimpleNamespace
+
+    for fwht, enc in (("valu", "encode_kernel<128, 4>"), ("rows", "rows_encode_kernel<8, 4>")):
+        codec = SimpleNamespace(axes=("channel", "token"), fwht=fwht, transform=True)
+        assert bench.hip_kernel_names(codec, 16, 8, 128, 4)["kvmi_encode_paged"] == enc

@@ -389,6 +389,17 @@ def test_geometries_match_oracle(cuda, H, S, D, bits):
 def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
     """The generic row kernels (kvmi_rows.hip) run the oracle's FWHT stage order, so
     symbols, metadata and the decompressed KV are bit-exact with the oracle."""
+    _rows_exact(cuda, H, S, D, bits, layout)
+
+
+@pytest.mark.parametrize("H,S,D,bits", [(8, 16, 128, 4), (8, 16, 64, 4), (4, 32, 128, 3)])
+def test_forced_row_kernels_match_oracle_exactly(cuda, H, S, D, bits):
+    """fwht='rows' runs the generic row kernels on geometries the MFMA kernels serve (the
+    register-FWHT comparison of the profile summaries): bit-exact with the oracle too."""
+    _rows_exact(cuda, H, S, D, bits, "permuted", fwht="rows")
+
+
+def _rows_exact(cuda, H, S, D, bits, layout, fwht=None):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.profiles import section_profile
     from kvserve_amd.workloads import kv_blocks
@@ -402,9 +413,9 @@ def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
         p[:, ids] = kv_blocks(g, B, S, H, D)
     prof = [section_profile([bool(v) for v in torch.randint(0, 2, (H,), generator=g)], levels[0], levels[0],
                             levels[1], levels[1]) for _ in range(L)]
-    print(f"generic geometry H={H} S={S} D={D} bits={bits} {layout}", flush=True)
+    print(f"generic geometry H={H} S={S} D={D} bits={bits} {layout} fwht={fwht}", flush=True)
     pools = [p.to(cuda) for p in pools]
-    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout)
+    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, fwht=fwht)
     dev_ids = ids.to(torch.int32).to(cuda)
     packet = codec.compress(pools, dev_ids, prof)
     check_packet(packet)
@@ -424,7 +435,7 @@ def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
         assert np.array_equal(_bits(dst[l][:, dev_ids.long()]), ref), l
 
 
-@pytest.mark.parametrize("fwht", ["mfma", "valu"])
+@pytest.mark.parametrize("fwht", ["mfma", "valu", "rows"])
 def test_batch_with_empty_request_writes_its_header(cuda, fwht):
     """A request without blocks in a batch still gets a valid 16-byte header for N = 0
     from the encode launch (the C-ABI contract, independent of the host's plan-time
