@@ -72,6 +72,15 @@ def test_host_contract_errors_return_einval():
     assert lib.kvmi_encode_paged(ctypes.byref(gg), None, 1, 1, None, None) == E
     # zero jobs / zero blocks: nothing to do
     assert lib.kvmi_encode_paged(ctypes.byref(g), None, 0, 5, None, None) == 0
+    # unknown flag bits are refused
+    gg = _lib.Geometry.from_buffer_copy(g)
+    gg.flags = 2048
+    assert lib.kvmi_encode_paged(ctypes.byref(gg), None, 1, 1, None, None) == E
+    # the device block-table check: no jobs is a no-op, bad arguments are refused
+    assert lib.kvmi_check_block_ids(None, 0, None, None) == 0
+    assert lib.kvmi_check_block_ids(None, -1, None, None) == E
+    assert lib.kvmi_check_block_ids(None, 2, ctypes.addressof(err), None) == E
+    assert lib.kvmi_check_block_ids(ctypes.addressof(buf), 2, None, None) == E
 
 
 def test_rans_sizes_and_contract_errors():
