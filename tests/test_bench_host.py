@@ -54,3 +54,12 @@ def test_kernel_names_follow_the_forced_fwht():
     for fwht, enc in (("valu", "encode_kernel<128, 4>"), ("rows", "rows_encode_kernel<8, 4>")):
         codec = SimpleNamespace(axes=("channel", "token"), fwht=fwht, transform=True)
         assert bench.hip_kernel_names(codec, 16, 8, 128, 4)["kvmi_encode_paged"] == enc
+
+
+def test_settle_phase_is_off_at_zero_and_a_flag_of_the_bench():
+    """--settle-ms 0 runs no untimed steps; the default settles before the warmup."""
+    calls = []
+    assert bench.settle_device(lambda: calls.append(1), 0) == 0 and not calls
+    import inspect
+
+    assert "--settle-ms" in inspect.getsource(bench.main)
