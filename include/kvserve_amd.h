@@ -410,7 +410,7 @@ typedef struct kvmi_rt_layer {
 } kvmi_rt_layer;               /* 136 bytes; an array of them in device memory */
 
 /*
- * Encode the body of one chunk for one KV part (runtime pipeline.py:554-651): rows of
+ * Encode the body of one chunk for one KV part (runtime pipeline.py:557-669): rows of
  * `num_blocks` physical blocks (block_ids, device int64) of every layer.  Quantized:
  * aux receives the section minima / scales (and, at +aux_half_bytes, maxima /
  * inverses), the payload the u8 symbols at each layer's u8_offset; `canon` is device
@@ -422,7 +422,7 @@ int kvmi_rt_encode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, in
                    int64_t aux_half_bytes, kvmi_stream_t stream);
 /* Scratch bytes kvmi_rt_encode needs for `rows` rows of `num_layers` layers of H x D. */
 int64_t kvmi_rt_scratch_bytes(int32_t num_layers, int64_t rows, int32_t num_heads, int32_t head_dim);
-/* Inverse (pipeline.py:652-763): payload (+ aux) -> the caches at block_ids. */
+/* Inverse (pipeline.py:720-804): payload (+ aux) -> the caches at block_ids. */
 int kvmi_rt_decode(const kvmi_rt_geometry* geom, const kvmi_rt_layer* layers, int32_t num_layers,
                    const int64_t* block_ids, int64_t num_blocks, const uint8_t* packed, const uint8_t* aux,
                    kvmi_stream_t stream);

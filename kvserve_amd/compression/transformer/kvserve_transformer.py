@@ -13,7 +13,7 @@ from ... import ops
 from ..components import Transformer
 from .hadamard_func import HadamardTransform
 
-DEFAULT_SEED = 0x3333  # kvserve_transformer.py:253
+DEFAULT_SEED = 0x3333  # kvserve_transformer.py:22
 
 
 class KVServeTransformer(Transformer):

@@ -54,6 +54,61 @@ class _Carver:
         return out
 
 
+class _OutputBank:
+    """A payload / auxiliary tensor pair that an encode may leave its result in."""
+
+    def __init__(self, payload: torch.Tensor, aux: torch.Tensor, owner: Optional[int]):
+        self.payload, self.aux = payload, aux
+        self.owner = owner  # slot index of a slot's own arena pair; None for a lease
+
+    def spans(self) -> List[Tuple[int, int]]:
+        return [(t.data_ptr(), t.numel() * t.element_size()) for t in (self.payload, self.aux) if t.numel()]
+
+    def holds(self, device: torch.device, payload_bytes: int, aux_bytes: int) -> bool:
+        """Both tensors are contiguous uint8 on `device` with room for the chunk."""
+        return all(t.device == device and t.dtype == torch.uint8 and t.is_contiguous() and t.numel() >= need
+                   for t, need in ((self.payload, payload_bytes), (self.aux, aux_bytes)))
+
+    def take_from(self, slot: CompressionSlotBuffers, payload_bytes: int, aux_bytes: int) -> None:
+        """Copy a finished chunk out of `slot`'s arenas (enqueued on the current stream)."""
+        self.payload[:payload_bytes].copy_(slot.arena_a[:payload_bytes], non_blocking=True)
+        self.aux[:aux_bytes].copy_(slot.aux[:aux_bytes], non_blocking=True)
+
+
+class _BankTable:
+    """The runtime-owned output banks: every slot's own arena pair plus the leases.
+    Banks are found by the identity of both tensors, so a view, a slice or a copy of
+    a bank (which could alias a live arena) is never accepted."""
+
+    def __init__(self, slots: List[CompressionSlotBuffers]):
+        self._by_identity: Dict[Tuple[int, int], _OutputBank] = {}
+        self.leases: List[_OutputBank] = []
+        self.sealed = False
+        for index, slot in enumerate(slots):
+            self._enter(_OutputBank(slot.arena_a, slot.aux, index))
+
+    def _enter(self, bank: _OutputBank) -> None:
+        self._by_identity[(id(bank.payload), id(bank.aux))] = bank
+
+    def find(self, payload, aux) -> Optional[_OutputBank]:
+        bank = self._by_identity.get((id(payload), id(aux)))
+        return bank if bank is not None and bank.payload is payload and bank.aux is aux else None
+
+    def reserve(self, count: int, like: CompressionSlotBuffers) -> int:
+        """Allocate `count` leases shaped like `like`'s arenas; returns their bytes."""
+        self.sealed = True
+        for _ in range(count):
+            bank = _OutputBank(torch.empty_like(like.arena_a), torch.empty_like(like.aux), None)
+            self.leases.append(bank)
+            self._enter(bank)
+        return sum(size for bank in self.leases for _, size in bank.spans())
+
+    def release_leases(self) -> None:
+        for bank in self.leases:
+            self._by_identity.pop((id(bank.payload), id(bank.aux)), None)
+        self.leases.clear()
+
+
 class CompressionRuntime:
     def __init__(self, plan: CompressionMemoryPlan, kv_cache_layout: str, blocks_per_logical: int,
                  device: torch.device, *, codec_factory=None, external_execution: bool = False,
@@ -67,8 +122,6 @@ class CompressionRuntime:
         self.plan = plan
         self.config = plan.config
         self.layout = plan.layout
-        self.output_slots: List[Tuple[torch.Tensor, torch.Tensor]] = []
-        self._output_slots_allocated = False
         self._external_execution = external_execution
         self._metadata_initialized = False
         self.wire_profile: Optional[str] = None
@@ -94,6 +147,7 @@ class CompressionRuntime:
                 block_indices=taken["indices"].view(torch.int64).view(rows, physical),
                 completion_event=SlotEvent(), host_indices=None, raw_tail=taken["raw_tail"],
                 canonical=taken["canonical"] if taken["canonical"].numel() else None))
+        self._banks = _BankTable(self.slots)
         self.streams = [torch.cuda.Stream(device=device) for _ in self.slots]
         self.workspace_allocators: List[FixedWorkspaceAllocator] = []
         if self.config.uses_codec:
@@ -179,93 +233,98 @@ class CompressionRuntime:
                     sorted(self.layout.fa_group_indices))
 
     # ------------------------------------------------------------------ sizes
+    @property
+    def _quantized(self) -> bool:
+        return "quantizer" in self.config.pipeline
+
     def data_bytes(self, kv_part: int, tokens: Optional[Dict[int, int]] = None) -> int:
-        """manager.py:347-366."""
+        """Stored (decoded) bytes of one chunk of `kv_part` (manager.py:343-359):
+        `tokens` maps FA group -> valid tokens, None means a full chunk."""
+        layout = self.layout
         if self.config.uses_aggregate:
+            # the aggregate transport ships every layer's whole raw blocks
             if tokens is None:
-                return self.layout.raw_bytes_by_part[kv_part]
-            total = 0
-            for part in self.layout.parts(kv_part):
-                blocks = (tokens.get(part.group_index, 0) + part.block_size - 1) // part.block_size
-                total += blocks * part.num_heads * part.block_size * part.head_size * 2
-            return total
-        if tokens is not None and not self.layout.has_body(tokens):
+                return layout.raw_bytes_by_part[kv_part]
+            return sum(p.block_size * p.token_bytes * -(-tokens.get(p.group_index, 0) // p.block_size)
+                       for p in layout.parts(kv_part))
+        if not self._has_body(tokens):
             return 0
-        return (self.layout.u8_bytes_by_part if "quantizer" in self.config.pipeline
-                else self.layout.raw_bytes_by_part)[kv_part]
+        return (layout.u8_bytes_by_part if self._quantized else layout.raw_bytes_by_part)[kv_part]
 
     def aux_bytes(self, kv_part: int, tokens: Optional[Dict[int, int]] = None) -> int:
-        if tokens is not None and not self.layout.has_body(tokens):
-            return 0
-        return self.layout.aux_bytes_by_part[kv_part] if "quantizer" in self.config.pipeline else 0
+        """Quantization-table bytes of one chunk (manager.py:361-368)."""
+        return self.layout.aux_bytes_by_part[kv_part] if self._quantized and self._has_body(tokens) else 0
+
+    def _has_body(self, tokens: Optional[Dict[int, int]]) -> bool:
+        return tokens is None or self.layout.has_body(tokens)
+
+    # ------------------------------------------------------------------ output banks
+    @property
+    def output_slots(self) -> List[Tuple[torch.Tensor, torch.Tensor]]:
+        """The leased (payload, auxiliary) banks, in reservation order."""
+        return [(bank.payload, bank.aux) for bank in self._banks.leases]
 
     def registered_memory(self) -> Tuple[List[int], List[int]]:
+        """Device ranges a transport registers (manager.py:370-379): the bulk
+        allocation, then every non-empty lease tensor."""
         storage = self.bulk.untyped_storage()
-        pointers, sizes = [storage.data_ptr()], [storage.nbytes()]
-        for payload, auxiliary in self.output_slots:
-            for tensor in (payload, auxiliary):
-                size = tensor.numel() * tensor.element_size()
-                if size:
-                    pointers.append(tensor.data_ptr())
-                    sizes.append(size)
-        return pointers, sizes
+        spans = [(storage.data_ptr(), storage.nbytes())]
+        spans += [span for bank in self._banks.leases for span in bank.spans()]
+        return [ptr for ptr, _ in spans], [size for _, size in spans]
 
     def allocate_output_slots(self, count: int) -> None:
-        """Reserve encoded-output banks before binding (manager.py:383-396)."""
+        """Reserve `count` encoded-output leases, once and before binding
+        (manager.py:381-394); each is shaped like a slot's payload and aux arenas."""
         if type(count) is not int or not 0 <= count <= 16:
             raise ValueError("Encoded output slot count must be 0..16")
-        if self._output_slots_allocated or self._metadata_initialized:
+        if self._banks.sealed or self._metadata_initialized:
             raise RuntimeError("Encoded output banks must be reserved once before binding")
-        self.output_slots = [(torch.empty_like(self.slots[0].arena_a), torch.empty_like(self.slots[0].aux))
-                             for _ in range(count)]
-        extra = sum(t.numel() * t.element_size() for bank in self.output_slots for t in bank)
-        self.plan = replace(self.plan, reserved_bytes=self.plan.reserved_bytes + extra)
-        self._output_slots_allocated = True
+        added = self._banks.reserve(count, self.slots[0])
+        self.plan = replace(self.plan, reserved_bytes=self.plan.reserved_bytes + added)
 
-    def _validate_output_bank(self, slot_id, output, auxiliary) -> CompressionSlotBuffers:
+    def _check_slot_id(self, slot_id) -> CompressionSlotBuffers:
         if type(slot_id) is not int or not 0 <= slot_id < len(self.slots):
             raise ValueError("Invalid compression slot")
-        slot = self.slots[slot_id]
-        pairs = [(slot.arena_a, slot.aux), *self.output_slots]
-        if not any(output is payload and auxiliary is aux for payload, aux in pairs):
-            raise ValueError("Encoded output and auxiliary must be one Runtime-owned bank")
-        return slot
+        return self.slots[slot_id]
 
     def _require_execution(self, operation: str) -> None:
         if self.execution not in ("both", operation):
             raise RuntimeError(f"KVServe {self.execution}-only runtime cannot {operation}")
 
     def _check_slot(self, slot_id) -> None:
-        if type(slot_id) is not int or not 0 <= slot_id < len(self.slots):
-            raise ValueError("Invalid compression slot")
+        self._check_slot_id(slot_id)
         if not self._metadata_initialized:
             raise RuntimeError("bind_kv_caches must run before encode / decode")
 
     # ------------------------------------------------------------------ execution
     def encode_into(self, slot_id, logical_ids_by_group, kv_part, *, valid_tokens_by_group, output,
                     auxiliary) -> EncodedChunk:
-        """Encode, then copy payload and aux into a runtime-owned bank (manager.py:406-444)."""
+        """Encode one chunk and leave it in a runtime-owned bank (manager.py:396-444):
+        the slot's own arena pair, or a lease the result is copied into on the slot's
+        stream.  The codec's byte count is read on the host, so this waits for the
+        encode; the returned event closes the copy.  The caller must not reuse the
+        bank before that event."""
         self._require_execution("encode")
-        slot = self._validate_output_bank(slot_id, output, auxiliary)
-        stream = self.streams[slot_id]
+        slot = self._check_slot_id(slot_id)
+        bank = self._banks.find(output, auxiliary)
+        if bank is None or bank.owner not in (None, slot_id):
+            raise ValueError("Encoded output and auxiliary must be one Runtime-owned bank")
         aux_bytes = self.aux_bytes(kv_part, valid_tokens_by_group)
-        for tensor, capacity in ((output, slot.arena_a.numel()), (auxiliary, aux_bytes)):
-            if (tensor.device != slot.arena_a.device or tensor.dtype != torch.uint8 or not tensor.is_contiguous()
-                    or tensor.numel() < capacity):
-                raise ValueError("Invalid encoded output or auxiliary bank")
-        encoded = self.encode(slot_id, logical_ids_by_group, kv_part, valid_tokens_by_group=valid_tokens_by_group)
-        encoded.event.synchronize()
-        if encoded.raw_tail_bytes:
+        if not (bank.holds(slot.arena_a.device, slot.arena_a.numel(), aux_bytes)):
+            raise ValueError("Invalid encoded output or auxiliary bank")
+        chunk = self.encode(slot_id, logical_ids_by_group, kv_part, valid_tokens_by_group=valid_tokens_by_group)
+        chunk.event.synchronize()
+        if chunk.raw_tail_bytes:
             raise ValueError("Leased output requires a complete compressed token body")
-        size = encoded.codec_bytes
-        if not 0 < size <= output.numel():
+        size = chunk.codec_bytes
+        if size <= 0 or size > bank.payload.numel():
             raise ValueError("Encoded payload exceeds output bank")
+        stream = self.streams[slot_id]
         with torch.cuda.stream(stream):
-            if output is not slot.arena_a:
-                output[:size].copy_(slot.arena_a[:size], non_blocking=True)
-                auxiliary[:aux_bytes].copy_(slot.aux[:aux_bytes], non_blocking=True)
+            if bank.owner is None:
+                bank.take_from(slot, size, aux_bytes)
             slot.completion_event.record(stream)
-        return EncodedChunk(encoded.array, slot.completion_event, encoded.u8_bytes, payload_bytes=size)
+        return EncodedChunk(chunk.array, slot.completion_event, chunk.u8_bytes, payload_bytes=size)
 
     def encode(self, slot_id: int, logical_ids_by_group: List[List[int]], kv_part: KVPart, *,
                valid_tokens_by_group: Dict[int, int]) -> EncodedChunk:
@@ -276,23 +335,30 @@ class CompressionRuntime:
 
     def decode(self, slot_id: int, logical_ids_by_group: List[List[int]], kv_part: KVPart, codec_bytes: int,
                u8_bytes: int, *, valid_tokens_by_group: Dict[int, int]) -> torch.cuda.Event:
-        """Size checks of manager.py:462-488, then the slot's pipeline."""
+        """Reject a chunk whose sizes do not fit this runtime's layout and slot
+        (manager.py:462-488), then run the slot's pipeline."""
         self._require_execution("decode")
         self._check_slot(slot_id)
-        if u8_bytes != self.data_bytes(kv_part, valid_tokens_by_group):
-            raise ValueError("Compressed chunk has an incompatible decoded size")
-        if not 0 <= codec_bytes <= self.slots[slot_id].arena_a.numel():
-            raise ValueError("Compressed chunk exceeds receive buffer capacity")
-        if "codec" not in self.config.pipeline and codec_bytes != u8_bytes:
-            raise ValueError("Unencoded chunk payload size does not match its layout")
+        capacity = self.slots[slot_id].arena_a.numel()
+        rules = (
+            (u8_bytes == self.data_bytes(kv_part, valid_tokens_by_group),
+             "Compressed chunk has an incompatible decoded size"),
+            (0 <= codec_bytes <= capacity, "Compressed chunk exceeds receive buffer capacity"),
+            ("codec" in self.config.pipeline or codec_bytes == u8_bytes,
+             "Unencoded chunk payload size does not match its layout"),
+        )
+        for holds, message in rules:
+            if not holds:
+                raise ValueError(message)
         return self.pipelines[slot_id].decode(slot_id, logical_ids_by_group, kv_part, codec_bytes, u8_bytes,
                                               valid_tokens_by_group=valid_tokens_by_group)
 
     def shutdown(self) -> None:
+        """Drain every slot stream and drop the pipelines and leases."""
         for stream in self.streams:
             stream.synchronize()
         self.pipelines.clear()
-        self.output_slots.clear()
+        self._banks.release_leases()
 
 
 def create_runtime(plan: CompressionMemoryPlan, cache_layout: str, blocks_per_logical: int, device, *,

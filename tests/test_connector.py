@@ -14,7 +14,8 @@ import torch
 import kvserve_amd.connector.compressed_kv_connector as connector_module
 from kvserve_amd.connector import (CompressedKVConnector, CompressedKVConnectorMetadata, KVConnectorRole,
                                    LoopbackTransport, ReqMeta, make_slot_mapping)
-from kvserve_amd.connector.transport import CreditLoopbackTransport, payload_nbytes
+from kvserve_amd.connector.transport import payload_nbytes
+from tests._credit_transport import CreditLoopbackTransport
 
 PROFILE = {"pipeline": ["transformer", "quantizer", "codec"],
            "transformer_config": {"transform_type": "hadamard", "seed": 3237919422},

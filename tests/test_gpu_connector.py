@@ -30,7 +30,7 @@ def profile(min_size=0, hybrid=0.3):
             "codec_config": {"codec_type": "bitpack", "bitpack_bits": 4}, "min_compress_size": min_size}
 
 
-CREDIT = "kvserve_amd.connector.transport:CreditLoopbackTransport"  # msgpack metadata, staging copies, credit
+CREDIT = "tests._credit_transport:CreditLoopbackTransport"  # msgpack metadata, staging copies, credit
 
 
 def vllm_config(producer, port, compression, heads=8, head=128, tp=(0, 1), transport="loopback"):
