@@ -11,10 +11,12 @@ Llama-3.1-8B mask at hybrid 0.3, 16/16 levels, bitpack 4 bits, 4 streams of 8 la
 
 value = raw bf16 KV bytes of the request / (compress + decompress time), GB/s.
 Inputs are resident in HBM before the timed region; plans (device descriptors) are
-built before it too.  Before the W warmup steps the bench runs untimed steps back to back
-for --settle-ms (default 150 ms; reported as settle_steps), so the timed steps see the
-device's sustained-load clocks.  Per-direction throughput and the fraction of HBM peak are
-printed alongside.  Prints ONE JSON line.
+built before it too.  After the W warmup steps the K steps are timed once ("unsettled"),
+then untimed steps run back to back for --settle-ms (default 150 ms; reported as
+settle_steps) and the K steps are timed again: that second timing is the headline, the
+sustained-load rate (from idle the step time falls over the first ~40 ms of load,
+--settle-curve).  Per-direction throughput and the fraction of HBM peak are printed
+alongside.  Prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5]
                     [--workload config2|config3|config4|config5|config2_ans|connector]
@@ -952,12 +954,73 @@ def runtime_cpu_baseline(plan, caches, source, budget_s: float):
     }
 
 
+def timed_steps(launches, nc: int, steps: int, stream):
+    """Time `steps` steps with a HIP event after every launch (on the launch stream).
+    Returns (compress ms, decompress ms, per-launch ms, wall seconds); the first `nc`
+    launches are the compress direction."""
+    import torch
+
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        ev[k][0].record(stream)
+        for i, (plan, name) in enumerate(launches):
+            plan.launch(name)
+            ev[k][i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_i = [sum(ev[k][i].elapsed_time(ev[k][i + 1]) for k in range(steps)) / steps for i in range(len(launches))]
+    return sum(per_i[:nc]), sum(per_i[nc:]), per_i, wall
+
+
+def _sysfs_clocks() -> dict:
+    """Current shader / memory clock levels from the amdgpu sysfs tables, where readable."""
+    out = {}
+    for card in sorted(Path("/sys/class/drm").glob("card*/device")):
+        for key in ("pp_dpm_sclk", "pp_dpm_mclk", "pp_dpm_fclk"):
+            try:
+                rows = (card / key).read_text().splitlines()
+            except OSError:
+                continue
+            cur = [r.split(":", 1)[1].strip().rstrip("*").strip() for r in rows if r.rstrip().endswith("*")]
+            if cur:
+                out[key[7:]] = cur[0]
+        if out:
+            break
+    return out
+
+
+def settle_curve(step, launches, nc: int, args) -> dict:
+    """Step time against time under load from an idle device: after a 0.5 s pause, run
+    windows of 8 steps back to back for about 300 ms and report each window's mean
+    compress / decompress time (HIP events) and its start time since the load began,
+    with the amdgpu sysfs clock levels read after the window where the box exposes them."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    time.sleep(0.5)
+    rows, t_start = [], time.perf_counter()
+    while time.perf_counter() - t_start < 0.3:
+        t_w = (time.perf_counter() - t_start) * 1e3
+        t_c, t_d, _, _ = timed_steps(launches, nc, 8, stream)
+        rows.append({"t_ms": round(t_w, 2), "compress_ms": round(t_c, 4), "decompress_ms": round(t_d, 4),
+                     **_sysfs_clocks()})
+    return {"settle_curve": rows, "window_steps": 8, "workload": args.workload}
+
+
 def settle_device(step, settle_ms: float) -> int:
     """Run untimed steps back to back for `settle_ms` of wall time before the warmup and
-    return how many ran.  Under sustained load the device's step time falls for the first
-    ~50 ms (clock and power management settling; on config 2 decode goes from ~0.29 to
-    ~0.27 ms), so a few warmup steps alone would time that transient, not the sustained
-    rate a serving loop sees.  The timed steps are unchanged."""
+    return how many ran.  From an idle device the step time falls over the first ~40 ms
+    of load and is flat afterwards (config 2: compress 0.49 -> 0.41 ms, decompress 0.30
+    -> 0.28 ms) while the shader clock keeps falling (2.36 -> 2.07 GHz over 300 ms) and
+    the memory clock stays at 2.0 GHz: a memory / fabric-side transient, which a few
+    warmup steps alone would time instead of the sustained rate a serving loop sees
+    (bench.py --settle-curve prints the curve).  The same timed steps are also run
+    before this phase and reported as "unsettled"."""
     import torch
 
     n = 0
@@ -990,6 +1053,8 @@ def main() -> int:
     ap.add_argument("--rt-layers", type=int, default=28, help="(runtime) layers")
     ap.add_argument("--compress-path", default=None, choices=["two_pass", "one_pass"],
                     help="compress kernels: two_pass (default) or one_pass (kvmi_compress_paged, K read once)")
+    ap.add_argument("--settle-curve", action="store_true",
+                    help="only print the per-window step times over the first ~300 ms of load after idle")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy --steps times (scales rocprof byte counters)")
     args = ap.parse_args()
@@ -1039,43 +1104,36 @@ def main() -> int:
         cplan = codec.plan_compress_batch([(r.pools, r.block_ids, r.profiles, r.layer_ids) for r in reqs])
         packets = cplan.packets
         dplan = codec.plan_decompress_batch([(pk, r.pools, r.block_ids) for pk, r in zip(packets, reqs)])
+    # first run of each plan: a device block table is checked by it (kvmi_check_block_ids
+    # runs on a plan's first run only), so the timed steps enqueue the kernels alone
+    cplan.run()
+    dplan.run()
     torch.cuda.synchronize()
+    cplan.check_errors()
 
     stream = torch.cuda.current_stream()
     launches = [(cplan, n) for n in cplan.launches()] + [(dplan, n) for n in dplan.launches()]
-    settle = settle_device(lambda: [plan.launch(name) for plan, name in launches], args.settle_ms)
+    nc = len(cplan.launches())
+    step = lambda: [plan.launch(name) for plan, name in launches]
+    if args.settle_curve:
+        print(json.dumps(settle_curve(step, launches, nc, args)), flush=True)
+        return 0
     print(f"bench: warmup {args.warmup} steps", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
-        for plan, name in launches:
-            plan.launch(name)
+        step()
+    torch.cuda.synchronize()
+    # the same timing before the settle phase (clocks still ramping under the new load)
+    t_c_cold, t_d_cold, _, _ = timed_steps(launches, nc, args.steps, stream)
+    settle = settle_device(step, args.settle_ms)
     torch.cuda.synchronize()
 
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)] for _ in range(args.steps)]
     print(f"bench: timing {args.steps} steps", file=sys.stderr, flush=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        ev[k][0].record(stream)
-        for i, (plan, name) in enumerate(launches):
-            plan.launch(name)
-            ev[k][i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    t_c, t_d, per_i, wall = timed_steps(launches, nc, args.steps, stream)
     cplan.check_errors()
     dplan.check_errors()
-
-    # per entry point and direction (both plans may name kvmi_check_block_ids, which
-    # runs on a plan's first run only and is timed as ~0 after the warm-up)
-    per_i = [0.0] * len(launches)
-    for k in range(args.steps):
-        for i in range(len(launches)):
-            per_i[i] += ev[k][i].elapsed_time(ev[k][i + 1]) / args.steps
-    nc = len(launches) - sum(1 for plan, _ in launches if plan is dplan)
-    t_c, t_d = sum(per_i[:nc]), sum(per_i[nc:])
     per = {}
     for i, (_, name) in enumerate(launches):
-        if name != "kvmi_check_block_ids":
-            per[name] = per.get(name, 0.0) + per_i[i]
+        per[name] = per.get(name, 0.0) + per_i[i]
 
     R = sum(len(r.pools) * 2 * r.block_ids.numel() * S * H * D * 2 for r in reqs)
     P = sum(pk.compressed_bytes() for pk in packets)
@@ -1114,6 +1172,10 @@ def main() -> int:
         "decompress_gbps": round(dec_gbps, 2),
         "compress_hbm_frac": round(comp_frac, 4),
         "decompress_hbm_frac": round(dec_frac, 4),
+        # the same steps timed right after the warmup, before the settle phase
+        "unsettled": {"compress_hbm_frac": round(alg / t_c_cold / 1e6 / HBM_PEAK_GBPS, 4),
+                      "decompress_hbm_frac": round(alg / t_d_cold / 1e6 / HBM_PEAK_GBPS, 4),
+                      "compress_ms": round(t_c_cold, 4), "decompress_ms": round(t_d_cold, 4)},
         # the same times over the bytes the kernels actually move (rocprofv3 FETCH_SIZE /
         # WRITE_SIZE per dispatch, copy-calibrated): compress reads K twice
         "compress_traffic_hbm_frac": traffic_frac(compress_kernels(names, cplan), t_c / 1e3, args.workload),

@@ -67,6 +67,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_EINVAL (-22)
 #define KVMI_ELAUNCH (-5)
 #define KVMI_ENOSPC (-28) /* the call needs more than a fixed scratch array holds */
+#define KVMI_ERANGE (-34) /* kvmi_compress_paged: the epoch reached 2^31; re-zero the workspace, reset it to 0 */
 
 /* Stream format constants (bitpack_codec.py:20-21). */
 #define KVMI_HEADER_BYTES 16
@@ -251,7 +252,10 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  *   is cleared between calls).  NULL selects the two-pass kernels.
  * epoch: host pointer to the workspace's call counter, 0 before the first call; it
  *   is incremented when (and only when) the one-pass kernel is enqueued.  Calls
- *   sharing a workspace must be ordered on one stream.
+ *   sharing a workspace must be ordered on one stream.  Once it reaches 2^31 the call
+ *   returns KVMI_ERANGE: zero the workspace again and set *epoch to 0 first.  The
+ *   epoch is a kernel argument, so a captured graph would replay one epoch: do not
+ *   capture this call (capture kvmi_kstats_paged + kvmi_encode_paged instead).
  * A barrier that does not complete within about 0.3 s sets KVMI_ERR_SYNC (the
  * kernel still ends; later barriers of the launch then no longer wait).
  */

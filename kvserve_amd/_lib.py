@@ -21,7 +21,7 @@ ERR_BAD_HEADER = 2
 ERR_CORRUPT = 4
 ERR_SYNC = 8
 ERR_BLOCK_ID = 16
-OK, EINVAL, ELAUNCH, ENOSPC = 0, -22, -5, -28
+OK, EINVAL, ELAUNCH, ENOSPC, ERANGE = 0, -22, -5, -28, -34
 # Bytes of the fixed device array behind kvmi_v3_compress_noalloc (per GPU).
 V3_NOALLOC_SCRATCH_BYTES = 4 * 1024 * 1024
 
@@ -196,4 +196,6 @@ def check(rc: int, what: str) -> None:
         raise ValueError(f"{what}: invalid arguments (KVMI_EINVAL)")
     if rc == ENOSPC:
         raise ValueError(f"{what}: the call needs more scratch than the fixed device array holds (KVMI_ENOSPC)")
+    if rc == ERANGE:
+        raise ValueError(f"{what}: the workspace epoch reached 2^31; zero the workspace and reset the epoch (KVMI_ERANGE)")
     raise KvmiError(f"{what}: failed with code {rc}")

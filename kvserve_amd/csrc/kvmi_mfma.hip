@@ -21,6 +21,8 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
 
   __shared__ Tables T;
   __shared__ uint32_t lkey[2 * kMH * 128];
+  // per-wave buffer that turns a coalesced tile into the lanes' half-rows
+  __shared__ uint4 tbuf[kWaves * tile_buf_q<NC>()];
   fill_signs(T, job.signs, H, D);
   for (int i = threadIdx.x; i < H * D; i += kMW) {
     lkey[i] = 0xffffffffu;
@@ -43,14 +45,16 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
       mx[a][c] = -__builtin_inff();
     }
   const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
+  uint4* wbuf = tbuf + wave * tile_buf_q<NC>();
   auto accumulate = [&](uint4 (&x)[2 * NC]) {
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(x[u]);
+    tile_to_half_rows<NC>(wbuf, x);
     sign_half_row<NC>(T, hme, hl, x);
     kstats_tile<NC>(x, hp, hn, mn, mx);
   };
   auto fetch = [&](int t, uint4 (&x)[2 * NC]) {
-    load_half_row<NC>(pool, tile_row0(job, S, H, tile_tok(run.tok0, H, t)) + r, hl, x);
+    load_tile<NC>(pool, tile_row0(job, S, H, tile_tok(run.tok0, H, t)), x);
   };
   // Two buffers: the loads of tile t + 4 are in flight while tile t is reduced.  The
   // prefetch is unconditional (past the end it re-reads the current tile, a cache
@@ -100,8 +104,9 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   constexpr int TQ = kTok * RB / 16;          // uint4 per tile
   __shared__ uint4 ostage[kWaves * TQ];
   // per-wave parking of a V tile's rounded outputs between its statistics and its
-  // quantization (2*NC uint4 per lane)
-  __shared__ uint4 ypark[kWaves * 2 * NC * 64];
+  // quantization (2*NC uint4 per lane); the same space rearranges each loaded tile
+  static_assert(tile_buf_q<NC>() >= 2 * NC * 64, "a tile buffer holds a wave's parked V tile");
+  __shared__ uint4 ypark[kWaves * tile_buf_q<NC>()];
   const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
   stage_profile(T, job.profile, H);
   fill_signs(T, job.signs, H, D);
@@ -145,17 +150,21 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
       }
     }
   };
+  // The wave's parking buffer also turns each coalesced tile into the lanes' half-rows
+  // (the V tile is rearranged before its rounded outputs are parked there).
+  uint4* wbuf = ypark + wave * tile_buf_q<NC>();
   uint4 xk[2 * NC], xv[2 * NC];
-  if (wave < run.tiles) load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, wave)) + r, hl, xk);
+  if (wave < run.tiles) load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, wave)), xk);
   for (int t = wave; t < run.tiles; t += kWaves) {
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(xk[u]);
     const int ta = tile_tok(run.tok0, H, t);
-    const int64_t row = tile_row0(job, S, H, ta) + r;
+    const int64_t row0 = tile_row0(job, S, H, ta);
     const int tok = ta + r / H;
-    load_half_row<NC>(poolV, row, hl, xv);
+    load_tile<NC>(poolV, row0, xv);
     // ---------------- K: per-channel statistics from the kstats pass
     {
+      tile_to_half_rows<NC>(wbuf, xk);
       sign_half_row<NC>(T, hme, hl, xk);
       LanePack<HALF, BITS> pkd;
       quant_k_tile<NC, BITS, CLAMP>(xk, hp, hn, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), s, lp.lvk, pkd,
@@ -165,12 +174,12 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
     }
     // next tile's K (unconditional: past the end it re-reads this tile, a cache hit)
     const int tn = min(t + kWaves, run.tiles - 1);
-    load_half_row<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)) + r, hl, xk);
+    load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)), xk);
     // ---------------- V: per-token statistics over the heads of a group
+    tile_to_half_rows<NC>(wbuf, xv);
     sign_half_row<NC>(T, hme, hl, xv);
     LanePack<HALF, BITS> pkd;
-    quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, ypark + wave * (2 * NC * 64) + l, pkd,
-                                      over);
+    quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, wbuf + l, pkd, over);
     pkd.store_lds(ost + offv);
     flush(1, ta);
   }

@@ -385,6 +385,40 @@ __device__ __forceinline__ void load_half_row(const uint16_t* __restrict__ pool,
 #pragma unroll
   for (int u = 0; u < 2 * NC; ++u) x[u] = gld(src + u);
 }
+// Coalesced load of the 32 rows of a tile (contiguous in the pool, from row `row0`):
+// instruction v reads 1 KiB, lane l the 16-byte piece 64 v + l of the tile.  Random
+// 32 KiB blocks read this way stream at ~5.8 TB/s on MI355X, against ~4.2 TB/s when
+// each lane reads its own half-row (every instruction then touches 64 cache lines).
+template <int NC>
+__device__ __forceinline__ void load_tile(const uint16_t* __restrict__ pool, int64_t row0, uint4 (&x)[2 * NC]) {
+  const uint4* src = reinterpret_cast<const uint4*>(pool + row0 * (32 * NC)) + (threadIdx.x & 63);
+#pragma unroll
+  for (int v = 0; v < 2 * NC; ++v) x[v] = gld(src + 64 * v);
+}
+
+// uint4 of a wave's buffer for tile_to_half_rows: 32 rows at a pitch of 4NC + 1 pieces.
+template <int NC>
+constexpr int tile_buf_q() { return kTok * (4 * NC + 1); }
+
+// Rearrange a tile loaded by load_tile into the MFMA layout (lane (r, hl): half-row hl
+// of row r, as load_half_row) through the wave's LDS buffer `buf` (tile_buf_q<NC>()
+// uint4).  Rows sit at a pitch of 4NC + 1 pieces, so the lanes that write one row and
+// the lanes that read one piece of consecutive rows fall on distinct banks, and every
+// access is a per-lane base plus a compile-time offset.  LDS executes a wave's
+// operations in order, so no barrier is needed; the buffer belongs to this wave.
+template <int NC>
+__device__ __forceinline__ void tile_to_half_rows(uint4* buf, uint4 (&x)[2 * NC]) {
+  constexpr int PR = 4 * NC, PP = PR + 1;  // pieces per row, pitch
+  const int l = threadIdx.x & 63, r = l & 31, hl = l >> 5;
+  // piece 64 v + l of the tile: row (64 v + l) / PR = (64 / PR) v + l / PR, piece l % PR
+  uint4* wr = buf + (l / PR) * PP + l % PR;
+#pragma unroll
+  for (int v = 0; v < 2 * NC; ++v) wr[(64 / PR) * PP * v] = x[v];
+  const uint4* rd = buf + r * PP + 2 * NC * hl;
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) x[u] = rd[u];
+}
+
 // The same from a sign-mask table laid out like Tables::smask.
 template <int NC>
 __device__ __forceinline__ void sign_half_row(const uint32_t (*smask)[64 + 4], int h, int hl, uint4 (&x)[2 * NC]) {

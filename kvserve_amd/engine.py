@@ -281,7 +281,9 @@ class FusedKVCodec:
         if isinstance(block_ids, torch.Tensor) and block_ids.is_cuda:
             if block_ids.dim() != 1:
                 raise ValueError("block_ids must be 1-D")
-            ids = block_ids.to(device=device, dtype=torch.int32).contiguous()
+            # the plan's own copy: the first run checks it once, and a caller that
+            # rewrites its table in place later cannot slip unchecked ids under the plan
+            ids = block_ids.to(device=device, dtype=torch.int32, copy=True).contiguous()
             if host_check and ids.numel():
                 lo, hi = int(ids.min().item()), int(ids.max().item())
                 if lo < 0 or hi >= pool_blocks:
@@ -590,6 +592,11 @@ class Plan:
                     self._ids_checked = True
                 return
             if name == "kvmi_compress_paged":
+                if torch.cuda.is_current_stream_capturing():
+                    # the barrier epoch is a kernel argument the host advances per launch;
+                    # a replayed graph would reuse it and meet the previous replay's arrivals
+                    raise RuntimeError("the one-pass compress (compress_path='one_pass') cannot be captured "
+                                       "into a graph; capture a two_pass plan")
                 if self.epoch.value >= 1 << 31:  # epoch tags are 32-bit: start the workspace afresh
                     self.workspace.zero_()
                     self.epoch.value = 0
