@@ -110,7 +110,12 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> di
     not MFMA-eligible)."""
     default_axes = tuple(getattr(codec, "axes", ("channel", "token"))) == ("channel", "token")
     pow2 = D in (64, 128) and default_axes
-    mfma = pow2 and codec.fwht == "mfma" and codec.transform and 8 % H == 0 and (S * H) % 32 == 0
+    wide = H in (16, 32) and S & (S - 1) == 0 and ((32 // H) * D * bits // 8) % 16 == 0  # wide-head MFMA
+    mfma = pow2 and codec.fwht == "mfma" and codec.transform and (8 % H == 0 or wide) and (S * H) % 32 == 0
+    if mfma and wide:
+        return {"kvmi_encode_paged": f"encode_mfma_wide_kernel<{D // 32}, {bits}, false>",
+                "kvmi_decode_paged": f"decode_mfma_wide_kernel<{D // 32}, {bits}, 8>",
+                "kvmi_kstats_paged": f"kstats_wide_kernel<{D // 32}>", "finalize": "kstats_finalize_kernel"}
     if mfma:
         names = {"kvmi_encode_paged": f"encode_mfma_kernel<{D // 32}, {bits}, false>",
                  "kvmi_decode_paged": ("decode_kt_kernel<8>" if (D, bits) == (128, 4)
@@ -1046,6 +1051,10 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU-oracle work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=32, help="(debug) layers of the config-2 request")
+    ap.add_argument("--heads", type=int, default=8,
+                    help="KV heads of the config-2 request (other than 8: a wide-head variant, not the metric's config)")
+    ap.add_argument("--head-dim", type=int, default=128,
+                    help="head_dim of the config-2 request (other than 128: a variant, not the metric's config)")
     ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS),
                     help="BASELINE.json configuration to time (the metric is quoted on config2)")
     ap.add_argument("--rt-block-size", type=int, default=1, help="(runtime) tokens per block; 1 = token view")
@@ -1088,7 +1097,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     print(f"bench: building {args.workload} workload", file=sys.stderr, flush=True)
     if args.workload == "config2":
-        wl = workloads.make_config2(device=dev, num_layers=args.layers)
+        wl = workloads.make_config2(device=dev, num_layers=args.layers, num_heads=args.heads, head_dim=args.head_dim)
     else:
         wl = getattr(workloads, "make_" + args.workload)(device=dev)
     reqs = wl.requests
@@ -1163,7 +1172,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
         "config": {
-            "workload": WORKLOADS[args.workload],
+            "workload": WORKLOADS[args.workload] + (f" [variant: {H} KV heads, head_dim {D}]"
+                                                    if args.workload == "config2" and (H, D) != (8, 128) else ""),
             "requests": len(reqs), "layers": len(reqs[0].pools),
             "tokens": sum(r.block_ids.numel() for r in reqs) * S, "raw_bytes": R, "packed_bytes": P,
             "meta_bytes": M,

@@ -133,9 +133,9 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
 }
 
 // Kernel families, by geometry:
-//  * MFMA (kvmi_mfma.hip): the transform profile with D in {64, 128}, H dividing 8 and
-//    S*H a multiple of 32, unless the caller forces the register FWHT
-//    (KVMI_F_VALU_FWHT);
+//  * MFMA (kvmi_mfma.hip): the transform profile with D in {64, 128}, H dividing 8
+//    (or H = 16 or 32 with a power-of-two S, and 16-byte stream runs) and S*H a
+//    multiple of 32, unless the caller forces the register FWHT (KVMI_F_VALU_FWHT);
 //  * quad-per-row register FWHT (kvmi_codec.hip): D in {64, 128}, H dividing 128,
 //    H <= 16;
 //  * generic rows (kvmi_rows.hip): every other geometry check_geo admits (D a
@@ -143,8 +143,13 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
 //    H up to 64), every non-default quantization axis, and any geometry when the
 //    caller forces them (KVMI_F_ROW_FWHT).
 inline bool mfma_eligible(const Geo& g) {
+  // The encoder writes each stream run (32/H tokens of one head) in 16-byte pieces, so
+  // a run's packed bytes (32/H) * D * bits / 8 must be a multiple of 16: at 32 heads
+  // that excludes D = 64 at odd widths (24-byte runs at 3 bits).
+  const bool runs16 = ((32 / g.H) * g.D * g.bits / 8) % 16 == 0;
+  const bool heads = (8 % g.H) == 0 || ((g.H == 16 || g.H == 32) && (g.S & (g.S - 1)) == 0 && runs16);
   return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_ROW_FWHT | KVMI_F_NO_TRANSFORM | kAxisFlags)) &&
-         (g.D == 64 || g.D == 128) && (8 % g.H) == 0 && ((g.S * g.H) % 32) == 0;
+         (g.D == 64 || g.D == 128) && heads && ((g.S * g.H) % 32) == 0;
 }
 inline bool quad_eligible(const Geo& g) {
   return !(g.flags & (KVMI_F_ROW_FWHT | kAxisFlags)) && (g.D == 64 || g.D == 128) && g.H <= kMaxQuadH &&

@@ -627,7 +627,7 @@ extern "C" int kvmi_compress_paged(const kvmi_geometry* geom, const kvmi_layer_j
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (mfma_eligible(g) && !(g.flags & KVMI_F_TWO_PASS) && workspace) {
+  if (mfma_eligible(g) && g.H <= kMH && !(g.flags & KVMI_F_TWO_PASS) && workspace) {
     if (!epoch || ((uintptr_t)workspace & 255)) return KVMI_EINVAL;
     // tags are 32-bit: past 2^31 calls a tag could come back while keys or flags of an
     // earlier call still hold it, so the caller must start the workspace afresh

@@ -78,10 +78,118 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
   }
 }
 
-// ============================================================== encode (orientation T)
-template <int NC, int BITS, bool CLAMP>
-__global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+// ============================================================== K statistics, 16 or 32 heads
+// With 16 or 32 heads a token-major tile holds 16 heads per lane's registers in
+// orientation N, too many running min / max to keep.  Here a tile is 32 consecutive
+// tokens of ONE head instead (rows 2*H*D bytes apart in the pool, each row read by
+// PR = 4NC lanes in 16-byte pieces; a run's last tile repeats its last token, which
+// min / max ignore), so every output register of a lane is the same (head, channel):
+// one running pair per chunk.  Wave w owns heads w, w + 4, ... of the workgroup's run
+// and writes their keys into the workgroup's LDS keys without atomics.
+struct SignTable {
+  uint32_t smask[kWideH][64 + 4];
+};
+template <int NC>
+__global__ __launch_bounds__(kMW) void kstats_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
                                                           int32_t* __restrict__ err) {
+  constexpr int D = 32 * NC, HALF = 16 * NC, PR = 4 * NC;
+  const kvmi_layer_job job = jobs[blockIdx.y];
+  const int S = g.S, H = g.H, HD = H * D;
+  const Run run = wg_run(job, g);
+  if ((int)blockIdx.x >= run.nwg) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
+
+  __shared__ SignTable T;
+  __shared__ uint32_t lkey[2 * kWideH * 128];
+  __shared__ uint4 tbuf[kWaves * tile_buf_q<NC>()];
+  fill_signs(T, job.signs, H, D);
+  for (int i = threadIdx.x; i < HD; i += kMW) {
+    lkey[i] = 0xffffffffu;
+    lkey[HD + i] = 0u;
+  }
+  __syncthreads();
+
+  uint4 hp[2], hn[2];
+  hp[0] = hadamard_tile(0, true, false);
+  hp[1] = hadamard_tile(1, true, false);
+  hn[0] = hadamard_tile(0, true, true);
+  hn[1] = hadamard_tile(1, true, true);
+  const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
+  const int sh = __builtin_ctz((unsigned)S);  // S is a power of two (mfma_eligible)
+  const int last_tok = run.tok_end - 1;
+  const int nk = (run.tok_end - run.tok0 + kTok - 1) / kTok;  // tiles per head
+  const int nhw = (H - wave + kWaves - 1) / kWaves;           // heads of this wave
+  const int ntw = nhw * nk;
+  uint4* wbuf = tbuf + wave * tile_buf_q<NC>();
+  // tile n of this wave: head wave + 4 (n / nk), tokens tok0 + 32 (n % nk) + (0..31);
+  // instruction v of a lane reads piece l % PR of row (64 / PR) v + l / PR
+  auto fetch = [&](int n, uint4 (&x)[2 * NC]) {
+    const int h = wave + kWaves * (n / nk), t0 = run.tok0 + kTok * (n % nk);
+#pragma unroll
+    for (int v = 0; v < 2 * NC; ++v) {
+      const int t = min(t0 + (64 / PR) * v + l / PR, last_tok);
+      const int64_t row = ((int64_t)gld(job.block_ids + (t >> sh)) * S + (t & (S - 1))) * H + h;
+      x[v] = gld(reinterpret_cast<const uint4*>(pool + row * D) + l % PR);
+    }
+  };
+  float mn[4][NC], mx[4][NC];
+  auto reset = [&]() {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        mn[a][c] = __builtin_inff();
+        mx[a][c] = -__builtin_inff();
+      }
+  };
+  auto accumulate = [&](int n, uint4 (&x)[2 * NC]) {
+#pragma unroll
+    for (int u = 0; u < 2 * NC; ++u) pin(x[u]);
+    const int h = wave + kWaves * (n / nk);
+    tile_to_half_rows<NC>(wbuf, x);
+    sign_half_row<NC>(T, h, hl, x);
+    kstats_tile<NC>(x, hp, hn, mn, mx);
+    if (n % nk == nk - 1) {
+      // the head's last tile: its keys (channel HALF (r >> 4) + 16 c + (r & 15) of
+      // chunk c; lanes r and r + 32 hold other rows of the same channel)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float a = fminf(fminf(mn[0][c], mn[1][c]), fminf(mn[2][c], mn[3][c]));
+        float b = fmaxf(fmaxf(mx[0][c], mx[1][c]), fmaxf(mx[2][c], mx[3][c]));
+        a = halves_min(a);
+        b = halves_max(b);
+        if (hl == 0) {
+          const int f = HALF * (r >> 4) + 16 * c + (r & 15);
+          lkey[h * D + f] = f2key(a * g.scale);
+          lkey[HD + h * D + f] = f2key(b * g.scale);
+        }
+      }
+      reset();
+    }
+  };
+  reset();
+  uint4 xa[2 * NC], xb[2 * NC];
+  if (ntw > 0) fetch(0, xa);
+  for (int n = 0; n < ntw; n += 2) {
+    fetch(min(n + 1, ntw - 1), xb);
+    accumulate(n, xa);
+    if (n + 1 >= ntw) break;
+    fetch(min(n + 2, ntw - 1), xa);
+    accumulate(n + 1, xb);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < HD; i += kMW) {
+    if (lkey[i] != 0xffffffffu) atomicMin(&job.kstats[i], lkey[i]);
+    if (lkey[HD + i] != 0u) atomicMax(&job.kstats[HD + i], lkey[HD + i]);
+  }
+}
+
+// ============================================================== encode (orientation T)
+// HM: head capacity of the tables (kMH, or kWideH for 16 and 32 heads).
+template <int NC, int BITS, bool CLAMP, int HM>
+__device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs,
+                                            int32_t* __restrict__ err) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int S = g.S, H = g.H, G = g.G, HD = H * D;
@@ -96,16 +204,17 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
 
-  __shared__ Tables T;
-  // Per-wave staging of a section's packed symbols as the byte image of the stream
-  // runs the tile covers: H runs of 32/H tokens (permuted order) or one run of 32
-  // rows (native order).  The runs are then written lane-linear, 16 bytes a lane.
+  __shared__ TablesT<HM> T;
+  // Per-wave LDS buffer with three uses in turn: it rearranges each loaded tile into the
+  // lanes' half-rows, parks a V tile's rounded outputs between its statistics and its
+  // quantization (2*NC uint4 per lane), and stages a section's packed symbols as the
+  // byte image of the stream runs the tile covers -- H runs of 32/H tokens (permuted
+  // order) or one run of 32 rows (native order) -- which are then written lane-linear,
+  // 16 bytes a lane.  A wave's LDS operations execute in order, so the uses follow one
+  // another without waits.
   constexpr int RB = D * BITS / 8;            // bytes of one packed row
   constexpr int TQ = kTok * RB / 16;          // uint4 per tile
-  __shared__ uint4 ostage[kWaves * TQ];
-  // per-wave parking of a V tile's rounded outputs between its statistics and its
-  // quantization (2*NC uint4 per lane); the same space rearranges each loaded tile
-  static_assert(tile_buf_q<NC>() >= 2 * NC * 64, "a tile buffer holds a wave's parked V tile");
+  static_assert(tile_buf_q<NC>() >= 2 * NC * 64 && tile_buf_q<NC>() >= TQ, "a wave buffer holds each use");
   __shared__ uint4 ypark[kWaves * tile_buf_q<NC>()];
   const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
   stage_profile(T, job.profile, H);
@@ -131,7 +240,8 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   const LaneProfile lp = lane_profile(T, hme, hl);
   const float s = g.scale;
 
-  uint8_t* ost = reinterpret_cast<uint8_t*>(ostage + wave * TQ);
+  uint4* ostage = ypark + wave * tile_buf_q<NC>();
+  uint8_t* ost = reinterpret_cast<uint8_t*>(ostage);
   const int tpt = kTok / H;  // tokens per tile
   // byte offset of this lane's half-row in the staged image, by output position
   auto stage_off = [&](int j) { return native ? (r / H) * (H * RB) + j * RB + hl * (RB / 2)
@@ -146,7 +256,7 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
       if (TQ % 64 == 0 || q < TQ) {
         const int run_j = q / rq;
         uint8_t* dst = seg_addr<BITS>(job, g, part, native ? 0 : run_j, ta, 0) + 16 * (q - run_j * rq);
-        gst(reinterpret_cast<uint4*>(dst), ostage[wave * TQ + q]);
+        gst(reinterpret_cast<uint4*>(dst), ostage[q]);
       }
     }
   };
@@ -186,11 +296,23 @@ __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_laye
   if (over & overflow_mask<BITS>()) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
 }
 
+template <int NC, int BITS, bool CLAMP>
+__global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                          int32_t* __restrict__ err) {
+  encode_body<NC, BITS, CLAMP, kMH>(g, jobs, err);
+}
+// 16 or 32 KV heads: a tile holds 2 tokens or 1 (32 rows), with tables for 32 heads.
+template <int NC, int BITS, bool CLAMP>
+__global__ __launch_bounds__(kMW) void encode_mfma_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                               int32_t* __restrict__ err) {
+  encode_body<NC, BITS, CLAMP, kWideH>(g, jobs, err);
+}
+
 // ============================================================== decode (orientation T)
 // NW waves per workgroup share one set of tables (and one header check).
-template <int NC, int BITS, int NW>
-__global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
-                                                              int32_t* __restrict__ err) {
+template <int NC, int BITS, int NW, int HM>
+__device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs,
+                                            int32_t* __restrict__ err) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int S = g.S, H = g.H, G = g.G;
@@ -200,7 +322,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
 
-  __shared__ Tables T;
+  __shared__ TablesT<HM> T;
   __shared__ int ok;
   // Per-wave staging of an output tile (32 rows, row pitch RP uint4 with one of
   // padding): rows are written as the MFMA leaves them and stored lane-linear, so
@@ -208,6 +330,11 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
   constexpr int RQ = 4 * NC, RP = RQ + 1;  // uint4 per row, pitch
   __shared__ uint4 stage[NW * kTok * RP];
   static_assert(!kVTable<BITS> || vtab_bytes<BITS>() <= kTok * RP * 16, "V table fits a wave's staging space");
+  static_assert(vtab_bytes<3>() <= kTok * 9 * 16, "the 3-bit V table fits a wave's staging space");
+  // At D = 64 and widths up to 4 (and up to 8 heads), K is dequantized by lookups in
+  // a table of every (source head, channel, symbol) value too (9 KiB at 3 bits).
+  constexpr bool kKTab = NC == 2 && BITS <= 4 && HM == kMH;
+  __shared__ __attribute__((aligned(16))) uint8_t ktab[kKTab ? D * ktab_row<BITS>() : 16];
   if (threadIdx.x == 0) {
     int good = 1;
     if (!(g.flags & KVMI_F_NO_HEADER)) {
@@ -221,7 +348,10 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
   __syncthreads();
   if (!ok) return;
   fill_positions(T, H);
-  fill_kconst<false>(T, job.kmeta, H, D);
+  if constexpr (kKTab)
+    fill_k_table_w<BITS>(ktab, T, job.kmeta, H, D);
+  else
+    fill_kconst<false>(T, job.kmeta, H, D);
   __syncthreads();
 
   uint4 hp[2], hn[2];
@@ -234,6 +364,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
   const int jk = T.posk[hme], jv = T.posv[hme];
   const int gv = T.prof[1][2][jv];
   const float s = g.scale;
+  const uint32_t kbase = lds_addr(ktab) + (uint32_t)(2 * hme + HALF * hl * ktab_row<kKTab ? BITS : 1>());
 
   // section q = part * tiles + t: K tiles, then V tiles.  A section's inputs are its
   // packed symbols and, for V, the row's (min, scale).
@@ -264,8 +395,12 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
       // V: the row table lives in the wave's staging space (free until the transform)
       if constexpr (kVTable<BITS>)
         dequant_v_table<NC, BITS>(in.pk, bf16_to_f32(in.mn), bf16_to_f32(in.sc), stg, x);
+      else if constexpr (BITS == 3)
+        dequant_v_table_bfe<NC, BITS>(in.pk, bf16_to_f32(in.mn), bf16_to_f32(in.sc), stg, x);
       else
         dequant_half_row<NC, BITS, false>(in.pk, nullptr, bf16_to_f32(in.mn), bf16_to_f32(in.sc), x);
+    } else if constexpr (kKTab) {
+      dequant_k_table_w<NC, BITS>(in.pk, opaque(kbase), x);
     } else
       dequant_half_row<NC, BITS, true>(in.pk, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), 0.f, 0.f, x);
     chunk_fence();
@@ -300,6 +435,17 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_
     fetch(min(q + 2 * NW, last_sec), a);
     section(q + NW, b);
   }
+}
+
+template <int NC, int BITS, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                              int32_t* __restrict__ err) {
+  decode_body<NC, BITS, NW, kMH>(g, jobs, err);
+}
+template <int NC, int BITS, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_mfma_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                                   int32_t* __restrict__ err) {
+  decode_body<NC, BITS, NW, kWideH>(g, jobs, err);
 }
 
 // ============================================================== decode, K by table (D = 128, 4 bits)
@@ -481,13 +627,19 @@ int launch(K kernel, Geo g, int32_t num_jobs, int32_t max_blocks, const kvmi_lay
 
 template <int NC, int BITS>
 int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
-  if (g.flags & KVMI_F_CLAMP_LEVELS)
-    return launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode);
-  return launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
+  const bool clamp = g.flags & KVMI_F_CLAMP_LEVELS;
+  if (g.H > kMH)
+    return clamp ? launch(encode_mfma_wide_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode)
+                 : launch(encode_mfma_wide_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
+  return clamp ? launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode)
+               : launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
 }
 constexpr int kDecodeWaves = 8;  // waves per decode workgroup (two workgroups per CU)
 template <int NC, int BITS>
 int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
+  if (g.H > kMH)
+    return launch(decode_mfma_wide_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode,
+                  64 * kDecodeWaves);
   if constexpr (NC == 4 && BITS == 4)
     return launch(decode_kt_kernel<kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode, 64 * kDecodeWaves);
   else
@@ -510,6 +662,9 @@ int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
 }  // namespace
 
 int mfma_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
+  if (g.H > kMH)
+    return g.D == 64 ? launch(kstats_wide_kernel<2>, g, nj, mb, jobs, err, st, kWavesKstats)
+                     : launch(kstats_wide_kernel<4>, g, nj, mb, jobs, err, st, kWavesKstats);
   if (g.D == 64) return launch(kstats_mfma_kernel<2>, g, nj, mb, jobs, err, st, kWavesKstats);
   return launch(kstats_mfma_kernel<4>, g, nj, mb, jobs, err, st, kWavesKstats);
 }

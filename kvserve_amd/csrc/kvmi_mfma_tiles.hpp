@@ -288,13 +288,16 @@ constexpr uint32_t overflow_mask() {
   return 0x01010101u * (0xffu & ~((1u << BITS) - 1u));
 }
 
-// Shared per-workgroup tables.
-struct Tables {
-  uint32_t smask[kMH][64 + 4];  // bf16 sign-flip masks per (head, element pair), padded rows
-  float2 kc[kMH][128 + 4];      // K (min, 1/scale) [encode] or (min, scale) [decode], by source head
-  uint8_t prof[2][3][kMH];      // the job's profile bytes (kvmi_layer_job::profile)
-  int posk[kMH], posv[kMH], gfirst[kMH];
+// Shared per-workgroup tables for up to HM heads (8, or 32 for the wide-head kernels).
+template <int HM>
+struct TablesT {
+  uint32_t smask[HM][64 + 4];  // bf16 sign-flip masks per (head, element pair), padded rows
+  float2 kc[HM][128 + 4];      // K (min, 1/scale) [encode] or (min, scale) [decode], by source head
+  uint8_t prof[2][3][HM];      // the job's profile bytes (kvmi_layer_job::profile)
+  int posk[HM], posv[HM], gfirst[HM];
 };
+using Tables = TablesT<kMH>;
+constexpr int kWideH = 32;  // head capacity of the wide-head kernels (H = 16 or 32)
 
 // Decode tables of the K-table decode: the per-channel K pairs are replaced by the
 // table of dequantized values (decode_kt_kernel).
@@ -342,8 +345,8 @@ __device__ __forceinline__ void fill_positions(TT& T, int H) {
 
 // K constants by source head from kmeta (stored by output position j, whose source
 // head is order[j]).  DIV: store (min, 1/scale) instead of (min, scale).
-template <bool DIV>
-__device__ __forceinline__ void fill_kconst(Tables& T, const uint16_t* kmeta, int H, int D) {
+template <bool DIV, class TT>
+__device__ __forceinline__ void fill_kconst(TT& T, const uint16_t* kmeta, int H, int D) {
   const int HD = H * D;
   for (int i = threadIdx.x; i < HD; i += (int)blockDim.x) {
     const int j = i / D, e = i % D, hs = T.prof[0][0][j];
@@ -427,8 +430,8 @@ __device__ __forceinline__ void sign_half_row(const uint32_t (*smask)[64 + 4], i
 #pragma unroll
   for (int u = 0; u < 2 * NC; ++u) x[u] = xor4(x[u], sm[u]);
 }
-template <int NC>
-__device__ __forceinline__ void sign_half_row(const Tables& T, int h, int hl, uint4 (&x)[2 * NC]) {
+template <int NC, class TT>
+__device__ __forceinline__ void sign_half_row(const TT& T, int h, int hl, uint4 (&x)[2 * NC]) {
   constexpr int HALF = 16 * NC;
   const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(h * (64 + 4) + (HALF / 2) * hl));
 #pragma unroll
@@ -726,13 +729,103 @@ __device__ __forceinline__ void dequant_k_table(const uint32_t (&W)[8], uint32_t
   }
 }
 
+// ---------------------------------------------------------------- tables at any width
+// Widths whose symbols do not sit in byte lanes (3 bits) address the tables with a
+// bit-field extract and a shift-add per element instead of the byte-select adds.
+
+// v * 16 + base in one v_lshl_add_u32 (left to itself the compiler folds the shift
+// into the extract that feeds it and spends a third instruction on the add).
+__device__ __forceinline__ uint32_t lshl4_add(uint32_t v, uint32_t base) {
+  uint32_t r;
+  asm("v_lshl_add_u32 %0, %1, 4, %2" : "=v"(r) : "v"(v), "v"(base));
+  return r;
+}
+
+// base + 16 * (symbol idx of the lane's packed half-row); idx is compile-time.
+template <int HALF, int BITS>
+__device__ __forceinline__ uint32_t sym_addr16(const LanePack<HALF, BITS>& pk, int idx, uint32_t base) {
+  const int bit = idx * BITS, wi = bit >> 5, sh = bit & 31;
+  uint32_t v;
+  if (sh + BITS <= 32)
+    v = __builtin_amdgcn_ubfe(pk.w[wi], (uint32_t)sh, (uint32_t)BITS);
+  else  // the symbol straddles two words
+    v = __builtin_amdgcn_alignbit(pk.w[wi + 1], pk.w[wi], (uint32_t)sh) & ((1u << BITS) - 1u);
+  return lshl4_add(v, base);
+}
+
+// Dequantized V operands from the wave's row table (filled here) for the widths the
+// byte-select lookup of dequant_v_table does not serve: the values of
+// dequant_half_row<NC, BITS, false>.
+template <int NC, int BITS>
+__device__ __forceinline__ void dequant_v_table_bfe(const LanePack<16 * NC, BITS>& pk, float mn, float sc, void* tab,
+                                                    uint4 (&x)[2 * NC]) {
+  const int r = threadIdx.x & 31;
+  const uint32_t row_base = lds_addr(tab) + (uint32_t)((r >> 3) * vtab_group<BITS>() + 2 * (r & 7));
+  fill_v_table<BITS>(row_base, mn, sc);
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) {
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int e = 8 * u + 2 * p;
+      w[p] = lds_read_u16(sym_addr16<16 * NC, BITS>(pk, e, row_base)) |
+             lds_read_u16(sym_addr16<16 * NC, BITS>(pk, e + 1, row_base)) << 16;
+    }
+    x[u] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// K table of decode_mfma_kernel at D = 64 and widths up to 4: the 2^BITS dequantized
+// values of every (source head hs, channel c) at byte c * ktab_row + 16 * q + 2 * hs.
+template <int BITS>
+constexpr int ktab_row() { return 16 * (1 << BITS) + 16; }
+
+template <int BITS, class TT>
+__device__ __forceinline__ void fill_k_table_w(uint8_t* ktab, const TT& T, const uint16_t* kmeta, int H, int D) {
+  const int HD = H * D;
+  const uint32_t base = lds_addr(ktab);
+  for (int i = threadIdx.x; i < HD; i += (int)blockDim.x) {
+    const int j = i / D, c = i % D, hs = T.prof[0][0][j];
+    const float mn = bf16_to_f32(gld(kmeta + i));
+    const float sc = bf16_to_f32(gld(kmeta + HD + i));
+    const uint32_t a = base + (uint32_t)(c * ktab_row<BITS>() + 2 * hs);
+#pragma unroll
+    for (int q = 0; q < (1 << BITS); q += 2) {
+      const uint32_t w = pack_bf16x2(rbf((float)q * sc) + mn, rbf((float)(q + 1) * sc) + mn);
+      lds_write_u16(a + 16u * q, w);
+      lds_write_u16(a + 16u * (q + 1), w >> 16);
+    }
+  }
+}
+
+// Dequantized K operands of the lane's half-row from that table; `kbase` is the
+// address of (the lane's source head, channel HALF * hl): element e of the half-row
+// is channel HALF * hl + e.
+template <int NC, int BITS>
+__device__ __forceinline__ void dequant_k_table_w(const LanePack<16 * NC, BITS>& pk, uint32_t kbase,
+                                                  uint4 (&x)[2 * NC]) {
+  constexpr int R = ktab_row<BITS>();
+#pragma unroll
+  for (int u = 0; u < 2 * NC; ++u) {
+    uint32_t w[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int e = 8 * u + 2 * p;
+      w[p] = lds_read_u16(sym_addr16<16 * NC, BITS>(pk, e, kbase) + (uint32_t)(e * R)) |
+             lds_read_u16(sym_addr16<16 * NC, BITS>(pk, e + 1, kbase) + (uint32_t)((e + 1) * R)) << 16;
+    }
+    x[u] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // DPP lane exchange of a float (no bound_ctrl; every lane is enabled).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
 }
-// Min / max over the H lanes of a token (aligned groups of H in 1, 2, 4, 8):
-// quad_perm xor 1, xor 2, then row_half_mirror (lane i <-> 7 - i of each 8).
+// Min / max over the H lanes of a token (aligned groups of H in 1, 2, 4, 8, 16, 32):
+// quad_perm xor 1, xor 2, row_half_mirror (lane i <-> 7 - i of each 8), row_mirror
+// (lane i <-> 15 - i of each 16), then lane xor 16 through ds_bpermute.
 __device__ __forceinline__ void token_minmax(float& a, float& b, int H) {
   if (H >= 2) {
     a = fminf(a, dpp<0xB1>(a));
@@ -745,6 +838,15 @@ __device__ __forceinline__ void token_minmax(float& a, float& b, int H) {
   if (H >= 8) {
     a = fminf(a, dpp<0x141>(a));
     b = fmaxf(b, dpp<0x141>(b));
+  }
+  if (H >= 16) {
+    a = fminf(a, dpp<0x140>(a));
+    b = fmaxf(b, dpp<0x140>(b));
+  }
+  if (H >= 32) {
+    const int src = (int)((threadIdx.x & 63) ^ 16) << 2;
+    a = fminf(a, __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(a))));
+    b = fmaxf(b, __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(b))));
   }
 }
 // Min / max of x over lanes l and l ^ 32.  v_permlane32_swap exchanges the upper 32
@@ -812,7 +914,8 @@ struct LaneProfile {
   float lvk, lvv;
   bool rep_lane;  // writes the V metadata of (group, token)
 };
-__device__ __forceinline__ LaneProfile lane_profile(const Tables& T, int hme, int hl) {
+template <class TT>
+__device__ __forceinline__ LaneProfile lane_profile(const TT& T, int hme, int hl) {
   LaneProfile p;
   p.jk = T.posk[hme];
   p.jv = T.posv[hme];

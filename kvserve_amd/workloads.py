@@ -80,7 +80,9 @@ def llama_row_profiles(num_layers: int, H: int, levels=(16, 16, 16, 16), ratio: 
     l % 32); levels = (high K, high V, low K, low V)."""
     mask = head_low_mask(scores_from_csv("Llama-3.1-8B-Instruct"), ratio)
     hk, hv, lk, lv = levels
-    return [section_profile(mask[l % mask.shape[0]][:H], hk, hv, lk, lv) for l in range(num_layers)]
+    # more heads than the CSV's 8 (the wide-head benchmark variants): the row repeats
+    return [section_profile(np.resize(mask[l % mask.shape[0]], H) if H > mask.shape[1] else mask[l % mask.shape[0]][:H],
+                            hk, hv, lk, lv) for l in range(num_layers)]
 
 
 def make_config1(device="cuda", seed: int = 1) -> Workload:
@@ -93,12 +95,15 @@ def make_config1(device="cuda", seed: int = 1) -> Workload:
     return Workload("config1", [req], H, D, S, 4, SEED_HADAMARD)
 
 
-def make_config2(device="cuda", seed: int = 2, num_layers: int = 32, pool_blocks: int = 65536,
-                 fill: str = "zeros") -> Workload:
+def make_config2(device="cuda", seed: int = 2, num_layers: int = 32, pool_blocks: Optional[int] = None,
+                 fill: str = "zeros", num_heads: int = 8, head_dim: int = 128) -> Workload:
     """Llama-3-8B-shaped request: 32 layers x 8192 tokens in a 65536-block pool per layer
     (4 GiB per layer, 128 GiB total).  Only the request's blocks hold data; the rest
-    of each pool is `fill` ("zeros" or "empty")."""
-    L, S, H, D, B = num_layers, 16, 8, 128, 512
+    of each pool is `fill` ("zeros" or "empty").  `num_heads` / `head_dim` other than
+    8 / 128 give the same request with wider rows (the pool keeps 4 GiB per layer)."""
+    L, S, H, D, B = num_layers, 16, num_heads, head_dim, 512
+    if pool_blocks is None:
+        pool_blocks = 65536 * 8 * 128 // (H * D)
     gen = torch.Generator(device=device).manual_seed(seed)
     perm = torch.randperm(pool_blocks, generator=torch.Generator(device="cpu").manual_seed(seed))
     ids = perm[:B].to(torch.int32).to(device)

@@ -344,7 +344,12 @@ def test_config5_full_size_batch_sampled_matches_oracle(cuda):
     (4, 32, 64, 3),
     (8, 32, 128, 2),
     (8, 16, 128, 8),
-    (16, 16, 128, 4),  # 8 % H != 0: register-FWHT kernels
+    (16, 16, 128, 4),  # 16 heads: wide-head MFMA kernels (2 tokens per tile)
+    (32, 16, 128, 4),  # 32 heads: one token per tile, head-major statistics tiles
+    (32, 16, 64, 2),
+    (32, 16, 64, 3),   # 24-byte stream runs at 32 heads: the generic row kernels
+    (16, 32, 64, 3),
+    (32, 1, 128, 4),   # one-token blocks: a statistics tile spans 32 blocks
     (8, 16, 64, 5),
     (8, 16, 64, 4),    # D = 64 with the V row table
     (4, 16, 64, 2),
@@ -388,8 +393,9 @@ def test_geometries_match_oracle(cuda, H, S, D, bits):
 ])
 def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
     """The generic row kernels (kvmi_rows.hip) run the oracle's FWHT stage order, so
-    symbols, metadata and the decompressed KV are bit-exact with the oracle."""
-    _rows_exact(cuda, H, S, D, bits, layout)
+    symbols, metadata and the decompressed KV are bit-exact with the oracle.  (32 heads
+    at D = 128 would take the wide-head MFMA kernels: the row kernels are forced.)"""
+    _rows_exact(cuda, H, S, D, bits, layout, fwht="rows" if (H in (16, 32) and D in (64, 128)) else None)
 
 
 @pytest.mark.parametrize("H,S,D,bits", [(8, 16, 128, 4), (8, 16, 64, 4), (4, 32, 128, 3)])
