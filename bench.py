@@ -110,6 +110,15 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> di
     not MFMA-eligible)."""
     default_axes = tuple(getattr(codec, "axes", ("channel", "token"))) == ("channel", "token")
     pow2 = D in (64, 128) and default_axes
+    if D == 256 and H <= 16 and default_axes and codec.fwht == "mfma" and codec.transform:
+        Hv = 2 * H  # paired virtual heads of 128 (kvmi_common.hpp paired_view)
+        ok = 8 % Hv == 0 or (Hv in (16, 32) and S & (S - 1) == 0 and ((32 // Hv) * 128 * bits // 8) % 16 == 0)
+        if ok and (S * Hv) % 32 == 0:
+            hm = 8 if Hv <= 8 else 32
+            return {"kvmi_encode_paged": f"encode_mfma_pair_kernel<{bits}, false, {hm}>",
+                    "kvmi_decode_paged": f"decode_mfma_pair_kernel<{bits}, 8, {hm}>",
+                    "kvmi_kstats_paged": "kstats_mfma_pair_kernel" if Hv <= 8 else "kstats_wide_pair_kernel",
+                    "finalize": "kstats_finalize_kernel"}
     wide = H in (16, 32) and S & (S - 1) == 0 and ((32 // H) * D * bits // 8) % 16 == 0  # wide-head MFMA
     mfma = pow2 and codec.fwht == "mfma" and codec.transform and (8 % H == 0 or wide) and (S * H) % 32 == 0
     if mfma and wide:

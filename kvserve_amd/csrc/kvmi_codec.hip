@@ -419,7 +419,11 @@ extern "C" int kvmi_kstats_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (mfma_eligible(g)) {
+  Geo v;
+  if (paired_view(g, &v)) {  // the keys have the same layout in both views: finalize with g
+    rc = mfma_kstats(v, jobs, num_jobs, max_blocks, err, st);
+    if (rc) return rc;
+  } else if (mfma_eligible(g)) {
     rc = mfma_kstats(g, jobs, num_jobs, max_blocks, err, st);
     if (rc) return rc;
   } else if (!quad_eligible(g)) {
@@ -450,6 +454,8 @@ extern "C" int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Geo v;
+  if (paired_view(g, &v)) return mfma_encode(v, jobs, num_jobs, max_blocks, err, st);
   if (mfma_eligible(g)) return mfma_encode(g, jobs, num_jobs, max_blocks, err, st);
   if (!quad_eligible(g)) return rows_encode(g, jobs, num_jobs, max_blocks, err, st);
   set_valu_bpw(&g);
@@ -471,6 +477,8 @@ extern "C" int kvmi_decode_paged(const kvmi_geometry* geom, const kvmi_layer_job
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   if (!jobs || !err) return KVMI_EINVAL;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  Geo v;
+  if (paired_view(g, &v)) return mfma_decode(v, jobs, num_jobs, max_blocks, err, st);
   if (mfma_eligible(g)) return mfma_decode(g, jobs, num_jobs, max_blocks, err, st);
   if (!quad_eligible(g)) return rows_decode(g, jobs, num_jobs, max_blocks, err, st);
   set_valu_bpw(&g);

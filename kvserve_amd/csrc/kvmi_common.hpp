@@ -21,6 +21,12 @@ __host__ __device__ constexpr int next_pow2(int x) {
 // token; the KVMI_F_* axis flags select the others.
 enum Axis { kAxChannel = 0, kAxToken = 1, kAxTensor = 2 };
 constexpr uint32_t kAxisFlags = KVMI_F_K_TOKEN | KVMI_F_K_TENSOR | KVMI_F_V_CHANNEL | KVMI_F_V_TENSOR;
+// Internal (never part of a caller's geometry): head_dim 256 served by the D = 128 MFMA
+// kernels as 2H "virtual heads" of 128 channels, virtual head 2h + b being half b of
+// head h.  Pool rows, sign bits, K metadata and K keys have the same bytes in both
+// views; the permuted stream and the profile are mapped (seg_addr, stage_profile), and
+// the 256-point transform is rebuilt from the two 128-point ones by one butterfly.
+constexpr uint32_t kPairedHeads = 1u << 30;
 __host__ __device__ inline int part_axis(uint32_t flags, int part) {
   if (part == 0) return (flags & KVMI_F_K_TOKEN) ? kAxToken : (flags & KVMI_F_K_TENSOR) ? kAxTensor : kAxChannel;
   return (flags & KVMI_F_V_CHANNEL) ? kAxChannel : (flags & KVMI_F_V_TENSOR) ? kAxTensor : kAxToken;
@@ -71,16 +77,23 @@ __device__ __forceinline__ RowPos row_pos(const kvmi_layer_job& job, int blk0, i
 // Byte address of the packed symbols of (part, output head position j, token tok)
 // starting at element e0 of the row, in the permuted [l,2,H',B,S,D] or native
 // [l,2,B,S,H',D] symbol order.  Callers keep e0*BITS a multiple of 8.
-template <int BITS>
+// PAIRED: j is a paired virtual head (kPairedHeads); the permuted order is then
+// [H/2][tokens][2 halves x D].
+template <int BITS, bool PAIRED = false>
 __device__ __forceinline__ uint8_t* seg_addr(const kvmi_layer_job& job, const Geo& g, int part, int j, int tok,
                                              int e0) {
   const int64_t D = g.D;
   const int64_t ntok = (int64_t)job.num_blocks * g.S;
   int64_t ts, hs, ps;
-  if (g.flags & KVMI_F_NATIVE_LAYOUT) {
+  if (g.flags & KVMI_F_NATIVE_LAYOUT) {  // the same bytes for paired virtual heads
     ts = (int64_t)g.H * D;
     hs = D;
     ps = ntok * g.H * D;
+  } else if (PAIRED) {  // [H/2][tokens][2 halves x D]
+    ts = 2 * D;
+    ps = ntok * g.H * D;
+    return job.stream + ((g.flags & KVMI_F_NO_HEADER) ? 0 : KVMI_HEADER_BYTES) +
+           ((job.symbol_offset + part * ps + (j >> 1) * (2 * ntok * D) + (j & 1) * D + tok * ts + e0) * BITS) / 8;
   } else {
     ts = D;
     hs = ntok * D;
@@ -150,6 +163,19 @@ inline bool mfma_eligible(const Geo& g) {
   const bool heads = (8 % g.H) == 0 || ((g.H == 16 || g.H == 32) && (g.S & (g.S - 1)) == 0 && runs16);
   return !(g.flags & (KVMI_F_VALU_FWHT | KVMI_F_ROW_FWHT | KVMI_F_NO_TRANSFORM | kAxisFlags)) &&
          (g.D == 64 || g.D == 128) && heads && ((g.S * g.H) % 32) == 0;
+}
+// head_dim 256 on the MFMA kernels (the transform profile, default axes, up to 16
+// heads): fills *v with the virtual-head view (2H heads of 128, scale still 1/16).
+inline bool paired_view(const Geo& g, Geo* v) {
+  if (g.D != 256 || g.H > 16 || (g.flags & (KVMI_F_VALU_FWHT | KVMI_F_ROW_FWHT | KVMI_F_NO_TRANSFORM | kAxisFlags)))
+    return false;
+  Geo w = g;
+  w.H = 2 * g.H;
+  w.D = 128;
+  w.flags |= kPairedHeads;
+  if (!mfma_eligible(w)) return false;
+  *v = w;
+  return true;
 }
 inline bool quad_eligible(const Geo& g) {
   return !(g.flags & (KVMI_F_ROW_FWHT | kAxisFlags)) && (g.D == 64 || g.D == 128) && g.H <= kMaxQuadH &&

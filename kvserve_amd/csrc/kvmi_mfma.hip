@@ -7,9 +7,8 @@ namespace kvmi {
 namespace {
 
 // ============================================================== K statistics (orientation N)
-template <int NC>
-__global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
-                                                          int32_t* __restrict__ err) {
+template <int NC, bool PAIRED>
+__device__ __forceinline__ void kstats_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs) {
   constexpr int D = 32 * NC;
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int S = g.S, H = g.H;
@@ -46,12 +45,13 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
     }
   const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
   uint4* wbuf = tbuf + wave * tile_buf_q<NC>();
+  constexpr bool paired = PAIRED;
   auto accumulate = [&](uint4 (&x)[2 * NC]) {
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(x[u]);
     tile_to_half_rows<NC>(wbuf, x);
     sign_half_row<NC>(T, hme, hl, x);
-    kstats_tile<NC>(x, hp, hn, mn, mx);
+    kstats_tile<NC>(x, hp, hn, mn, mx, paired);
   };
   auto fetch = [&](int t, uint4 (&x)[2 * NC]) {
     load_tile<NC>(pool, tile_row0(job, S, H, tile_tok(run.tok0, H, t)), x);
@@ -78,6 +78,17 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
   }
 }
 
+template <int NC>
+__global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                          int32_t* __restrict__ err) {
+  kstats_body<NC, false>(g, jobs);
+}
+// head_dim 256 as paired virtual heads of 128 (kPairedHeads), up to 4 real heads
+__global__ __launch_bounds__(kMW) void kstats_mfma_pair_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                               int32_t* __restrict__ err) {
+  kstats_body<4, true>(g, jobs);
+}
+
 // ============================================================== K statistics, 16 or 32 heads
 // With 16 or 32 heads a token-major tile holds 16 heads per lane's registers in
 // orientation N, too many running min / max to keep.  Here a tile is 32 consecutive
@@ -89,9 +100,8 @@ __global__ __launch_bounds__(kMW) void kstats_mfma_kernel(Geo g, const kvmi_laye
 struct SignTable {
   uint32_t smask[kWideH][64 + 4];
 };
-template <int NC>
-__global__ __launch_bounds__(kMW) void kstats_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
-                                                          int32_t* __restrict__ err) {
+template <int NC, bool PAIRED>
+__device__ __forceinline__ void kstats_wide_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs) {
   constexpr int D = 32 * NC, HALF = 16 * NC, PR = 4 * NC;
   const kvmi_layer_job job = jobs[blockIdx.y];
   const int S = g.S, H = g.H, HD = H * D;
@@ -118,18 +128,25 @@ __global__ __launch_bounds__(kMW) void kstats_wide_kernel(Geo g, const kvmi_laye
   const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool);
   const int sh = __builtin_ctz((unsigned)S);  // S is a power of two (mfma_eligible)
   const int last_tok = run.tok_end - 1;
-  const int nk = (run.tok_end - run.tok0 + kTok - 1) / kTok;  // tiles per head
-  const int nhw = (H - wave + kWaves - 1) / kWaves;           // heads of this wave
+  // Paired virtual heads (head_dim 256): a tile is 16 tokens x both halves of one real
+  // head (rows 2i, 2i + 1 = the halves of token i), so the butterfly stays in a lane.
+  constexpr bool paired = PAIRED;
+  const int HU = paired ? H / 2 : H;                   // heads a wave walks
+  const int TPT = paired ? kTok / 2 : kTok;            // tokens per tile
+  const int nk = (run.tok_end - run.tok0 + TPT - 1) / TPT;  // tiles per head
+  const int nhw = (HU - wave + kWaves - 1) / kWaves;   // heads of this wave
   const int ntw = nhw * nk;
   uint4* wbuf = tbuf + wave * tile_buf_q<NC>();
-  // tile n of this wave: head wave + 4 (n / nk), tokens tok0 + 32 (n % nk) + (0..31);
+  // tile n of this wave: head wave + 4 (n / nk), tokens tok0 + TPT (n % nk) + ...;
   // instruction v of a lane reads piece l % PR of row (64 / PR) v + l / PR
   auto fetch = [&](int n, uint4 (&x)[2 * NC]) {
-    const int h = wave + kWaves * (n / nk), t0 = run.tok0 + kTok * (n % nk);
+    const int hu = wave + kWaves * (n / nk), t0 = run.tok0 + TPT * (n % nk);
 #pragma unroll
     for (int v = 0; v < 2 * NC; ++v) {
-      const int t = min(t0 + (64 / PR) * v + l / PR, last_tok);
-      const int64_t row = ((int64_t)gld(job.block_ids + (t >> sh)) * S + (t & (S - 1))) * H + h;
+      const int rho = (64 / PR) * v + l / PR;
+      const int t = min(t0 + (paired ? rho >> 1 : rho), last_tok);
+      const int vh = paired ? 2 * hu + (rho & 1) : hu;
+      const int64_t row = ((int64_t)gld(job.block_ids + (t >> sh)) * S + (t & (S - 1))) * H + vh;
       x[v] = gld(reinterpret_cast<const uint4*>(pool + row * D) + l % PR);
     }
   };
@@ -146,23 +163,32 @@ __global__ __launch_bounds__(kMW) void kstats_wide_kernel(Geo g, const kvmi_laye
   auto accumulate = [&](int n, uint4 (&x)[2 * NC]) {
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(x[u]);
-    const int h = wave + kWaves * (n / nk);
+    const int hu = wave + kWaves * (n / nk);
     tile_to_half_rows<NC>(wbuf, x);
-    sign_half_row<NC>(T, h, hl, x);
-    kstats_tile<NC>(x, hp, hn, mn, mx);
+    // the lane's row r is half r & 1 of a token when paired: that virtual head's signs
+    sign_half_row<NC>(T, paired ? 2 * hu + (r & 1) : hu, hl, x);
+    kstats_tile<NC>(x, hp, hn, mn, mx, paired);
     if (n % nk == nk - 1) {
       // the head's last tile: its keys (channel HALF (r >> 4) + 16 c + (r & 15) of
-      // chunk c; lanes r and r + 32 hold other rows of the same channel)
+      // chunk c; lanes r and r + 32 hold other rows of the same channel).  Register
+      // i % 4 = a holds rows with m & 1 = a & 1: the half of a paired head.
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        float a = fminf(fminf(mn[0][c], mn[1][c]), fminf(mn[2][c], mn[3][c]));
-        float b = fmaxf(fmaxf(mx[0][c], mx[1][c]), fmaxf(mx[2][c], mx[3][c]));
-        a = halves_min(a);
-        b = halves_max(b);
-        if (hl == 0) {
-          const int f = HALF * (r >> 4) + 16 * c + (r & 15);
-          lkey[h * D + f] = f2key(a * g.scale);
-          lkey[HD + h * D + f] = f2key(b * g.scale);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          if (!paired && half) break;
+          float a = paired ? fminf(mn[half][c], mn[half + 2][c])
+                           : fminf(fminf(mn[0][c], mn[1][c]), fminf(mn[2][c], mn[3][c]));
+          float b = paired ? fmaxf(mx[half][c], mx[half + 2][c])
+                           : fmaxf(fmaxf(mx[0][c], mx[1][c]), fmaxf(mx[2][c], mx[3][c]));
+          a = halves_min(a);
+          b = halves_max(b);
+          if (hl == 0) {
+            const int vh = paired ? 2 * hu + half : hu;
+            const int f = HALF * (r >> 4) + 16 * c + (r & 15);
+            lkey[vh * D + f] = f2key(a * g.scale);
+            lkey[HD + vh * D + f] = f2key(b * g.scale);
+          }
         }
       }
       reset();
@@ -185,9 +211,21 @@ __global__ __launch_bounds__(kMW) void kstats_wide_kernel(Geo g, const kvmi_laye
   }
 }
 
+template <int NC>
+__global__ __launch_bounds__(kMW) void kstats_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                          int32_t* __restrict__ err) {
+  kstats_wide_body<NC, false>(g, jobs);
+}
+// head_dim 256 as 16 or 32 paired virtual heads (8 or 16 real heads)
+__global__ __launch_bounds__(kMW) void kstats_wide_pair_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                               int32_t* __restrict__ err) {
+  kstats_wide_body<4, true>(g, jobs);
+}
+
 // ============================================================== encode (orientation T)
 // HM: head capacity of the tables (kMH, or kWideH for 16 and 32 heads).
-template <int NC, int BITS, bool CLAMP, int HM>
+// PAIRED: head_dim 256 as paired virtual heads of 128 (kPairedHeads).
+template <int NC, int BITS, bool CLAMP, int HM, bool PAIRED>
 __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs,
                                             int32_t* __restrict__ err) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
@@ -217,7 +255,8 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   static_assert(tile_buf_q<NC>() >= 2 * NC * 64 && tile_buf_q<NC>() >= TQ, "a wave buffer holds each use");
   __shared__ uint4 ypark[kWaves * tile_buf_q<NC>()];
   const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
-  stage_profile(T, job.profile, H);
+  constexpr bool paired = PAIRED;
+  stage_profile(T, job.profile, H, paired);
   fill_signs(T, job.signs, H, D);
   if (threadIdx.x == 0 && job.write_header && blockIdx.x == 0 && !(g.flags & KVMI_F_NO_HEADER))
     write_stream_header(job.stream, BITS, job.chunk_symbols);
@@ -243,19 +282,24 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   uint4* ostage = ypark + wave * tile_buf_q<NC>();
   uint8_t* ost = reinterpret_cast<uint8_t*>(ostage);
   const int tpt = kTok / H;  // tokens per tile
-  // byte offset of this lane's half-row in the staged image, by output position
-  auto stage_off = [&](int j) { return native ? (r / H) * (H * RB) + j * RB + hl * (RB / 2)
-                                              : j * (tpt * RB) + (r / H) * RB + hl * (RB / 2); };
+  // byte offset of this lane's half-row in the staged image, by output position; a
+  // permuted run of paired virtual heads is a real head's tokens, both halves each
+  auto stage_off = [&](int j) {
+    if (native) return (r / H) * (H * RB) + j * RB + hl * (RB / 2);
+    if (paired) return (j >> 1) * (2 * tpt * RB) + (r / H) * (2 * RB) + (j & 1) * RB + hl * (RB / 2);
+    return j * (tpt * RB) + (r / H) * RB + hl * (RB / 2);
+  };
   const int offk = stage_off(lp.jk), offv = stage_off(lp.jv);
   // write the staged image of (part, tile starting at token ta) to the stream
   auto flush = [&](int part, int ta) {
-    const int rq = native ? TQ : tpt * RB / 16;  // uint4 per run
+    const int rq = native ? TQ : (paired ? 2 : 1) * tpt * RB / 16;  // uint4 per run
 #pragma unroll
     for (int u = 0; u < (TQ + 63) / 64; ++u) {
       const int q = 64 * u + l;
       if (TQ % 64 == 0 || q < TQ) {
         const int run_j = q / rq;
-        uint8_t* dst = seg_addr<BITS>(job, g, part, native ? 0 : run_j, ta, 0) + 16 * (q - run_j * rq);
+        const int j0 = native ? 0 : (paired ? 2 * run_j : run_j);
+        uint8_t* dst = seg_addr<BITS, PAIRED>(job, g, part, j0, ta, 0) + 16 * (q - run_j * rq);
         gst(reinterpret_cast<uint4*>(dst), ostage[q]);
       }
     }
@@ -278,7 +322,7 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
       sign_half_row<NC>(T, hme, hl, xk);
       LanePack<HALF, BITS> pkd;
       quant_k_tile<NC, BITS, CLAMP>(xk, hp, hn, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), s, lp.lvk, pkd,
-                                    over);
+                                    over, paired);
       pkd.store_lds(ost + offk);
       flush(0, ta);
     }
@@ -289,7 +333,7 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
     tile_to_half_rows<NC>(wbuf, xv);
     sign_half_row<NC>(T, hme, hl, xv);
     LanePack<HALF, BITS> pkd;
-    quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, wbuf + l, pkd, over);
+    quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, wbuf + l, pkd, over, paired);
     pkd.store_lds(ost + offv);
     flush(1, ta);
   }
@@ -299,18 +343,24 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
 template <int NC, int BITS, bool CLAMP>
 __global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
                                                           int32_t* __restrict__ err) {
-  encode_body<NC, BITS, CLAMP, kMH>(g, jobs, err);
+  encode_body<NC, BITS, CLAMP, kMH, false>(g, jobs, err);
 }
 // 16 or 32 KV heads: a tile holds 2 tokens or 1 (32 rows), with tables for 32 heads.
 template <int NC, int BITS, bool CLAMP>
 __global__ __launch_bounds__(kMW) void encode_mfma_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
                                                                int32_t* __restrict__ err) {
-  encode_body<NC, BITS, CLAMP, kWideH>(g, jobs, err);
+  encode_body<NC, BITS, CLAMP, kWideH, false>(g, jobs, err);
+}
+// head_dim 256 as paired virtual heads of 128, with tables for HM virtual heads
+template <int BITS, bool CLAMP, int HM>
+__global__ __launch_bounds__(kMW) void encode_mfma_pair_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                               int32_t* __restrict__ err) {
+  encode_body<4, BITS, CLAMP, HM, true>(g, jobs, err);
 }
 
 // ============================================================== decode (orientation T)
 // NW waves per workgroup share one set of tables (and one header check).
-template <int NC, int BITS, int NW, int HM>
+template <int NC, int BITS, int NW, int HM, bool PAIRED>
 __device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs,
                                             int32_t* __restrict__ err) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
@@ -343,7 +393,8 @@ __device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* 
     }
     ok = good;
   }
-  stage_profile(T, job.profile, H);
+  constexpr bool paired = PAIRED;
+  stage_profile(T, job.profile, H, paired);
   fill_signs(T, job.signs, H, D);
   __syncthreads();
   if (!ok) return;
@@ -377,7 +428,7 @@ __device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* 
   auto fetch = [&](int q, In& in) {
     const int part = q >= run.tiles, t = q - part * run.tiles;
     const int tok = tile_tok(run.tok0, H, t) + r / H;
-    in.pk.load(seg_addr<BITS>(job, g, part, part ? jv : jk, tok, HALF * hl));
+    in.pk.load(seg_addr<BITS, PAIRED>(job, g, part, part ? jv : jk, tok, HALF * hl));
     in.mn = gld(job.vmeta + (int64_t)gv * ntok + tok);
     in.sc = gld(job.vmeta + (int64_t)(G + gv) * ntok + tok);
   };
@@ -407,7 +458,8 @@ __device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* 
     const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(hme * (64 + 4) + (HALF / 2) * hl));
 #pragma unroll
     for (int cp = 0; cp < NC; ++cp) {
-      const f32x16 acc = transform_T<NC>(x, hp, hn, cp);
+      f32x16 acc = transform_T<NC>(x, hp, hn, cp);
+      if (paired) pair_butterfly_T(acc);
       uint32_t w[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) w[i] = pack_bf16x2(acc[2 * i] * s, acc[2 * i + 1] * s);
@@ -440,12 +492,17 @@ __device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* 
 template <int NC, int BITS, int NW>
 __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
                                                               int32_t* __restrict__ err) {
-  decode_body<NC, BITS, NW, kMH>(g, jobs, err);
+  decode_body<NC, BITS, NW, kMH, false>(g, jobs, err);
 }
 template <int NC, int BITS, int NW>
 __global__ __launch_bounds__(64 * NW) void decode_mfma_wide_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
                                                                    int32_t* __restrict__ err) {
-  decode_body<NC, BITS, NW, kWideH>(g, jobs, err);
+  decode_body<NC, BITS, NW, kWideH, false>(g, jobs, err);
+}
+template <int BITS, int NW, int HM>
+__global__ __launch_bounds__(64 * NW) void decode_mfma_pair_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                                   int32_t* __restrict__ err) {
+  decode_body<4, BITS, NW, HM, true>(g, jobs, err);
 }
 
 // ============================================================== decode, K by table (D = 128, 4 bits)
@@ -628,6 +685,14 @@ int launch(K kernel, Geo g, int32_t num_jobs, int32_t max_blocks, const kvmi_lay
 template <int NC, int BITS>
 int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
   const bool clamp = g.flags & KVMI_F_CLAMP_LEVELS;
+  if constexpr (NC == 4)
+    if (g.flags & kPairedHeads) {
+      if (g.H > kMH)
+        return clamp ? launch(encode_mfma_pair_kernel<BITS, true, kWideH>, g, nj, mb, jobs, err, st, kWavesEncode)
+                     : launch(encode_mfma_pair_kernel<BITS, false, kWideH>, g, nj, mb, jobs, err, st, kWavesEncode);
+      return clamp ? launch(encode_mfma_pair_kernel<BITS, true, kMH>, g, nj, mb, jobs, err, st, kWavesEncode)
+                   : launch(encode_mfma_pair_kernel<BITS, false, kMH>, g, nj, mb, jobs, err, st, kWavesEncode);
+    }
   if (g.H > kMH)
     return clamp ? launch(encode_mfma_wide_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode)
                  : launch(encode_mfma_wide_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
@@ -637,6 +702,14 @@ int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
 constexpr int kDecodeWaves = 8;  // waves per decode workgroup (two workgroups per CU)
 template <int NC, int BITS>
 int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
+  if constexpr (NC == 4)
+    if (g.flags & kPairedHeads) {
+      if (g.H > kMH)
+        return launch(decode_mfma_pair_kernel<BITS, kDecodeWaves, kWideH>, g, nj, mb, jobs, err, st, kWavesDecode,
+                      64 * kDecodeWaves);
+      return launch(decode_mfma_pair_kernel<BITS, kDecodeWaves, kMH>, g, nj, mb, jobs, err, st, kWavesDecode,
+                    64 * kDecodeWaves);
+    }
   if (g.H > kMH)
     return launch(decode_mfma_wide_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode,
                   64 * kDecodeWaves);
@@ -662,6 +735,9 @@ int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
 }  // namespace
 
 int mfma_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
+  if (g.flags & kPairedHeads)
+    return g.H > kMH ? launch(kstats_wide_pair_kernel, g, nj, mb, jobs, err, st, kWavesKstats)
+                     : launch(kstats_mfma_pair_kernel, g, nj, mb, jobs, err, st, kWavesKstats);
   if (g.H > kMH)
     return g.D == 64 ? launch(kstats_wide_kernel<2>, g, nj, mb, jobs, err, st, kWavesKstats)
                      : launch(kstats_wide_kernel<4>, g, nj, mb, jobs, err, st, kWavesKstats);

@@ -307,12 +307,20 @@ struct DecTables {
   int posk[kMH], posv[kMH], gfirst[kMH];
 };
 
-// Stage the profile bytes into LDS (one load per thread, no dependent chains).
+// Stage the profile bytes into LDS (one load per thread, no dependent chains).  With
+// paired virtual heads (kPairedHeads) the job's profile is the real one, [2][3][H / 2]:
+// virtual position 2j + b is half b of position j, whose source head is 2 order[j] + b.
 template <class TT>
-__device__ __forceinline__ void stage_profile(TT& T, const uint8_t* profile, int H) {
+__device__ __forceinline__ void stage_profile(TT& T, const uint8_t* profile, int H, bool paired = false) {
   if (threadIdx.x < 6u * H) {
     const int i = threadIdx.x, part = i / (3 * H), f = (i / H) % 3, k = i % H;
-    T.prof[part][f][k] = gld(profile + i);
+    if (paired) {
+      const int hr = H / 2;
+      const uint8_t b = gld(profile + part * 3 * hr + f * hr + (k >> 1));
+      T.prof[part][f][k] = f == 0 ? (uint8_t)(2 * b + (k & 1)) : b;
+    } else {
+      T.prof[part][f][k] = gld(profile + i);
+    }
   }
 }
 
@@ -436,6 +444,29 @@ __device__ __forceinline__ void sign_half_row(const TT& T, int h, int hl, uint4 
   const uint4* sm = reinterpret_cast<const uint4*>(&T.smask[0][0] + opaque(h * (64 + 4) + (HALF / 2) * hl));
 #pragma unroll
   for (int u = 0; u < 2 * NC; ++u) x[u] = xor4(x[u], sm[u]);
+}
+
+// Paired virtual heads: the 256-point transform of a row from the 128-point transforms
+// a_lo, a_hi of its halves, y_lo = a_lo + a_hi and y_hi = a_lo - a_hi (the Sylvester
+// matrix's last stage; the inverse has the same form).  Orientation T holds the two
+// halves of a row in the lane pair (2i, 2i + 1): fma(+-1, a, partner) is the one
+// rounding of the sum or difference.
+__device__ __forceinline__ void pair_butterfly_T(f32x16& acc) {
+  const float sgn = (threadIdx.x & 1) ? -1.f : 1.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float partner = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[i]), 0xB1, 0xF, 0xF, false));
+    acc[i] = __builtin_fmaf(sgn, acc[i], partner);
+  }
+}
+// Orientation N holds them in registers 2i and 2i + 1 of a lane (rows m and m ^ 1).
+__device__ __forceinline__ void pair_butterfly_N(f32x16& acc) {
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const float a = acc[i], b = acc[i + 1];
+    acc[i] = a + b;
+    acc[i + 1] = a - b;
+  }
 }
 
 // Forward / inverse transform, orientation T, output chunk cp (unscaled fp32).
@@ -868,7 +899,7 @@ __device__ __forceinline__ float halves_max(float x) {
 // H <= 8).  Running min / max per (s, c) of the unscaled accumulators.
 template <int NC>
 __device__ __forceinline__ void kstats_tile(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
-                                            float (&mn)[4][NC], float (&mx)[4][NC]) {
+                                            float (&mn)[4][NC], float (&mx)[4][NC], bool paired = false) {
 #pragma unroll
   for (int cp = 0; cp < NC; ++cp) {
     f32x16 acc = {};
@@ -879,6 +910,7 @@ __device__ __forceinline__ void kstats_tile(const uint4 (&x)[2 * NC], const uint
       acc = mfma(x[2 * c], neg ? hn[0] : hp[0], acc);
       acc = mfma(x[2 * c + 1], neg ? hn[1] : hp[1], acc);
     }
+    if (paired) pair_butterfly_N(acc);
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       mn[a][cp] = fminf(fminf(mn[a][cp], acc[a]), fminf(acc[a + 4], fminf(acc[a + 8], acc[a + 12])));
@@ -931,11 +963,12 @@ __device__ __forceinline__ LaneProfile lane_profile(const TT& T, int hme, int hl
 template <int NC, int BITS, bool CLAMP>
 __device__ __forceinline__ void quant_k_tile(const uint4 (&xk)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
                                              const float2* kq, float s, float lvk, LanePack<16 * NC, BITS>& pkd,
-                                             uint32_t& over) {
+                                             uint32_t& over, bool paired = false) {
   pkd.clear();
 #pragma unroll
   for (int cp = 0; cp < NC; ++cp) {
-    const f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
+    f32x16 acc = transform_T<NC>(xk, hp, hn, cp);
+    if (paired) pair_butterfly_T(acc);
     quant_chunk_k<16 * NC, BITS, CLAMP>(acc, cp, s, kq + 16 * cp, lvk, pkd, over);
     chunk_fence();
   }
@@ -1003,12 +1036,13 @@ __device__ __forceinline__ void quant_v_tile_lds(const uint4 (&xv)[2 * NC], cons
                                                  const uint4 (&hn)[2], const LaneProfile& lp,
                                                  const kvmi_layer_job& job, int ntok, int tok, int G, int H,
                                                  float s, uint4* ylane, LanePack<16 * NC, BITS>& pkd,
-                                                 uint32_t& over) {
+                                                 uint32_t& over, bool paired = false) {
   constexpr int HALF = 16 * NC;
   float amn = __builtin_inff(), amx = -__builtin_inff();
 #pragma unroll
   for (int cp = 0; cp < NC; ++cp) {
-    const f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+    f32x16 acc = transform_T<NC>(xv, hp, hn, cp);
+    if (paired) pair_butterfly_T(acc);
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
       amn = fminf(fminf(amn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));

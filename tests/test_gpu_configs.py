@@ -338,6 +338,10 @@ def test_config5_full_size_batch_sampled_matches_oracle(cuda):
 
 # ------------------------------------------------------------------ other geometries
 @pytest.mark.parametrize("H,S,D,bits", [
+    (8, 16, 256, 4),   # head_dim 256: paired virtual heads of 128 (16 of them: wide tables)
+    (4, 16, 256, 4),   # 8 virtual heads
+    (16, 16, 256, 2),  # 32 virtual heads
+    (2, 32, 256, 3),
     (4, 16, 128, 4),   # tensor-parallel half of 8 KV heads
     (2, 16, 128, 4),
     (1, 32, 128, 4),   # one head, 32-token blocks
@@ -355,6 +359,16 @@ def test_config5_full_size_batch_sampled_matches_oracle(cuda):
     (4, 16, 64, 2),
 ])
 def test_geometries_match_oracle(cuda, H, S, D, bits):
+    _geometry_vs_oracle(cuda, H, S, D, bits)
+
+
+@pytest.mark.parametrize("H,S,D,bits", [(8, 16, 256, 4), (4, 16, 256, 3), (16, 16, 128, 4), (32, 16, 64, 2)])
+def test_geometries_native_layout_match_oracle(cuda, H, S, D, bits):
+    """The native symbol order [l, 2, B, S, H', D] on the paired and wide-head kernels."""
+    _geometry_vs_oracle(cuda, H, S, D, bits, layout="native")
+
+
+def _geometry_vs_oracle(cuda, H, S, D, bits, layout="permuted"):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.profiles import section_profile
     from kvserve_amd.workloads import kv_blocks
@@ -369,7 +383,8 @@ def test_geometries_match_oracle(cuda, H, S, D, bits):
     prof = [section_profile([bool(v) for v in torch.randint(0, 2, (H,), generator=g)], levels[0], levels[0],
                             levels[1], levels[1]) for _ in range(L)]
     pools = [p.to(cuda) for p in pools]
-    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE)
+    print(f"geometry H={H} S={S} D={D} bits={bits} {layout}", flush=True)
+    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout)
     packet = codec.compress(pools, ids.to(torch.int32).to(cuda), prof)
     check_packet(packet)
     x = [_bits(p[:, ids.to(cuda).long()]) for p in pools]
@@ -394,8 +409,9 @@ def test_geometries_match_oracle(cuda, H, S, D, bits):
 def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
     """The generic row kernels (kvmi_rows.hip) run the oracle's FWHT stage order, so
     symbols, metadata and the decompressed KV are bit-exact with the oracle.  (32 heads
-    at D = 128 would take the wide-head MFMA kernels: the row kernels are forced.)"""
-    _rows_exact(cuda, H, S, D, bits, layout, fwht="rows" if (H in (16, 32) and D in (64, 128)) else None)
+    at D = 128 and D = 256 would take the MFMA kernels: the row kernels are forced.)"""
+    _rows_exact(cuda, H, S, D, bits, layout,
+                fwht="rows" if (H in (16, 32) and D in (64, 128)) or (D == 256 and H <= 16) else None)
 
 
 @pytest.mark.parametrize("H,S,D,bits", [(8, 16, 128, 4), (8, 16, 64, 4), (4, 32, 128, 3)])
