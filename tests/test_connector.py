@@ -326,3 +326,31 @@ def test_stale_buffers_dropped_and_consumer_side_noops():
     d.wait_for_save()
     assert d._layer_buffers == {}
     assert d.get_finished(set()) == (None, None)
+
+
+def test_sent_buffers_are_never_written_again():
+    """The loopback hands the consumer the producer's tensors themselves, so the producer
+    must never write a sent buffer again: a later request's save (after the caches
+    changed) leaves the earlier request's received tensor intact, in other storage."""
+    names = ["model.layers.0.attn", "model.layers.1.attn"]
+    tx = LoopbackTransport(False, port=15, device="cpu")
+    g = torch.Generator().manual_seed(5)
+    caches = {n: torch.randn((2, 6, 4, 2, 8), generator=g).to(torch.bfloat16) for n in names}
+    p = CompressedKVConnector(vllm_config(True, port=15), KVConnectorRole.WORKER)
+    got = {}
+    for rid, blocks in (("A", [1, 2]), ("B", [1, 2])):
+        m = CompressedKVConnectorMetadata()
+        m.add_request(rid, "T" + rid, [0] * 8, blocks, 4)
+        p.bind_connector_metadata(m)
+        for n in names:
+            p.save_kv_layer(n, caches[n], None)
+        p.wait_for_save()
+        ((_, stacked),) = tx.drain_received()["T" + rid]
+        got[rid] = (stacked, stacked.clone())
+        for n in names:
+            caches[n].mul_(-1)  # the producer's caches move on before the next save
+    a, a_at_receive = got["A"]
+    b, _ = got["B"]
+    assert torch.equal(a, a_at_receive)
+    assert torch.equal(b, -a)
+    assert a.untyped_storage().data_ptr() != b.untyped_storage().data_ptr()
