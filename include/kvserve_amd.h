@@ -95,9 +95,10 @@ typedef struct ihipStream_t* kvmi_stream_t;
 typedef struct kvmi_geometry {
   int32_t block_size; /* S: tokens per paged block (vLLM block_size) */
   int32_t num_heads;  /* H: KV heads of this worker's shard, 1..64 */
-  int32_t head_dim;   /* D: a multiple of 16 in [16, 256], with H * next_pow2(D) <= 8192; a D
-                         that is not a power of two is transformed in descending
-                         power-of-two chunks (hadamard_func.py:50-103) */
+  int32_t head_dim;   /* D: even in [2, 256], with H * next_pow2(D) <= 8192 and D * bits a
+                         multiple of 8 (whole-byte packed rows); a D that is not a power of
+                         two is transformed in descending power-of-two chunks, down to
+                         chunks of 1 channel (hadamard_func.py:50-103: 100 = 64 + 32 + 4) */
   int32_t bits;       /* bitpack width in [1, 8] */
   uint32_t flags;     /* KVMI_F_* */
   int32_t max_groups; /* G: V statistic groups per layer (<= H) */
@@ -203,8 +204,7 @@ int kvmi_check_block_ids(kvmi_layer_job* jobs, int32_t num_jobs, int32_t* err, k
 
 /*
  * Random-sign Hadamard transform of contiguous bf16 rows [rows, D], row r
- * belonging to head r % num_heads (hadamard_func.py:161-231), D a multiple of 16 in
- * [16, 256].  Each power-of-two chunk c of D (descending, hadamard_func.py:50-103) is
+ * belonging to head r % num_heads (hadamard_func.py:161-231), D even in [2, 256].  Each power-of-two chunk c of D (descending, hadamard_func.py:50-103) is
  * transformed on its own:
  *   forward: out = bf16( FWHT_fp32(x * s) * (1/sqrt(c)) )
  *   inverse: out = bf16( FWHT_fp32(x) * (1/sqrt(c)) ) * s

@@ -291,7 +291,7 @@ class FusedCompressionManager(CompressionManager):
         if "codec" in pipe and (self.config.codec_config or {}).get("codec_type", "nvcomp") not in (
                 "bitpack", "rans", "nvcomp", "lc"):
             return False
-        return dtype == torch.bfloat16 and supported_geometry(H, D)
+        return dtype == torch.bfloat16 and supported_geometry(H, D, self._settings()[3])
 
     def _axes(self):
         return (self.quantizer.axis_key, self.quantizer.axis_value)

@@ -3,8 +3,8 @@
 transform: y = bf16(FWHT_fp32(x * s) / sqrt(c));  inverse: x = bf16(FWHT_fp32(y) / sqrt(c)) * s,
 per power-of-two chunk c of head_dim (descending, :50-103; c = D for a power of two), with
 Rademacher signs s from a CPU torch.Generator seeded base_seed ^ (layer << 16) ^ head
-(:33-48, :137-152).  The transform itself runs in the kvmi_hadamard kernel; head_dim is a
-multiple of 16 up to 256.
+(:33-48, :137-152).  The transform itself runs in the kvmi_hadamard kernel; head_dim is
+even, up to 256 (chunks below 16 channels included: 100 = 64 + 32 + 4).
 """
 
 from __future__ import annotations

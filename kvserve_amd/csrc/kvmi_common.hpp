@@ -125,8 +125,11 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
   if (!geom || num_jobs < 0 || max_blocks < 0) return KVMI_EINVAL;
   const int S = geom->block_size, H = geom->num_heads, D = geom->head_dim, bits = geom->bits;
   if (S < 1 || H < 1 || H > kMaxHeads) return KVMI_EINVAL;
-  if (D < 16 || D > 256 || D % 16 || H * next_pow2(D) > kMaxRowSlots) return KVMI_EINVAL;
-  if (bits < 1 || bits > 8) return KVMI_EINVAL;
+  // D even up to 256; below 16 or not a multiple of 16 its power-of-two chunks go below
+  // one 16-channel lane (the row kernels' SM variants), and every packed row must then
+  // still be whole bytes (D * bits a multiple of 8)
+  if (D < 2 || D > 256 || D % 2 || H * next_pow2(D) > kMaxRowSlots) return KVMI_EINVAL;
+  if (bits < 1 || bits > 8 || (D * bits) % 8) return KVMI_EINVAL;
   if (geom->max_groups < 1 || geom->max_groups > H) return KVMI_EINVAL;
   if ((geom->flags & KVMI_F_NO_HEADER) && bits != 8) return KVMI_EINVAL;
   if (geom->flags & ~(KVMI_F_NO_TRANSFORM | KVMI_F_NATIVE_LAYOUT | KVMI_F_NO_HEADER | KVMI_F_VALU_FWHT |
@@ -151,10 +154,10 @@ inline int check_geo(const kvmi_geometry* geom, int32_t num_jobs, int32_t max_bl
 //    multiple of 32, unless the caller forces the register FWHT (KVMI_F_VALU_FWHT);
 //  * quad-per-row register FWHT (kvmi_codec.hip): D in {64, 128}, H dividing 128,
 //    H <= 16;
-//  * generic rows (kvmi_rows.hip): every other geometry check_geo admits (D a
-//    multiple of 16 up to 256, split into power-of-two chunks when it is not one;
-//    H up to 64), every non-default quantization axis, and any geometry when the
-//    caller forces them (KVMI_F_ROW_FWHT).
+//  * generic rows (kvmi_rows.hip): every other geometry check_geo admits (D even up
+//    to 256 with whole-byte packed rows, split into power-of-two chunks when it is not
+//    one, chunks below 16 channels included; H up to 64), every non-default
+//    quantization axis, and any geometry when the caller forces them (KVMI_F_ROW_FWHT).
 inline bool mfma_eligible(const Geo& g) {
   // The encoder writes each stream run (32/H tokens of one head) in 16-byte pieces, so
   // a run's packed bytes (32/H) * D * bits / 8 must be a multiple of 16: at 32 heads

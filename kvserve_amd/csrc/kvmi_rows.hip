@@ -7,8 +7,18 @@
 // transformed on its own with scale 1/sqrt(chunk).
 //
 // Row mapping.  A row (one token x one KV head, D contiguous bf16) is held by LPR =
-// next_pow2(D/16) lanes, lane `sub` owning the 16 contiguous channels [16 sub, 16 sub
-// + 16); lanes with 16 sub >= D only pad the row.  A workgroup of 512 threads holds
+// next_pow2(ceil(D/16)) lanes, lane `sub` owning the 16 contiguous channels [16 sub,
+// 16 sub + 16); lanes with 16 sub >= D only pad the row.
+//
+// D not a multiple of 16 (the SM variants, D even and D * bits a multiple of 8): D's
+// chunks below 16 channels (8, 4, 2, 1: its low four bits, descending) all sit in the
+// last, partial lane from its first channel on, each at an offset that is a multiple of
+// its size (hadamard_func.py:63-64: 100 = 64 + 32 + 4).  That lane runs only the
+// in-lane stages that stay inside an element's chunk, scales each element by its own
+// chunk's 1/sqrt(c) and treats the channels past D as padding (never loaded, stored or
+// counted in statistics).  Rows are then only 4-byte aligned in the caches (200 bytes
+// at D = 100) and whole bytes but not words in the stream (50 bytes at 4 bits), so the
+// SM variants move bf16 in 4-byte pieces and packed symbols byte by byte.  A workgroup of 512 threads holds
 // P = 512 / LPR row slots and processes RP = floor(P / H) * H rows per pass (whole
 // tokens), so slot i always sees head i % H: its signs, its K statistics and its K
 // quantization constants stay in registers across passes.  A chunk of c channels
@@ -29,19 +39,22 @@ namespace {
 constexpr int kRWG = 512;  // threads per workgroup
 constexpr int kSeg = 16;   // channels per lane
 
-// fp32 values of 1/sqrt(c) for c = 16, 32, .., 256 (computed in double on the host and
-// rounded once, as the reference passes the Python float 1/sqrt(size)).
+// fp32 values of 1/sqrt(c) for c = 1, 2, 4, .., 256 (index log2 c; computed in double
+// on the host and rounded once, as the reference passes the Python float 1/sqrt(size)).
 struct ChunkScales {
-  float s[5];
+  float s[9];
 };
 
 // A lane's place in its row: segment, whether it holds channels, and the chunk that
-// contains them (lanes of the chunk, scale).
+// contains them (lanes of the chunk, scale); `nvalid` channels of the segment are
+// inside the row (16 but in the partial lane of a D with D % 16 != 0).
 struct Lane {
   int slot, sub;
   bool seg_ok;
   int chunk_lanes;
   float scale;
+  int nvalid;
+  bool partial;
 };
 
 template <int LPR>
@@ -51,8 +64,10 @@ __device__ __forceinline__ Lane lane_of(int D, const ChunkScales& cs) {
   l.sub = threadIdx.x % LPR;
   const int c0 = l.sub * kSeg;
   l.seg_ok = c0 < D;
+  l.nvalid = min(max(D - c0, 0), kSeg);
+  l.partial = l.nvalid > 0 && l.nvalid < kSeg;
   l.chunk_lanes = 1;
-  l.scale = cs.s[0];
+  l.scale = cs.s[4];
   int start = 0;  // first channel of the chunk of size c (chunks descend, as D's bits)
 #pragma unroll
   for (int b = 8; b >= 4; --b) {
@@ -60,7 +75,7 @@ __device__ __forceinline__ Lane lane_of(int D, const ChunkScales& cs) {
     if (!(D & c)) continue;
     if (c0 >= start && c0 < start + c) {
       l.chunk_lanes = c / kSeg;
-      l.scale = cs.s[b - 4];
+      l.scale = cs.s[b];
     }
     start += c;
   }
@@ -84,10 +99,79 @@ __device__ __forceinline__ void cross_stages(float (&v)[kSeg], int sub, int chun
   }
 }
 
-template <int LPR>
-__device__ __forceinline__ void fwht_seg(float (&v)[kSeg], const Lane& l) {
-  fwht_in_lane<kSeg>(v);
+// Size of the chunk below 16 channels that holds element i of the partial lane (0 for
+// padding): the chunks are the set bits of low = D % 16, descending, from element 0.
+__device__ __forceinline__ int small_chunk(int i, int low) {
+  int start = 0;
+#pragma unroll
+  for (int b = 3; b >= 0; --b) {
+    const int c = 1 << b;
+    if (!(low & c)) continue;
+    if (i >= start && i < start + c) return c;
+    start += c;
+  }
+  return 0;
+}
+// The scale of element i: its chunk's, which differs per element only in the partial lane.
+template <bool SM>
+__device__ __forceinline__ float elem_scale(const Lane& l, int i, int D, const ChunkScales& cs) {
+  if constexpr (!SM) return l.scale;
+  const int c = small_chunk(i, D & (kSeg - 1));  // wave-uniform
+  return l.partial ? cs.s[c ? __builtin_ctz((unsigned)c) : 0] : l.scale;
+}
+
+template <int LPR, bool SM = false>
+__device__ __forceinline__ void fwht_seg(float (&v)[kSeg], const Lane& l, int D = 0) {
+  if constexpr (SM) {
+    // in-lane stages, in the partial lane only inside an element's own chunk (a chunk is
+    // aligned to its size, so i and i + h share it when its size exceeds h)
+    const int low = D & (kSeg - 1);
+#pragma unroll
+    for (int h = 1; h < kSeg; h <<= 1) {
+#pragma unroll
+      for (int i = 0; i < kSeg; ++i) {
+        if (!(i & h)) {
+          const bool on = !l.partial || small_chunk(i, low) > h;
+          const float a = v[i], b = v[i + h];
+          v[i] = on ? a + b : a;
+          v[i + h] = on ? a - b : b;
+        }
+      }
+    }
+  } else {
+    fwht_in_lane<kSeg>(v);
+  }
   cross_stages<1, LPR>(v, l.sub, l.chunk_lanes);
+}
+
+// bf16 segments and packed symbols of the SM variants: 4-byte pieces of the lane's
+// `nvalid` channels (D is even), and the packed bytes one at a time.
+__device__ __forceinline__ void load_bf16_n(const uint16_t* __restrict__ p, int nvalid, uint32_t (&w)[kSeg / 2]) {
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+  for (int i = 0; i < kSeg / 2; ++i) w[i] = 2 * i < nvalid ? gld(q + i) : 0u;
+}
+__device__ __forceinline__ void store_bf16_n(uint16_t* __restrict__ p, int nvalid, const uint32_t (&w)[kSeg / 2]) {
+  uint32_t* q = reinterpret_cast<uint32_t*>(p);
+#pragma unroll
+  for (int i = 0; i < kSeg / 2; ++i)
+    if (2 * i < nvalid) gst(q + i, w[i]);
+}
+template <int BITS>
+__device__ __forceinline__ void store_packed_n(uint8_t* __restrict__ p, int nvalid, const Packed<kSeg, BITS>& v) {
+  const int nb = nvalid * BITS / 8;
+#pragma unroll
+  for (int k = 0; k < Packed<kSeg, BITS>::kBytes; ++k)
+    if (k < nb) gst(p + k, (uint8_t)(v.w[k / 4] >> (8 * (k % 4))));
+}
+template <int BITS>
+__device__ __forceinline__ void load_packed_n(const uint8_t* __restrict__ p, int nvalid, Packed<kSeg, BITS>& v) {
+  const int nb = nvalid * BITS / 8;
+#pragma unroll
+  for (int i = 0; i < Packed<kSeg, BITS>::kWords; ++i) v.w[i] = 0u;
+#pragma unroll
+  for (int k = 0; k < Packed<kSeg, BITS>::kBytes; ++k)
+    if (k < nb) v.w[k / 4] |= (uint32_t)gld(p + k) << (8 * (k % 4));
 }
 
 template <int LPR>
@@ -116,12 +200,15 @@ __device__ __forceinline__ uint32_t seg_signs(const uint32_t* signs, int h, int 
 
 // Load the lane's 16 channels, apply signs + chunked FWHT + scale (unless transform
 // is off) and return fp32 values (ROUND: rounded to bf16).  Padding lanes load nothing.
-template <int LPR, bool ROUND>
+template <int LPR, bool ROUND, bool SM>
 __device__ __forceinline__ void load_transform(const uint16_t* src, const Lane& l, uint32_t sb, bool transform,
-                                               float (&y)[kSeg]) {
+                                               float (&y)[kSeg], int D, const ChunkScales& cs) {
   uint32_t w[kSeg / 2];
   if (l.seg_ok) {
-    load_bf16_seg<kSeg>(src, w);
+    if constexpr (SM)
+      load_bf16_n(src, l.nvalid, w);
+    else
+      load_bf16_seg<kSeg>(src, w);
   } else {
 #pragma unroll
     for (int i = 0; i < kSeg / 2; ++i) w[i] = 0u;
@@ -129,10 +216,18 @@ __device__ __forceinline__ void load_transform(const uint16_t* src, const Lane& 
   if (transform) apply_sign_bf16<kSeg>(w, sb);
   unpack_bf16<kSeg>(w, y);
   if (transform) {
-    fwht_seg<LPR>(y, l);
+    fwht_seg<LPR, SM>(y, l, D);
 #pragma unroll
-    for (int i = 0; i < kSeg; ++i) y[i] = ROUND ? round_bf16(y[i] * l.scale) : y[i] * l.scale;
+    for (int i = 0; i < kSeg; ++i) {
+      const float sc = elem_scale<SM>(l, i, D, cs);
+      y[i] = ROUND ? round_bf16(y[i] * sc) : y[i] * sc;
+    }
   }
+}
+// Element i of the lane is a channel of the row (all 16 unless SM and the partial lane).
+template <bool SM>
+__device__ __forceinline__ bool elem_ok(const Lane& l, int i) {
+  return SM ? i < l.nvalid : l.seg_ok;
 }
 
 struct Pass {
@@ -191,14 +286,22 @@ __device__ __forceinline__ int group_count(const Profile& p, int H) {
 
 // The lane's quantization constants of a channel- or tensor-axis part: (min, x) per
 // channel, x = 1/scale (encode) or scale (decode).
-template <bool RCP>
+template <bool RCP, bool SM>
 __device__ __forceinline__ void part_consts(const Geo& g, const PartCtx& c, const Lane& l, float (&mn)[kSeg],
                                             float (&x)[kSeg]) {
   if (c.axis == kAxChannel) {
     const int HD = g.H * g.D, e0 = l.seg_ok ? l.sub * kSeg : 0;
     uint32_t wm[kSeg / 2], ws[kSeg / 2];
-    load_bf16_seg<kSeg>(c.meta + c.j * g.D + e0, wm);
-    load_bf16_seg<kSeg>(c.meta + HD + c.j * g.D + e0, ws);
+    if constexpr (SM) {  // padding channels: (0, 1)
+      load_bf16_n(c.meta + c.j * g.D + e0, l.nvalid, wm);
+      load_bf16_n(c.meta + HD + c.j * g.D + e0, l.nvalid, ws);
+#pragma unroll
+      for (int i = 0; i < kSeg / 2; ++i)
+        if (2 * i >= l.nvalid) ws[i] = 0x3F803F80u;
+    } else {
+      load_bf16_seg<kSeg>(c.meta + c.j * g.D + e0, wm);
+      load_bf16_seg<kSeg>(c.meta + HD + c.j * g.D + e0, ws);
+    }
     unpack_bf16<kSeg>(wm, mn);
     unpack_bf16<kSeg>(ws, x);
   } else if (c.axis == kAxTensor) {
@@ -222,7 +325,7 @@ __device__ __forceinline__ void part_consts(const Geo& g, const PartCtx& c, cons
 // Pass 1 of compress for every part on the channel or tensor axis: min / max over all
 // tokens of the job, per (head, channel) or per group, reduced through LDS atomics and
 // then global atomics on order-preserving keys (part p at kstats + p * 2*H*D).
-template <int LPR>
+template <int LPR, bool SM>
 __global__ __launch_bounds__(kRWG) void rows_stats_kernel(Geo g, ChunkScales cs,
                                                           const kvmi_layer_job* __restrict__ jobs) {
   extern __shared__ uint32_t lkey[];  // [2][H*D]: min keys, then max keys (one part at a time)
@@ -256,10 +359,11 @@ __global__ __launch_bounds__(kRWG) void rows_stats_kernel(Geo g, ChunkScales cs,
       const RowPos rp = row_pos(job, blk0, rows, r0 + l.slot, S, H);
       if (ps.on && rp.active) {
         float y[kSeg];
-        load_transform<LPR, false>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
+        load_transform<LPR, false, SM>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y, D, cs);
         any = true;
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
+          if (SM && i >= l.nvalid) continue;  // padding channels
           mn[i] = fminf(mn[i], y[i]);
           mx[i] = fmaxf(mx[i], y[i]);
         }
@@ -279,7 +383,9 @@ __global__ __launch_bounds__(kRWG) void rows_stats_kernel(Geo g, ChunkScales cs,
         const int seg = (ps.h * D) / kSeg + l.sub;
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
-          const int slot = seg * kSeg + ((i + seg) & (kSeg - 1));
+          if (SM && i >= l.nvalid) continue;
+          // SM: rows are not whole segments, so keys sit at their channel index
+          const int slot = SM ? ps.h * D + l.sub * kSeg + i : seg * kSeg + ((i + seg) & (kSeg - 1));
           atomicMin(&lkey[slot], f2key(mn[i]));
           atomicMax(&lkey[HD + slot], f2key(mx[i]));
         }
@@ -289,6 +395,7 @@ __global__ __launch_bounds__(kRWG) void rows_stats_kernel(Geo g, ChunkScales cs,
       if (l.seg_ok) {
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
+          if (SM && i >= l.nvalid) continue;
           a = fminf(a, mn[i]);
           b = fmaxf(b, mx[i]);
         }
@@ -307,7 +414,7 @@ __global__ __launch_bounds__(kRWG) void rows_stats_kernel(Geo g, ChunkScales cs,
     __syncthreads();
     uint32_t* keys = job.kstats + part * 2 * HD;
     for (int i = threadIdx.x; i < nkeys; i += kRWG) {
-      const int slot = axis == kAxChannel ? (i / kSeg) * kSeg + ((i + i / kSeg) & (kSeg - 1)) : i;
+      const int slot = axis == kAxChannel && !SM ? (i / kSeg) * kSeg + ((i + i / kSeg) & (kSeg - 1)) : i;
       const uint32_t kmn = lkey[slot], kmx = lkey[HD + slot];
       if (kmn != 0xffffffffu) atomicMin(&keys[i], kmn);
       if (kmx != 0u) atomicMax(&keys[HD + i], kmx);
@@ -368,7 +475,7 @@ __global__ __launch_bounds__(kRWG) void rows_finalize_kernel(Geo g, const kvmi_l
 // Per-token statistics of one part over the heads of each group (token axis): row
 // min / max -> LDS, then one thread per (token of the pass, group) forms (min, 1/scale)
 // and writes the part's token table.  Every thread of the workgroup calls this.
-template <int LPR>
+template <int LPR, bool SM>
 __device__ __forceinline__ float2 token_stats(const Geo& g, const kvmi_layer_job& job, const PartCtx& c,
                                               const Lane& l, const Pass& ps, const float (&y)[kSeg], bool act,
                                               int64_t r0, int64_t rows, int blk0, int ngroups, float2* rowmm,
@@ -379,6 +486,7 @@ __device__ __forceinline__ float2 token_stats(const Geo& g, const kvmi_layer_job
     if (l.seg_ok) {
 #pragma unroll
       for (int i = 0; i < kSeg; ++i) {
+        if (SM && i >= l.nvalid) continue;
         lmn = fminf(lmn, y[i]);
         lmx = fmaxf(lmx, y[i]);
       }
@@ -417,7 +525,7 @@ __device__ __forceinline__ float2 token_stats(const Geo& g, const kvmi_layer_job
   return q;
 }
 
-template <int LPR, int BITS>
+template <int LPR, int BITS, bool SM>
 __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs,
                                                            const kvmi_layer_job* __restrict__ jobs,
                                                            int32_t* __restrict__ err) {
@@ -453,7 +561,7 @@ __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs
 #pragma unroll
   for (int part = 0; part < 2; ++part) {
     ctx[part] = part_ctx(g, job, part, pos[part], ps.h);
-    part_consts<true>(g, ctx[part], l, cmn[part], crc[part]);
+    part_consts<true, SM>(g, ctx[part], l, cmn[part], crc[part]);
     ngroups[part] = group_count(ctx[part].prof, H);
   }
   uint32_t over = 0;
@@ -466,9 +574,10 @@ __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs
       const PartCtx& c = ctx[part];
       const uint16_t* pool = reinterpret_cast<const uint16_t*>(job.pool) + part * job.pool_part_stride;
       float y[kSeg];
-      if (act) load_transform<LPR, true>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y);
+      if (act) load_transform<LPR, true, SM>(pool + rp.pool_row * D + l.sub * kSeg, l, sb, transform, y, D, cs);
       if (c.axis == kAxToken) {  // uniform over the workgroup
-        const float2 q = token_stats<LPR>(g, job, c, l, ps, y, act, r0, rows, blk0, ngroups[part], rowmm, tokq);
+        const float2 q =
+            token_stats<LPR, SM>(g, job, c, l, ps, y, act, r0, rows, blk0, ngroups[part], rowmm, tokq);
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
           cmn[part][i] = q.x;
@@ -480,11 +589,14 @@ __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs
 #pragma unroll
         for (int i = 0; i < kSeg; ++i) {
           s[i] = (uint32_t)quant_value(y[i], cmn[part][i], crc[part][i], c.level);
-          over |= s[i];
+          if (!SM || i < l.nvalid) over |= s[i];  // padding symbols are not stored
         }
         Packed<kSeg, BITS> pkd;
         pack_syms<kSeg, BITS>(s, pkd);
-        store_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), pkd);
+        if constexpr (SM)
+          store_packed_n<BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), l.nvalid, pkd);
+        else
+          store_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), pkd);
       }
     }
   }
@@ -492,7 +604,7 @@ __global__ __launch_bounds__(kRWG) void rows_encode_kernel(Geo g, ChunkScales cs
 }
 
 // ============================================================== decode
-template <int LPR, int BITS>
+template <int LPR, int BITS, bool SM>
 __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs,
                                                            const kvmi_layer_job* __restrict__ jobs,
                                                            int32_t* __restrict__ err) {
@@ -526,7 +638,7 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
 #pragma unroll
   for (int part = 0; part < 2; ++part) {
     ctx[part] = part_ctx(g, job, part, pos[part], ps.h);
-    part_consts<false>(g, ctx[part], l, cmn[part], csc[part]);
+    part_consts<false, SM>(g, ctx[part], l, cmn[part], csc[part]);
   }
   const int64_t ntok = (int64_t)B * S;
 
@@ -539,7 +651,10 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
       uint32_t s[kSeg];
       if (l.seg_ok) {
         Packed<kSeg, BITS> pkd;
-        load_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), pkd);
+        if constexpr (SM)
+          load_packed_n<BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), l.nvalid, pkd);
+        else
+          load_packed<kSeg, BITS>(seg_addr<BITS>(job, g, part, c.j, rp.tok, l.sub * kSeg), pkd);
         unpack_syms<kSeg, BITS>(pkd, s);
       } else {
 #pragma unroll
@@ -557,18 +672,23 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
       }
       uint32_t w[kSeg / 2];
       if (transform) {
-        fwht_seg<LPR>(x, l);
+        fwht_seg<LPR, SM>(x, l, D);
 #pragma unroll
-        for (int i = 0; i < kSeg / 2; ++i) w[i] = pack_bf16x2(x[2 * i] * l.scale, x[2 * i + 1] * l.scale);
+        for (int i = 0; i < kSeg / 2; ++i)
+          w[i] = pack_bf16x2(x[2 * i] * elem_scale<SM>(l, 2 * i, D, cs), x[2 * i + 1] * elem_scale<SM>(l, 2 * i + 1, D, cs));
         apply_sign_bf16<kSeg>(w, sb);
       } else {
 #pragma unroll
         for (int i = 0; i < kSeg / 2; ++i) w[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
       }
-      if (l.seg_ok)
-        store_bf16_seg<kSeg>(reinterpret_cast<uint16_t*>(job.pool) + part * job.pool_part_stride +
-                                 rp.pool_row * D + l.sub * kSeg,
-                             w);
+      uint16_t* dst = reinterpret_cast<uint16_t*>(job.pool) + part * job.pool_part_stride + rp.pool_row * D +
+                      l.sub * kSeg;
+      if (l.seg_ok) {
+        if constexpr (SM)
+          store_bf16_n(dst, l.nvalid, w);
+        else
+          store_bf16_seg<kSeg>(dst, w);
+      }
     }
   }
 }
@@ -576,7 +696,7 @@ __global__ __launch_bounds__(kRWG) void rows_decode_kernel(Geo g, ChunkScales cs
 // ============================================================== unit transform
 // Contiguous rows [rows, D], row r of head r % H: forward = signs then chunked FWHT,
 // inverse = chunked FWHT then signs (hadamard_func.py:161-231).  One row per LPR lanes.
-template <int LPR>
+template <int LPR, bool SM>
 __global__ __launch_bounds__(kRWG) void rows_hadamard_kernel(const uint16_t* __restrict__ in,
                                                              uint16_t* __restrict__ out, int64_t rows, int H, int D,
                                                              const uint32_t* __restrict__ signs, int inverse,
@@ -587,7 +707,10 @@ __global__ __launch_bounds__(kRWG) void rows_hadamard_kernel(const uint16_t* __r
   const uint32_t sb = seg_signs(signs, (int)(r % H), D, l);
   uint32_t w[kSeg / 2];
   if (l.seg_ok) {
-    load_bf16_seg<kSeg>(in + r * D + l.sub * kSeg, w);
+    if constexpr (SM)
+      load_bf16_n(in + r * D + l.sub * kSeg, l.nvalid, w);
+    else
+      load_bf16_seg<kSeg>(in + r * D + l.sub * kSeg, w);
   } else {
 #pragma unroll
     for (int i = 0; i < kSeg / 2; ++i) w[i] = 0u;
@@ -595,41 +718,59 @@ __global__ __launch_bounds__(kRWG) void rows_hadamard_kernel(const uint16_t* __r
   if (!inverse) apply_sign_bf16<kSeg>(w, sb);
   float v[kSeg];
   unpack_bf16<kSeg>(w, v);
-  fwht_seg<LPR>(v, l);
+  fwht_seg<LPR, SM>(v, l, D);
 #pragma unroll
-  for (int i = 0; i < kSeg / 2; ++i) w[i] = pack_bf16x2(v[2 * i] * l.scale, v[2 * i + 1] * l.scale);
+  for (int i = 0; i < kSeg / 2; ++i)
+    w[i] = pack_bf16x2(v[2 * i] * elem_scale<SM>(l, 2 * i, D, cs), v[2 * i + 1] * elem_scale<SM>(l, 2 * i + 1, D, cs));
   if (inverse) apply_sign_bf16<kSeg>(w, sb);
-  if (l.seg_ok) store_bf16_seg<kSeg>(out + r * D + l.sub * kSeg, w);
+  if (l.seg_ok) {
+    if constexpr (SM)
+      store_bf16_n(out + r * D + l.sub * kSeg, l.nvalid, w);
+    else
+      store_bf16_seg<kSeg>(out + r * D + l.sub * kSeg, w);
+  }
 }
 
 // ============================================================== host side
 ChunkScales chunk_scales() {
   ChunkScales cs;
-  for (int b = 4; b <= 8; ++b) cs.s[b - 4] = (float)(1.0 / __builtin_sqrt((double)(1 << b)));
+  for (int b = 0; b <= 8; ++b) cs.s[b] = (float)(1.0 / __builtin_sqrt((double)(1 << b)));
   return cs;
 }
+// lanes per row: next_pow2(ceil(D / 16))
+int row_lanes(int D) { return next_pow2((D + kSeg - 1) / kSeg); }
 
 // Blocks per workgroup: enough for one pass of whole tokens; kstats also caps a job
 // at ~16 workgroups, which keeps the global atomics per channel few.
-int rows_per_pass(const Geo& g) { return (kRWG / next_pow2(g.D / kSeg) / g.H) * g.H; }
+int rows_per_pass(const Geo& g) { return (kRWG / row_lanes(g.D) / g.H) * g.H; }
 void set_rows_bpw(Geo* g, int32_t max_blocks, bool stats) {
   const int rpb = g->S * g->H, rp = rows_per_pass(*g);
   g->bpw = rpb >= rp ? 1 : (rp + rpb - 1) / rpb;
   if (stats) g->bpw = max(g->bpw, (max_blocks + 15) / 16);
 }
 
+// The SM variants (D % 16 != 0) are separate instantiations, so the others keep their code.
 template <int LPR>
 void launch_stats(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, hipStream_t st) {
   const size_t lds = (size_t)2 * g.H * g.D * sizeof(uint32_t);
-  hipLaunchKernelGGL((rows_stats_kernel<LPR>), grid, dim3(kRWG), lds, st, g, chunk_scales(), jobs);
+  if (g.D % kSeg)
+    hipLaunchKernelGGL((rows_stats_kernel<LPR, true>), grid, dim3(kRWG), lds, st, g, chunk_scales(), jobs);
+  else
+    hipLaunchKernelGGL((rows_stats_kernel<LPR, false>), grid, dim3(kRWG), lds, st, g, chunk_scales(), jobs);
 }
 template <int LPR, int BITS>
 void launch_encode(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
-  hipLaunchKernelGGL((rows_encode_kernel<LPR, BITS>), grid, dim3(kRWG), 0, st, g, chunk_scales(), jobs, err);
+  if (g.D % kSeg)
+    hipLaunchKernelGGL((rows_encode_kernel<LPR, BITS, true>), grid, dim3(kRWG), 0, st, g, chunk_scales(), jobs, err);
+  else
+    hipLaunchKernelGGL((rows_encode_kernel<LPR, BITS, false>), grid, dim3(kRWG), 0, st, g, chunk_scales(), jobs, err);
 }
 template <int LPR, int BITS>
 void launch_decode(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
-  hipLaunchKernelGGL((rows_decode_kernel<LPR, BITS>), grid, dim3(kRWG), 0, st, g, chunk_scales(), jobs, err);
+  if (g.D % kSeg)
+    hipLaunchKernelGGL((rows_decode_kernel<LPR, BITS, true>), grid, dim3(kRWG), 0, st, g, chunk_scales(), jobs, err);
+  else
+    hipLaunchKernelGGL((rows_decode_kernel<LPR, BITS, false>), grid, dim3(kRWG), 0, st, g, chunk_scales(), jobs, err);
 }
 
 template <template <int, int> class F, int LPR>
@@ -663,7 +804,7 @@ struct Dec {
 
 template <template <int, int> class F>
 void by_lanes(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err, hipStream_t st) {
-  switch (next_pow2(g.D / kSeg)) {
+  switch (row_lanes(g.D)) {
     case 1: ByBits<F, 1>::run(g.bits, g, grid, jobs, err, st); break;
     case 2: ByBits<F, 2>::run(g.bits, g, grid, jobs, err, st); break;
     case 4: ByBits<F, 4>::run(g.bits, g, grid, jobs, err, st); break;
@@ -672,11 +813,20 @@ void by_lanes(const Geo& g, dim3 grid, const kvmi_layer_job* jobs, int32_t* err,
   }
 }
 
+template <int LPR>
+void launch_hadamard(dim3 gr, dim3 bl, hipStream_t st, const uint16_t* i16, uint16_t* o16, int64_t rows, int H, int D,
+                     const uint32_t* signs, int inverse, const ChunkScales& cs) {
+  if (D % kSeg)
+    hipLaunchKernelGGL((rows_hadamard_kernel<LPR, true>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs);
+  else
+    hipLaunchKernelGGL((rows_hadamard_kernel<LPR, false>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs);
+}
+
 }  // namespace
 
 int rows_hadamard(const void* in, void* out, int64_t rows, int32_t H, int32_t D, const uint32_t* signs,
                   int32_t inverse, hipStream_t st) {
-  const int lpr = next_pow2(D / kSeg);
+  const int lpr = row_lanes(D);
   const int64_t grid = (rows + kRWG / lpr - 1) / (kRWG / lpr);
   if (grid > 0x7fffffffLL) return KVMI_EINVAL;
   const uint16_t* i16 = static_cast<const uint16_t*>(in);
@@ -684,11 +834,11 @@ int rows_hadamard(const void* in, void* out, int64_t rows, int32_t H, int32_t D,
   const dim3 gr((unsigned)grid), bl(kRWG);
   const ChunkScales cs = chunk_scales();
   switch (lpr) {
-    case 1: hipLaunchKernelGGL((rows_hadamard_kernel<1>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs); break;
-    case 2: hipLaunchKernelGGL((rows_hadamard_kernel<2>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs); break;
-    case 4: hipLaunchKernelGGL((rows_hadamard_kernel<4>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs); break;
-    case 8: hipLaunchKernelGGL((rows_hadamard_kernel<8>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs); break;
-    default: hipLaunchKernelGGL((rows_hadamard_kernel<16>), gr, bl, 0, st, i16, o16, rows, H, D, signs, inverse, cs); break;
+    case 1: launch_hadamard<1>(gr, bl, st, i16, o16, rows, H, D, signs, inverse, cs); break;
+    case 2: launch_hadamard<2>(gr, bl, st, i16, o16, rows, H, D, signs, inverse, cs); break;
+    case 4: launch_hadamard<4>(gr, bl, st, i16, o16, rows, H, D, signs, inverse, cs); break;
+    case 8: launch_hadamard<8>(gr, bl, st, i16, o16, rows, H, D, signs, inverse, cs); break;
+    default: launch_hadamard<16>(gr, bl, st, i16, o16, rows, H, D, signs, inverse, cs); break;
   }
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
 }
@@ -699,7 +849,7 @@ int rows_kstats(const Geo& g0, const kvmi_layer_job* jobs, int32_t num_jobs, int
   set_rows_bpw(&g, max_blocks, true);
   const dim3 grid((unsigned)((max_blocks + g.bpw - 1) / g.bpw), (unsigned)num_jobs);
   if (part_axis(g.flags, 0) == kAxToken && part_axis(g.flags, 1) == kAxToken) return KVMI_OK;  // nothing to reduce
-  switch (next_pow2(g.D / kSeg)) {
+  switch (row_lanes(g.D)) {
     case 1: launch_stats<1>(g, grid, jobs, st); break;
     case 2: launch_stats<2>(g, grid, jobs, st); break;
     case 4: launch_stats<4>(g, grid, jobs, st); break;

@@ -149,7 +149,7 @@ extern "C" int kvmi_check_block_ids(kvmi_layer_job* jobs, int32_t num_jobs, int3
 extern "C" int kvmi_hadamard(const void* in, void* out, int64_t rows, int32_t num_heads, int32_t head_dim,
                              const uint32_t* signs, int32_t inverse, kvmi_stream_t stream) {
   using namespace kvmi;
-  if (rows < 0 || num_heads < 1 || head_dim < 16 || head_dim > 256 || head_dim % 16) return KVMI_EINVAL;
+  if (rows < 0 || num_heads < 1 || head_dim < 2 || head_dim > 256 || head_dim % 2) return KVMI_EINVAL;
   if (rows == 0) return KVMI_OK;
   if (!in || !out || !signs) return KVMI_EINVAL;
   if ((uintptr_t)in % 16 || (uintptr_t)out % 16) return KVMI_EINVAL;

@@ -29,7 +29,7 @@ from .profiles import LayerProfile, rademacher_sign_bits
 
 CHUNK_THRESHOLD_BYTES = 500 * 1024 * 1024  # compression_manager.py:230-231
 CHUNK_LAYERS = 8                             # compression_manager.py:235
-DEFAULT_SEED = 0x3333                        # kvserve_transformer.py:253
+DEFAULT_SEED = 0x3333                        # kvserve_transformer.py:22
 
 
 def chunk_ranges(num_layers: int, raw_bytes: int, chunk_layers: int = CHUNK_LAYERS) -> List[Tuple[int, int]]:
@@ -126,21 +126,26 @@ MAX_HEADS = 64        # kvmi_common.hpp kMaxHeads
 MAX_ROW_SLOTS = 8192  # kvmi_common.hpp kMaxRowSlots: H * next_pow2(D)
 
 
-def supported_geometry(num_heads: int, head_dim: int) -> bool:
-    """The geometries the paged kernels take (kvmi_common.hpp check_geo): head_dim a
-    multiple of 16 in [16, 256] (split into power-of-two chunks when it is not one,
-    hadamard_func.py:50-103), 1..64 heads, and heads * next_pow2(head_dim) <= 8192."""
+def supported_geometry(num_heads: int, head_dim: int, bits: Optional[int] = None) -> bool:
+    """The geometries the paged kernels take (kvmi_common.hpp check_geo): head_dim even
+    in [2, 256] (split into power-of-two chunks when it is not one, hadamard_func.py:50-103,
+    chunks below 16 channels included), 1..64 heads, heads * next_pow2(head_dim) <= 8192,
+    and with a symbol width: whole-byte packed rows (head_dim * bits a multiple of 8)."""
     if type(num_heads) is not int or type(head_dim) is not int:
         return False
-    if not 1 <= num_heads <= MAX_HEADS or not 16 <= head_dim <= 256 or head_dim % 16:
+    if not 1 <= num_heads <= MAX_HEADS or not 2 <= head_dim <= 256 or head_dim % 2:
+        return False
+    if bits is not None and (head_dim * bits) % 8:
         return False
     return num_heads * (1 << (head_dim - 1).bit_length()) <= MAX_ROW_SLOTS
 
 
-def check_geometry(num_heads: int, head_dim: int) -> None:
-    if not supported_geometry(num_heads, head_dim):
-        raise ValueError(f"unsupported geometry: {num_heads} heads of head_dim {head_dim} (head_dim a multiple "
-                         f"of 16 in [16, 256], 1..{MAX_HEADS} heads, heads * next_pow2(head_dim) <= {MAX_ROW_SLOTS})")
+def check_geometry(num_heads: int, head_dim: int, bits: Optional[int] = None) -> None:
+    if not supported_geometry(num_heads, head_dim, bits):
+        raise ValueError(f"unsupported geometry: {num_heads} heads of head_dim {head_dim}"
+                         + (f" at {bits} bits" if bits is not None else "")
+                         + f" (head_dim even in [2, 256], 1..{MAX_HEADS} heads, heads * next_pow2(head_dim) <= "
+                         f"{MAX_ROW_SLOTS}, head_dim * bits a multiple of 8)")
 
 
 class FusedKVCodec:
@@ -148,7 +153,7 @@ class FusedKVCodec:
 
     Parameters mirror the reference's configuration keys:
       bits       codec_config.bitpack_bits (bitpack_codec.py:87-91)
-      seed       transformer_config.seed (kvserve_transformer.py:253)
+      seed       transformer_config.seed (kvserve_transformer.py:22)
       transform  "transformer" in the pipeline
       layout     KVSERVE_CODEC_LAYOUT permuted|native (compression_manager.py:136-140)
     """
@@ -159,7 +164,7 @@ class FusedKVCodec:
                  axes: Tuple[str, str] = DEFAULT_AXES):
         if type(bits) is not int or not 1 <= bits <= 8:
             raise ValueError("bitpack_bits must be an integer in [1, 8]")
-        check_geometry(num_heads, head_dim)
+        check_geometry(num_heads, head_dim, bits)
         if layout not in ("permuted", "native"):
             raise ValueError("layout must be 'permuted' or 'native'")
         if not header and bits != 8:

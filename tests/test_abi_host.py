@@ -169,10 +169,11 @@ def test_codec_constructor_contracts():
     for bits in (0, 9, True, 3.5, None):
         with pytest.raises(ValueError, match="bitpack_bits"):
             FusedKVCodec(8, 128, 16, bits)
-    for H, D in ((8, 100), (8, 272), (65, 64), (64, 256), (0, 128)):
+    for H, D, b in ((8, 101, 4), (8, 100, 3), (8, 272, 4), (65, 64, 4), (64, 256, 4), (0, 128, 4)):
         with pytest.raises(ValueError, match="unsupported geometry"):
-            FusedKVCodec(H, D, 16, 4)
+            FusedKVCodec(H, D, 16, b)  # odd D, 37.5-byte packed rows, too wide, too many heads, none
     FusedKVCodec(6, 96, 16, 4)  # D split into power-of-two chunks, H not dividing 128
+    FusedKVCodec(8, 100, 16, 4)  # 64 + 32 + 4: a chunk below 16 channels (hadamard_func.py:63-64)
     with pytest.raises(ValueError):
         FusedKVCodec(8, 128, 16, 4, header=False)
 

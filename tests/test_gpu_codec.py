@@ -137,7 +137,8 @@ def test_gather_scatter_kv_adjacent_bit_exact(cuda, shape):
         ops.scatter_blocks(dst, got[:, :1], ids)  # not a [nb, 2, ...] payload
 
 
-@pytest.mark.parametrize("D,H", [(64, 8), (128, 8), (96, 8), (256, 4), (80, 6), (16, 3), (224, 2)])
+@pytest.mark.parametrize("D,H", [(64, 8), (128, 8), (96, 8), (256, 4), (80, 6), (16, 3), (224, 2), (100, 8), (70, 5),
+                                 (6, 3), (108, 2)])
 def test_hadamard_unit_matches_oracle(cuda, D, H):
     """Power-of-two D and D split into power-of-two chunks (hadamard_func.py:50-103):
     bit-exact with the oracle, whose chunked transform is pinned to the Sylvester

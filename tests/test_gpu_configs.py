@@ -405,6 +405,12 @@ def _geometry_vs_oracle(cuda, H, S, D, bits, layout="permuted"):
     (5, 32, 224, 5, "native"),     # D = 128 + 64 + 32
     (3, 16, 16, 8, "permuted"),    # D = 16: one lane per row
     (24, 16, 160, 6, "permuted"),  # D = 128 + 32
+    (8, 16, 100, 4, "permuted"),   # D = 64 + 32 + 4 (hadamard_func.py:63-64): a chunk inside one lane
+    (4, 16, 100, 2, "native"),     # 25-byte packed rows
+    (3, 16, 108, 8, "permuted"),   # D = 64 + 32 + 8 + 4
+    (5, 32, 70, 4, "native"),      # D = 64 + 4 + 2
+    (2, 16, 6, 4, "permuted"),     # D = 4 + 2: the whole row in one partial lane
+    (6, 16, 100, 6, "permuted"),
 ])
 def test_generic_geometries_match_oracle_exactly(cuda, H, S, D, bits, layout):
     """The generic row kernels (kvmi_rows.hip) run the oracle's FWHT stage order, so
