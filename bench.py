@@ -130,8 +130,8 @@ def hip_kernel_names(codec, S: int, H: int, D: int, bits: int, cplan=None) -> di
                  "kvmi_decode_paged": ("decode_kt_kernel<8>" if (D, bits) == (128, 4)
                                        else f"decode_mfma_kernel<{D // 32}, {bits}, 8>"),
                  "kvmi_kstats_paged": f"kstats_mfma_kernel<{D // 32}>", "finalize": "kstats_finalize_kernel"}
-        if cplan is not None and cplan.epoch.value > 0:  # the one-pass kernel ran
-            names["kvmi_compress_paged"] = f"compress_pass_kernel<{D // 32}, {bits}, false>"
+        if cplan is not None and getattr(cplan, "workspace", None) is not None:  # the one-pass kernel runs
+            names["kvmi_compress_paged"] = f"onepass_kernel<{D // 32}, {bits}, false>"
         return names
     if pow2 and H <= 16 and 128 % H == 0 and codec.fwht != "rows":  # quad-per-row register FWHT
         return {"kvmi_encode_paged": f"encode_kernel<{D}, {bits}>", "kvmi_decode_paged": f"decode_kernel<{D}, {bits}>",

@@ -53,7 +53,7 @@ extern "C" {
 /* hipStream_t without pulling in the HIP headers. */
 typedef struct ihipStream_t* kvmi_stream_t;
 
-#define KVMI_ABI_VERSION 1
+#define KVMI_ABI_VERSION 2
 
 /* Bits OR-ed into the caller's device error word. */
 #define KVMI_ERR_SYMBOL_RANGE 1 /* a symbol >= 2^bits reached the packer */
@@ -67,7 +67,6 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_EINVAL (-22)
 #define KVMI_ELAUNCH (-5)
 #define KVMI_ENOSPC (-28) /* the call needs more than a fixed scratch array holds */
-#define KVMI_ERANGE (-34) /* kvmi_compress_paged: the epoch reached 2^31; re-zero the workspace, reset it to 0 */
 
 /* Stream format constants (bitpack_codec.py:20-21). */
 #define KVMI_HEADER_BYTES 16
@@ -236,32 +235,40 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  * Compress in one call: the gather, transform, quantization and bitpack of
  * kvmi_kstats_paged + kvmi_encode_paged (same outputs, bit for bit), reading every
  * K value from HBM once.  Replaces the same reference path as those two
- * (compression_manager.py:200-537 with kv_utils.py:59-80).
+ * (compression_manager.py:200-537 with kv_utils.py:59-80).  No counterpart of its own
+ * in the reference.
  *
- * Where the one-pass kernel applies (MFMA geometry, cooperative launch, and each
- * job's K fits the LDS of the workgroups sharing it: num_blocks*S*H*D*2 <= 64 KiB
- * per CU on at most 256 CUs, e.g. 8192 tokens x 8 heads x 128), one cooperative
- * launch keeps every workgroup's share of a job's K on chip from the statistics to
- * the quantization.  Otherwise, or with KVMI_F_TWO_PASS, it runs kvmi_kstats_paged
- * then kvmi_encode_paged (which use each job's `kstats`).
+ * kvmi_compress_schedule (host only) cuts the jobs' K into (job, head) groups of
+ * 32-token head-tiles and V into token-major tiles and lays them out as the steps of a
+ * persistent grid of the current device (one workgroup of 8 waves per CU).  It writes
+ * the schedule image into `image` (when not NULL and image_bytes suffices) and returns
+ * its size in bytes; 0 when the one-pass kernel does not serve the geometry (MFMA
+ * geometry with H dividing 8, S a power of two >= 4 (>= 8 at D = 64), default axes, no
+ * KVMI_F_TWO_PASS), the device has no cooperative launch, or one head of a job has more
+ * K than the grid holds (8 head-tiles of 32 tokens per workgroup: 65,536 tokens on 256
+ * CUs); a negative KVMI_* code on bad arguments.  num_blocks: host array, B of each job.
  *
- * workspace: kvmi_compress_workspace_bytes(geom, num_jobs) bytes of device memory,
- *   256-byte aligned, zeroed once by the caller before its first use and then passed
- *   unchanged to every call for the same jobs (per job: one barrier flag per
- *   workgroup and 64-bit min / max keys, both holding the call's epoch, so nothing
- *   is cleared between calls).  NULL selects the two-pass kernels.
- * epoch: host pointer to the workspace's call counter, 0 before the first call; it
- *   is incremented when (and only when) the one-pass kernel is enqueued.  Calls
- *   sharing a workspace must be ordered on one stream.  Once it reaches 2^31 the call
- *   returns KVMI_ERANGE: zero the workspace again and set *epoch to 0 first.  The
- *   epoch is a kernel argument, so a captured graph would replay one epoch: do not
- *   capture this call (capture kvmi_kstats_paged + kvmi_encode_paged instead).
+ * kvmi_compress_workspace_bytes: device bytes the workspace of a schedule needs.
+ *
+ * kvmi_compress_paged: schedule = the host image (NULL selects the two passes, as does
+ *   KVMI_F_TWO_PASS); workspace = 256-byte aligned device memory of
+ *   kvmi_compress_workspace_bytes(schedule) bytes whose first bytes hold a copy of the
+ *   image and the rest zero before the first call, then passed unchanged to every call
+ *   for the same jobs (barrier flags and 64-bit min / max keys tagged with the call's
+ *   epoch, so nothing is cleared between calls; the epoch lives in the workspace and a
+ *   one-thread kernel enqueued before the pass advances it, so the call can be captured
+ *   in a graph).  Calls sharing a workspace must be ordered on one stream.  From 2^31
+ *   calls on one workspace on, KVMI_ERR_SYNC is set: initialise the workspace again.
+ *   A schedule built for other jobs or another device returns KVMI_EINVAL (the jobs'
+ *   num_blocks may be lower than the schedule's: the kernel skips missing tiles).
  * A barrier that does not complete within about 0.3 s sets KVMI_ERR_SYNC (the
  * kernel still ends; later barriers of the launch then no longer wait).
  */
-int64_t kvmi_compress_workspace_bytes(const kvmi_geometry* geom, int32_t num_jobs);
+int64_t kvmi_compress_schedule(const kvmi_geometry* geom, const int32_t* num_blocks, int32_t num_jobs,
+                               void* image, int64_t image_bytes);
+int64_t kvmi_compress_workspace_bytes(const void* schedule);
 int kvmi_compress_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int32_t num_jobs,
-                        int32_t max_blocks, void* workspace, uint32_t* epoch, int32_t* err,
+                        int32_t max_blocks, const void* schedule, void* workspace, int32_t* err,
                         kvmi_stream_t stream);
 
 /*

@@ -13,7 +13,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvserve_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Device error bits (KVMI_ERR_*) and host return codes (KVMI_*).
 ERR_SYMBOL_RANGE = 1
@@ -21,7 +21,7 @@ ERR_BAD_HEADER = 2
 ERR_CORRUPT = 4
 ERR_SYNC = 8
 ERR_BLOCK_ID = 16
-OK, EINVAL, ELAUNCH, ENOSPC, ERANGE = 0, -22, -5, -28, -34
+OK, EINVAL, ELAUNCH, ENOSPC = 0, -22, -5, -28
 # Bytes of the fixed device array behind kvmi_v3_compress_noalloc (per GPU).
 V3_NOALLOC_SCRATCH_BYTES = 4 * 1024 * 1024
 
@@ -51,8 +51,9 @@ EXPORTS = (
     "kvmi_kstats_paged",
     "kvmi_encode_paged",
     "kvmi_decode_paged",
-    "kvmi_compress_paged",
+    "kvmi_compress_schedule",
     "kvmi_compress_workspace_bytes",
+    "kvmi_compress_paged",
     "kvmi_rans_max_bytes",
     "kvmi_rans_scratch_bytes",
     "kvmi_rans_encode",
@@ -143,9 +144,9 @@ _SIGNATURES = {
     "kvmi_kstats_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_encode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
     "kvmi_decode_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp], ctypes.c_int),
-    "kvmi_compress_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, ctypes.POINTER(ctypes.c_uint32), _vp,
-                             _vp], ctypes.c_int),
-    "kvmi_compress_workspace_bytes": ([ctypes.POINTER(Geometry), _i32], _i64),
+    "kvmi_compress_schedule": ([ctypes.POINTER(Geometry), _vp, _i32, _vp, _i64], _i64),
+    "kvmi_compress_workspace_bytes": ([_vp], _i64),
+    "kvmi_compress_paged": ([ctypes.POINTER(Geometry), _vp, _i32, _i32, _vp, _vp, _vp, _vp], ctypes.c_int),
     "kvmi_rans_max_bytes": ([_i64, _i32], _i64),
     "kvmi_rans_scratch_bytes": ([_i64, _i32], _i64),
     "kvmi_rans_encode": ([_vp, _i64, _i32, _vp, _i64, _vp, _i64, _vp, _vp], ctypes.c_int),
@@ -196,6 +197,4 @@ def check(rc: int, what: str) -> None:
         raise ValueError(f"{what}: invalid arguments (KVMI_EINVAL)")
     if rc == ENOSPC:
         raise ValueError(f"{what}: the call needs more scratch than the fixed device array holds (KVMI_ENOSPC)")
-    if rc == ERANGE:
-        raise ValueError(f"{what}: the workspace epoch reached 2^31; zero the workspace and reset the epoch (KVMI_ERANGE)")
     raise KvmiError(f"{what}: failed with code {rc}")

@@ -181,9 +181,9 @@ class FusedKVCodec:
         self.fwht = (fwht or os.environ.get("KVSERVE_AMD_FWHT", "mfma")).strip().lower()
         if self.fwht not in ("mfma", "valu", "rows"):
             raise ValueError("fwht must be 'mfma', 'valu' or 'rows'")
-        # compress: "two_pass" (kvmi_kstats_paged + kvmi_encode_paged, the faster on
-        # MI355X) or "one_pass" (kvmi_compress_paged: every K value read from HBM once
-        # where the jobs fit the one-pass kernel; KVSERVE_AMD_COMPRESS=one_pass)
+        # compress: "one_pass" (kvmi_compress_paged: every K value read from HBM once
+        # where the jobs fit the one-pass kernel) or "two_pass" (kvmi_kstats_paged +
+        # kvmi_encode_paged, K read twice); KVSERVE_AMD_COMPRESS overrides the default
         self.compress_path = (compress_path or os.environ.get("KVSERVE_AMD_COMPRESS", "two_pass")).strip().lower()
         if self.compress_path not in ("one_pass", "two_pass"):
             raise ValueError("compress_path must be 'one_pass' or 'two_pass'")
@@ -276,24 +276,18 @@ class FusedKVCodec:
                 raise ValueError("KV caches must live on one GPU")
         return dev
 
-    def _block_table(self, block_ids, device, pool_blocks: int, host_check: bool = False):
+    def _block_table(self, block_ids, device, pool_blocks: int):
         """The block table: a host int32 array, every id checked against the cache size
         here and uploaded with the plan's job table; or, for a device tensor, the int32
         device tensor, checked by the plan's first launch (kvmi_check_block_ids: a bad
-        id sets the error the plan reports and leaves the caches untouched), so that
-        building a plan does not synchronize.  `host_check` checks a device tensor here
-        too (the one-pass compress wants jobs that cannot be cleared under it)."""
+        id sets the error the plan reports, zeroes every job's block count and so leaves
+        the caches untouched), so that building a plan does not synchronize."""
         if isinstance(block_ids, torch.Tensor) and block_ids.is_cuda:
             if block_ids.dim() != 1:
                 raise ValueError("block_ids must be 1-D")
             # the plan's own copy: the first run checks it once, and a caller that
             # rewrites its table in place later cannot slip unchecked ids under the plan
-            ids = block_ids.to(device=device, dtype=torch.int32, copy=True).contiguous()
-            if host_check and ids.numel():
-                lo, hi = int(ids.min().item()), int(ids.max().item())
-                if lo < 0 or hi >= pool_blocks:
-                    raise IndexError("block id outside the KV cache")
-            return ids
+            return block_ids.to(device=device, dtype=torch.int32, copy=True).contiguous()
         ids = np.asarray(block_ids.numpy() if isinstance(block_ids, torch.Tensor) else block_ids, dtype=np.int64)
         if ids.ndim != 1:
             raise ValueError("block_ids must be 1-D")
@@ -432,8 +426,7 @@ class FusedKVCodec:
             raise ValueError("one profile per layer is required")
         self._validate_profiles(profiles, self._profile_key(profiles))
         layer_ids = list(range(L)) if layer_ids is None else [int(x) for x in layer_ids]
-        ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools),
-                                host_check=self.compress_path == "one_pass")
+        ids = self._block_table(block_ids, dev, min(p.shape[1] for p in pools))
         B = int(ids.numel()) if isinstance(ids, torch.Tensor) else int(ids.size)
         H, D, S = self.H, self.D, self.S
         raw = L * 2 * B * S * H * D * 2
@@ -564,17 +557,34 @@ class Plan:
         max_level = max(max(max(p.k_levels), max(p.v_levels)) for p in packet.profiles)
         self.geo = codec._geometry(packet_groups(packet), max_level)
         packet.__dict__["_err"] = self.err
+        self.job_blocks = np.full(L, B, dtype=np.int32)
         self._init_workspace()
 
     def _init_workspace(self) -> None:
-        """Device workspace of kvmi_compress_paged (barrier counters and epoch-tagged
-        keys), zeroed once; the host-side epoch counts the one-pass launches on it."""
-        self.workspace, self.epoch = None, ctypes.c_uint32(0)
-        if self.kind == "compress" and self.codec.compress_path == "one_pass":
-            n = int(self.codec._lib.kvmi_compress_workspace_bytes(ctypes.byref(self.geo), self.num_jobs))
-            if n < 0:
-                raise ValueError("geometry not supported by kvmi_compress_paged")
-            self.workspace = torch.zeros(max(n, 256), dtype=torch.uint8, device=self.device)
+        """Schedule and workspace of kvmi_compress_paged, built once per plan: the host
+        schedule image (from every job's block count) and a device workspace holding a
+        copy of it followed by zeroed barrier flags, keys and epoch.  No schedule (the
+        one-pass kernel does not take these jobs): the plan runs the two passes."""
+        self.schedule, self.workspace = None, None
+        if self.kind != "compress" or self.codec.compress_path != "one_pass" or self.max_blocks == 0:
+            return
+        lib, geo = self.codec._lib, ctypes.byref(self.geo)
+        nb = np.ascontiguousarray(self.job_blocks, dtype=np.int32)
+        n = int(lib.kvmi_compress_schedule(geo, nb.ctypes.data, self.num_jobs, None, 0))
+        if n < 0:
+            _lib.check(n, "kvmi_compress_schedule")
+        if n == 0:
+            return
+        img = np.zeros(n, dtype=np.uint8)
+        _lib.check(min(0, int(lib.kvmi_compress_schedule(geo, nb.ctypes.data, self.num_jobs, img.ctypes.data, n))),
+                   "kvmi_compress_schedule")
+        total = int(lib.kvmi_compress_workspace_bytes(img.ctypes.data))
+        ws = torch.zeros(total, dtype=torch.uint8, device=self.device)
+        stage = self.codec._staging(n)
+        stage.numpy()[:] = img
+        ws[:n].copy_(stage, non_blocking=True)
+        self.codec._staged(self.device)
+        self.schedule, self.workspace = img, ws
 
     def launches(self) -> List[str]:
         """Names of the C entry points one run() enqueues, in order."""
@@ -597,16 +607,8 @@ class Plan:
                     self._ids_checked = True
                 return
             if name == "kvmi_compress_paged":
-                if torch.cuda.is_current_stream_capturing():
-                    # the barrier epoch is a kernel argument the host advances per launch;
-                    # a replayed graph would reuse it and meet the previous replay's arrivals
-                    raise RuntimeError("the one-pass compress (compress_path='one_pass') cannot be captured "
-                                       "into a graph; capture a two_pass plan")
-                if self.epoch.value >= 1 << 31:  # epoch tags are 32-bit: start the workspace afresh
-                    self.workspace.zero_()
-                    self.epoch.value = 0
                 _lib.check(fn(ctypes.byref(self.geo), _ptr(self.jobs), self.num_jobs, self.max_blocks,
-                              _ptr(self.workspace), ctypes.byref(self.epoch), _ptr(self.err), _stream_handle()),
+                              self.schedule.ctypes.data, _ptr(self.workspace), _ptr(self.err), _stream_handle()),
                            name)
                 return
             _lib.check(fn(ctypes.byref(self.geo), _ptr(self.jobs), self.num_jobs, self.max_blocks, _ptr(self.err),
@@ -651,6 +653,7 @@ class BatchPlan:
         self.err = torch.zeros(1, dtype=torch.int32, device=self.device)
         for pk in self.packets:
             pk.__dict__["_err"] = self.err
+        self.job_blocks = np.concatenate([p.job_blocks for p in plans])
         self._init_workspace()
 
     _init_workspace = Plan._init_workspace

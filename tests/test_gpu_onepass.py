@@ -1,10 +1,11 @@
-"""One-pass compress (kvmi_compress_paged, K read once; opt-in, the default is the two
-passes) against the two-pass kernels (kvmi_kstats_paged + kvmi_encode_paged) through the
-C-ABI: packed streams, K and V metadata must be identical, bit for bit, on every call,
-with new pool contents (a smaller K range) before each repeated call, so keys or barrier
-flags left by an earlier call would show.  The two-pass path is pinned to the oracle by
+"""One-pass compress (kvmi_compress_paged with a schedule, K read once) against the
+two-pass kernels (kvmi_kstats_paged + kvmi_encode_paged) through the C-ABI: packed
+streams, K and V metadata must be identical, bit for bit, on every call, with new pool
+contents (a smaller K range) before each repeated call, so keys or barrier flags left by
+an earlier call would show.  The two-pass path is pinned to the oracle by
 test_gpu_codec.py and test_gpu_configs.py; test_one_pass_matches_oracle checks the
-one-pass output against the oracle directly."""
+one-pass output against the oracle directly, and test_gpu_configs.py runs the
+benchmark configurations through whichever path is the codec's default."""
 
 import ctypes
 
@@ -62,7 +63,11 @@ def _compare(cuda, pools, reqs, H, D, S, bits, layout="permuted", runs=3, expect
     one_codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path="one_pass")
     ref = ref_codec.plan_compress_batch(args)
     one = one_codec.plan_compress_batch(args)
-    assert one.launches() == ["kvmi_check_block_ids", "kvmi_compress_paged"]
+    if expect_one_pass:
+        assert one.launches() == ["kvmi_check_block_ids", "kvmi_compress_paged"]
+    else:  # the one-pass kernel does not take these jobs: the plan runs the two passes
+        assert one.workspace is None
+        assert one.launches() == ["kvmi_check_block_ids", "kvmi_kstats_paged", "kvmi_encode_paged"]
     for k in range(runs):
         if k:  # new contents with half the range (exact in bf16): stale keys of call k-1 are larger
             for p in pools:
@@ -80,9 +85,16 @@ def _compare(cuda, pools, reqs, H, D, S, bits, layout="permuted", runs=3, expect
         one.run()
         one.check_errors()
         _assert_same(_outputs(one), want)
-    # the host-side epoch counts the one-pass launches (it stays 0 on the fallback)
-    assert one.epoch.value == (runs if expect_one_pass else 0)
+    if expect_one_pass:  # the device epoch counts the one-pass launches
+        assert _epoch(one) == runs
     torch.cuda.synchronize()
+
+
+def _epoch(plan) -> int:
+    """The call counter in a plan's workspace (its offset: the schedule header's int64 at
+    byte 64)."""
+    off = int(np.frombuffer(plan.schedule[64:72].tobytes(), dtype=np.int64)[0])
+    return int(plan.workspace[off:off + 4].view(torch.int32).item())
 
 
 @pytest.mark.parametrize("H,S,D,bits,layout", [
@@ -125,15 +137,24 @@ def test_one_pass_config2_shape_whole_grid(cuda):
 
 
 def test_job_too_large_for_one_pass_falls_back(cuda):
-    """A job whose K exceeds the LDS of the whole grid runs the two passes inside
-    kvmi_compress_paged (and leaves the epoch alone)."""
+    """A job with more tokens per head than the grid's registers hold (8 head-tiles of 32
+    tokens per workgroup: 65,536 on 256 CUs) gets no schedule: the plan runs the two
+    passes."""
     g = torch.Generator().manual_seed(9)
-    pools, reqs = _requests(g, [4096], 1, 8, 128, 16, 4096, (16, 16))
+    pools, reqs = _requests(g, [4100], 1, 8, 128, 16, 4100, (16, 16))
     _compare(cuda, pools, reqs, 8, 128, 16, 4, runs=1, expect_one_pass=False)
 
 
+def test_one_pass_largest_job_the_grid_holds(cuda):
+    """4096 blocks of 16 tokens: each head's K fills every workgroup of a 256-CU grid."""
+    g = torch.Generator().manual_seed(19)
+    pools, reqs = _requests(g, [4096], 1, 8, 128, 16, 4096, (16, 12))
+    _compare(cuda, pools, reqs, 8, 128, 16, 4, runs=2)
+
+
 def test_workspace_contract_through_the_c_abi(cuda):
-    """Direct C-ABI use: a zeroed workspace, a host epoch counter advanced by the call."""
+    """Direct C-ABI use: the host schedule, a workspace holding its image and zeros, two
+    calls with the same workspace, and the host-side argument checks."""
     from kvserve_amd import _lib
     from kvserve_amd.engine import FusedKVCodec
 
@@ -145,23 +166,30 @@ def test_workspace_contract_through_the_c_abi(cuda):
     plan.run()
     want = _outputs(plan)
     lib = _lib.load()
-    n = lib.kvmi_compress_workspace_bytes(ctypes.byref(plan.geo), plan.num_jobs)
-    assert n == 256 * ((plan.num_jobs * 1024 + 255) // 256) + plan.num_jobs * 2 * 8 * 128 * 8
-    ws = torch.zeros(n, dtype=torch.uint8, device=cuda)
-    epoch = ctypes.c_uint32(0)
+    geo = ctypes.byref(plan.geo)
+    nb = np.full(plan.num_jobs, plan.max_blocks, dtype=np.int32)
+    n = lib.kvmi_compress_schedule(geo, nb.ctypes.data, plan.num_jobs, None, 0)
+    assert n > 0
+    img = np.zeros(n, dtype=np.uint8)
+    assert lib.kvmi_compress_schedule(geo, nb.ctypes.data, plan.num_jobs, img.ctypes.data, n - 1) == _lib.EINVAL
+    assert lib.kvmi_compress_schedule(geo, nb.ctypes.data, plan.num_jobs, img.ctypes.data, n) == n
+    total = lib.kvmi_compress_workspace_bytes(img.ctypes.data)
+    assert total >= n
+    ws = torch.zeros(total, dtype=torch.uint8, device=cuda)
+    ws[:n].copy_(torch.from_numpy(img))
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for k in range(2):
-        rc = lib.kvmi_compress_paged(ctypes.byref(plan.geo), plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks,
-                                     ws.data_ptr(), ctypes.byref(epoch), plan.err.data_ptr(), stream)
-        assert rc == 0 and epoch.value == k + 1
+        rc = lib.kvmi_compress_paged(geo, plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks, img.ctypes.data,
+                                     ws.data_ptr(), plan.err.data_ptr(), stream)
+        assert rc == 0
         plan.check_errors()
         _assert_same(_outputs(plan), want)
-    # misaligned workspace / missing epoch pointer: rejected on the host
-    assert lib.kvmi_compress_paged(ctypes.byref(plan.geo), plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks,
-                                   ws.data_ptr() + 16, ctypes.byref(epoch), plan.err.data_ptr(), stream) == _lib.EINVAL
-    assert lib.kvmi_compress_paged(ctypes.byref(plan.geo), plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks,
-                                   ws.data_ptr(), None, plan.err.data_ptr(), stream) == _lib.EINVAL
-    assert epoch.value == 2
+    # misaligned workspace, a schedule of other jobs: rejected on the host
+    assert lib.kvmi_compress_paged(geo, plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks, img.ctypes.data,
+                                   ws.data_ptr() + 16, plan.err.data_ptr(), stream) == _lib.EINVAL
+    assert lib.kvmi_compress_paged(geo, plan.jobs.data_ptr(), plan.num_jobs - 1, plan.max_blocks, img.ctypes.data,
+                                   ws.data_ptr(), plan.err.data_ptr(), stream) == _lib.EINVAL
+    torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("H,S,D,bits", [(8, 16, 128, 4), (4, 16, 64, 3)])
@@ -189,7 +217,7 @@ def test_one_pass_matches_oracle(cuda, H, S, D, bits):
     assert plan.launches()[-1] == "kvmi_compress_paged"
     plan.run()
     check_packet(plan.packet)
-    assert plan.epoch.value == 1
+    assert plan.workspace is not None and _epoch(plan) == 1
     dst = [torch.zeros_like(p) for p in pools]
     codec.decompress(plan.packet, dst, dev_ids)
     torch.cuda.synchronize()
@@ -197,31 +225,41 @@ def test_one_pass_matches_oracle(cuda, H, S, D, bits):
         _check_layer(plan.packet, l, _bits(pools[l][:, dev_ids.long()]), _bits(dst[l][:, dev_ids.long()]))
 
 
-def test_one_pass_plan_refuses_graph_capture(cuda):
-    """The one-pass barrier epoch is a kernel argument the host advances, so a replayed
-    graph would reuse it: launching a one-pass plan under capture raises (nothing is
-    enqueued), and the plan still runs eagerly afterwards."""
-    from kvserve_amd.engine import FusedKVCodec, check_packet
-    from kvserve_amd.workloads import make_config1
+def test_one_pass_plan_captured_in_graph(cuda):
+    """The epoch lives in the workspace and a kernel of the plan advances it, so a graph
+    captured from a one-pass plan's run() replays correctly: every replay, with new pool
+    contents each time (a smaller range, so stale keys would be larger), equals the two
+    passes run eagerly on the same contents."""
+    from kvserve_amd.engine import FusedKVCodec
 
-    wl = make_config1(device=cuda)
-    req = wl.requests[0]
-    codec = FusedKVCodec(8, 128, 16, 4, wl.seed, compress_path="one_pass")
-    plan = codec.plan_compress(req.pools, req.block_ids, req.profiles)
-    plan.run()  # the first run checks the block table
-    check_packet(plan.packet)
-    want = [s.clone() for s in plan.packet.streams]
+    g = torch.Generator().manual_seed(23)
+    pools, reqs = _requests(g, [40, 9], 2, 8, 128, 16, 64, (16, 12))
+    pools = [p.to(cuda) for p in pools]
+    args = [(pools, ids.to(cuda), prof) for ids, prof in reqs]
+    ref = FusedKVCodec(8, 128, 16, 4, 0xC0FEBABE, compress_path="two_pass").plan_compress_batch(args)
+    one = FusedKVCodec(8, 128, 16, 4, 0xC0FEBABE, compress_path="one_pass").plan_compress_batch(args)
+    one.run()  # the first run checks the block tables (outside the graph)
+    one.check_errors()
+    assert one.launches() == ["kvmi_compress_paged"]
     st = torch.cuda.Stream()
     st.wait_stream(torch.cuda.current_stream())
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.stream(st):
-        with pytest.raises(RuntimeError, match="cannot be captured"):
-            with torch.cuda.graph(graph, stream=st):
-                plan.run()
+        with torch.cuda.graph(graph, stream=st):
+            one.run()
     torch.cuda.synchronize()
-    assert plan.epoch.value == 1
-    plan.run()
-    check_packet(plan.packet)
-    assert plan.epoch.value == 2
-    for a, b in zip(plan.packet.streams, want):
-        assert torch.equal(a, b)
+    for k in range(3):
+        for p in pools:
+            p.mul_(-0.5)
+        ref.run()
+        ref.check_errors()
+        want = _outputs(ref)
+        for pk in one.packets:
+            for s in pk.streams:
+                s.fill_(0xA5)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        one.check_errors()
+        _assert_same(_outputs(one), want)
+    assert _epoch(one) == 4  # the eager run and three replays (capturing runs nothing)
