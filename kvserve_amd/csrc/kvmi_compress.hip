@@ -37,6 +37,7 @@
 //   * Every wait is bounded: on timeout the kernel sets KVMI_ERR_SYNC, later device
 //     waits give up at once, and every wave reaches the end of the kernel.
 #include <algorithm>
+#include <climits>
 #include <cstring>
 #include <vector>
 
@@ -45,8 +46,8 @@
 namespace kvmi {
 namespace {
 
-constexpr int kOW = 8;        // waves per workgroup
-constexpr int kOT = 512;      // threads per workgroup
+constexpr int kOW = 8;        // waves per workgroup (two per SIMD: three do not fit the registers at D = 128)
+constexpr int kOT = 64 * kOW; // threads per workgroup
 constexpr int kTPW = kOW;     // K head-tiles and V tiles per workgroup and step (one per wave)
 constexpr uint32_t kOpMagic = 0x5350314Bu;  // "K1PS"
 constexpr uint32_t kMaxPolls = 1u << 18;    // ~0.3 s of polling before KVMI_ERR_SYNC
@@ -134,13 +135,193 @@ __device__ __forceinline__ OpRec no_rec() {
   return r;
 }
 
-// Tables of one step's V job (signs of every head, profile) and K-statistics head.
+// Everything a workgroup needs of one step, staged into LDS two steps ahead by one wave
+// (so that no other wave waits on the scalar loads of records, job descriptors and block
+// ids: on gfx950 LDS and scalar loads share one wait counter, so an outstanding scalar
+// load holds up the next LDS access of its wave).
 struct StepTables {
   uint32_t smask[kMH][64 + 4];  // V: sign-flip masks per (head, element pair)
   uint32_t kmask[64 + 4];       // K statistics: the masks of the group's head
-  uint8_t prof[2][3][kMH];
+  uint8_t prof[2][3][kMH];      // the V job's profile
   int posk[kMH], posv[kMH], gfirst[kMH];
+  OpRec rec;                    // this workgroup's record of the step
+  int kjk, kjlv;                // K job: output position and levels of the group's head
+  kvmi_layer_job kj, vj;        // the K and V jobs
+  int32_t krow[kOW][8];         // K: pool row of each wave's load instruction v (-1 - row past the
+                                // job's last token, INT32_MIN without a tile)
+  int64_t vrow[kOW];            // V: first pool row of each wave's tile (-1 without one)
 };
+
+// Wave-uniform copies of LDS values (v_readfirstlane: the compiler cannot see that every
+// lane reads the same address).
+__device__ __forceinline__ int32_t uni(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uni(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+template <class T>
+__device__ __forceinline__ T* uni(T* p) { return reinterpret_cast<T*>(uni((int64_t)reinterpret_cast<uintptr_t>(p))); }
+__device__ __forceinline__ OpRec uni(const OpRec& r) {
+  OpRec u;
+  u.kjob = uni(r.kjob);
+  u.khead = uni(r.khead);
+  u.ktile0 = uni(r.ktile0);
+  u.kgroup = uni(r.kgroup);
+  u.kslot = uni(r.kslot);
+  u.vjob = uni(r.vjob);
+  u.vtile0 = uni(r.vtile0);
+  u.vn = uni(r.vn);
+  return u;
+}
+__device__ __forceinline__ kvmi_layer_job uni(const kvmi_layer_job& j) {
+  kvmi_layer_job u;
+  u.pool = uni(j.pool);
+  u.block_ids = uni(j.block_ids);
+  u.stream = uni(j.stream);
+  u.kmeta = uni(j.kmeta);
+  u.vmeta = uni(j.vmeta);
+  u.signs = uni(j.signs);
+  u.profile = uni(j.profile);
+  u.kstats = nullptr;
+  u.pool_blocks = 0;
+  u.pool_part_stride = uni(j.pool_part_stride);
+  u.symbol_offset = uni(j.symbol_offset);
+  u.chunk_symbols = uni(j.chunk_symbols);
+  u.num_blocks = uni(j.num_blocks);
+  u.write_header = uni(j.write_header);
+  return u;
+}
+
+// ---------------------------------------------------------------- pipelined tile work
+// Within a wave the products of output chunk cp + 1 are issued while chunk cp's results
+// are reduced or quantized: the MFMA chain of one chunk and the VALU work of the other
+// are independent, so the matrix cores and the VALU work at the same time (two
+// accumulators live instead of one).  A fence closes each chunk so that no further
+// chunk is hoisted.
+
+// Orientation N product of output chunk cp (A = rows, B = Hadamard tile): column n of
+// the result is channel HALF n2 + 16 cp + 8 n4 + 4 n3 + 2 n1 + n0 with the orientation-T
+// operand tiles (the Sylvester matrix is symmetric).
+template <int NC>
+__device__ __forceinline__ f32x16 transform_N(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                              int cp) {
+  f32x16 acc = {};
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int c = cp ^ k;
+    const bool neg = __builtin_popcount(c & cp) & 1;
+    acc = mfma(x[2 * c], neg ? hn[0] : hp[0], acc);
+    acc = mfma(x[2 * c + 1], neg ? hn[1] : hp[1], acc);
+  }
+  return acc;
+}
+
+// K statistics of one signed head-tile into the workgroup's LDS keys [2][D] (unscaled).
+template <int NC>
+__device__ __forceinline__ void kstats_head_tile(const uint4 (&x)[2 * NC], const uint4 (&hp)[2], const uint4 (&hn)[2],
+                                                 uint32_t* lkey) {
+  constexpr int D = 32 * NC, HALF = 16 * NC;
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31;
+  f32x16 a0 = transform_N<NC>(x, hp, hn, 0);
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    f32x16 a1 = a0;
+    if (cp + 1 < NC) a1 = transform_N<NC>(x, hp, hn, cp + 1);
+    float mn = fminf(fminf(a0[0], a0[1]), fminf(a0[2], a0[3]));
+    float mx = fmaxf(fmaxf(a0[0], a0[1]), fmaxf(a0[2], a0[3]));
+#pragma unroll
+    for (int i = 4; i < 16; i += 4) {
+      mn = fminf(fminf(mn, a0[i]), fminf(a0[i + 1], fminf(a0[i + 2], a0[i + 3])));
+      mx = fmaxf(fmaxf(mx, a0[i]), fmaxf(a0[i + 1], fmaxf(a0[i + 2], a0[i + 3])));
+    }
+    mn = halves_min(mn);
+    mx = halves_max(mx);
+    if (hl == 0) {
+      const int f = HALF * ((r >> 2) & 1) + 16 * cp + 8 * ((r >> 4) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
+      atomicMin(&lkey[f], f2key(mn));  // unscaled: 1/sqrt(D) > 0 commutes with min / max
+      atomicMax(&lkey[D + f], f2key(mx));
+    }
+    chunk_fence();
+    a0 = a1;
+  }
+}
+
+// quant_k_tile with the next chunk's products in flight during each quantization.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_k_tile_pipe(const uint4 (&xk)[2 * NC], const uint4 (&hp)[2],
+                                                  const uint4 (&hn)[2], const float2* kq, float s, float lvk,
+                                                  LanePack<16 * NC, BITS>& pkd, uint32_t& over) {
+  pkd.clear();
+  f32x16 a0 = transform_T<NC>(xk, hp, hn, 0);
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    f32x16 a1 = a0;
+    if (cp + 1 < NC) a1 = transform_T<NC>(xk, hp, hn, cp + 1);
+    quant_chunk_k<16 * NC, BITS, CLAMP>(a0, cp, s, kq + 16 * cp, lvk, pkd, over);
+    chunk_fence();
+    a0 = a1;
+  }
+}
+
+// quant_v_tile_lds with the next chunk's products in flight during each chunk's
+// statistics and rounding.
+template <int NC, int BITS, bool CLAMP>
+__device__ __forceinline__ void quant_v_tile_pipe(const uint4 (&xv)[2 * NC], const uint4 (&hp)[2],
+                                                  const uint4 (&hn)[2], const LaneProfile& lp,
+                                                  const kvmi_layer_job& job, int ntok, int tok, int G, int H,
+                                                  float s, uint4* ylane, LanePack<16 * NC, BITS>& pkd,
+                                                  uint32_t& over) {
+  constexpr int HALF = 16 * NC;
+  float amn = __builtin_inff(), amx = -__builtin_inff();
+  f32x16 a0 = transform_T<NC>(xv, hp, hn, 0);
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    f32x16 a1 = a0;
+    if (cp + 1 < NC) a1 = transform_T<NC>(xv, hp, hn, cp + 1);
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      amn = fminf(fminf(amn, a0[i]), fminf(a0[i + 1], fminf(a0[i + 2], a0[i + 3])));
+      amx = fmaxf(fmaxf(amx, a0[i]), fmaxf(a0[i + 1], fmaxf(a0[i + 2], a0[i + 3])));
+    }
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) w[i / 2] = pack_bf16x2(a0[i] * s, a0[i + 1] * s);
+    ylane[(2 * cp) * 64] = make_uint4(w[0], w[1], w[2], w[3]);
+    ylane[(2 * cp + 1) * 64] = make_uint4(w[4], w[5], w[6], w[7]);
+    chunk_fence();
+    a0 = a1;
+  }
+  amn = halves_min(amn);
+  amx = halves_max(amx);
+  float mn = 0.f, mx = 0.f;
+  for (int gg = 0; gg < G; ++gg) {
+    float a = lp.gv == gg ? amn : __builtin_inff();
+    float b = lp.gv == gg ? amx : -__builtin_inff();
+    token_minmax(a, b, H);
+    if (lp.gv == gg) {
+      mn = a;
+      mx = b;
+    }
+  }
+  mn = rbf(mn * s);
+  mx = rbf(mx * s);
+  const float sc = quant_scale(mn, mx, (int)lp.lvv);
+  const float rcp = 1.0f / sc;
+  if (lp.rep_lane) {
+    gst(job.vmeta + (int64_t)lp.gv * ntok + tok, (uint16_t)f32_to_bf16_bits(mn));
+    gst(job.vmeta + (int64_t)(G + lp.gv) * ntok + tok, (uint16_t)f32_to_bf16_bits(sc));
+  }
+  pkd.clear();
+#pragma unroll
+  for (int cp = 0; cp < NC; ++cp) {
+    const uint4 a = ylane[(2 * cp) * 64], b = ylane[(2 * cp + 1) * 64];
+    const uint32_t ypk[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    quant_chunk_v<HALF, BITS, CLAMP>(ypk, cp, mn, rcp, lp.lvv, pkd, over);
+    chunk_fence();
+  }
+}
+
 
 // Advances the workspace epoch (one thread); the pass reads it at its start.  Tags are
 // 32-bit: from 2^31 calls on one workspace on, a tag could come back while keys or flags
@@ -159,42 +340,62 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
   constexpr int RPI = 64 / PR;         // rows per coalesced load instruction
   constexpr int RB = D * BITS / 8;     // bytes of one packed row
   constexpr int TQ = kTok * RB / 16;   // uint4 per packed tile
+  constexpr int NSET = 8;              // table sets (a power of two: indices are masks)
   static_assert(tile_buf_q<NC>() >= 2 * NC * 64 && tile_buf_q<NC>() * 16 >= kTok * RB, "wave buffer uses");
   const Geo g = a.g;
   const int S = g.S, H = g.H, G = g.G, HD = H * D;
   const int wg = blockIdx.x, grid = a.grid, steps = a.steps;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31, hme = r % H;
+  // H and S are powers of two here (mfma_eligible, onepass_geometry): shifts, not divisions
+  const int lgH = __builtin_ctz((unsigned)H), lgS = __builtin_ctz((unsigned)S);
+  const int l = threadIdx.x & 63, hl = l >> 5, r = l & 31, hme = r & (H - 1), rtok = r >> lgH;
   const float sc_d = g.scale;
   const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
   const int tpt = kTok / H;  // tokens per V tile
   const uint32_t epoch = __builtin_amdgcn_readfirstlane(gld(a.epoch));
 
-  __shared__ StepTables tab[3];           // by step % 3
-  __shared__ uint32_t lkey[3][2 * D];     // the workgroup's min / max keys of a step's group, by step % 3
-  __shared__ float2 kc[2][D + 4];         // (min, 1/scale) per channel of the group being quantized
-  __shared__ int kinfo[2][2];             // its output position and levels
+  // Waves are ordered by LDS flags and counters, not workgroup barriers, so that they
+  // can be in different phases and steps.  Every wave starts step s only once every wave
+  // has finished step s - 3 (`fin` counts finished steps: 8 per step), so at most three
+  // steps are in flight, and each piece of per-step LDS state is buffered deeper than
+  // that: table sets by s % 8 (staged two steps ahead by wave s % 8, and read up to the
+  // next step), the workgroup keys and their arrival counters by s % 4, the K constants by
+  // the step that uses them % 4.  A buffer's flag holds the step (+ 1) it was last
+  // filled for, so no flag is ever cleared and every wait is "flag >= value".
+  __shared__ StepTables tab[NSET];
+  __shared__ uint32_t lkey[4][2 * D];     // the workgroup's min / max keys of a step's K group
+  __shared__ float2 kc[4][D + 4];         // (min, 1/scale) per channel of the group quantized in step q
   __shared__ uint4 wbuf[kOW * tile_buf_q<NC>()];
-  // Waves are ordered by monotone LDS counters, not workgroup barriers, so they may be up
-  // to two steps apart: `staged` is the number of steps whose tables are staged (wave
-  // s % 8 stages step s + 1's at the start of step s), `fin` counts the steps the waves
-  // finished (every wave is past step s at 8 (s + 1)); a set is restaged only once every
-  // wave is past its last step, and per-step LDS state is buffered deep enough for that.
-  __shared__ uint32_t karr[2], kclaim, kready, kfinal, staged, fin;
+  __shared__ uint32_t tready[NSET];       // step + 1 of the tables in each set
+  __shared__ uint32_t karr[4], kfin[4];   // K waves arrived in step s; step + 1 once its keys are final
+  __shared__ uint32_t kown[4], kready[4]; // claim and readiness of the constants used in step q
+  __shared__ uint32_t fin;
 
   uint4* wb = wbuf + wave * tile_buf_q<NC>();
   uint8_t* ost = reinterpret_cast<uint8_t*>(wb);
+  bool broken = false;  // a device wait of this wave timed out: later ones give up at once
 
-  // ---------------------------------------------------------------- tables
-  // Tables of a step into set e, by one wave: the job's sign words and profile bytes are
-  // loaded once (one load per lane, all in flight together) and spread by lane shuffles.
-  auto stage = [&](const OpRec& rc, int e) {
+  // ---------------------------------------------------------------- staging
+  // Step k's tables into set e, by one wave: its record, the K and V job descriptors,
+  // the pool rows every wave will load, sign masks and profile positions.
+  auto stage = [&](int k, int e) {
     StepTables& T = tab[e];
+    const OpRec rc = load_rec(a.recs, (int64_t)k * grid + wg);
+    if (l == 0) T.rec = rc;
+    int64_t vr = -1;
     if (rc.vjob >= 0) {
       const kvmi_layer_job jv = load_job(a.jobs, rc.vjob);
+      if (l == 0) T.vj = jv;
       constexpr int W = D / 32;  // sign words per head
       const uint32_t sw = l < H * W ? gld(jv.signs + l) : 0u;
       const uint32_t pb = l < 6 * H ? (uint32_t)gld(jv.profile + l) : 0u;
+      if (l < kOW && l < rc.vn) {  // lane w: first pool row of wave w's V tile
+        const int vt = rc.vtile0 + l;
+        if (vt * kTok < jv.num_blocks * S * H) {
+          const int ta = vt * tpt;
+          vr = ((int64_t)gld(jv.block_ids + (ta >> lgS)) * S + (ta & (S - 1))) * H;
+        }
+      }
       for (int i = l; i < H * (D / 2); i += 64) {
         const int h = i / (D / 2), q = i % (D / 2);
         const uint32_t sb = (uint32_t)__shfl((int)sw, h * W + (2 * q) / 32) >> ((2 * q) & 31);
@@ -202,16 +403,17 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
       }
       if (l < 6 * H) T.prof[l / (3 * H)][(l / H) % 3][l % H] = (uint8_t)pb;
       // lane h < H: output positions of source head h (K, V) and the source head of
-      // the first output position of V group h
+      // the first output position of V group h (shuffles outside branches: every lane
+      // takes part)
       int pk = 0, pv = 0, gf = -1;
-      for (int k = 0; k < H; ++k) {
-        const int ok = __shfl((int)pb, k), ov = __shfl((int)pb, 3 * H + k);
-        if (ok == l) pk = k;
-        if (ov == l) pv = k;
+      for (int q = 0; q < H; ++q) {
+        const int ok = __shfl((int)pb, q), ov = __shfl((int)pb, 3 * H + q);
+        if (ok == l) pk = q;
+        if (ov == l) pv = q;
       }
-      for (int k = H - 1; k >= 0; --k) {  // (shuffles outside the branch: every lane takes part)
-        const int gk = __shfl((int)pb, 5 * H + k), ok = __shfl((int)pb, 3 * H + k);
-        if (gk == l) gf = ok;
+      for (int q = H - 1; q >= 0; --q) {
+        const int gq = __shfl((int)pb, 5 * H + q), oq = __shfl((int)pb, 3 * H + q);
+        if (gq == l) gf = oq;
       }
       if (l < H) {
         T.posk[l] = pk;
@@ -221,88 +423,164 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
     }
     if (rc.kjob >= 0) {
       const kvmi_layer_job jk = load_job(a.jobs, rc.kjob);
-      const int h = rc.khead & 0xff;
+      const int h = rc.khead & 0xff, kn = rc.khead >> 8, T_ = jk.num_blocks * S;
+      if (l == 0) T.kj = jk;
       for (int q = l; q < D / 2; q += 64) {
         const uint32_t sb = gld(jk.signs + h * (D / 32) + (2 * q) / 32) >> ((2 * q) & 31);
         T.kmask[q] = ((sb & 1u) << 15) | ((sb & 2u) << 30);
       }
+      const int pb = l < 2 * H ? (int)gld(jk.profile + l) : 0;  // K order and levels
+      int jk_ = 0;
+      for (int q = 0; q < H; ++q)
+        if (__shfl(pb, q) == h) jk_ = q;
+      const int lv = __shfl(pb, H + jk_);
+      if (l == 0) {
+        T.kjk = jk_;
+        T.kjlv = lv;
+      }
+      // entry (w, v): row of wave w's load instruction v
+      for (int i = l; i < kOW * U; i += 64) {
+        const int w = i / U, v = i % U, tt = rc.ktile0 + w;
+        int32_t kr = INT32_MIN;
+        if (w < kn && 32 * tt < T_) {
+          const int tv = 32 * tt + RPI * v;
+          const bool past = tv >= T_;
+          const int tb = past ? T_ - 1 : tv;
+          const int row = (gld(jk.block_ids + (tb >> lgS)) * S + (tb & (S - 1))) * H + h;
+          kr = past ? -1 - row : row;
+        }
+        T.krow[w][v] = kr;
+      }
+    } else {
+      for (int i = l; i < kOW * U; i += 64) T.krow[i / U][i % U] = INT32_MIN;
     }
+    if (l < kOW) T.vrow[l] = vr;
+    lds_order();
+    if (l == 0) __hip_atomic_store(&tready[e], (uint32_t)(k + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  auto wait_tables = [&](int k) {
+    if (k < steps && !lds_wait(&tready[k & (NSET - 1)], (uint32_t)(k + 1)) && l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
   };
 
   // ---------------------------------------------------------------- loads
   // Every wave issues the same loads on every path (idle waves read `dummy`): a load
   // issued on one path only makes the compiler wait for every load in flight where the
-  // paths join.
-  //
-  // K head-tile t of (job, head): tokens 32t .. 32t + 31, instruction v reads rows
-  // RPI v .. RPI v + RPI - 1 (PR lanes per row, 16 bytes each).  S is a power of two
-  // >= RPI, so the rows of one instruction lie in one block (block id by a scalar load);
-  // rows past the job's last token repeat that token (min / max ignore repeats, and the
-  // quantization does not write them).
-  auto issue_k = [&](const OpRec& rc, uint4 (&x)[U]) {
-    const uint16_t* base = a.dummy;
-    int64_t rowoff[U];
+  // paths join.  K head-tile t of (job, head): tokens 32t .. 32t + 31, instruction v reads
+  // rows RPI v .. RPI v + RPI - 1 (PR lanes per row, 16 bytes each); S is a power of two
+  // >= RPI, so the rows of one instruction lie in one block; rows past the job's last
+  // token repeat that token (min / max ignore repeats, and the quantization does not
+  // write them).
+  // (`valid` false: no such step, every load reads `dummy`)
+  auto k_fire = [&](const StepTables& T, bool valid, uint4 (&x)[U]) {
+    const int32_t* kr = &T.krow[wave][0];
+    const int32_t r0 = valid ? uni(kr[0]) : INT32_MIN;
+    const uint16_t* base = r0 == INT32_MIN ? a.dummy : reinterpret_cast<const uint16_t*>(uni(T.kj.pool));
+    const int lo = (l / PR) * H;
 #pragma unroll
-    for (int v = 0; v < U; ++v) rowoff[v] = 0;
-    const int kn = rc.kjob >= 0 ? (rc.khead >> 8) : 0;
-    if (wave < kn) {
-      const kvmi_layer_job jb = load_job(a.jobs, rc.kjob);
-      const int T = jb.num_blocks * S, tt = rc.ktile0 + wave, h = rc.khead & 0xff;
-      if (32 * tt < T) {
-        base = reinterpret_cast<const uint16_t*>(jb.pool);
-#pragma unroll
-        for (int v = 0; v < U; ++v) {
-          const int tv = 32 * tt + RPI * v;                // first token of the instruction
-          const int tb = tv < T ? tv : T - 1;              // (uniform) token naming the block
-          const int64_t blk = cld(jb.block_ids + tb / S);
-          const int tok = tv < T ? tv + l / PR : T - 1;    // this lane's token
-          rowoff[v] = ((blk * S + (tok & (S - 1))) * H + h) * D;
-        }
-      }
+    for (int v = 0; v < U; ++v) {
+      const int32_t rb = r0 == INT32_MIN ? INT32_MIN : uni(kr[v]);
+      const int64_t row = rb == INT32_MIN ? 0 : rb < 0 ? (int64_t)(-1 - rb) : (int64_t)rb + lo;
+      x[v] = gld(reinterpret_cast<const uint4*>(base + row * D) + l % PR);
     }
-#pragma unroll
-    for (int v = 0; v < U; ++v) x[v] = gld(reinterpret_cast<const uint4*>(base + rowoff[v]) + l % PR);
   };
-  // V tile vt of a job: rows 32 vt .. 32 vt + 31 of the job's token-major rows, within
-  // one block (S*H % 32 == 0), loaded 1 KiB per instruction.
-  auto issue_v = [&](const OpRec& rc, uint4 (&x)[U]) {
+  // V tile: 32 consecutive pool rows (one block), loaded 1 KiB per instruction
+  auto v_fire = [&](const StepTables& T, bool valid, uint4 (&x)[U]) {
+    const int64_t row0 = valid ? uni(T.vrow[wave]) : (int64_t)-1;
     const uint16_t* base = a.dummy;
-    int64_t row0 = 0;
-    if (rc.vjob >= 0 && wave < rc.vn) {
-      const kvmi_layer_job jb = load_job(a.jobs, rc.vjob);
-      const int vt = rc.vtile0 + wave;
-      if (vt * kTok < jb.num_blocks * S * H) {
-        base = reinterpret_cast<const uint16_t*>(jb.pool) + jb.pool_part_stride;
-        row0 = tile_row0(jb, S, H, vt * tpt);
+    if (row0 >= 0) {
+      const kvmi_layer_job* vj = &T.vj;
+      base = reinterpret_cast<const uint16_t*>(uni(vj->pool)) + uni(vj->pool_part_stride);
+    }
+    load_tile<NC>(base, row0 >= 0 ? row0 : 0, x);
+  };
+
+  // ---------------------------------------------------------------- K constants
+  // The constants of step s's K group (used in step s + 1), by the first wave to finish
+  // step s: once the group's keys are final (this workgroup's arrivals, or every
+  // workgroup's flag), per-channel (min, 1/scale) into kc[(s + 1) % 4] and the K metadata
+  // (the group's first workgroup).
+  auto claim = [&](int s, const OpRec& rc, const StepTables& T) {
+    const int q = s + 1, e = q & 3, pk3 = s & 3;
+    uint32_t old = 0;
+    if (l == 0) old = __hip_atomic_fetch_max(&kown[e], (uint32_t)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old >= (uint32_t)q) return;  // another wave has it
+    const int gw0 = rc.kgroup & 0xffff, gws = rc.kgroup >> 16;
+    if (gws > 1) {
+      const uint32_t* fl = a.flags + (int64_t)s * grid + gw0;
+      bool done = false;
+      for (uint32_t polls = 0; !broken && polls < kMaxPolls; ++polls) {
+        bool ok = true;
+        for (int w = l; w < gws; w += 64)
+          ok &= __hip_atomic_load(fl + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+        if (__all(ok)) {
+          done = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!done) {
+        broken = true;
+        if (l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
+      }
+    } else if (!lds_wait(&kfin[pk3], (uint32_t)(s + 1)) && l == 0) {  // this workgroup's keys are final
+      atomicOr(a.err, KVMI_ERR_SYNC);
+    }
+    const int jk = uni(T.kjk), lv = uni(T.kjlv);
+    uint16_t* kmeta = uni(T.kj.kmeta);
+    const int T_ = uni(T.kj.num_blocks) * S;
+    const unsigned long long* kk = a.keys + (int64_t)rc.kslot * 2 * D;
+    bool stale = false;
+    for (int c = l; c < D; c += 64) {
+      uint32_t kmn, kmx;
+      if (gws > 1) {
+        const unsigned long long vmn = __hip_atomic_load(kk + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long vmx = __hip_atomic_load(kk + D + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        stale |= (uint32_t)(vmn >> 32) != epoch || (uint32_t)(vmx >> 32) != epoch;
+        kmn = ~(uint32_t)vmn;
+        kmx = (uint32_t)vmx;
+      } else {
+        kmn = lkey[pk3][c];
+        kmx = lkey[pk3][D + c];
+        lkey[pk3][c] = 0xffffffffu;
+        lkey[pk3][D + c] = 0u;
+      }
+      const float mn = round_bf16(key2f(kmn) * sc_d);  // keys are unscaled
+      const float mx = round_bf16(key2f(kmx) * sc_d);
+      const float scl = quant_scale(mn, mx, lv);
+      kc[e][c] = make_float2(mn, 1.0f / scl);
+      if (rc.ktile0 == 0 && T_ > 0) {  // the group's first workgroup writes the K metadata
+        gst(kmeta + jk * D + c, (uint16_t)f32_to_bf16_bits(mn));
+        gst(kmeta + HD + jk * D + c, (uint16_t)f32_to_bf16_bits(scl));
       }
     }
-    load_tile<NC>(base, row0, x);
+    if (stale && !broken) atomicOr(a.err, KVMI_ERR_SYNC);
+    lds_order();
+    if (l == 0) __hip_atomic_store(&kready[e], (uint32_t)q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   };
 
   // ---------------------------------------------------------------- set-up
-  uint4 hpN[2], hnN[2], hpT[2], hnT[2];
-  hpN[0] = hadamard_tile(0, true, false);
-  hpN[1] = hadamard_tile(1, true, false);
-  hnN[0] = hadamard_tile(0, true, true);
-  hnN[1] = hadamard_tile(1, true, true);
+  // The Sylvester matrix is symmetric, so the orientation-T operand tiles serve the
+  // statistics (orientation N) too: column n of the product is then channel
+  // HALF n2 + 16 c + 8 n4 + 4 n3 + 2 n1 + n0 instead of the T layout's row.
+  uint4 hpT[2], hnT[2];
   hpT[0] = hadamard_tile(0, false, false);
   hpT[1] = hadamard_tile(1, false, false);
   hnT[0] = hadamard_tile(0, false, true);
   hnT[1] = hadamard_tile(1, false, true);
   uint32_t over = 0;
-  bool broken = false;  // a device wait of this wave timed out: later ones give up at once
 
   for (int i = threadIdx.x; i < 2 * D; i += kOT) {
     const uint32_t init = i < D ? 0xffffffffu : 0u;
     lkey[0][i] = init;
     lkey[1][i] = init;
     lkey[2][i] = init;
+    lkey[3][i] = init;
   }
-  if (threadIdx.x == 0) {
-    karr[0] = karr[1] = 0;
-    kclaim = kready = kfinal = fin = 0;
-    staged = 1;  // step 0's tables, staged below
-  }
+  if (threadIdx.x < NSET) tready[threadIdx.x] = 0;
+  if (threadIdx.x < 4) karr[threadIdx.x] = kfin[threadIdx.x] = 0;
+  if (threadIdx.x < 4) kown[threadIdx.x] = kready[threadIdx.x] = 0;
+  if (threadIdx.x == 0) fin = 0;
   // chunks of jobs without blocks still get their header (the stream of N = 0 symbols)
   if (wg == 0 && !(g.flags & KVMI_F_NO_HEADER)) {
     for (int j = threadIdx.x; j < a.num_jobs; j += kOT) {
@@ -311,85 +589,48 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
         write_stream_header(gld(&q->stream), BITS, gld(&q->chunk_symbols));
     }
   }
-  if (steps > 0 && wave == 0) stage(load_rec(a.recs, wg), 0);
   __syncthreads();
+  if (wave < 2 && wave < steps) stage(wave, wave);  // steps 0 and 1
 
   uint4 kb0[U], kb1[U], vb[U];
-  {
-    const OpRec r0 = steps > 0 ? load_rec(a.recs, wg) : no_rec();
-    issue_k(r0, kb0);
-    issue_v(r0, vb);
-  }
+  wait_tables(0);
+  k_fire(tab[0], steps > 0, kb0);
+  v_fire(tab[0], steps > 0, vb);
 
   // ---------------------------------------------------------------- one step
   auto step = [&](int s, uint4 (&cur)[U], uint4 (&prev)[U]) {
-    const int p = s & 1, p3 = s % 3;
-    // step s's tables are staged (step 0's before the loop)
-    if (s > 0 && s < steps && !lds_wait(&staged, (uint32_t)(s + 1)) && l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
-    const OpRec rc = s < steps ? load_rec(a.recs, (int64_t)s * grid + wg) : no_rec();
-    const OpRec rp = s > 0 ? load_rec(a.recs, (int64_t)(s - 1) * grid + wg) : no_rec();
-    const OpRec rn = s + 1 < steps ? load_rec(a.recs, (int64_t)(s + 1) * grid + wg) : no_rec();
-    if (s + 1 < steps && wave == s % kOW) {
-      // step s + 1's tables into set (s + 1) % 3, last used in step s - 2
-      if (s >= 2 && !lds_wait(&fin, (uint32_t)(kOW * (s - 1))) && l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
-      stage(rn, (s + 1) % 3);
-      lds_order();
-      if (l == 0) __hip_atomic_store(&staged, (uint32_t)(s + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
+    const int p3 = s & 3;
+    if (s >= 3 && !lds_wait(&fin, (uint32_t)(kOW * (s - 2))) && l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
+    if (s + 2 < steps && wave == s % kOW) stage(s + 2, (s + 2) & (NSET - 1));  // set last used in step s - 6
+    wait_tables(s);
+    const StepTables& T = tab[s & (NSET - 1)];
+    const StepTables& TP = tab[(s - 1) & (NSET - 1)];
+    const OpRec rc = s < steps ? uni(T.rec) : no_rec();
+    const OpRec rp = s > 0 ? uni(TP.rec) : no_rec();
 
     // ------------------------------------------------ P1: K statistics of step s
     const int kn = rc.kjob >= 0 ? (rc.khead >> 8) : 0;
     if (wave < kn) {
-      const kvmi_layer_job jb = load_job(a.jobs, rc.kjob);
-      const bool mine = 32 * (rc.ktile0 + wave) < jb.num_blocks * S;
-      if (mine) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) pin(cur[u]);
+      const int T_ = uni(T.kj.num_blocks) * S;
+      if (32 * (rc.ktile0 + wave) < T_) {
         tile_to_half_rows<NC>(wb, cur);
-        const uint4* sm = reinterpret_cast<const uint4*>(&tab[p3].kmask[0] + opaque((HALF / 2) * hl));
+        const uint4* sm = reinterpret_cast<const uint4*>(&T.kmask[0] + opaque((HALF / 2) * hl));
 #pragma unroll
         for (int u = 0; u < U; ++u) cur[u] = xor4(cur[u], sm[u]);
-        // orientation N: register i of chunk cp holds row 8(i/4) + 4hl + i%4, channel
-        // HALF (r >> 4) + 16 cp + (r & 15); every row is the group's head
-#pragma unroll
-        for (int cp = 0; cp < NC; ++cp) {
-          f32x16 acc = {};
-#pragma unroll
-          for (int k = 0; k < NC; ++k) {
-            const int c = cp ^ k;
-            const bool neg = __builtin_popcount(c & cp) & 1;
-            acc = mfma(cur[2 * c], neg ? hnN[0] : hpN[0], acc);
-            acc = mfma(cur[2 * c + 1], neg ? hnN[1] : hpN[1], acc);
-          }
-          float mn = fminf(fminf(acc[0], acc[1]), fminf(acc[2], acc[3]));
-          float mx = fmaxf(fmaxf(acc[0], acc[1]), fmaxf(acc[2], acc[3]));
-#pragma unroll
-          for (int i = 4; i < 16; i += 4) {
-            mn = fminf(fminf(mn, acc[i]), fminf(acc[i + 1], fminf(acc[i + 2], acc[i + 3])));
-            mx = fmaxf(fmaxf(mx, acc[i]), fmaxf(acc[i + 1], fmaxf(acc[i + 2], acc[i + 3])));
-          }
-          mn = halves_min(mn);
-          mx = halves_max(mx);
-          if (hl == 0) {
-            const int f = HALF * (r >> 4) + 16 * cp + (r & 15);
-            atomicMin(&lkey[p3][f], f2key(mn));  // unscaled: 1/sqrt(D) > 0 commutes with min / max
-            atomicMax(&lkey[p3][D + f], f2key(mx));
-          }
-          chunk_fence();
-        }
+        kstats_head_tile<NC>(cur, hpT, hnT, &lkey[p3][0]);
       }
-      if (wave == 0 && rc.ktile0 == 0 && (rc.khead & 0xff) == 0 && jb.write_header &&
-          !(g.flags & KVMI_F_NO_HEADER) && l == 0)
-        write_stream_header(jb.stream, BITS, jb.chunk_symbols);
+      if (wave == 0 && rc.ktile0 == 0 && (rc.khead & 0xff) == 0 && !(g.flags & KVMI_F_NO_HEADER)) {
+        const kvmi_layer_job jb = uni(T.kj);
+        if (jb.write_header && l == 0) write_stream_header(jb.stream, BITS, jb.chunk_symbols);
+      }
       // arrival: the last of the workgroup's K waves publishes its keys
       lds_order();
       uint32_t v = 0;
-      if (l == 0) v = __hip_atomic_fetch_add(&karr[p], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (l == 0) v = __hip_atomic_fetch_add(&karr[p3], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       v = __builtin_amdgcn_readfirstlane(v);
       if (v == (uint32_t)(kn - 1)) {
-        if (l == 0) karr[p] = 0;
-        const int gws = rc.kgroup >> 16;
-        if (gws > 1) {
+        if (l == 0) karr[p3] = 0;
+        if ((rc.kgroup >> 16) > 1) {
           unsigned long long* kk = a.keys + (int64_t)rc.kslot * 2 * D;
           const unsigned long long tag = (unsigned long long)epoch << 32;
           for (int e = l; e < 2 * D; e += 64) {
@@ -401,93 +642,27 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
           if (l == 0)
             __hip_atomic_store(a.flags + (int64_t)s * grid + wg, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        // a group of one workgroup keeps its final keys in lkey[p3] for P3 of step s + 1
+        // a group of one workgroup keeps its final keys in lkey[p3] for the claim
         lds_order();
-        if (l == 0) __hip_atomic_store(&kfinal, (uint32_t)(s + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (l == 0) __hip_atomic_store(&kfin[p3], (uint32_t)(s + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
     }
 
     // ------------------------------------------------ P3: K quantization of step s - 1
     const int knp = rp.kjob >= 0 ? (rp.khead >> 8) : 0;
     if (wave < knp) {
-      const kvmi_layer_job jb = load_job(a.jobs, rp.kjob);
-      const int pp = (s - 1) % 3, hk = rp.khead & 0xff, T = jb.num_blocks * S;
-      uint32_t old = 0;
-      if (l == 0) old = __hip_atomic_fetch_max(&kclaim, (uint32_t)s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      old = __builtin_amdgcn_readfirstlane(old);
-      if (old < (uint32_t)s) {
-        // the first wave here: wait for the group, then the constants of its channels
-        const int gw0 = rp.kgroup & 0xffff, gws = rp.kgroup >> 16;
-        if (gws > 1) {
-          const uint32_t* fl = a.flags + (int64_t)(s - 1) * grid + gw0;
-          bool done = false;
-          for (uint32_t polls = 0; !broken && polls < kMaxPolls; ++polls) {
-            bool ok = true;
-            for (int w = l; w < gws; w += 64)
-              ok &= __hip_atomic_load(fl + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
-            if (__all(ok)) {
-              done = true;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-          }
-          if (!done) {
-            broken = true;
-            if (l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
-          }
-        } else if (!lds_wait(&kfinal, (uint32_t)s) && l == 0) {  // step s - 1's keys are final (kfinal = s)
-          atomicOr(a.err, KVMI_ERR_SYNC);
-        }
-        int jk = 0;
-        for (int k = 0; k < H; ++k)
-          if (cld(jb.profile + k) == hk) jk = k;
-        const int lv = cld(jb.profile + H + jk);
-        const unsigned long long* kk = a.keys + (int64_t)rp.kslot * 2 * D;
-        bool stale = false;
-        for (int e = l; e < D; e += 64) {
-          uint32_t kmn, kmx;
-          if (gws > 1) {
-            const unsigned long long vmn = __hip_atomic_load(kk + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned long long vmx = __hip_atomic_load(kk + D + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            stale |= (uint32_t)(vmn >> 32) != epoch || (uint32_t)(vmx >> 32) != epoch;
-            kmn = ~(uint32_t)vmn;
-            kmx = (uint32_t)vmx;
-          } else {
-            kmn = lkey[pp][e];
-            kmx = lkey[pp][D + e];
-            lkey[pp][e] = 0xffffffffu;
-            lkey[pp][D + e] = 0u;
-          }
-          const float mn = round_bf16(key2f(kmn) * sc_d);
-          const float mx = round_bf16(key2f(kmx) * sc_d);
-          const float scl = quant_scale(mn, mx, lv);
-          kc[p][e] = make_float2(mn, 1.0f / scl);
-          if (rp.ktile0 == 0 && T > 0) {  // the group's first workgroup writes the K metadata
-            gst(jb.kmeta + jk * D + e, (uint16_t)f32_to_bf16_bits(mn));
-            gst(jb.kmeta + HD + jk * D + e, (uint16_t)f32_to_bf16_bits(scl));
-          }
-        }
-        if (stale && !broken) atomicOr(a.err, KVMI_ERR_SYNC);
-        if (l == 0) {
-          kinfo[p][0] = jk;
-          kinfo[p][1] = lv;
-        }
-        lds_order();
-        if (l == 0) __hip_atomic_store(&kready, (uint32_t)s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      } else if (!lds_wait(&kready, (uint32_t)s) && l == 0) {
-        atomicOr(a.err, KVMI_ERR_SYNC);
-      }
-      const int tt = rp.ktile0 + wave;
-      if (32 * tt < T) {
-        const int jk = kinfo[p][0];
-        const float lvk = (float)kinfo[p][1];
-#pragma unroll
-        for (int u = 0; u < U; ++u) pin(prev[u]);
+      const int e = s & 3;
+      if (!lds_wait(&kready[e], (uint32_t)s) && l == 0) atomicOr(a.err, KVMI_ERR_SYNC);
+      const kvmi_layer_job jb = uni(TP.kj);
+      const int T_ = jb.num_blocks * S, tt = rp.ktile0 + wave;
+      if (32 * tt < T_) {
+        const int jk = uni(TP.kjk);
+        const float lvk = (float)uni(TP.kjlv);
         LanePack<HALF, BITS> pkd;
-        quant_k_tile<NC, BITS, CLAMP>(prev, hpT, hnT, &kc[p][0] + opaque(HALF * hl), sc_d, lvk, pkd, over);
+        quant_k_tile_pipe<NC, BITS, CLAMP>(prev, hpT, hnT, &kc[e][0] + opaque(HALF * hl), sc_d, lvk, pkd, over);
         pkd.store_lds(ost + r * RB + hl * (RB / 2));
         // rows 0 .. nv - 1 of the head-tile exist (nv a multiple of S, or 32)
-        const int nv = min(32, T - 32 * tt), t0 = 32 * tt;
+        const int nv = min(32, T_ - 32 * tt), t0 = 32 * tt;
         if (!native) {  // one run of nv rows of the head's stream
           uint4* dst = reinterpret_cast<uint4*>(seg_addr<BITS>(jb, g, 0, jk, t0, 0));
           const int nq = nv * RB / 16;
@@ -502,40 +677,46 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
         }
       }
     }
-
     // next step's K tile, into the registers of the tile just quantized
-    issue_k(rn, prev);
+    wait_tables(s + 1);
+    const StepTables& TN = tab[(s + 1) & (NSET - 1)];
+    k_fire(TN, s + 1 < steps, prev);
 
     // ------------------------------------------------ P2: V encode of step s
     if (rc.vjob >= 0 && wave < rc.vn) {
-      const kvmi_layer_job jv = load_job(a.jobs, rc.vjob);
-      const int ntok = jv.num_blocks * S, vt = rc.vtile0 + wave;
-      if (vt * kTok < ntok * H) {
-        const StepTables& T = tab[p3];
-        const int ta = vt * tpt;
-#pragma unroll
-        for (int u = 0; u < U; ++u) pin(vb[u]);
+      const int64_t row0 = uni(T.vrow[wave]);
+      if (row0 >= 0) {
+        const kvmi_layer_job jv = uni(T.vj);
+        const int ntok = jv.num_blocks * S, ta = (rc.vtile0 + wave) * tpt;
         tile_to_half_rows<NC>(wb, vb);
         sign_half_row<NC>(T, hme, hl, vb);
         const LaneProfile lp = lane_profile(T, hme, hl);
         LanePack<HALF, BITS> pkd;
-        quant_v_tile_lds<NC, BITS, CLAMP>(vb, hpT, hnT, lp, jv, ntok, ta + r / H, G, H, sc_d, wb + l, pkd, over);
-        const int off = native ? (r / H) * (H * RB) + lp.jv * RB + hl * (RB / 2)
-                               : lp.jv * (tpt * RB) + (r / H) * RB + hl * (RB / 2);
+        quant_v_tile_pipe<NC, BITS, CLAMP>(vb, hpT, hnT, lp, jv, ntok, ta + rtok, G, H, sc_d, wb + l, pkd, over);
+        const int off = native ? rtok * (H * RB) + lp.jv * RB + hl * (RB / 2)
+                               : ((lp.jv * kTok * RB) >> lgH) + rtok * RB + hl * (RB / 2);
         pkd.store_lds(ost + off);
-        const int rq = native ? TQ : tpt * RB / 16;  // uint4 per run
+        // staged image: one run of the tile's tokens per output position (permuted,
+        // 32 RB / H bytes each, run j at stream offset j * ntok * RB) or the tile's rows
+        // in order (native); 16-byte pieces, lane-linear
+        uint8_t* vbase = seg_addr<BITS>(jv, g, 1, 0, ta, 0);
+        const int64_t jstride = (int64_t)ntok * RB;
 #pragma unroll
         for (int u = 0; u < (TQ + 63) / 64; ++u) {
           const int q = 64 * u + l;
           if (TQ % 64 == 0 || q < TQ) {
-            const int run_j = q / rq;
-            uint8_t* dst = seg_addr<BITS>(jv, g, 1, native ? 0 : run_j, ta, 0) + 16 * (q - run_j * rq);
-            gst(reinterpret_cast<uint4*>(dst), wb[q]);
+            int64_t o = 16 * q;
+            if (!native) {
+              const int run_j = (q << (lgH + 4)) / (kTok * RB);  // byte 16 q of runs of 32 RB / H bytes
+              o += run_j * (jstride - ((kTok * RB) >> lgH));
+            }
+            gst(reinterpret_cast<uint4*>(vbase + o), wb[q]);
           }
         }
       }
     }
-    issue_v(rn, vb);
+    v_fire(TN, s + 1 < steps, vb);
+    if (rc.kjob >= 0) claim(s, rc, T);
     lds_signal(&fin);
   };
 
