@@ -140,7 +140,9 @@ def test_batch_of_variable_requests_equals_single_plans_and_oracle(cuda):
     pools, reqs = _small_requests(cuda, g, [3, 7, 12, 1], L, H, D, S, P)
     codec = FusedKVCodec(H, D, S, 4, 0xC0FEBABE)
     bplan = codec.plan_compress_batch([(pools, ids.to(cuda), prof) for ids, prof in reqs])
-    assert bplan.launches() == ["kvmi_check_block_ids", "kvmi_kstats_paged", "kvmi_encode_paged"]
+    # requests of up to 192 tokens: every K group fits one workgroup, so the default
+    # ("auto") compresses them in one pass
+    assert bplan.launches() == ["kvmi_check_block_ids", "kvmi_compress_paged"]
     assert bplan.num_jobs == L * len(reqs)
     bplan.run()
     for pk in bplan.packets:
@@ -257,38 +259,44 @@ def _full_run(codec, pools, ids, prof, layer_ids, sample):
     return packet
 
 
-def test_config2_full_size_sampled_layers_match_oracle(cuda):
+# The full-size configurations run through the default compress path ("auto": two
+# passes for long requests, one pass where every K group fits one workgroup) and
+# through the other one.
+@pytest.mark.parametrize("path", ["auto", "one_pass"])
+def test_config2_full_size_sampled_layers_match_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec
     from kvserve_amd.workloads import make_config2
 
     wl = make_config2(device=cuda)
     req = wl.requests[0]
-    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed)
+    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed, compress_path=path)
     packet = _full_run(codec, req.pools, req.block_ids, req.profiles, req.layer_ids, [0, 17, 31])
     assert packet.chunks == [(0, 8), (8, 16), (16, 24), (24, 32)]
     del wl, req, packet
     _free()
 
 
-def test_config4_full_size_sampled_layers_match_oracle(cuda):
+@pytest.mark.parametrize("path", ["auto", "one_pass"])
+def test_config4_full_size_sampled_layers_match_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec
     from kvserve_amd.workloads import make_config4
 
     wl = make_config4(device=cuda)
     req = wl.requests[0]
-    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed)
+    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed, compress_path=path)
     packet = _full_run(codec, req.pools, req.block_ids, req.profiles, req.layer_ids, [0, 1, 79])
     assert len(packet.chunks) == 10
     del wl, req, packet
     _free()
 
 
-def test_config3_full_size_batch_sampled_matches_oracle(cuda):
+@pytest.mark.parametrize("path", ["auto", "one_pass"])
+def test_config3_full_size_batch_sampled_matches_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.workloads import make_config3
 
     wl = make_config3(device=cuda)
-    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed)
+    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed, compress_path=path)
     reqs = wl.requests
     bplan = codec.plan_compress_batch([(r.pools, r.block_ids, r.profiles, r.layer_ids) for r in reqs])
     bplan.run()
@@ -313,15 +321,18 @@ def test_config3_full_size_batch_sampled_matches_oracle(cuda):
     _free()
 
 
-def test_config5_full_size_batch_sampled_matches_oracle(cuda):
+@pytest.mark.parametrize("path", ["auto", "two_pass"])
+def test_config5_full_size_batch_sampled_matches_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.workloads import make_config5
 
     wl = make_config5(device=cuda)
-    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed)
+    codec = FusedKVCodec(wl.num_heads, wl.head_dim, wl.block_size, wl.bits, wl.seed, compress_path=path)
     reqs = wl.requests
     bplan = codec.plan_compress_batch([(r.pools, r.block_ids, r.profiles, r.layer_ids) for r in reqs])
     assert bplan.num_jobs == 256 * 16
+    # 256-token requests: the default takes the one-pass kernel
+    assert bplan.launches()[-1] == ("kvmi_compress_paged" if path == "auto" else "kvmi_encode_paged")
     bplan.run()
     for pk in bplan.packets:
         check_packet(pk)
