@@ -247,6 +247,9 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  * KVMI_F_TWO_PASS), the device has no cooperative launch, or one head of a job has more
  * K than the grid holds (8 head-tiles of 32 tokens per workgroup: 65,536 tokens on 256
  * CUs); a negative KVMI_* code on bad arguments.  num_blocks: host array, B of each job.
+ * The image's int32 at byte offset 36 counts the K groups that span several workgroups
+ * (each needs a device barrier); 0 means every group fits one workgroup, where the one
+ * pass is faster than the two on MI355X.
  *
  * kvmi_compress_workspace_bytes: device bytes the workspace of a schedule needs.
  *
