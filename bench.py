@@ -1072,9 +1072,9 @@ def main() -> int:
     ap.add_argument("--rt-block-size", type=int, default=1, help="(runtime) tokens per block; 1 = token view")
     ap.add_argument("--rt-blocks", type=int, default=1024, help="(runtime) blocks per chunk")
     ap.add_argument("--rt-layers", type=int, default=28, help="(runtime) layers")
-    ap.add_argument("--compress-path", default=None, choices=["auto", "two_pass", "one_pass"],
-                    help="compress kernels: auto (default: one pass where every K group fits one workgroup), "
-                         "two_pass, or one_pass (kvmi_compress_paged, K read once)")
+    ap.add_argument("--compress-path", default=None, choices=["two_pass", "one_pass"],
+                    help="compress kernels: two_pass (the engine's default) or one_pass "
+                         "(kvmi_compress_paged, K read once)")
     ap.add_argument("--settle-curve", action="store_true",
                     help="only print the per-window step times over the first ~300 ms of load after idle")
     ap.add_argument("--copy-calibration", action="store_true",

@@ -248,8 +248,7 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  * K than the grid holds (8 head-tiles of 32 tokens per workgroup: 65,536 tokens on 256
  * CUs); a negative KVMI_* code on bad arguments.  num_blocks: host array, B of each job.
  * The image's int32 at byte offset 36 counts the K groups that span several workgroups
- * (each needs a device barrier); 0 means every group fits one workgroup, where the one
- * pass is faster than the two on MI355X.
+ * (each needs a device barrier); 0 means every group fits one workgroup.
  *
  * kvmi_compress_workspace_bytes: device bytes the workspace of a schedule needs.
  *

@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
   // filled for, so no flag is ever cleared and every wait is "flag >= value".
   __shared__ StepTables tab[NSET];
   __shared__ uint32_t lkey[4][2 * D];     // the workgroup's min / max keys of a step's K group
-  __shared__ float2 kc[4][D + 4];         // (min, 1/scale) per channel of the group quantized in step q
+  __shared__ float2 kc[4][D + 4];         // (min, -1/scale) per channel of the group quantized in step q
   __shared__ uint4 wbuf[kOW * tile_buf_q<NC>()];
   __shared__ uint32_t tready[NSET];       // step + 1 of the tables in each set
   __shared__ uint32_t karr[4], kfin[4];   // K waves arrived in step s; step + 1 once its keys are final
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
   // ---------------------------------------------------------------- K constants
   // The constants of step s's K group (used in step s + 1), by the first wave to finish
   // step s: once the group's keys are final (this workgroup's arrivals, or every
-  // workgroup's flag), per-channel (min, 1/scale) into kc[(s + 1) % 4] and the K metadata
+  // workgroup's flag), per-channel (min, -1/scale) into kc[(s + 1) % 4] and the K metadata
   // (the group's first workgroup).
   auto claim = [&](int s, const OpRec& rc, const StepTables& T) {
     const int q = s + 1, e = q & 3, pk3 = s & 3;
@@ -548,7 +548,7 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
       const float mn = round_bf16(key2f(kmn) * sc_d);  // keys are unscaled
       const float mx = round_bf16(key2f(kmx) * sc_d);
       const float scl = quant_scale(mn, mx, lv);
-      kc[e][c] = make_float2(mn, 1.0f / scl);
+      kc[e][c] = make_float2(mn, -1.0f / scl);
       if (rc.ktile0 == 0 && T_ > 0) {  // the group's first workgroup writes the K metadata
         gst(kmeta + jk * D + c, (uint16_t)f32_to_bf16_bits(mn));
         gst(kmeta + HD + jk * D + c, (uint16_t)f32_to_bf16_bits(scl));

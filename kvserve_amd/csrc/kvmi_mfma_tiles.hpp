@@ -172,6 +172,26 @@ __device__ __forceinline__ float add_hi(uint32_t pk, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, pk), sgpr_pair(0x3F800000u), c, false);
 }
 
+// (rbf(c0 - lo(pk)), rbf(c1 - hi(pk))) for a bf16 pair pk and bf16-valued c0, c1: the
+// differences by v_dot2_f32_bf16 against (-1, 0) / (0, -1), each rounded to bf16 by
+// v_cvt_pk_bf16_f32 with a zero low half (see rbf).  The same argument as for add_lo
+// holds (both terms bf16 values, the sum rounded to bf16 next).  A dot instruction's
+// result may be read by another VALU instruction only 3 wait states after it: the
+// compiler pads that for the instructions it emits itself, not for the reads inside an
+// asm statement, so the pair is written out with its padding (the second dot and an
+// s_nop 1 before the first read, the s_nop and the first conversion before the second).
+// Outputs are early-clobber: the first difference is written before the second dot
+// reads pk and c1.
+__device__ __forceinline__ void rsub_rbf_pair(uint32_t pk, float c0, float c1, float& t0, float& t1) {
+  asm("v_dot2_f32_bf16 %0, %2, %3, %5\n\t"
+      "v_dot2_f32_bf16 %1, %2, %4, %6\n\t"
+      "s_nop 1\n\t"
+      "v_cvt_pk_bf16_f32 %0, 0, %0\n\t"
+      "v_cvt_pk_bf16_f32 %1, 0, %1"
+      : "=&v"(t0), "=&v"(t1)
+      : "v"(pk), "s"(sgpr_pair(0x0000BF80u)), "s"(sgpr_pair(0xBF800000u)), "v"(c0), "v"(c1));
+}
+
 // fp32 value of x rounded to bf16 (round to nearest even) in one instruction:
 // v_cvt_pk_bf16_f32 with a zero low half leaves bf16(x) << 16, which is that value.
 __device__ __forceinline__ float rbf(float x) {
@@ -292,7 +312,7 @@ constexpr uint32_t overflow_mask() {
 template <int HM>
 struct TablesT {
   uint32_t smask[HM][64 + 4];  // bf16 sign-flip masks per (head, element pair), padded rows
-  float2 kc[HM][128 + 4];      // K (min, 1/scale) [encode] or (min, scale) [decode], by source head
+  float2 kc[HM][128 + 4];      // K (min, -1/scale) [encode] or (min, scale) [decode], by source head
   uint8_t prof[2][3][HM];      // the job's profile bytes (kvmi_layer_job::profile)
   int posk[HM], posv[HM], gfirst[HM];
 };
@@ -352,7 +372,7 @@ __device__ __forceinline__ void fill_positions(TT& T, int H) {
 }
 
 // K constants by source head from kmeta (stored by output position j, whose source
-// head is order[j]).  DIV: store (min, 1/scale) instead of (min, scale).
+// head is order[j]).  DIV: store (min, -1/scale) (the quantizer's form) instead of (min, scale).
 template <bool DIV, class TT>
 __device__ __forceinline__ void fill_kconst(TT& T, const uint16_t* kmeta, int H, int D) {
   const int HD = H * D;
@@ -360,7 +380,7 @@ __device__ __forceinline__ void fill_kconst(TT& T, const uint16_t* kmeta, int H,
     const int j = i / D, e = i % D, hs = T.prof[0][0][j];
     const float m = bf16_to_f32(gld(kmeta + i));
     const float sc = bf16_to_f32(gld(kmeta + HD + i));
-    T.kc[hs][e] = make_float2(m, DIV ? 1.0f / sc : sc);
+    T.kc[hs][e] = make_float2(m, DIV ? -1.0f / sc : sc);
   }
 }
 
@@ -519,7 +539,7 @@ __device__ __forceinline__ void pack_chunk(const float (&q)[16], int cp, LanePac
 }
 
 // Quantize output chunk cp (16 accumulators of the lane's half-row) with per-element
-// (min, 1/scale) pairs from the LDS table at kq (K: per-channel statistics).
+// (min, -1/scale) pairs from the LDS table at kq (K: per-channel statistics).
 template <int HALF, int BITS, bool CLAMP>
 __device__ __forceinline__ void quant_chunk_k(const f32x16& acc, int cp, float s, const float2* kq, float lv,
                                               LanePack<HALF, BITS>& pk, uint32_t& over) {
@@ -527,8 +547,13 @@ __device__ __forceinline__ void quant_chunk_k(const f32x16& acc, int cp, float s
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
     const float4 c = *reinterpret_cast<const float4*>(kq + i);
-    q[i] = quant_q(acc[i], s, c.x, c.y);
-    q[i + 1] = quant_q(acc[i + 1], s, c.z, c.w);
+    // y pair rounded by one v_cvt_pk_bf16_f32; with c = (mn, -1/scale), and negation
+    // commuting with round-to-nearest-even: rbf(rbf(mn - y) * -rcp) == rbf(rbf(y - mn) * rcp)
+    const uint32_t y2 = pack_bf16x2(acc[i] * s, acc[i + 1] * s);
+    float t0, t1;
+    rsub_rbf_pair(y2, c.x, c.z, t0, t1);
+    q[i] = rbf(t0 * c.y);
+    q[i + 1] = rbf(t1 * c.w);
     if constexpr (CLAMP) {
       q[i] = fminf(q[i], lv);
       q[i + 1] = fminf(q[i + 1], lv);
@@ -542,12 +567,14 @@ __device__ __forceinline__ void quant_chunk_k(const f32x16& acc, int cp, float s
 template <int HALF, int BITS, bool CLAMP>
 __device__ __forceinline__ void quant_chunk_v(const uint32_t* ypk, int cp, float mn, float rcp, float lv,
                                               LanePack<HALF, BITS>& pk, uint32_t& over) {
+  const float nrcp = -rcp;
   float q[16];
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
-    const uint32_t y2 = ypk[i / 2];
-    q[i] = rbf(rbf(bf_lo(y2) - mn) * rcp);
-    q[i + 1] = rbf(rbf(bf_hi(y2) - mn) * rcp);
+    float t0, t1;
+    rsub_rbf_pair(ypk[i / 2], mn, mn, t0, t1);
+    q[i] = rbf(t0 * nrcp);
+    q[i + 1] = rbf(t1 * nrcp);
     if constexpr (CLAMP) {
       q[i] = fminf(q[i], lv);
       q[i + 1] = fminf(q[i + 1], lv);

@@ -181,15 +181,13 @@ class FusedKVCodec:
         self.fwht = (fwht or os.environ.get("KVSERVE_AMD_FWHT", "mfma")).strip().lower()
         if self.fwht not in ("mfma", "valu", "rows"):
             raise ValueError("fwht must be 'mfma', 'valu' or 'rows'")
-        # compress: "one_pass" (kvmi_compress_paged: every K value read from HBM once
-        # where the jobs fit the one-pass kernel), "two_pass" (kvmi_kstats_paged +
-        # kvmi_encode_paged, K read twice) or "auto" (the default: one pass where every K
-        # group of the plan fits one workgroup, so the pass needs no barrier across
-        # workgroups, e.g. requests of up to 256 tokens; two passes otherwise, the faster
-        # on MI355X for long requests); KVSERVE_AMD_COMPRESS overrides the default
-        self.compress_path = (compress_path or os.environ.get("KVSERVE_AMD_COMPRESS", "auto")).strip().lower()
-        if self.compress_path not in ("one_pass", "two_pass", "auto"):
-            raise ValueError("compress_path must be 'one_pass', 'two_pass' or 'auto'")
+        # compress: "two_pass" (the default: kvmi_kstats_paged + kvmi_encode_paged, K read
+        # twice; the faster on MI355X for short and long requests alike) or "one_pass"
+        # (kvmi_compress_paged: every K value read from HBM once where the jobs fit the
+        # one-pass kernel); KVSERVE_AMD_COMPRESS overrides the default
+        self.compress_path = (compress_path or os.environ.get("KVSERVE_AMD_COMPRESS", "two_pass")).strip().lower()
+        if self.compress_path not in ("one_pass", "two_pass"):
+            raise ValueError("compress_path must be 'one_pass' or 'two_pass'")
         self._lib = _lib.load()
         self._prof_cache: Dict[tuple, torch.Tensor] = {}
         self._prof_valid: set = set()
@@ -567,8 +565,7 @@ class Plan:
         """Schedule and workspace of kvmi_compress_paged, built once per plan: the host
         schedule image (from every job's block count) and a device workspace holding a
         copy of it followed by zeroed barrier flags, keys and epoch.  No schedule (the
-        one-pass kernel does not take these jobs, or "auto" and a K group spans several
-        workgroups): the plan runs the two passes."""
+        one-pass kernel does not take these jobs): the plan runs the two passes."""
         self.schedule, self.workspace = None, None
         if self.kind != "compress" or self.codec.compress_path == "two_pass" or self.max_blocks == 0:
             return
@@ -582,8 +579,6 @@ class Plan:
         img = np.zeros(n, dtype=np.uint8)
         _lib.check(min(0, int(lib.kvmi_compress_schedule(geo, nb.ctypes.data, self.num_jobs, img.ctypes.data, n))),
                    "kvmi_compress_schedule")
-        if self.codec.compress_path == "auto" and int(np.frombuffer(img[36:40].tobytes(), dtype=np.int32)[0]) > 0:
-            return  # the schedule's device key slots: some K group needs a barrier across workgroups
         total = int(lib.kvmi_compress_workspace_bytes(img.ctypes.data))
         ws = torch.zeros(total, dtype=torch.uint8, device=self.device)
         stage = self.codec._staging(n)

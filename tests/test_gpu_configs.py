@@ -138,10 +138,9 @@ def test_batch_of_variable_requests_equals_single_plans_and_oracle(cuda):
     g = torch.Generator().manual_seed(31)
     L, H, D, S, P = 4, 8, 128, 16, 64
     pools, reqs = _small_requests(cuda, g, [3, 7, 12, 1], L, H, D, S, P)
-    codec = FusedKVCodec(H, D, S, 4, 0xC0FEBABE)
+    codec = FusedKVCodec(H, D, S, 4, 0xC0FEBABE, compress_path="one_pass")
     bplan = codec.plan_compress_batch([(pools, ids.to(cuda), prof) for ids, prof in reqs])
-    # requests of up to 192 tokens: every K group fits one workgroup, so the default
-    # ("auto") compresses them in one pass
+    # requests of up to 192 tokens, compressed in one pass
     assert bplan.launches() == ["kvmi_check_block_ids", "kvmi_compress_paged"]
     assert bplan.num_jobs == L * len(reqs)
     bplan.run()
@@ -259,10 +258,9 @@ def _full_run(codec, pools, ids, prof, layer_ids, sample):
     return packet
 
 
-# The full-size configurations run through the default compress path ("auto": two
-# passes for long requests, one pass where every K group fits one workgroup) and
-# through the other one.
-@pytest.mark.parametrize("path", ["auto", "one_pass"])
+# The full-size configurations run through both compress paths (the default two
+# passes, and the one-pass kernel).
+@pytest.mark.parametrize("path", ["two_pass", "one_pass"])
 def test_config2_full_size_sampled_layers_match_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec
     from kvserve_amd.workloads import make_config2
@@ -276,7 +274,7 @@ def test_config2_full_size_sampled_layers_match_oracle(cuda, path):
     _free()
 
 
-@pytest.mark.parametrize("path", ["auto", "one_pass"])
+@pytest.mark.parametrize("path", ["two_pass", "one_pass"])
 def test_config4_full_size_sampled_layers_match_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec
     from kvserve_amd.workloads import make_config4
@@ -290,7 +288,7 @@ def test_config4_full_size_sampled_layers_match_oracle(cuda, path):
     _free()
 
 
-@pytest.mark.parametrize("path", ["auto", "one_pass"])
+@pytest.mark.parametrize("path", ["two_pass", "one_pass"])
 def test_config3_full_size_batch_sampled_matches_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.workloads import make_config3
@@ -321,7 +319,7 @@ def test_config3_full_size_batch_sampled_matches_oracle(cuda, path):
     _free()
 
 
-@pytest.mark.parametrize("path", ["auto", "two_pass"])
+@pytest.mark.parametrize("path", ["two_pass", "one_pass"])
 def test_config5_full_size_batch_sampled_matches_oracle(cuda, path):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.workloads import make_config5
@@ -331,8 +329,7 @@ def test_config5_full_size_batch_sampled_matches_oracle(cuda, path):
     reqs = wl.requests
     bplan = codec.plan_compress_batch([(r.pools, r.block_ids, r.profiles, r.layer_ids) for r in reqs])
     assert bplan.num_jobs == 256 * 16
-    # 256-token requests: the default takes the one-pass kernel
-    assert bplan.launches()[-1] == ("kvmi_compress_paged" if path == "auto" else "kvmi_encode_paged")
+    assert bplan.launches()[-1] == ("kvmi_compress_paged" if path == "one_pass" else "kvmi_encode_paged")
     bplan.run()
     for pk in bplan.packets:
         check_packet(pk)

@@ -5,7 +5,7 @@ contents (a smaller K range) before each repeated call, so keys or barrier flags
 an earlier call would show.  The two-pass path is pinned to the oracle by
 test_gpu_codec.py and test_gpu_configs.py; test_one_pass_matches_oracle checks the
 one-pass output against the oracle directly, and test_gpu_configs.py runs the
-benchmark configurations through whichever path is the codec's default."""
+benchmark configurations (full size) through both paths against the oracle."""
 
 import ctypes
 
