@@ -312,9 +312,12 @@ int64_t kvmi_v3_scratch_bytes(int64_t rows, int32_t num_heads, int32_t head_dim)
  * held from the library's first use on that GPU until the process ends.  A call needs
  * min(ceil(rows*H/64), 256) * 8*H*D bytes of it (every H*D <= 2048 fits); larger
  * calls return KVMI_ENOSPC before enqueueing anything.  Every call on one GPU shares
- * that GPU's array, so calls that overlap on one GPU (different streams, or threads
- * without stream order) race; calls ordered on one stream do not.  Results are
- * identical to kvmi_v3_compress.
+ * that GPU's array, so the library puts the calls on one GPU in one order: each call's
+ * launches wait for the previous call's on that GPU (an event the library records after
+ * them, created with the array's address on the GPU's first call), whichever stream or
+ * host thread made it.  Calls enqueued under graph capture take no part in that order:
+ * a replayed graph that runs at the same time as another call on the same GPU races
+ * with it.  Results are identical to kvmi_v3_compress.
  */
 #define KVMI_V3_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)
 int kvmi_v3_compress_noalloc(const void* x, int64_t rows, int32_t num_heads, int32_t head_dim,

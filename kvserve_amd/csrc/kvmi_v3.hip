@@ -480,21 +480,33 @@ int v3_compress_args(const void* x, int64_t rows, int32_t H, int32_t D, const ui
 // comes from hipGetSymbolAddress (with that GPU current), once per device.
 static __device__ __align__(256) uint8_t scratch[KVMI_V3_NOALLOC_SCRATCH_BYTES];
 
+// Calls on one GPU share its array, so they are put in one order: each call's launches
+// wait (hipStreamWaitEvent) for the event recorded after the previous call's launches on
+// that GPU, whichever stream or host thread made it, and the mutex keeps the wait, the
+// launches and the record of one call together.  Launches enqueued under graph capture
+// take no part (an event of an eager call cannot be waited on inside a capture): a
+// replayed graph is ordered only by the stream it is launched on.
 constexpr int kMaxScratchDevices = 64;
+struct NoAllocSlot {
+  void* ptr = nullptr;         // device address of this GPU's copy of `scratch`
+  hipEvent_t done = nullptr;   // recorded after the last eager call's launches
+  bool recorded = false;
+};
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxScratchDevices];
+NoAllocSlot g_scratch[kMaxScratchDevices];
 
-// Device address of the current GPU's copy of `scratch` (null on failure).
-void* noalloc_scratch() {
+// The current GPU's slot, set up on its first use (null on failure); g_scratch_mu held.
+NoAllocSlot* noalloc_slot() {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return nullptr;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  NoAllocSlot& sl = g_scratch[dev];
+  if (!sl.ptr) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
-    g_scratch_ptr[dev] = p;
+    if (hipEventCreateWithFlags(&sl.done, hipEventDisableTiming) != hipSuccess) return nullptr;
+    sl.ptr = p;
   }
-  return g_scratch_ptr[dev];
+  return &sl;
 }
 
 }  // namespace
@@ -532,10 +544,21 @@ extern "C" int kvmi_v3_compress_noalloc(const void* x, int64_t rows, int32_t num
   // K partials of this call: v3_kgrid workgroups x 2 x H x D keys
   const int64_t need = (int64_t)v3_kgrid(rows, num_heads) * 2 * num_heads * head_dim * 4;
   if (need > KVMI_V3_NOALLOC_SCRATCH_BYTES) return KVMI_ENOSPC;
-  void* kpart = noalloc_scratch();
-  if (!kpart) return KVMI_ELAUNCH;
-  return v3_compress_launch(x, rows, num_heads, head_dim, signs, levels, vgroup, q, kmeta, vmeta,
-                            static_cast<uint32_t*>(kpart), reinterpret_cast<hipStream_t>(stream));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  NoAllocSlot* sl = noalloc_slot();
+  if (!sl) return KVMI_ELAUNCH;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess) return KVMI_ELAUNCH;
+  const bool ordered = cap == hipStreamCaptureStatusNone;
+  if (ordered && sl->recorded && hipStreamWaitEvent(st, sl->done, 0) != hipSuccess) return KVMI_ELAUNCH;
+  rc = v3_compress_launch(x, rows, num_heads, head_dim, signs, levels, vgroup, q, kmeta, vmeta,
+                          static_cast<uint32_t*>(sl->ptr), st);
+  if (rc == KVMI_OK && ordered) {
+    if (hipEventRecord(sl->done, st) != hipSuccess) return KVMI_ELAUNCH;
+    sl->recorded = true;
+  }
+  return rc;
 }
 
 extern "C" int kvmi_v3_decompress(const uint8_t* q, int64_t rows, int32_t num_heads, int32_t head_dim,

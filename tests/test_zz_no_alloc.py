@@ -2,7 +2,8 @@
 fixed device array instead of a caller workspace) against kvmi_v3_compress, both
 called through the C-ABI on the same inputs: quantized symbols, K and V metadata must be
 identical.  Two calls in a row, the second smaller than the first, so that the second
-runs on the scratch contents the first left behind."""
+runs on the scratch contents the first left behind; and two calls on two streams, the
+second enqueued right after the first, which the library must order."""
 
 import ctypes
 
@@ -60,3 +61,33 @@ def test_noalloc_matches_workspace_entry_point_twice(cuda):
     _run_pair(lib, cuda, 512, 16, 8, 128, seed=11)   # 256 K partials (2 MiB of the array)
     print("noalloc call 2: B=3 S=16 H=4 D=64", flush=True)
     _run_pair(lib, cuda, 3, 16, 4, 64, seed=12)      # 3 partials, over the first call's leftovers
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(cuda):
+    """Two large calls on two streams with no order between them given by the caller:
+    each must equal the workspace entry point's output (without the library's ordering
+    the second call's K partials would overwrite the first's while it still reads them)."""
+    lib = _lib.load()
+    H, D, rows = 8, 128, 512 * 16
+    runs = []
+    for seed in (21, 22):
+        x, signs, levels, vgroup = _inputs(cuda, 512, 16, H, D, seed)
+        runs.append((x, signs, levels, vgroup, _outputs(cuda, rows, H, D), _outputs(cuda, rows, H, D)))
+    ws = torch.empty(int(lib.kvmi_v3_scratch_bytes(rows, H, D)), dtype=torch.uint8, device=cuda)
+    cur = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for x, signs, levels, vgroup, (q0, k0, v0), _ in runs:
+        _lib.check(lib.kvmi_v3_compress(x.data_ptr(), rows, H, D, signs.data_ptr(), levels.data_ptr(),
+                                        vgroup.data_ptr(), q0.data_ptr(), k0.data_ptr(), v0.data_ptr(), ws.data_ptr(),
+                                        cur), "kvmi_v3_compress")
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]  # default priority
+    print("noalloc two streams: B=512 S=16 H=8 D=128 x2", flush=True)
+    for st, (x, signs, levels, vgroup, _, (q1, k1, v1)) in zip(streams, runs):
+        _lib.check(lib.kvmi_v3_compress_noalloc(x.data_ptr(), rows, H, D, signs.data_ptr(), levels.data_ptr(),
+                                                vgroup.data_ptr(), q1.data_ptr(), k1.data_ptr(), v1.data_ptr(),
+                                                ctypes.c_void_p(st.cuda_stream)), "kvmi_v3_compress_noalloc")
+    torch.cuda.synchronize()
+    for _, _, _, _, (q0, k0, v0), (q1, k1, v1) in runs:
+        assert torch.equal(q0, q1)
+        assert torch.equal(k0.view(torch.int32), k1.view(torch.int32))
+        assert torch.equal(v0.view(torch.int32), v1.view(torch.int32))
