@@ -61,6 +61,7 @@ typedef struct ihipStream_t* kvmi_stream_t;
 #define KVMI_ERR_CORRUPT 4      /* an entropy-coded block does not decode consistently */
 #define KVMI_ERR_SYNC 8         /* a one-pass compress barrier timed out or met another call's keys */
 #define KVMI_ERR_BLOCK_ID 16    /* a block id outside its pool (kvmi_check_block_ids) */
+#define KVMI_ERR_SCHEDULE 32    /* a job has more blocks than its one-pass schedule */
 
 /* Host-visible return codes. */
 #define KVMI_OK 0
@@ -262,7 +263,9 @@ int kvmi_encode_paged(const kvmi_geometry* geom, const kvmi_layer_job* jobs, int
  *   in a graph).  Calls sharing a workspace must be ordered on one stream.  From 2^31
  *   calls on one workspace on, KVMI_ERR_SYNC is set: initialise the workspace again.
  *   A schedule built for other jobs or another device returns KVMI_EINVAL (the jobs'
- *   num_blocks may be lower than the schedule's: the kernel skips missing tiles).
+ *   num_blocks may be lower than the schedule's: the kernel skips missing tiles; a job
+ *   with more blocks than the schedule's sets KVMI_ERR_SCHEDULE, and the blocks past
+ *   the schedule's are not compressed).
  * A barrier that does not complete within about 0.3 s sets KVMI_ERR_SYNC (the
  * kernel still ends; later barriers of the launch then no longer wait).
  */

@@ -21,6 +21,7 @@ ERR_BAD_HEADER = 2
 ERR_CORRUPT = 4
 ERR_SYNC = 8
 ERR_BLOCK_ID = 16
+ERR_SCHEDULE = 32
 OK, EINVAL, ELAUNCH, ENOSPC = 0, -22, -5, -28
 # Bytes of the fixed device array behind kvmi_v3_compress_noalloc (per GPU).
 V3_NOALLOC_SCRATCH_BYTES = 4 * 1024 * 1024

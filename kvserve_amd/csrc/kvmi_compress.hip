@@ -75,6 +75,7 @@ struct OpHeader {
   int32_t nslots;
   int64_t rec_off, flag_off, key_off, epoch_off, total;
   int64_t image_bytes;
+  int64_t blk_off;  // int32 [num_jobs]: the blocks of each job the schedule was built for
 };
 constexpr int64_t kHeaderBytes = 256;
 static_assert(sizeof(OpHeader) <= kHeaderBytes, "header fits its slot");
@@ -90,6 +91,7 @@ struct OpArgs {
   unsigned long long* keys;  // [nslots][2][D]
   const uint32_t* epoch;     // advanced by onepass_epoch_kernel
   const uint16_t* dummy;     // 8 KiB of readable memory for the loads of idle waves
+  const int32_t* sched_blocks;  // [num_jobs] blocks per job in the schedule
   int steps, grid, num_jobs;
 };
 
@@ -581,6 +583,9 @@ __global__ __launch_bounds__(kOT) void onepass_kernel(OpArgs a) {
   if (threadIdx.x < 4) karr[threadIdx.x] = kfin[threadIdx.x] = 0;
   if (threadIdx.x < 4) kown[threadIdx.x] = kready[threadIdx.x] = 0;
   if (threadIdx.x == 0) fin = 0;
+  // a job with more blocks than the schedule holds would be compressed in part: flagged
+  for (int j = wg * kOT + (int)threadIdx.x; j < a.num_jobs; j += grid * kOT)
+    if (gld(&a.jobs[j].num_blocks) > gld(a.sched_blocks + j)) atomicOr(a.err, KVMI_ERR_SCHEDULE);
   // chunks of jobs without blocks still get their header (the stream of N = 0 symbols)
   if (wg == 0 && !(g.flags & KVMI_F_NO_HEADER)) {
     for (int j = threadIdx.x; j < a.num_jobs; j += kOT) {
@@ -876,7 +881,8 @@ extern "C" int64_t kvmi_compress_schedule(const kvmi_geometry* geom, const int32
   h.flags = g.flags;
   h.nslots = nslots;
   h.rec_off = kHeaderBytes;
-  h.image_bytes = h.rec_off + (int64_t)recs.size() * (int64_t)sizeof(OpRec);
+  h.blk_off = h.rec_off + (int64_t)recs.size() * (int64_t)sizeof(OpRec);
+  h.image_bytes = h.blk_off + 4 * (int64_t)num_jobs;
   h.flag_off = round256(h.image_bytes);
   h.key_off = round256(h.flag_off + (int64_t)steps * grid * 4);
   h.epoch_off = round256(h.key_off + (int64_t)nslots * 2 * g.D * 8);
@@ -886,6 +892,7 @@ extern "C" int64_t kvmi_compress_schedule(const kvmi_geometry* geom, const int32
     std::memset(image, 0, (size_t)kHeaderBytes);
     std::memcpy(image, &h, sizeof h);
     if (!recs.empty()) std::memcpy(static_cast<uint8_t*>(image) + h.rec_off, recs.data(), recs.size() * sizeof(OpRec));
+    if (num_jobs > 0) std::memcpy(static_cast<uint8_t*>(image) + h.blk_off, num_blocks, 4 * (size_t)num_jobs);
   }
   return h.image_bytes;
 }
@@ -934,6 +941,7 @@ extern "C" int kvmi_compress_paged(const kvmi_geometry* geom, const kvmi_layer_j
       a.keys = reinterpret_cast<unsigned long long*>(ws + h.key_off);
       a.epoch = reinterpret_cast<const uint32_t*>(ws + h.epoch_off);
       a.dummy = reinterpret_cast<const uint16_t*>(ws);
+      a.sched_blocks = reinterpret_cast<const int32_t*>(ws + h.blk_off);
       a.steps = h.steps;
       a.grid = h.grid;
       a.num_jobs = num_jobs;

@@ -686,6 +686,8 @@ def raise_device_error(code: int) -> None:
         raise IndexError("block id outside the KV cache")
     if code & _lib.ERR_SYNC:
         raise RuntimeError("one-pass compress: a workgroup barrier timed out or met keys of another call")
+    if code & _lib.ERR_SCHEDULE:
+        raise RuntimeError("one-pass compress: a job has more blocks than its schedule")
 
 
 def check_packet(packet: Packet, force: bool = False) -> None:

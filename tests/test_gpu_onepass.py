@@ -190,6 +190,19 @@ def test_workspace_contract_through_the_c_abi(cuda):
     assert lib.kvmi_compress_paged(geo, plan.jobs.data_ptr(), plan.num_jobs - 1, plan.max_blocks, img.ctypes.data,
                                    ws.data_ptr(), plan.err.data_ptr(), stream) == _lib.EINVAL
     torch.cuda.synchronize()
+    # a schedule built for fewer blocks than the jobs hold: flagged on the device
+    nb_short = nb - 1
+    n2 = lib.kvmi_compress_schedule(geo, nb_short.ctypes.data, plan.num_jobs, None, 0)
+    img2 = np.zeros(n2, dtype=np.uint8)
+    assert lib.kvmi_compress_schedule(geo, nb_short.ctypes.data, plan.num_jobs, img2.ctypes.data, n2) == n2
+    ws2 = torch.zeros(lib.kvmi_compress_workspace_bytes(img2.ctypes.data), dtype=torch.uint8, device=cuda)
+    ws2[:n2].copy_(torch.from_numpy(img2))
+    plan.err.zero_()
+    assert lib.kvmi_compress_paged(geo, plan.jobs.data_ptr(), plan.num_jobs, plan.max_blocks, img2.ctypes.data,
+                                   ws2.data_ptr(), plan.err.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(plan.err.item()) == _lib.ERR_SCHEDULE
+    plan.err.zero_()
 
 
 @pytest.mark.parametrize("H,S,D,bits", [(8, 16, 128, 4), (4, 16, 64, 3)])
