@@ -307,35 +307,83 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   // The wave's parking buffer also turns each coalesced tile into the lanes' half-rows
   // (the V tile is rearranged before its rounded outputs are parked there).
   uint4* wbuf = ypark + wave * tile_buf_q<NC>();
+#ifndef KVMI_COOP_FLUSH
+#define KVMI_COOP_FLUSH 1
+#endif
+  // Permuted order: the workgroup's waves take consecutive tiles t0 .. t0 + 3, so head
+  // j's runs of the four tiles are consecutive in the stream; after a barrier the
+  // workgroup writes them as one run per head (4x longer runs than a wave's own flush),
+  // each thread a fixed set of 16-byte pieces.  Entry e of a thread: piece q = tid +
+  // kMW e of the 4 tiles' image, from wave w's buffer, to byte `dst` of head j's run.
+  const bool coop = KVMI_COOP_FLUSH && !native && !paired;
+  constexpr int QE = (4 * TQ + kMW - 1) / kMW;  // pieces per thread
+  int qsrc[QE], qw[QE];
+  int64_t qdst[QE];
+  {
+    const int rq = tpt * RB / 16;  // uint4 per tile run
+    const int64_t hs_bytes = (int64_t)ntok * RB;
+#pragma unroll
+    for (int e = 0; e < QE; ++e) {
+      const int q = (int)threadIdx.x + kMW * e;
+      const int j = q / (kWaves * rq), rem = q - j * (kWaves * rq), w = rem / rq;
+      qw[e] = q < kWaves * TQ ? w : kWaves;  // kWaves: no piece
+      qsrc[e] = w * tile_buf_q<NC>() + j * rq + (rem - w * rq);
+      qdst[e] = j * hs_bytes + 16 * rem;
+    }
+  }
+  auto flush_wg = [&](int part, int t0) {
+    const int na = min(kWaves, run.tiles - t0);
+    uint8_t* base = seg_addr<BITS, PAIRED>(job, g, part, 0, tile_tok(run.tok0, H, t0), 0);
+#pragma unroll
+    for (int e = 0; e < QE; ++e)
+      if (qw[e] < na) gst(reinterpret_cast<uint4*>(base + qdst[e]), ypark[qsrc[e]]);
+  };
+
   uint4 xk[2 * NC], xv[2 * NC];
-  if (wave < run.tiles) load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, wave)), xk);
-  for (int t = wave; t < run.tiles; t += kWaves) {
+  const int last_tile = run.tiles - 1;
+  load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, min(wave, last_tile))), xk);
+  const int niter = (run.tiles + kWaves - 1) / kWaves;  // the same for every wave (barriers)
+  for (int it = 0; it < niter; ++it) {
+    const int t = it * kWaves + wave;
+    const bool act = t < run.tiles;  // wave-uniform
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(xk[u]);
-    const int ta = tile_tok(run.tok0, H, t);
+    const int ta = tile_tok(run.tok0, H, act ? t : last_tile);
     const int64_t row0 = tile_row0(job, S, H, ta);
     const int tok = ta + r / H;
     load_tile<NC>(poolV, row0, xv);
     // ---------------- K: per-channel statistics from the kstats pass
-    {
+    if (act) {
       tile_to_half_rows<NC>(wbuf, xk);
       sign_half_row<NC>(T, hme, hl, xk);
       LanePack<HALF, BITS> pkd;
       quant_k_tile<NC, BITS, CLAMP>(xk, hp, hn, &T.kc[0][0] + opaque(hme * (128 + 4) + HALF * hl), s, lp.lvk, pkd,
                                     over, paired);
       pkd.store_lds(ost + offk);
-      flush(0, ta);
+      if (!coop) flush(0, ta);
     }
-    // next tile's K (unconditional: past the end it re-reads this tile, a cache hit)
-    const int tn = min(t + kWaves, run.tiles - 1);
+    if (coop) {
+      __syncthreads();
+      flush_wg(0, it * kWaves);
+      __syncthreads();
+    }
+    // next tile's K (unconditional: past the end it re-reads the last tile, a cache hit)
+    const int tn = min(t + kWaves, last_tile);
     load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)), xk);
     // ---------------- V: per-token statistics over the heads of a group
-    tile_to_half_rows<NC>(wbuf, xv);
-    sign_half_row<NC>(T, hme, hl, xv);
-    LanePack<HALF, BITS> pkd;
-    quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, wbuf + l, pkd, over, paired);
-    pkd.store_lds(ost + offv);
-    flush(1, ta);
+    if (act) {
+      tile_to_half_rows<NC>(wbuf, xv);
+      sign_half_row<NC>(T, hme, hl, xv);
+      LanePack<HALF, BITS> pkd;
+      quant_v_tile_lds<NC, BITS, CLAMP>(xv, hp, hn, lp, job, ntok, tok, G, H, s, wbuf + l, pkd, over, paired);
+      pkd.store_lds(ost + offv);
+      if (!coop) flush(1, ta);
+    }
+    if (coop) {
+      __syncthreads();
+      flush_wg(1, it * kWaves);
+      __syncthreads();
+    }
   }
   if (over & overflow_mask<BITS>()) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
 }
