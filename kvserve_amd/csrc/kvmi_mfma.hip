@@ -313,8 +313,9 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   // Permuted order: the workgroup's waves take consecutive tiles t0 .. t0 + 3, so head
   // j's runs of the four tiles are consecutive in the stream; after a barrier the
   // workgroup writes them as one run per head (4x longer runs than a wave's own flush),
-  // each thread a fixed set of 16-byte pieces.  Entry e of a thread: piece q = tid +
-  // kMW e of the 4 tiles' image, from wave w's buffer, to byte `dst` of head j's run.
+  // each thread a fixed set of 16-byte pieces, with streaming stores (the packed
+  // stream is not read again by this pass).  Entry e of a thread: piece q = tid + kMW e
+  // of the 4 tiles' image, from wave w's buffer, to byte `dst` of head j's run.
   const bool coop = KVMI_COOP_FLUSH && !native && !paired;
   constexpr int QE = (4 * TQ + kMW - 1) / kMW;  // pieces per thread
   int qsrc[QE], qw[QE];
@@ -336,7 +337,7 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
     uint8_t* base = seg_addr<BITS, PAIRED>(job, g, part, 0, tile_tok(run.tok0, H, t0), 0);
 #pragma unroll
     for (int e = 0; e < QE; ++e)
-      if (qw[e] < na) gst(reinterpret_cast<uint4*>(base + qdst[e]), ypark[qsrc[e]]);
+      if (qw[e] < na) gst_stream(reinterpret_cast<uint4*>(base + qdst[e]), ypark[qsrc[e]]);
   };
 
   uint4 xk[2 * NC], xv[2 * NC];
