@@ -1,6 +1,9 @@
 // Two-pass paged compress (K statistics, then encode) and the paged decompress
 // with the Hadamard transform on MFMA (gfx950); the tile layout and the shared
 // device helpers are described in kvmi_mfma_tiles.hpp.
+#include <mutex>
+#include <unordered_map>
+
 #include "kvmi_mfma_tiles.hpp"
 
 namespace kvmi {
@@ -686,23 +689,23 @@ __global__ __launch_bounds__(64 * NW) void decode_kt_kernel(Geo g, const kvmi_la
 
 // ============================================================== launch
 // Workgroups that fit on the device at once for `kernel` (CUs x resident
-// workgroups per CU), per device, computed on first use.
+// workgroups per CU), per (device, kernel), computed on first use.
 constexpr int kMaxDevices = 64;
+std::mutex g_resident_mu;
+std::unordered_map<const void*, int> g_resident[kMaxDevices];
 template <class K>
 int resident_wgs(K kernel, int threads = kMW) {
-  static std::atomic<int> cache[kMaxDevices];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1024;
-  int v = cache[dev].load(std::memory_order_relaxed);
-  if (v == 0) {
-    int cus = 0, per = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(kernel), threads, 0) !=
-        hipSuccess)
-      per = 2;
-    v = (cus > 0 ? cus : 1) * (per > 0 ? per : 1);
-    cache[dev].store(v, std::memory_order_relaxed);
-  }
+  const void* key = reinterpret_cast<const void*>(kernel);
+  std::lock_guard<std::mutex> lock(g_resident_mu);
+  auto it = g_resident[dev].find(key);
+  if (it != g_resident[dev].end()) return it->second;
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, key, threads, 0) != hipSuccess) per = 2;
+  const int v = (cus > 0 ? cus : 1) * (per > 0 ? per : 1);
+  g_resident[dev].emplace(key, v);
   return v;
 }
 
@@ -718,14 +721,22 @@ int run_blocks(const Geo& g, int32_t max_blocks, int32_t num_jobs, int target) {
 }
 
 // Workgroups per resident slot: more, shorter runs balance the end of a launch
-// better; each run also pays its table set-up once.
+// better; each run also pays its table set-up once.  A slot is a resident workgroup of
+// the statistics kernel of the geometry's head_dim (slot_wgs), for every kernel: the
+// launch shapes these counts were measured with (config 2: 768 slots, so 768, 2304 and
+// 2304 workgroups; decode's own occupancy, 2 per CU, would give 1536 at 3 rounds,
+// 2.4 % slower).
 constexpr int kWavesKstats = 1, kWavesEncode = 3, kWavesDecode = 3;
+
+int slot_wgs(const Geo& g) {
+  return g.D == 64 ? resident_wgs(kstats_mfma_kernel<2>) : resident_wgs(kstats_mfma_kernel<4>);
+}
 
 template <class K>
 int launch(K kernel, Geo g, int32_t num_jobs, int32_t max_blocks, const kvmi_layer_job* jobs, int32_t* err,
            hipStream_t st, int rounds, int threads = kMW) {
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
-  g.bpw = run_blocks(g, max_blocks, num_jobs, resident_wgs(kernel, threads) * rounds);
+  g.bpw = run_blocks(g, max_blocks, num_jobs, slot_wgs(g) * rounds);
   const int per_job = (max_blocks + g.bpw - 1) / g.bpw;
   hipLaunchKernelGGL(kernel, dim3((unsigned)per_job, (unsigned)num_jobs), dim3(threads), 0, st, g, jobs, err);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
