@@ -6,6 +6,7 @@
 
 #include "kvmi_mfma_tiles.hpp"
 
+
 namespace kvmi {
 namespace {
 
@@ -13,7 +14,10 @@ namespace {
 template <int NC, bool PAIRED>
 __device__ __forceinline__ void kstats_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs) {
   constexpr int D = 32 * NC;
-  const kvmi_layer_job job = jobs[blockIdx.y];
+  // jobs in reverse order: the statistics pass starts on the layers the previous kernel
+  // (a decode, or the attention that wrote the cache) touched last, whose lines the
+  // memory-side cache still holds, and ends on the first layers, where encode begins
+  const kvmi_layer_job job = jobs[gridDim.y - 1 - blockIdx.y];
   const int S = g.S, H = g.H;
   const Run run = wg_run(job, g);
   if ((int)blockIdx.x >= run.nwg) return;
@@ -106,7 +110,10 @@ struct SignTable {
 template <int NC, bool PAIRED>
 __device__ __forceinline__ void kstats_wide_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs) {
   constexpr int D = 32 * NC, HALF = 16 * NC, PR = 4 * NC;
-  const kvmi_layer_job job = jobs[blockIdx.y];
+  // jobs in reverse order: the statistics pass starts on the layers the previous kernel
+  // (a decode, or the attention that wrote the cache) touched last, whose lines the
+  // memory-side cache still holds, and ends on the first layers, where encode begins
+  const kvmi_layer_job job = jobs[gridDim.y - 1 - blockIdx.y];
   const int S = g.S, H = g.H, HD = H * D;
   const Run run = wg_run(job, g);
   if ((int)blockIdx.x >= run.nwg) return;
