@@ -733,7 +733,7 @@ int run_blocks(const Geo& g, int32_t max_blocks, int32_t num_jobs, int target) {
 // launch shapes these counts were measured with (config 2: 768 slots, so 768, 2304 and
 // 2304 workgroups; decode's own occupancy, 2 per CU, would give 1536 at 3 rounds,
 // 2.4 % slower).
-constexpr int kWavesKstats = 1, kWavesEncode = 3, kWavesDecode = 3;
+constexpr int kRoundsKstats = 1, kRoundsEncode = 3, kRoundsDecode = 3;
 
 int slot_wgs(const Geo& g) {
   return g.D == 64 ? resident_wgs(kstats_mfma_kernel<2>) : resident_wgs(kstats_mfma_kernel<4>);
@@ -755,16 +755,16 @@ int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
   if constexpr (NC == 4)
     if (g.flags & kPairedHeads) {
       if (g.H > kMH)
-        return clamp ? launch(encode_mfma_pair_kernel<BITS, true, kWideH>, g, nj, mb, jobs, err, st, kWavesEncode)
-                     : launch(encode_mfma_pair_kernel<BITS, false, kWideH>, g, nj, mb, jobs, err, st, kWavesEncode);
-      return clamp ? launch(encode_mfma_pair_kernel<BITS, true, kMH>, g, nj, mb, jobs, err, st, kWavesEncode)
-                   : launch(encode_mfma_pair_kernel<BITS, false, kMH>, g, nj, mb, jobs, err, st, kWavesEncode);
+        return clamp ? launch(encode_mfma_pair_kernel<BITS, true, kWideH>, g, nj, mb, jobs, err, st, kRoundsEncode)
+                     : launch(encode_mfma_pair_kernel<BITS, false, kWideH>, g, nj, mb, jobs, err, st, kRoundsEncode);
+      return clamp ? launch(encode_mfma_pair_kernel<BITS, true, kMH>, g, nj, mb, jobs, err, st, kRoundsEncode)
+                   : launch(encode_mfma_pair_kernel<BITS, false, kMH>, g, nj, mb, jobs, err, st, kRoundsEncode);
     }
   if (g.H > kMH)
-    return clamp ? launch(encode_mfma_wide_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode)
-                 : launch(encode_mfma_wide_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
-  return clamp ? launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kWavesEncode)
-               : launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kWavesEncode);
+    return clamp ? launch(encode_mfma_wide_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kRoundsEncode)
+                 : launch(encode_mfma_wide_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kRoundsEncode);
+  return clamp ? launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kRoundsEncode)
+               : launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kRoundsEncode);
 }
 constexpr int kDecodeWaves = 8;  // waves per decode workgroup (two workgroups per CU)
 template <int NC, int BITS>
@@ -772,18 +772,18 @@ int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
   if constexpr (NC == 4)
     if (g.flags & kPairedHeads) {
       if (g.H > kMH)
-        return launch(decode_mfma_pair_kernel<BITS, kDecodeWaves, kWideH>, g, nj, mb, jobs, err, st, kWavesDecode,
+        return launch(decode_mfma_pair_kernel<BITS, kDecodeWaves, kWideH>, g, nj, mb, jobs, err, st, kRoundsDecode,
                       64 * kDecodeWaves);
-      return launch(decode_mfma_pair_kernel<BITS, kDecodeWaves, kMH>, g, nj, mb, jobs, err, st, kWavesDecode,
+      return launch(decode_mfma_pair_kernel<BITS, kDecodeWaves, kMH>, g, nj, mb, jobs, err, st, kRoundsDecode,
                     64 * kDecodeWaves);
     }
   if (g.H > kMH)
-    return launch(decode_mfma_wide_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode,
+    return launch(decode_mfma_wide_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kRoundsDecode,
                   64 * kDecodeWaves);
   if constexpr (NC == 4 && BITS == 4)
-    return launch(decode_kt_kernel<kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode, 64 * kDecodeWaves);
+    return launch(decode_kt_kernel<kDecodeWaves>, g, nj, mb, jobs, err, st, kRoundsDecode, 64 * kDecodeWaves);
   else
-    return launch(decode_mfma_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kWavesDecode,
+    return launch(decode_mfma_kernel<NC, BITS, kDecodeWaves>, g, nj, mb, jobs, err, st, kRoundsDecode,
                   64 * kDecodeWaves);
 }
 
@@ -803,13 +803,13 @@ int launch_dec(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
 
 int mfma_kstats(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
   if (g.flags & kPairedHeads)
-    return g.H > kMH ? launch(kstats_wide_pair_kernel, g, nj, mb, jobs, err, st, kWavesKstats)
-                     : launch(kstats_mfma_pair_kernel, g, nj, mb, jobs, err, st, kWavesKstats);
+    return g.H > kMH ? launch(kstats_wide_pair_kernel, g, nj, mb, jobs, err, st, kRoundsKstats)
+                     : launch(kstats_mfma_pair_kernel, g, nj, mb, jobs, err, st, kRoundsKstats);
   if (g.H > kMH)
-    return g.D == 64 ? launch(kstats_wide_kernel<2>, g, nj, mb, jobs, err, st, kWavesKstats)
-                     : launch(kstats_wide_kernel<4>, g, nj, mb, jobs, err, st, kWavesKstats);
-  if (g.D == 64) return launch(kstats_mfma_kernel<2>, g, nj, mb, jobs, err, st, kWavesKstats);
-  return launch(kstats_mfma_kernel<4>, g, nj, mb, jobs, err, st, kWavesKstats);
+    return g.D == 64 ? launch(kstats_wide_kernel<2>, g, nj, mb, jobs, err, st, kRoundsKstats)
+                     : launch(kstats_wide_kernel<4>, g, nj, mb, jobs, err, st, kRoundsKstats);
+  if (g.D == 64) return launch(kstats_mfma_kernel<2>, g, nj, mb, jobs, err, st, kRoundsKstats);
+  return launch(kstats_mfma_kernel<4>, g, nj, mb, jobs, err, st, kRoundsKstats);
 }
 
 int mfma_encode(const Geo& g, const kvmi_layer_job* jobs, int32_t nj, int32_t mb, int32_t* err, hipStream_t st) {
