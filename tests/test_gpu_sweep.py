@@ -1,0 +1,113 @@
+"""Seeded sweep of request geometries against the CPU oracle (calls go through the C-ABI).
+
+The fixed geometry lists elsewhere pick one case per kernel variant; this sweep draws
+head count, block size, head_dim, width, per-head levels, layer and block counts, symbol
+order and compress path together from a fixed seed, so that combinations no list names
+(a ragged tile run per workgroup, several V groups at odd widths, one-block layers,
+levels at the top of a width) are compared with the oracle as well.  The cases are the
+same on every run; each prints its parameters before it touches the GPU.
+
+Bars: those of the configuration tests (symbols |delta| <= 1 on <= 1e-4 of the elements,
+metadata equal, dequantized KV within 1e-2 of the oracle's own round trip).
+
+Levels reach 2^bits up to 6 bits.  From 7 bits on, a symbol can round up to 2^bits at
+2^bits levels (quantizer_func.py:62-65 clamps to max_value, not max_value - 1), which
+the reference's bitpack rejects (bitpack_codec.py:32, "symbol exceeds bitpack_bits"):
+the sweep keeps those widths below 2^bits levels, since on the MFMA kernels the fp32
+summation order may round such an element the other way, and a separate test pins the
+rejection on the bit-exact row kernels.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kvpipe as kp
+from test_gpu_configs import _bits, _check_layer, _oracle_profile
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(n: int, seed: int):
+    rs = np.random.RandomState(seed)
+    out = []
+    while len(out) < n:
+        H = int(rs.choice([1, 2, 4, 8, 16, 32]))
+        S = int(rs.choice([1, 2, 4, 8, 16, 32]))
+        D = int(rs.choice([64, 128, 256, 96, 80]))
+        bits = int(rs.randint(1, 9))
+        if D * bits % 8 or H * (1 << (D - 1).bit_length()) > 8192:
+            continue  # outside the engine's geometry range
+        L = int(rs.randint(1, 4))
+        B = int(rs.randint(1, 12))
+        layout = str(rs.choice(["permuted", "native"]))
+        path = str(rs.choice(["two_pass", "one_pass"]))
+        out.append((H, S, D, bits, L, B, layout, path, int(rs.randint(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("H,S,D,bits,L,B,layout,path,seed", _cases(48, 20261202))
+def test_sweep_matches_oracle(cuda, H, S, D, bits, L, B, layout, path, seed):
+    from kvserve_amd.engine import FusedKVCodec, check_packet
+    from kvserve_amd.profiles import per_head_profile
+    from kvserve_amd.workloads import kv_blocks
+
+    g = torch.Generator().manual_seed(seed)
+    P = B + 5
+    top = (1 << bits) - (1 if bits >= 7 else 0)
+    pools = [torch.zeros((2, P, S, H, D), dtype=torch.bfloat16) for _ in range(L)]
+    ids = torch.randperm(P, generator=g)[:B]
+    for p in pools:
+        p[:, ids] = kv_blocks(g, B, S, H, D)
+    # per-head levels in [2, top]
+    prof = []
+    for _ in range(L):
+        kl = [int(v) for v in torch.randint(2, top + 1, (H,), generator=g)]
+        vl = [int(v) for v in torch.randint(2, top + 1, (H,), generator=g)]
+        prof.append(per_head_profile(kl, vl))
+    print(f"sweep H={H} S={S} D={D} bits={bits} L={L} B={B} {layout} {path} seed={seed}", flush=True)
+    pools = [p.to(cuda) for p in pools]
+    dev_ids = ids.to(torch.int32).to(cuda)
+    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path=path)
+    packet = codec.compress(pools, dev_ids, prof)
+    check_packet(packet)
+    dst = [torch.zeros_like(p) for p in pools]
+    codec.decompress(packet, dst, dev_ids)
+    torch.cuda.synchronize()
+    for l in range(L):
+        _check_layer(packet, l, _bits(pools[l][:, dev_ids.long()]), _bits(dst[l][:, dev_ids.long()]))
+
+
+def test_symbol_at_the_top_of_the_width_is_rejected_like_the_reference(cuda):
+    """128 levels at 7 bits, D = 96 (the generic row kernels, bit-exact with the oracle):
+    on this seeded request the oracle rounds some element to symbol 128 and rejects the
+    layer; the engine's error check after the run raises the reference's bitpack error.
+    With 127 levels the same request compresses and matches the oracle."""
+    from kvserve_amd.engine import FusedKVCodec, check_packet
+    from kvserve_amd.profiles import per_head_profile
+    from kvserve_amd.workloads import kv_blocks
+
+    H, S, D, bits, B = 32, 16, 96, 7, 11
+    g = torch.Generator().manual_seed(1007978485)
+    P = B + 5
+    pool = torch.zeros((2, P, S, H, D), dtype=torch.bfloat16)
+    ids = torch.randperm(P, generator=g)[:B]
+    pool[:, ids] = kv_blocks(g, B, S, H, D)
+    pools = [pool.to(cuda)]
+    dev_ids = ids.to(torch.int32).to(cuda)
+    x = _bits(pools[0][:, dev_ids.long()])
+    for levels, rejects in ((128, True), (127, False)):
+        prof = [per_head_profile([levels] * H, [levels] * H)]
+        print(f"top of width: H={H} D={D} bits={bits} levels={levels}", flush=True)
+        codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout="native")
+        if rejects:
+            with pytest.raises(ValueError, match="symbol exceeds bitpack_bits"):
+                kp.compress_request([x], list(range(B)), [_oracle_profile(prof[0])], codec.seed, bits,
+                                    layout="native", layer_ids=[0], chunks=[(0, 1)])
+            # the kernels flag the symbol; the check after the run raises it
+            with pytest.raises(RuntimeError, match="symbol exceeds bitpack_bits"):
+                check_packet(codec.compress(pools, dev_ids, prof), force=True)
+        else:
+            packet = codec.compress(pools, dev_ids, prof)
+            check_packet(packet)
+            _check_layer(packet, 0, x)
