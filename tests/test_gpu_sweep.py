@@ -1,11 +1,13 @@
 """Seeded sweep of request geometries against the CPU oracle (calls go through the C-ABI).
 
 The fixed geometry lists elsewhere pick one case per kernel variant; this sweep draws
-head count, block size, head_dim, width, per-head levels, layer and block counts, symbol
-order and compress path together from a fixed seed, so that combinations no list names
-(a ragged tile run per workgroup, several V groups at odd widths, one-block layers,
-levels at the top of a width) are compared with the oracle as well.  The cases are the
-same on every run; each prints its parameters before it touches the GPU.
+head count (1 - 64), block size, head_dim (power-of-two chunks down to 2 channels),
+width, per-head levels, layer and block counts (up to 89 blocks: several workgroups per
+job), symbol order, compress path and kernel family (MFMA, or the row or quad-per-row
+FWHT forced) together from a fixed seed, so that combinations no list names (ragged
+tile runs, several V groups at odd widths, one-block layers, levels at the top of a
+width) are compared with the oracle as well.  The cases are the same on every run; each
+prints its parameters before it touches the GPU.
 
 Bars: those of the configuration tests (symbols |delta| <= 1 on <= 1e-4 of the elements,
 metadata equal, dequantized KV within 1e-2 of the oracle's own round trip).
@@ -17,6 +19,8 @@ the sweep keeps those widths below 2^bits levels, since on the MFMA kernels the 
 summation order may round such an element the other way, and a separate test pins the
 rejection on the bit-exact row kernels.
 """
+
+import os
 
 import numpy as np
 import pytest
@@ -32,22 +36,27 @@ def _cases(n: int, seed: int):
     rs = np.random.RandomState(seed)
     out = []
     while len(out) < n:
-        H = int(rs.choice([1, 2, 4, 8, 16, 32]))
+        H = int(rs.choice([1, 2, 3, 4, 5, 6, 8, 12, 16, 24, 32, 64]))
         S = int(rs.choice([1, 2, 4, 8, 16, 32]))
-        D = int(rs.choice([64, 128, 256, 96, 80]))
+        D = int(rs.choice([6, 16, 64, 70, 80, 96, 100, 108, 128, 160, 224, 256]))
         bits = int(rs.randint(1, 9))
         if D * bits % 8 or H * (1 << (D - 1).bit_length()) > 8192:
             continue  # outside the engine's geometry range
         L = int(rs.randint(1, 4))
-        B = int(rs.randint(1, 12))
+        B = int(rs.randint(1, 14)) if rs.rand() < 0.6 else int(rs.randint(14, 90))
         layout = str(rs.choice(["permuted", "native"]))
         path = str(rs.choice(["two_pass", "one_pass"]))
-        out.append((H, S, D, bits, L, B, layout, path, int(rs.randint(1 << 30))))
+        fwht = str(rs.choice(["mfma", "mfma", "rows", "valu"]))
+        if fwht == "valu" and not (D in (64, 128) and 128 % H == 0 and H <= 16):
+            fwht = "mfma"  # the quad-per-row kernels' range
+        out.append((H, S, D, bits, L, B, layout, path, fwht, int(rs.randint(1 << 30))))
     return out
 
 
-@pytest.mark.parametrize("H,S,D,bits,L,B,layout,path,seed", _cases(48, 20261202))
-def test_sweep_matches_oracle(cuda, H, S, D, bits, L, B, layout, path, seed):
+# KVSERVE_AMD_SWEEP_CASES=N draws N cases instead of 48 (the same first 48)
+@pytest.mark.parametrize("H,S,D,bits,L,B,layout,path,fwht,seed",
+                         _cases(int(os.environ.get("KVSERVE_AMD_SWEEP_CASES", "48")), 20261202))
+def test_sweep_matches_oracle(cuda, H, S, D, bits, L, B, layout, path, fwht, seed):
     from kvserve_amd.engine import FusedKVCodec, check_packet
     from kvserve_amd.profiles import per_head_profile
     from kvserve_amd.workloads import kv_blocks
@@ -58,17 +67,17 @@ def test_sweep_matches_oracle(cuda, H, S, D, bits, L, B, layout, path, seed):
     pools = [torch.zeros((2, P, S, H, D), dtype=torch.bfloat16) for _ in range(L)]
     ids = torch.randperm(P, generator=g)[:B]
     for p in pools:
-        p[:, ids] = kv_blocks(g, B, S, H, D)
+        p[:, ids] = kv_blocks(g, B, S, H, D, k_outliers=min(4, D))
     # per-head levels in [2, top]
     prof = []
     for _ in range(L):
         kl = [int(v) for v in torch.randint(2, top + 1, (H,), generator=g)]
         vl = [int(v) for v in torch.randint(2, top + 1, (H,), generator=g)]
         prof.append(per_head_profile(kl, vl))
-    print(f"sweep H={H} S={S} D={D} bits={bits} L={L} B={B} {layout} {path} seed={seed}", flush=True)
+    print(f"sweep H={H} S={S} D={D} bits={bits} L={L} B={B} {layout} {path} {fwht} seed={seed}", flush=True)
     pools = [p.to(cuda) for p in pools]
     dev_ids = ids.to(torch.int32).to(cuda)
-    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path=path)
+    codec = FusedKVCodec(H, D, S, bits, 0xC0FEBABE, layout=layout, compress_path=path, fwht=fwht)
     packet = codec.compress(pools, dev_ids, prof)
     check_packet(packet)
     dst = [torch.zeros_like(p) for p in pools]
