@@ -451,20 +451,26 @@ def test_runtime_matches_reference_golden_chunks(name, drop_codec):
 def test_runtime_matches_oracle_at_model_shape(tmp_path, split, axis_v, bpl, tokens):
     """8 layers x 4 KV heads x 128, both parts, against the oracle bit for bit."""
     print(f"oracle runtime split={split} axis_v={axis_v} bpl={bpl} tokens={tokens}", flush=True)
+    runtime_vs_oracle(tmp_path, 8, 4, 128, 16, bpl, tokens, {"split_type": split, "axis_value": axis_v})
+
+
+def runtime_vs_oracle(tmp_path, layers, heads, dim, block, bpl, tokens, options, seed=7, score_seed=3):
+    """One chunk of `tokens` tokens through a runtime built from `options` (compression
+    keys over enable-compression-pipeline and logical_blocks_per_chunk), both parts,
+    encoded and decoded on the GPU and by the oracle: payload, aux, raw tail, rANS
+    stream and the restored caches bit for bit."""
     rt = _runtime()
-    layers, heads, dim, block = 8, 4, 128, 16
     blocks = (tokens + block - 1) // block
-    compression = {"enable-compression-pipeline": True, "logical_blocks_per_chunk": blocks, "split_type": split,
-                   "axis_value": axis_v}
-    if split == "head":
-        scores = np.random.default_rng(3).random((layers, heads)).astype(np.float32)
+    compression = {"enable-compression-pipeline": True, "logical_blocks_per_chunk": blocks, **options}
+    if compression.get("split_type") == "head":
+        scores = np.random.default_rng(score_seed).random((layers, heads)).astype(np.float32)
         np.save(tmp_path / "scores.npy", scores)
         compression["score_path"] = str(tmp_path / "scores.npy")
     config = rt.CompressionConfig.from_extra_config({"compression": compression})
     specs = {f"layer.{i}": rt.CacheSpec(i, block, heads, dim, torch.bfloat16) for i in range(layers)}
     plan = rt.build_memory_plan(config, specs, blocks_per_logical=bpl, num_layers=layers)
     runtime = rt.CompressionRuntime(plan, "HND", bpl, torch.device("cuda", 0))
-    gen = torch.Generator(device="cuda").manual_seed(7)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
     total = 2 * blocks * bpl
     caches = {n: torch.randn(total, heads, block // bpl, 2 * dim, device="cuda", dtype=torch.bfloat16, generator=gen)
               for n in specs}
@@ -492,7 +498,11 @@ def test_runtime_matches_oracle_at_model_shape(tmp_path, split, axis_v, bpl, tok
             assert np.array_equal(slot.arena_b[base:base + u8].cpu().numpy(), payload)
             assert np.array_equal(slot.aux[:aux_n].cpu().numpy(), aux)
             assert np.array_equal(slot.raw_tail[:encoded.raw_tail_bytes].cpu().numpy(), tail)
-            assert np.array_equal(slot.arena_a[:encoded.codec_bytes].cpu().numpy(), crans.encode(payload, 8))
+            if u8:
+                assert np.array_equal(slot.arena_a[:encoded.codec_bytes].cpu().numpy(), crans.encode(payload, 8))
+            else:
+                # no complete logical block: no body and no codec call (pipeline.py:595-596, :645-657)
+                assert payload.size == 0 and encoded.codec_bytes == 0
             runtime.decode(part, [dst_logical], part, encoded.codec_bytes, u8,
                            valid_tokens_by_group={0: tokens}).synchronize()
             targets = [replace(o, cache=target[p.layer_index]) for o, p in zip(parts, runtime.layout.parts(part))]

@@ -201,3 +201,73 @@ def test_axes_sweep_matches_oracle_exactly(cuda, H, S, D, bits, ak, av, L, B, la
         kp.decompress_request([ch], [ref], list(range(B)), [op], packet.seed, bits, layout=layout,
                               layer_ids=[packet.layer_ids[l]], axes=axes)
         assert np.array_equal(_bits(dst[l][:, dev_ids.long()]), ref), (axes, l)
+
+
+def _rans_cases(n: int, seed: int):
+    rs = np.random.RandomState(seed)
+    out = []
+    for _ in range(n):
+        w = int(rs.randint(1, 9))
+        size = int(rs.choice([rs.randint(1, 4096), rs.randint(4096, 200000), rs.randint(200000, 700000)]))
+        out.append((w, size, float(rs.choice([0.05, 0.3, 1.0, 5.0])), int(rs.randint(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("w,n,conc,seed", _rans_cases(int(os.environ.get("KVSERVE_AMD_SWEEP_CASES", "48")) // 2,
+                                                      20261204))
+def test_rans_sweep_equals_oracle(cuda, w, n, conc, seed):
+    """The GPU rANS stream of drawn symbol sequences (width, length, and per-64 Ki-block
+    statistics from a Dirichlet of the drawn concentration, with some blocks uniform or
+    a single symbol) is byte-equal to oracle/rans.c's, and decodes back on the GPU."""
+    from kvserve_amd import ops
+    from oracle import crans
+
+    rng = np.random.default_rng(seed)
+    A = 1 << w
+    s = np.empty(n, np.uint8)
+    for lo in range(0, n, 65536):
+        m = min(65536, n - lo)
+        kind = rng.integers(0, 6)
+        if kind == 0:
+            s[lo:lo + m] = rng.integers(0, A, m)
+        elif kind == 1:
+            s[lo:lo + m] = rng.integers(0, A)
+        else:
+            s[lo:lo + m] = rng.choice(A, m, p=rng.dirichlet(np.full(A, conc)))
+    print(f"rans sweep w={w} n={n} conc={conc} seed={seed}", flush=True)
+    body = crans.pack(s, w)
+    st = ops.rans_encode(torch.from_numpy(body.copy()).to(cuda), n, w)
+    ref = crans.encode_packed(body, n, w)
+    got = st.cpu().numpy()
+    assert got.size == ref.size and np.array_equal(got, ref), (w, n, conc, seed)
+    assert np.array_equal(ops.rans_decode(st, n, w).cpu().numpy(), body)
+
+
+def _runtime_cases(n: int, seed: int):
+    rs = np.random.RandomState(seed)
+    out = []
+    for _ in range(n):
+        block = int(rs.choice([8, 16, 32]))
+        bpl = int(rs.choice([1, 2, 4]))
+        opts = {"split_type": str(rs.choice(["layer", "head"])), "axis_key": str(rs.choice(kp.AXES)),
+                "axis_value": str(rs.choice(kp.AXES)), "hybrid_ratio": float(rs.choice([0.0, 0.3, 0.8, 1.0]))}
+        for name in ("high_key_num_levels", "low_key_num_levels", "high_value_num_levels", "low_value_num_levels"):
+            opts[name] = int(rs.choice([rs.randint(2, 17), rs.randint(2, 257)]))
+        out.append((int(rs.randint(1, 7)), int(rs.choice([1, 2, 4, 8])), int(rs.choice([32, 64, 128, 256])), block,
+                    bpl, int(rs.randint(1, int(rs.randint(1, 25)) * block + 1)), opts, int(rs.randint(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("layers,heads,dim,block,bpl,tokens,opts,seed",
+                         _runtime_cases(int(os.environ.get("KVSERVE_AMD_SWEEP_CASES", "48")) // 4, 20261205))
+def test_runtime_sweep_matches_oracle(tmp_path, layers, heads, dim, block, bpl, tokens, opts, seed):
+    """The fixed-profile runtime on drawn model shapes, block sizes, blocks per logical
+    block, partial tails, split types, quantization axes and level counts: payload, aux,
+    raw tail, rANS stream and restored caches bit for bit against oracle/runtime_ref.py."""
+    from test_gpu_runtime import runtime_vs_oracle
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    print(f"runtime sweep layers={layers} heads={heads} dim={dim} block={block} bpl={bpl} tokens={tokens} "
+          f"{opts} seed={seed}", flush=True)
+    runtime_vs_oracle(tmp_path, layers, heads, dim, block, bpl, tokens, opts, seed=seed, score_seed=seed + 1)
