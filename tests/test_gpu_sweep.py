@@ -26,6 +26,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import fused_v3 as fv
 from oracle import kvpipe as kp
 from test_gpu_configs import _bits, _check_layer, _oracle_profile
 
@@ -271,3 +272,60 @@ def test_runtime_sweep_matches_oracle(tmp_path, layers, heads, dim, block, bpl, 
     print(f"runtime sweep layers={layers} heads={heads} dim={dim} block={block} bpl={bpl} tokens={tokens} "
           f"{opts} seed={seed}", flush=True)
     runtime_vs_oracle(tmp_path, layers, heads, dim, block, bpl, tokens, opts, seed=seed, score_seed=seed + 1)
+
+
+def _v3_cases(n: int, seed: int):
+    rs = np.random.RandomState(seed)
+    out = []
+    for _ in range(n):
+        H = int(rs.choice([1, 2, 4, 8, 16, 32, 64]))
+        D = int(rs.choice([64, 128]))
+        S = int(rs.choice([1, 3, 7, 16, 32]))
+        B = int(rs.randint(1, 12)) if rs.rand() < 0.6 else int(rs.randint(12, 300))
+        B = min(B, max(1, (1 << 21) // (S * H * D)))  # keeps the numpy oracle to seconds
+        model = "Llama-3.1-8B-Instruct" if (H <= 8 and rs.rand() < 0.5) else None
+        kw = {"hybrid_ratio": float(rs.choice([0.0, 0.3, 0.8, 1.0])), "split_type": str(rs.choice(["head", "layer"])),
+              "high_key_max_value": int(rs.randint(2, 256)), "low_key_max_value": int(rs.randint(2, 256)),
+              "high_value_max_value": int(rs.randint(2, 256)), "low_value_max_value": int(rs.randint(2, 256))}
+        out.append((B, S, H, D, model, int(rs.randint(0, 32)), kw, int(rs.randint(1 << 30))))
+    return out
+
+
+@pytest.mark.parametrize("B,S,H,D,model,layer,kw,seed",
+                         _v3_cases(int(os.environ.get("KVSERVE_AMD_SWEEP_CASES", "48")) // 4, 20261206))
+def test_fused_quantizer_sweep_matches_oracle(cuda, B, S, H, D, model, layer, kw, seed):
+    """impl "tilelang_fused" (kvmi_v3_*) on drawn layer shapes, level settings, split types
+    and score-CSV head masks with tensor-parallel slices: float16 metadata, symbols and
+    the dequantized layer bit for bit against oracle/fused_v3.py."""
+    from kvserve_amd.compression.quantizer import FusedHadamardQuantizer
+
+    print(f"v3 sweep B={B} S={S} H={H} D={D} model={model} layer={layer} {kw} seed={seed}", flush=True)
+    kw = {"base_seed": seed, **kw}
+    if model:
+        kw["model_name"] = model
+        if H != 8:
+            kw.update(tensor_parallel_size=8 // H, tp_rank=(seed % (8 // H)))
+    q = FusedHadamardQuantizer(**kw)
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((2, B, S, H, D), generator=g)
+    x[0, :, :, :, torch.randint(0, D, (3,), generator=g)] *= 10.0
+    x = x.to(torch.bfloat16)
+    sym, meta = q.quantize(layer, x.to(cuda))
+    torch.cuda.synchronize()
+    k_lv, v_lv = q.levels(layer, H)
+    signs = kp.rademacher_signs(seed, layer, H, D)
+    R = B * S
+    xb = x.view(torch.int16).numpy().view(np.uint16).reshape(2, R, H, D)
+    ref_q, ref_m = fv.compress_layer(xb, signs, k_lv, v_lv)
+    km, vm = meta["key_meta"], meta["value_meta"]
+    assert np.array_equal(km["min_val"].cpu().numpy(), ref_m["kmin"].astype(np.float16))
+    assert np.array_equal(km["quant_scale"].cpu().numpy(), ref_m["kscale"].astype(np.float16))
+    assert np.array_equal(vm["min_val"].cpu().numpy(), ref_m["vmin"].astype(np.float16))
+    assert np.array_equal(vm["quant_scale"].cpu().numpy(), ref_m["vscale"].astype(np.float16))
+    got = sym.cpu().numpy().reshape(2, R, H, D)
+    assert np.array_equal(got, ref_q), int(np.count_nonzero(got != ref_q))
+    out = q.dequantize(layer, sym, meta)
+    torch.cuda.synchronize()
+    ref_out = fv.decompress_layer(got, km["min_val"].cpu().numpy(), km["quant_scale"].cpu().numpy(),
+                                  vm["min_val"].cpu().numpy(), vm["quant_scale"].cpu().numpy(), signs)
+    assert np.array_equal(_bits(out).reshape(2, R, H, D), ref_out)
