@@ -534,17 +534,39 @@ __device__ __forceinline__ void decode_body(const Geo& g, const kvmi_layer_job* 
       gst_stream(dst + qq, stg[(qq / RQ) * RP + qq % RQ]);
     }
   };
-  // Two input buffers: section q + 4 is loading while section q is computed (past the
-  // end the prefetch re-reads the current section, a cache hit).
   const int nsec = 2 * run.tiles, last_sec = nsec - 1;
-  In a, b;
-  if (wave < nsec) fetch(wave, a);
-  for (int q = wave; q < nsec; q += 2 * NW) {
-    fetch(min(q + NW, last_sec), b);
-    section(q, a);
-    if (q + NW >= nsec) break;
-    fetch(min(q + 2 * NW, last_sec), a);
-    section(q + NW, b);
+  if constexpr (NC == 2) {
+    // Three input buffers: sections q + NW and q + 2 NW are loading while section q is
+    // computed.  At D = 64 a section's loads are several small pieces (a 3-bit half-row
+    // is 12 bytes) and its compute is short, so one section of look-ahead left them
+    // exposed; a buffer is 5 VGPRs here.
+    In a, b, c;
+    if (wave < nsec) {
+      fetch(wave, a);
+      fetch(min(wave + NW, last_sec), b);
+    }
+    for (int q = wave; q < nsec; q += 3 * NW) {
+      fetch(min(q + 2 * NW, last_sec), c);
+      section(q, a);
+      if (q + NW >= nsec) break;
+      fetch(min(q + 3 * NW, last_sec), a);
+      section(q + NW, b);
+      if (q + 2 * NW >= nsec) break;
+      fetch(min(q + 4 * NW, last_sec), b);
+      section(q + 2 * NW, c);
+    }
+  } else {
+    // Two input buffers: section q + NW is loading while section q is computed (past
+    // the end the prefetch re-reads the current section, a cache hit).
+    In a, b;
+    if (wave < nsec) fetch(wave, a);
+    for (int q = wave; q < nsec; q += 2 * NW) {
+      fetch(min(q + NW, last_sec), b);
+      section(q, a);
+      if (q + NW >= nsec) break;
+      fetch(min(q + 2 * NW, last_sec), a);
+      section(q + NW, b);
+    }
   }
 }
 
