@@ -1067,6 +1067,9 @@ def main() -> int:
                     help="KV heads of the config-2 request (other than 8: a wide-head variant, not the metric's config)")
     ap.add_argument("--head-dim", type=int, default=128,
                     help="head_dim of the config-2 request (other than 128: a variant, not the metric's config)")
+    ap.add_argument("--axes", default="channel,token",
+                    help="(config2) axis_key,axis_value of the quantizer (other than channel,token: the "
+                         "generic row kernels, a variant, not the metric's config)")
     ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS),
                     help="BASELINE.json configuration to time (the metric is quoted on config2)")
     ap.add_argument("--rt-block-size", type=int, default=1, help="(runtime) tokens per block; 1 = token view")
@@ -1115,7 +1118,10 @@ def main() -> int:
         wl = getattr(workloads, "make_" + args.workload)(device=dev)
     reqs = wl.requests
     S, H, D, bits = wl.block_size, wl.num_heads, wl.head_dim, wl.bits
-    codec = FusedKVCodec(H, D, S, bits, wl.seed, compress_path=args.compress_path)
+    axes = tuple(a.strip() for a in args.axes.split(","))
+    if axes != ("channel", "token") and args.workload != "config2":
+        raise SystemExit("--axes applies to the config2 workload only")
+    codec = FusedKVCodec(H, D, S, bits, wl.seed, compress_path=args.compress_path, axes=axes)
     if len(reqs) == 1:
         req = reqs[0]
         cplan = codec.plan_compress(req.pools, req.block_ids, req.profiles, req.layer_ids)
@@ -1186,7 +1192,9 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) KV, 4 outlier K channels/head x10)",
         "config": {
             "workload": WORKLOADS[args.workload] + (f" [variant: {H} KV heads, head_dim {D}]"
-                                                    if args.workload == "config2" and (H, D) != (8, 128) else ""),
+                                                    if args.workload == "config2" and (H, D) != (8, 128) else "")
+                        + (f" [variant: axis_key {axes[0]}, axis_value {axes[1]}]"
+                           if axes != ("channel", "token") else ""),
             "requests": len(reqs), "layers": len(reqs[0].pools),
             "tokens": sum(r.block_ids.numel() for r in reqs) * S, "raw_bytes": R, "packed_bytes": P,
             "meta_bytes": M,
