@@ -292,12 +292,21 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   uint4* ostage = ypark + wave * tile_buf_q<NC>();
   uint8_t* ost = reinterpret_cast<uint8_t*>(ostage);
   const int tpt = kTok / H;  // tokens per tile
+#ifndef KVMI_COOP_FLUSH
+#define KVMI_COOP_FLUSH 1
+#endif
+  // In the permuted order, flushed by the whole workgroup, each head's run in the staged
+  // image is followed by 16 bytes: the lanes of one LDS store pass (two tokens of every
+  // head) then fall 4 banks apart per head, instead of all on the same 4 banks (a run is
+  // a multiple of the 256-byte bank row at 8 heads): 8-way conflicts become 2-way.
+  constexpr int kRunPad = KVMI_COOP_FLUSH ? 1 : 0;  // uint4 after each head's run
+  static_assert(tile_buf_q<NC>() >= TQ + HM * kRunPad, "the padded image fits a wave buffer");
   // byte offset of this lane's half-row in the staged image, by output position; a
   // permuted run of paired virtual heads is a real head's tokens, both halves each
   auto stage_off = [&](int j) {
     if (native) return (r / H) * (H * RB) + j * RB + hl * (RB / 2);
     if (paired) return (j >> 1) * (2 * tpt * RB) + (r / H) * (2 * RB) + (j & 1) * RB + hl * (RB / 2);
-    return j * (tpt * RB) + (r / H) * RB + hl * (RB / 2);
+    return j * (tpt * RB + 16 * kRunPad) + (r / H) * RB + hl * (RB / 2);
   };
   const int offk = stage_off(lp.jk), offv = stage_off(lp.jv);
   // write the staged image of (part, tile starting at token ta) to the stream
@@ -317,9 +326,6 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   // The wave's parking buffer also turns each coalesced tile into the lanes' half-rows
   // (the V tile is rearranged before its rounded outputs are parked there).
   uint4* wbuf = ypark + wave * tile_buf_q<NC>();
-#ifndef KVMI_COOP_FLUSH
-#define KVMI_COOP_FLUSH 1
-#endif
   // Permuted order: the workgroup's waves take consecutive tiles t0 .. t0 + 3, so head
   // j's runs of the four tiles are consecutive in the stream; after a barrier the
   // workgroup writes them as one run per head (4x longer runs than a wave's own flush),
@@ -338,7 +344,7 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
       const int q = (int)threadIdx.x + kMW * e;
       const int j = q / (kWaves * rq), rem = q - j * (kWaves * rq), w = rem / rq;
       qw[e] = q < kWaves * TQ ? w : kWaves;  // kWaves: no piece
-      qsrc[e] = w * tile_buf_q<NC>() + j * rq + (rem - w * rq);
+      qsrc[e] = w * tile_buf_q<NC>() + j * (rq + kRunPad) + (rem - w * rq);
       qdst[e] = j * hs_bytes + 16 * rem;
     }
   }
