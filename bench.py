@@ -1067,6 +1067,9 @@ def main() -> int:
                     help="KV heads of the config-2 request (other than 8: a wide-head variant, not the metric's config)")
     ap.add_argument("--head-dim", type=int, default=128,
                     help="head_dim of the config-2 request (other than 128: a variant, not the metric's config)")
+    ap.add_argument("--layout", default="permuted", choices=["permuted", "native"],
+                    help="(config2) symbol order of the stream, KVSERVE_CODEC_LAYOUT (native: a variant, "
+                         "not the metric's config)")
     ap.add_argument("--axes", default="channel,token",
                     help="(config2) axis_key,axis_value of the quantizer (other than channel,token: the "
                          "generic row kernels, a variant, not the metric's config)")
@@ -1119,9 +1122,9 @@ def main() -> int:
     reqs = wl.requests
     S, H, D, bits = wl.block_size, wl.num_heads, wl.head_dim, wl.bits
     axes = tuple(a.strip() for a in args.axes.split(","))
-    if axes != ("channel", "token") and args.workload != "config2":
-        raise SystemExit("--axes applies to the config2 workload only")
-    codec = FusedKVCodec(H, D, S, bits, wl.seed, compress_path=args.compress_path, axes=axes)
+    if (axes != ("channel", "token") or args.layout != "permuted") and args.workload != "config2":
+        raise SystemExit("--axes and --layout apply to the config2 workload only")
+    codec = FusedKVCodec(H, D, S, bits, wl.seed, compress_path=args.compress_path, axes=axes, layout=args.layout)
     if len(reqs) == 1:
         req = reqs[0]
         cplan = codec.plan_compress(req.pools, req.block_ids, req.profiles, req.layer_ids)
@@ -1194,7 +1197,8 @@ def main() -> int:
             "workload": WORKLOADS[args.workload] + (f" [variant: {H} KV heads, head_dim {D}]"
                                                     if args.workload == "config2" and (H, D) != (8, 128) else "")
                         + (f" [variant: axis_key {axes[0]}, axis_value {axes[1]}]"
-                           if axes != ("channel", "token") else ""),
+                           if axes != ("channel", "token") else "")
+                        + (f" [variant: {args.layout} symbol order]" if args.layout != "permuted" else ""),
             "requests": len(reqs), "layers": len(reqs[0].pools),
             "tokens": sum(r.block_ids.numel() for r in reqs) * S, "raw_bytes": R, "packed_bytes": P,
             "meta_bytes": M,
