@@ -235,7 +235,7 @@ __global__ __launch_bounds__(kMW) void kstats_wide_pair_kernel(Geo g, const kvmi
 // ============================================================== encode (orientation T)
 // HM: head capacity of the tables (kMH, or kWideH for 16 and 32 heads).
 // PAIRED: head_dim 256 as paired virtual heads of 128 (kPairedHeads).
-template <int NC, int BITS, bool CLAMP, int HM, bool PAIRED>
+template <int NC, int BITS, bool CLAMP, int HM, bool PAIRED, int W = kWaves>
 __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* __restrict__ jobs,
                                             int32_t* __restrict__ err) {
   constexpr int D = 32 * NC, HALF = 16 * NC;
@@ -263,7 +263,7 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   constexpr int RB = D * BITS / 8;            // bytes of one packed row
   constexpr int TQ = kTok * RB / 16;          // uint4 per tile
   static_assert(tile_buf_q<NC>() >= 2 * NC * 64 && tile_buf_q<NC>() >= TQ, "a wave buffer holds each use");
-  __shared__ uint4 ypark[kWaves * tile_buf_q<NC>()];
+  __shared__ uint4 ypark[W * tile_buf_q<NC>()];
   const bool native = g.flags & KVMI_F_NATIVE_LAYOUT;
   constexpr bool paired = PAIRED;
   stage_profile(T, job.profile, H, paired);
@@ -326,14 +326,14 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   // The wave's parking buffer also turns each coalesced tile into the lanes' half-rows
   // (the V tile is rearranged before its rounded outputs are parked there).
   uint4* wbuf = ypark + wave * tile_buf_q<NC>();
-  // Permuted order: the workgroup's waves take consecutive tiles t0 .. t0 + 3, so head
-  // j's runs of the four tiles are consecutive in the stream; after a barrier the
-  // workgroup writes them as one run per head (4x longer runs than a wave's own flush),
-  // each thread a fixed set of 16-byte pieces, with streaming stores (the packed
-  // stream is not read again by this pass).  Entry e of a thread: piece q = tid + kMW e
-  // of the 4 tiles' image, from wave w's buffer, to byte `dst` of head j's run.
+  // Permuted order: the workgroup's W waves take consecutive tiles t0 .. t0 + W - 1, so
+  // head j's runs of the W tiles are consecutive in the stream; after a barrier the
+  // workgroup writes them as one run per head (W times longer runs than a wave's own
+  // flush), each thread a fixed set of 16-byte pieces, with streaming stores (the packed
+  // stream is not read again by this pass).  Entry e of a thread: piece q = tid + 64 W e
+  // of the W tiles' image, from wave w's buffer, to byte `dst` of head j's run.
   const bool coop = KVMI_COOP_FLUSH && !native && !paired;
-  constexpr int QE = (4 * TQ + kMW - 1) / kMW;  // pieces per thread
+  constexpr int QE = (W * TQ + 64 * W - 1) / (64 * W);  // pieces per thread
   int qsrc[QE], qw[QE];
   int64_t qdst[QE];
   {
@@ -341,15 +341,15 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
     const int64_t hs_bytes = (int64_t)ntok * RB;
 #pragma unroll
     for (int e = 0; e < QE; ++e) {
-      const int q = (int)threadIdx.x + kMW * e;
-      const int j = q / (kWaves * rq), rem = q - j * (kWaves * rq), w = rem / rq;
-      qw[e] = q < kWaves * TQ ? w : kWaves;  // kWaves: no piece
+      const int q = (int)threadIdx.x + 64 * W * e;
+      const int j = q / (W * rq), rem = q - j * (W * rq), w = rem / rq;
+      qw[e] = q < W * TQ ? w : W;  // W: no piece
       qsrc[e] = w * tile_buf_q<NC>() + j * (rq + kRunPad) + (rem - w * rq);
       qdst[e] = j * hs_bytes + 16 * rem;
     }
   }
   auto flush_wg = [&](int part, int t0) {
-    const int na = min(kWaves, run.tiles - t0);
+    const int na = min(W, run.tiles - t0);
     uint8_t* base = seg_addr<BITS, PAIRED>(job, g, part, 0, tile_tok(run.tok0, H, t0), 0);
 #pragma unroll
     for (int e = 0; e < QE; ++e)
@@ -359,9 +359,9 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
   uint4 xk[2 * NC], xv[2 * NC];
   const int last_tile = run.tiles - 1;
   load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, min(wave, last_tile))), xk);
-  const int niter = (run.tiles + kWaves - 1) / kWaves;  // the same for every wave (barriers)
+  const int niter = (run.tiles + W - 1) / W;  // the same for every wave (barriers)
   for (int it = 0; it < niter; ++it) {
-    const int t = it * kWaves + wave;
+    const int t = it * W + wave;
     const bool act = t < run.tiles;  // wave-uniform
 #pragma unroll
     for (int u = 0; u < 2 * NC; ++u) pin(xk[u]);
@@ -381,11 +381,11 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
     }
     if (coop) {
       __syncthreads();
-      flush_wg(0, it * kWaves);
+      flush_wg(0, it * W);
       __syncthreads();
     }
     // next tile's K (unconditional: past the end it re-reads the last tile, a cache hit)
-    const int tn = min(t + kWaves, last_tile);
+    const int tn = min(t + W, last_tile);
     load_tile<NC>(poolK, tile_row0(job, S, H, tile_tok(run.tok0, H, tn)), xk);
     // ---------------- V: per-token statistics over the heads of a group
     if (act) {
@@ -398,17 +398,22 @@ __device__ __forceinline__ void encode_body(const Geo& g, const kvmi_layer_job* 
     }
     if (coop) {
       __syncthreads();
-      flush_wg(1, it * kWaves);
+      flush_wg(1, it * W);
       __syncthreads();
     }
   }
   if (over & overflow_mask<BITS>()) atomicOr(err, KVMI_ERR_SYMBOL_RANGE);
 }
 
+// Waves per workgroup of encode_mfma_kernel: 8 at D = 64, so that the workgroup-wide flush
+// of the permuted order joins 8 tiles per head run (8 x 96 bytes at 3 bits) instead of 4;
+// at D = 64 two such workgroups per CU hold the same 16 waves as four of 4.
+template <int NC>
+constexpr int kEncWaves = NC == 2 ? 8 : kWaves;
 template <int NC, int BITS, bool CLAMP>
-__global__ __launch_bounds__(kMW) void encode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
-                                                          int32_t* __restrict__ err) {
-  encode_body<NC, BITS, CLAMP, kMH, false>(g, jobs, err);
+__global__ __launch_bounds__(64 * kEncWaves<NC>) void encode_mfma_kernel(Geo g, const kvmi_layer_job* __restrict__ jobs,
+                                                                          int32_t* __restrict__ err) {
+  encode_body<NC, BITS, CLAMP, kMH, false, kEncWaves<NC>>(g, jobs, err);
 }
 // 16 or 32 KV heads: a tile holds 2 tokens or 1 (32 rows), with tables for 32 heads.
 template <int NC, int BITS, bool CLAMP>
@@ -791,8 +796,9 @@ int launch_enc(const Geo& g, int32_t nj, int32_t mb, const kvmi_layer_job* jobs,
   if (g.H > kMH)
     return clamp ? launch(encode_mfma_wide_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kRoundsEncode)
                  : launch(encode_mfma_wide_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kRoundsEncode);
-  return clamp ? launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kRoundsEncode)
-               : launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kRoundsEncode);
+  return clamp ? launch(encode_mfma_kernel<NC, BITS, true>, g, nj, mb, jobs, err, st, kRoundsEncode, 64 * kEncWaves<NC>)
+               : launch(encode_mfma_kernel<NC, BITS, false>, g, nj, mb, jobs, err, st, kRoundsEncode,
+                        64 * kEncWaves<NC>);
 }
 constexpr int kDecodeWaves = 8;  // waves per decode workgroup (two workgroups per CU)
 template <int NC, int BITS>
