@@ -767,7 +767,7 @@ int run_blocks(const Geo& g, int32_t max_blocks, int32_t num_jobs, int target) {
 // 2304 workgroups; decode's own occupancy, 2 per CU, would give 1536 at 3 rounds,
 // 2.4 % slower).
 constexpr int kRoundsKstats = 1, kRoundsEncode = 3, kRoundsDecode = 3;
-constexpr int kManyJobs = 256;
+constexpr int kLongRunTiles = 128;
 
 int slot_wgs(const Geo& g) {
   return g.D == 64 ? resident_wgs(kstats_mfma_kernel<2>) : resident_wgs(kstats_mfma_kernel<4>);
@@ -778,12 +778,13 @@ int launch(K kernel, Geo g, int32_t num_jobs, int32_t max_blocks, const kvmi_lay
            hipStream_t st, int rounds, int threads = kMW) {
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   g.bpw = run_blocks(g, max_blocks, num_jobs, slot_wgs(g) * rounds);
-  // Batches of many jobs (the layers of several requests) are sized as if every job had
-  // max_blocks, so with requests of unequal lengths the runs come out long and the launch
-  // ends unbalanced.  There twice the rounds, as long as the longest job still splits into
-  // at least four runs (config 3: compress and decompress -4.5 %).  Short jobs keep
-  // theirs: splitting a 16-block job in two uneven runs made config 5 14 % slower.
-  if (rounds > 1 && num_jobs >= kManyJobs) {
+  // Long runs (more than kLongRunTiles tiles a workgroup: long requests, or batches sized
+  // as if every request were as long as the longest) end the launch unbalanced: there
+  // twice the rounds, as long as the longest job still splits into at least four runs
+  // (config 3: compress and decompress -4.5 %, config 4 -4 / -3 %).  Config 2's runs of
+  // 32 tiles keep theirs (twice the rounds: +1 %), and so do short jobs: splitting a
+  // 16-block job in two uneven runs made config 5 14 % slower.
+  if (rounds > 1 && (int64_t)g.bpw * g.S * g.H > (int64_t)kLongRunTiles * kTok) {
     const int bpw2 = run_blocks(g, max_blocks, num_jobs, slot_wgs(g) * rounds * 2);
     if (max_blocks >= 4 * bpw2) g.bpw = bpw2;
   }
