@@ -779,15 +779,18 @@ int launch(K kernel, Geo g, int32_t num_jobs, int32_t max_blocks, const kvmi_lay
   if (num_jobs == 0 || max_blocks == 0) return KVMI_OK;
   g.bpw = run_blocks(g, max_blocks, num_jobs, slot_wgs(g) * rounds);
   // Long runs (more than kLongRunTiles tiles a workgroup: long requests, or batches sized
-  // as if every request were as long as the longest) end the launch unbalanced: there
-  // twice the rounds, as long as the longest job still splits into at least four runs
-  // (config 3: compress and decompress -4.5 %, config 4 -4 / -3 %).  Config 2's runs of
-  // 32 tiles keep theirs (twice the rounds: +1 %), and so do short jobs: splitting a
-  // 16-block job in two uneven runs made config 5 14 % slower.
-  if (rounds > 1 && (int64_t)g.bpw * g.S * g.H > (int64_t)kLongRunTiles * kTok) {
-    const int bpw2 = run_blocks(g, max_blocks, num_jobs, slot_wgs(g) * rounds * 2);
-    if (max_blocks >= 4 * bpw2) g.bpw = bpw2;
+  // as if every request were as long as the longest) end the launch unbalanced: there the
+  // rounds double, up to three times, while runs stay long and the longest job still splits
+  // into at least four runs (config 3: compress -6.7 %, decompress -5.5 %; config 4 -5.5 %
+  // and -5.8 %).  Config 2's runs of 32 tiles keep theirs (twice the rounds: +1 %), and so
+  // do short jobs: splitting a 16-block job in two uneven runs made config 5 14 % slower.
+  for (int k = 0; k < 3 && rounds > 1 && (int64_t)g.bpw * g.S * g.H > (int64_t)kLongRunTiles * kTok; ++k) {
+    rounds *= 2;
+    const int bpw2 = run_blocks(g, max_blocks, num_jobs, slot_wgs(g) * rounds);
+    if (max_blocks < 4 * bpw2) break;
+    g.bpw = bpw2;
   }
+
   const int per_job = (max_blocks + g.bpw - 1) / g.bpw;
   hipLaunchKernelGGL(kernel, dim3((unsigned)per_job, (unsigned)num_jobs), dim3(threads), 0, st, g, jobs, err);
   return hipGetLastError() == hipSuccess ? KVMI_OK : KVMI_ELAUNCH;
