@@ -56,8 +56,9 @@ WORKLOADS = {
                "Hadamard seed 0xC0FEBABE, head split (Llama-3.1-8B mask, hybrid 0.3), "
                "16/16 levels, bitpack 4 bits, 4 streams of 8 layers; step = compress + decompress",
     "config3": "config3: 16 requests of U[1024,16384] tokens, 32 layers x 8 heads x D=128, per-(layer, head) "
-               "levels in {6,12} for K and V, bitpack 4, seeded random blocks of a 262144-block pool (32 "
-               "logical layer pools alias 2 physical pools), one batched plan per direction; "
+               "levels in {6,12} for K and V, bitpack 4, seeded random blocks of a 32768-block pool per "
+               "layer (32 distinct pools: the 262144-block pool of the configuration needs 512 GiB for 32 "
+               "layers), one batched plan per direction; "
                "step = compress + decompress",
     "config4": "config4: Qwen2.5-72B-shaped request, 80 layers x 8 heads x D=128 x 32768 tokens, 2% "
                "Student-t(3) outliers, layer split levels 12/6 alternating, bitpack 4, contiguous caches, "
@@ -1073,6 +1074,10 @@ def main() -> int:
     ap.add_argument("--axes", default="channel,token",
                     help="(config2) axis_key,axis_value of the quantizer (other than channel,token: the "
                          "generic row kernels, a variant, not the metric's config)")
+    ap.add_argument("--config3-pools", default="distinct", choices=["distinct", "aliased"],
+                    help="(config3) distinct: one 32768-block pool per layer (64 GiB), every layer its own "
+                         "memory; aliased: 32 logical 262144-block layer pools over 2 physical ones, so 16 "
+                         "layers read the same blocks and some compress reads hit the caches (a variant)")
     ap.add_argument("--workload", default="config2", choices=sorted(WORKLOADS),
                     help="BASELINE.json configuration to time (the metric is quoted on config2)")
     ap.add_argument("--rt-block-size", type=int, default=1, help="(runtime) tokens per block; 1 = token view")
@@ -1117,11 +1122,16 @@ def main() -> int:
     print(f"bench: building {args.workload} workload", file=sys.stderr, flush=True)
     if args.workload == "config2":
         wl = workloads.make_config2(device=dev, num_layers=args.layers, num_heads=args.heads, head_dim=args.head_dim)
+    elif args.workload == "config3":
+        wl = (workloads.make_config3(device=dev, pool_blocks=32768, physical_pools=32)
+              if args.config3_pools == "distinct" else workloads.make_config3(device=dev))
     else:
         wl = getattr(workloads, "make_" + args.workload)(device=dev)
     reqs = wl.requests
     S, H, D, bits = wl.block_size, wl.num_heads, wl.head_dim, wl.bits
     axes = tuple(a.strip() for a in args.axes.split(","))
+    if args.config3_pools != "distinct" and args.workload != "config3":
+        raise SystemExit("--config3-pools applies to the config3 workload only")
     if (axes != ("channel", "token") or args.layout != "permuted") and args.workload != "config2":
         raise SystemExit("--axes and --layout apply to the config2 workload only")
     codec = FusedKVCodec(H, D, S, bits, wl.seed, compress_path=args.compress_path, axes=axes, layout=args.layout)
@@ -1198,7 +1208,9 @@ def main() -> int:
                                                     if args.workload == "config2" and (H, D) != (8, 128) else "")
                         + (f" [variant: axis_key {axes[0]}, axis_value {axes[1]}]"
                            if axes != ("channel", "token") else "")
-                        + (f" [variant: {args.layout} symbol order]" if args.layout != "permuted" else ""),
+                        + (f" [variant: {args.layout} symbol order]" if args.layout != "permuted" else "")
+                        + (" [variant: 262144-block layer pools aliasing 2 physical pools]"
+                           if args.workload == "config3" and args.config3_pools == "aliased" else ""),
             "requests": len(reqs), "layers": len(reqs[0].pools),
             "tokens": sum(r.block_ids.numel() for r in reqs) * S, "raw_bytes": R, "packed_bytes": P,
             "meta_bytes": M,
